@@ -1,0 +1,594 @@
+// C ABI of the gfx950 CQ library (libneedle2_native.so).
+//
+// The first group of exports is the reference's ctypes boundary, with the same
+// names, argument meaning, ownership and error behaviour
+// (needle2/native.py:124-146; needle2/csrc/cq.cpp:342-371,
+// needle2/csrc/sdot.cpp:349-360). The handle uploads the packed codes and
+// norms to device memory at create time; linear calls copy x in, run the
+// kernels on the handle's stream and copy y out before returning.
+// The second group (needle2_gpu_*) is additive: device-resident entry points,
+// multi-matrix plans, memory/stream/event helpers and a thread-local error.
+#include "abi_internal.h"
+
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <memory>
+#include <mutex>
+#include <vector>
+
+namespace nd {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const std::string &msg) { g_error = msg; }
+const char *get_error() { return g_error.c_str(); }
+
+void hip_fail(const char *expr, hipError_t e, const char *file, int line) {
+    throw Error(std::string("HIP error ") + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ") in " + expr +
+                " at " + file + ":" + std::to_string(line));
+}
+
+static bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// ---------------------------------------------------------------------------
+// Matrix upload
+// ---------------------------------------------------------------------------
+void Matrix::upload(const uint8_t *packed, const uint16_t *host_norms, int out_, int in_, int bits_, int group_,
+                    const float *cb, hipStream_t s) {
+    ND_CHECK(out_ > 0 && in_ > 0, "CQ matrix shape must be positive");
+    ND_CHECK(bits_ == 2 || bits_ == 3 || bits_ == 4 || bits_ == 5, "CQ storage bits must be 2, 3, 4, or ternary marker 5");
+    ND_CHECK(is_pow2(group_) && group_ >= 8, "CQ group size must be a power of two >= 8");
+    ND_CHECK(packed && host_norms && cb, "CQ create: null buffer");
+    out = out_;
+    in = in_;
+    bits = bits_;
+    group = group_;
+    int64_t padded64 = (int64_t(in) + group - 1) / group * group;
+    ND_CHECK(padded64 <= std::numeric_limits<int>::max() / 4, "CQ row too long");
+    padded = static_cast<int>(padded64);
+    groups = padded / group;
+    const int storage_bits = bits == 5 ? 2 : bits;
+    rowbytes = padded * storage_bits / 8;
+    kind = (bits == 2 || bits == 5) ? kCrumb : kNib;
+    windows = (padded + kWindow - 1) / kWindow;
+    dev = windows * kWindow;
+    chunks = dev / (kind == kNib ? 32 : 64);
+    n_pad = (out + kRowsPerBlock - 1) / kRowsPerBlock * kRowsPerBlock;
+    scale = 1 / std::sqrt(float(group));  // cq.cpp:44
+    std::memset(lut, 0, sizeof lut);
+    if (bits == 5) {  // ternary crumbs: 3 -> cb[0], 0 -> cb[1], 1 -> cb[2] (cq.cpp:68, 73); 2 is invalid
+        lut[0] = cb[1];
+        lut[1] = cb[2];
+        lut[2] = 0.0f;
+        lut[3] = cb[0];
+    } else {
+        std::memcpy(lut, cb, sizeof(float) * (1u << bits));
+    }
+    std::memcpy(cb_raw, cb, sizeof(float) * (bits == 5 ? 3 : 1u << bits));
+
+    DevBuf<uint8_t> raw;
+    const size_t raw_bytes = size_t(out) * rowbytes;
+    raw.reserve(raw_bytes);
+    ND_HIP(hipMemcpyAsync(raw.p, packed, raw_bytes, hipMemcpyHostToDevice, s));
+    codes.reserve(size_t(chunks) * n_pad);
+    launch_relayout(raw.p, out, rowbytes, bits, padded, codes.p, n_pad, chunks, s);
+    DevBuf<uint16_t> nraw;
+    nraw.reserve(size_t(out) * groups);
+    ND_HIP(hipMemcpyAsync(nraw.p, host_norms, size_t(out) * groups * 2, hipMemcpyHostToDevice, s));
+    norms.reserve(size_t(groups) * n_pad);
+    launch_norms_transpose(nraw.p, out, groups, norms.p, n_pad, s);
+    ND_HIP(hipStreamSynchronize(s));
+}
+
+CqGeom Matrix::geom() const {
+    CqGeom g{};
+    g.kind = kind;
+    g.group = group;
+    g.groups = groups;
+    g.windows = windows;
+    g.chunks = chunks;
+    g.scale = scale;
+    std::memcpy(g.lut, lut, sizeof lut);
+    return g;
+}
+
+void Matrix::transform(const float *x, int x_stride, float *rot, int nvec, DevBuf<float> &big, hipStream_t s) const {
+    if (group <= 16384) {
+        launch_transform(x, x_stride, rot, dev, nvec, in, padded, dev, group, scale, s);
+    } else {
+        big.reserve(size_t(nvec) * padded);
+        launch_transform_big(x, x_stride, rot, dev, nvec, in, padded, dev, group, scale, big.p, s);
+    }
+}
+
+Staging::Staging() { ND_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking)); }
+Staging::~Staging() {
+    if (stream) (void)hipStreamDestroy(stream);
+}
+
+// ---------------------------------------------------------------------------
+// FP32 handle
+// ---------------------------------------------------------------------------
+void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s) {
+    if (batch <= 0) return;
+    st.rot.reserve(size_t(batch) * m.dev);
+    m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
+    const CqJob job{m.codes.p, m.norms.p, st.rot.p, d_y, m.out, m.n_pad, 0, batch};
+    launch_cq_gemv(m.geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, exact_crumbs, s);
+}
+
+void CqHandle::linear_host(const float *x, float *y, int batch) {
+    if (batch <= 0) return;
+    const size_t nx = size_t(batch) * m.in, ny = size_t(batch) * m.out;
+    st.hx.reserve(nx);
+    st.hy.reserve(ny);
+    st.x.reserve(nx);
+    st.y.reserve(ny);
+    std::memcpy(st.hx.p, x, nx * sizeof(float));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, nx * sizeof(float), hipMemcpyHostToDevice, st.stream));
+    run_device(st.x.p, st.y.p, batch, st.stream);
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, ny * sizeof(float), hipMemcpyDeviceToHost, st.stream));
+    ND_HIP(hipStreamSynchronize(st.stream));
+    std::memcpy(y, st.hy.p, ny * sizeof(float));
+}
+
+void CqHandle::rows_host(const int64_t *ids, float *y, int count) {
+    if (count <= 0) return;
+    for (int i = 0; i < count; ++i) ND_CHECK(ids[i] >= 0 && ids[i] < m.out, "CQ row index outside matrix");
+    DevBuf<int64_t> dids;
+    dids.reserve(count);
+    st.rot.reserve(size_t(count) * m.padded);
+    st.y.reserve(size_t(count) * m.in);
+    ND_HIP(hipMemcpyAsync(dids.p, ids, size_t(count) * sizeof(int64_t), hipMemcpyHostToDevice, st.stream));
+    launch_cq_rows(m.geom(), m.codes.p, m.norms.p, m.n_pad, dids.p, count, m.in, m.padded, st.rot.p, st.y.p,
+                   st.stream);
+    ND_HIP(hipMemcpyAsync(y, st.y.p, size_t(count) * m.in * sizeof(float), hipMemcpyDeviceToHost, st.stream));
+    ND_HIP(hipStreamSynchronize(st.stream));
+}
+
+// ---------------------------------------------------------------------------
+// int8 handle
+// ---------------------------------------------------------------------------
+void SdotHandle::init_tables() {
+    // sdot.cpp:38-44: cs = max|cb|/127 (1 if zero), centroids = clamp(nearbyint(cb/cs))
+    float maximum = 0;
+    const int n = 1 << m.bits;
+    for (int i = 0; i < n; ++i) maximum = std::max(maximum, std::abs(m.cb_raw[i]));
+    centroid_scale = maximum > 0 ? maximum / 127 : 1;
+    uint8_t cent[16] = {};
+    for (int i = 0; i < n; ++i) {
+        float v = std::nearbyint(m.cb_raw[i] / centroid_scale);
+        v = v < -127.0f ? -127.0f : (127.0f < v ? 127.0f : v);
+        cent[i] = static_cast<uint8_t>(static_cast<int8_t>(v));
+    }
+    std::memcpy(centroids, cent, sizeof centroids);
+}
+
+SdotGeom SdotHandle::geom() const {
+    SdotGeom g{};
+    g.kind = m.kind;
+    g.group = m.group;
+    g.groups = m.groups;
+    g.windows = m.windows;
+    g.chunks = m.chunks;
+    g.centroid_scale = centroid_scale;
+    std::memcpy(g.cent, centroids, sizeof g.cent);
+    return g;
+}
+
+void SdotHandle::prepare_device(const float *d_x, int batch, int32_t *q, float *xs, hipStream_t s) {
+    st.rot.reserve(size_t(batch) * m.dev);
+    m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
+    launch_sdot_quantize(st.rot.p, m.dev, batch, m.padded, m.dev, m.group, m.kind, q, xs, s);
+}
+
+void SdotHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s) {
+    if (batch <= 0) return;
+    st.q.reserve(size_t(batch) * m.dev / 4);
+    st.xs.reserve(size_t(batch) * m.groups);
+    prepare_device(d_x, batch, st.q.p, st.xs.p, s);
+    const SdotJob job{m.codes.p, m.norms.p, st.q.p, st.xs.p, d_y, m.out, m.n_pad, 0, batch};
+    launch_sdot_gemv(geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, s);
+}
+
+void SdotHandle::linear_host(const float *x, float *y, int batch) {
+    if (batch <= 0) return;
+    const size_t nx = size_t(batch) * m.in, ny = size_t(batch) * m.out;
+    st.hx.reserve(nx);
+    st.hy.reserve(ny);
+    st.x.reserve(nx);
+    st.y.reserve(ny);
+    std::memcpy(st.hx.p, x, nx * sizeof(float));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, nx * sizeof(float), hipMemcpyHostToDevice, st.stream));
+    run_device(st.x.p, st.y.p, batch, st.stream);
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, ny * sizeof(float), hipMemcpyDeviceToHost, st.stream));
+    ND_HIP(hipStreamSynchronize(st.stream));
+    std::memcpy(y, st.hy.p, ny * sizeof(float));
+}
+
+// ---------------------------------------------------------------------------
+// Plans: many matrices of one geometry, one transform and one GEMV launch.
+// ---------------------------------------------------------------------------
+struct Plan {
+    bool sdot = false;
+    int count = 0, batch = 1;
+    std::vector<CqHandle *> cq;
+    std::vector<SdotHandle *> sd;
+    std::vector<const float *> xs_in;
+    std::vector<float *> ys;
+    DevBuf<float> rot;
+    DevBuf<int32_t> q;
+    DevBuf<float> xscale;
+    DevBuf<uint8_t> jobs;
+    int blocks = 0;
+    const Matrix *first = nullptr;
+    Staging st;
+};
+
+static void plan_upload(Plan &p) {
+    const Matrix &m = *p.first;
+    std::vector<uint8_t> host;
+    int block = 0;
+    if (!p.sdot) {
+        p.rot.reserve(size_t(p.count) * p.batch * m.dev);
+        std::vector<CqJob> jobs(p.count);
+        for (int i = 0; i < p.count; ++i) {
+            const Matrix &mi = p.cq[i]->m;
+            jobs[i] = CqJob{mi.codes.p, mi.norms.p, p.rot.p + size_t(i) * p.batch * m.dev, p.ys[i], mi.out, mi.n_pad,
+                            block, p.batch};
+            block += mi.n_pad / kRowsPerBlock;
+        }
+        host.assign(reinterpret_cast<uint8_t *>(jobs.data()), reinterpret_cast<uint8_t *>(jobs.data() + p.count));
+    } else {
+        p.rot.reserve(size_t(p.count) * p.batch * m.dev);
+        p.q.reserve(size_t(p.count) * p.batch * m.dev / 4);
+        p.xscale.reserve(size_t(p.count) * p.batch * m.groups);
+        std::vector<SdotJob> jobs(p.count);
+        for (int i = 0; i < p.count; ++i) {
+            const Matrix &mi = p.sd[i]->m;
+            jobs[i] = SdotJob{mi.codes.p,
+                              mi.norms.p,
+                              p.q.p + size_t(i) * p.batch * m.dev / 4,
+                              p.xscale.p + size_t(i) * p.batch * m.groups,
+                              p.ys[i],
+                              mi.out,
+                              mi.n_pad,
+                              block,
+                              p.batch};
+            block += mi.n_pad / kRowsPerBlock;
+        }
+        host.assign(reinterpret_cast<uint8_t *>(jobs.data()), reinterpret_cast<uint8_t *>(jobs.data() + p.count));
+    }
+    p.blocks = block;
+    p.jobs.reserve(host.size());
+    ND_HIP(hipMemcpy(p.jobs.p, host.data(), host.size(), hipMemcpyHostToDevice));
+}
+
+static void plan_run(Plan &p, hipStream_t s) {
+    const Matrix &m = *p.first;
+    // x_i is [batch][in] on the device; one transform launch per matrix input
+    for (int i = 0; i < p.count; ++i)
+        m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
+    if (!p.sdot) {
+        launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks,
+                       p.cq[0]->exact_crumbs, s);
+    } else {
+        const SdotHandle &h0 = *p.sd[0];
+        launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
+                             p.xscale.p, s);
+        launch_sdot_gemv(h0.geom(), SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, s);
+    }
+}
+
+static bool same_geometry(const Matrix &a, const Matrix &b) {
+    return a.in == b.in && a.bits == b.bits && a.group == b.group && std::memcmp(a.lut, b.lut, sizeof a.lut) == 0;
+}
+
+}  // namespace nd
+
+using namespace nd;
+
+// Runs f, converting exceptions into -1 plus the thread-local message. The
+// message is cleared first so a non-empty needle2_gpu_error() after a call
+// always belongs to that call.
+template <class F>
+static int guarded(F &&f) {
+    set_error("");
+    try {
+        f();
+        return 0;
+    } catch (const std::exception &e) {
+        set_error(e.what());
+    } catch (...) {
+        set_error("unknown error");
+    }
+    return -1;
+}
+
+static void poison(float *y, size_t n) {
+    if (!y) return;
+    const float nan = std::numeric_limits<float>::quiet_NaN();
+    for (size_t i = 0; i < n; ++i) y[i] = nan;
+}
+
+extern "C" {
+
+// ===================== reference ABI (drop-in) ===========================
+
+const char *needle2_native_features(void) { return "gfx950-hip;float32-accumulate;direct-packed-cq;int8-dot4"; }
+
+void *needle2_cq_create(const uint8_t *p, const uint16_t *n, int out, int in, int bits, int group, const float *cb) {
+    CqHandle *h = nullptr;
+    int rc = guarded([&] {
+        auto u = std::make_unique<CqHandle>();
+        u->m.upload(p, n, out, in, bits, group, cb, u->st.stream);
+        h = u.release();
+    });
+    return rc ? nullptr : h;
+}
+
+void needle2_cq_destroy(void *handle) { delete static_cast<CqHandle *>(handle); }
+
+void needle2_cq_linear(void *handle, const float *x, float *y, int batch, int threads) {
+    (void)threads;
+    auto *h = static_cast<CqHandle *>(handle);
+    if (guarded([&] { h->linear_host(x, y, batch); })) poison(y, size_t(batch > 0 ? batch : 0) * h->m.out);
+}
+
+// The reference's activation-table modes 1-3 are alternative CPU summation
+// schemes with the same tolerance contract (tests/test_native.py:39-40); on
+// the GPU every mode runs the packed GEMV.
+void needle2_cq_linear_lookup(void *handle, const float *x, float *y, int batch, int threads, int mode) {
+    (void)mode;
+    needle2_cq_linear(handle, x, y, batch, threads);
+}
+
+// cq.cpp:360-366: one shared x for several matrices.
+void needle2_cq_linear_many(void *const *handles, int count, const float *x, float *const *ys, int threads, int mode) {
+    (void)threads;
+    (void)mode;
+    for (int i = 0; i < count; ++i) needle2_cq_linear(handles[i], x, ys[i], 1, threads);
+}
+
+void needle2_cq_rows(void *handle, const int64_t *ids, float *y, int count) {
+    auto *h = static_cast<CqHandle *>(handle);
+    if (guarded([&] { h->rows_host(ids, y, count); })) poison(y, size_t(count > 0 ? count : 0) * h->m.in);
+}
+
+int needle2_sdot_supported(void) { return 1; }
+
+static void *sdot_create_impl(const uint8_t *p, const uint16_t *n, int out, int in, int bits, int group,
+                              const float *cb, int min_group) {
+    SdotHandle *h = nullptr;
+    int rc = guarded([&] {
+        ND_CHECK(bits == 2 || bits == 4, "SDOT requires CQ2/CQ4");
+        ND_CHECK(group >= min_group && group <= 131072, "SDOT group size outside the supported range");
+        ND_CHECK(bits == 4 || group >= 16, "SDOT CQ2 requires group >= 16");
+        auto u = std::make_unique<SdotHandle>();
+        u->m.upload(p, n, out, in, bits, group, cb, u->st.stream);
+        u->init_tables();
+        h = u.release();
+    });
+    return rc ? nullptr : h;
+}
+
+// sdot.cpp:351-354: bits in {2,4}, group in [64, 131072].
+void *needle2_sdot_create(const uint8_t *p, const uint16_t *n, int out, int in, int bits, int group, const float *cb) {
+    return sdot_create_impl(p, n, out, in, bits, group, cb, 64);
+}
+
+void needle2_sdot_destroy(void *p) { delete static_cast<SdotHandle *>(p); }
+
+void needle2_sdot_linear(void *p, const float *x, float *y, int batch, int threads) {
+    (void)threads;
+    auto *h = static_cast<SdotHandle *>(p);
+    if (guarded([&] { h->linear_host(x, y, batch); })) poison(y, size_t(batch > 0 ? batch : 0) * h->m.out);
+}
+
+// ===================== additive gfx950 exports ===========================
+
+const char *needle2_gpu_error(void) { return get_error(); }
+
+// Same arithmetic as needle2_sdot_create, with groups down to 8 (CQ4) / 16 (CQ2).
+void *needle2_gpu_sdot_create(const uint8_t *p, const uint16_t *n, int out, int in, int bits, int group,
+                              const float *cb) {
+    return sdot_create_impl(p, n, out, in, bits, group, cb, 8);
+}
+
+int needle2_gpu_cq_set_exact(void *handle, int exact) {
+    return guarded([&] { static_cast<CqHandle *>(handle)->exact_crumbs = exact != 0; });
+}
+
+int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {
+    auto *h = static_cast<CqHandle *>(handle);
+    return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream); });
+}
+
+int needle2_gpu_sdot_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {
+    auto *h = static_cast<SdotHandle *>(handle);
+    return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream); });
+}
+
+// Plans: count matrices sharing (in, bits, group, codebook); matrix i reads
+// d_x[i] ([batch][in], device) and writes d_y[i] ([batch][out_i], device).
+static void *plan_create(void *const *handles, int count, const float *const *d_x, float *const *d_y, int batch,
+                         bool sdot) {
+    Plan *out = nullptr;
+    guarded([&] {
+        ND_CHECK(count > 0 && batch > 0, "plan needs matrices and batch >= 1");
+        auto p = std::make_unique<Plan>();
+        p->sdot = sdot;
+        p->count = count;
+        p->batch = batch;
+        for (int i = 0; i < count; ++i) {
+            if (sdot) p->sd.push_back(static_cast<SdotHandle *>(handles[i]));
+            else p->cq.push_back(static_cast<CqHandle *>(handles[i]));
+            p->xs_in.push_back(d_x[i]);
+            p->ys.push_back(d_y[i]);
+        }
+        p->first = sdot ? &p->sd[0]->m : &p->cq[0]->m;
+        for (int i = 1; i < count; ++i)
+            ND_CHECK(same_geometry(*p->first, sdot ? p->sd[i]->m : p->cq[i]->m),
+                     "plan matrices must share input size, bits, group and codebook");
+        plan_upload(*p);
+        out = p.release();
+    });
+    return out;
+}
+
+void *needle2_gpu_cq_plan_create(void *const *handles, int count, const float *const *d_x, float *const *d_y,
+                                 int batch) {
+    return plan_create(handles, count, d_x, d_y, batch, false);
+}
+
+void *needle2_gpu_sdot_plan_create(void *const *handles, int count, const float *const *d_x, float *const *d_y,
+                                   int batch) {
+    return plan_create(handles, count, d_x, d_y, batch, true);
+}
+
+int needle2_gpu_plan_run(void *plan, void *stream) {
+    auto *p = static_cast<Plan *>(plan);
+    return guarded([&] { plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream); });
+}
+
+void needle2_gpu_plan_destroy(void *plan) { delete static_cast<Plan *>(plan); }
+
+// ---- memory, streams, events -------------------------------------------
+void *needle2_gpu_malloc(size_t bytes) {
+    void *p = nullptr;
+    if (guarded([&] { ND_HIP(hipMalloc(&p, bytes ? bytes : 1)); })) return nullptr;
+    return p;
+}
+
+void needle2_gpu_free(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+// kind: 0 host->device, 1 device->host, 2 device->device
+int needle2_gpu_memcpy(void *dst, const void *src, size_t bytes, int kind) {
+    return guarded([&] {
+        hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice : kind == 1 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+        ND_HIP(hipMemcpy(dst, src, bytes, k));
+    });
+}
+
+int needle2_gpu_memset(void *dst, int value, size_t bytes) {
+    return guarded([&] { ND_HIP(hipMemset(dst, value, bytes)); });
+}
+
+int needle2_gpu_synchronize(void) {
+    return guarded([&] { ND_HIP(hipDeviceSynchronize()); });
+}
+
+void *needle2_gpu_stream_create(void) {
+    hipStream_t s = nullptr;
+    if (guarded([&] { ND_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking)); })) return nullptr;
+    return s;
+}
+
+void needle2_gpu_stream_destroy(void *s) {
+    if (s) (void)hipStreamDestroy(static_cast<hipStream_t>(s));
+}
+
+int needle2_gpu_stream_synchronize(void *s) {
+    return guarded([&] { ND_HIP(hipStreamSynchronize(static_cast<hipStream_t>(s))); });
+}
+
+void *needle2_gpu_event_create(void) {
+    hipEvent_t e = nullptr;
+    if (guarded([&] { ND_HIP(hipEventCreate(&e)); })) return nullptr;
+    return e;
+}
+
+void needle2_gpu_event_destroy(void *e) {
+    if (e) (void)hipEventDestroy(static_cast<hipEvent_t>(e));
+}
+
+int needle2_gpu_event_record(void *e, void *s) {
+    return guarded([&] { ND_HIP(hipEventRecord(static_cast<hipEvent_t>(e), static_cast<hipStream_t>(s))); });
+}
+
+// milliseconds between two recorded events (waits for the second)
+float needle2_gpu_event_elapsed(void *start, void *stop) {
+    float ms = -1.0f;
+    guarded([&] {
+        ND_HIP(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+        ND_HIP(hipEventElapsedTime(&ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+    });
+    return ms;
+}
+
+// "name;gfx;cus;hbm_bytes;clock_khz"
+int needle2_gpu_device_info(char *buf, int len) {
+    return guarded([&] {
+        int dev = 0;
+        ND_HIP(hipGetDevice(&dev));
+        hipDeviceProp_t prop;
+        ND_HIP(hipGetDeviceProperties(&prop, dev));
+        std::string s = std::string(prop.name) + ";" + prop.gcnArchName + ";" + std::to_string(prop.multiProcessorCount) +
+                        ";" + std::to_string(prop.totalGlobalMem) + ";" + std::to_string(prop.clockRate);
+        std::snprintf(buf, size_t(len), "%s", s.c_str());
+    });
+}
+
+// ===================== engine (not on the GPU path yet) ==================
+// NativeEngine (needle2/native.py:307-663) binds these lazily; creation fails
+// through the reference's own error channel (engine.cpp:1499-1547).
+static const char *kNoEngine =
+    "needle2_engine_*: the gfx950 library provides the CQ/SDOT kernels and batched int8-KV attention; "
+    "the whole-model engine is not part of this library";
+
+const char *needle2_engine_error(void) { return get_error(); }
+void *needle2_engine_create(const void *, const void *, int, int, int) {
+    set_error(kNoEngine);
+    return nullptr;
+}
+void needle2_engine_destroy(void *) {}
+void needle2_engine_set_lookup(void *, int) {}
+int needle2_engine_set_sdot(void *) {
+    set_error(kNoEngine);
+    return -1;
+}
+void needle2_engine_reset(void *, int) {}
+int needle2_engine_cache_prefix(void *) {
+    set_error(kNoEngine);
+    return -1;
+}
+int needle2_engine_reset_to_prefix(void *) {
+    set_error(kNoEngine);
+    return -1;
+}
+int needle2_engine_step(void *, int, float *, float *) {
+    set_error(kNoEngine);
+    return -1;
+}
+int needle2_engine_prefill(void *, const int *, int, int, float *, float *) {
+    set_error(kNoEngine);
+    return -1;
+}
+int needle2_engine_step_candidates(void *, int, const int *, int, float *, float *) {
+    set_error(kNoEngine);
+    return -1;
+}
+int needle2_engine_decode_loop(void *, int, int, const void *, int *, int *) {
+    set_error(kNoEngine);
+    return -1;
+}
+int needle2_engine_import(void *, int, int, const int *, const int *, int, const float *, const float *) {
+    set_error(kNoEngine);
+    return -1;
+}
+int needle2_engine_set_int8_kv(void *, int) {
+    set_error(kNoEngine);
+    return -1;
+}
+size_t needle2_engine_kv_storage_bytes(void *) { return 0; }
+int needle2_engine_project_candidates(void *, const float *, const int *, int, float *) {
+    set_error(kNoEngine);
+    return -1;
+}
+
+}  // extern "C"

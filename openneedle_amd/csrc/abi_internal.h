@@ -1,0 +1,61 @@
+// Host-side objects behind the C ABI.
+#pragma once
+
+#include "common.h"
+
+namespace nd {
+
+void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stride, int nvec, int in, int padded,
+                          int out_limit, int group, float scale, float *scratch, hipStream_t s);
+
+// A CQ matrix resident in device memory (layout described in common.h).
+struct Matrix {
+    int out = 0, in = 0, bits = 0, group = 0, padded = 0, groups = 0, rowbytes = 0;
+    int kind = kNib, windows = 0, dev = 0, chunks = 0, n_pad = 0;
+    float scale = 1.0f;
+    float lut[16] = {};
+    float cb_raw[16] = {};
+    DevBuf<uint4> codes;
+    DevBuf<uint16_t> norms;
+
+    void upload(const uint8_t *packed, const uint16_t *norms, int out, int in, int bits, int group, const float *cb,
+                hipStream_t s);
+    CqGeom geom() const;
+    // rot[v] = FWHT(x[v]) over dev positions for nvec vectors.
+    void transform(const float *x, int x_stride, float *rot, int nvec, DevBuf<float> &big, hipStream_t s) const;
+};
+
+// Per-handle stream and grow-only staging buffers.
+struct Staging {
+    hipStream_t stream = nullptr;
+    DevBuf<float> x, rot, y, big, xs;
+    DevBuf<int32_t> q;
+    HostBuf<float> hx, hy;
+    Staging();
+    ~Staging();
+    Staging(const Staging &) = delete;
+    Staging &operator=(const Staging &) = delete;
+};
+
+struct CqHandle {
+    Matrix m;
+    Staging st;
+    bool exact_crumbs = false;  // 2-bit codes: per-code table (reference order) instead of pair table
+    void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
+    void linear_host(const float *x, float *y, int batch);
+    void rows_host(const int64_t *ids, float *y, int count);
+};
+
+struct SdotHandle {
+    Matrix m;
+    Staging st;
+    float centroid_scale = 1.0f;
+    uint32_t centroids[4] = {};
+    void init_tables();
+    SdotGeom geom() const;
+    void prepare_device(const float *d_x, int batch, int32_t *q, float *xs, hipStream_t s);
+    void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
+    void linear_host(const float *x, float *y, int batch);
+};
+
+}  // namespace nd

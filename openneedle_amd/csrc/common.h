@@ -1,0 +1,176 @@
+// Shared host/device definitions for the gfx950 CQ library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace nd {
+
+// ---------------------------------------------------------------------------
+// Errors: every entry point converts exceptions into the reference's error
+// channels (NULL / -1 / NaN-poisoned outputs) plus a thread-local message.
+// ---------------------------------------------------------------------------
+struct Error : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void set_error(const std::string &msg);
+const char *get_error();
+
+[[noreturn]] void hip_fail(const char *expr, hipError_t e, const char *file, int line);
+
+#define ND_HIP(expr)                                                   \
+    do {                                                               \
+        hipError_t nd_e_ = (expr);                                     \
+        if (nd_e_ != hipSuccess) nd::hip_fail(#expr, nd_e_, __FILE__, __LINE__); \
+    } while (0)
+
+#define ND_CHECK(cond, msg)                        \
+    do {                                           \
+        if (!(cond)) throw nd::Error(msg);         \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Owning device / pinned-host buffers.
+// ---------------------------------------------------------------------------
+template <class T>
+struct DevBuf {
+    T *p = nullptr;
+    size_t n = 0;
+    DevBuf() = default;
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    ~DevBuf() { release(); }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    // Grow-only allocation; contents are not preserved.
+    void reserve(size_t count) {
+        if (count <= n && p) return;
+        release();
+        ND_HIP(hipMalloc(reinterpret_cast<void **>(&p), (count ? count : 1) * sizeof(T)));
+        n = count;
+    }
+};
+
+template <class T>
+struct HostBuf {
+    T *p = nullptr;
+    size_t n = 0;
+    HostBuf() = default;
+    HostBuf(const HostBuf &) = delete;
+    HostBuf &operator=(const HostBuf &) = delete;
+    ~HostBuf() { release(); }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    void reserve(size_t count) {
+        if (count <= n && p) return;
+        release();
+        ND_HIP(hipHostMalloc(reinterpret_cast<void **>(&p), (count ? count : 1) * sizeof(T), hipHostMallocDefault));
+        n = count;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Device layout of a CQ matrix.
+//
+// Codes are re-laid out at create time into "chunk-major" order: a chunk is
+// 16 bytes of one row (32 four-bit codes or 64 two-bit codes) and
+//     codes[(chunk * n_pad + row)]   (one uint4 per (chunk, row))
+// so the 64 lanes of a wavefront, one row each, read 1 KiB contiguous per
+// chunk. Norms are fp16 [groups][n_pad]. Rows are padded to a multiple of
+// kRowsPerBlock with zero codes/norms; each row's codes are padded to a whole
+// number of table windows (kWindow positions) with zero codes.
+// CQ4 and CQ3 use 4-bit device codes (CQ3 is widened once at create time);
+// CQ2 and ternary use 2-bit device codes.
+// ---------------------------------------------------------------------------
+// Address-space qualifiers for device code: pointers read out of job
+// descriptors are cast so loads compile to global_* (not flat_*) and
+// wave-uniform activations to scalar s_load_*.
+#define ND_GLOBAL __attribute__((address_space(1)))
+#define ND_CONST __attribute__((address_space(4)))
+
+// 16-byte code chunk as a clang vector (trivially copyable from any address space)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRowsPerBlock = 256;  // rows per workgroup (one per lane, 4 waves)
+constexpr int kWindow = 256;        // code positions per LDS table window
+
+enum CodeKind : int { kNib = 0, kCrumb = 1 };
+
+struct CqGeom {
+    int kind;        // kNib or kCrumb
+    int group;       // group size (power of two >= 8)
+    int groups;      // real groups per row (padded / group)
+    int windows;     // table windows per row (device positions / kWindow)
+    int chunks;      // 16-byte chunks per row in the device layout
+    float scale;     // 1/sqrt(group), computed on the host as the reference does
+    float lut[16];   // fp32 codebook indexed by device code
+};
+
+struct CqJob {
+    const uint4 *codes;       // [chunks][n_pad]
+    const uint16_t *norms;    // [groups][n_pad]
+    const float *rot;         // transformed activations [batch][windows*kWindow]
+    float *y;                 // outputs [batch][rows]
+    int rows;
+    int n_pad;
+    int block_begin;          // first workgroup index of this job
+    int batch;
+};
+
+// int8 ("SDOT") path: same code layout, activations pre-quantized.
+struct SdotGeom {
+    int kind, group, groups, windows, chunks;
+    float centroid_scale;     // cs = max|cb|/127
+    uint32_t cent[4];         // int8 centroids packed little-endian (16 entries)
+};
+
+struct SdotJob {
+    const uint4 *codes;
+    const uint16_t *norms;
+    const int32_t *q;         // permuted int8 activations [batch][windows*kWindow/4]
+    const float *xs;          // per-group activation scales [batch][groups]
+    float *y;
+    int rows, n_pad, block_begin, batch;
+};
+
+// ---------------------------------------------------------------------------
+// Kernel launchers (implemented in the .hip files).
+// ---------------------------------------------------------------------------
+
+// Re-lay out row-major packed codes (rowbytes per row) into the device layout.
+// bits: 2, 3, 4 or 5 (ternary); CQ3 is widened to 4-bit codes.
+void launch_relayout(const uint8_t *packed, int rows, int rowbytes, int bits, int padded,
+                     uint4 *codes, int n_pad, int chunks, hipStream_t s);
+void launch_norms_transpose(const uint16_t *norms, int rows, int groups, uint16_t *out, int n_pad, hipStream_t s);
+
+// rot[v][0..dev) = FWHT per group of zero-padded x[v][0..in), for nvec vectors.
+void launch_transform(const float *x, int x_stride, float *rot, int rot_stride, int nvec, int in,
+                      int padded, int dev_positions, int group, float scale, hipStream_t s);
+
+// njobs == 0: one job passed by value (job0); otherwise jobs_dev[0..njobs).
+void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs_dev, int njobs, int total_blocks,
+                    bool exact, hipStream_t s);
+
+// Dequantize rows: y[i][0..in) = FWHT(cb[code]*norm) cropped; uses rot-sized scratch.
+void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, int n_pad,
+                    const int64_t *ids, int count, int in, int padded, float *scratch, float *y,
+                    hipStream_t s);
+
+// int8 path: quantize rot (already transformed) into permuted int8 + scales.
+void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded, int dev_positions,
+                          int group, int kind, int32_t *q, float *xs, hipStream_t s);
+void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs_dev, int njobs, int total_blocks,
+                      hipStream_t s);
+
+}  // namespace nd

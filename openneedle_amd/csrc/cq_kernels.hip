@@ -1,0 +1,495 @@
+// gfx950 kernels for the FP32 CQ path: device layout, activation FWHT,
+// packed GEMV and row dequantization.
+//
+// GEMV design (decode, HBM-bound): one lane per output row. Codes are stored
+// chunk-major (common.h) so a wavefront reads 1 KiB contiguous per 16-byte
+// chunk step. The activation side is turned into per-position product tables
+// in LDS, rebuilt per 256-position window and shared by the workgroup's 256
+// rows:
+//   4-bit codes:  T[p][c]     = cb[c] * rot[p]                       (16 floats)
+//   2-bit codes:  T[pp][c0|c1<<2] = cb[c0]*rot[2pp] + cb[c1]*rot[2pp+1]   (pair mode)
+//                 T[p][c]     = cb[c] * rot[p]                       (exact mode)
+// so each code costs one LDS read plus one add. For 4-bit codes the per-row
+// arithmetic is the reference's own sequence (cq.cpp:104-107, 161-162):
+// gd += cb[c]*x sequentially inside a group, then sum += gd*half(norm)
+// sequentially over groups; results are therefore bit-identical to the
+// reference's portable build. All files are compiled with -ffp-contract=off.
+#include "common.h"
+
+#include <hip/hip_fp16.h>
+
+namespace nd {
+
+namespace {
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+__device__ __forceinline__ float lds_at(const float *base, uint32_t byte_offset) {
+    return *reinterpret_cast<const float *>(reinterpret_cast<const char *>(base) + byte_offset);
+}
+
+// ---------------------------------------------------------------------------
+// Layout
+// ---------------------------------------------------------------------------
+__global__ void relayout_kernel(const uint8_t *__restrict__ packed, int rows, int rowbytes, int bits,
+                                int padded, uint4 *__restrict__ codes, int n_pad, int chunks) {
+    int r = blockIdx.x * blockDim.x + threadIdx.x;
+    int c = blockIdx.y;
+    if (r >= n_pad || c >= chunks) return;
+    uint32_t out[4] = {0, 0, 0, 0};
+    if (r < rows) {
+        const uint8_t *row = packed + static_cast<size_t>(r) * rowbytes;
+        if (bits == 3) {
+            // widen LSB-first 3-bit codes to nibbles: positions 32c .. 32c+31
+            for (int i = 0; i < 32; ++i) {
+                int pos = c * 32 + i;
+                if (pos >= padded) break;
+                int bit = pos * 3, byte = bit >> 3, shift = bit & 7;
+                unsigned word = row[byte];
+                if (shift + 3 > 8) word |= unsigned(row[byte + 1]) << 8;
+                unsigned code = (word >> shift) & 7u;
+                out[i >> 3] |= code << ((i & 7) * 4);
+            }
+        } else {
+            for (int i = 0; i < 16; ++i) {
+                int byte = c * 16 + i;
+                if (byte < rowbytes) out[i >> 2] |= uint32_t(row[byte]) << ((i & 3) * 8);
+            }
+        }
+    }
+    codes[static_cast<size_t>(c) * n_pad + r] = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+__global__ void norms_transpose_kernel(const uint16_t *__restrict__ norms, int rows, int groups,
+                                       uint16_t *__restrict__ out, int n_pad) {
+    int r = blockIdx.x * blockDim.x + threadIdx.x;
+    int g = blockIdx.y;
+    if (r >= n_pad) return;
+    out[static_cast<size_t>(g) * n_pad + r] = r < rows ? norms[static_cast<size_t>(r) * groups + g] : uint16_t(0);
+}
+
+// ---------------------------------------------------------------------------
+// FWHT per group (cq.cpp:30-46, 153-156). Each butterfly is the same
+// (a+b, a-b) on the same operands as the sequential loop, stage h ascending,
+// then one multiply by the host-computed float 1/sqrt(group): bit-exact.
+// One block owns a segment of `seg` positions (a multiple of the group).
+// Positions >= in are zero before the transform; positions in
+// [padded, out_limit) are stored as zero.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void transform_kernel(const float *__restrict__ x, int x_stride,
+                                                        float *__restrict__ rot, int rot_stride, int in,
+                                                        int padded, int out_limit, int group, float scale,
+                                                        int seg) {
+    extern __shared__ float buf[];
+    const int v = blockIdx.y;
+    const int base = blockIdx.x * seg;
+    const float *xv = x + static_cast<size_t>(v) * x_stride;
+    float *rv = rot + static_cast<size_t>(v) * rot_stride;
+    for (int i = threadIdx.x; i < seg; i += blockDim.x) {
+        int p = base + i;
+        buf[i] = p < in ? xv[p] : 0.0f;
+    }
+    __syncthreads();
+    if (base < padded) {
+        for (int h = 1; h < group; h <<= 1) {
+            for (int t = threadIdx.x; t < seg / 2; t += blockDim.x) {
+                int lo = (t / h) * 2 * h + (t % h);
+                float a = buf[lo], b = buf[lo + h];
+                buf[lo] = a + b;
+                buf[lo + h] = a - b;
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = threadIdx.x; i < seg; i += blockDim.x) {
+        int p = base + i;
+        if (p < out_limit) rv[p] = p < padded ? buf[i] * scale : 0.0f;
+    }
+}
+
+// Fallback for groups too large for one block's LDS: global-memory stages.
+__global__ void pad_copy_kernel(const float *__restrict__ x, int x_stride, float *__restrict__ rot,
+                                int rot_stride, int in, int n) {
+    int p = blockIdx.x * blockDim.x + threadIdx.x;
+    int v = blockIdx.y;
+    if (p < n) rot[static_cast<size_t>(v) * rot_stride + p] = p < in ? x[static_cast<size_t>(v) * x_stride + p] : 0.0f;
+}
+
+__global__ void butterfly_stage_kernel(float *__restrict__ rot, int rot_stride, int padded, int h) {
+    int t = blockIdx.x * blockDim.x + threadIdx.x;
+    int v = blockIdx.y;
+    if (t >= padded / 2) return;
+    float *rv = rot + static_cast<size_t>(v) * rot_stride;
+    int lo = (t / h) * 2 * h + (t % h);
+    float a = rv[lo], b = rv[lo + h];
+    rv[lo] = a + b;
+    rv[lo + h] = a - b;
+}
+
+__global__ void scale_crop_kernel(const float *__restrict__ src, int src_stride, float *__restrict__ dst,
+                                  int dst_stride, int padded, int out_limit, float scale) {
+    int p = blockIdx.x * blockDim.x + threadIdx.x;
+    int v = blockIdx.y;
+    if (p < out_limit)
+        dst[static_cast<size_t>(v) * dst_stride + p] =
+            p < padded ? src[static_cast<size_t>(v) * src_stride + p] * scale : 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Packed FP32 GEMV
+// ---------------------------------------------------------------------------
+template <int KIND, bool PAIR>
+struct TableShape {
+    static constexpr int kCodesPerChunk = KIND == kNib ? 32 : 64;
+    static constexpr int kChunksPerWindow = kWindow / kCodesPerChunk;
+    static constexpr int kEntries = (KIND == kNib || PAIR) ? 16 : 4;            // floats per slot
+    static constexpr int kSlots = (KIND == kCrumb && PAIR) ? kWindow / 2 : kWindow;  // slots per window
+    static constexpr int kFloats = kEntries * kSlots;
+};
+
+// Build the window's product table from rot[0..kWindow) of this window.
+template <int KIND, bool PAIR>
+__device__ __forceinline__ void build_table(float *__restrict__ T, const float *lut, float r_a, float r_b) {
+    using S = TableShape<KIND, PAIR>;
+    const int t = threadIdx.x;
+    if constexpr (KIND == kNib) {
+        // slot t: 16 products, written as four 16-byte stores
+        float4 *dst = reinterpret_cast<float4 *>(T + t * 16);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            dst[q] = make_float4(lut[4 * q] * r_a, lut[4 * q + 1] * r_a, lut[4 * q + 2] * r_a, lut[4 * q + 3] * r_a);
+    } else if constexpr (PAIR) {
+        // slot t (< 128): pair (2t, 2t+1); r_a = rot[2t], r_b = rot[2t+1]
+        if (t < S::kSlots) {
+            float p0[4], p1[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                p0[c] = lut[c] * r_a;
+                p1[c] = lut[c] * r_b;
+            }
+            float4 *dst = reinterpret_cast<float4 *>(T + t * 16);
+#pragma unroll
+            for (int hi = 0; hi < 4; ++hi)
+                dst[hi] = make_float4(p0[0] + p1[hi], p0[1] + p1[hi], p0[2] + p1[hi], p0[3] + p1[hi]);
+        }
+    } else {
+        reinterpret_cast<float4 *>(T)[t] = make_float4(lut[0] * r_a, lut[1] * r_a, lut[2] * r_a, lut[3] * r_a);
+    }
+}
+
+// rot values a thread needs for building one window's table.
+template <int KIND, bool PAIR>
+__device__ __forceinline__ void load_rot(const ND_GLOBAL float *__restrict__ rot_w, float &r_a, float &r_b) {
+    const int t = threadIdx.x;
+    if constexpr (KIND == kCrumb && PAIR) {
+        if (t < kWindow / 2) {
+            r_a = rot_w[2 * t];
+            r_b = rot_w[2 * t + 1];
+        } else {
+            r_a = r_b = 0.0f;
+        }
+    } else {
+        r_a = rot_w[t];
+        r_b = 0.0f;
+    }
+}
+
+// Compile-time group handling: GROUP > 0 is the group size when it is at most
+// one window; GROUP == 0 means group > kWindow (closes at window ends).
+template <int GROUP>
+struct NormsPerWindow {
+    static constexpr int value = GROUP > 0 ? kWindow / GROUP : 1;
+};
+
+template <int KIND, bool PAIR, int GROUP>
+struct WindowState {
+    static constexpr int kChunks = TableShape<KIND, PAIR>::kChunksPerWindow;
+    static constexpr int kNorms = NormsPerWindow<GROUP>::value;
+    u32x4 codes[kChunks];
+    uint16_t norms[kNorms];
+};
+
+template <int KIND, bool PAIR, int GROUP>
+__device__ __forceinline__ void load_window(WindowState<KIND, PAIR, GROUP> &st, const ND_GLOBAL u32x4 *__restrict__ codes,
+                                            const ND_GLOBAL uint16_t *__restrict__ norms, int n_pad, int row, int w,
+                                            int groups, int windows_per_group) {
+    constexpr int C = WindowState<KIND, PAIR, GROUP>::kChunks;
+    constexpr int NN = WindowState<KIND, PAIR, GROUP>::kNorms;
+    const ND_GLOBAL u32x4 *cw = codes + static_cast<size_t>(w) * C * n_pad + row;
+#pragma unroll
+    for (int c = 0; c < C; ++c) st.codes[c] = cw[static_cast<size_t>(c) * n_pad];
+    if constexpr (GROUP > 0) {
+#pragma unroll
+        for (int k = 0; k < NN; ++k) {
+            int g = w * NN + k;
+            st.norms[k] = g < groups ? norms[static_cast<size_t>(g) * n_pad + row] : uint16_t(0);
+        }
+    } else {
+        int g = w / windows_per_group;
+        st.norms[0] = g < groups ? norms[static_cast<size_t>(g) * n_pad + row] : uint16_t(0);
+    }
+}
+
+// Process one window: T is this window's table (LDS); positions are handled in
+// the reference's order; groups close at multiples of GROUP.
+template <int KIND, bool PAIR, int GROUP>
+__device__ __forceinline__ void compute_window(const WindowState<KIND, PAIR, GROUP> &st, const float *T,
+                                               float &sum, float &gd, int w, int groups, int windows_per_group) {
+    using S = TableShape<KIND, PAIR>;
+    constexpr int NN = WindowState<KIND, PAIR, GROUP>::kNorms;
+    // code positions per table slot
+    constexpr int PPS = (KIND == kCrumb && PAIR) ? 2 : 1;
+    int gbase = w * NN;  // first group index closing in this window (GROUP > 0)
+#pragma unroll
+    for (int c = 0; c < S::kChunksPerWindow; ++c) {
+        const uint32_t words[4] = {st.codes[c].x, st.codes[c].y, st.codes[c].z, st.codes[c].w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t wd = words[d];
+            if constexpr (KIND == kNib || PAIR) {
+                // 8 nibbles per dword: 4*nibble spread into bytes of X (even) and Y (odd)
+                uint32_t X = (wd << 2) & 0x3C3C3C3Cu;
+                uint32_t Y = (wd >> 2) & 0x3C3C3C3Cu;
+                // opaque to the optimizer: keeps one v_bfe per code instead of
+                // a re-derived shift+and pair
+                asm("" : "+v"(X));
+                asm("" : "+v"(Y));
+                const int slot0 = c * 32 + d * 8;  // slots per chunk = 32 for both layouts
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t src = (i & 1) ? Y : X;
+                    const int sh = (i >> 1) * 8;
+                    const uint32_t off = sh == 24 ? (src >> 24) : ((src >> sh) & 0xFFu);
+                    gd += lds_at(T + (slot0 + i) * 16, off);
+                    if constexpr (GROUP > 0) {
+                        const int pos_end = (slot0 + i + 1) * PPS;  // positions consumed in window
+                        if (pos_end % GROUP == 0) {
+                            const int k = pos_end / GROUP - 1;
+                            if (gbase + k < groups) sum += gd * h2f(st.norms[k]);
+                            gd = 0.0f;
+                        }
+                    }
+                }
+            } else {
+                // exact 2-bit: 16 crumbs per dword, 4*crumb spread into bytes of Z[m]
+                uint32_t Z[4] = {(wd << 2) & 0x0C0C0C0Cu, wd & 0x0C0C0C0Cu, (wd >> 2) & 0x0C0C0C0Cu,
+                                 (wd >> 4) & 0x0C0C0C0Cu};
+#pragma unroll
+                for (int m = 0; m < 4; ++m) asm("" : "+v"(Z[m]));
+                const int slot0 = c * 64 + d * 16;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t src = Z[i & 3];
+                    const int sh = (i >> 2) * 8;
+                    const uint32_t off = sh == 24 ? (src >> 24) : ((src >> sh) & 0xFFu);
+                    gd += lds_at(T + (slot0 + i) * 4, off);
+                    if constexpr (GROUP > 0) {
+                        const int pos_end = slot0 + i + 1;
+                        if (pos_end % GROUP == 0) {
+                            const int k = pos_end / GROUP - 1;
+                            if (gbase + k < groups) sum += gd * h2f(st.norms[k]);
+                            gd = 0.0f;
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (GROUP == 0) {
+        if ((w + 1) % windows_per_group == 0) {
+            if (w / windows_per_group < groups) sum += gd * h2f(st.norms[0]);
+            gd = 0.0f;
+        }
+    }
+}
+
+template <int KIND, bool PAIR, int GROUP>
+__global__ __launch_bounds__(kRowsPerBlock) void cq_gemv_kernel(CqJob job0, const CqJob *__restrict__ jobs, int njobs,
+                                                                CqGeom geom) {
+    using S = TableShape<KIND, PAIR>;
+    __shared__ __attribute__((aligned(16))) float T[2][S::kFloats];
+
+    const int blk = blockIdx.x;
+    CqJob J = job0;
+    if (njobs > 0) {
+        const ND_CONST CqJob *cj = (const ND_CONST CqJob *)(jobs);
+        int j = 0;
+        for (int k = 1; k < njobs; ++k)
+            if (cj[k].block_begin <= blk) j = k;
+        J.codes = cj[j].codes;
+        J.norms = cj[j].norms;
+        J.rot = cj[j].rot;
+        J.y = cj[j].y;
+        J.rows = cj[j].rows;
+        J.n_pad = cj[j].n_pad;
+        J.block_begin = cj[j].block_begin;
+        J.batch = cj[j].batch;
+    }
+    const ND_GLOBAL u32x4 *__restrict__ codes = (const ND_GLOBAL u32x4 *)(J.codes);
+    const ND_GLOBAL uint16_t *__restrict__ norms = (const ND_GLOBAL uint16_t *)(J.norms);
+    const int n_pad = J.n_pad, rows = J.rows, batch = J.batch;
+    const int row = (blk - J.block_begin) * kRowsPerBlock + threadIdx.x;
+    const int windows = geom.windows, groups = geom.groups;
+    const int wpg = GROUP == 0 ? geom.group / kWindow : 1;
+    const int dev = windows * kWindow;
+    float lut[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lut[i] = geom.lut[i];
+
+    for (int b = 0; b < batch; ++b) {
+        const ND_GLOBAL float *__restrict__ rot =
+            (const ND_GLOBAL float *)(J.rot) + static_cast<size_t>(b) * dev;
+        WindowState<KIND, PAIR, GROUP> cur, nxt;
+        float ra, rb, ra_next = 0.0f, rb_next = 0.0f;
+        load_window<KIND, PAIR, GROUP>(cur, codes, norms, n_pad, row, 0, groups, wpg);
+        load_rot<KIND, PAIR>(rot, ra, rb);
+        if (windows > 1) load_rot<KIND, PAIR>(rot + kWindow, ra_next, rb_next);
+        __syncthreads();  // previous batch row finished reading T[0]
+        build_table<KIND, PAIR>(T[0], lut, ra, rb);
+        __syncthreads();
+        float sum = 0.0f, gd = 0.0f;
+        for (int w = 0; w < windows; w += 2) {
+            // ---- window w (table T[0]) ----
+            if (w + 1 < windows) {
+                load_window<KIND, PAIR, GROUP>(nxt, codes, norms, n_pad, row, w + 1, groups, wpg);
+                build_table<KIND, PAIR>(T[1], lut, ra_next, rb_next);
+                if (w + 2 < windows) load_rot<KIND, PAIR>(rot + (w + 2) * kWindow, ra_next, rb_next);
+            }
+            compute_window<KIND, PAIR, GROUP>(cur, T[0], sum, gd, w, groups, wpg);
+            __syncthreads();
+            if (w + 1 >= windows) break;
+            // ---- window w+1 (table T[1]) ----
+            if (w + 2 < windows) {
+                load_window<KIND, PAIR, GROUP>(cur, codes, norms, n_pad, row, w + 2, groups, wpg);
+                build_table<KIND, PAIR>(T[0], lut, ra_next, rb_next);
+                if (w + 3 < windows) load_rot<KIND, PAIR>(rot + (w + 3) * kWindow, ra_next, rb_next);
+            }
+            compute_window<KIND, PAIR, GROUP>(nxt, T[1], sum, gd, w + 1, groups, wpg);
+            __syncthreads();
+        }
+        if (row < rows) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b) * rows + row] = sum;
+    }
+}
+
+template <int KIND, bool PAIR>
+void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
+    dim3 grid(blocks), block(kRowsPerBlock);
+    switch (g.group) {
+    case 8: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 8>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 16: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 16>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 32: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 64>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 128>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 256: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 0>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    }
+    ND_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// Row dequantization (cq.cpp:276-284): tmp = cb[code]*half(norm), then FWHT.
+// ---------------------------------------------------------------------------
+__global__ void dequant_rows_kernel(CqGeom geom, const uint4 *__restrict__ codes, const uint16_t *__restrict__ norms,
+                                    int n_pad, const int64_t *__restrict__ ids, int padded, float *__restrict__ tmp,
+                                    int tmp_stride) {
+    int p = blockIdx.x * blockDim.x + threadIdx.x;
+    int i = blockIdx.y;
+    if (p >= padded) return;
+    const int row = static_cast<int>(ids[i]);
+    const int cpc = geom.kind == kNib ? 32 : 64;
+    const int c = p / cpc, within = p % cpc;
+    const uint4 v = codes[static_cast<size_t>(c) * n_pad + row];
+    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+    unsigned code;
+    if (geom.kind == kNib) code = (words[within >> 3] >> ((within & 7) * 4)) & 15u;
+    else code = (words[within >> 4] >> ((within & 15) * 2)) & 3u;
+    const float norm = h2f(norms[static_cast<size_t>(p / geom.group) * n_pad + row]);
+    tmp[static_cast<size_t>(i) * tmp_stride + p] = geom.lut[code] * norm;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+void launch_relayout(const uint8_t *packed, int rows, int rowbytes, int bits, int padded, uint4 *codes, int n_pad,
+                     int chunks, hipStream_t s) {
+    dim3 grid((n_pad + 255) / 256, chunks), block(256);
+    hipLaunchKernelGGL(relayout_kernel, grid, block, 0, s, packed, rows, rowbytes, bits, padded, codes, n_pad, chunks);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_norms_transpose(const uint16_t *norms, int rows, int groups, uint16_t *out, int n_pad, hipStream_t s) {
+    dim3 grid((n_pad + 255) / 256, groups), block(256);
+    hipLaunchKernelGGL(norms_transpose_kernel, grid, block, 0, s, norms, rows, groups, out, n_pad);
+    ND_HIP(hipGetLastError());
+}
+
+static constexpr int kMaxLdsGroup = 16384;
+
+static void transform_impl(const float *x, int x_stride, float *rot, int rot_stride, int nvec, int in, int padded,
+                           int out_limit, int group, float scale, hipStream_t s, float *scratch) {
+    if (nvec <= 0) return;
+    if (group <= kMaxLdsGroup) {
+        int seg = group > 1024 ? group : 1024;
+        dim3 grid((out_limit + seg - 1) / seg, nvec), block(256);
+        hipLaunchKernelGGL(transform_kernel, grid, block, seg * sizeof(float), s, x, x_stride, rot, rot_stride, in,
+                           padded, out_limit, group, scale, seg);
+        ND_HIP(hipGetLastError());
+        return;
+    }
+    // large groups: stage through a padded scratch copy in global memory
+    ND_CHECK(scratch != nullptr, "internal: FWHT scratch missing for large group");
+    dim3 block(256);
+    dim3 gcopy((padded + 255) / 256, nvec);
+    hipLaunchKernelGGL(pad_copy_kernel, gcopy, block, 0, s, x, x_stride, scratch, padded, in, padded);
+    dim3 gst((padded / 2 + 255) / 256, nvec);
+    for (int h = 1; h < group; h <<= 1)
+        hipLaunchKernelGGL(butterfly_stage_kernel, gst, block, 0, s, scratch, padded, padded, h);
+    dim3 gout((out_limit + 255) / 256, nvec);
+    hipLaunchKernelGGL(scale_crop_kernel, gout, block, 0, s, scratch, padded, rot, rot_stride, padded, out_limit,
+                       scale);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_transform(const float *x, int x_stride, float *rot, int rot_stride, int nvec, int in, int padded,
+                      int dev_positions, int group, float scale, hipStream_t s) {
+    // Large groups need scratch; callers of this entry point guarantee
+    // group <= kMaxLdsGroup (larger groups go through launch_transform_big).
+    transform_impl(x, x_stride, rot, rot_stride, nvec, in, padded, dev_positions, group, scale, s, nullptr);
+}
+
+void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stride, int nvec, int in, int padded,
+                          int out_limit, int group, float scale, float *scratch, hipStream_t s) {
+    transform_impl(x, x_stride, rot, rot_stride, nvec, in, padded, out_limit, group, scale, s, scratch);
+}
+
+void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, bool exact,
+                    hipStream_t s) {
+    if (blocks <= 0) return;
+    if (g.kind == kNib) launch_gemv_kind<kNib, false>(g, job0, jobs, njobs, blocks, s);
+    else if (exact) launch_gemv_kind<kCrumb, false>(g, job0, jobs, njobs, blocks, s);
+    else launch_gemv_kind<kCrumb, true>(g, job0, jobs, njobs, blocks, s);
+}
+
+void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, int n_pad, const int64_t *ids,
+                    int count, int in, int padded, float *scratch, float *y, hipStream_t s) {
+    if (count <= 0) return;
+    dim3 grid((padded + 255) / 256, count), block(256);
+    hipLaunchKernelGGL(dequant_rows_kernel, grid, block, 0, s, g, codes, norms, n_pad, ids, padded, scratch, padded);
+    ND_HIP(hipGetLastError());
+    // in-place FWHT of scratch rows, cropped to `in` columns into y
+    float scale = g.scale;
+    if (g.group <= kMaxLdsGroup) {
+        transform_impl(scratch, padded, y, in, count, padded, padded, in, g.group, scale, s, nullptr);
+    } else {
+        dim3 gst((padded / 2 + 255) / 256, count);
+        for (int h = 1; h < g.group; h <<= 1)
+            hipLaunchKernelGGL(butterfly_stage_kernel, gst, block, 0, s, scratch, padded, padded, h);
+        dim3 gout((in + 255) / 256, count);
+        hipLaunchKernelGGL(scale_crop_kernel, gout, block, 0, s, scratch, padded, y, in, padded, in, scale);
+        ND_HIP(hipGetLastError());
+    }
+}
+
+}  // namespace nd

@@ -1,0 +1,367 @@
+"""ctypes access to the gfx950 CQ library (``libneedle2_native.so``).
+
+Mirrors ``needle2/native.py`` (NativeCQ, available, features, sdot_available)
+with the same names, argument validation and error messages, so code written
+against the reference's loader runs unchanged on this library. The library is
+selected the same way: ``NEEDLE2_NATIVE_LIBRARY`` if set, otherwise the
+in-tree build next to this file. There is no CPU fallback: without the HIP
+library every call raises.
+
+Additive (device-resident) API: :class:`Device`, :meth:`NativeCQ.linear_device`,
+:class:`Plan`, :class:`KVAttention`.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import functools
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+DEFAULT_LIBRARY = PKG / "libneedle2_native.so"
+
+_P = ct.c_void_p
+_I = ct.c_int
+
+
+def library_path() -> Path:
+    """needle2/native.py:76-84 semantics for NEEDLE2_NATIVE_LIBRARY, else the in-tree build."""
+    prebuilt = os.environ.get("NEEDLE2_NATIVE_LIBRARY")
+    if prebuilt is not None:
+        if not prebuilt.strip():
+            raise RuntimeError("NEEDLE2_NATIVE_LIBRARY must name a prebuilt OpenNeedle shared library")
+        target = Path(prebuilt).expanduser().resolve()
+        if not target.is_file():
+            raise RuntimeError(f"Prebuilt OpenNeedle library not found: {target}")
+        return target
+    if not DEFAULT_LIBRARY.is_file():
+        raise RuntimeError(f"gfx950 library not built: {DEFAULT_LIBRARY} (run python -m openneedle_amd.build)")
+    return DEFAULT_LIBRARY
+
+
+def _bind(lib, name, args, res=None):
+    f = getattr(lib, name)
+    f.argtypes = args
+    f.restype = res
+    return f
+
+
+@functools.lru_cache(maxsize=1)
+def _library():
+    lib = ct.CDLL(str(library_path()))
+    # reference ABI (needle2/native.py:128-145)
+    _bind(lib, "needle2_native_features", [], ct.c_char_p)
+    _bind(lib, "needle2_cq_create", [_P, _P, _I, _I, _I, _I, _P], _P)
+    _bind(lib, "needle2_cq_destroy", [_P])
+    _bind(lib, "needle2_cq_linear", [_P, _P, _P, _I, _I])
+    _bind(lib, "needle2_cq_linear_lookup", [_P, _P, _P, _I, _I, _I])
+    _bind(lib, "needle2_sdot_supported", [], _I)
+    _bind(lib, "needle2_sdot_create", [_P, _P, _I, _I, _I, _I, _P], _P)
+    _bind(lib, "needle2_sdot_destroy", [_P])
+    _bind(lib, "needle2_sdot_linear", [_P, _P, _P, _I, _I])
+    _bind(lib, "needle2_cq_rows", [_P, _P, _P, _I])
+    # additive gfx950 exports
+    _bind(lib, "needle2_gpu_error", [], ct.c_char_p)
+    _bind(lib, "needle2_gpu_sdot_create", [_P, _P, _I, _I, _I, _I, _P], _P)
+    _bind(lib, "needle2_gpu_cq_set_exact", [_P, _I], _I)
+    _bind(lib, "needle2_gpu_cq_linear_device", [_P, _P, _P, _I, _P], _I)
+    _bind(lib, "needle2_gpu_sdot_linear_device", [_P, _P, _P, _I, _P], _I)
+    _bind(lib, "needle2_gpu_cq_plan_create", [_P, _I, _P, _P, _I], _P)
+    _bind(lib, "needle2_gpu_sdot_plan_create", [_P, _I, _P, _P, _I], _P)
+    _bind(lib, "needle2_gpu_plan_run", [_P, _P], _I)
+    _bind(lib, "needle2_gpu_plan_destroy", [_P])
+    _bind(lib, "needle2_gpu_malloc", [ct.c_size_t], _P)
+    _bind(lib, "needle2_gpu_free", [_P])
+    _bind(lib, "needle2_gpu_memcpy", [_P, _P, ct.c_size_t, _I], _I)
+    _bind(lib, "needle2_gpu_memset", [_P, _I, ct.c_size_t], _I)
+    _bind(lib, "needle2_gpu_synchronize", [], _I)
+    _bind(lib, "needle2_gpu_stream_create", [], _P)
+    _bind(lib, "needle2_gpu_stream_destroy", [_P])
+    _bind(lib, "needle2_gpu_stream_synchronize", [_P], _I)
+    _bind(lib, "needle2_gpu_event_create", [], _P)
+    _bind(lib, "needle2_gpu_event_destroy", [_P])
+    _bind(lib, "needle2_gpu_event_record", [_P, _P], _I)
+    _bind(lib, "needle2_gpu_event_elapsed", [_P, _P], ct.c_float)
+    _bind(lib, "needle2_gpu_device_info", [ct.c_char_p, _I], _I)
+    return lib
+
+
+def available() -> bool:
+    try:
+        _library()
+        return True
+    except (OSError, RuntimeError):
+        return False
+
+
+def features() -> str:
+    return _library().needle2_native_features().decode()
+
+
+def sdot_available() -> bool:
+    return bool(_library().needle2_sdot_supported())
+
+
+def last_error() -> str:
+    return _library().needle2_gpu_error().decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc:
+        raise RuntimeError(f"{what}: {last_error()}")
+
+
+class NativeCQ:
+    """A packed ``[out, in]`` matrix resident on the GPU (needle2/native.py:165-279).
+
+    The codebook must already include ``1/sqrt(group_size)`` as in a CACT header.
+    ``bits=5`` denotes the official signed ternary crumb storage, with 3 centroids.
+    """
+
+    def __init__(self, packed, norms, shape, bits, group_size, codebook):
+        self.shape = tuple(int(v) for v in shape)
+        if len(self.shape) != 2 or min(self.shape) <= 0:
+            raise ValueError("NativeCQ requires a positive two-dimensional matrix shape")
+        self.bits, self.group_size = int(bits), int(group_size)
+        if self.bits not in (2, 3, 4, 5):
+            raise ValueError("CQ storage bits must be 2, 3, 4, or ternary marker 5")
+        if self.group_size < 8 or self.group_size & (self.group_size - 1):
+            raise ValueError("CQ group size must be a power of two >= 8")
+        out, dim = self.shape
+        limit = np.iinfo(np.int32).max
+        if max(out, dim, self.group_size) > limit or dim + self.group_size - 1 > limit:
+            raise ValueError("CQ dimensions exceed the native int32 interface")
+        padded = ((dim + self.group_size - 1) // self.group_size) * self.group_size
+        storage_bits = 2 if self.bits == 5 else self.bits
+        if padded * storage_bits > limit:
+            raise ValueError("CQ row bit count exceeds the native int32 interface")
+        self.packed = np.ascontiguousarray(packed, dtype=np.uint8).reshape(out, padded * storage_bits // 8)
+        self.norms = np.ascontiguousarray(norms, dtype=np.float16).reshape(out, padded // self.group_size)
+        self.codebook = np.ascontiguousarray(codebook, dtype=np.float32)
+        if self.codebook.shape != (3 if self.bits == 5 else 1 << self.bits,):
+            raise ValueError("Codebook has incorrect number of centroids")
+        if not np.isfinite(self.norms).all() or np.any(self.norms < 0):
+            raise ValueError("CQ norms must be finite and nonnegative")
+        if not np.isfinite(self.codebook).all() or not np.all(np.diff(self.codebook) > 0):
+            raise ValueError("CQ codebook must be finite and strictly sorted")
+        if self.bits == 5:
+            for shift in (0, 2, 4, 6):
+                if np.any(((self.packed >> shift) & 3) == 2):
+                    raise ValueError("Invalid ternary crumb code 2")
+        self._lib = _library()
+        self._handle = self._lib.needle2_cq_create(self.packed.ctypes.data, self.norms.ctypes.data,
+                                                   out, dim, self.bits, self.group_size,
+                                                   self.codebook.ctypes.data)
+        if not self._handle:
+            raise MemoryError(f"Could not construct native CQ matrix ({last_error()})")
+
+    @classmethod
+    def from_record(cls, record):
+        cb = record.codebook
+        if record.bits == 5 and cb is None:
+            cb = (np.array([-1.2240064, 0., 1.2240064], np.float64) / np.sqrt(record.group_size)).astype(np.float32)
+        return cls(record.packed, record.norms, record.shape, record.bits, record.group_size, cb)
+
+    def __del__(self):
+        for attr, fn in (("_sdot_handle", "needle2_sdot_destroy"), ("_handle", "needle2_cq_destroy")):
+            h = getattr(self, attr, None)
+            if h:
+                getattr(self._lib, fn)(h)
+                setattr(self, attr, None)
+
+    def set_exact(self, exact: bool = True) -> None:
+        """2-bit codes: per-code tables in the reference's summation order (slower)."""
+        _check(self._lib.needle2_gpu_cq_set_exact(self._handle, int(bool(exact))), "set_exact")
+
+    def linear(self, x, threads: int = 1, *, lookup: int = 0):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim < 1 or x.shape[-1] != self.shape[1]:
+            raise ValueError(f"Expected input last dimension {self.shape[1]}; got {x.shape}")
+        if not 1 <= int(threads) <= 256:
+            raise ValueError("threads must be between 1 and 256")
+        if (x.size // self.shape[1]) * self.shape[0] > np.iinfo(np.int32).max:
+            raise ValueError("CQ batch output count exceeds the native int32 interface")
+        y = np.empty(x.shape[:-1] + (self.shape[0],), dtype=np.float32)
+        if lookup not in (0, 1, 2, 3):
+            raise ValueError("lookup must be 0 (NEON), 1 (byte table), 2 (nibble table), or 3 (group byte table)")
+        if lookup:
+            self._lib.needle2_cq_linear_lookup(self._handle, x.ctypes.data, y.ctypes.data,
+                                               x.size // self.shape[1], int(threads), int(lookup))
+        else:
+            self._lib.needle2_cq_linear(self._handle, x.ctypes.data, y.ctypes.data,
+                                        x.size // self.shape[1], int(threads))
+        err = last_error()
+        if err:
+            raise RuntimeError(f"CQ linear failed: {err}")
+        return y
+
+    def _sdot(self, extended: bool):
+        if not getattr(self, "_sdot_handle", None):
+            create = self._lib.needle2_gpu_sdot_create if extended else self._lib.needle2_sdot_create
+            self._sdot_handle = create(self.packed.ctypes.data, self.norms.ctypes.data,
+                                       *self.shape, self.bits, self.group_size, self.codebook.ctypes.data)
+            if not self._sdot_handle:
+                raise RuntimeError(f"could not construct SDOT matrix ({last_error()})")
+        return self._sdot_handle
+
+    def linear_sdot(self, x, threads: int = 1):
+        """Approximate DotProd GEMV; additionally rounds rotated inputs and centroids to INT8."""
+        if self.bits not in (2, 4) or not 64 <= self.group_size <= 131072:
+            raise ValueError("SDOT requires CQ2/CQ4 and group size between 64 and 131072")
+        return self._linear_int8(x, threads, extended=False)
+
+    def linear_int8(self, x, threads: int = 1):
+        """The SDOT arithmetic for every group the GPU supports (CQ4 g>=8, CQ2 g>=16)."""
+        if self.bits not in (2, 4) or self.group_size > 131072 or self.group_size < (8 if self.bits == 4 else 16):
+            raise ValueError("int8 path requires CQ4 (group >= 8) or CQ2 (group >= 16), group <= 131072")
+        return self._linear_int8(x, threads, extended=True)
+
+    def _linear_int8(self, x, threads, extended):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.ndim < 1 or x.shape[-1] != self.shape[1] or not np.isfinite(x).all():
+            raise ValueError("SDOT input must have the expected last dimension and finite values")
+        if not 1 <= int(threads) <= 256:
+            raise ValueError("threads must be between 1 and 256")
+        handle = self._sdot(extended)
+        if (x.size // self.shape[1]) * self.shape[0] > np.iinfo(np.int32).max:
+            raise ValueError("SDOT batch output count exceeds the native int32 interface")
+        y = np.empty(x.shape[:-1] + (self.shape[0],), dtype=np.float32)
+        self._lib.needle2_sdot_linear(handle, x.ctypes.data, y.ctypes.data, x.size // self.shape[1], int(threads))
+        err = last_error()
+        if err:
+            raise RuntimeError(f"SDOT linear failed: {err}")
+        return y
+
+    def rows(self, ids):
+        ids = np.asarray(ids)
+        if ids.dtype.kind not in "iu":
+            raise TypeError("row indices must be integers")
+        ids_shape = ids.shape
+        ids = np.ascontiguousarray(ids, dtype=np.int64)
+        if np.any((ids < 0) | (ids >= self.shape[0])):
+            raise IndexError("CQ row index outside matrix")
+        result = np.empty(ids_shape + (self.shape[1],), dtype=np.float32)
+        self._lib.needle2_cq_rows(self._handle, ids.ctypes.data, result.ctypes.data, ids.size)
+        err = last_error()
+        if err:
+            raise RuntimeError(f"CQ rows failed: {err}")
+        return result
+
+    def dequantize(self):
+        return self.rows(np.arange(self.shape[0], dtype=np.int64))
+
+    # ---- device-resident entry points ----------------------------------
+    def linear_device(self, d_x, d_y, batch: int, stream=None) -> None:
+        _check(self._lib.needle2_gpu_cq_linear_device(self._handle, d_x, d_y, int(batch), stream), "cq linear_device")
+
+    def int8_device(self, d_x, d_y, batch: int, stream=None, extended: bool = True) -> None:
+        _check(self._lib.needle2_gpu_sdot_linear_device(self._sdot(extended), d_x, d_y, int(batch), stream),
+               "sdot linear_device")
+
+
+# --------------------------------------------------------------------------
+# Device helpers
+# --------------------------------------------------------------------------
+class DeviceArray:
+    """A device allocation owned by the library (freed on delete)."""
+
+    def __init__(self, nbytes: int):
+        self._lib = _library()
+        self.nbytes = int(nbytes)
+        self.ptr = self._lib.needle2_gpu_malloc(self.nbytes)
+        if not self.ptr:
+            raise MemoryError(f"device allocation of {nbytes} bytes failed: {last_error()}")
+
+    @classmethod
+    def from_host(cls, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = cls(a.nbytes)
+        d.upload(a)
+        return d
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        _check(self._lib.needle2_gpu_memcpy(self.ptr + offset, a.ctypes.data, a.nbytes, 0), "upload")
+
+    def download(self, out: np.ndarray, offset: int = 0) -> np.ndarray:
+        assert out.flags.c_contiguous and offset + out.nbytes <= self.nbytes
+        _check(self._lib.needle2_gpu_memcpy(out.ctypes.data, self.ptr + offset, out.nbytes, 1), "download")
+        return out
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            self._lib.needle2_gpu_free(self.ptr)
+            self.ptr = None
+
+
+class Stream:
+    def __init__(self):
+        self._lib = _library()
+        self.ptr = self._lib.needle2_gpu_stream_create()
+        if not self.ptr:
+            raise RuntimeError(last_error())
+
+    def synchronize(self):
+        _check(self._lib.needle2_gpu_stream_synchronize(self.ptr), "stream sync")
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            self._lib.needle2_gpu_stream_destroy(self.ptr)
+            self.ptr = None
+
+
+class Event:
+    def __init__(self):
+        self._lib = _library()
+        self.ptr = self._lib.needle2_gpu_event_create()
+        if not self.ptr:
+            raise RuntimeError(last_error())
+
+    def record(self, stream: Stream):
+        _check(self._lib.needle2_gpu_event_record(self.ptr, stream.ptr), "event record")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        return float(self._lib.needle2_gpu_event_elapsed(self.ptr, end.ptr))
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            self._lib.needle2_gpu_event_destroy(self.ptr)
+            self.ptr = None
+
+
+def synchronize() -> None:
+    _check(_library().needle2_gpu_synchronize(), "synchronize")
+
+
+def device_info() -> dict:
+    buf = ct.create_string_buffer(512)
+    _check(_library().needle2_gpu_device_info(buf, 512), "device_info")
+    name, arch, cus, mem, clk = buf.value.decode().split(";")
+    return {"name": name, "arch": arch, "cus": int(cus), "hbm_bytes": int(mem), "clock_khz": int(clk)}
+
+
+class Plan:
+    """Many same-geometry matrices, each with its own device input, in one GEMV launch."""
+
+    def __init__(self, matrices, d_x, d_y, batch: int = 1, int8: bool = False, extended: bool = True):
+        self._lib = _library()
+        n = len(matrices)
+        handles = (_P * n)(*[m._sdot(extended) if int8 else m._handle for m in matrices])
+        xs = (_P * n)(*[int(p) for p in d_x])
+        ys = (_P * n)(*[int(p) for p in d_y])
+        create = self._lib.needle2_gpu_sdot_plan_create if int8 else self._lib.needle2_gpu_cq_plan_create
+        self._keep = (matrices, handles, xs, ys)
+        self.ptr = create(handles, n, xs, ys, int(batch))
+        if not self.ptr:
+            raise RuntimeError(f"plan create failed: {last_error()}")
+
+    def run(self, stream: Stream | None = None) -> None:
+        _check(self._lib.needle2_gpu_plan_run(self.ptr, stream.ptr if stream else None), "plan run")
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            self._lib.needle2_gpu_plan_destroy(self.ptr)
+            self.ptr = None
