@@ -1,0 +1,204 @@
+"""Benchmark of the gfx950 CQ GEMV hot path (one GPU).
+
+Headline workload (``value``): 16 independent CQ4 8192x8192 group-32 matrices,
+FP32 activations, batch 1 - one "step" runs the activation FWHT and the packed
+GEMV for all 16 matrices (one plan: 16 transform launches + one GEMV launch).
+``value`` is effective HBM GB/s over the packed codes plus fp16 norms
+(603,979,776 B per step) with everything already resident in HBM. Weight stacks
+are rotated so consecutive steps never re-read data that could still sit in
+the 256 MB last-level cache.
+
+Also reported (``extra``): the same for CQ2, the int8 path on stacked CQ4
+4096x4096 matrices at batch 1/4/16, and the CPU baseline (the reference's own
+C++ library built from source, on all host cores, bounded sample).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "CQ4/CQ2 GEMV effective HBM GB/s (% of peak); decode tokens/s at batch 1/64"
+HBM_PEAK_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def random_cq(rng, count, rows, cols, bits, group):
+    """`count` matrices of uniform codes (uniform random bytes) and fp16 norms U[0.005, 0.05]."""
+    rowbytes = cols * bits // 8
+    packed = rng.integers(0, 256, size=(count, rows, rowbytes), dtype=np.uint8)
+    norms = rng.uniform(0.005, 0.05, size=(count, rows, cols // group)).astype(np.float16)
+    cb = (np.arange(1 << bits, dtype=np.float32) - np.float32(1 << (bits - 1)))
+    return packed, norms, cb
+
+
+class Stack:
+    """`rot` rotations of the same `count` matrices (distinct device copies) with plans."""
+
+    def __init__(self, packed, norms, cb, bits, group, batch, rot, int8=False):
+        from openneedle_amd.native import DeviceArray, NativeCQ, Plan
+        count, rows, _ = packed.shape
+        cols = norms.shape[2] * group
+        rng = np.random.default_rng(7)
+        self.x = [DeviceArray.from_host(rng.normal(size=(batch, cols)).astype(np.float32)) for _ in range(count)]
+        self.y = [DeviceArray(batch * rows * 4) for _ in range(count)]
+        self.mats, self.plans = [], []
+        for _ in range(rot):
+            mats = [NativeCQ(packed[i], norms[i], (rows, cols), bits, group, cb) for i in range(count)]
+            self.mats.append(mats)
+            self.plans.append(Plan(mats, [d.ptr for d in self.x], [d.ptr for d in self.y], batch=batch, int8=int8))
+        self.bytes_per_step = packed.nbytes + norms.nbytes
+
+    def run(self, steps, warmup, stream):
+        from openneedle_amd.native import Event, synchronize
+        for i in range(warmup):
+            self.plans[i % len(self.plans)].run(stream)
+        synchronize()
+        ev = [(Event(), Event()) for _ in range(steps)]
+        t0, t1 = Event(), Event()
+        t0.record(stream)
+        for i in range(steps):
+            self.plans[i % len(self.plans)].run(stream, gemv_events=ev[i])
+        t1.record(stream)
+        synchronize()
+        total_ms = t0.elapsed_ms(t1)
+        gemv_ms = [a.elapsed_ms(b) for a, b in ev]
+        return total_ms / steps, statistics.mean(gemv_ms), statistics.median(gemv_ms)
+
+
+def cpu_baseline(budget_s=20.0):
+    """The reference's CQ::linear (oracle/_ref) - or the oracle port - on one CQ4 8192x8192 g32 matrix."""
+    import oracle
+    cores = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(11)
+    packed, norms, cb = random_cq(rng, 1, 8192, 8192, 4, 32)
+    x = rng.normal(size=8192).astype(np.float32)
+    nbytes = packed.nbytes + norms.nbytes
+    kind = "reference"
+    try:
+        m = oracle.RefCQ(packed[0], norms[0], (8192, 8192), 4, 32, cb)
+        run = lambda: m.linear(x, cores)  # noqa: E731
+    except RuntimeError:
+        kind = "port"
+        run = lambda: oracle.cq_linear(packed[0], norms[0], (8192, 8192), 4, 32, cb, x, cores)  # noqa: E731
+    run()
+    times = []
+    start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - start < budget_s and len(times) < 50):
+        t = time.perf_counter_ns()
+        run()
+        times.append((time.perf_counter_ns() - t) / 1e9)
+    med = statistics.median(times)
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        model = "unknown"
+    return {
+        "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+        "sample": f"1 x CQ4 8192x8192 g32 FP32 GEMV (1/16 of the step), batch 1, {len(times)} runs, "
+                  f"median {med * 1e3:.1f} ms, {model}",
+        "ms_per_step_equivalent": round(med * 16 * 1e3, 2),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the CQ GEMV path shards by output rows with no exchange, and this "
+              "build runs on a single MI355X. Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from openneedle_amd.native import Stream, device_info
+    info = device_info()
+    log(f"device {info}")
+    stream = Stream()
+    rng = np.random.default_rng(20261201)
+
+    log("building CQ4 stack: 16 x 8192x8192 g32 (3 rotations)")
+    packed, norms, cb = random_cq(rng, 16, 8192, 8192, 4, 32)
+    cq4 = Stack(packed, norms, cb, 4, 32, batch=1, rot=3)
+    ms, gemv_mean, gemv_med = cq4.run(args.steps, args.warmup, stream)
+    nbytes = cq4.bytes_per_step
+    value = nbytes / (ms * 1e-3) / 1e9
+    achieved = nbytes / (gemv_mean * 1e-3) / 1e9
+    log(f"CQ4 step {ms * 1e3:.1f} us ({value:.0f} GB/s); GEMV kernel mean {gemv_mean * 1e3:.1f} us ({achieved:.0f} GB/s)")
+    del cq4, packed, norms
+
+    extra = {}
+    if not args.no_extra:
+        log("building CQ2 stack: 16 x 8192x8192 g32 (3 rotations)")
+        packed, norms, cb = random_cq(rng, 16, 8192, 8192, 2, 32)
+        cq2 = Stack(packed, norms, cb, 2, 32, batch=1, rot=3)
+        ms2, g2, _ = cq2.run(args.steps, args.warmup, stream)
+        extra["cq2_fp32_gbs"] = round(cq2.bytes_per_step / (ms2 * 1e-3) / 1e9, 1)
+        extra["cq2_fp32_gemv_us"] = round(g2 * 1e3, 2)
+        extra["cq2_fp32_gemv_frac"] = round(cq2.bytes_per_step / (g2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        log(f"CQ2 step {ms2 * 1e3:.1f} us; GEMV {g2 * 1e3:.1f} us ({extra['cq2_fp32_gbs']} GB/s step)")
+        del cq2, packed, norms
+
+        log("building int8 stack: 64 x CQ4 4096x4096 g32 (2 rotations)")
+        packed, norms, cb = random_cq(rng, 64, 4096, 4096, 4, 32)
+        for batch in (1, 4, 16):
+            st = Stack(packed, norms, cb, 4, 32, batch=batch, rot=2, int8=True)
+            msb, gb, _ = st.run(max(10, args.steps // 2), args.warmup, stream)
+            extra[f"int8_b{batch}_gbs"] = round(st.bytes_per_step / (msb * 1e-3) / 1e9, 1)
+            extra[f"int8_b{batch}_gemv_us"] = round(gb * 1e3, 2)
+            extra[f"int8_b{batch}_gemv_frac"] = round(st.bytes_per_step / (gb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            log(f"int8 b{batch} step {msb * 1e3:.1f} us; GEMV {gb * 1e3:.1f} us")
+            del st
+        del packed, norms
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (reference CQ::linear, all host cores)")
+        cpu = cpu_baseline()
+        log(f"CPU {cpu}")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 activations x 4-bit codebook weights (fp16 group norms)",
+        "data": "synthetic (uniform codes, fp16 norms U[0.005,0.05], x ~ N(0,1)); weights resident in HBM",
+        "config": {"workload": "16 x CQ4 8192x8192 g32 GEMV, FP32 path, batch 1", "bits": 4, "group": 32,
+                   "matrices": 16, "rows": 8192, "cols": 8192, "batch": 1, "weight_rotations": 3,
+                   "bytes_per_step": nbytes, "device": info["name"], "cus": info["cus"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "cq_gemv_kernel<kNib,false,32>", "gemv_mean_us": round(gemv_mean * 1e3, 2),
+                     "gemv_median_us": round(gemv_med * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

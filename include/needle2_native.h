@@ -1,0 +1,122 @@
+/*
+ * libneedle2_native.so - gfx950 (MI355X) implementation of OpenNeedle's
+ * quantized-matmul hot path behind the reference's C ABI.
+ *
+ * Section 1 is the reference's ctypes boundary; each declaration cites the
+ * reference definition it replaces. Section 2 lists additive exports (no
+ * counterpart in the reference). All entry points are synchronous unless they
+ * take a stream argument; pointers in section 1 are host pointers.
+ *
+ * Conventions (the reference's, needle2/native.py:165-279, cq.cpp:342-371):
+ *  - *_create returns NULL on failure; the reason is in needle2_gpu_error().
+ *  - void entry points have no error channel in the reference; on failure
+ *    this library fills the output with NaN and sets needle2_gpu_error().
+ *  - int entry points return 0 on success and -1 on failure.
+ *  - Calls on one handle must be serialized (needle2/native.py:313);
+ *    different handles may be used concurrently (each owns a HIP stream).
+ */
+#ifndef NEEDLE2_NATIVE_H
+#define NEEDLE2_NATIVE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ======================= 1. Reference ABI (drop-in) ===================== */
+
+/* needle2/csrc/cq.cpp:343-349 */
+const char *needle2_native_features(void);
+
+/* needle2/csrc/cq.cpp:350-352. Uploads packed codes ([out][padded*bits/8],
+ * LSB-first), fp16 norms ([out][padded/group]) and the codebook (16/8/4/3
+ * floats) to device memory; the host buffers are not retained.
+ * bits: 2, 3, 4 or 5 (ternary crumbs); group: power of two >= 8. */
+void *needle2_cq_create(const uint8_t *packed, const uint16_t *norms, int out, int in, int bits, int group,
+                        const float *codebook);
+/* needle2/csrc/cq.cpp:353 */
+void needle2_cq_destroy(void *handle);
+/* needle2/csrc/cq.cpp:354-356. x: [batch][in], y: [batch][out]. threads is ignored. */
+void needle2_cq_linear(void *handle, const float *x, float *y, int batch, int threads);
+/* needle2/csrc/cq.cpp:357-359. Every mode runs the GPU GEMV (same tolerance contract). */
+void needle2_cq_linear_lookup(void *handle, const float *x, float *y, int batch, int threads, int mode);
+/* needle2/csrc/cq.cpp:360-366. One x for count matrices; ys[i] receives matrix i's output. */
+void needle2_cq_linear_many(void *const *handles, int count, const float *x, float *const *ys, int threads,
+                            int mode);
+/* needle2/csrc/cq.cpp:367-370. y: [count][in] = FWHT(cb[code]*norm) of each row. */
+void needle2_cq_rows(void *handle, const int64_t *ids, float *y, int count);
+
+/* needle2/csrc/sdot.cpp:350. Always 1: the int8 path runs on the GPU. */
+int needle2_sdot_supported(void);
+/* needle2/csrc/sdot.cpp:351-354. NULL unless bits is 2 or 4 and 64 <= group <= 131072. */
+void *needle2_sdot_create(const uint8_t *packed, const uint16_t *norms, int out, int in, int bits, int group,
+                          const float *codebook);
+/* needle2/csrc/sdot.cpp:355 */
+void needle2_sdot_destroy(void *handle);
+/* needle2/csrc/sdot.cpp:356-359. Bit-exact with the reference's int8 arithmetic. */
+void needle2_sdot_linear(void *handle, const float *x, float *y, int batch, int threads);
+
+/* needle2/csrc/engine.cpp:1500-1548. The whole-model engine is not part of
+ * this library: needle2_engine_create returns NULL and needle2_engine_error()
+ * explains why (NativeEngine raises RuntimeError, needle2/native.py:405-406).
+ * The remaining needle2_engine_* symbols exist so that binding them succeeds. */
+const char *needle2_engine_error(void);
+void *needle2_engine_create(const void *config, const void *tensors, int count, int threads, int activation_bits);
+void needle2_engine_destroy(void *engine);
+
+/* ======================= 2. Additive gfx950 exports ===================== */
+
+/* Thread-local message of the last failed call on this thread ("" after a
+ * successful one). */
+const char *needle2_gpu_error(void);
+
+/* needle2_sdot_create with groups down to 8 (CQ4) or 16 (CQ2). Same
+ * arithmetic; the reference cannot run these groups (its ABI rejects them). */
+void *needle2_gpu_sdot_create(const uint8_t *packed, const uint16_t *norms, int out, int in, int bits, int group,
+                              const float *codebook);
+
+/* 2-bit codes: exact=1 sums per code in the reference's order (bit-exact,
+ * slower); exact=0 (default) uses two-code product tables. */
+int needle2_gpu_cq_set_exact(void *handle, int exact);
+
+/* Device-resident variants: d_x [batch][in] and d_y [batch][out] are device
+ * pointers; work is enqueued on `stream` (hipStream_t, NULL = the handle's
+ * stream) and the call returns without waiting. */
+int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream);
+int needle2_gpu_sdot_linear_device(void *sdot_handle, const float *d_x, float *d_y, int batch, void *stream);
+
+/* Plans: `count` handles of one geometry (in, bits, group, codebook), matrix
+ * i reading d_x[i] ([batch][in]) and writing d_y[i] ([batch][out_i]); one
+ * GEMV launch covers all of them. */
+void *needle2_gpu_cq_plan_create(void *const *handles, int count, const float *const *d_x, float *const *d_y,
+                                 int batch);
+void *needle2_gpu_sdot_plan_create(void *const *sdot_handles, int count, const float *const *d_x,
+                                   float *const *d_y, int batch);
+int needle2_gpu_plan_run(void *plan, void *stream);
+/* needle2_gpu_plan_run, recording gemv_start/gemv_stop (hipEvent_t) on the
+ * stream immediately before and after the GEMV launch. */
+int needle2_gpu_plan_run_timed(void *plan, void *stream, void *gemv_start, void *gemv_stop);
+void needle2_gpu_plan_destroy(void *plan);
+
+/* Device memory, streams and events (HIP runtime of this library). */
+void *needle2_gpu_malloc(size_t bytes);
+void needle2_gpu_free(void *ptr);
+int needle2_gpu_memcpy(void *dst, const void *src, size_t bytes, int kind); /* 0 H2D, 1 D2H, 2 D2D */
+int needle2_gpu_memset(void *dst, int value, size_t bytes);
+int needle2_gpu_synchronize(void);
+void *needle2_gpu_stream_create(void);
+void needle2_gpu_stream_destroy(void *stream);
+int needle2_gpu_stream_synchronize(void *stream);
+void *needle2_gpu_event_create(void);
+void needle2_gpu_event_destroy(void *event);
+int needle2_gpu_event_record(void *event, void *stream);
+float needle2_gpu_event_elapsed(void *start, void *stop); /* ms; waits for stop */
+int needle2_gpu_device_info(char *buf, int len);         /* "name;arch;cus;hbm_bytes;clock_khz" */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEEDLE2_NATIVE_H */

@@ -267,20 +267,23 @@ static void plan_upload(Plan &p) {
     ND_HIP(hipMemcpy(p.jobs.p, host.data(), host.size(), hipMemcpyHostToDevice));
 }
 
-static void plan_run(Plan &p, hipStream_t s) {
+static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hipEvent_t gemv_stop = nullptr) {
     const Matrix &m = *p.first;
     // x_i is [batch][in] on the device; one transform launch per matrix input
     for (int i = 0; i < p.count; ++i)
         m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
     if (!p.sdot) {
+        if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
         launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks,
                        p.cq[0]->exact_crumbs, s);
     } else {
         const SdotHandle &h0 = *p.sd[0];
         launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
                              p.xscale.p, s);
+        if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
         launch_sdot_gemv(h0.geom(), SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, s);
     }
+    if (gemv_stop) ND_HIP(hipEventRecord(gemv_stop, s));
 }
 
 static bool same_geometry(const Matrix &a, const Matrix &b) {
@@ -452,6 +455,16 @@ void *needle2_gpu_sdot_plan_create(void *const *handles, int count, const float 
 int needle2_gpu_plan_run(void *plan, void *stream) {
     auto *p = static_cast<Plan *>(plan);
     return guarded([&] { plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream); });
+}
+
+// As needle2_gpu_plan_run, also recording two events on the stream right
+// before and right after the GEMV launch (the plan's dominant kernel).
+int needle2_gpu_plan_run_timed(void *plan, void *stream, void *gemv_start, void *gemv_stop) {
+    auto *p = static_cast<Plan *>(plan);
+    return guarded([&] {
+        plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream, static_cast<hipEvent_t>(gemv_start),
+                 static_cast<hipEvent_t>(gemv_stop));
+    });
 }
 
 void needle2_gpu_plan_destroy(void *plan) { delete static_cast<Plan *>(plan); }

@@ -71,6 +71,7 @@ def _library():
     _bind(lib, "needle2_gpu_cq_plan_create", [_P, _I, _P, _P, _I], _P)
     _bind(lib, "needle2_gpu_sdot_plan_create", [_P, _I, _P, _P, _I], _P)
     _bind(lib, "needle2_gpu_plan_run", [_P, _P], _I)
+    _bind(lib, "needle2_gpu_plan_run_timed", [_P, _P, _P, _P], _I)
     _bind(lib, "needle2_gpu_plan_destroy", [_P])
     _bind(lib, "needle2_gpu_malloc", [ct.c_size_t], _P)
     _bind(lib, "needle2_gpu_free", [_P])
@@ -358,8 +359,13 @@ class Plan:
         if not self.ptr:
             raise RuntimeError(f"plan create failed: {last_error()}")
 
-    def run(self, stream: Stream | None = None) -> None:
-        _check(self._lib.needle2_gpu_plan_run(self.ptr, stream.ptr if stream else None), "plan run")
+    def run(self, stream: Stream | None = None, gemv_events=None) -> None:
+        s = stream.ptr if stream else None
+        if gemv_events is None:
+            _check(self._lib.needle2_gpu_plan_run(self.ptr, s), "plan run")
+        else:
+            start, stop = gemv_events
+            _check(self._lib.needle2_gpu_plan_run_timed(self.ptr, s, start.ptr, stop.ptr), "plan run")
 
     def __del__(self):
         if getattr(self, "ptr", None):

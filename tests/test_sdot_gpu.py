@@ -1,0 +1,84 @@
+"""GPU parity of the int8 ("SDOT") path: bit-exact with the oracle, whose
+arithmetic is bit-exact with the reference's own SdotCQ (tests/test_oracle.py),
+on identical seeded inputs."""
+import numpy as np
+import pytest
+
+import oracle
+from openneedle_amd.native import DeviceArray, NativeCQ, Plan, synchronize
+from tests.cases import activations, baseline, example
+
+pytestmark = pytest.mark.gpu
+
+
+def special_inputs(dim, seed):
+    x = activations((4, dim), seed=seed)
+    x[0] = 0           # zero groups: scale 1, q 0
+    x[1] = 0
+    x[1, 0] = 1        # one-hot
+    return x
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("group", [64, 128])
+@pytest.mark.parametrize("rows", [9, 129])
+def test_reference_domain_bit_exact(bits, group, rows):
+    packed, norms, cb, dense = example(bits, rows=rows, dim=257, group=group)
+    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    x = special_inputs(257, seed=315)
+    expected = oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x)
+    for threads in (1, 4):
+        np.testing.assert_array_equal(q.linear_sdot(x, threads), expected)
+    np.testing.assert_array_equal(q.linear_sdot(x[2]), expected[2])
+
+
+def test_reference_group_bounds():
+    packed, norms, cb, dense = example(4, group=32)
+    q = NativeCQ(packed, norms, dense.shape, 4, 32, cb)
+    with pytest.raises(ValueError, match="between 64 and 131072"):
+        q.linear_sdot(np.ones(257, np.float32))
+    with pytest.raises(ValueError, match="finite"):
+        NativeCQ(*example(4)[:2], (9, 257), 4, 128, example(4)[2]).linear_sdot(np.full(257, np.nan, np.float32))
+
+
+@pytest.mark.parametrize("bits,group", [(4, 8), (4, 16), (4, 32), (2, 16), (2, 32), (4, 256), (2, 512), (4, 1024)])
+def test_extended_groups_bit_exact(bits, group):
+    packed, norms, cb, dense = example(bits, rows=300, dim=1000, group=group, seed=group + bits)
+    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    x = special_inputs(1000, seed=group)
+    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
+
+
+def test_subnormal_scale_guard():
+    packed, norms, cb, dense = example(4, rows=4, dim=64, group=32)
+    q = NativeCQ(packed, norms, dense.shape, 4, 32, cb)
+    x = np.zeros(64, np.float32)
+    x[:32] = np.float32(4e-45)
+    x[40] = np.float32(1e-39)
+    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, dense.shape, 4, 32, cb, x))
+
+
+@pytest.mark.parametrize("batch", [1, 4, 16])
+def test_int8_4096_square_batches(batch):
+    """CQ4 4096 x 4096 g32, activations quantized per group after the FWHT."""
+    packed, norms, cb, _ = baseline(4, 4096, 4096, seed=33)
+    q = NativeCQ(packed, norms, (4096, 4096), 4, 32, cb)
+    x = activations((batch, 4096), seed=batch)
+    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, (4096, 4096), 4, 32, cb, x, 8))
+
+
+def test_int8_plan_many_matrices():
+    mats, d_x, d_y, expected = [], [], [], []
+    for i in range(3):
+        packed, norms, cb, _ = baseline(4, 512 + 64 * i, 1024, seed=500 + i)
+        m = NativeCQ(packed, norms, (512 + 64 * i, 1024), 4, 32, cb)
+        x = activations((2, 1024), seed=600 + i)
+        mats.append(m)
+        expected.append(oracle.sdot_linear(packed, norms, m.shape, 4, 32, cb, x))
+        d_x.append(DeviceArray.from_host(x))
+        d_y.append(DeviceArray(2 * 4 * m.shape[0]))
+    plan = Plan(mats, [d.ptr for d in d_x], [d.ptr for d in d_y], batch=2, int8=True)
+    plan.run()
+    synchronize()
+    for m, dy, e in zip(mats, d_y, expected):
+        np.testing.assert_array_equal(dy.download(np.empty((2, m.shape[0]), np.float32)), e)
