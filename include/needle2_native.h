@@ -38,7 +38,8 @@ void *needle2_cq_create(const uint8_t *packed, const uint16_t *norms, int out, i
                         const float *codebook);
 /* needle2/csrc/cq.cpp:353 */
 void needle2_cq_destroy(void *handle);
-/* needle2/csrc/cq.cpp:354-356. x: [batch][in], y: [batch][out]. threads is ignored. */
+/* needle2/csrc/cq.cpp:354-356. x: [batch][in], y: [batch][out]. threads is ignored.
+ * Bit-identical to the reference's portable (non-NEON) build for every bit width. */
 void needle2_cq_linear(void *handle, const float *x, float *y, int batch, int threads);
 /* needle2/csrc/cq.cpp:357-359. Every mode runs the GPU GEMV (same tolerance contract). */
 void needle2_cq_linear_lookup(void *handle, const float *x, float *y, int batch, int threads, int mode);
@@ -76,10 +77,6 @@ const char *needle2_gpu_error(void);
  * arithmetic; the reference cannot run these groups (its ABI rejects them). */
 void *needle2_gpu_sdot_create(const uint8_t *packed, const uint16_t *norms, int out, int in, int bits, int group,
                               const float *codebook);
-
-/* 2-bit codes: exact=1 sums per code in the reference's order (bit-exact,
- * slower); exact=0 (default) uses two-code product tables. */
-int needle2_gpu_cq_set_exact(void *handle, int exact);
 
 /* Device-resident variants: d_x [batch][in] and d_y [batch][out] are device
  * pointers; work is enqueued on `stream` (hipStream_t, NULL = the handle's

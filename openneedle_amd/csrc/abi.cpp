@@ -117,7 +117,7 @@ void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s
     st.rot.reserve(size_t(batch) * m.dev);
     m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
     const CqJob job{m.codes.p, m.norms.p, st.rot.p, d_y, m.out, m.n_pad, 0, batch};
-    launch_cq_gemv(m.geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, exact_crumbs, s);
+    launch_cq_gemv(m.geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, s);
 }
 
 void CqHandle::linear_host(const float *x, float *y, int batch) {
@@ -274,8 +274,7 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
         m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
     if (!p.sdot) {
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
-        launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks,
-                       p.cq[0]->exact_crumbs, s);
+        launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s);
     } else {
         const SdotHandle &h0 = *p.sd[0];
         launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
@@ -399,10 +398,6 @@ const char *needle2_gpu_error(void) { return get_error(); }
 void *needle2_gpu_sdot_create(const uint8_t *p, const uint16_t *n, int out, int in, int bits, int group,
                               const float *cb) {
     return sdot_create_impl(p, n, out, in, bits, group, cb, 8);
-}
-
-int needle2_gpu_cq_set_exact(void *handle, int exact) {
-    return guarded([&] { static_cast<CqHandle *>(handle)->exact_crumbs = exact != 0; });
 }
 
 int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {

@@ -40,7 +40,6 @@ struct Staging {
 struct CqHandle {
     Matrix m;
     Staging st;
-    bool exact_crumbs = false;  // 2-bit codes: per-code table (reference order) instead of pair table
     void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
     void linear_host(const float *x, float *y, int batch);
     void rows_host(const int64_t *ids, float *y, int count);

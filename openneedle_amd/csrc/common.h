@@ -160,7 +160,7 @@ void launch_transform(const float *x, int x_stride, float *rot, int rot_stride, 
 
 // njobs == 0: one job passed by value (job0); otherwise jobs_dev[0..njobs).
 void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs_dev, int njobs, int total_blocks,
-                    bool exact, hipStream_t s);
+                    hipStream_t s);
 
 // Dequantize rows: y[i][0..in) = FWHT(cb[code]*norm) cropped; uses rot-sized scratch.
 void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, int n_pad,

@@ -3,17 +3,10 @@
 //
 // GEMV design (decode, HBM-bound): one lane per output row. Codes are stored
 // chunk-major (common.h) so a wavefront reads 1 KiB contiguous per 16-byte
-// chunk step. The activation side is turned into per-position product tables
-// in LDS, rebuilt per 256-position window and shared by the workgroup's 256
-// rows:
-//   4-bit codes:  T[p][c]     = cb[c] * rot[p]                       (16 floats)
-//   2-bit codes:  T[pp][c0|c1<<2] = cb[c0]*rot[2pp] + cb[c1]*rot[2pp+1]   (pair mode)
-//                 T[p][c]     = cb[c] * rot[p]                       (exact mode)
-// so each code costs one LDS read plus one add. For 4-bit codes the per-row
-// arithmetic is the reference's own sequence (cq.cpp:104-107, 161-162):
-// gd += cb[c]*x sequentially inside a group, then sum += gd*half(norm)
-// sequentially over groups; results are therefore bit-identical to the
-// reference's portable build. All files are compiled with -ffp-contract=off.
+// chunk step. The activation side becomes per-position product tables in LDS,
+// rebuilt per 256-position window and shared by the workgroup's 256 rows, so
+// each code costs one LDS read plus one add, in the reference's own order.
+// All files are compiled with -ffp-contract=off.
 #include "common.h"
 
 #include <hip/hip_fp16.h>
@@ -137,29 +130,37 @@ __global__ void scale_crop_kernel(const float *__restrict__ src, int src_stride,
 
 // ---------------------------------------------------------------------------
 // Packed FP32 GEMV
+//
+// Per 256-position window the workgroup builds a product table in LDS:
+//   4-bit codes: slot p (one position), 16 floats  T[p][c]        = cb[c]*rot[p]
+//   2-bit codes: slot s (two positions), 16 float2 T[s][c0|c1<<2] = (cb[c0]*rot[2s], cb[c1]*rot[2s+1])
+// Each lane (one row) walks its codes in order: one LDS read per 4-bit code
+// or per pair of 2-bit codes, then gd += product (sequentially, one add per
+// code). Groups close with sum += gd * half(norm). This is the reference's
+// exact operation sequence (cq.cpp:104-107, 157-164, 185-194) for every bit
+// width, so results are bit-identical to its portable build.
 // ---------------------------------------------------------------------------
-template <int KIND, bool PAIR>
+template <int KIND>
 struct TableShape {
     static constexpr int kCodesPerChunk = KIND == kNib ? 32 : 64;
     static constexpr int kChunksPerWindow = kWindow / kCodesPerChunk;
-    static constexpr int kEntries = (KIND == kNib || PAIR) ? 16 : 4;            // floats per slot
-    static constexpr int kSlots = (KIND == kCrumb && PAIR) ? kWindow / 2 : kWindow;  // slots per window
-    static constexpr int kFloats = kEntries * kSlots;
+    static constexpr int kPositionsPerSlot = KIND == kNib ? 1 : 2;
+    static constexpr int kSlots = kWindow / kPositionsPerSlot;    // slots per window
+    static constexpr int kSlotFloats = KIND == kNib ? 16 : 32;    // floats per slot
+    static constexpr int kFloats = kSlots * kSlotFloats;          // 4096 floats = 16 KiB either way
 };
 
-// Build the window's product table from rot[0..kWindow) of this window.
-template <int KIND, bool PAIR>
+// Build one window's table. Thread t owns slot t (4-bit: t < 256; 2-bit: t < 128).
+template <int KIND>
 __device__ __forceinline__ void build_table(float *__restrict__ T, const float *lut, float r_a, float r_b) {
-    using S = TableShape<KIND, PAIR>;
+    using S = TableShape<KIND>;
     const int t = threadIdx.x;
     if constexpr (KIND == kNib) {
-        // slot t: 16 products, written as four 16-byte stores
-        float4 *dst = reinterpret_cast<float4 *>(T + t * 16);
+        float4 *dst = reinterpret_cast<float4 *>(T + t * S::kSlotFloats);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             dst[q] = make_float4(lut[4 * q] * r_a, lut[4 * q + 1] * r_a, lut[4 * q + 2] * r_a, lut[4 * q + 3] * r_a);
-    } else if constexpr (PAIR) {
-        // slot t (< 128): pair (2t, 2t+1); r_a = rot[2t], r_b = rot[2t+1]
+    } else {
         if (t < S::kSlots) {
             float p0[4], p1[4];
 #pragma unroll
@@ -167,21 +168,22 @@ __device__ __forceinline__ void build_table(float *__restrict__ T, const float *
                 p0[c] = lut[c] * r_a;
                 p1[c] = lut[c] * r_b;
             }
-            float4 *dst = reinterpret_cast<float4 *>(T + t * 16);
+            // entry n = c0 | c1 << 2 holds (p0[c0], p1[c1]); two entries per float4
+            float4 *dst = reinterpret_cast<float4 *>(T + t * S::kSlotFloats);
 #pragma unroll
-            for (int hi = 0; hi < 4; ++hi)
-                dst[hi] = make_float4(p0[0] + p1[hi], p0[1] + p1[hi], p0[2] + p1[hi], p0[3] + p1[hi]);
+            for (int hi = 0; hi < 4; ++hi) {
+                dst[2 * hi] = make_float4(p0[0], p1[hi], p0[1], p1[hi]);
+                dst[2 * hi + 1] = make_float4(p0[2], p1[hi], p0[3], p1[hi]);
+            }
         }
-    } else {
-        reinterpret_cast<float4 *>(T)[t] = make_float4(lut[0] * r_a, lut[1] * r_a, lut[2] * r_a, lut[3] * r_a);
     }
 }
 
 // rot values a thread needs for building one window's table.
-template <int KIND, bool PAIR>
+template <int KIND>
 __device__ __forceinline__ void load_rot(const ND_GLOBAL float *__restrict__ rot_w, float &r_a, float &r_b) {
     const int t = threadIdx.x;
-    if constexpr (KIND == kCrumb && PAIR) {
+    if constexpr (KIND == kCrumb) {
         if (t < kWindow / 2) {
             r_a = rot_w[2 * t];
             r_b = rot_w[2 * t + 1];
@@ -194,27 +196,27 @@ __device__ __forceinline__ void load_rot(const ND_GLOBAL float *__restrict__ rot
     }
 }
 
-// Compile-time group handling: GROUP > 0 is the group size when it is at most
-// one window; GROUP == 0 means group > kWindow (closes at window ends).
+// GROUP > 0: the group size, at most one window; GROUP == 0: group > kWindow
+// (a group spans whole windows and closes at a window end).
 template <int GROUP>
 struct NormsPerWindow {
     static constexpr int value = GROUP > 0 ? kWindow / GROUP : 1;
 };
 
-template <int KIND, bool PAIR, int GROUP>
+template <int KIND, int GROUP>
 struct WindowState {
-    static constexpr int kChunks = TableShape<KIND, PAIR>::kChunksPerWindow;
+    static constexpr int kChunks = TableShape<KIND>::kChunksPerWindow;
     static constexpr int kNorms = NormsPerWindow<GROUP>::value;
     u32x4 codes[kChunks];
     uint16_t norms[kNorms];
 };
 
-template <int KIND, bool PAIR, int GROUP>
-__device__ __forceinline__ void load_window(WindowState<KIND, PAIR, GROUP> &st, const ND_GLOBAL u32x4 *__restrict__ codes,
+template <int KIND, int GROUP>
+__device__ __forceinline__ void load_window(WindowState<KIND, GROUP> &st, const ND_GLOBAL u32x4 *__restrict__ codes,
                                             const ND_GLOBAL uint16_t *__restrict__ norms, int n_pad, int row, int w,
                                             int groups, int windows_per_group) {
-    constexpr int C = WindowState<KIND, PAIR, GROUP>::kChunks;
-    constexpr int NN = WindowState<KIND, PAIR, GROUP>::kNorms;
+    constexpr int C = WindowState<KIND, GROUP>::kChunks;
+    constexpr int NN = WindowState<KIND, GROUP>::kNorms;
     const ND_GLOBAL u32x4 *cw = codes + static_cast<size_t>(w) * C * n_pad + row;
 #pragma unroll
     for (int c = 0; c < C; ++c) st.codes[c] = cw[static_cast<size_t>(c) * n_pad];
@@ -230,66 +232,49 @@ __device__ __forceinline__ void load_window(WindowState<KIND, PAIR, GROUP> &st, 
     }
 }
 
-// Process one window: T is this window's table (LDS); positions are handled in
-// the reference's order; groups close at multiples of GROUP.
-template <int KIND, bool PAIR, int GROUP>
-__device__ __forceinline__ void compute_window(const WindowState<KIND, PAIR, GROUP> &st, const float *T,
-                                               float &sum, float &gd, int w, int groups, int windows_per_group) {
-    using S = TableShape<KIND, PAIR>;
-    constexpr int NN = WindowState<KIND, PAIR, GROUP>::kNorms;
-    // code positions per table slot
-    constexpr int PPS = (KIND == kCrumb && PAIR) ? 2 : 1;
-    int gbase = w * NN;  // first group index closing in this window (GROUP > 0)
+// Process one window against its table T (LDS), in the reference's order.
+template <int KIND, int GROUP>
+__device__ __forceinline__ void compute_window(const WindowState<KIND, GROUP> &st, const float *T, float &sum,
+                                               float &gd, int w, int groups, int windows_per_group) {
+    using S = TableShape<KIND>;
+    constexpr int NN = WindowState<KIND, GROUP>::kNorms;
+    const int gbase = w * NN;  // first group index closing in this window (GROUP > 0)
 #pragma unroll
     for (int c = 0; c < S::kChunksPerWindow; ++c) {
         const uint32_t words[4] = {st.codes[c].x, st.codes[c].y, st.codes[c].z, st.codes[c].w};
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const uint32_t wd = words[d];
-            if constexpr (KIND == kNib || PAIR) {
-                // 8 nibbles per dword: 4*nibble spread into bytes of X (even) and Y (odd)
-                uint32_t X = (wd << 2) & 0x3C3C3C3Cu;
-                uint32_t Y = (wd >> 2) & 0x3C3C3C3Cu;
-                // opaque to the optimizer: keeps one v_bfe per code instead of
-                // a re-derived shift+and pair
-                asm("" : "+v"(X));
-                asm("" : "+v"(Y));
-                const int slot0 = c * 32 + d * 8;  // slots per chunk = 32 for both layouts
+            // 8 nibbles per dword (one 4-bit code, or two 2-bit codes, per slot),
+            // spread as byte offsets into X (even nibbles) and Y (odd nibbles).
+            constexpr int kShift = KIND == kNib ? 2 : 3;           // entry bytes: 4 or 8
+            constexpr uint32_t kMask = KIND == kNib ? 0x3C3C3C3Cu : 0x78787878u;
+            uint32_t X = (wd << kShift) & kMask;
+            uint32_t Y = (wd >> (4 - kShift)) & kMask;
+            // opaque to the optimizer: keeps one v_bfe per slot instead of a
+            // re-derived shift+and pair
+            asm("" : "+v"(X));
+            asm("" : "+v"(Y));
+            const int slot0 = c * 32 + d * 8;  // 32 slots per chunk for both layouts
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint32_t src = (i & 1) ? Y : X;
-                    const int sh = (i >> 1) * 8;
-                    const uint32_t off = sh == 24 ? (src >> 24) : ((src >> sh) & 0xFFu);
-                    gd += lds_at(T + (slot0 + i) * 16, off);
-                    if constexpr (GROUP > 0) {
-                        const int pos_end = (slot0 + i + 1) * PPS;  // positions consumed in window
-                        if (pos_end % GROUP == 0) {
-                            const int k = pos_end / GROUP - 1;
-                            if (gbase + k < groups) sum += gd * h2f(st.norms[k]);
-                            gd = 0.0f;
-                        }
-                    }
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t src = (i & 1) ? Y : X;
+                const int sh = (i >> 1) * 8;
+                const uint32_t off = sh == 24 ? (src >> 24) : ((src >> sh) & 0xFFu);
+                const float *slot = T + (slot0 + i) * S::kSlotFloats;
+                if constexpr (KIND == kNib) {
+                    gd += lds_at(slot, off);
+                } else {
+                    const float2 pr = *reinterpret_cast<const float2 *>(reinterpret_cast<const char *>(slot) + off);
+                    gd += pr.x;
+                    gd += pr.y;
                 }
-            } else {
-                // exact 2-bit: 16 crumbs per dword, 4*crumb spread into bytes of Z[m]
-                uint32_t Z[4] = {(wd << 2) & 0x0C0C0C0Cu, wd & 0x0C0C0C0Cu, (wd >> 2) & 0x0C0C0C0Cu,
-                                 (wd >> 4) & 0x0C0C0C0Cu};
-#pragma unroll
-                for (int m = 0; m < 4; ++m) asm("" : "+v"(Z[m]));
-                const int slot0 = c * 64 + d * 16;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const uint32_t src = Z[i & 3];
-                    const int sh = (i >> 2) * 8;
-                    const uint32_t off = sh == 24 ? (src >> 24) : ((src >> sh) & 0xFFu);
-                    gd += lds_at(T + (slot0 + i) * 4, off);
-                    if constexpr (GROUP > 0) {
-                        const int pos_end = slot0 + i + 1;
-                        if (pos_end % GROUP == 0) {
-                            const int k = pos_end / GROUP - 1;
-                            if (gbase + k < groups) sum += gd * h2f(st.norms[k]);
-                            gd = 0.0f;
-                        }
+                if constexpr (GROUP > 0) {
+                    const int pos_end = (slot0 + i + 1) * S::kPositionsPerSlot;  // positions consumed in window
+                    if (pos_end % GROUP == 0) {
+                        const int k = pos_end / GROUP - 1;
+                        if (gbase + k < groups) sum += gd * h2f(st.norms[k]);
+                        gd = 0.0f;
                     }
                 }
             }
@@ -303,10 +288,10 @@ __device__ __forceinline__ void compute_window(const WindowState<KIND, PAIR, GRO
     }
 }
 
-template <int KIND, bool PAIR, int GROUP>
+template <int KIND, int GROUP>
 __global__ __launch_bounds__(kRowsPerBlock) void cq_gemv_kernel(CqJob job0, const CqJob *__restrict__ jobs, int njobs,
                                                                 CqGeom geom) {
-    using S = TableShape<KIND, PAIR>;
+    using S = TableShape<KIND>;
     __shared__ __attribute__((aligned(16))) float T[2][S::kFloats];
 
     const int blk = blockIdx.x;
@@ -337,51 +322,51 @@ __global__ __launch_bounds__(kRowsPerBlock) void cq_gemv_kernel(CqJob job0, cons
     for (int i = 0; i < 16; ++i) lut[i] = geom.lut[i];
 
     for (int b = 0; b < batch; ++b) {
-        const ND_GLOBAL float *__restrict__ rot =
-            (const ND_GLOBAL float *)(J.rot) + static_cast<size_t>(b) * dev;
-        WindowState<KIND, PAIR, GROUP> cur, nxt;
+        const ND_GLOBAL float *__restrict__ rot = (const ND_GLOBAL float *)(J.rot) + static_cast<size_t>(b) * dev;
+        WindowState<KIND, GROUP> cur, nxt;
         float ra, rb, ra_next = 0.0f, rb_next = 0.0f;
-        load_window<KIND, PAIR, GROUP>(cur, codes, norms, n_pad, row, 0, groups, wpg);
-        load_rot<KIND, PAIR>(rot, ra, rb);
-        if (windows > 1) load_rot<KIND, PAIR>(rot + kWindow, ra_next, rb_next);
-        __syncthreads();  // previous batch row finished reading T[0]
-        build_table<KIND, PAIR>(T[0], lut, ra, rb);
+        load_window<KIND, GROUP>(cur, codes, norms, n_pad, row, 0, groups, wpg);
+        load_rot<KIND>(rot, ra, rb);
+        if (windows > 1) load_rot<KIND>(rot + kWindow, ra_next, rb_next);
+        __syncthreads();  // the previous batch row finished reading T[0]
+        build_table<KIND>(T[0], lut, ra, rb);
         __syncthreads();
         float sum = 0.0f, gd = 0.0f;
+        // Two windows per iteration so each table buffer index is a constant:
+        // while window w is summed from T[w&1], the next table is built in the
+        // other buffer and the next window's codes are in flight.
         for (int w = 0; w < windows; w += 2) {
-            // ---- window w (table T[0]) ----
             if (w + 1 < windows) {
-                load_window<KIND, PAIR, GROUP>(nxt, codes, norms, n_pad, row, w + 1, groups, wpg);
-                build_table<KIND, PAIR>(T[1], lut, ra_next, rb_next);
-                if (w + 2 < windows) load_rot<KIND, PAIR>(rot + (w + 2) * kWindow, ra_next, rb_next);
+                load_window<KIND, GROUP>(nxt, codes, norms, n_pad, row, w + 1, groups, wpg);
+                build_table<KIND>(T[1], lut, ra_next, rb_next);
+                if (w + 2 < windows) load_rot<KIND>(rot + (w + 2) * kWindow, ra_next, rb_next);
             }
-            compute_window<KIND, PAIR, GROUP>(cur, T[0], sum, gd, w, groups, wpg);
+            compute_window<KIND, GROUP>(cur, T[0], sum, gd, w, groups, wpg);
             __syncthreads();
             if (w + 1 >= windows) break;
-            // ---- window w+1 (table T[1]) ----
             if (w + 2 < windows) {
-                load_window<KIND, PAIR, GROUP>(cur, codes, norms, n_pad, row, w + 2, groups, wpg);
-                build_table<KIND, PAIR>(T[0], lut, ra_next, rb_next);
-                if (w + 3 < windows) load_rot<KIND, PAIR>(rot + (w + 3) * kWindow, ra_next, rb_next);
+                load_window<KIND, GROUP>(cur, codes, norms, n_pad, row, w + 2, groups, wpg);
+                build_table<KIND>(T[0], lut, ra_next, rb_next);
+                if (w + 3 < windows) load_rot<KIND>(rot + (w + 3) * kWindow, ra_next, rb_next);
             }
-            compute_window<KIND, PAIR, GROUP>(nxt, T[1], sum, gd, w + 1, groups, wpg);
+            compute_window<KIND, GROUP>(nxt, T[1], sum, gd, w + 1, groups, wpg);
             __syncthreads();
         }
         if (row < rows) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b) * rows + row] = sum;
     }
 }
 
-template <int KIND, bool PAIR>
+template <int KIND>
 void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
     dim3 grid(blocks), block(kRowsPerBlock);
     switch (g.group) {
-    case 8: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 8>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 16: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 16>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 32: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 64>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 128>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 256: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    default: hipLaunchKernelGGL((cq_gemv_kernel<KIND, PAIR, 0>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 8: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 8>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 16: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 16>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 32: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 64>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 128>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 256: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 0>), grid, block, 0, s, job0, jobs, njobs, g); break;
     }
     ND_HIP(hipGetLastError());
 }
@@ -464,12 +449,10 @@ void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stri
     transform_impl(x, x_stride, rot, rot_stride, nvec, in, padded, out_limit, group, scale, s, scratch);
 }
 
-void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, bool exact,
-                    hipStream_t s) {
+void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
     if (blocks <= 0) return;
-    if (g.kind == kNib) launch_gemv_kind<kNib, false>(g, job0, jobs, njobs, blocks, s);
-    else if (exact) launch_gemv_kind<kCrumb, false>(g, job0, jobs, njobs, blocks, s);
-    else launch_gemv_kind<kCrumb, true>(g, job0, jobs, njobs, blocks, s);
+    if (g.kind == kNib) launch_gemv_kind<kNib>(g, job0, jobs, njobs, blocks, s);
+    else launch_gemv_kind<kCrumb>(g, job0, jobs, njobs, blocks, s);
 }
 
 void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, int n_pad, const int64_t *ids,

@@ -65,7 +65,6 @@ def _library():
     # additive gfx950 exports
     _bind(lib, "needle2_gpu_error", [], ct.c_char_p)
     _bind(lib, "needle2_gpu_sdot_create", [_P, _P, _I, _I, _I, _I, _P], _P)
-    _bind(lib, "needle2_gpu_cq_set_exact", [_P, _I], _I)
     _bind(lib, "needle2_gpu_cq_linear_device", [_P, _P, _P, _I, _P], _I)
     _bind(lib, "needle2_gpu_sdot_linear_device", [_P, _P, _P, _I, _P], _I)
     _bind(lib, "needle2_gpu_cq_plan_create", [_P, _I, _P, _P, _I], _P)
@@ -171,10 +170,6 @@ class NativeCQ:
             if h:
                 getattr(self._lib, fn)(h)
                 setattr(self, attr, None)
-
-    def set_exact(self, exact: bool = True) -> None:
-        """2-bit codes: per-code tables in the reference's summation order (slower)."""
-        _check(self._lib.needle2_gpu_cq_set_exact(self._handle, int(bool(exact))), "set_exact")
 
     def linear(self, x, threads: int = 1, *, lookup: int = 0):
         x = np.ascontiguousarray(x, dtype=np.float32)
