@@ -122,6 +122,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also run one 1 GiB streaming copy kernel (reference for byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the CQ GEMV path shards by output rows with no exchange, and this "
@@ -133,6 +135,14 @@ def main():
     log(f"device {info}")
     stream = Stream()
     rng = np.random.default_rng(20261201)
+
+    if args.calibrate:
+        from openneedle_amd.native import DeviceArray, copy_kernel, synchronize
+        a, b = DeviceArray(1 << 30), DeviceArray(1 << 30)
+        copy_kernel(b, a, 1 << 30, stream)
+        synchronize()
+        log("calibration copy: 1 GiB read + 1 GiB written by copy_kernel")
+        del a, b
 
     log("building CQ4 stack: 16 x 8192x8192 g32 (3 rotations)")
     packed, norms, cb = random_cq(rng, 16, 8192, 8192, 4, 32)

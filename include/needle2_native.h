@@ -102,6 +102,9 @@ void *needle2_gpu_malloc(size_t bytes);
 void needle2_gpu_free(void *ptr);
 int needle2_gpu_memcpy(void *dst, const void *src, size_t bytes, int kind); /* 0 H2D, 1 D2H, 2 D2D */
 int needle2_gpu_memset(void *dst, int value, size_t bytes);
+/* Streaming copy kernel (16 B per lane per step; bytes rounded down to 16), the
+ * reference point for scaling hardware byte counters to HBM bytes. */
+int needle2_gpu_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
 int needle2_gpu_synchronize(void);
 void *needle2_gpu_stream_create(void);
 void needle2_gpu_stream_destroy(void *stream);

@@ -483,6 +483,11 @@ int needle2_gpu_memcpy(void *dst, const void *src, size_t bytes, int kind) {
     });
 }
 
+// Streaming device-to-device copy kernel (bytes rounded down to 16).
+int needle2_gpu_copy_kernel(void *dst, const void *src, size_t bytes, void *stream) {
+    return guarded([&] { launch_copy(src, dst, bytes, static_cast<hipStream_t>(stream)); });
+}
+
 int needle2_gpu_memset(void *dst, int value, size_t bytes) {
     return guarded([&] { ND_HIP(hipMemset(dst, value, bytes)); });
 }

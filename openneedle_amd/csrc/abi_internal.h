@@ -8,6 +8,8 @@ namespace nd {
 void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stride, int nvec, int in, int padded,
                           int out_limit, int group, float scale, float *scratch, hipStream_t s);
 
+void launch_copy(const void *src, void *dst, size_t bytes, hipStream_t s);
+
 // A CQ matrix resident in device memory (layout described in common.h).
 struct Matrix {
     int out = 0, in = 0, bits = 0, group = 0, padded = 0, groups = 0, rowbytes = 0;

@@ -392,7 +392,23 @@ __global__ void dequant_rows_kernel(CqGeom geom, const uint4 *__restrict__ codes
     tmp[static_cast<size_t>(i) * tmp_stride + p] = geom.lut[code] * norm;
 }
 
+// Plain streaming copy (16 B per lane per step): the reference point for
+// scaling hardware byte counters to HBM bytes.
+__global__ __launch_bounds__(256) void copy_kernel(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst, size_t n) {
+    size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    for (; i < n; i += stride) dst[i] = src[i];
+}
+
 }  // namespace
+
+void launch_copy(const void *src, void *dst, size_t bytes, hipStream_t s) {
+    const size_t n = bytes / 16;
+    if (!n) return;
+    hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, static_cast<const u32x4 *>(src),
+                       static_cast<u32x4 *>(dst), n);
+    ND_HIP(hipGetLastError());
+}
 
 // ---------------------------------------------------------------------------
 // Launchers

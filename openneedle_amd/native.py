@@ -76,6 +76,7 @@ def _library():
     _bind(lib, "needle2_gpu_free", [_P])
     _bind(lib, "needle2_gpu_memcpy", [_P, _P, ct.c_size_t, _I], _I)
     _bind(lib, "needle2_gpu_memset", [_P, _I, ct.c_size_t], _I)
+    _bind(lib, "needle2_gpu_copy_kernel", [_P, _P, ct.c_size_t, _P], _I)
     _bind(lib, "needle2_gpu_synchronize", [], _I)
     _bind(lib, "needle2_gpu_stream_create", [], _P)
     _bind(lib, "needle2_gpu_stream_destroy", [_P])
@@ -326,6 +327,11 @@ class Event:
         if getattr(self, "ptr", None):
             self._lib.needle2_gpu_event_destroy(self.ptr)
             self.ptr = None
+
+
+def copy_kernel(dst: DeviceArray, src: DeviceArray, nbytes: int, stream: "Stream | None" = None) -> None:
+    assert nbytes <= dst.nbytes and nbytes <= src.nbytes
+    _check(_library().needle2_gpu_copy_kernel(dst.ptr, src.ptr, int(nbytes), stream.ptr if stream else None), "copy")
 
 
 def synchronize() -> None:
