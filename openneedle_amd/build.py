@@ -41,9 +41,9 @@ def sources():
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON, *DEVICE, "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, build_dir: Path = BUILD, defines=()) -> Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [hipcc(), *COMMON, *DEVICE, *[f"-D{d}" for d in defines], "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".hip":
         cmd[1:1] = ["-x", "hip"]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -52,20 +52,21 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build(verbose: bool = False, out: Path = OUT, build_dir: Path = BUILD, defines=()) -> Path:
+    """Compile every source and link ``out``; ``defines`` are extra -D tuning macros."""
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = OUT.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, build_dir, defines), srcs))
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{res.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {OUT}")
-    return OUT
+        print(f"built {out}")
+    return out
 
 
 if __name__ == "__main__":

@@ -90,6 +90,7 @@ CqGeom Matrix::geom() const {
     g.groups = groups;
     g.windows = windows;
     g.chunks = chunks;
+    g.in = in;
     g.scale = scale;
     std::memcpy(g.lut, lut, sizeof lut);
     return g;
@@ -114,9 +115,13 @@ Staging::~Staging() {
 // ---------------------------------------------------------------------------
 void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s) {
     if (batch <= 0) return;
-    st.rot.reserve(size_t(batch) * m.dev);
-    m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
-    const CqJob job{m.codes.p, m.norms.p, st.rot.p, d_y, m.out, m.n_pad, 0, batch};
+    const float *act = d_x;
+    if (!gemv_fuses_fwht(m.group)) {
+        st.rot.reserve(size_t(batch) * m.dev);
+        m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
+        act = st.rot.p;
+    }
+    const CqJob job{m.codes.p, m.norms.p, act, d_y, m.out, m.n_pad, 0, batch};
     launch_cq_gemv(m.geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, s);
 }
 
@@ -235,10 +240,11 @@ static void plan_upload(Plan &p) {
     if (!p.sdot) {
         p.rot.reserve(size_t(p.count) * p.batch * m.dev);
         std::vector<CqJob> jobs(p.count);
+        const bool fused = gemv_fuses_fwht(m.group);
         for (int i = 0; i < p.count; ++i) {
             const Matrix &mi = p.cq[i]->m;
-            jobs[i] = CqJob{mi.codes.p, mi.norms.p, p.rot.p + size_t(i) * p.batch * m.dev, p.ys[i], mi.out, mi.n_pad,
-                            block, p.batch};
+            const float *act = fused ? p.xs_in[i] : p.rot.p + size_t(i) * p.batch * m.dev;
+            jobs[i] = CqJob{mi.codes.p, mi.norms.p, act, p.ys[i], mi.out, mi.n_pad, block, p.batch};
             block += mi.n_pad / kRowsPerBlock;
         }
         host.assign(reinterpret_cast<uint8_t *>(jobs.data()), reinterpret_cast<uint8_t *>(jobs.data() + p.count));
@@ -269,9 +275,11 @@ static void plan_upload(Plan &p) {
 
 static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hipEvent_t gemv_stop = nullptr) {
     const Matrix &m = *p.first;
-    // x_i is [batch][in] on the device; one transform launch per matrix input
-    for (int i = 0; i < p.count; ++i)
-        m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
+    // x_i is [batch][in] on the device; the FP32 GEMV transforms it in-kernel
+    // unless the group exceeds one table window
+    if (p.sdot || !gemv_fuses_fwht(m.group))
+        for (int i = 0; i < p.count; ++i)
+            m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
     if (!p.sdot) {
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
         launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s);

@@ -102,8 +102,21 @@ struct HostBuf {
 // 16-byte code chunk as a clang vector (trivially copyable from any address space)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRowsPerBlock = 256;  // rows per workgroup (one per lane, 4 waves)
-constexpr int kWindow = 256;        // code positions per LDS table window
+// Raw buffer resource over [base, base + bytes): loads take a wave-uniform
+// soffset plus one per-lane voffset, and offsets >= bytes read as zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+#ifndef ND_ROWS
+#define ND_ROWS 256
+#endif
+#ifndef ND_WINDOW
+#define ND_WINDOW 256
+#endif
+constexpr int kRowsPerBlock = ND_ROWS;  // rows per workgroup (one per lane)
+constexpr int kWindow = ND_WINDOW;      // code positions per LDS table window
+static_assert(kRowsPerBlock >= 64 && kWindow % kRowsPerBlock == 0 && kWindow % 64 == 0, "window/block geometry");
 
 enum CodeKind : int { kNib = 0, kCrumb = 1 };
 
@@ -113,14 +126,19 @@ struct CqGeom {
     int groups;      // real groups per row (padded / group)
     int windows;     // table windows per row (device positions / kWindow)
     int chunks;      // 16-byte chunks per row in the device layout
+    int in;          // input length (x row stride when the FWHT is fused)
     float scale;     // 1/sqrt(group), computed on the host as the reference does
     float lut[16];   // fp32 codebook indexed by device code
 };
 
+// Groups up to one table window run the activation FWHT inside the GEMV
+// kernel; larger groups use a separate transform pass.
+inline bool gemv_fuses_fwht(int group) { return group <= kWindow; }
+
 struct CqJob {
     const uint4 *codes;       // [chunks][n_pad]
     const uint16_t *norms;    // [groups][n_pad]
-    const float *rot;         // transformed activations [batch][windows*kWindow]
+    const float *act;         // x [batch][in] (fused FWHT) or rot [batch][windows*kWindow]
     float *y;                 // outputs [batch][rows]
     int rows;
     int n_pad;

@@ -139,60 +139,139 @@ __global__ void scale_crop_kernel(const float *__restrict__ src, int src_stride,
 // code). Groups close with sum += gd * half(norm). This is the reference's
 // exact operation sequence (cq.cpp:104-107, 157-164, 185-194) for every bit
 // width, so results are bit-identical to its portable build.
+//
+// For groups up to one window the activation FWHT (cq.cpp:30-46, 153-156) is
+// computed in the kernel from x: lane t owns position t of the window;
+// butterflies of stride < 64 are wave shuffles, 64 and 128 go through LDS.
+// Slot strides are padded (17 / 34 floats) so table writes are bank-conflict
+// free; reads are wave-uniform per slot (broadcast).
 // ---------------------------------------------------------------------------
 template <int KIND>
 struct TableShape {
     static constexpr int kCodesPerChunk = KIND == kNib ? 32 : 64;
     static constexpr int kChunksPerWindow = kWindow / kCodesPerChunk;
     static constexpr int kPositionsPerSlot = KIND == kNib ? 1 : 2;
-    static constexpr int kSlots = kWindow / kPositionsPerSlot;    // slots per window
-    static constexpr int kSlotFloats = KIND == kNib ? 16 : 32;    // floats per slot
-    static constexpr int kFloats = kSlots * kSlotFloats;          // 4096 floats = 16 KiB either way
+    static constexpr int kSlots = kWindow / kPositionsPerSlot;     // slots per window
+    static constexpr int kEntryBytes = KIND == kNib ? 4 : 8;
+    static constexpr int kSlotFloats = KIND == kNib ? 17 : 36;     // 16 entries + padding
+    static constexpr int kFloats = kSlots * kSlotFloats;
 };
 
-// Build one window's table. Thread t owns slot t (4-bit: t < 256; 2-bit: t < 128).
-template <int KIND>
-__device__ __forceinline__ void build_table(float *__restrict__ T, const float *lut, float r_a, float r_b) {
-    using S = TableShape<KIND>;
-    const int t = threadIdx.x;
-    if constexpr (KIND == kNib) {
-        float4 *dst = reinterpret_cast<float4 *>(T + t * S::kSlotFloats);
+// Positions of a window handled by one thread: t, t + kRowsPerBlock, ...
+constexpr int kPositionsPerThread = kWindow / kRowsPerBlock;
+
+// Window activations: x (fused) or rot (precomputed) for this thread's
+// positions, through a buffer resource bounded at the row's end, so positions
+// >= in read as zero (the reference's zero padding, cq.cpp:154).
+__device__ __forceinline__ void load_act(__amdgpu_buffer_rsrc_t act, int w, float (&a)[kPositionsPerThread]) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            dst[q] = make_float4(lut[4 * q] * r_a, lut[4 * q + 1] * r_a, lut[4 * q + 2] * r_a, lut[4 * q + 3] * r_a);
+    for (int k = 0; k < kPositionsPerThread; ++k)
+        a[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             act, (k * kRowsPerBlock + threadIdx.x) * 4u, w * kWindow * 4, 0));
+}
+
+// Value of the butterfly partner lane t ^ H (H < 64) without LDS round trips:
+// DPP quad permutes (1, 2), row shifts (4, 8) and the gfx950 row swaps (16, 32).
+template <int H>
+__device__ __forceinline__ float butterfly_partner(float v, int t) {
+    const int iv = __builtin_bit_cast(int, v);
+    if constexpr (H == 1) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    } else if constexpr (H == 2) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    } else if constexpr (H == 4 || H == 8) {
+        const float up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x100 + H, 0xF, 0xF, false));
+        const float down = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x110 + H, 0xF, 0xF, false));
+        return (t & H) ? down : up;  // row_shl:H reads lane t+H, row_shr:H reads lane t-H
+    } else if constexpr (H == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+        return __builtin_bit_cast(float, (t & 16) ? r[0] : r[1]);
     } else {
-        if (t < S::kSlots) {
-            float p0[4], p1[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                p0[c] = lut[c] * r_a;
-                p1[c] = lut[c] * r_b;
-            }
-            // entry n = c0 | c1 << 2 holds (p0[c0], p1[c1]); two entries per float4
-            float4 *dst = reinterpret_cast<float4 *>(T + t * S::kSlotFloats);
-#pragma unroll
-            for (int hi = 0; hi < 4; ++hi) {
-                dst[2 * hi] = make_float4(p0[0], p1[hi], p0[1], p1[hi]);
-                dst[2 * hi + 1] = make_float4(p0[2], p1[hi], p0[3], p1[hi]);
-            }
-        }
+        static_assert(H == 32, "butterfly stride");
+        const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+        return __builtin_bit_cast(float, (t & 32) ? r[0] : r[1]);
     }
 }
 
-// rot values a thread needs for building one window's table.
-template <int KIND>
-__device__ __forceinline__ void load_rot(const ND_GLOBAL float *__restrict__ rot_w, float &r_a, float &r_b) {
+template <int GROUP, int H>
+__device__ __forceinline__ void wave_butterflies(float &v, int t) {
+    if constexpr (H < GROUP && H < 64) {
+        const float o = butterfly_partner<H>(v, t);
+        // lower lane: v + o = a + b; upper lane: o + (-v) = a - b (exact negation)
+        const float sv = (t & H) ? -v : v;
+        v = o + sv;
+        wave_butterflies<GROUP, H * 2>(v, t);
+    }
+}
+
+// In-kernel FWHT of the window (GROUP <= kWindow), identical butterflies to
+// the reference (stage h ascending: (a+b, a-b)), then the multiply by the
+// host-computed 1/sqrt(group). Strides below 64 are wave shuffles; larger
+// strides exchange through LDS.
+template <int GROUP>
+__device__ __forceinline__ void window_fwht(float (&v)[kPositionsPerThread], float scale, float *stage) {
     const int t = threadIdx.x;
-    if constexpr (KIND == kCrumb) {
-        if (t < kWindow / 2) {
-            r_a = rot_w[2 * t];
-            r_b = rot_w[2 * t + 1];
-        } else {
-            r_a = r_b = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPositionsPerThread; ++k) wave_butterflies<GROUP, 1>(v[k], t & 63);
+    if constexpr (GROUP > 64) {
+#pragma unroll
+        for (int h = 64; h < GROUP; h <<= 1) {
+#pragma unroll
+            for (int k = 0; k < kPositionsPerThread; ++k) stage[k * kRowsPerBlock + t] = v[k];
+            __syncthreads();
+            float o[kPositionsPerThread];
+#pragma unroll
+            for (int k = 0; k < kPositionsPerThread; ++k) o[k] = stage[(k * kRowsPerBlock + t) ^ h];
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kPositionsPerThread; ++k) {
+                const int p = k * kRowsPerBlock + t;
+                const float sv = (p & h) ? -v[k] : v[k];
+                v[k] = o[k] + sv;
+            }
         }
-    } else {
-        r_a = rot_w[t];
-        r_b = 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < kPositionsPerThread; ++k) v[k] = v[k] * scale;
+}
+
+// Write the window's products into the table. 4-bit: lane t fills slot t
+// (stride 17 floats: conflict-free 4-byte writes). 2-bit: in each wave, lanes
+// 0..31 fill slots for the wave's 64 positions, taking the two positions'
+// values from their neighbours by shuffle (stride 36 floats, 16-byte writes).
+template <int KIND>
+__device__ __forceinline__ void build_table(float *__restrict__ T, const float *lut,
+                                            const float (&r)[kPositionsPerThread]) {
+    using S = TableShape<KIND>;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kPositionsPerThread; ++k) {
+        if constexpr (KIND == kNib) {
+            float *dst = T + (k * kRowsPerBlock + t) * S::kSlotFloats;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) dst[c] = lut[c] * r[k];
+        } else {
+            const int lane = t & 63;
+            const int l = lane & 31;
+            const float r0 = __shfl(r[k], 2 * l);
+            const float r1 = __shfl(r[k], 2 * l + 1);
+            if (lane < 32) {
+                float p0[4], p1[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    p0[c] = lut[c] * r0;
+                    p1[c] = lut[c] * r1;
+                }
+                // entry n = c0 | c1 << 2 holds (p0[c0], p1[c1]); two entries per 16-byte store
+                const int slot = (k * kRowsPerBlock + (t & ~63)) / 2 + l;
+                float4 *dst = reinterpret_cast<float4 *>(T + slot * S::kSlotFloats);
+#pragma unroll
+                for (int hi = 0; hi < 4; ++hi) {
+                    dst[2 * hi] = make_float4(p0[0], p1[hi], p0[1], p1[hi]);
+                    dst[2 * hi + 1] = make_float4(p0[2], p1[hi], p0[3], p1[hi]);
+                }
+            }
+        }
     }
 }
 
@@ -211,74 +290,134 @@ struct WindowState {
     uint16_t norms[kNorms];
 };
 
+// Buffer loads: the chunk / norm-row offset is wave-uniform (soffset) and the
+// per-lane offset is one shared VGPR, so no per-chunk addresses stay live.
 template <int KIND, int GROUP>
-__device__ __forceinline__ void load_window(WindowState<KIND, GROUP> &st, const ND_GLOBAL u32x4 *__restrict__ codes,
-                                            const ND_GLOBAL uint16_t *__restrict__ norms, int n_pad, int row, int w,
-                                            int groups, int windows_per_group) {
+__device__ __forceinline__ void load_window(WindowState<KIND, GROUP> &st, __amdgpu_buffer_rsrc_t codes,
+                                            __amdgpu_buffer_rsrc_t norms, int n_pad, int row, int w, int groups,
+                                            int windows_per_group) {
     constexpr int C = WindowState<KIND, GROUP>::kChunks;
     constexpr int NN = WindowState<KIND, GROUP>::kNorms;
-    const ND_GLOBAL u32x4 *cw = codes + static_cast<size_t>(w) * C * n_pad + row;
+    const uint32_t code_lane = static_cast<uint32_t>(row) * 16u;
+    const uint32_t norm_lane = static_cast<uint32_t>(row) * 2u;
 #pragma unroll
-    for (int c = 0; c < C; ++c) st.codes[c] = cw[static_cast<size_t>(c) * n_pad];
+    for (int c = 0; c < C; ++c)
+        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * n_pad * 16, 0);
+    // group indices are clamped (phantom groups past the last are never closed)
     if constexpr (GROUP > 0) {
 #pragma unroll
         for (int k = 0; k < NN; ++k) {
-            int g = w * NN + k;
-            st.norms[k] = g < groups ? norms[static_cast<size_t>(g) * n_pad + row] : uint16_t(0);
+            const int g = min(w * NN + k, groups - 1);
+            st.norms[k] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, g * n_pad * 2, 0);
         }
     } else {
-        int g = w / windows_per_group;
-        st.norms[0] = g < groups ? norms[static_cast<size_t>(g) * n_pad + row] : uint16_t(0);
+        const int g = min(w / windows_per_group, groups - 1);
+        st.norms[0] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, g * n_pad * 2, 0);
     }
 }
 
+// Byte offsets of the 8 slot entries addressed by one code dword: 8 nibbles,
+// spread into X (even nibbles) and Y (odd nibbles), one v_bfe each.
+template <int KIND>
+__device__ __forceinline__ void slot_offsets(uint32_t wd, uint32_t off[8]) {
+    constexpr int kShift = KIND == kNib ? 2 : 3;  // entry bytes: 4 or 8
+    constexpr uint32_t kMask = KIND == kNib ? 0x3C3C3C3Cu : 0x78787878u;
+    uint32_t X = (wd << kShift) & kMask;
+    uint32_t Y = (wd >> (4 - kShift)) & kMask;
+    // opaque to the optimizer: keeps one v_bfe per slot instead of a
+    // re-derived shift+and pair
+    asm("" : "+v"(X));
+    asm("" : "+v"(Y));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t src = (i & 1) ? Y : X;
+        const int sh = (i >> 1) * 8;
+        off[i] = sh == 24 ? (src >> 24) : ((src >> sh) & 0xFFu);
+    }
+}
+
+template <int KIND>
+struct SlotValues {
+    float a[8];
+    float b[8];  // second code of a 2-bit pair
+};
+
+template <int KIND>
+__device__ __forceinline__ void read_slots(const float *T, int slot0, const uint32_t off[8], SlotValues<KIND> &v) {
+    using S = TableShape<KIND>;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const char *slot = reinterpret_cast<const char *>(T + (slot0 + i) * S::kSlotFloats);
+        if constexpr (KIND == kNib) {
+            v.a[i] = *reinterpret_cast<const float *>(slot + off[i]);
+        } else {
+            const float2 pr = *reinterpret_cast<const float2 *>(slot + off[i]);
+            v.a[i] = pr.x;
+            v.b[i] = pr.y;
+        }
+    }
+}
+
+#ifndef ND_PIPE
+#define ND_PIPE 2
+#endif
+#ifndef ND_SCHED_BARRIER
+#define ND_SCHED_BARRIER 1
+#endif
+
 // Process one window against its table T (LDS), in the reference's order.
+// Software pipeline, fixed with scheduling barriers: the LDS reads for code
+// dword d+1 are issued before the adds of dword d, so each add consumes a
+// value read one dword earlier and LDS latency overlaps the add chain.
 template <int KIND, int GROUP>
 __device__ __forceinline__ void compute_window(const WindowState<KIND, GROUP> &st, const float *T, float &sum,
                                                float &gd, int w, int groups, int windows_per_group) {
     using S = TableShape<KIND>;
     constexpr int NN = WindowState<KIND, GROUP>::kNorms;
-    const int gbase = w * NN;  // first group index closing in this window (GROUP > 0)
+    constexpr int D = S::kChunksPerWindow * 4;  // code dwords per window
+    const int gbase = w * NN;                   // first group index closing in this window (GROUP > 0)
+    constexpr int P = ND_PIPE;  // code dwords read ahead of the adds
+    SlotValues<KIND> v[P + 1];
 #pragma unroll
-    for (int c = 0; c < S::kChunksPerWindow; ++c) {
-        const uint32_t words[4] = {st.codes[c].x, st.codes[c].y, st.codes[c].z, st.codes[c].w};
+    for (int dn = 0; dn < P && dn < D; ++dn) {
+        const u32x4 &cn = st.codes[dn >> 2];
+        const uint32_t wn = (dn & 3) == 0 ? cn.x : (dn & 3) == 1 ? cn.y : (dn & 3) == 2 ? cn.z : cn.w;
+        uint32_t off[8];
+        slot_offsets<KIND>(wn, off);
+        read_slots<KIND>(T, dn * 8, off, v[dn % (P + 1)]);
+    }
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t wd = words[d];
-            // 8 nibbles per dword (one 4-bit code, or two 2-bit codes, per slot),
-            // spread as byte offsets into X (even nibbles) and Y (odd nibbles).
-            constexpr int kShift = KIND == kNib ? 2 : 3;           // entry bytes: 4 or 8
-            constexpr uint32_t kMask = KIND == kNib ? 0x3C3C3C3Cu : 0x78787878u;
-            uint32_t X = (wd << kShift) & kMask;
-            uint32_t Y = (wd >> (4 - kShift)) & kMask;
-            // opaque to the optimizer: keeps one v_bfe per slot instead of a
-            // re-derived shift+and pair
-            asm("" : "+v"(X));
-            asm("" : "+v"(Y));
-            const int slot0 = c * 32 + d * 8;  // 32 slots per chunk for both layouts
+    for (int d = 0; d < D; ++d) {
+        if (d + P < D) {
+            const int dn = d + P;
+            const u32x4 &cn = st.codes[dn >> 2];
+            const uint32_t wn = (dn & 3) == 0 ? cn.x : (dn & 3) == 1 ? cn.y : (dn & 3) == 2 ? cn.z : cn.w;
+            uint32_t off[8];
+            slot_offsets<KIND>(wn, off);
+            read_slots<KIND>(T, dn * 8, off, v[dn % (P + 1)]);
+        }
+        // compiler-only fence: keeps each dword's LDS reads in its pipeline
+        // slot (otherwise every read of the window is hoisted and spilled)
+        asm volatile("" ::: "memory");
+        if (ND_SCHED_BARRIER) __builtin_amdgcn_sched_barrier(0);
+        const SlotValues<KIND> &cur = v[d % (P + 1)];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t src = (i & 1) ? Y : X;
-                const int sh = (i >> 1) * 8;
-                const uint32_t off = sh == 24 ? (src >> 24) : ((src >> sh) & 0xFFu);
-                const float *slot = T + (slot0 + i) * S::kSlotFloats;
-                if constexpr (KIND == kNib) {
-                    gd += lds_at(slot, off);
-                } else {
-                    const float2 pr = *reinterpret_cast<const float2 *>(reinterpret_cast<const char *>(slot) + off);
-                    gd += pr.x;
-                    gd += pr.y;
-                }
-                if constexpr (GROUP > 0) {
-                    const int pos_end = (slot0 + i + 1) * S::kPositionsPerSlot;  // positions consumed in window
-                    if (pos_end % GROUP == 0) {
-                        const int k = pos_end / GROUP - 1;
-                        if (gbase + k < groups) sum += gd * h2f(st.norms[k]);
-                        gd = 0.0f;
-                    }
+        for (int i = 0; i < 8; ++i) {
+            gd += cur.a[i];
+            if constexpr (KIND == kCrumb) gd += cur.b[i];
+            if constexpr (GROUP > 0) {
+                const int pos_end = (d * 8 + i + 1) * S::kPositionsPerSlot;  // positions consumed in window
+                if (pos_end % GROUP == 0) {
+                    const int k = pos_end / GROUP - 1;
+                    if (gbase + k < groups) sum += gd * h2f(st.norms[k]);
+                    gd = 0.0f;
                 }
             }
         }
+        // pins this dword's adds before the next dword's reads (the fence
+        // above only orders memory operations)
+        asm volatile("" : "+v"(gd), "+v"(sum));
+        if (ND_SCHED_BARRIER) __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (GROUP == 0) {
         if ((w + 1) % windows_per_group == 0) {
@@ -289,10 +428,12 @@ __device__ __forceinline__ void compute_window(const WindowState<KIND, GROUP> &s
 }
 
 template <int KIND, int GROUP>
-__global__ __launch_bounds__(kRowsPerBlock) void cq_gemv_kernel(CqJob job0, const CqJob *__restrict__ jobs, int njobs,
+__global__ __launch_bounds__(kRowsPerBlock, 2) void cq_gemv_kernel(CqJob job0, const CqJob *__restrict__ jobs, int njobs,
                                                                 CqGeom geom) {
     using S = TableShape<KIND>;
     __shared__ __attribute__((aligned(16))) float T[2][S::kFloats];
+    __shared__ float stage[GROUP > 64 ? kWindow : 1];
+    constexpr int PPT = kPositionsPerThread;
 
     const int blk = blockIdx.x;
     CqJob J = job0;
@@ -303,53 +444,63 @@ __global__ __launch_bounds__(kRowsPerBlock) void cq_gemv_kernel(CqJob job0, cons
             if (cj[k].block_begin <= blk) j = k;
         J.codes = cj[j].codes;
         J.norms = cj[j].norms;
-        J.rot = cj[j].rot;
+        J.act = cj[j].act;
         J.y = cj[j].y;
         J.rows = cj[j].rows;
         J.n_pad = cj[j].n_pad;
         J.block_begin = cj[j].block_begin;
         J.batch = cj[j].batch;
     }
-    const ND_GLOBAL u32x4 *__restrict__ codes = (const ND_GLOBAL u32x4 *)(J.codes);
-    const ND_GLOBAL uint16_t *__restrict__ norms = (const ND_GLOBAL uint16_t *)(J.norms);
     const int n_pad = J.n_pad, rows = J.rows, batch = J.batch;
+    const __amdgpu_buffer_rsrc_t codes = buffer_rsrc(J.codes, static_cast<uint32_t>(geom.chunks) * n_pad * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms, static_cast<uint32_t>(geom.groups) * n_pad * 2u);
     const int row = (blk - J.block_begin) * kRowsPerBlock + threadIdx.x;
-    const int windows = geom.windows, groups = geom.groups;
+    const int windows = geom.windows, groups = geom.groups, in = geom.in;
     const int wpg = GROUP == 0 ? geom.group / kWindow : 1;
-    const int dev = windows * kWindow;
+    const int act_stride = GROUP > 0 ? in : windows * kWindow;
+    const float scale = geom.scale;
     float lut[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) lut[i] = geom.lut[i];
 
     for (int b = 0; b < batch; ++b) {
-        const ND_GLOBAL float *__restrict__ rot = (const ND_GLOBAL float *)(J.rot) + static_cast<size_t>(b) * dev;
+        const __amdgpu_buffer_rsrc_t act =
+            buffer_rsrc(J.act + static_cast<size_t>(b) * act_stride, static_cast<uint32_t>(act_stride) * 4u);
         WindowState<KIND, GROUP> cur, nxt;
-        float ra, rb, ra_next = 0.0f, rb_next = 0.0f;
+        float xa[PPT];
+        load_act(act, 0, xa);
         load_window<KIND, GROUP>(cur, codes, norms, n_pad, row, 0, groups, wpg);
-        load_rot<KIND>(rot, ra, rb);
-        if (windows > 1) load_rot<KIND>(rot + kWindow, ra_next, rb_next);
         __syncthreads();  // the previous batch row finished reading T[0]
-        build_table<KIND>(T[0], lut, ra, rb);
+        if constexpr (GROUP > 0) window_fwht<GROUP>(xa, scale, stage);
+        build_table<KIND>(T[0], lut, xa);
         __syncthreads();
         float sum = 0.0f, gd = 0.0f;
-        // Two windows per iteration so each table buffer index is a constant:
-        // while window w is summed from T[w&1], the next table is built in the
-        // other buffer and the next window's codes are in flight.
+        // Two windows per iteration so each table buffer index is a constant.
+        // Per window: issue the next window's activation and code loads (in that
+        // order, unconditionally, clamped at the last window), sum this window
+        // from its table, then transform the next activations and build the
+        // next table in the other buffer; one barrier per window. Every loaded
+        // value is consumed within the iteration that loads it, so no register
+        // copy of a pending load (and no full vector-memory wait) is needed.
         for (int w = 0; w < windows; w += 2) {
-            if (w + 1 < windows) {
-                load_window<KIND, GROUP>(nxt, codes, norms, n_pad, row, w + 1, groups, wpg);
-                build_table<KIND>(T[1], lut, ra_next, rb_next);
-                if (w + 2 < windows) load_rot<KIND>(rot + (w + 2) * kWindow, ra_next, rb_next);
-            }
+            const int w1 = min(w + 1, windows - 1);
+            load_act(act, w1, xa);
+            load_window<KIND, GROUP>(nxt, codes, norms, n_pad, row, w1, groups, wpg);
             compute_window<KIND, GROUP>(cur, T[0], sum, gd, w, groups, wpg);
+            if (w + 1 < windows) {
+                if constexpr (GROUP > 0) window_fwht<GROUP>(xa, scale, stage);
+                build_table<KIND>(T[1], lut, xa);
+            }
             __syncthreads();
             if (w + 1 >= windows) break;
-            if (w + 2 < windows) {
-                load_window<KIND, GROUP>(cur, codes, norms, n_pad, row, w + 2, groups, wpg);
-                build_table<KIND>(T[0], lut, ra_next, rb_next);
-                if (w + 3 < windows) load_rot<KIND>(rot + (w + 3) * kWindow, ra_next, rb_next);
-            }
+            const int w2 = min(w + 2, windows - 1);
+            load_act(act, w2, xa);
+            load_window<KIND, GROUP>(cur, codes, norms, n_pad, row, w2, groups, wpg);
             compute_window<KIND, GROUP>(nxt, T[1], sum, gd, w + 1, groups, wpg);
+            if (w + 2 < windows) {
+                if constexpr (GROUP > 0) window_fwht<GROUP>(xa, scale, stage);
+                build_table<KIND>(T[0], lut, xa);
+            }
             __syncthreads();
         }
         if (row < rows) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b) * rows + row] = sum;
@@ -359,7 +510,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void cq_gemv_kernel(CqJob job0, cons
 template <int KIND>
 void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
     dim3 grid(blocks), block(kRowsPerBlock);
-    switch (g.group) {
+    switch (g.group > kWindow ? 0 : g.group) {
     case 8: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 8>), grid, block, 0, s, job0, jobs, njobs, g); break;
     case 16: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 16>), grid, block, 0, s, job0, jobs, njobs, g); break;
     case 32: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;

@@ -100,15 +100,16 @@ __device__ __forceinline__ void sdot_load(SdotWindow<KIND, GROUP> &st, const ND_
     const ND_GLOBAL u32x4 *cw = codes + static_cast<size_t>(w) * C * n_pad + row;
 #pragma unroll
     for (int c = 0; c < C; ++c) st.codes[c] = cw[static_cast<size_t>(c) * n_pad];
+    // clamped group indices: unconditional loads (phantom groups are never closed)
     if constexpr (GROUP > 0) {
 #pragma unroll
         for (int k = 0; k < NN; ++k) {
-            int g = w * NN + k;
-            st.norms[k] = g < groups ? norms[static_cast<size_t>(g) * n_pad + row] : uint16_t(0);
+            const int g = min(w * NN + k, groups - 1);
+            st.norms[k] = norms[static_cast<size_t>(g) * n_pad + row];
         }
     } else {
-        int g = w / wpg;
-        st.norms[0] = g < groups ? norms[static_cast<size_t>(g) * n_pad + row] : uint16_t(0);
+        const int g = min(w / wpg, groups - 1);
+        st.norms[0] = norms[static_cast<size_t>(g) * n_pad + row];
     }
 }
 
@@ -221,7 +222,7 @@ template <int KIND>
 void launch_sdot_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
                       hipStream_t s) {
     dim3 grid(blocks), block(kRowsPerBlock);
-    switch (g.group) {
+    switch (g.group > kWindow ? 0 : g.group) {
     case 16: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 16>), grid, block, 0, s, job0, jobs, njobs, g); break;
     case 32: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;
     case 64: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 64>), grid, block, 0, s, job0, jobs, njobs, g); break;
