@@ -122,6 +122,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", choices=["cq4", "cq2", "int8"], default=None,
+                    help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one 1 GiB streaming copy kernel (reference for byte counters)")
     args = ap.parse_args()
@@ -143,6 +145,16 @@ def main():
         synchronize()
         log("calibration copy: 1 GiB read + 1 GiB written by copy_kernel")
         del a, b
+
+    if args.only:
+        bits, count, rows, rot = (4, 16, 8192, 3) if args.only == "cq4" else (2, 16, 8192, 3) if args.only == "cq2" \
+            else (4, 64, 4096, 2)
+        packed, norms, cb = random_cq(rng, count, rows, rows, bits, 32)
+        st = Stack(packed, norms, cb, bits, 32, batch=1, rot=rot, int8=args.only == "int8")
+        ms1, g1, _ = st.run(args.steps, args.warmup, stream)
+        log(f"{args.only}: step {ms1 * 1e3:.1f} us, GEMV {g1 * 1e3:.1f} us "
+            f"({st.bytes_per_step / (g1 * 1e-3) / 1e9:.0f} GB/s)")
+        return
 
     log("building CQ4 stack: 16 x 8192x8192 g32 (3 rotations)")
     packed, norms, cb = random_cq(rng, 16, 8192, 8192, 4, 32)

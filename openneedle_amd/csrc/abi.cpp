@@ -196,7 +196,7 @@ void SdotHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t
     st.xs.reserve(size_t(batch) * m.groups);
     prepare_device(d_x, batch, st.q.p, st.xs.p, s);
     const SdotJob job{m.codes.p, m.norms.p, st.q.p, st.xs.p, d_y, m.out, m.n_pad, 0, batch};
-    launch_sdot_gemv(geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, s);
+    launch_sdot_gemv(geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, batch, s);
 }
 
 void SdotHandle::linear_host(const float *x, float *y, int batch) {
@@ -288,7 +288,8 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
         launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
                              p.xscale.p, s);
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
-        launch_sdot_gemv(h0.geom(), SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, s);
+        launch_sdot_gemv(h0.geom(), SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, p.batch,
+                         s);
     }
     if (gemv_stop) ND_HIP(hipEventRecord(gemv_stop, s));
 }

@@ -188,7 +188,8 @@ void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, 
 // int8 path: quantize rot (already transformed) into permuted int8 + scales.
 void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded, int dev_positions,
                           int group, int kind, int32_t *q, float *xs, hipStream_t s);
+// The batch (uniform across jobs) is processed in tiles that decode each code once.
 void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs_dev, int njobs, int total_blocks,
-                      hipStream_t s);
+                      int batch, hipStream_t s);
 
 }  // namespace nd

@@ -91,88 +91,156 @@ struct SdotWindow {
     uint16_t norms[kNorms];
 };
 
+// Buffer loads with a wave-uniform soffset and one shared per-lane voffset;
+// group indices are clamped (phantom groups past the last are never closed).
 template <int KIND, int GROUP>
-__device__ __forceinline__ void sdot_load(SdotWindow<KIND, GROUP> &st, const ND_GLOBAL u32x4 *__restrict__ codes,
-                                          const ND_GLOBAL uint16_t *__restrict__ norms, int n_pad, int row, int w,
-                                          int groups, int wpg) {
+__device__ __forceinline__ void sdot_load(SdotWindow<KIND, GROUP> &st, __amdgpu_buffer_rsrc_t codes,
+                                          __amdgpu_buffer_rsrc_t norms, int n_pad, int row, int w, int groups,
+                                          int wpg) {
     constexpr int C = SdotWindow<KIND, GROUP>::kChunks;
     constexpr int NN = SdotWindow<KIND, GROUP>::kNorms;
-    const ND_GLOBAL u32x4 *cw = codes + static_cast<size_t>(w) * C * n_pad + row;
+    const uint32_t code_lane = static_cast<uint32_t>(row) * 16u, norm_lane = static_cast<uint32_t>(row) * 2u;
 #pragma unroll
-    for (int c = 0; c < C; ++c) st.codes[c] = cw[static_cast<size_t>(c) * n_pad];
-    // clamped group indices: unconditional loads (phantom groups are never closed)
+    for (int c = 0; c < C; ++c)
+        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * n_pad * 16, 0);
     if constexpr (GROUP > 0) {
 #pragma unroll
-        for (int k = 0; k < NN; ++k) {
-            const int g = min(w * NN + k, groups - 1);
-            st.norms[k] = norms[static_cast<size_t>(g) * n_pad + row];
-        }
+        for (int k = 0; k < NN; ++k)
+            st.norms[k] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, min(w * NN + k, groups - 1) * n_pad * 2, 0);
     } else {
-        const int g = min(w / wpg, groups - 1);
-        st.norms[0] = norms[static_cast<size_t>(g) * n_pad + row];
+        st.norms[0] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, min(w / wpg, groups - 1) * n_pad * 2, 0);
     }
 }
 
-template <int KIND, int GROUP>
-__device__ __forceinline__ void sdot_compute(const SdotWindow<KIND, GROUP> &st, const ND_CONST int32_t *__restrict__ qw,
-                                             const ND_CONST float *__restrict__ xs, const uint32_t cent[4], float cs,
-                                             float &value, int &dot, int w, int groups, int wpg) {
+// Per window and batch row, the permuted int8 activations (kWindow/4 dwords)
+// and the group scales closing in the window are staged in LDS once per
+// workgroup and read back as wave-uniform (broadcast) loads.
+template <int GROUP, int BT>
+struct Stage {
+    static constexpr int kQ = kWindow / 4;                               // dwords per batch row
+    static constexpr int kXs = GROUP > 0 ? kWindow / GROUP : 1;          // scales per batch row
+    static constexpr int kQ4 = BT * kQ / 4;                              // uint4 per window
+    static constexpr int kXsAll = BT * kXs;
+};
+
+template <int GROUP, int BT>
+struct StageRegs {
+    u32x4 q[(Stage<GROUP, BT>::kQ4 + kRowsPerBlock - 1) / kRowsPerBlock];
+    float xs[(Stage<GROUP, BT>::kXsAll + kRowsPerBlock - 1) / kRowsPerBlock];
+};
+
+// Thread t fetches staged items t, t + blockDim, ... of window w.
+template <int GROUP, int BT>
+__device__ __forceinline__ void stage_load(StageRegs<GROUP, BT> &r, __amdgpu_buffer_rsrc_t q,
+                                           __amdgpu_buffer_rsrc_t xs, int qdw, int groups, int w, int wpg) {
+    using S = Stage<GROUP, BT>;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < int(sizeof(r.q) / sizeof(r.q[0])); ++k) {
+        const int i = t + k * kRowsPerBlock;  // uint4 index within the window
+        const int b = i / (S::kQ / 4), j = i % (S::kQ / 4);
+        // out-of-range indices read zero through the buffer bound
+        r.q[k] = __builtin_amdgcn_raw_buffer_load_b128(q, (b * qdw + w * S::kQ + j * 4) * 4u, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < int(sizeof(r.xs) / sizeof(r.xs[0])); ++k) {
+        const int i = t + k * kRowsPerBlock;
+        const int b = i / S::kXs, gi = i % S::kXs;
+        const int g = GROUP > 0 ? min(w * S::kXs + gi, groups - 1) : min(w / wpg, groups - 1);
+        r.xs[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xs, (b * groups + g) * 4u, 0, 0));
+    }
+}
+
+template <int GROUP, int BT>
+__device__ __forceinline__ void stage_store(const StageRegs<GROUP, BT> &r, u32x4 *lq, float *lxs) {
+    using S = Stage<GROUP, BT>;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < int(sizeof(r.q) / sizeof(r.q[0])); ++k) {
+        const int i = t + k * kRowsPerBlock;
+        if (i < S::kQ4) lq[i] = r.q[k];
+    }
+#pragma unroll
+    for (int k = 0; k < int(sizeof(r.xs) / sizeof(r.xs[0])); ++k) {
+        const int i = t + k * kRowsPerBlock;
+        if (i < S::kXsAll) lxs[i] = r.xs[k];
+    }
+}
+
+// One window: decode each code dword once, dot it against BT batch rows.
+template <int KIND, int GROUP, int BT>
+__device__ __forceinline__ void sdot_compute(const SdotWindow<KIND, GROUP> &st, const u32x4 *lq, const float *lxs,
+                                             const uint32_t cent[4], float cs, float (&value)[BT], int (&dot)[BT],
+                                             int w, int groups, int wpg) {
+    using S = Stage<GROUP, BT>;
     constexpr int C = SdotWindow<KIND, GROUP>::kChunks;
     constexpr int NN = SdotWindow<KIND, GROUP>::kNorms;
     const int gbase = w * NN;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
         const uint32_t words[4] = {st.codes[c].x, st.codes[c].y, st.codes[c].z, st.codes[c].w};
+        // this chunk's activations: 8 (4-bit) or 16 (2-bit) dwords per batch row
+        constexpr int QPC = KIND == kNib ? 8 : 16;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             const uint32_t wd = words[d];
             if constexpr (KIND == kNib) {
                 uint32_t ce, co;
                 decode_nib(wd, cent[0], cent[1], cent[2], cent[3], ce, co);
-                const int qi = (c * 4 + d) * 2;
-                dot = __builtin_amdgcn_sdot4(static_cast<int>(ce), qw[qi], dot, false);
-                dot = __builtin_amdgcn_sdot4(static_cast<int>(co), qw[qi + 1], dot, false);
-                if constexpr (GROUP > 0) {
-                    const int pos_end = (c * 4 + d + 1) * 8;
-                    if (pos_end % GROUP == 0) {
-                        const int k = pos_end / GROUP - 1;
-                        if (gbase + k < groups)
-                            value += (static_cast<float>(dot) * (h2f(st.norms[k]) * cs)) * xs[gbase + k];
-                        dot = 0;
-                    }
+#pragma unroll
+                for (int b = 0; b < BT; ++b) {
+                    const uint32_t *qb = reinterpret_cast<const uint32_t *>(lq + b * (S::kQ / 4)) + c * QPC + d * 2;
+                    dot[b] = __builtin_amdgcn_sdot4(static_cast<int>(ce), static_cast<int>(qb[0]), dot[b], false);
+                    dot[b] = __builtin_amdgcn_sdot4(static_cast<int>(co), static_cast<int>(qb[1]), dot[b], false);
                 }
             } else {
-                const int qi = (c * 4 + d) * 4;
+                uint32_t cc[4];
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    const uint32_t sel = (wd >> (2 * m)) & 0x03030303u;
-                    const uint32_t cc = __builtin_amdgcn_perm(0u, cent[0], sel);
-                    dot = __builtin_amdgcn_sdot4(static_cast<int>(cc), qw[qi + m], dot, false);
+                for (int m = 0; m < 4; ++m) cc[m] = __builtin_amdgcn_perm(0u, cent[0], (wd >> (2 * m)) & 0x03030303u);
+#pragma unroll
+                for (int b = 0; b < BT; ++b) {
+                    const uint32_t *qb = reinterpret_cast<const uint32_t *>(lq + b * (S::kQ / 4)) + c * QPC + d * 4;
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        dot[b] = __builtin_amdgcn_sdot4(static_cast<int>(cc[m]), static_cast<int>(qb[m]), dot[b], false);
                 }
-                if constexpr (GROUP > 0) {
-                    const int pos_end = (c * 4 + d + 1) * 16;
-                    if (pos_end % GROUP == 0) {
-                        const int k = pos_end / GROUP - 1;
-                        if (gbase + k < groups)
-                            value += (static_cast<float>(dot) * (h2f(st.norms[k]) * cs)) * xs[gbase + k];
-                        dot = 0;
+            }
+            if constexpr (GROUP > 0) {
+                const int pos_end = (c * 4 + d + 1) * (KIND == kNib ? 8 : 16);
+                if (pos_end % GROUP == 0) {
+                    const int k = pos_end / GROUP - 1;
+                    if (gbase + k < groups) {
+                        const float ns = h2f(st.norms[k]) * cs;  // sdot.cpp:43-44
+#pragma unroll
+                        for (int b = 0; b < BT; ++b)
+                            value[b] += (static_cast<float>(dot[b]) * ns) * lxs[b * S::kXs + k];
                     }
+#pragma unroll
+                    for (int b = 0; b < BT; ++b) dot[b] = 0;
                 }
             }
         }
     }
     if constexpr (GROUP == 0) {
         if ((w + 1) % wpg == 0) {
-            const int g = w / wpg;
-            if (g < groups) value += (static_cast<float>(dot) * (h2f(st.norms[0]) * cs)) * xs[g];
-            dot = 0;
+            if (w / wpg < groups) {
+                const float ns = h2f(st.norms[0]) * cs;
+#pragma unroll
+                for (int b = 0; b < BT; ++b) value[b] += (static_cast<float>(dot[b]) * ns) * lxs[b];
+            }
+#pragma unroll
+            for (int b = 0; b < BT; ++b) dot[b] = 0;
         }
     }
 }
 
-template <int KIND, int GROUP>
-__global__ __launch_bounds__(kRowsPerBlock) void sdot_gemv_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
-                                                                  int njobs, SdotGeom geom) {
+// Batch rows [b_begin, b_end) in tiles of BT; one lane per output row.
+template <int KIND, int GROUP, int BT>
+__global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+                                                                     int njobs, SdotGeom geom, int b_begin, int b_end) {
+    using S = Stage<GROUP, BT>;
+    __shared__ u32x4 lq[2][S::kQ4];
+    __shared__ float lxs[2][S::kXsAll];
     const int blk = blockIdx.x;
     SdotJob J = job0;
     if (njobs > 0) {
@@ -190,47 +258,96 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_gemv_kernel(SdotJob job0, 
         J.block_begin = cj[j].block_begin;
         J.batch = cj[j].batch;
     }
-    const ND_GLOBAL u32x4 *__restrict__ codes = (const ND_GLOBAL u32x4 *)(J.codes);
-    const ND_GLOBAL uint16_t *__restrict__ norms = (const ND_GLOBAL uint16_t *)(J.norms);
-    const int n_pad = J.n_pad, rows = J.rows, batch = J.batch;
+    const int n_pad = J.n_pad, rows = J.rows;
     const int row = (blk - J.block_begin) * kRowsPerBlock + threadIdx.x;
     const int windows = geom.windows, groups = geom.groups;
     const int wpg = GROUP == 0 ? geom.group / kWindow : 1;
     const int qdw = windows * (kWindow / 4);  // int32 activation words per batch row
     const uint32_t cent[4] = {geom.cent[0], geom.cent[1], geom.cent[2], geom.cent[3]};
     const float cs = geom.centroid_scale;
+    const __amdgpu_buffer_rsrc_t codes = buffer_rsrc(J.codes, static_cast<uint32_t>(geom.chunks) * n_pad * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms, static_cast<uint32_t>(groups) * n_pad * 2u);
 
-    for (int b = 0; b < batch; ++b) {
-        const ND_CONST int32_t *__restrict__ q = (const ND_CONST int32_t *)(J.q) + static_cast<size_t>(b) * qdw;
-        const ND_CONST float *__restrict__ xs = (const ND_CONST float *)(J.xs) + static_cast<size_t>(b) * groups;
+    for (int b0 = b_begin; b0 < b_end; b0 += BT) {
+        const __amdgpu_buffer_rsrc_t q = buffer_rsrc(J.q + static_cast<size_t>(b0) * qdw, static_cast<uint32_t>(BT) * qdw * 4u);
+        const __amdgpu_buffer_rsrc_t xs = buffer_rsrc(J.xs + static_cast<size_t>(b0) * groups, static_cast<uint32_t>(BT) * groups * 4u);
         SdotWindow<KIND, GROUP> cur, nxt;
+        StageRegs<GROUP, BT> sr;
+        stage_load<GROUP, BT>(sr, q, xs, qdw, groups, 0, wpg);
         sdot_load<KIND, GROUP>(cur, codes, norms, n_pad, row, 0, groups, wpg);
-        float value = 0.0f;
-        int dot = 0;
-        for (int w = 0; w < windows; w += 2) {
-            if (w + 1 < windows) sdot_load<KIND, GROUP>(nxt, codes, norms, n_pad, row, w + 1, groups, wpg);
-            sdot_compute<KIND, GROUP>(cur, q + w * (kWindow / 4), xs, cent, cs, value, dot, w, groups, wpg);
-            if (w + 1 >= windows) break;
-            if (w + 2 < windows) sdot_load<KIND, GROUP>(cur, codes, norms, n_pad, row, w + 2, groups, wpg);
-            sdot_compute<KIND, GROUP>(nxt, q + (w + 1) * (kWindow / 4), xs, cent, cs, value, dot, w + 1, groups, wpg);
+        __syncthreads();  // previous tile finished reading stage buffer 0
+        stage_store<GROUP, BT>(sr, lq[0], lxs[0]);
+        __syncthreads();
+        float value[BT];
+        int dot[BT];
+#pragma unroll
+        for (int b = 0; b < BT; ++b) {
+            value[b] = 0.0f;
+            dot[b] = 0;
         }
-        if (row < rows) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b) * rows + row] = value;
+        // Per window: issue the next window's staged activations and codes
+        // (unconditional, clamped), compute this window, store the next
+        // staging buffer, one barrier.
+        for (int w = 0; w < windows; w += 2) {
+            const int w1 = min(w + 1, windows - 1);
+            stage_load<GROUP, BT>(sr, q, xs, qdw, groups, w1, wpg);
+            sdot_load<KIND, GROUP>(nxt, codes, norms, n_pad, row, w1, groups, wpg);
+            sdot_compute<KIND, GROUP, BT>(cur, lq[0], lxs[0], cent, cs, value, dot, w, groups, wpg);
+            if (w + 1 < windows) stage_store<GROUP, BT>(sr, lq[1], lxs[1]);
+            __syncthreads();
+            if (w + 1 >= windows) break;
+            const int w2 = min(w + 2, windows - 1);
+            stage_load<GROUP, BT>(sr, q, xs, qdw, groups, w2, wpg);
+            sdot_load<KIND, GROUP>(cur, codes, norms, n_pad, row, w2, groups, wpg);
+            sdot_compute<KIND, GROUP, BT>(nxt, lq[1], lxs[1], cent, cs, value, dot, w + 1, groups, wpg);
+            if (w + 2 < windows) stage_store<GROUP, BT>(sr, lq[0], lxs[0]);
+            __syncthreads();
+        }
+        if (row < rows) {
+#pragma unroll
+            for (int b = 0; b < BT; ++b) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + b) * rows + row] = value[b];
+        }
     }
 }
 
-template <int KIND>
-void launch_sdot_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
-                      hipStream_t s) {
+template <int KIND, int BT>
+void launch_sdot_bt(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int b0,
+                    int b1, hipStream_t s) {
     dim3 grid(blocks), block(kRowsPerBlock);
     switch (g.group > kWindow ? 0 : g.group) {
-    case 16: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 16>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 32: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 64>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 128>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 256: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    default: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 0>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 8:
+        if constexpr (KIND == kNib) {
+            hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 8, BT>), grid, block, 0, s, job0, jobs, njobs, g, b0, b1);
+            break;
+        }
+        [[fallthrough]];
+    case 16: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 16, BT>), grid, block, 0, s, job0, jobs, njobs, g, b0, b1); break;
+    case 32: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 32, BT>), grid, block, 0, s, job0, jobs, njobs, g, b0, b1); break;
+    case 64: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 64, BT>), grid, block, 0, s, job0, jobs, njobs, g, b0, b1); break;
+    case 128: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 128, BT>), grid, block, 0, s, job0, jobs, njobs, g, b0, b1); break;
+    case 256: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 256, BT>), grid, block, 0, s, job0, jobs, njobs, g, b0, b1); break;
+    default: hipLaunchKernelGGL((sdot_gemv_kernel<KIND, 0, BT>), grid, block, 0, s, job0, jobs, njobs, g, b0, b1); break;
     }
     ND_HIP(hipGetLastError());
+}
+
+// The batch is covered by tiles of 16, 8, 4, 2 and 1 rows (largest first).
+template <int KIND>
+void launch_sdot_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                      hipStream_t s) {
+    int b = 0;
+    auto run = [&](int bt, auto launcher) {
+        const int n = (batch - b) / bt * bt;
+        if (n > 0) {
+            launcher(b, b + n);
+            b += n;
+        }
+    };
+    run(16, [&](int b0, int b1) { launch_sdot_bt<KIND, 16>(g, job0, jobs, njobs, blocks, b0, b1, s); });
+    run(8, [&](int b0, int b1) { launch_sdot_bt<KIND, 8>(g, job0, jobs, njobs, blocks, b0, b1, s); });
+    run(4, [&](int b0, int b1) { launch_sdot_bt<KIND, 4>(g, job0, jobs, njobs, blocks, b0, b1, s); });
+    run(2, [&](int b0, int b1) { launch_sdot_bt<KIND, 2>(g, job0, jobs, njobs, blocks, b0, b1, s); });
+    run(1, [&](int b0, int b1) { launch_sdot_bt<KIND, 1>(g, job0, jobs, njobs, blocks, b0, b1, s); });
 }
 
 }  // namespace
@@ -246,22 +363,13 @@ void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded
     ND_HIP(hipGetLastError());
 }
 
-void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
+void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
                       hipStream_t s) {
-    if (blocks <= 0) return;
+    if (blocks <= 0 || batch <= 0) return;
     ND_CHECK(g.group >= 8, "int8 path: group must be >= 8");
     ND_CHECK(g.kind == kNib || g.group >= 16, "int8 path: 2-bit codes need group >= 16");
-    if (g.kind == kNib) {
-        if (g.group == 8) {
-            dim3 grid(blocks), block(kRowsPerBlock);
-            hipLaunchKernelGGL((sdot_gemv_kernel<kNib, 8>), grid, block, 0, s, job0, jobs, njobs, g);
-            ND_HIP(hipGetLastError());
-        } else {
-            launch_sdot_kind<kNib>(g, job0, jobs, njobs, blocks, s);
-        }
-    } else {
-        launch_sdot_kind<kCrumb>(g, job0, jobs, njobs, blocks, s);
-    }
+    if (g.kind == kNib) launch_sdot_kind<kNib>(g, job0, jobs, njobs, blocks, batch, s);
+    else launch_sdot_kind<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
 }
 
 }  // namespace nd
