@@ -185,6 +185,8 @@ SdotGeom SdotHandle::geom() const {
 }
 
 void SdotHandle::prepare_device(const float *d_x, int batch, int32_t *q, float *xs, hipStream_t s) {
+    if (launch_sdot_prepare(d_x, nullptr, batch, batch, m.in, m.padded, m.dev, m.group, m.scale, m.kind, q, xs, s))
+        return;
     st.rot.reserve(size_t(batch) * m.dev);
     m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
     launch_sdot_quantize(st.rot.p, m.dev, batch, m.padded, m.dev, m.group, m.kind, q, xs, s);
@@ -227,6 +229,7 @@ struct Plan {
     DevBuf<float> rot;
     DevBuf<int32_t> q;
     DevBuf<float> xscale;
+    DevBuf<const float *> xptr;  // device table of the count input pointers (int8 prepare)
     DevBuf<uint8_t> jobs;
     int blocks = 0;
     const Matrix *first = nullptr;
@@ -267,6 +270,8 @@ static void plan_upload(Plan &p) {
             block += mi.n_pad / kRowsPerBlock;
         }
         host.assign(reinterpret_cast<uint8_t *>(jobs.data()), reinterpret_cast<uint8_t *>(jobs.data() + p.count));
+        p.xptr.reserve(p.count);
+        ND_HIP(hipMemcpy(p.xptr.p, p.xs_in.data(), p.count * sizeof(const float *), hipMemcpyHostToDevice));
     }
     p.blocks = block;
     p.jobs.reserve(host.size());
@@ -277,16 +282,22 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
     const Matrix &m = *p.first;
     // x_i is [batch][in] on the device; the FP32 GEMV transforms it in-kernel
     // unless the group exceeds one table window
-    if (p.sdot || !gemv_fuses_fwht(m.group))
-        for (int i = 0; i < p.count; ++i)
-            m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
     if (!p.sdot) {
+        if (!gemv_fuses_fwht(m.group))
+            for (int i = 0; i < p.count; ++i)
+                m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
         launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s);
     } else {
         const SdotHandle &h0 = *p.sd[0];
-        launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
-                             p.xscale.p, s);
+        // one launch prepares every (matrix, batch row) input
+        if (!launch_sdot_prepare(nullptr, p.xptr.p, p.batch, p.count * p.batch, m.in, m.padded, m.dev, m.group,
+                                 m.scale, m.kind, p.q.p, p.xscale.p, s)) {
+            for (int i = 0; i < p.count; ++i)
+                m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
+            launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
+                                 p.xscale.p, s);
+        }
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
         launch_sdot_gemv(h0.geom(), SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, p.batch,
                          s);

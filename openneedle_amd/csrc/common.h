@@ -185,6 +185,13 @@ void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, 
                     const int64_t *ids, int count, int in, int padded, float *scratch, float *y,
                     hipStream_t s);
 
+// int8 path, one launch for nvec = count * batch vectors: vector v is row
+// v % batch of matrix input v / batch, read from x0 (count == 1, xptr null) or
+// xptr[v / batch] (a device table); each row has `in` floats. FWHT per group,
+// quantize, permute. Returns false (nothing launched) when the group is too
+// large for one block's LDS; callers then transform and quantize separately.
+bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, int nvec, int in, int padded,
+                         int dev_positions, int group, float scale, int kind, int32_t *q, float *xs, hipStream_t s);
 // int8 path: quantize rot (already transformed) into permuted int8 + scales.
 void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded, int dev_positions,
                           int group, int kind, int32_t *q, float *xs, hipStream_t s);

@@ -10,7 +10,7 @@
 // GEMV: one lane per output row, codes chunk-major (common.h). Codes become
 // int8 centroids with v_perm_b32 byte lookups (three perms per four 4-bit
 // codes, one per four 2-bit codes) and are multiplied with v_dot4_i32_i8
-// against activations held in scalar registers (uniform across the wave).
+// against activations staged in LDS per workgroup (wave-uniform reads).
 // The int32 group dot is exact in any order; the epilogue is the reference's
 //   value += (float(dot) * (half(norm) * cs)) * x_scale[g]
 // sequentially over g (sdot.cpp:43-44, 142-149), so outputs are bit-exact.
@@ -61,6 +61,64 @@ __global__ __launch_bounds__(256) void sdot_quantize_kernel(const float *__restr
             if (scale == 0.0f) scale = absmax;  // subnormal absmax/127 underflows
             if (p % group == 0) xs[static_cast<size_t>(v) * groups + p / group] = scale;
             float val = rintf(rv[p] / scale);
+            val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
+            out = static_cast<int8_t>(val);
+        }
+        qv[permuted_index(kind, p)] = out;
+    }
+}
+
+// Fused prepare: one block per (segment of positions, vector). The FWHT
+// runs in LDS with the reference's stage order (cq.cpp:30-46: h = 1, 2, ...,
+// (a + b, a - b), then one multiply by 1/sqrt(group)), so the rotated values,
+// and from them the int8 codes and scales, are bit-identical to a separate
+// transform followed by sdot_quantize_kernel. seg = max(group, 1024).
+constexpr int kPrepareMaxGroup = 16384;
+constexpr int kPrepareMinSeg = 1024;
+
+__global__ __launch_bounds__(256) void sdot_prepare_kernel(const float *__restrict__ x0,
+                                                           const float *const *__restrict__ xptr, int batch, int in,
+                                                           int padded, int dev, int group, float scale, int kind,
+                                                           int8_t *__restrict__ q, float *__restrict__ xs, int groups,
+                                                           int seg) {
+    extern __shared__ float buf[];
+    __shared__ unsigned gmax[kPrepareMinSeg / 8];
+    const int v = blockIdx.y;
+    const int base = blockIdx.x * seg;
+    const int ngroups = seg / group;  // whole groups: seg is a multiple of group
+    const float *xv = (xptr ? xptr[v / batch] : x0) + static_cast<size_t>(v % batch) * in;
+    for (int i = threadIdx.x; i < ngroups; i += blockDim.x) gmax[i] = 0u;
+    for (int i = threadIdx.x; i < seg; i += blockDim.x) {
+        const int p = base + i;
+        buf[i] = p < in ? xv[p] : 0.0f;
+    }
+    __syncthreads();
+    for (int h = 1; h < group; h <<= 1) {
+        for (int t = threadIdx.x; t < seg / 2; t += blockDim.x) {
+            const int lo = (t / h) * 2 * h + (t % h);
+            const float a = buf[lo], b = buf[lo + h];
+            buf[lo] = a + b;
+            buf[lo + h] = a - b;
+        }
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < seg; i += blockDim.x) {
+        const float r = buf[i] * scale;
+        buf[i] = r;
+        if (base + i < padded) atomicMax(&gmax[i / group], __float_as_uint(fabsf(r)));
+    }
+    __syncthreads();
+    int8_t *qv = q + static_cast<size_t>(v) * dev;
+    for (int i = threadIdx.x; i < seg; i += blockDim.x) {
+        const int p = base + i;
+        if (p >= dev) break;
+        int8_t out = 0;
+        if (p < padded) {
+            const float absmax = __uint_as_float(gmax[i / group]);
+            float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
+            if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
+            if (p % group == 0) xs[static_cast<size_t>(v) * groups + p / group] = sc;
+            float val = rintf(buf[i] / sc);
             val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
             out = static_cast<int8_t>(val);
         }
@@ -125,8 +183,10 @@ struct Stage {
 
 template <int GROUP, int BT>
 struct StageRegs {
-    u32x4 q[(Stage<GROUP, BT>::kQ4 + kRowsPerBlock - 1) / kRowsPerBlock];
-    float xs[(Stage<GROUP, BT>::kXsAll + kRowsPerBlock - 1) / kRowsPerBlock];
+    static constexpr int kQn = (Stage<GROUP, BT>::kQ4 + kRowsPerBlock - 1) / kRowsPerBlock;
+    static constexpr int kXsn = (Stage<GROUP, BT>::kXsAll + kRowsPerBlock - 1) / kRowsPerBlock;
+    u32x4 q[kQn];
+    float xs[kXsn];
 };
 
 // Thread t fetches staged items t, t + blockDim, ... of window w.
@@ -136,18 +196,22 @@ __device__ __forceinline__ void stage_load(StageRegs<GROUP, BT> &r, __amdgpu_buf
     using S = Stage<GROUP, BT>;
     const int t = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < int(sizeof(r.q) / sizeof(r.q[0])); ++k) {
+    for (int k = 0; k < StageRegs<GROUP, BT>::kQn; ++k) {
         const int i = t + k * kRowsPerBlock;  // uint4 index within the window
         const int b = i / (S::kQ / 4), j = i % (S::kQ / 4);
-        // out-of-range indices read zero through the buffer bound
-        r.q[k] = __builtin_amdgcn_raw_buffer_load_b128(q, (b * qdw + w * S::kQ + j * 4) * 4u, 0, 0);
+        // Indices past the window get an offset beyond the buffer bound: the
+        // load returns zero without a memory request. Every thread loads and
+        // stores, so the loads stay where they are issued.
+        const uint32_t off = i < S::kQ4 ? (b * qdw + w * S::kQ + j * 4) * 4u : 0x80000000u;
+        r.q[k] = __builtin_amdgcn_raw_buffer_load_b128(q, off, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < int(sizeof(r.xs) / sizeof(r.xs[0])); ++k) {
+    for (int k = 0; k < StageRegs<GROUP, BT>::kXsn; ++k) {
         const int i = t + k * kRowsPerBlock;
         const int b = i / S::kXs, gi = i % S::kXs;
         const int g = GROUP > 0 ? min(w * S::kXs + gi, groups - 1) : min(w / wpg, groups - 1);
-        r.xs[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xs, (b * groups + g) * 4u, 0, 0));
+        const uint32_t off = i < S::kXsAll ? (b * groups + g) * 4u : 0x80000000u;
+        r.xs[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xs, off, 0, 0));
     }
 }
 
@@ -156,15 +220,9 @@ __device__ __forceinline__ void stage_store(const StageRegs<GROUP, BT> &r, u32x4
     using S = Stage<GROUP, BT>;
     const int t = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < int(sizeof(r.q) / sizeof(r.q[0])); ++k) {
-        const int i = t + k * kRowsPerBlock;
-        if (i < S::kQ4) lq[i] = r.q[k];
-    }
+    for (int k = 0; k < StageRegs<GROUP, BT>::kQn; ++k) lq[t + k * kRowsPerBlock] = r.q[k];
 #pragma unroll
-    for (int k = 0; k < int(sizeof(r.xs) / sizeof(r.xs[0])); ++k) {
-        const int i = t + k * kRowsPerBlock;
-        if (i < S::kXsAll) lxs[i] = r.xs[k];
-    }
+    for (int k = 0; k < StageRegs<GROUP, BT>::kXsn; ++k) lxs[t + k * kRowsPerBlock] = r.xs[k];
 }
 
 // One window: decode each code dword once, dot it against BT batch rows.
@@ -209,11 +267,14 @@ __device__ __forceinline__ void sdot_compute(const SdotWindow<KIND, GROUP> &st, 
                 const int pos_end = (c * 4 + d + 1) * (KIND == kNib ? 8 : 16);
                 if (pos_end % GROUP == 0) {
                     const int k = pos_end / GROUP - 1;
-                    if (gbase + k < groups) {
-                        const float ns = h2f(st.norms[k]) * cs;  // sdot.cpp:43-44
+                    // A select rather than a branch: the norm is used on every
+                    // path, so its load is never sunk next to its use.
+                    const bool real = gbase + k < groups;
+                    const float ns = h2f(st.norms[k]) * cs;  // sdot.cpp:43-44
 #pragma unroll
-                        for (int b = 0; b < BT; ++b)
-                            value[b] += (static_cast<float>(dot[b]) * ns) * lxs[b * S::kXs + k];
+                    for (int b = 0; b < BT; ++b) {
+                        const float sum = value[b] + (static_cast<float>(dot[b]) * ns) * lxs[b * S::kXs + k];
+                        value[b] = real ? sum : value[b];
                     }
 #pragma unroll
                     for (int b = 0; b < BT; ++b) dot[b] = 0;
@@ -223,10 +284,12 @@ __device__ __forceinline__ void sdot_compute(const SdotWindow<KIND, GROUP> &st, 
     }
     if constexpr (GROUP == 0) {
         if ((w + 1) % wpg == 0) {
-            if (w / wpg < groups) {
-                const float ns = h2f(st.norms[0]) * cs;
+            const bool real = w / wpg < groups;
+            const float ns = h2f(st.norms[0]) * cs;
 #pragma unroll
-                for (int b = 0; b < BT; ++b) value[b] += (static_cast<float>(dot[b]) * ns) * lxs[b];
+            for (int b = 0; b < BT; ++b) {
+                const float sum = value[b] + (static_cast<float>(dot[b]) * ns) * lxs[b];
+                value[b] = real ? sum : value[b];
             }
 #pragma unroll
             for (int b = 0; b < BT; ++b) dot[b] = 0;
@@ -239,8 +302,9 @@ template <int KIND, int GROUP, int BT>
 __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
                                                                      int njobs, SdotGeom geom, int b_begin, int b_end) {
     using S = Stage<GROUP, BT>;
-    __shared__ u32x4 lq[2][S::kQ4];
-    __shared__ float lxs[2][S::kXsAll];
+    // staging buffers padded to whole blocks: every thread stores its slots
+    __shared__ u32x4 lq[2][StageRegs<GROUP, BT>::kQn * kRowsPerBlock];
+    __shared__ float lxs[2][StageRegs<GROUP, BT>::kXsn * kRowsPerBlock];
     const int blk = blockIdx.x;
     SdotJob J = job0;
     if (njobs > 0) {
@@ -287,22 +351,26 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
         }
         // Per window: issue the next window's staged activations and codes
         // (unconditional, clamped), compute this window, store the next
-        // staging buffer, one barrier.
-        for (int w = 0; w < windows; w += 2) {
-            const int w1 = min(w + 1, windows - 1);
-            stage_load<GROUP, BT>(sr, q, xs, qdw, groups, w1, wpg);
-            sdot_load<KIND, GROUP>(nxt, codes, norms, n_pad, row, w1, groups, wpg);
+        // staging buffer, one barrier. Pairs of windows run in a loop with a
+        // single exit (no mid-body break), so the loop header is reached only
+        // from the loop itself and the prologue; an odd last window follows.
+        int w = 0;
+        for (; w + 1 < windows; w += 2) {
+            stage_load<GROUP, BT>(sr, q, xs, qdw, groups, w + 1, wpg);
+            sdot_load<KIND, GROUP>(nxt, codes, norms, n_pad, row, w + 1, groups, wpg);
+            asm volatile("" ::: "memory");  // keep the next window's loads ahead of this compute
             sdot_compute<KIND, GROUP, BT>(cur, lq[0], lxs[0], cent, cs, value, dot, w, groups, wpg);
-            if (w + 1 < windows) stage_store<GROUP, BT>(sr, lq[1], lxs[1]);
+            stage_store<GROUP, BT>(sr, lq[1], lxs[1]);
             __syncthreads();
-            if (w + 1 >= windows) break;
             const int w2 = min(w + 2, windows - 1);
             stage_load<GROUP, BT>(sr, q, xs, qdw, groups, w2, wpg);
             sdot_load<KIND, GROUP>(cur, codes, norms, n_pad, row, w2, groups, wpg);
+            asm volatile("" ::: "memory");
             sdot_compute<KIND, GROUP, BT>(nxt, lq[1], lxs[1], cent, cs, value, dot, w + 1, groups, wpg);
-            if (w + 2 < windows) stage_store<GROUP, BT>(sr, lq[0], lxs[0]);
+            stage_store<GROUP, BT>(sr, lq[0], lxs[0]);  // window w2 (re-staged if it is the last)
             __syncthreads();
         }
+        if (w < windows) sdot_compute<KIND, GROUP, BT>(cur, lq[0], lxs[0], cent, cs, value, dot, w, groups, wpg);
         if (row < rows) {
 #pragma unroll
             for (int b = 0; b < BT; ++b) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + b) * rows + row] = value[b];
@@ -351,6 +419,19 @@ void launch_sdot_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
 }
 
 }  // namespace
+
+bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, int nvec, int in, int padded,
+                         int dev, int group, float scale, int kind, int32_t *q, float *xs, hipStream_t s) {
+    if (group > kPrepareMaxGroup) return false;
+    ND_CHECK(group >= 8 && (group & (group - 1)) == 0, "int8 prepare: group must be a power of two >= 8");
+    if (nvec <= 0) return true;
+    const int seg = group > kPrepareMinSeg ? group : kPrepareMinSeg;
+    dim3 grid((dev + seg - 1) / seg, nvec), block(256);
+    hipLaunchKernelGGL(sdot_prepare_kernel, grid, block, seg * sizeof(float), s, x0, xptr, batch, in, padded, dev,
+                       group, scale, kind, reinterpret_cast<int8_t *>(q), xs, padded / group, seg);
+    ND_HIP(hipGetLastError());
+    return true;
+}
 
 void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded, int dev, int group, int kind,
                           int32_t *q, float *xs, hipStream_t s) {
