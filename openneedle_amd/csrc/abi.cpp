@@ -148,7 +148,7 @@ void CqHandle::rows_host(const int64_t *ids, float *y, int count) {
     st.rot.reserve(size_t(count) * m.padded);
     st.y.reserve(size_t(count) * m.in);
     ND_HIP(hipMemcpyAsync(dids.p, ids, size_t(count) * sizeof(int64_t), hipMemcpyHostToDevice, st.stream));
-    launch_cq_rows(m.geom(), m.codes.p, m.norms.p, m.n_pad, dids.p, count, m.in, m.padded, st.rot.p, st.y.p,
+    launch_cq_rows(m.geom(), m.codes.p, m.norms.p, dids.p, count, m.in, m.padded, st.rot.p, st.y.p,
                    st.stream);
     ND_HIP(hipMemcpyAsync(y, st.y.p, size_t(count) * m.in * sizeof(float), hipMemcpyDeviceToHost, st.stream));
     ND_HIP(hipStreamSynchronize(st.stream));

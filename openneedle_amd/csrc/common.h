@@ -83,13 +83,14 @@ struct HostBuf {
 // ---------------------------------------------------------------------------
 // Device layout of a CQ matrix.
 //
-// Codes are re-laid out at create time into "chunk-major" order: a chunk is
-// 16 bytes of one row (32 four-bit codes or 64 two-bit codes) and
-//     codes[(chunk * n_pad + row)]   (one uint4 per (chunk, row))
-// so the 64 lanes of a wavefront, one row each, read 1 KiB contiguous per
-// chunk. Norms are fp16 [groups][n_pad]. Rows are padded to a multiple of
-// kRowsPerBlock with zero codes/norms; each row's codes are padded to a whole
-// number of table windows (kWindow positions) with zero codes.
+// Codes are re-laid out at create time into row tiles of kRowsPerBlock rows,
+// chunk-major inside a tile: a chunk is 16 bytes of one row (32 four-bit
+// codes or 64 two-bit codes), one uint4 per (chunk, row) at code_index(), so
+// the 64 lanes of a wavefront, one row each, read 1 KiB contiguous per chunk
+// and a workgroup's whole tile is one contiguous run. Norms are fp16 at
+// norm_index(). Rows are padded to a multiple of kRowsPerBlock with zero
+// codes/norms; each row's codes are padded to a whole number of table
+// windows (kWindow positions) with zero codes.
 // CQ4 and CQ3 use 4-bit device codes (CQ3 is widened once at create time);
 // CQ2 and ternary use 2-bit device codes.
 // ---------------------------------------------------------------------------
@@ -131,13 +132,26 @@ struct CqGeom {
     float lut[16];   // fp32 codebook indexed by device code
 };
 
+// Device layout of one matrix: rows in tiles of kRowsPerBlock (one GEMV
+// workgroup each); inside a tile, chunk-major with one 16-byte chunk per row:
+//   codes[tile][chunk][kRowsPerBlock]   norms[tile][group][kRowsPerBlock]
+// A workgroup therefore streams one contiguous run of chunks * 4 KiB of codes
+// (and groups * 512 B of norms), which HBM serves faster than the same bytes
+// strided across the whole matrix.
+__host__ __device__ inline size_t code_index(int r, int c, int chunks) {
+    return (static_cast<size_t>(r / kRowsPerBlock) * chunks + c) * kRowsPerBlock + r % kRowsPerBlock;
+}
+__host__ __device__ inline size_t norm_index(int r, int g, int groups) {
+    return (static_cast<size_t>(r / kRowsPerBlock) * groups + g) * kRowsPerBlock + r % kRowsPerBlock;
+}
+
 // Groups up to one table window run the activation FWHT inside the GEMV
 // kernel; larger groups use a separate transform pass.
 inline bool gemv_fuses_fwht(int group) { return group <= kWindow; }
 
 struct CqJob {
-    const uint4 *codes;       // [chunks][n_pad]
-    const uint16_t *norms;    // [groups][n_pad]
+    const uint4 *codes;       // [n_pad / kRowsPerBlock][chunks][kRowsPerBlock]
+    const uint16_t *norms;    // [n_pad / kRowsPerBlock][groups][kRowsPerBlock]
     const float *act;         // x [batch][in] (fused FWHT) or rot [batch][windows*kWindow]
     float *y;                 // outputs [batch][rows]
     int rows;
@@ -181,8 +195,7 @@ void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs_dev, i
                     hipStream_t s);
 
 // Dequantize rows: y[i][0..in) = FWHT(cb[code]*norm) cropped; uses rot-sized scratch.
-void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, int n_pad,
-                    const int64_t *ids, int count, int in, int padded, float *scratch, float *y,
+void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, const int64_t *ids, int count, int in, int padded, float *scratch, float *y,
                     hipStream_t s);
 
 // int8 path, one launch for nvec = count * batch vectors: vector v is row

@@ -50,7 +50,7 @@ __global__ void relayout_kernel(const uint8_t *__restrict__ packed, int rows, in
             }
         }
     }
-    codes[static_cast<size_t>(c) * n_pad + r] = make_uint4(out[0], out[1], out[2], out[3]);
+    codes[code_index(r, c, chunks)] = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
 __global__ void norms_transpose_kernel(const uint16_t *__restrict__ norms, int rows, int groups,
@@ -58,7 +58,7 @@ __global__ void norms_transpose_kernel(const uint16_t *__restrict__ norms, int r
     int r = blockIdx.x * blockDim.x + threadIdx.x;
     int g = blockIdx.y;
     if (r >= n_pad) return;
-    out[static_cast<size_t>(g) * n_pad + r] = r < rows ? norms[static_cast<size_t>(r) * groups + g] : uint16_t(0);
+    out[norm_index(r, g, groups)] = r < rows ? norms[static_cast<size_t>(r) * groups + g] : uint16_t(0);
 }
 
 // ---------------------------------------------------------------------------
@@ -290,29 +290,29 @@ struct WindowState {
     uint16_t norms[kNorms];
 };
 
-// Buffer loads: the chunk / norm-row offset is wave-uniform (soffset) and the
-// per-lane offset is one shared VGPR, so no per-chunk addresses stay live.
+// Buffer loads from the workgroup's row tile: the chunk / group offset is
+// wave-uniform (soffset) and the per-lane offset is one shared VGPR, so no
+// per-chunk addresses stay live.
 template <int KIND, int GROUP>
 __device__ __forceinline__ void load_window(WindowState<KIND, GROUP> &st, __amdgpu_buffer_rsrc_t codes,
-                                            __amdgpu_buffer_rsrc_t norms, int n_pad, int row, int w, int groups,
-                                            int windows_per_group) {
+                                            __amdgpu_buffer_rsrc_t norms, int w, int groups, int windows_per_group) {
     constexpr int C = WindowState<KIND, GROUP>::kChunks;
     constexpr int NN = WindowState<KIND, GROUP>::kNorms;
-    const uint32_t code_lane = static_cast<uint32_t>(row) * 16u;
-    const uint32_t norm_lane = static_cast<uint32_t>(row) * 2u;
+    const uint32_t code_lane = threadIdx.x * 16u;
+    const uint32_t norm_lane = threadIdx.x * 2u;
 #pragma unroll
     for (int c = 0; c < C; ++c)
-        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * n_pad * 16, 0);
+        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * kRowsPerBlock * 16, 0);
     // group indices are clamped (phantom groups past the last are never closed)
     if constexpr (GROUP > 0) {
 #pragma unroll
         for (int k = 0; k < NN; ++k) {
             const int g = min(w * NN + k, groups - 1);
-            st.norms[k] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, g * n_pad * 2, 0);
+            st.norms[k] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, g * kRowsPerBlock * 2, 0);
         }
     } else {
         const int g = min(w / windows_per_group, groups - 1);
-        st.norms[0] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, g * n_pad * 2, 0);
+        st.norms[0] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, g * kRowsPerBlock * 2, 0);
     }
 }
 
@@ -451,10 +451,16 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void cq_gemv_kernel(CqJob job0, c
         J.block_begin = cj[j].block_begin;
         J.batch = cj[j].batch;
     }
-    const int n_pad = J.n_pad, rows = J.rows, batch = J.batch;
-    const __amdgpu_buffer_rsrc_t codes = buffer_rsrc(J.codes, static_cast<uint32_t>(geom.chunks) * n_pad * 16u);
-    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms, static_cast<uint32_t>(geom.groups) * n_pad * 2u);
-    const int row = (blk - J.block_begin) * kRowsPerBlock + threadIdx.x;
+    const int rows = J.rows, batch = J.batch;
+    const int tile = blk - J.block_begin;
+    const int row = tile * kRowsPerBlock + threadIdx.x;
+    // this workgroup's row tile of codes and norms
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms =
+        buffer_rsrc(J.norms + static_cast<size_t>(tile) * geom.groups * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.groups) * kRowsPerBlock * 2u);
     const int windows = geom.windows, groups = geom.groups, in = geom.in;
     const int wpg = GROUP == 0 ? geom.group / kWindow : 1;
     const int act_stride = GROUP > 0 ? in : windows * kWindow;
@@ -469,7 +475,7 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void cq_gemv_kernel(CqJob job0, c
         WindowState<KIND, GROUP> cur, nxt;
         float xa[PPT];
         load_act(act, 0, xa);
-        load_window<KIND, GROUP>(cur, codes, norms, n_pad, row, 0, groups, wpg);
+        load_window<KIND, GROUP>(cur, codes, norms, 0, groups, wpg);
         __syncthreads();  // the previous batch row finished reading T[0]
         if constexpr (GROUP > 0) window_fwht<GROUP>(xa, scale, stage);
         build_table<KIND>(T[0], lut, xa);
@@ -485,7 +491,7 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void cq_gemv_kernel(CqJob job0, c
         for (int w = 0; w < windows; w += 2) {
             const int w1 = min(w + 1, windows - 1);
             load_act(act, w1, xa);
-            load_window<KIND, GROUP>(nxt, codes, norms, n_pad, row, w1, groups, wpg);
+            load_window<KIND, GROUP>(nxt, codes, norms, w1, groups, wpg);
             compute_window<KIND, GROUP>(cur, T[0], sum, gd, w, groups, wpg);
             if (w + 1 < windows) {
                 if constexpr (GROUP > 0) window_fwht<GROUP>(xa, scale, stage);
@@ -495,7 +501,7 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void cq_gemv_kernel(CqJob job0, c
             if (w + 1 >= windows) break;
             const int w2 = min(w + 2, windows - 1);
             load_act(act, w2, xa);
-            load_window<KIND, GROUP>(cur, codes, norms, n_pad, row, w2, groups, wpg);
+            load_window<KIND, GROUP>(cur, codes, norms, w2, groups, wpg);
             compute_window<KIND, GROUP>(nxt, T[1], sum, gd, w + 1, groups, wpg);
             if (w + 2 < windows) {
                 if constexpr (GROUP > 0) window_fwht<GROUP>(xa, scale, stage);
@@ -526,7 +532,7 @@ void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int
 // Row dequantization (cq.cpp:276-284): tmp = cb[code]*half(norm), then FWHT.
 // ---------------------------------------------------------------------------
 __global__ void dequant_rows_kernel(CqGeom geom, const uint4 *__restrict__ codes, const uint16_t *__restrict__ norms,
-                                    int n_pad, const int64_t *__restrict__ ids, int padded, float *__restrict__ tmp,
+                                    const int64_t *__restrict__ ids, int padded, float *__restrict__ tmp,
                                     int tmp_stride) {
     int p = blockIdx.x * blockDim.x + threadIdx.x;
     int i = blockIdx.y;
@@ -534,12 +540,12 @@ __global__ void dequant_rows_kernel(CqGeom geom, const uint4 *__restrict__ codes
     const int row = static_cast<int>(ids[i]);
     const int cpc = geom.kind == kNib ? 32 : 64;
     const int c = p / cpc, within = p % cpc;
-    const uint4 v = codes[static_cast<size_t>(c) * n_pad + row];
+    const uint4 v = codes[code_index(row, c, geom.chunks)];
     const uint32_t words[4] = {v.x, v.y, v.z, v.w};
     unsigned code;
     if (geom.kind == kNib) code = (words[within >> 3] >> ((within & 7) * 4)) & 15u;
     else code = (words[within >> 4] >> ((within & 15) * 2)) & 3u;
-    const float norm = h2f(norms[static_cast<size_t>(p / geom.group) * n_pad + row]);
+    const float norm = h2f(norms[norm_index(row, p / geom.group, geom.groups)]);
     tmp[static_cast<size_t>(i) * tmp_stride + p] = geom.lut[code] * norm;
 }
 
@@ -622,11 +628,11 @@ void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int n
     else launch_gemv_kind<kCrumb>(g, job0, jobs, njobs, blocks, s);
 }
 
-void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, int n_pad, const int64_t *ids,
+void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, const int64_t *ids,
                     int count, int in, int padded, float *scratch, float *y, hipStream_t s) {
     if (count <= 0) return;
     dim3 grid((padded + 255) / 256, count), block(256);
-    hipLaunchKernelGGL(dequant_rows_kernel, grid, block, 0, s, g, codes, norms, n_pad, ids, padded, scratch, padded);
+    hipLaunchKernelGGL(dequant_rows_kernel, grid, block, 0, s, g, codes, norms, ids, padded, scratch, padded);
     ND_HIP(hipGetLastError());
     // in-place FWHT of scratch rows, cropped to `in` columns into y
     float scale = g.scale;

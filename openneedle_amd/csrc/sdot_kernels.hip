@@ -153,20 +153,20 @@ struct SdotWindow {
 // group indices are clamped (phantom groups past the last are never closed).
 template <int KIND, int GROUP>
 __device__ __forceinline__ void sdot_load(SdotWindow<KIND, GROUP> &st, __amdgpu_buffer_rsrc_t codes,
-                                          __amdgpu_buffer_rsrc_t norms, int n_pad, int row, int w, int groups,
-                                          int wpg) {
+                                          __amdgpu_buffer_rsrc_t norms, int w, int groups, int wpg) {
     constexpr int C = SdotWindow<KIND, GROUP>::kChunks;
     constexpr int NN = SdotWindow<KIND, GROUP>::kNorms;
-    const uint32_t code_lane = static_cast<uint32_t>(row) * 16u, norm_lane = static_cast<uint32_t>(row) * 2u;
+    constexpr int CS = kRowsPerBlock * 16, NS = kRowsPerBlock * 2;  // tile strides of a chunk / a group
+    const uint32_t code_lane = threadIdx.x * 16u, norm_lane = threadIdx.x * 2u;
 #pragma unroll
     for (int c = 0; c < C; ++c)
-        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * n_pad * 16, 0);
+        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * CS, 0);
     if constexpr (GROUP > 0) {
 #pragma unroll
         for (int k = 0; k < NN; ++k)
-            st.norms[k] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, min(w * NN + k, groups - 1) * n_pad * 2, 0);
+            st.norms[k] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, min(w * NN + k, groups - 1) * NS, 0);
     } else {
-        st.norms[0] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, min(w / wpg, groups - 1) * n_pad * 2, 0);
+        st.norms[0] = __builtin_amdgcn_raw_buffer_load_b16(norms, norm_lane, min(w / wpg, groups - 1) * NS, 0);
     }
 }
 
@@ -322,15 +322,20 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
         J.block_begin = cj[j].block_begin;
         J.batch = cj[j].batch;
     }
-    const int n_pad = J.n_pad, rows = J.rows;
-    const int row = (blk - J.block_begin) * kRowsPerBlock + threadIdx.x;
+    const int rows = J.rows;
+    const int tile = blk - J.block_begin;
+    const int row = tile * kRowsPerBlock + threadIdx.x;
     const int windows = geom.windows, groups = geom.groups;
     const int wpg = GROUP == 0 ? geom.group / kWindow : 1;
     const int qdw = windows * (kWindow / 4);  // int32 activation words per batch row
     const uint32_t cent[4] = {geom.cent[0], geom.cent[1], geom.cent[2], geom.cent[3]};
     const float cs = geom.centroid_scale;
-    const __amdgpu_buffer_rsrc_t codes = buffer_rsrc(J.codes, static_cast<uint32_t>(geom.chunks) * n_pad * 16u);
-    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms, static_cast<uint32_t>(groups) * n_pad * 2u);
+    // this workgroup's row tile of codes and norms
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms + static_cast<size_t>(tile) * groups * kRowsPerBlock,
+                                                     static_cast<uint32_t>(groups) * kRowsPerBlock * 2u);
 
     for (int b0 = b_begin; b0 < b_end; b0 += BT) {
         const __amdgpu_buffer_rsrc_t q = buffer_rsrc(J.q + static_cast<size_t>(b0) * qdw, static_cast<uint32_t>(BT) * qdw * 4u);
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
         SdotWindow<KIND, GROUP> cur, nxt;
         StageRegs<GROUP, BT> sr;
         stage_load<GROUP, BT>(sr, q, xs, qdw, groups, 0, wpg);
-        sdot_load<KIND, GROUP>(cur, codes, norms, n_pad, row, 0, groups, wpg);
+        sdot_load<KIND, GROUP>(cur, codes, norms, 0, groups, wpg);
         __syncthreads();  // previous tile finished reading stage buffer 0
         stage_store<GROUP, BT>(sr, lq[0], lxs[0]);
         __syncthreads();
@@ -357,14 +362,14 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
         int w = 0;
         for (; w + 1 < windows; w += 2) {
             stage_load<GROUP, BT>(sr, q, xs, qdw, groups, w + 1, wpg);
-            sdot_load<KIND, GROUP>(nxt, codes, norms, n_pad, row, w + 1, groups, wpg);
+            sdot_load<KIND, GROUP>(nxt, codes, norms, w + 1, groups, wpg);
             asm volatile("" ::: "memory");  // keep the next window's loads ahead of this compute
             sdot_compute<KIND, GROUP, BT>(cur, lq[0], lxs[0], cent, cs, value, dot, w, groups, wpg);
             stage_store<GROUP, BT>(sr, lq[1], lxs[1]);
             __syncthreads();
             const int w2 = min(w + 2, windows - 1);
             stage_load<GROUP, BT>(sr, q, xs, qdw, groups, w2, wpg);
-            sdot_load<KIND, GROUP>(cur, codes, norms, n_pad, row, w2, groups, wpg);
+            sdot_load<KIND, GROUP>(cur, codes, norms, w2, groups, wpg);
             asm volatile("" ::: "memory");
             sdot_compute<KIND, GROUP, BT>(nxt, lq[1], lxs[1], cent, cs, value, dot, w + 1, groups, wpg);
             stage_store<GROUP, BT>(sr, lq[0], lxs[0]);  // window w2 (re-staged if it is the last)
