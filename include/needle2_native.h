@@ -115,6 +115,37 @@ int needle2_gpu_event_record(void *event, void *stream);
 float needle2_gpu_event_elapsed(void *start, void *stop); /* ms; waits for stop */
 int needle2_gpu_device_info(char *buf, int len);         /* "name;arch;cus;hbm_bytes;clock_khz" */
 
+/* ---- int8 KV cache and batched decode attention ----------------------------
+ * Replaces the int8 branch of the reference Engine's cache and attention,
+ * which it exposes only through needle2_engine_set_int8_kv and
+ * needle2_engine_kv_storage_bytes (needle2/native.py:418-433):
+ *   allocation      needle2/csrc/engine.cpp:433-449 (reset)
+ *   quantize/store  needle2/csrc/engine.cpp:1005-1021
+ *   attention       needle2/csrc/engine.cpp:898-967 (with 56-74, 137-147, 816-897)
+ * Here one handle holds `seqs` sequences, so one call serves a whole decode
+ * batch. Layout on the device is private; kv_import / kv_export move host
+ * rows in the reference's layout ([slots][kvheads][head_dim] int8 and
+ * [slots][kvheads] fp32 scales). head_dim: 32, 64 or 128; query heads per
+ * kv head: 1, 2, 4 or 8. All return 0 / -1 (message in needle2_gpu_error). */
+void *needle2_gpu_kv_create(int layers, int capacity, int kvheads, int head_dim, int seqs);
+void needle2_gpu_kv_destroy(void *kv);
+size_t needle2_gpu_kv_storage_bytes(void *kv);   /* engine.cpp kv_storage_bytes (int8 cache) */
+/* d_k, d_v: device fp32 [seqs][count][kvheads][head_dim]; token i of
+ * sequence s goes to slot (seq_first_slot ? seq_first_slot[s] : first_slot) + i
+ * (seq_first_slot is a host array). */
+int needle2_gpu_kv_store(void *kv, int layer, const float *d_k, const float *d_v, int count, int first_slot,
+                         const int *seq_first_slot, void *stream);
+/* d_q, d_out: device fp32 [seqs][heads][head_dim]. Sequence s attends slots
+ * d_slots[j] (device, >= length entries; NULL: j) for j < d_lengths[s]
+ * (device; NULL: length), never more than `length`; listed slots outside
+ * [0, capacity) are skipped. splits: slot-range pieces (0: automatic). */
+int needle2_gpu_attention(void *kv, int layer, const float *d_q, float *d_out, int heads, int length,
+                          const int *d_slots, const int *d_lengths, int splits, void *stream);
+int needle2_gpu_kv_import(void *kv, int layer, int seq, const int8_t *k, const int8_t *v, const float *k_scales,
+                          const float *v_scales, int first_slot, int count);
+int needle2_gpu_kv_export(void *kv, int layer, int seq, int8_t *k, int8_t *v, float *k_scales, float *v_scales,
+                          int first_slot, int count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -313,23 +313,6 @@ static bool same_geometry(const Matrix &a, const Matrix &b) {
 
 using namespace nd;
 
-// Runs f, converting exceptions into -1 plus the thread-local message. The
-// message is cleared first so a non-empty needle2_gpu_error() after a call
-// always belongs to that call.
-template <class F>
-static int guarded(F &&f) {
-    set_error("");
-    try {
-        f();
-        return 0;
-    } catch (const std::exception &e) {
-        set_error(e.what());
-    } catch (...) {
-        set_error("unknown error");
-    }
-    return -1;
-}
-
 static void poison(float *y, size_t n) {
     if (!y) return;
     const float nan = std::numeric_limits<float>::quiet_NaN();

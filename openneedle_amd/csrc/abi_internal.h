@@ -10,6 +10,23 @@ void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stri
 
 void launch_copy(const void *src, void *dst, size_t bytes, hipStream_t s);
 
+// Runs f, converting exceptions into -1 plus the thread-local message. The
+// message is cleared first so a non-empty needle2_gpu_error() after a call
+// always belongs to that call.
+template <class F>
+int guarded(F &&f) {
+    set_error("");
+    try {
+        f();
+        return 0;
+    } catch (const std::exception &e) {
+        set_error(e.what());
+    } catch (...) {
+        set_error("unknown error");
+    }
+    return -1;
+}
+
 // A CQ matrix resident in device memory (layout described in common.h).
 struct Matrix {
     int out = 0, in = 0, bits = 0, group = 0, padded = 0, groups = 0, rowbytes = 0;

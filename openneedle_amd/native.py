@@ -7,8 +7,9 @@ selected the same way: ``NEEDLE2_NATIVE_LIBRARY`` if set, otherwise the
 in-tree build next to this file. There is no CPU fallback: without the HIP
 library every call raises.
 
-Additive (device-resident) API: :class:`Device`, :meth:`NativeCQ.linear_device`,
-:class:`Plan`, :class:`KVAttention`.
+Additive (device-resident) API: :class:`DeviceArray`, :class:`Stream`,
+:class:`Event`, :meth:`NativeCQ.linear_device`, :class:`Plan` and
+:class:`KVCache` (int8 KV cache and batched decode attention).
 """
 from __future__ import annotations
 
@@ -86,6 +87,13 @@ def _library():
     _bind(lib, "needle2_gpu_event_record", [_P, _P], _I)
     _bind(lib, "needle2_gpu_event_elapsed", [_P, _P], ct.c_float)
     _bind(lib, "needle2_gpu_device_info", [ct.c_char_p, _I], _I)
+    _bind(lib, "needle2_gpu_kv_create", [_I, _I, _I, _I, _I], _P)
+    _bind(lib, "needle2_gpu_kv_destroy", [_P])
+    _bind(lib, "needle2_gpu_kv_storage_bytes", [_P], ct.c_size_t)
+    _bind(lib, "needle2_gpu_kv_store", [_P, _I, _P, _P, _I, _I, _P, _P], _I)
+    _bind(lib, "needle2_gpu_attention", [_P, _I, _P, _P, _I, _I, _P, _P, _I, _P], _I)
+    _bind(lib, "needle2_gpu_kv_import", [_P, _I, _I, _P, _P, _P, _P, _I, _I], _I)
+    _bind(lib, "needle2_gpu_kv_export", [_P, _I, _I, _P, _P, _P, _P, _I, _I], _I)
     return lib
 
 
@@ -371,4 +379,77 @@ class Plan:
     def __del__(self):
         if getattr(self, "ptr", None):
             self._lib.needle2_gpu_plan_destroy(self.ptr)
+            self.ptr = None
+
+
+class KVCache:
+    """Device int8 KV cache for ``seqs`` sequences plus batched decode attention.
+
+    The arithmetic is the reference Engine's int8 cache (needle2/csrc/engine.cpp:
+    1005-1021 quantize/store, 898-967 compute_attention); the host arrays of
+    :meth:`load` / :meth:`read` use its layout, [slots][kvheads][head_dim] int8
+    and [slots][kvheads] fp32 scales.
+    """
+
+    def __init__(self, layers: int, capacity: int, kvheads: int, head_dim: int, seqs: int = 1):
+        self._lib = _library()
+        self.layers, self.capacity, self.kvheads, self.head_dim, self.seqs = layers, capacity, kvheads, head_dim, seqs
+        self.ptr = self._lib.needle2_gpu_kv_create(layers, capacity, kvheads, head_dim, seqs)
+        if not self.ptr:
+            raise RuntimeError(f"KV cache create failed: {last_error()}")
+
+    def storage_bytes(self) -> int:
+        return int(self._lib.needle2_gpu_kv_storage_bytes(self.ptr))
+
+    def store(self, layer: int, d_k, d_v, count: int, first_slot=0, stream: "Stream | None" = None) -> None:
+        """Quantize ``count`` tokens per sequence from device fp32 [seqs][count][kvheads][head_dim].
+
+        ``first_slot``: one int for every sequence, or a sequence of ``seqs`` ints.
+        """
+        per_seq = None
+        if np.ndim(first_slot):
+            per_seq = np.ascontiguousarray(first_slot, np.int32)
+            if per_seq.shape != (self.seqs,):
+                raise ValueError("first_slot needs one entry per sequence")
+            first = 0
+        else:
+            first = int(first_slot)
+        _check(self._lib.needle2_gpu_kv_store(self.ptr, layer, int(d_k), int(d_v), int(count), first,
+                                              per_seq.ctypes.data if per_seq is not None else None,
+                                              stream.ptr if stream else None), "KV store")
+
+    def attention(self, layer: int, d_q, d_out, heads: int, length: int, d_slots=None, d_lengths=None,
+                  splits: int = 0, stream: "Stream | None" = None) -> None:
+        """One decode step for every sequence: device q/out fp32 [seqs][heads][head_dim]."""
+        _check(self._lib.needle2_gpu_attention(self.ptr, layer, int(d_q), int(d_out), int(heads), int(length),
+                                               int(d_slots) if d_slots else None,
+                                               int(d_lengths) if d_lengths else None, int(splits),
+                                               stream.ptr if stream else None), "attention")
+
+    def load(self, layer: int, seq: int, k, v, ks, vs, first_slot: int = 0) -> None:
+        """Copy host int8 rows and fp32 scales (reference layout) into the cache."""
+        k = np.ascontiguousarray(k, np.int8)
+        v = np.ascontiguousarray(v, np.int8)
+        ks = np.ascontiguousarray(ks, np.float32)
+        vs = np.ascontiguousarray(vs, np.float32)
+        n = k.shape[0]
+        if k.shape != (n, self.kvheads, self.head_dim) or v.shape != k.shape or ks.shape != (n, self.kvheads) \
+                or vs.shape != ks.shape:
+            raise ValueError("KV load: shapes must be [n, kvheads, head_dim] and [n, kvheads]")
+        _check(self._lib.needle2_gpu_kv_import(self.ptr, layer, seq, k.ctypes.data, v.ctypes.data, ks.ctypes.data,
+                                               vs.ctypes.data, int(first_slot), n), "KV import")
+
+    def read(self, layer: int, seq: int, count: int, first_slot: int = 0):
+        """(k int8, v int8, k_scales, v_scales) of ``count`` slots in the reference layout."""
+        k = np.empty((count, self.kvheads, self.head_dim), np.int8)
+        v = np.empty_like(k)
+        ks = np.empty((count, self.kvheads), np.float32)
+        vs = np.empty_like(ks)
+        _check(self._lib.needle2_gpu_kv_export(self.ptr, layer, seq, k.ctypes.data, v.ctypes.data, ks.ctypes.data,
+                                               vs.ctypes.data, int(first_slot), count), "KV export")
+        return k, v, ks, vs
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            self._lib.needle2_gpu_kv_destroy(self.ptr)
             self.ptr = None
