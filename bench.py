@@ -80,6 +80,38 @@ class Stack:
         return total_ms / steps, statistics.mean(gemv_ms), statistics.median(gemv_ms)
 
 
+ATTN_BYTES = 2 * 64 * 2048 * 8 * 64 + 2 * 64 * 2048 * 8 * 4 + 2 * 64 * 8 * 64 * 4  # K, V codes + scales + q, out
+
+
+def bench_attention(steps, warmup, stream, splits=0):
+    """64 sequences x 8 heads (8 kv heads) x head_dim 64, 2048 cached slots: one
+    decode-attention launch per step over a cache filled through the store kernel."""
+    from openneedle_amd.native import DeviceArray, Event, KVCache, synchronize
+    seqs, cap, kvh, hd, heads = 64, 2048, 8, 64, 8
+    rng = np.random.default_rng(5)
+    caches = []
+    for _ in range(2):  # two caches (2 x 143 MB) alternate so no step reads what the last left in cache
+        kv = KVCache(1, cap, kvh, hd, seqs)
+        for c0 in range(0, cap, 512):
+            k = rng.normal(size=(seqs, 512, kvh, hd)).astype(np.float32)
+            d_k, d_v = DeviceArray.from_host(k), DeviceArray.from_host(k[:, ::-1].copy())
+            kv.store(0, d_k.ptr, d_v.ptr, 512, first_slot=c0, stream=stream)
+            stream.synchronize()
+        caches.append(kv)
+    q = DeviceArray.from_host(rng.normal(size=(seqs, heads, hd)).astype(np.float32))
+    out = DeviceArray(seqs * heads * hd * 4)
+    for i in range(warmup):
+        caches[i % 2].attention(0, q.ptr, out.ptr, heads, cap, splits=splits, stream=stream)
+    synchronize()
+    t0, t1 = Event(), Event()
+    t0.record(stream)
+    for i in range(steps):
+        caches[i % 2].attention(0, q.ptr, out.ptr, heads, cap, splits=splits, stream=stream)
+    t1.record(stream)
+    synchronize()
+    return t0.elapsed_ms(t1) / steps
+
+
 def cpu_baseline(budget_s=20.0):
     """The reference's CQ::linear (oracle/_ref) - or the oracle port - on one CQ4 8192x8192 g32 matrix."""
     import oracle
@@ -122,7 +154,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["cq4", "cq2", "int8"], default=None,
+    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn"], default=None,
                     help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one 1 GiB streaming copy kernel (reference for byte counters)")
@@ -146,6 +178,11 @@ def main():
         log("calibration copy: 1 GiB read + 1 GiB written by copy_kernel")
         del a, b
 
+    if args.only == "attn":
+        for splits in (0, 1, 2, 4, 8):
+            ms_a = bench_attention(args.steps, args.warmup, stream, splits)
+            log(f"attention splits={splits}: {ms_a * 1e3:.1f} us ({ATTN_BYTES / (ms_a * 1e-3) / 1e9:.0f} GB/s)")
+        return
     if args.only:
         bits, count, rows, rot = (4, 16, 8192, 3) if args.only == "cq4" else (2, 16, 8192, 3) if args.only == "cq2" \
             else (4, 64, 4096, 2)
@@ -189,6 +226,13 @@ def main():
             log(f"int8 b{batch} step {msb * 1e3:.1f} us; GEMV {gb * 1e3:.1f} us")
             del st
         del packed, norms
+
+        log("attention: 64 seqs x 8 heads x hd 64, 2048 int8 slots")
+        ms_a = bench_attention(args.steps, args.warmup, stream)
+        extra["attn_decode_us"] = round(ms_a * 1e3, 2)
+        extra["attn_gbs"] = round(ATTN_BYTES / (ms_a * 1e-3) / 1e9, 1)
+        extra["attn_frac"] = round(ATTN_BYTES / (ms_a * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+        log(f"attention {ms_a * 1e3:.1f} us ({extra['attn_gbs']} GB/s)")
 
     cpu = None
     if not args.no_cpu:

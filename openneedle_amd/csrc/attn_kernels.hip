@@ -20,25 +20,13 @@
 // contiguous run): codes [layer][seq][kvh][capacity][HD] int8, scales
 // [layer][seq][kvh][capacity] fp32.
 #include "attn.h"
+#include "wave.h"
 
 #include <cmath>
 
 namespace nd {
 
 namespace {
-
-constexpr int kTile = 256;  // cache slots per block iteration (one per thread in the score phase)
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
 
 // One wave per (sequence, token, kv head) row; K and V rows together.
 __global__ __launch_bounds__(256) void kv_store_kernel(KvStoreArgs a) {
@@ -58,8 +46,8 @@ __global__ __launch_bounds__(256) void kv_store_kernel(KvStoreArgs a) {
         mk = fmaxf(mk, fabsf(a.k[src + d]));
         mv = fmaxf(mv, fabsf(a.v[src + d]));
     }
-    mk = wave_max(mk);
-    mv = wave_max(mv);
+    mk = wave_max(mk, lane);
+    mv = wave_max(mv, lane);
     const float sk = mk > 0 ? mk / 127.0f : 1.0f, sv = mv > 0 ? mv / 127.0f : 1.0f;
     const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
     if (lane == 0) {
@@ -79,16 +67,31 @@ __device__ __forceinline__ float i8f(uint32_t w, int c) {
     return static_cast<float>(static_cast<int8_t>((w >> (8 * c)) & 0xffu));
 }
 
-// Block (split, kv head, sequence). HD: head dim; G: query heads per kv head.
-template <int HD, int G>
+// Block (split, kv head, sequence): 4 waves, each an independent
+// online-softmax worker over 64-slot sub-tiles w, w + 4, w + 8, ... of the
+// block's slot range, with the next sub-tile's loads in flight while the
+// current one is computed. No block barrier inside the loop; the 4 waves'
+// (m, l, o) are combined once at the end.
+//   Score phase: lane = slot; the K row is HD/16 16-byte loads; q comes from
+//   scalar loads (uniform); dot by fma over d.
+//   Value phase: a slot row is HD/4 words, VW words per lane, LPR = HD/4/VW
+//   lanes per row, 64/LPR slot lanes, LPR slots per lane per sub-tile.
+// All cache reads are buffer loads over this context's rows: a slot that is
+// not attended (past the range, or outside [0, capacity) in the caller's
+// list) gets an offset past the buffer and reads zero without a memory
+// request, so loads need no branches.
+template <int HD, int G, int VW, bool SLOTS>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
-    constexpr int DW = HD / 4;        // int8x4 words per cache row
-    constexpr int NL = kTile / DW;    // slot lanes in the value phase
-    constexpr int TPT = kTile / NL;   // slots per thread per tile in the value phase (== DW)
-    __shared__ float lq[G][HD];
-    __shared__ float lw[G][kTile];      // p_s * v_scale_s of the tile
-    __shared__ float red[8][G];         // per-wave partial max / sum
-    __shared__ float lred[NL][G][HD];   // value-phase lane partials
+    constexpr int DW = HD / 4;
+    constexpr int LPR = DW / VW;   // lanes per value row
+    constexpr int NLW = 64 / LPR;  // slot lanes per wave
+    constexpr int SPL = LPR;       // slots per lane per sub-tile
+    constexpr int KC = HD / 16;    // 16-byte chunks per K row
+    constexpr uint32_t kOut = 0x80000000u;  // past every buffer (capacity * HD < 2^31)
+    static_assert(DW % VW == 0 && 64 % LPR == 0, "value-phase lane mapping");
+    __shared__ float lw[4][G][64];
+    __shared__ float lred[4][NLW][G][HD];
+    __shared__ float lm[4][G], ll[4][G];
 
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int sp = blockIdx.x, kh = blockIdx.y, seq = blockIdx.z;
@@ -97,115 +100,150 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     len = len < a.length ? len : a.length;
     const int begin = sp * a.slots_per_split;
     const int end = min(begin + a.slots_per_split, len);
+    const uint32_t cap = static_cast<uint32_t>(a.capacity);
 
-    for (int i = t; i < G * HD; i += 256)
-        lq[i / HD][i % HD] = a.q[(static_cast<size_t>(seq) * H + kh * G) * HD + i];
-    const size_t row0 = (static_cast<size_t>(seq) * a.kvheads + kh) * a.capacity;
-    const int8_t *kc = a.k8 + row0 * HD;
-    const int8_t *vc = a.v8 + row0 * HD;
-    const float *ksc = a.ks + row0;
-    const float *vsc = a.vs + row0;
-    __syncthreads();
+    const ND_CONST float *qh = (const ND_CONST float *)(a.q + (static_cast<size_t>(seq) * H + kh * G) * HD);
+    const size_t row0 = (static_cast<size_t>(seq) * a.kvheads + kh) * cap;
+    const auto rk = buffer_rsrc(a.k8 + row0 * HD, cap * HD);
+    const auto rv = buffer_rsrc(a.v8 + row0 * HD, cap * HD);
+    const auto rks = buffer_rsrc(a.ks + row0, cap * 4u);
+    const auto rvs = buffer_rsrc(a.vs + row0, cap * 4u);
+    const auto rsl = buffer_rsrc(a.slots, static_cast<uint32_t>(a.length) * 4u);
+    const int vj = lane % LPR, vr = lane / LPR;  // value phase: word group, slot lane
 
-    float m[G], l[G], acc[G][4];
+    // slot of list position s, or -1 when not attended
+    auto slot_of = [&](int s) -> int {
+        int raw = s;
+        if constexpr (SLOTS) raw = static_cast<int>(__builtin_amdgcn_raw_buffer_load_b32(rsl, s * 4u, 0, 0));
+        return (s < end && static_cast<uint32_t>(raw) < cap) ? raw : -1;
+    };
+
+    struct Tile {
+        u32x4 k[KC];
+        uint32_t v[SPL][VW];
+        float ks, vs;
+        bool valid;
+    };
+    auto load = [&](Tile &T, int st) {
+        const int slot = slot_of(st + lane);
+        T.valid = slot >= 0;
+        const uint32_t kb = slot >= 0 ? static_cast<uint32_t>(slot) * HD : kOut;
+        const uint32_t sb = slot >= 0 ? static_cast<uint32_t>(slot) * 4u : kOut;
+#pragma unroll
+        for (int c = 0; c < KC; ++c) T.k[c] = __builtin_amdgcn_raw_buffer_load_b128(rk, kb, c * 16, 0);
+        T.ks = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, sb, 0, 0));
+        T.vs = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, sb, 0, 0));
+#pragma unroll
+        for (int i = 0; i < SPL; ++i) {
+            const int sv = slot_of(st + vr + i * NLW);
+            const uint32_t vb = sv >= 0 ? static_cast<uint32_t>(sv) * HD + vj * VW * 4u : kOut;
+            if constexpr (VW == 4) {
+                const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rv, vb, 0, 0);
+                T.v[i][0] = w.x;
+                T.v[i][1] = w.y;
+                T.v[i][2] = w.z;
+                T.v[i][3] = w.w;
+            } else {
+#pragma unroll
+                for (int u = 0; u < VW; ++u) T.v[i][u] = __builtin_amdgcn_raw_buffer_load_b32(rv, vb, u * 4, 0);
+            }
+        }
+    };
+
+    float m[G], l[G], acc[G][4 * VW];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
         l[g] = 0.0f;
-        acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4 * VW; ++c) acc[g][c] = 0.0f;
     }
-    const int vj = t % DW, vr = t / DW;  // value phase: word and slot lane
 
-    for (int base = begin; base < end; base += kTile) {
-        // issue the tile's K row (score phase) and V words (value phase) together
-        // a slot outside [0, capacity) in the caller's list is not attended
-        const int s = base + t;
-        const int slot_raw = s < end ? (a.slots ? a.slots[s] : s) : -1;
-        const bool valid = static_cast<unsigned>(slot_raw) < static_cast<unsigned>(a.capacity);
-        const int slot = valid ? slot_raw : 0;
-        u32x4 kr[HD / 16];
-#pragma unroll
-        for (int c = 0; c < HD / 16; ++c)
-            kr[c] = valid ? reinterpret_cast<const u32x4 *>(kc + static_cast<size_t>(slot) * HD)[c] : u32x4{0, 0, 0, 0};
-        const float kscale = valid ? ksc[slot] : 0.0f;
-        const float vscale = valid ? vsc[slot] : 0.0f;
-        uint32_t vw[TPT];
-#pragma unroll
-        for (int i = 0; i < TPT; ++i) {
-            const int sv = base + vr + i * NL;
-            const int slv = sv < end ? (a.slots ? a.slots[sv] : sv) : -1;
-            vw[i] = static_cast<unsigned>(slv) < static_cast<unsigned>(a.capacity)
-                        ? reinterpret_cast<const uint32_t *>(vc + static_cast<size_t>(slv) * HD)[vj]
-                        : 0u;
-        }
-        // scores: the reference's sequential dot, then * k_scale, * 1/sqrt(HD)
-        float sc[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int c = 0; c < HD / 16; ++c) {
-                const uint32_t w4[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) sum += lq[g][c * 16 + j * 4 + b] * i8f(w4[j], b);
-            }
-            float x = sum * kscale;
-            x *= a.scale;
-            sc[g] = valid ? x : -INFINITY;
-        }
-        // tile max -> running max
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float wm = wave_max(sc[g]);
-            if (lane == 0) red[wave][g] = wm;
-        }
-        __syncthreads();
+    auto compute = [&](const Tile &T) {
         float alpha[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            float tm = red[0][g];
+            float dot = 0.0f;
 #pragma unroll
-            for (int w = 1; w < 4; ++w) tm = fmaxf(tm, red[w][g]);
-            const float mn = fmaxf(m[g], tm);
-            alpha[g] = mn == -INFINITY ? 1.0f : expf(m[g] - mn);  // 0 on the first attended tile
+            for (int c = 0; c < KC; ++c) {
+                const uint32_t w4[4] = {T.k[c].x, T.k[c].y, T.k[c].z, T.k[c].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) dot = __builtin_fmaf(qh[g * HD + c * 16 + j * 4 + b], i8f(w4[j], b), dot);
+            }
+            float x = dot * T.ks;
+            x *= a.scale;
+            x = T.valid ? x : -INFINITY;
+            const float mn = fmaxf(m[g], wave_max(x, lane));
+            alpha[g] = mn == -INFINITY ? 1.0f : expf(m[g] - mn);
             m[g] = mn;
-            const float e = valid ? expf(sc[g] - mn) : 0.0f;
+            const float e = T.valid ? expf(x - mn) : 0.0f;
             l[g] = l[g] * alpha[g] + e;
-            lw[g][t] = e * vscale;
+            lw[wave][g][lane] = e * T.vs;
         }
-        __syncthreads();
-        // value phase: acc[g][c] = alpha * acc + sum_i w_i * v_i[4 vj + c]
+        // LDS operations of one wave complete in order; the fences only stop
+        // the compiler from moving the reads above the writes (and the next
+        // sub-tile's writes above these reads).
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc[g][c] *= alpha[g];
+            for (int c = 0; c < 4 * VW; ++c) acc[g][c] *= alpha[g];
 #pragma unroll
-        for (int i = 0; i < TPT; ++i) {
+        for (int i = 0; i < SPL; ++i) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float w = lw[g][vr + i * NL];
+                const float w = lw[wave][g][vr + i * NLW];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) acc[g][c] = __builtin_fmaf(w, i8f(vw[i], c), acc[g][c]);
+                for (int u = 0; u < VW; ++u)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) acc[g][u * 4 + b] = __builtin_fmaf(w, i8f(T.v[i][u], b), acc[g][u * 4 + b]);
             }
         }
-        __syncthreads();  // lw and red are rewritten by the next tile
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    // The next sub-tile is loaded before this one is computed; loads past the
+    // end read zero.
+    Tile cur, nxt;
+    int st = begin + wave * 64;
+    load(cur, st);
+    for (; st < end; st += 256) {
+        load(nxt, st + 256);
+        asm volatile("" ::: "memory");  // keep the prefetch ahead of the compute
+        compute(cur);
+        cur = nxt;
     }
-    // combine: l over all threads, acc over the NL slot lanes
+    // wave partials -> LDS; combine the 4 waves with their own maxima
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const float ws = wave_sum(l[g]);
-        if (lane == 0) red[wave][g] = ws;
+        const float ws = wave_sum(l[g], lane);
+        if (lane == 0) {
+            lm[wave][g] = m[g];
+            ll[wave][g] = ws;
+        }
 #pragma unroll
-        for (int c = 0; c < 4; ++c) lred[vr][g][vj * 4 + c] = acc[g][c];
+        for (int c = 0; c < 4 * VW; ++c) lred[wave][vr][g][vj * 4 * VW + c] = acc[g][c];
     }
     __syncthreads();
     for (int i = t; i < G * HD; i += 256) {
         const int g = i / HD, d = i % HD;
-        float o = 0.0f;
-        for (int r = 0; r < NL; ++r) o += lred[r][g][d];
-        const float lt = red[0][g] + red[1][g] + red[2][g] + red[3][g];
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, lm[w][g]);
+        float o = 0.0f, lt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            if (lm[w][g] == -INFINITY) continue;  // a wave with nothing attended
+            const float f = expf(lm[w][g] - M);
+            float ow = 0.0f;
+            for (int r = 0; r < NLW; ++r) ow += lred[w][r][g][d];
+            o += f * ow;
+            lt += f * ll[w][g];
+        }
         const size_t head = static_cast<size_t>(seq) * H + kh * G + g;
         if (a.splits == 1) {
             a.out[head * HD + d] = lt > 0 ? o * (1.0f / lt) : 0.0f;
@@ -213,7 +251,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
             float *rec = a.part + (head * a.splits + sp) * (HD + 2);
             rec[2 + d] = o;
             if (d == 0) {
-                rec[0] = begin < end ? m[g] : -INFINITY;
+                rec[0] = M;
                 rec[1] = lt;
             }
         }
@@ -240,16 +278,24 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
     }
 }
 
-template <int HD>
+// 16-byte value loads (VW = 4) while the accumulators fit; single words for
+// 4 or 8 query heads per kv head.
+template <int HD, bool SLOTS>
 void launch_attn_hd(const AttnArgs &a, int G, dim3 grid, hipStream_t s) {
     switch (G) {
-    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4>), grid, dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8>), grid, dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((attn_kernel<HD, 1, 4, SLOTS>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<HD, 2, 4, SLOTS>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((attn_kernel<HD, 4, 1, SLOTS>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((attn_kernel<HD, 8, 1, SLOTS>), grid, dim3(256), 0, s, a); break;
     default: ND_CHECK(false, "attention: heads per kv head must be 1, 2, 4 or 8");
     }
     ND_HIP(hipGetLastError());
+}
+
+template <int HD>
+void launch_attn_slots(const AttnArgs &a, int G, dim3 grid, hipStream_t s) {
+    if (a.slots) launch_attn_hd<HD, true>(a, G, grid, s);
+    else launch_attn_hd<HD, false>(a, G, grid, s);
 }
 
 }  // namespace
@@ -270,9 +316,9 @@ void launch_attention(AttnArgs a, int group, hipStream_t s) {
     const int H = a.kvheads * group;
     dim3 grid(a.splits, a.kvheads, a.seqs);
     switch (a.head_dim) {
-    case 32: launch_attn_hd<32>(a, group, grid, s); break;
-    case 64: launch_attn_hd<64>(a, group, grid, s); break;
-    default: launch_attn_hd<128>(a, group, grid, s); break;
+    case 32: launch_attn_slots<32>(a, group, grid, s); break;
+    case 64: launch_attn_slots<64>(a, group, grid, s); break;
+    default: launch_attn_slots<128>(a, group, grid, s); break;
     }
     if (a.splits > 1) {
         hipLaunchKernelGGL(attn_merge_kernel, dim3(a.seqs * H), dim3(128), 0, s, a.part, a.out, a.seqs * H, a.splits,

@@ -8,6 +8,7 @@
 // each code costs one LDS read plus one add, in the reference's own order.
 // All files are compiled with -ffp-contract=off.
 #include "common.h"
+#include "wave.h"
 
 #include <hip/hip_fp16.h>
 
@@ -168,29 +169,6 @@ __device__ __forceinline__ void load_act(__amdgpu_buffer_rsrc_t act, int w, floa
     for (int k = 0; k < kPositionsPerThread; ++k)
         a[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              act, (k * kRowsPerBlock + threadIdx.x) * 4u, w * kWindow * 4, 0));
-}
-
-// Value of the butterfly partner lane t ^ H (H < 64) without LDS round trips:
-// DPP quad permutes (1, 2), row shifts (4, 8) and the gfx950 row swaps (16, 32).
-template <int H>
-__device__ __forceinline__ float butterfly_partner(float v, int t) {
-    const int iv = __builtin_bit_cast(int, v);
-    if constexpr (H == 1) {
-        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
-    } else if constexpr (H == 2) {
-        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
-    } else if constexpr (H == 4 || H == 8) {
-        const float up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x100 + H, 0xF, 0xF, false));
-        const float down = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x110 + H, 0xF, 0xF, false));
-        return (t & H) ? down : up;  // row_shl:H reads lane t+H, row_shr:H reads lane t-H
-    } else if constexpr (H == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
-        return __builtin_bit_cast(float, (t & 16) ? r[0] : r[1]);
-    } else {
-        static_assert(H == 32, "butterfly stride");
-        const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
-        return __builtin_bit_cast(float, (t & 32) ? r[0] : r[1]);
-    }
 }
 
 template <int GROUP, int H>

@@ -41,13 +41,15 @@ static void check_layer(const KvHandle &kv, int layer) {
     ND_CHECK(layer >= 0 && layer < kv.layers, "KV cache: layer out of range");
 }
 
-// Splits of the slot range: enough (sequence, kv head, split) blocks to give
-// every CU several, never a split shorter than one 256-slot tile.
+// Splits of the slot range: enough (sequence, kv head, split) blocks for two
+// per CU, never a split shorter than one 256-slot tile. With that many
+// (sequence, kv head) pairs already (a large decode batch) there is one split
+// and no merge pass.
 static int auto_splits(int pairs, int length) {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const int tiles = (length + 255) / 256;
-    const int want = (4 * cus + pairs - 1) / pairs;
+    const int want = (2 * cus + pairs - 1) / pairs;
     return std::max(1, std::min(want, tiles));
 }
 
@@ -66,6 +68,7 @@ void *needle2_gpu_kv_create(int layers, int capacity, int kvheads, int head_dim,
     if (guarded([&] {
             ND_CHECK(layers > 0 && capacity > 0 && kvheads > 0 && seqs > 0, "KV cache: sizes must be positive");
             ND_CHECK(head_dim == 32 || head_dim == 64 || head_dim == 128, "KV cache: head_dim must be 32, 64 or 128");
+            ND_CHECK(size_t(capacity) * head_dim < (size_t(1) << 31), "KV cache: capacity * head_dim must be < 2^31");
             auto h = std::make_unique<KvHandle>();
             h->layers = layers;
             h->capacity = capacity;

@@ -1,0 +1,49 @@
+// Wave-level exchange helpers for gfx950 (64-lane wavefronts).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace nd {
+
+// Value of the butterfly partner lane t ^ H (H < 64) without LDS round trips:
+// DPP quad permutes (1, 2), row shifts (4, 8) and the gfx950 row swaps (16, 32).
+template <int H>
+__device__ __forceinline__ float butterfly_partner(float v, int t) {
+    const int iv = __builtin_bit_cast(int, v);
+    if constexpr (H == 1) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+    } else if constexpr (H == 2) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+    } else if constexpr (H == 4 || H == 8) {
+        const float up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x100 + H, 0xF, 0xF, false));
+        const float down = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, iv, 0x110 + H, 0xF, 0xF, false));
+        return (t & H) ? down : up;  // row_shl:H reads lane t+H, row_shr:H reads lane t-H
+    } else if constexpr (H == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+        return __builtin_bit_cast(float, (t & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(H == 32, "butterfly stride");
+        const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+        return __builtin_bit_cast(float, (t & 32) ? r[0] : r[1]);
+    }
+}
+
+// Max / sum over the 64 lanes, result in every lane (xor butterflies).
+__device__ __forceinline__ float wave_max(float v, int t) {
+    v = fmaxf(v, butterfly_partner<1>(v, t));
+    v = fmaxf(v, butterfly_partner<2>(v, t));
+    v = fmaxf(v, butterfly_partner<4>(v, t));
+    v = fmaxf(v, butterfly_partner<8>(v, t));
+    v = fmaxf(v, butterfly_partner<16>(v, t));
+    return fmaxf(v, butterfly_partner<32>(v, t));
+}
+__device__ __forceinline__ float wave_sum(float v, int t) {
+    v += butterfly_partner<1>(v, t);
+    v += butterfly_partner<2>(v, t);
+    v += butterfly_partner<4>(v, t);
+    v += butterfly_partner<8>(v, t);
+    v += butterfly_partner<16>(v, t);
+    return v + butterfly_partner<32>(v, t);
+}
+
+}  // namespace nd
