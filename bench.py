@@ -112,6 +112,31 @@ def bench_attention(steps, warmup, stream, splits=0):
     return t0.elapsed_ms(t1) / steps
 
 
+PREFILL_FLOP = 2 * 512 * 8192 * 2048
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(steps, warmup, stream):
+    """512 tokens x K 2048 through CQ4 8192 x 2048 g32 on fp16 MFMA: (step ms, GEMM-kernel ms)."""
+    from openneedle_amd.native import DeviceArray, Event, NativeCQ, synchronize
+    rng = np.random.default_rng(17)
+    packed, norms, cb = random_cq(rng, 1, 8192, 2048, 4, 32)
+    q = NativeCQ(packed[0], norms[0], (8192, 2048), 4, 32, cb)
+    x = DeviceArray.from_host(rng.normal(size=(512, 2048)).astype(np.float32))
+    y = DeviceArray(512 * 8192 * 4)
+    for _ in range(warmup):
+        q.gemm_device(x.ptr, y.ptr, 512, stream)
+    synchronize()
+    ev = [(Event(), Event()) for _ in range(steps)]
+    t0, t1 = Event(), Event()
+    t0.record(stream)
+    for i in range(steps):
+        q.gemm_device(x.ptr, y.ptr, 512, stream, events=ev[i])
+    t1.record(stream)
+    synchronize()
+    return t0.elapsed_ms(t1) / steps, statistics.mean(a.elapsed_ms(b) for a, b in ev)
+
+
 def cpu_baseline(budget_s=20.0):
     """The reference's CQ::linear (oracle/_ref) - or the oracle port - on one CQ4 8192x8192 g32 matrix."""
     import oracle
@@ -154,7 +179,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn"], default=None,
+    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill"], default=None,
                     help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one 1 GiB streaming copy kernel (reference for byte counters)")
@@ -178,6 +203,11 @@ def main():
         log("calibration copy: 1 GiB read + 1 GiB written by copy_kernel")
         del a, b
 
+    if args.only == "prefill":
+        ms_p, g_p = bench_prefill(args.steps, args.warmup, stream)
+        log(f"prefill: step {ms_p * 1e3:.1f} us, GEMM {g_p * 1e3:.1f} us "
+            f"({PREFILL_FLOP / (g_p * 1e-3) / 1e12:.0f} TFLOP/s)")
+        return
     if args.only == "attn":
         for splits in (0, 1, 2, 4, 8):
             ms_a = bench_attention(args.steps, args.warmup, stream, splits)
@@ -233,6 +263,14 @@ def main():
         extra["attn_gbs"] = round(ATTN_BYTES / (ms_a * 1e-3) / 1e9, 1)
         extra["attn_frac"] = round(ATTN_BYTES / (ms_a * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         log(f"attention {ms_a * 1e3:.1f} us ({extra['attn_gbs']} GB/s)")
+
+        log("prefill GEMM: 512 x 2048 through CQ4 8192 x 2048 g32 (fp16 MFMA)")
+        ms_p, g_p = bench_prefill(args.steps, args.warmup, stream)
+        extra["prefill_step_us"] = round(ms_p * 1e3, 2)
+        extra["prefill_gemm_us"] = round(g_p * 1e3, 2)
+        extra["prefill_tflops"] = round(PREFILL_FLOP / (g_p * 1e-3) / 1e12, 1)
+        extra["prefill_mfma_util"] = round(extra["prefill_tflops"] / MFMA_FP16_PEAK_TFLOPS, 4)
+        log(f"prefill GEMM {g_p * 1e3:.1f} us ({extra['prefill_tflops']} TFLOP/s), step {ms_p * 1e3:.1f} us")
 
     cpu = None
     if not args.no_cpu:

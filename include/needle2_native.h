@@ -84,6 +84,17 @@ void *needle2_gpu_sdot_create(const uint8_t *packed, const uint16_t *norms, int 
 int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream);
 int needle2_gpu_sdot_linear_device(void *sdot_handle, const float *d_x, float *d_y, int batch, void *stream);
 
+/* Prefill GEMM (replaces the per-token-pair CQ loops of Engine::linear_batch /
+ * attention_projections_batch, needle2/csrc/engine.cpp:607-750, for prompt
+ * chunks): d_y[m][out] = FWHT-domain product of d_x[m][in] (device fp32) on
+ * fp16 MFMA with fp32 accumulation; activations and cb*norm weights are
+ * rounded to fp16 (agreement with needle2_cq_linear about 1e-3 normwise).
+ * 4-bit codes (CQ4, CQ3) only. The _timed form records two events around
+ * the GEMM kernel. */
+int needle2_gpu_cq_gemm_device(void *cq_handle, const float *d_x, float *d_y, int m, void *stream);
+int needle2_gpu_cq_gemm_timed(void *cq_handle, const float *d_x, float *d_y, int m, void *stream, void *gemm_start,
+                              void *gemm_stop);
+
 /* Plans: `count` handles of one geometry (in, bits, group, codebook), matrix
  * i reading d_x[i] ([batch][in]) and writing d_y[i] ([batch][out_i]); one
  * GEMV launch covers all of them. */

@@ -125,6 +125,19 @@ void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s
     launch_cq_gemv(m.geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, s);
 }
 
+void CqHandle::gemm_device(const float *d_x, float *d_y, int m_rows, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+    if (m_rows <= 0) return;
+    ND_CHECK(m.kind == kNib, "prefill GEMM: 4-bit (CQ4 / CQ3) codes only");
+    ND_CHECK(size_t(m_rows) * m.dev * 2 < (size_t(1) << 31), "prefill GEMM: m * padded input must be < 2^30");
+    st.xh.reserve(size_t(m_rows) * m.dev);
+    launch_prefill_transform(d_x, m_rows, m.in, m.padded, m.dev, m.group, m.scale, st.xh.p, s);
+    uint16_t cbh[16];
+    for (int i = 0; i < 16; ++i) cbh[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(m.lut[i]));
+    if (ev0) ND_HIP(hipEventRecord(ev0, s));
+    launch_prefill_gemm(m.geom(), m.codes.p, m.norms.p, m.out, st.xh.p, m_rows, m.dev, m.padded, cbh, d_y, s);
+    if (ev1) ND_HIP(hipEventRecord(ev1, s));
+}
+
 void CqHandle::linear_host(const float *x, float *y, int batch) {
     if (batch <= 0) return;
     const size_t nx = size_t(batch) * m.in, ny = size_t(batch) * m.out;
@@ -406,6 +419,29 @@ void *needle2_gpu_sdot_create(const uint8_t *p, const uint16_t *n, int out, int 
 int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {
     auto *h = static_cast<CqHandle *>(handle);
     return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream); });
+}
+
+// Prefill GEMM: d_y[m][out] = d_x[m][in] through the matrix on fp16 MFMA
+// (fp32 accumulation); the batched form of needle2_cq_linear used for prompt
+// chunks (engine.cpp:607-670). 4-bit codes (CQ4, CQ3).
+int needle2_gpu_cq_gemm_device(void *handle, const float *d_x, float *d_y, int m, void *stream) {
+    return guarded([&] {
+        ND_CHECK(handle, "null CQ handle");
+        auto *h = static_cast<CqHandle *>(handle);
+        h->gemm_device(d_x, d_y, m, stream ? static_cast<hipStream_t>(stream) : h->st.stream, nullptr, nullptr);
+    });
+}
+
+// As needle2_gpu_cq_gemm_device, with two events recorded around the GEMM
+// kernel (after the activation transform).
+int needle2_gpu_cq_gemm_timed(void *handle, const float *d_x, float *d_y, int m, void *stream, void *gemm_start,
+                              void *gemm_stop) {
+    return guarded([&] {
+        ND_CHECK(handle, "null CQ handle");
+        auto *h = static_cast<CqHandle *>(handle);
+        h->gemm_device(d_x, d_y, m, stream ? static_cast<hipStream_t>(stream) : h->st.stream,
+                       static_cast<hipEvent_t>(gemm_start), static_cast<hipEvent_t>(gemm_stop));
+    });
 }
 
 int needle2_gpu_sdot_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {

@@ -10,6 +10,11 @@ void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stri
 
 void launch_copy(const void *src, void *dst, size_t bytes, hipStream_t s);
 
+void launch_prefill_transform(const float *x, int m, int in, int padded, int dev, int group, float scale,
+                              _Float16 *xh, hipStream_t s);
+void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes, const uint16_t *norms, int rows, const _Float16 *xh,
+                         int m, int dev, int padded, const uint16_t *cb_half, float *y, hipStream_t s);
+
 // Runs f, converting exceptions into -1 plus the thread-local message. The
 // message is cleared first so a non-empty needle2_gpu_error() after a call
 // always belongs to that call.
@@ -49,6 +54,7 @@ struct Staging {
     hipStream_t stream = nullptr;
     DevBuf<float> x, rot, y, big, xs;
     DevBuf<int32_t> q;
+    DevBuf<_Float16> xh;  // fp16 transformed activations of the prefill GEMM
     HostBuf<float> hx, hy;
     Staging();
     ~Staging();
@@ -62,6 +68,8 @@ struct CqHandle {
     void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
     void linear_host(const float *x, float *y, int batch);
     void rows_host(const int64_t *ids, float *y, int count);
+    // prefill GEMM on fp16 MFMA; events (nullable) bracket the GEMM kernel
+    void gemm_device(const float *d_x, float *d_y, int m, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
 };
 
 struct SdotHandle {
