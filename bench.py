@@ -33,6 +33,14 @@ METRIC = "CQ4/CQ2 GEMV effective HBM GB/s (% of peak); decode tokens/s at batch 
 HBM_PEAK_GBS = 8000.0
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary (profiles/traffic.json), or None."""
+    try:
+        return json.load(open(ROOT / "profiles" / "traffic.json"))["kernels"][kernel]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -181,6 +189,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill"], default=None,
                     help="run a single workload (for profiling); prints no JSON line")
+    ap.add_argument("--sweep", action="store_true", help="with --only attn: also time fixed split counts")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one 1 GiB streaming copy kernel (reference for byte counters)")
     args = ap.parse_args()
@@ -209,7 +218,7 @@ def main():
             f"({PREFILL_FLOP / (g_p * 1e-3) / 1e12:.0f} TFLOP/s)")
         return
     if args.only == "attn":
-        for splits in (0, 1, 2, 4, 8):
+        for splits in ((0, 1, 2, 4, 8) if args.sweep else (0,)):
             ms_a = bench_attention(args.steps, args.warmup, stream, splits)
             log(f"attention splits={splits}: {ms_a * 1e3:.1f} us ({ATTN_BYTES / (ms_a * 1e-3) / 1e9:.0f} GB/s)")
         return
@@ -295,9 +304,9 @@ def main():
                    "matrices": 16, "rows": 8192, "cols": 8192, "batch": 1, "weight_rotations": 3,
                    "bytes_per_step": nbytes, "device": info["name"], "cus": info["cus"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "cq_gemv_kernel<kNib,false,32>", "gemv_mean_us": round(gemv_mean * 1e3, 2),
-                     "gemv_median_us": round(gemv_med * 1e3, 2)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic("cq_gemv_kernel<0, 32>"),
+                     "kernel": "cq_gemv_kernel<0, 32>", "gemv_mean_us": round(gemv_mean * 1e3, 2),
+                     "gemv_median_us": round(gemv_med * 1e3, 2), "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu,
         "extra": extra,
     }
