@@ -145,6 +145,54 @@ def bench_prefill(steps, warmup, stream):
     return t0.elapsed_ms(t1) / steps, statistics.mean(a.elapsed_ms(b) for a, b in ev)
 
 
+def bench_decode_layer(steps, warmup, stream):
+    """One decoder layer for 64 sequences at context 2048 (hidden 512, 8 heads = 8 kv heads, head_dim 64,
+    MLP 2048): int8-path CQ4 g32 projections Q|K|V (one plan), KV store of the new token, decode
+    attention over 2048 int8 slots, O, MLP up and down. Elementwise glue (norms, RoPE, gates,
+    activation) is omitted. Returns ms per layer step."""
+    from openneedle_amd.native import DeviceArray, Event, KVCache, NativeCQ, Plan, synchronize
+    seqs, cap, kvh, hd, heads, hidden, mlp = 64, 2048, 8, 64, 8, 512, 2048
+    rng = np.random.default_rng(23)
+
+    def mat(rows, cols):
+        packed, norms, cb = random_cq(rng, 1, rows, cols, 4, 32)
+        return NativeCQ(packed[0], norms[0], (rows, cols), 4, 32, cb)
+
+    wq, wk, wv, wo = (mat(hidden, hidden) for _ in range(4))
+    wu, wd = mat(mlp, hidden), mat(hidden, mlp)
+    buf = {n: DeviceArray(seqs * w * 4) for n, w in
+           (("x", hidden), ("q", hidden), ("k", hidden), ("v", hidden), ("a", hidden), ("o", hidden),
+            ("u", mlp), ("d", hidden))}
+    buf["x"].upload(rng.normal(size=(seqs, hidden)).astype(np.float32))
+    p = lambda ms, xs, ys: Plan(ms, [buf[n].ptr for n in xs], [buf[n].ptr for n in ys], batch=seqs, int8=True)  # noqa: E731
+    plans = [p([wq, wk, wv], "xxx", "qkv"), None, None, p([wo], "a", "o"), p([wu], "o", "u"), p([wd], "u", "d")]
+    kv = KVCache(1, cap, kvh, hd, seqs)
+    for c0 in range(0, cap - 1, 512):
+        n = min(512, cap - 1 - c0)
+        k = DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32))
+        v = DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32))
+        kv.store(0, k.ptr, v.ptr, n, first_slot=c0, stream=stream)
+        stream.synchronize()
+
+    def step():
+        plans[0].run(stream)
+        kv.store(0, buf["k"].ptr, buf["v"].ptr, 1, first_slot=cap - 1, stream=stream)
+        kv.attention(0, buf["q"].ptr, buf["a"].ptr, heads, cap, stream=stream)
+        for pl in plans[3:]:
+            pl.run(stream)
+
+    for _ in range(warmup):
+        step()
+    synchronize()
+    t0, t1 = Event(), Event()
+    t0.record(stream)
+    for _ in range(steps):
+        step()
+    t1.record(stream)
+    synchronize()
+    return t0.elapsed_ms(t1) / steps
+
+
 def cpu_baseline(budget_s=20.0):
     """The reference's CQ::linear (oracle/_ref) - or the oracle port - on one CQ4 8192x8192 g32 matrix."""
     import oracle
@@ -187,7 +235,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill"], default=None,
+    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode"], default=None,
                     help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--sweep", action="store_true", help="with --only attn: also time fixed split counts")
     ap.add_argument("--calibrate", action="store_true",
@@ -212,6 +260,10 @@ def main():
         log("calibration copy: 1 GiB read + 1 GiB written by copy_kernel")
         del a, b
 
+    if args.only == "decode":
+        ms_d = bench_decode_layer(args.steps, args.warmup, stream)
+        log(f"decode layer (64 seqs, ctx 2048): {ms_d * 1e3:.1f} us -> {64 / (ms_d * 1e-3):.0f} tokens/s per layer")
+        return
     if args.only == "prefill":
         ms_p, g_p = bench_prefill(args.steps, args.warmup, stream)
         log(f"prefill: step {ms_p * 1e3:.1f} us, GEMM {g_p * 1e3:.1f} us "
@@ -280,6 +332,13 @@ def main():
         extra["prefill_tflops"] = round(PREFILL_FLOP / (g_p * 1e-3) / 1e12, 1)
         extra["prefill_mfma_util"] = round(extra["prefill_tflops"] / MFMA_FP16_PEAK_TFLOPS, 4)
         log(f"prefill GEMM {g_p * 1e3:.1f} us ({extra['prefill_tflops']} TFLOP/s), step {ms_p * 1e3:.1f} us")
+
+        log("decode layer: 64 sequences, ctx 2048, int8-path CQ4 projections + int8-KV attention")
+        ms_d = bench_decode_layer(args.steps, args.warmup, stream)
+        extra["decode_layer_us"] = round(ms_d * 1e3, 2)
+        extra["decode_tokens_per_s_per_layer"] = round(64 / (ms_d * 1e-3), 0)
+        extra["decode_tokens_per_s_27_layers"] = round(64 / (27 * ms_d * 1e-3), 0)
+        log(f"decode layer {ms_d * 1e3:.1f} us -> {extra['decode_tokens_per_s_per_layer']:.0f} tokens/s per layer")
 
     cpu = None
     if not args.no_cpu:

@@ -337,7 +337,8 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
     const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms + static_cast<size_t>(tile) * groups * kRowsPerBlock,
                                                      static_cast<uint32_t>(groups) * kRowsPerBlock * 2u);
 
-    for (int b0 = b_begin; b0 < b_end; b0 += BT) {
+    // one batch tile per blockIdx.y (b_end bounds the tiles this launch covers)
+    for (int b0 = b_begin + static_cast<int>(blockIdx.y) * BT; b0 < b_end; b0 += BT * static_cast<int>(gridDim.y)) {
         const __amdgpu_buffer_rsrc_t q = buffer_rsrc(J.q + static_cast<size_t>(b0) * qdw, static_cast<uint32_t>(BT) * qdw * 4u);
         const __amdgpu_buffer_rsrc_t xs = buffer_rsrc(J.xs + static_cast<size_t>(b0) * groups, static_cast<uint32_t>(BT) * groups * 4u);
         SdotWindow<KIND, GROUP> cur, nxt;
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
 template <int KIND, int BT>
 void launch_sdot_bt(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int b0,
                     int b1, hipStream_t s) {
-    dim3 grid(blocks), block(kRowsPerBlock);
+    dim3 grid(blocks, (b1 - b0) / BT), block(kRowsPerBlock);
     switch (g.group > kWindow ? 0 : g.group) {
     case 8:
         if constexpr (KIND == kNib) {
@@ -404,17 +405,30 @@ void launch_sdot_bt(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs,
     ND_HIP(hipGetLastError());
 }
 
-// The batch is covered by tiles of 16, 8, 4, 2 and 1 rows (largest first).
+int device_cus() {
+    static int cus = [] {
+        int dev = 0, n = 256;
+        if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        return n;
+    }();
+    return cus;
+}
+
+// The batch is covered by tiles of 16, 8, 4, 2 and 1 rows (largest first),
+// one tile per blockIdx.y. A tile size that would leave fewer than two
+// workgroups per CU is skipped: small matrices with many batch rows (a
+// decode batch) trade decode reuse for parallelism.
 template <int KIND>
 void launch_sdot_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
                       hipStream_t s) {
     int b = 0;
+    const int want = 2 * device_cus();
     auto run = [&](int bt, auto launcher) {
         const int n = (batch - b) / bt * bt;
-        if (n > 0) {
-            launcher(b, b + n);
-            b += n;
-        }
+        if (n <= 0) return;
+        if (bt > 1 && static_cast<long>(blocks) * (n / bt) < want) return;
+        launcher(b, b + n);
+        b += n;
     };
     run(16, [&](int b0, int b1) { launch_sdot_bt<KIND, 16>(g, job0, jobs, njobs, blocks, b0, b1, s); });
     run(8, [&](int b0, int b1) { launch_sdot_bt<KIND, 8>(g, job0, jobs, njobs, blocks, b0, b1, s); });
