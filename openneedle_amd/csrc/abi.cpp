@@ -118,7 +118,10 @@ void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s
     const float *act = d_x;
     if (!gemv_fuses_fwht(m.group)) {
         st.rot.reserve(size_t(batch) * m.dev);
-        m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
+        if (gemv_prepass(m.group))
+            launch_rot_many(d_x, nullptr, batch, batch, m.in, m.dev, m.group, m.scale, st.rot.p, s);
+        else
+            m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
         act = st.rot.p;
     }
     const CqJob job{m.codes.p, m.norms.p, act, d_y, m.out, m.n_pad, 0, batch};
@@ -264,6 +267,8 @@ static void plan_upload(Plan &p) {
             block += mi.n_pad / kRowsPerBlock;
         }
         host.assign(reinterpret_cast<uint8_t *>(jobs.data()), reinterpret_cast<uint8_t *>(jobs.data() + p.count));
+        p.xptr.reserve(p.count);
+        ND_HIP(hipMemcpy(p.xptr.p, p.xs_in.data(), p.count * sizeof(const float *), hipMemcpyHostToDevice));
     } else {
         p.rot.reserve(size_t(p.count) * p.batch * m.dev);
         p.q.reserve(size_t(p.count) * p.batch * m.dev / 4);
@@ -296,7 +301,9 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
     // x_i is [batch][in] on the device; the FP32 GEMV transforms it in-kernel
     // unless the group exceeds one table window
     if (!p.sdot) {
-        if (!gemv_fuses_fwht(m.group))
+        if (gemv_prepass(m.group))
+            launch_rot_many(nullptr, p.xptr.p, p.batch, p.count * p.batch, m.in, m.dev, m.group, m.scale, p.rot.p, s);
+        else if (!gemv_fuses_fwht(m.group))
             for (int i = 0; i < p.count; ++i)
                 m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));

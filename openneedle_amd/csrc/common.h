@@ -145,9 +145,11 @@ __host__ __device__ inline size_t norm_index(int r, int g, int groups) {
     return (static_cast<size_t>(r / kRowsPerBlock) * groups + g) * kRowsPerBlock + r % kRowsPerBlock;
 }
 
-// Groups up to one table window run the activation FWHT inside the GEMV
-// kernel; larger groups use a separate transform pass.
-inline bool gemv_fuses_fwht(int group) { return group <= kWindow; }
+// Groups of 128 and 256 run the activation FWHT inside the FP32 GEMV kernel.
+// Groups up to 64 take a batched pre-pass (launch_rot_many) ahead of the
+// quarter-split GEMV; groups above one window use the generic transform pass.
+inline bool gemv_fuses_fwht(int group) { return group > 64 && group <= kWindow; }
+inline bool gemv_prepass(int group) { return group <= 64; }
 
 struct CqJob {
     const uint4 *codes;       // [n_pad / kRowsPerBlock][chunks][kRowsPerBlock]
@@ -189,6 +191,11 @@ void launch_norms_transpose(const uint16_t *norms, int rows, int groups, uint16_
 // rot[v][0..dev) = FWHT per group of zero-padded x[v][0..in), for nvec vectors.
 void launch_transform(const float *x, int x_stride, float *rot, int rot_stride, int nvec, int in,
                       int padded, int dev_positions, int group, float scale, hipStream_t s);
+
+// rot[v][0..dev) = per-group FWHT of zero-padded x for nvec vectors (groups
+// of 8 .. 64): vector v is row v % batch of x0 (xptr null) or of xptr[v / batch].
+void launch_rot_many(const float *x0, const float *const *xptr, int batch, int nvec, int in, int dev, int group,
+                     float scale, float *rot, hipStream_t s);
 
 // njobs == 0: one job passed by value (job0); otherwise jobs_dev[0..njobs).
 void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs_dev, int njobs, int total_blocks,

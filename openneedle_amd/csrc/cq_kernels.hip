@@ -491,15 +491,619 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void cq_gemv_kernel(CqJob job0, c
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split-window FP32 GEMV (groups of 8 .. 128 positions)
+//
+// Two threads per output row: a workgroup of 512 threads covers a 256-row
+// tile, and its two halves (waves 0-3 and 4-7) take the lower and upper half
+// of every window's groups against one shared product table. Per-group
+// results p_g = gd_g * half(norm_g) are independent, so each half computes
+// its own groups with the reference's sequential code order; the lower half
+// owns the row sum and adds the upper half's p_g (handed over through LDS,
+// double-buffered by window parity) right after its own, so the row sum still
+// runs over g = 0, 1, 2, ... exactly as cq.cpp:157-164 does: bit-identical.
+// This doubles the waves in flight (4 per SIMD) and halves the code registers
+// each lane holds in its prefetch.
+//
+// Code extraction: the table entry of a 4-bit code is code*4 bytes into its
+// slot (code*8 for a 2-bit pair). With the code dword rotated left by 2 (3),
+// every even nibble sits at bits 2-5 (3-6) of a byte, and rotated right by 2
+// (1), every odd one does; one SDWA `and` with a byte select then yields a
+// slot offset, so a code costs one VALU op, one LDS read and one add.
+// ---------------------------------------------------------------------------
+constexpr int kSplitThreads = 2 * kRowsPerBlock;
+
+template <int KIND, int GROUP>
+struct SplitShape {
+    static constexpr int kChunks = TableShape<KIND>::kChunksPerWindow / 2;  // chunks per half window
+    static constexpr int kDwords = kChunks * 4;
+    static constexpr int kSlotsPerHalf = TableShape<KIND>::kSlots / 2;
+    static constexpr int kGroupsPerHalf = kWindow / GROUP / 2;
+    static_assert(GROUP >= 8 && GROUP <= kWindow / 2, "split GEMV takes groups of at most half a window");
+};
+
+template <int KIND, int GROUP>
+struct HalfState {
+    u32x4 codes[SplitShape<KIND, GROUP>::kChunks];
+    uint16_t norms[SplitShape<KIND, GROUP>::kGroupsPerHalf];
+};
+
+// (x byte BYTE) & mask, one SDWA op; mask lives in an SGPR.
+template <int BYTE>
+__device__ __forceinline__ uint32_t and_byte(uint32_t mask, uint32_t x) {
+    uint32_t r;
+    if constexpr (BYTE == 0)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+            : "=v"(r) : "s"(mask), "v"(x));
+    else if constexpr (BYTE == 1)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+            : "=v"(r) : "s"(mask), "v"(x));
+    else if constexpr (BYTE == 2)
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+            : "=v"(r) : "s"(mask), "v"(x));
+    else
+        asm("v_and_b32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+            : "=v"(r) : "s"(mask), "v"(x));
+    return r;
+}
+
+// Byte offsets of the 8 table entries addressed by one code dword, in code
+// order: off[2m] from nibble 2m, off[2m+1] from nibble 2m+1.
+template <int KIND>
+__device__ __forceinline__ void slot_offsets_sdwa(uint32_t wd, uint32_t mask, uint32_t off[8]) {
+    constexpr int kRot = KIND == kNib ? 2 : 3;                      // log2(entry bytes)
+    const uint32_t X = __builtin_amdgcn_alignbit(wd, wd, 32 - kRot);  // rotate left: even nibbles
+    const uint32_t Y = __builtin_amdgcn_alignbit(wd, wd, 4 - kRot);   // rotate right: odd nibbles
+    off[0] = and_byte<0>(mask, X);
+    off[1] = and_byte<0>(mask, Y);
+    off[2] = and_byte<1>(mask, X);
+    off[3] = and_byte<1>(mask, Y);
+    off[4] = and_byte<2>(mask, X);
+    off[5] = and_byte<2>(mask, Y);
+    off[6] = and_byte<3>(mask, X);
+    off[7] = and_byte<3>(mask, Y);
+}
+
+// Byte offset of window w's activations (wave-uniform, kept scalar).
+__device__ __forceinline__ int window_offset(int w) { return __builtin_amdgcn_readfirstlane(w * kWindow * 4); }
+
+// Loads of this thread's half of window w: code chunk c (of the half's
+// kChunks) and the norm of the half's group k. Both buffer resources end at
+// the tile's last window / group, so windows past the end read zero without
+// touching memory (the rolling prefetch below runs two windows ahead
+// unconditionally; phantom groups never reach the row sum).
+template <int KIND, int GROUP>
+__device__ __forceinline__ u32x4 load_chunk(__amdgpu_buffer_rsrc_t codes, int w, int half, int r, int c) {
+    using H = SplitShape<KIND, GROUP>;
+    constexpr int C = TableShape<KIND>::kChunksPerWindow;
+    const int soff = __builtin_amdgcn_readfirstlane((w * C + half * H::kChunks + c) * kRowsPerBlock * 16);
+    return __builtin_amdgcn_raw_buffer_load_b128(codes, r * 16u, soff, 0);
+}
+
+template <int KIND, int GROUP>
+__device__ __forceinline__ uint16_t load_norm(__amdgpu_buffer_rsrc_t norms, int w, int half, int r, int k) {
+    using H = SplitShape<KIND, GROUP>;
+    const int g = w * (2 * H::kGroupsPerHalf) + half * H::kGroupsPerHalf + k;
+    return __builtin_amdgcn_raw_buffer_load_b16(norms, r * 2u, __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2),
+                                                0);
+}
+
+template <int KIND, int GROUP>
+__device__ __forceinline__ void load_half(HalfState<KIND, GROUP> &st, __amdgpu_buffer_rsrc_t codes,
+                                          __amdgpu_buffer_rsrc_t norms, int w, int half, int r) {
+    using H = SplitShape<KIND, GROUP>;
+#pragma unroll
+    for (int c = 0; c < H::kChunks; ++c) st.codes[c] = load_chunk<KIND, GROUP>(codes, w, half, r, c);
+#pragma unroll
+    for (int k = 0; k < H::kGroupsPerHalf; ++k) st.norms[k] = load_norm<KIND, GROUP>(norms, w, half, r, k);
+}
+
+// One half window in the reference's order. HALF 0 adds each closed group
+// into the row sum; HALF 1 parks p_g in P[k][r] for the lower half.
+template <int KIND, int GROUP, int HALF>
+__device__ __forceinline__ void compute_half(HalfState<KIND, GROUP> &st, const float *T, float *P, int r,
+                                             uint32_t mask, float &sum, float &gd, int w, int groups,
+                                             __amdgpu_buffer_rsrc_t codes, __amdgpu_buffer_rsrc_t norms) {
+    using S = TableShape<KIND>;
+    using H = SplitShape<KIND, GROUP>;
+    constexpr int D = H::kDwords;
+    constexpr int P_AHEAD = ND_PIPE;
+    const int gbase = w * (2 * H::kGroupsPerHalf) + HALF * H::kGroupsPerHalf;  // first group of this half
+    SlotValues<KIND> v[P_AHEAD + 1];
+#pragma unroll
+    for (int dn = 0; dn < P_AHEAD && dn < D; ++dn) {
+        const u32x4 &cn = st.codes[dn >> 2];
+        const uint32_t wn = (dn & 3) == 0 ? cn.x : (dn & 3) == 1 ? cn.y : (dn & 3) == 2 ? cn.z : cn.w;
+        uint32_t off[8];
+        slot_offsets_sdwa<KIND>(wn, mask, off);
+        read_slots<KIND>(T, HALF * H::kSlotsPerHalf + dn * 8, off, v[dn % (P_AHEAD + 1)]);
+        if ((dn & 3) == 3) st.codes[dn >> 2] = load_chunk<KIND, GROUP>(codes, w + 2, HALF, r, dn >> 2);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (d + P_AHEAD < D) {
+            const int dn = d + P_AHEAD;
+            const u32x4 &cn = st.codes[dn >> 2];
+            const uint32_t wn = (dn & 3) == 0 ? cn.x : (dn & 3) == 1 ? cn.y : (dn & 3) == 2 ? cn.z : cn.w;
+            uint32_t off[8];
+            slot_offsets_sdwa<KIND>(wn, mask, off);
+            read_slots<KIND>(T, HALF * H::kSlotsPerHalf + dn * 8, off, v[dn % (P_AHEAD + 1)]);
+            // chunk dn / 4 is spent: refill it with the same chunk two windows ahead
+            if ((dn & 3) == 3) st.codes[dn >> 2] = load_chunk<KIND, GROUP>(codes, w + 2, HALF, r, dn >> 2);
+        }
+        asm volatile("" ::: "memory");
+        if (ND_SCHED_BARRIER) __builtin_amdgcn_sched_barrier(0);
+        const SlotValues<KIND> &cur = v[d % (P_AHEAD + 1)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            gd += cur.a[i];
+            if constexpr (KIND == kCrumb) gd += cur.b[i];
+            const int pos_end = (d * 8 + i + 1) * S::kPositionsPerSlot;  // positions consumed in this half
+            if (pos_end % GROUP == 0) {
+                const int k = pos_end / GROUP - 1;
+                const float p = gd * h2f(st.norms[k]);
+                if constexpr (HALF == 0) {
+                    if (gbase + k < groups) sum += p;
+                } else {
+                    P[k * kRowsPerBlock + r] = p;
+                }
+                gd = 0.0f;
+                st.norms[k] = load_norm<KIND, GROUP>(norms, w + 2, HALF, r, k);
+            }
+        }
+        asm volatile("" : "+v"(gd), "+v"(sum));
+        if (ND_SCHED_BARRIER) __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Lower half: add the upper half's p_g of window w (parked in P) in group order.
+template <int KIND, int GROUP>
+__device__ __forceinline__ void add_upper(const float *P, int r, float &sum, int w, int groups) {
+    using H = SplitShape<KIND, GROUP>;
+    const int gbase = w * (2 * H::kGroupsPerHalf) + H::kGroupsPerHalf;
+#pragma unroll
+    for (int k = 0; k < H::kGroupsPerHalf; ++k)
+        if (gbase + k < groups) sum += P[k * kRowsPerBlock + r];
+}
+
+// Table build for the split kernel: thread (half, r) owns window position r
+// and writes half of that position's entries (4-bit: codes 8*half .. +7;
+// 2-bit: pair entries with high code 2*half, 2*half+1).
+template <int KIND>
+__device__ __forceinline__ void build_table_half(float *__restrict__ T, const float *lut, float x, int half, int r) {
+    using S = TableShape<KIND>;
+    if constexpr (KIND == kNib) {
+        float *dst = T + r * S::kSlotFloats + half * 8;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) dst[c] = lut[half * 8 + c] * x;
+    } else {
+        const int lane = r & 63;
+        const int l = lane & 31;
+        const float r0 = __shfl(x, 2 * l);
+        const float r1 = __shfl(x, 2 * l + 1);
+        if (lane < 32) {
+            float p0[4], p1[2];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) p0[c] = lut[c] * r0;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) p1[c] = lut[half * 2 + c] * r1;
+            const int slot = (r & ~63) / 2 + l;
+            float4 *dst = reinterpret_cast<float4 *>(T + slot * S::kSlotFloats);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int hi = half * 2 + c;
+                dst[2 * hi] = make_float4(p0[0], p1[c], p0[1], p1[c]);
+                dst[2 * hi + 1] = make_float4(p0[2], p1[c], p0[3], p1[c]);
+            }
+        }
+    }
+}
+
+// All batch rows of one row tile for one half of the split kernel.
+template <int KIND, int GROUP, int HALF>
+__device__ __forceinline__ void split_rows(const CqJob &J, const CqGeom &geom, float (*T)[TableShape<KIND>::kFloats],
+                                           float (*P)[SplitShape<KIND, GROUP>::kGroupsPerHalf * kRowsPerBlock],
+                                           float *stage, int blk) {
+    const int r = threadIdx.x % kRowsPerBlock;
+    const int rows = J.rows, batch = J.batch;
+    const int tile = blk - J.block_begin;
+    const int row = tile * kRowsPerBlock + r;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms =
+        buffer_rsrc(J.norms + static_cast<size_t>(tile) * geom.groups * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.groups) * kRowsPerBlock * 2u);
+    const int windows = geom.windows, groups = geom.groups, in = geom.in;
+    const float scale = geom.scale;
+    const uint32_t mask = KIND == kNib ? 0x3Cu : 0x78u;
+    float lut[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lut[i] = geom.lut[i];
+
+    for (int b = 0; b < batch; ++b) {
+        const __amdgpu_buffer_rsrc_t act =
+            buffer_rsrc(J.act + static_cast<size_t>(b) * in, static_cast<uint32_t>(in) * 4u);
+        HalfState<KIND, GROUP> cur, nxt;
+        float xa[1];
+        xa[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(act, r * 4u, 0, 0));
+        load_half<KIND, GROUP>(cur, codes, norms, 0, HALF, r);
+        load_half<KIND, GROUP>(nxt, codes, norms, 1, HALF, r);
+        __syncthreads();  // the previous batch row finished with T[0] and P
+        window_fwht<GROUP>(xa, scale, stage);
+        build_table_half<KIND>(T[0], lut, xa[0], HALF, r);
+        xa[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(act, r * 4u, kWindow * 4, 0));
+        __syncthreads();
+        float sum = 0.0f, gd = 0.0f;
+        // Whole window pairs, then the last window if the count is odd; one
+        // barrier per window and no condition around any load, so every
+        // iteration issues the same loads in the same order. Window w is
+        // summed from `cur` (even) or `nxt` (odd), whose chunks are refilled
+        // with window w + 2 as they are spent: loads stream continuously two
+        // windows ahead. The activations of window w + 1 (loaded one window
+        // earlier) then become its table (a window past the end reads zeros
+        // into a buffer nobody reads again) and those of window w + 2 are
+        // requested. Before its own groups of window w the lower half adds the
+        // upper half's groups of window w - 1 (P[(w - 1) & 1]).
+        const int pairs = windows / 2;
+        for (int it = 0; it < pairs; ++it) {
+            const int w = 2 * it;
+            if (HALF == 0 && it > 0) add_upper<KIND, GROUP>(P[1], r, sum, w - 1, groups);
+            compute_half<KIND, GROUP, HALF>(cur, T[0], P[0], r, mask, sum, gd, w, groups, codes, norms);
+            window_fwht<GROUP>(xa, scale, stage);
+            build_table_half<KIND>(T[1], lut, xa[0], HALF, r);
+            xa[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(act, r * 4u, window_offset(w + 2), 0));
+            __syncthreads();
+            if (HALF == 0) add_upper<KIND, GROUP>(P[0], r, sum, w, groups);
+            compute_half<KIND, GROUP, HALF>(nxt, T[1], P[1], r, mask, sum, gd, w + 1, groups, codes, norms);
+            window_fwht<GROUP>(xa, scale, stage);
+            build_table_half<KIND>(T[0], lut, xa[0], HALF, r);
+            xa[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(act, r * 4u, window_offset(w + 3), 0));
+            __syncthreads();
+        }
+        if (windows & 1) {
+            const int w = windows - 1;
+            if (HALF == 0 && w > 0) add_upper<KIND, GROUP>(P[1], r, sum, w - 1, groups);
+            compute_half<KIND, GROUP, HALF>(cur, T[0], P[0], r, mask, sum, gd, w, groups, codes, norms);
+            __syncthreads();
+        }
+        if (HALF == 0) {
+            add_upper<KIND, GROUP>(P[(windows - 1) & 1], r, sum, windows - 1, groups);
+            if (row < rows) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b) * rows + row] = sum;
+        }
+    }
+}
+
+template <int KIND, int GROUP>
+__global__ __launch_bounds__(kSplitThreads, 4) void cq_gemv_split_kernel(CqJob job0, const CqJob *__restrict__ jobs,
+                                                                       int njobs, CqGeom geom) {
+    using S = TableShape<KIND>;
+    using H = SplitShape<KIND, GROUP>;
+    __shared__ __attribute__((aligned(16))) float T[2][S::kFloats];
+    __shared__ float P[2][H::kGroupsPerHalf * kRowsPerBlock];
+    __shared__ float stage[GROUP > 64 ? 2 * kWindow : 1];
+    static_assert(kPositionsPerThread == 1, "split GEMV assumes one window position per row thread");
+
+    const int blk = blockIdx.x;
+    CqJob J = job0;
+    if (njobs > 0) {
+        const ND_CONST CqJob *cj = (const ND_CONST CqJob *)(jobs);
+        int j = 0;
+        for (int k = 1; k < njobs; ++k)
+            if (cj[k].block_begin <= blk) j = k;
+        J.codes = cj[j].codes;
+        J.norms = cj[j].norms;
+        J.act = cj[j].act;
+        J.y = cj[j].y;
+        J.rows = cj[j].rows;
+        J.n_pad = cj[j].n_pad;
+        J.block_begin = cj[j].block_begin;
+        J.batch = cj[j].batch;
+    }
+    // The half is a compile-time constant of each copy of the window loop, so
+    // each copy is straight-line code whose load/wait bookkeeping does not mix
+    // with the other half's.
+    if (__builtin_amdgcn_readfirstlane(threadIdx.x / kRowsPerBlock) == 0)
+        split_rows<KIND, GROUP, 0>(J, geom, T, P, stage, blk);
+    else
+        split_rows<KIND, GROUP, 1>(J, geom, T, P, stage, blk);
+}
+
+// ---------------------------------------------------------------------------
+// Quarter-split FP32 GEMV (groups of 8 .. 64 positions)
+//
+// Four threads per output row: a 1024-thread workgroup covers a 256-row tile
+// and its quarters (waves 0-3, 4-7, 8-11, 12-15) take positions
+// [64q, 64q + 64) of every 256-position window against one shared product
+// table. As in the split kernel, each quarter computes its own groups in the
+// reference's code order, quarters 1-3 park their p_g in LDS and quarter 0
+// adds them right after its own, in group order: bit-identical to
+// cq.cpp:157-164. With 64 codes per thread per window the registers fit 64
+// VGPRs, so two workgroups give 8 waves per SIMD, which the LDS lookups need
+// to run near the LDS read rate.
+//
+// The activations arrive already transformed (rot = per-group FWHT of x,
+// zero past the padded length; one pre-pass launch for all inputs), so a
+// thread's per-window table work is one activation load, four products and
+// one 16-byte LDS store: slot p holds cb[c] * rot[p] for the 16 codes c at a
+// 20-float stride (conflict-free for both the 16-byte stores and the
+// per-code 4-byte reads); 2-bit slots hold (cb[c0] * rot[2s], cb[c1] * rot[2s+1])
+// pairs at a 36-float stride.
+// ---------------------------------------------------------------------------
+constexpr int kQuads = 4;
+constexpr int kQuadThreads = kQuads * kRowsPerBlock;
+
+template <int KIND, int GROUP>
+struct QuadShape {
+    static constexpr int kPositions = kWindow / kQuads;                          // per quarter window
+    static constexpr int kChunks = kPositions / TableShape<KIND>::kCodesPerChunk;  // 2 (4-bit) or 1 (2-bit)
+    static constexpr int kDwords = kChunks * 4;
+    static constexpr int kSlots = kPositions / TableShape<KIND>::kPositionsPerSlot;
+    static constexpr int kGroups = kPositions / GROUP;                           // groups per quarter window
+    static constexpr int kSlotFloats = KIND == kNib ? 20 : 36;
+    static constexpr int kFloats = (kWindow / TableShape<KIND>::kPositionsPerSlot) * kSlotFloats;
+    static constexpr int kPipe = KIND == kNib && GROUP >= 32 ? 2 : 1;             // code dwords read ahead
+    static_assert(GROUP >= 8 && GROUP <= kPositions, "quarter GEMV takes groups of at most 64 positions");
+};
+
+template <int KIND, int GROUP>
+struct QuadState {
+    u32x4 codes[QuadShape<KIND, GROUP>::kChunks];
+    uint16_t norms[QuadShape<KIND, GROUP>::kGroups];
+};
+
+template <int KIND, int GROUP>
+__device__ __forceinline__ u32x4 quad_chunk(__amdgpu_buffer_rsrc_t codes, int w, int q, int r, int c) {
+    constexpr int C = TableShape<KIND>::kChunksPerWindow;
+    const int soff =
+        __builtin_amdgcn_readfirstlane((w * C + q * QuadShape<KIND, GROUP>::kChunks + c) * kRowsPerBlock * 16);
+    return __builtin_amdgcn_raw_buffer_load_b128(codes, r * 16u, soff, 0);
+}
+
+template <int KIND, int GROUP>
+__device__ __forceinline__ uint16_t quad_norm(__amdgpu_buffer_rsrc_t norms, int w, int q, int r, int k) {
+    constexpr int NQ = QuadShape<KIND, GROUP>::kGroups;
+    const int g = w * (kQuads * NQ) + q * NQ + k;
+    return __builtin_amdgcn_raw_buffer_load_b16(norms, r * 2u, __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2),
+                                                0);
+}
+
+template <int KIND, int GROUP>
+__device__ __forceinline__ void quad_load(QuadState<KIND, GROUP> &st, __amdgpu_buffer_rsrc_t codes,
+                                          __amdgpu_buffer_rsrc_t norms, int w, int q, int r) {
+    using Q = QuadShape<KIND, GROUP>;
+#pragma unroll
+    for (int c = 0; c < Q::kChunks; ++c) st.codes[c] = quad_chunk<KIND, GROUP>(codes, w, q, r, c);
+#pragma unroll
+    for (int k = 0; k < Q::kGroups; ++k) st.norms[k] = quad_norm<KIND, GROUP>(norms, w, q, r, k);
+}
+
+// Transformed activations this thread turns into table entries: position r
+// (4-bit) or positions 2(r/2), 2(r/2)+1 (2-bit) of window w; past the end: 0.
+template <int KIND>
+__device__ __forceinline__ float2 quad_act(__amdgpu_buffer_rsrc_t rot, int w, int r) {
+    if constexpr (KIND == kNib) {
+        return make_float2(
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rot, r * 4u, window_offset(w), 0)), 0.0f);
+    } else {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rot, (r >> 1) * 8u, window_offset(w), 0);
+        return __builtin_bit_cast(float2, v);
+    }
+}
+
+// Quarter q's share of the table of one window: 4-bit slot r, codes 4q..4q+3;
+// 2-bit slot r/2, pair entries c0 | q << 2 for c0 = 2(r&1), 2(r&1)+1.
+template <int KIND, int GROUP>
+__device__ __forceinline__ void quad_build(float *__restrict__ T, const float *lut, float2 x, int q, int r) {
+    using Q = QuadShape<KIND, GROUP>;
+    if constexpr (KIND == kNib) {
+        *reinterpret_cast<float4 *>(T + r * Q::kSlotFloats + 4 * q) =
+            make_float4(lut[4 * q] * x.x, lut[4 * q + 1] * x.x, lut[4 * q + 2] * x.x, lut[4 * q + 3] * x.x);
+    } else {
+        const int part = r & 1;
+        const float hi = lut[q] * x.y;
+        *reinterpret_cast<float4 *>(T + (r >> 1) * Q::kSlotFloats + 8 * q + 4 * part) =
+            make_float4(lut[2 * part] * x.x, hi, lut[2 * part + 1] * x.x, hi);
+    }
+}
+
+// One quarter window in the reference's order, refilling each spent chunk /
+// norm with window w + 2. Quarter 0 adds closed groups into the row sum;
+// quarters 1-3 park p_g in P[q - 1][k][r].
+template <int KIND, int GROUP, int QUAD>
+__device__ __forceinline__ void quad_compute(QuadState<KIND, GROUP> &st, const float *T, float *P, int r,
+                                             uint32_t mask, float &sum, float &gd, int w, int groups,
+                                             __amdgpu_buffer_rsrc_t codes, __amdgpu_buffer_rsrc_t norms) {
+    using S = TableShape<KIND>;
+    using Q = QuadShape<KIND, GROUP>;
+    constexpr int D = Q::kDwords;
+    constexpr int PA = Q::kPipe;
+    const int gbase = w * (kQuads * Q::kGroups);  // quarter 0's first group
+    SlotValues<KIND> v[PA + 1];
+    auto issue = [&](int dn) {
+        const u32x4 &cn = st.codes[dn >> 2];
+        const uint32_t wn = (dn & 3) == 0 ? cn.x : (dn & 3) == 1 ? cn.y : (dn & 3) == 2 ? cn.z : cn.w;
+        uint32_t off[8];
+        slot_offsets_sdwa<KIND>(wn, mask, off);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const char *slot = reinterpret_cast<const char *>(T + (QUAD * Q::kSlots + dn * 8 + i) * Q::kSlotFloats);
+            if constexpr (KIND == kNib) {
+                v[dn % (PA + 1)].a[i] = *reinterpret_cast<const float *>(slot + off[i]);
+            } else {
+                const float2 pr = *reinterpret_cast<const float2 *>(slot + off[i]);
+                v[dn % (PA + 1)].a[i] = pr.x;
+                v[dn % (PA + 1)].b[i] = pr.y;
+            }
+        }
+        if ((dn & 3) == 3) st.codes[dn >> 2] = quad_chunk<KIND, GROUP>(codes, w + 2, QUAD, r, dn >> 2);
+    };
+#pragma unroll
+    for (int dn = 0; dn < PA && dn < D; ++dn) issue(dn);
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (d + PA < D) issue(d + PA);
+        asm volatile("" ::: "memory");
+        if (ND_SCHED_BARRIER) __builtin_amdgcn_sched_barrier(0);
+        const SlotValues<KIND> &cur = v[d % (PA + 1)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            gd += cur.a[i];
+            if constexpr (KIND == kCrumb) gd += cur.b[i];
+            const int pos_end = (d * 8 + i + 1) * S::kPositionsPerSlot;  // positions consumed in this quarter
+            if (pos_end % GROUP == 0) {
+                const int k = pos_end / GROUP - 1;
+                const float p = gd * h2f(st.norms[k]);
+                if constexpr (QUAD == 0) {
+                    if (gbase + k < groups) sum += p;
+                } else {
+                    P[((QUAD - 1) * Q::kGroups + k) * kRowsPerBlock + r] = p;
+                }
+                gd = 0.0f;
+                st.norms[k] = quad_norm<KIND, GROUP>(norms, w + 2, QUAD, r, k);
+            }
+        }
+        asm volatile("" : "+v"(gd), "+v"(sum));
+        if (ND_SCHED_BARRIER) __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Quarter 0: add quarters 1-3's p_g of window w (parked in P) in group order.
+template <int KIND, int GROUP>
+__device__ __forceinline__ void quad_add_parked(const float *P, int r, float &sum, int w, int groups) {
+    using Q = QuadShape<KIND, GROUP>;
+    const int gbase = w * (kQuads * Q::kGroups) + Q::kGroups;
+#pragma unroll
+    for (int k = 0; k < (kQuads - 1) * Q::kGroups; ++k)
+        if (gbase + k < groups) sum += P[k * kRowsPerBlock + r];
+}
+
+template <int KIND, int GROUP, int QUAD>
+__device__ __forceinline__ void quad_rows(const CqJob &J, const CqGeom &geom, float (*T)[QuadShape<KIND, GROUP>::kFloats],
+                                          float (*P)[(kQuads - 1) * QuadShape<KIND, GROUP>::kGroups * kRowsPerBlock],
+                                          int blk) {
+    const int r = threadIdx.x % kRowsPerBlock;
+    const int rows = J.rows, batch = J.batch;
+    const int tile = blk - J.block_begin;
+    const int row = tile * kRowsPerBlock + r;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms =
+        buffer_rsrc(J.norms + static_cast<size_t>(tile) * geom.groups * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.groups) * kRowsPerBlock * 2u);
+    const int windows = geom.windows, groups = geom.groups;
+    const int dev = windows * kWindow;
+    const uint32_t mask = KIND == kNib ? 0x3Cu : 0x78u;
+    float lut[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lut[i] = geom.lut[i];
+
+    for (int b = 0; b < batch; ++b) {
+        const __amdgpu_buffer_rsrc_t rot =
+            buffer_rsrc(J.act + static_cast<size_t>(b) * dev, static_cast<uint32_t>(dev) * 4u);
+        QuadState<KIND, GROUP> cur, nxt;
+        float2 xr = quad_act<KIND>(rot, 0, r);
+        quad_load<KIND, GROUP>(cur, codes, norms, 0, QUAD, r);
+        quad_load<KIND, GROUP>(nxt, codes, norms, 1, QUAD, r);
+        __syncthreads();  // the previous batch row finished with T[0] and P
+        quad_build<KIND, GROUP>(T[0], lut, xr, QUAD, r);
+        xr = quad_act<KIND>(rot, 1, r);
+        __syncthreads();
+        float sum = 0.0f, gd = 0.0f;
+        // Whole window pairs, then the last window if the count is odd; one
+        // barrier per window and no condition around any load. Window w is
+        // summed from `cur` (even) or `nxt` (odd), whose chunks are refilled
+        // with window w + 2 as they are spent; the activations of window
+        // w + 1 (loaded one window earlier) then become its table (past the
+        // end: zeros, into a buffer nobody reads) and those of window w + 2
+        // are requested. Before its own groups of window w quarter 0 adds the
+        // other quarters' groups of window w - 1 (P[(w - 1) & 1]).
+        const int pairs = windows / 2;
+        for (int it = 0; it < pairs; ++it) {
+            const int w = 2 * it;
+            if (QUAD == 0 && it > 0) quad_add_parked<KIND, GROUP>(P[1], r, sum, w - 1, groups);
+            quad_compute<KIND, GROUP, QUAD>(cur, T[0], P[0], r, mask, sum, gd, w, groups, codes, norms);
+            quad_build<KIND, GROUP>(T[1], lut, xr, QUAD, r);
+            xr = quad_act<KIND>(rot, w + 2, r);
+            __syncthreads();
+            if (QUAD == 0) quad_add_parked<KIND, GROUP>(P[0], r, sum, w, groups);
+            quad_compute<KIND, GROUP, QUAD>(nxt, T[1], P[1], r, mask, sum, gd, w + 1, groups, codes, norms);
+            quad_build<KIND, GROUP>(T[0], lut, xr, QUAD, r);
+            xr = quad_act<KIND>(rot, w + 3, r);
+            __syncthreads();
+        }
+        if (windows & 1) {
+            const int w = windows - 1;
+            if (QUAD == 0 && w > 0) quad_add_parked<KIND, GROUP>(P[1], r, sum, w - 1, groups);
+            quad_compute<KIND, GROUP, QUAD>(cur, T[0], P[0], r, mask, sum, gd, w, groups, codes, norms);
+            __syncthreads();
+        }
+        if (QUAD == 0) {
+            quad_add_parked<KIND, GROUP>(P[(windows - 1) & 1], r, sum, windows - 1, groups);
+            if (row < rows) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b) * rows + row] = sum;
+        }
+    }
+}
+
+template <int KIND, int GROUP>
+__global__ __launch_bounds__(kQuadThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void cq_gemv_quad_kernel(
+    CqJob job0, const CqJob *__restrict__ jobs, int njobs, CqGeom geom) {
+    using Q = QuadShape<KIND, GROUP>;
+    __shared__ __attribute__((aligned(16))) float T[2][Q::kFloats];
+    __shared__ float P[2][(kQuads - 1) * Q::kGroups * kRowsPerBlock];
+    const int blk = blockIdx.x;
+    CqJob J = job0;
+    if (njobs > 0) {
+        const ND_CONST CqJob *cj = (const ND_CONST CqJob *)(jobs);
+        int j = 0;
+        for (int k = 1; k < njobs; ++k)
+            if (cj[k].block_begin <= blk) j = k;
+        J.codes = cj[j].codes;
+        J.norms = cj[j].norms;
+        J.act = cj[j].act;
+        J.y = cj[j].y;
+        J.rows = cj[j].rows;
+        J.n_pad = cj[j].n_pad;
+        J.block_begin = cj[j].block_begin;
+        J.batch = cj[j].batch;
+    }
+    // one straight-line copy of the window loop per quarter (compile-time
+    // table offsets; no mixing of the quarters' load bookkeeping)
+    switch (__builtin_amdgcn_readfirstlane(threadIdx.x / kRowsPerBlock)) {
+    case 0: quad_rows<KIND, GROUP, 0>(J, geom, T, P, blk); break;
+    case 1: quad_rows<KIND, GROUP, 1>(J, geom, T, P, blk); break;
+    case 2: quad_rows<KIND, GROUP, 2>(J, geom, T, P, blk); break;
+    default: quad_rows<KIND, GROUP, 3>(J, geom, T, P, blk); break;
+    }
+}
+
+// Activation pre-pass of the quarter GEMV: rot[v][0..dev) = per-group FWHT
+// of zero-padded x (the reference's transform, cq.cpp:153-156, identical
+// butterflies), for nvec = count * batch vectors at once: vector v is row
+// v % batch of x0 (xptr null) or of xptr[v / batch] (a device table).
+template <int GROUP>
+__global__ __launch_bounds__(kRowsPerBlock) void rot_many_kernel(const float *__restrict__ x0,
+                                                                 const float *const *__restrict__ xptr, int batch,
+                                                                 int in, int dev, float scale, float *__restrict__ rot) {
+    static_assert(GROUP <= 64, "in-wave FWHT");
+    const int v = blockIdx.y;
+    const int p = blockIdx.x * kRowsPerBlock + threadIdx.x;
+    const float *xv = (xptr ? xptr[v / batch] : x0) + static_cast<size_t>(v % batch) * in;
+    float x[1] = {p < in ? xv[p] : 0.0f};
+    window_fwht<GROUP>(x, scale, nullptr);
+    if (p < dev) rot[static_cast<size_t>(v) * dev + p] = x[0];
+}
+
 template <int KIND>
 void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
-    dim3 grid(blocks), block(kRowsPerBlock);
+    dim3 grid(blocks), block(kRowsPerBlock), split(kSplitThreads), quad(kQuadThreads);
     switch (g.group > kWindow ? 0 : g.group) {
-    case 8: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 8>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 16: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 16>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 32: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 64>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 128>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 8: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 8>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+    case 16: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 16>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+    case 32: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 32>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 64>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((cq_gemv_split_kernel<KIND, 128>), grid, split, 0, s, job0, jobs, njobs, g); break;
     case 256: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
     default: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 0>), grid, block, 0, s, job0, jobs, njobs, g); break;
     }
@@ -598,6 +1202,20 @@ void launch_transform(const float *x, int x_stride, float *rot, int rot_stride, 
 void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stride, int nvec, int in, int padded,
                           int out_limit, int group, float scale, float *scratch, hipStream_t s) {
     transform_impl(x, x_stride, rot, rot_stride, nvec, in, padded, out_limit, group, scale, s, scratch);
+}
+
+void launch_rot_many(const float *x0, const float *const *xptr, int batch, int nvec, int in, int dev, int group,
+                     float scale, float *rot, hipStream_t s) {
+    if (nvec <= 0) return;
+    dim3 grid(dev / kRowsPerBlock, nvec), block(kRowsPerBlock);
+    switch (group) {
+    case 8: hipLaunchKernelGGL(rot_many_kernel<8>, grid, block, 0, s, x0, xptr, batch, in, dev, scale, rot); break;
+    case 16: hipLaunchKernelGGL(rot_many_kernel<16>, grid, block, 0, s, x0, xptr, batch, in, dev, scale, rot); break;
+    case 32: hipLaunchKernelGGL(rot_many_kernel<32>, grid, block, 0, s, x0, xptr, batch, in, dev, scale, rot); break;
+    case 64: hipLaunchKernelGGL(rot_many_kernel<64>, grid, block, 0, s, x0, xptr, batch, in, dev, scale, rot); break;
+    default: throw Error("internal: activation pre-pass takes groups of 8 .. 64");
+    }
+    ND_HIP(hipGetLastError());
 }
 
 void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
