@@ -28,6 +28,9 @@ COMMON = [
     "-fno-gpu-flush-denormals-to-zero", "-Wall", "-Wno-unused-function",
 ]
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Per-source extras: the int8 MFMA kernel keeps its accumulators in VGPRs
+# (no accumulator-register reads in the per-group epilogue).
+EXTRA = {"sdot_kernels": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:
@@ -43,7 +46,8 @@ def sources():
 
 def _compile(src: Path, build_dir: Path = BUILD, defines=()) -> Path:
     obj = build_dir / (src.stem + ".o")
-    cmd = [hipcc(), *COMMON, *DEVICE, *[f"-D{d}" for d in defines], "-I", str(CSRC), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON, *DEVICE, *EXTRA.get(src.stem, []), *[f"-D{d}" for d in defines], "-I", str(CSRC), "-c",
+           str(src), "-o", str(obj)]
     if src.suffix == ".hip":
         cmd[1:1] = ["-x", "hip"]
     res = subprocess.run(cmd, capture_output=True, text=True)

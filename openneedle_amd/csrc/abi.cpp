@@ -200,8 +200,9 @@ SdotGeom SdotHandle::geom() const {
     return g;
 }
 
-void SdotHandle::prepare_device(const float *d_x, int batch, int32_t *q, float *xs, hipStream_t s) {
-    if (launch_sdot_prepare(d_x, nullptr, batch, batch, m.in, m.padded, m.dev, m.group, m.scale, m.kind, q, xs, s))
+void SdotHandle::prepare_device(const float *d_x, int batch, int32_t *q, float *xs, float *xst, hipStream_t s) {
+    if (launch_sdot_prepare(d_x, nullptr, batch, batch, m.in, m.padded, m.dev, m.group, m.scale, m.kind, q, xs, xst,
+                            s))
         return;
     st.rot.reserve(size_t(batch) * m.dev);
     m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
@@ -212,8 +213,9 @@ void SdotHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t
     if (batch <= 0) return;
     st.q.reserve(size_t(batch) * m.dev / 4);
     st.xs.reserve(size_t(batch) * m.groups);
-    prepare_device(d_x, batch, st.q.p, st.xs.p, s);
-    const SdotJob job{m.codes.p, m.norms.p, st.q.p, st.xs.p, d_y, m.out, m.n_pad, 0, batch};
+    st.xst.reserve(size_t(batch) * m.groups);
+    prepare_device(d_x, batch, st.q.p, st.xs.p, st.xst.p, s);
+    const SdotJob job{m.codes.p, m.norms.p, st.q.p, st.xs.p, d_y, m.out, m.n_pad, 0, batch, st.xst.p};
     launch_sdot_gemv(geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, batch, s);
 }
 
@@ -244,7 +246,7 @@ struct Plan {
     std::vector<float *> ys;
     DevBuf<float> rot;
     DevBuf<int32_t> q;
-    DevBuf<float> xscale;
+    DevBuf<float> xscale, xscale_t;
     DevBuf<const float *> xptr;  // device table of the count input pointers (int8 prepare)
     DevBuf<uint8_t> jobs;
     int blocks = 0;
@@ -273,6 +275,7 @@ static void plan_upload(Plan &p) {
         p.rot.reserve(size_t(p.count) * p.batch * m.dev);
         p.q.reserve(size_t(p.count) * p.batch * m.dev / 4);
         p.xscale.reserve(size_t(p.count) * p.batch * m.groups);
+        p.xscale_t.reserve(size_t(p.count) * p.batch * m.groups);
         std::vector<SdotJob> jobs(p.count);
         for (int i = 0; i < p.count; ++i) {
             const Matrix &mi = p.sd[i]->m;
@@ -284,7 +287,8 @@ static void plan_upload(Plan &p) {
                               mi.out,
                               mi.n_pad,
                               block,
-                              p.batch};
+                              p.batch,
+                              p.xscale_t.p + size_t(i) * p.batch * m.groups};
             block += mi.n_pad / kRowsPerBlock;
         }
         host.assign(reinterpret_cast<uint8_t *>(jobs.data()), reinterpret_cast<uint8_t *>(jobs.data() + p.count));
@@ -312,7 +316,7 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
         const SdotHandle &h0 = *p.sd[0];
         // one launch prepares every (matrix, batch row) input
         if (!launch_sdot_prepare(nullptr, p.xptr.p, p.batch, p.count * p.batch, m.in, m.padded, m.dev, m.group,
-                                 m.scale, m.kind, p.q.p, p.xscale.p, s)) {
+                                 m.scale, m.kind, p.q.p, p.xscale.p, p.xscale_t.p, s)) {
             for (int i = 0; i < p.count; ++i)
                 m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
             launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,

@@ -52,7 +52,7 @@ struct Matrix {
 // Per-handle stream and grow-only staging buffers.
 struct Staging {
     hipStream_t stream = nullptr;
-    DevBuf<float> x, rot, y, big, xs;
+    DevBuf<float> x, rot, y, big, xs, xst;
     DevBuf<int32_t> q;
     DevBuf<_Float16> xh;  // fp16 transformed activations of the prefill GEMM
     HostBuf<float> hx, hy;
@@ -79,7 +79,7 @@ struct SdotHandle {
     uint32_t centroids[4] = {};
     void init_tables();
     SdotGeom geom() const;
-    void prepare_device(const float *d_x, int batch, int32_t *q, float *xs, hipStream_t s);
+    void prepare_device(const float *d_x, int batch, int32_t *q, float *xs, float *xst, hipStream_t s);
     void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
     void linear_host(const float *x, float *y, int batch);
 };

@@ -176,6 +176,7 @@ struct SdotJob {
     const float *xs;          // per-group activation scales [batch][groups]
     float *y;
     int rows, n_pad, block_begin, batch;
+    const float *xst;         // the same scales transposed, [groups][batch] (MFMA path; null: dot4 path only)
 };
 
 // ---------------------------------------------------------------------------
@@ -210,8 +211,10 @@ void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, 
 // xptr[v / batch] (a device table); each row has `in` floats. FWHT per group,
 // quantize, permute. Returns false (nothing launched) when the group is too
 // large for one block's LDS; callers then transform and quantize separately.
+// xst (nullable) also receives the scales transposed per matrix input: [v / batch][groups][v % batch].
 bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, int nvec, int in, int padded,
-                         int dev_positions, int group, float scale, int kind, int32_t *q, float *xs, hipStream_t s);
+                         int dev_positions, int group, float scale, int kind, int32_t *q, float *xs, float *xst,
+                         hipStream_t s);
 // int8 path: quantize rot (already transformed) into permuted int8 + scales.
 void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded, int dev_positions,
                           int group, int kind, int32_t *q, float *xs, hipStream_t s);

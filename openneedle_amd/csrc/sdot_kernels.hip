@@ -18,6 +18,9 @@
 
 #include <hip/hip_fp16.h>
 
+#include <cstdlib>
+#include <cstring>
+
 namespace nd {
 
 namespace {
@@ -79,8 +82,8 @@ constexpr int kPrepareMinSeg = 1024;
 __global__ __launch_bounds__(256) void sdot_prepare_kernel(const float *__restrict__ x0,
                                                            const float *const *__restrict__ xptr, int batch, int in,
                                                            int padded, int dev, int group, float scale, int kind,
-                                                           int8_t *__restrict__ q, float *__restrict__ xs, int groups,
-                                                           int seg) {
+                                                           int8_t *__restrict__ q, float *__restrict__ xs,
+                                                           float *__restrict__ xst, int groups, int seg) {
     extern __shared__ float buf[];
     __shared__ unsigned gmax[kPrepareMinSeg / 8];
     const int v = blockIdx.y;
@@ -117,7 +120,10 @@ __global__ __launch_bounds__(256) void sdot_prepare_kernel(const float *__restri
             const float absmax = __uint_as_float(gmax[i / group]);
             float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
             if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
-            if (p % group == 0) xs[static_cast<size_t>(v) * groups + p / group] = sc;
+            if (p % group == 0) {
+                xs[static_cast<size_t>(v) * groups + p / group] = sc;
+                if (xst) xst[(static_cast<size_t>(v / batch) * groups + p / group) * batch + v % batch] = sc;
+            }
             float val = rintf(buf[i] / sc);
             val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
             out = static_cast<int8_t>(val);
@@ -405,6 +411,194 @@ void launch_sdot_bt(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs,
     ND_HIP(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------
+// int8 path on MFMA (batch >= 2, groups of 32 .. 256 positions)
+//
+// One wave per (32 weight rows, 32 batch rows) and v_mfma_i32_32x32x32_i8
+// per 32 positions: B = decoded int8 centroids of weight row lane % 32,
+// A = the permuted int8 activations of batch row lane % 32; lanes 0-31 and
+// 32-63 cover positions 0-15 and 16-31 of the step, in the same byte order
+// for A and B (the sum over K is independent of how K is laid out across a
+// lane's bytes, as long as A and B agree). The accumulator of a group is the
+// exact int32 group dot, so the epilogue is the reference's
+//   value += (float(dot) * (half(norm) * cs)) * x_scale[g]
+// in group order (sdot.cpp:43-44, 142-149): bit-identical outputs.
+// Accumulator register r of lane l holds batch row 8(r/4) + 4(l/32) + r%4
+// and weight row l % 32; J = 1, 2, 4 keeps the 4, 8 or 16 registers that
+// cover the batch tile. Codes, activations, norms and the transposed scales
+// of three groups are in flight per lane (a register ring); loads past the
+// row tile, the batch tile or the last group read zero through the buffer
+// bounds or land on data that is never used.
+// ---------------------------------------------------------------------------
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int KIND, int GROUP, int J>
+struct MfmaSlot {
+    static constexpr int kSteps = GROUP / 32;
+    static constexpr int kCodeDw = KIND == kNib ? 2 : 1;  // code dwords per lane per step
+    uint32_t code[kSteps * kCodeDw];
+    u32x4 q[kSteps];
+    u32x4 xs[J];
+    uint16_t norm;
+};
+
+template <int KIND, int GROUP, int J>
+__device__ __forceinline__ void mfma_load(MfmaSlot<KIND, GROUP, J> &sl, __amdgpu_buffer_rsrc_t codes,
+                                          __amdgpu_buffer_rsrc_t norms, __amdgpu_buffer_rsrc_t q,
+                                          __amdgpu_buffer_rsrc_t xst, int g, int rt, int i, int h, int dev,
+                                          int batch, int b0) {
+    using S = MfmaSlot<KIND, GROUP, J>;
+#pragma unroll
+    for (int st = 0; st < S::kSteps; ++st) {
+        const int pos = g * GROUP + st * 32;  // first position of the step
+        if constexpr (KIND == kNib) {
+            // chunk = 32 positions; this lane's dwords 2h, 2h+1
+            const int soff = __builtin_amdgcn_readfirstlane((pos / 32) * kRowsPerBlock * 16);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(codes, rt * 16u + h * 8u, soff, 0);
+            sl.code[2 * st] = v[0];
+            sl.code[2 * st + 1] = v[1];
+        } else {
+            // chunk = 64 positions; this step is dwords 2((pos / 32) % 2) .. +1; this lane's is + h
+            const int soff = __builtin_amdgcn_readfirstlane((pos / 64) * kRowsPerBlock * 16 + ((pos / 32) % 2) * 8);
+            sl.code[st] = __builtin_amdgcn_raw_buffer_load_b32(codes, rt * 16u + h * 4u, soff, 0);
+        }
+        sl.q[st] = __builtin_amdgcn_raw_buffer_load_b128(q, static_cast<uint32_t>(i) * dev + h * 16u,
+                                                         __builtin_amdgcn_readfirstlane(pos), 0);
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        sl.xs[j] = __builtin_amdgcn_raw_buffer_load_b128(
+            xst, (b0 + 8 * j + 4 * h) * 4u, __builtin_amdgcn_readfirstlane(g * batch * 4), 0);
+    sl.norm = __builtin_amdgcn_raw_buffer_load_b16(norms, rt * 2u,
+                                                   __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2), 0);
+}
+
+template <int KIND, int GROUP, int J>
+__device__ __forceinline__ void mfma_group(const MfmaSlot<KIND, GROUP, J> &sl, const uint32_t cent[4], float cs,
+                                           float (&value)[4 * J]) {
+    using S = MfmaSlot<KIND, GROUP, J>;
+    v16i acc = {};
+#pragma unroll
+    for (int st = 0; st < S::kSteps; ++st) {
+        v4i b;
+        if constexpr (KIND == kNib) {
+            uint32_t ce0, co0, ce1, co1;
+            decode_nib(sl.code[2 * st], cent[0], cent[1], cent[2], cent[3], ce0, co0);
+            decode_nib(sl.code[2 * st + 1], cent[0], cent[1], cent[2], cent[3], ce1, co1);
+            b = v4i{static_cast<int>(ce0), static_cast<int>(co0), static_cast<int>(ce1), static_cast<int>(co1)};
+        } else {
+            const uint32_t wd = sl.code[st];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) b[m] = static_cast<int>(__builtin_amdgcn_perm(0u, cent[0], (wd >> (2 * m)) & 0x03030303u));
+        }
+        const v4i a = __builtin_bit_cast(v4i, sl.q[st]);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
+    }
+    const float ns = h2f(sl.norm) * cs;  // sdot.cpp:43-44
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        // bit_cast the whole vector: this compiler's __builtin_bit_cast of a
+        // single ext_vector element lvalue (v.y, v[t]) reads element 0
+        const f32x4 xs = __builtin_bit_cast(f32x4, sl.xs[j]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) value[4 * j + t] = value[4 * j + t] + (static_cast<float>(acc[4 * j + t]) * ns) * xs[t];
+    }
+}
+
+constexpr int kMfmaRing = 3;
+
+template <int KIND, int GROUP, int J>
+__global__ __launch_bounds__(kRowsPerBlock) void sdot_mfma_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+                                                                  int njobs, SdotGeom geom) {
+    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);      // wave-uniform
+    const int rb = blockIdx.x * (kRowsPerBlock / 64) + wave;                // 32-row block across the plan
+    const int blk = rb / (kRowsPerBlock / 32);                            // 256-row tile across the plan
+    SdotJob J0 = job0;
+    if (njobs > 0) {
+        const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
+        int j = 0;
+        for (int k = 1; k < njobs; ++k)
+            if (cj[k].block_begin <= blk) j = k;
+        J0.codes = cj[j].codes;
+        J0.norms = cj[j].norms;
+        J0.q = cj[j].q;
+        J0.y = cj[j].y;
+        J0.rows = cj[j].rows;
+        J0.block_begin = cj[j].block_begin;
+        J0.batch = cj[j].batch;
+        J0.xst = cj[j].xst;
+    }
+    const int rows = J0.rows, batch = J0.batch;
+    const int tile = blk - J0.block_begin;
+    const int rt = (rb % (kRowsPerBlock / 32)) * 32 + i;  // row within the tile
+    const int row = tile * kRowsPerBlock + rt;
+    const int b0 = static_cast<int>(blockIdx.y) * 32;
+    const int groups = geom.groups;
+    const int dev = geom.windows * kWindow;
+    const uint32_t cent[4] = {geom.cent[0], geom.cent[1], geom.cent[2], geom.cent[3]};
+    const float cs = geom.centroid_scale;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J0.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J0.norms + static_cast<size_t>(tile) * groups * kRowsPerBlock,
+                                                     static_cast<uint32_t>(groups) * kRowsPerBlock * 2u);
+    const int tile_rows = min(32, batch - b0);
+    const __amdgpu_buffer_rsrc_t q =
+        buffer_rsrc(reinterpret_cast<const int8_t *>(J0.q) + static_cast<size_t>(b0) * dev,
+                    static_cast<uint32_t>(tile_rows) * dev);
+    const __amdgpu_buffer_rsrc_t xst = buffer_rsrc(J0.xst, static_cast<uint32_t>(groups) * batch * 4u);
+
+    float value[4 * J];
+#pragma unroll
+    for (int r = 0; r < 4 * J; ++r) value[r] = 0.0f;
+    MfmaSlot<KIND, GROUP, J> ring[kMfmaRing];
+#pragma unroll
+    for (int k = 0; k < kMfmaRing; ++k) mfma_load(ring[k], codes, norms, q, xst, k, rt, i, h, dev, batch, b0);
+    // whole rounds of kMfmaRing groups, each slot refilled kMfmaRing groups ahead once used
+    int g = 0;
+    for (; g + kMfmaRing <= groups; g += kMfmaRing) {
+#pragma unroll
+        for (int k = 0; k < kMfmaRing; ++k) {
+            mfma_group(ring[k], cent, cs, value);
+            mfma_load(ring[k], codes, norms, q, xst, g + k + kMfmaRing, rt, i, h, dev, batch, b0);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kMfmaRing; ++k)
+        if (g + k < groups) mfma_group(ring[k], cent, cs, value);
+    if (row < rows) {
+#pragma unroll
+        for (int r = 0; r < 4 * J; ++r) {
+            const int m = b0 + 8 * (r / 4) + 4 * h + (r % 4);
+            if (m < batch) ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * rows + row] = value[r];
+        }
+    }
+}
+
+template <int KIND, int J>
+void launch_sdot_mfma_j(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                        hipStream_t s) {
+    dim3 grid(blocks * (kRowsPerBlock / 128), (batch + 31) / 32), block(kRowsPerBlock);
+    switch (g.group) {
+    case 32: hipLaunchKernelGGL((sdot_mfma_kernel<KIND, 32, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((sdot_mfma_kernel<KIND, 64, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((sdot_mfma_kernel<KIND, 128, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL((sdot_mfma_kernel<KIND, 256, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    }
+    ND_HIP(hipGetLastError());
+}
+
+template <int KIND>
+void launch_sdot_mfma(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                      hipStream_t s) {
+    if (batch <= 8) launch_sdot_mfma_j<KIND, 1>(g, job0, jobs, njobs, blocks, batch, s);
+    else if (batch <= 16) launch_sdot_mfma_j<KIND, 2>(g, job0, jobs, njobs, blocks, batch, s);
+    else launch_sdot_mfma_j<KIND, 4>(g, job0, jobs, njobs, blocks, batch, s);
+}
+
 int device_cus() {
     static int cus = [] {
         int dev = 0, n = 256;
@@ -440,14 +634,14 @@ void launch_sdot_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
 }  // namespace
 
 bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, int nvec, int in, int padded,
-                         int dev, int group, float scale, int kind, int32_t *q, float *xs, hipStream_t s) {
+                         int dev, int group, float scale, int kind, int32_t *q, float *xs, float *xst, hipStream_t s) {
     if (group > kPrepareMaxGroup) return false;
     ND_CHECK(group >= 8 && (group & (group - 1)) == 0, "int8 prepare: group must be a power of two >= 8");
     if (nvec <= 0) return true;
     const int seg = group > kPrepareMinSeg ? group : kPrepareMinSeg;
     dim3 grid((dev + seg - 1) / seg, nvec), block(256);
     hipLaunchKernelGGL(sdot_prepare_kernel, grid, block, seg * sizeof(float), s, x0, xptr, batch, in, padded, dev,
-                       group, scale, kind, reinterpret_cast<int8_t *>(q), xs, padded / group, seg);
+                       group, scale, kind, reinterpret_cast<int8_t *>(q), xs, xst, padded / group, seg);
     ND_HIP(hipGetLastError());
     return true;
 }
@@ -468,6 +662,22 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     if (blocks <= 0 || batch <= 0) return;
     ND_CHECK(g.group >= 8, "int8 path: group must be >= 8");
     ND_CHECK(g.kind == kNib || g.group >= 16, "int8 path: 2-bit codes need group >= 16");
+    // Batches of 8 or more rows go to MFMA (groups of 32 .. 256; its jobs carry
+    // the transposed scales) when the 32-row x 32-batch-row wave tiles give
+    // at least two waves per SIMD; smaller batches decode once per row and
+    // run v_dot4, which does no work for padding batch rows.
+    // NEEDLE2_GPU_INT8_MFMA=always / never overrides the choice (auto).
+    const long mfma_waves = static_cast<long>(blocks) * (kRowsPerBlock / 32) * ((batch + 31) / 32);
+    const char *mode = std::getenv("NEEDLE2_GPU_INT8_MFMA");
+    const bool mfma_ok = batch >= 2 && g.group >= 32 && g.group <= kWindow;
+    bool mfma = mfma_ok && batch >= 8 && mfma_waves >= 2L * 4 * device_cus();
+    if (mode && std::strcmp(mode, "always") == 0) mfma = mfma_ok;
+    if (mode && std::strcmp(mode, "never") == 0) mfma = false;
+    if (mfma) {
+        if (g.kind == kNib) launch_sdot_mfma<kNib>(g, job0, jobs, njobs, blocks, batch, s);
+        else launch_sdot_mfma<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
+        return;
+    }
     if (g.kind == kNib) launch_sdot_kind<kNib>(g, job0, jobs, njobs, blocks, batch, s);
     else launch_sdot_kind<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
 }

@@ -82,3 +82,43 @@ def test_int8_plan_many_matrices():
     synchronize()
     for m, dy, e in zip(mats, d_y, expected):
         np.testing.assert_array_equal(dy.download(np.empty((2, m.shape[0]), np.float32)), e)
+
+
+@pytest.mark.parametrize("mode", ["always", "never"])
+@pytest.mark.parametrize("bits,group,batch", [(4, 32, 3), (4, 32, 9), (4, 32, 17), (4, 32, 33), (4, 32, 64),
+                                              (4, 64, 40), (4, 128, 12), (4, 256, 5), (2, 32, 8), (2, 32, 33),
+                                              (2, 64, 20)])
+def test_int8_batched_tiles_bit_exact(bits, group, batch, mode, monkeypatch):
+    """Batches run on int8 MFMA (tiles of 32 batch rows: ragged last tile) or on v_dot4 batch tiles, forced
+    either way here (the library picks by size otherwise); 300 ragged weight rows, zero / one-hot activation
+    rows: bit-exact with the oracle."""
+    monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", mode)
+    packed, norms, cb, dense = example(bits, rows=300, dim=1000, group=group, seed=7 * batch + group)
+    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    x = activations((batch, 1000), seed=batch)
+    x[0] = 0
+    if batch > 2:
+        x[2] = 0
+        x[2, 5] = 1
+    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
+
+
+@pytest.mark.parametrize("mode", ["always", "auto"])
+def test_int8_plan_decode_batch(mode, monkeypatch):
+    """A layer's Q | K | V projections for 64 sequences in one plan (one prepare and one GEMV launch)."""
+    monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", mode)
+    mats, d_x, d_y, expected = [], [], [], []
+    x = activations((64, 512), seed=640)
+    d_in = DeviceArray.from_host(x)
+    for i in range(3):
+        packed, norms, cb, _ = baseline(4, 512, 512, seed=700 + i)
+        m = NativeCQ(packed, norms, (512, 512), 4, 32, cb)
+        mats.append(m)
+        expected.append(oracle.sdot_linear(packed, norms, m.shape, 4, 32, cb, x))
+        d_y.append(DeviceArray(64 * 4 * 512))
+    plan = Plan(mats, [d_in.ptr] * 3, [d.ptr for d in d_y], batch=64, int8=True)
+    for _ in range(2):
+        plan.run()
+        synchronize()
+        for dy, e in zip(d_y, expected):
+            np.testing.assert_array_equal(dy.download(np.empty((64, 512), np.float32)), e)
