@@ -147,13 +147,13 @@ def bench_prefill(steps, warmup, stream):
     return t0.elapsed_ms(t1) / steps, statistics.mean(a.elapsed_ms(b) for a, b in ev)
 
 
-def bench_decode_layer(steps, warmup, stream):
-    """One decoder layer for 64 sequences at context 2048 (hidden 512, 8 heads = 8 kv heads, head_dim 64,
-    MLP 2048): int8-path CQ4 g32 projections Q|K|V (one plan), KV store of the new token, decode
-    attention over 2048 int8 slots, O, MLP up and down. Elementwise glue (norms, RoPE, gates,
-    activation) is omitted. Returns ms per layer step."""
-    from openneedle_amd.native import DeviceArray, Event, KVCache, NativeCQ, Plan, synchronize
-    seqs, cap, kvh, hd, heads, hidden, mlp = 64, 2048, 8, 64, 8, 512, 2048
+def bench_decode_layer(steps, warmup, stream, seqs=64):
+    """One decoder layer for `seqs` sequences at context 2048 (hidden 512, 8 heads = 8 kv heads, head_dim 64,
+    MLP 2048): int8-path CQ4 g32 projections Q|K|V (one plan), KV store of the new token, decode attention
+    over 2048 int8 slots, O, MLP up and down. Elementwise glue (norms, RoPE, gates, activation) is omitted.
+    Returns (eager ms per step, ms per step replaying the step captured in a HIP graph)."""
+    from openneedle_amd.native import DeviceArray, Event, Graph, KVCache, NativeCQ, Plan, synchronize
+    cap, kvh, hd, heads, hidden, mlp = 2048, 8, 64, 8, 512, 2048
     rng = np.random.default_rng(23)
 
     def mat(rows, cols):
@@ -167,7 +167,7 @@ def bench_decode_layer(steps, warmup, stream):
             ("u", mlp), ("d", hidden))}
     buf["x"].upload(rng.normal(size=(seqs, hidden)).astype(np.float32))
     p = lambda ms, xs, ys: Plan(ms, [buf[n].ptr for n in xs], [buf[n].ptr for n in ys], batch=seqs, int8=True)  # noqa: E731
-    plans = [p([wq, wk, wv], "xxx", "qkv"), None, None, p([wo], "a", "o"), p([wu], "o", "u"), p([wd], "u", "d")]
+    plans = [p([wq, wk, wv], "xxx", "qkv"), p([wo], "a", "o"), p([wu], "o", "u"), p([wd], "u", "d")]
     kv = KVCache(1, cap, kvh, hd, seqs)
     for c0 in range(0, cap - 1, 512):
         n = min(512, cap - 1 - c0)
@@ -175,24 +175,32 @@ def bench_decode_layer(steps, warmup, stream):
         v = DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32))
         kv.store(0, k.ptr, v.ptr, n, first_slot=c0, stream=stream)
         stream.synchronize()
+    first = DeviceArray.from_host(np.full(seqs, cap - 1, np.int32))  # the new token's slot, on the device
 
     def step():
         plans[0].run(stream)
-        kv.store(0, buf["k"].ptr, buf["v"].ptr, 1, first_slot=cap - 1, stream=stream)
+        kv.store_device(0, buf["k"].ptr, buf["v"].ptr, 1, first.ptr, stream=stream)
         kv.attention(0, buf["q"].ptr, buf["a"].ptr, heads, cap, stream=stream)
-        for pl in plans[3:]:
+        for pl in plans[1:]:
             pl.run(stream)
 
-    for _ in range(warmup):
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        synchronize()
+        t0, t1 = Event(), Event()
+        t0.record(stream)
+        for _ in range(steps):
+            fn()
+        t1.record(stream)
+        synchronize()
+        return t0.elapsed_ms(t1) / steps
+
+    eager = timed(step)
+    with Graph.capture(stream) as g:
         step()
-    synchronize()
-    t0, t1 = Event(), Event()
-    t0.record(stream)
-    for _ in range(steps):
-        step()
-    t1.record(stream)
-    synchronize()
-    return t0.elapsed_ms(t1) / steps
+    graphed = timed(lambda: g.launch(stream))
+    return eager, graphed
 
 
 def cpu_baseline(budget_s=20.0):
@@ -263,8 +271,10 @@ def main():
         del a, b
 
     if args.only == "decode":
-        ms_d = bench_decode_layer(args.steps, args.warmup, stream)
-        log(f"decode layer (64 seqs, ctx 2048): {ms_d * 1e3:.1f} us -> {64 / (ms_d * 1e-3):.0f} tokens/s per layer")
+        for seqs in (64, 1):
+            ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs)
+            log(f"decode layer ({seqs} seqs, ctx 2048): eager {ms_e * 1e3:.1f} us, graph {ms_g * 1e3:.1f} us -> "
+                f"{seqs / (ms_g * 1e-3):.0f} tokens/s per layer")
         return
     if args.only == "prefill":
         ms_p, g_p = bench_prefill(args.steps, args.warmup, stream)
@@ -335,12 +345,15 @@ def main():
         extra["prefill_mfma_util"] = round(extra["prefill_tflops"] / MFMA_FP16_PEAK_TFLOPS, 4)
         log(f"prefill GEMM {g_p * 1e3:.1f} us ({extra['prefill_tflops']} TFLOP/s), step {ms_p * 1e3:.1f} us")
 
-        log("decode layer: 64 sequences, ctx 2048, int8-path CQ4 projections + int8-KV attention")
-        ms_d = bench_decode_layer(args.steps, args.warmup, stream)
-        extra["decode_layer_us"] = round(ms_d * 1e3, 2)
-        extra["decode_tokens_per_s_per_layer"] = round(64 / (ms_d * 1e-3), 0)
-        extra["decode_tokens_per_s_27_layers"] = round(64 / (27 * ms_d * 1e-3), 0)
-        log(f"decode layer {ms_d * 1e3:.1f} us -> {extra['decode_tokens_per_s_per_layer']:.0f} tokens/s per layer")
+        for seqs in (64, 1):
+            log(f"decode layer: {seqs} sequence(s), ctx 2048, int8-path CQ4 projections + int8-KV attention")
+            ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs)
+            extra[f"decode_b{seqs}_layer_us"] = round(ms_g * 1e3, 2)
+            extra[f"decode_b{seqs}_layer_eager_us"] = round(ms_e * 1e3, 2)
+            extra[f"decode_b{seqs}_tokens_per_s_per_layer"] = round(seqs / (ms_g * 1e-3), 0)
+            extra[f"decode_b{seqs}_tokens_per_s_27_layers"] = round(seqs / (27 * ms_g * 1e-3), 0)
+            log(f"decode layer b{seqs}: graph {ms_g * 1e3:.1f} us (eager {ms_e * 1e3:.1f} us) -> "
+                f"{extra[f'decode_b{seqs}_tokens_per_s_per_layer']:.0f} tokens/s per layer")
 
     cpu = None
     if not args.no_cpu:

@@ -125,6 +125,14 @@ void needle2_gpu_event_destroy(void *event);
 int needle2_gpu_event_record(void *event, void *stream);
 float needle2_gpu_event_elapsed(void *start, void *stop); /* ms; waits for stop */
 int needle2_gpu_device_info(char *buf, int len);         /* "name;arch;cus;hbm_bytes;clock_khz" */
+/* HIP graphs (no counterpart in the reference, which has no device): capture
+ * what is issued to `stream` between begin and end, instantiate, replay with
+ * one launch. Entry points used inside must have run once before the capture
+ * and must not read host memory: plan_run, attention, kv_store_device. */
+int needle2_gpu_graph_begin(void *stream);
+void *needle2_gpu_graph_end(void *stream);                /* instantiated graph, or NULL */
+int needle2_gpu_graph_launch(void *graph, void *stream);
+void needle2_gpu_graph_destroy(void *graph);
 
 /* ---- int8 KV cache and batched decode attention ----------------------------
  * Replaces the int8 branch of the reference Engine's cache and attention,
@@ -146,6 +154,11 @@ size_t needle2_gpu_kv_storage_bytes(void *kv);   /* engine.cpp kv_storage_bytes 
  * (seq_first_slot is a host array). */
 int needle2_gpu_kv_store(void *kv, int layer, const float *d_k, const float *d_v, int count, int first_slot,
                          const int *seq_first_slot, void *stream);
+/* The same with the first slots in device memory (d_first_slot[seqs]); no
+ * host copy or wait, so it can be captured in a graph. Rows whose slot falls
+ * outside [0, capacity) are skipped. */
+int needle2_gpu_kv_store_device(void *kv, int layer, const float *d_k, const float *d_v, int count,
+                                const int *d_first_slot, void *stream);
 /* d_q, d_out: device fp32 [seqs][heads][head_dim]. Sequence s attends slots
  * d_slots[j] (device, >= length entries; NULL: j) for j < d_lengths[s]
  * (device; NULL: length), never more than `length`; listed slots outside

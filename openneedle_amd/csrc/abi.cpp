@@ -560,6 +560,42 @@ int needle2_gpu_stream_synchronize(void *s) {
     return guarded([&] { ND_HIP(hipStreamSynchronize(static_cast<hipStream_t>(s))); });
 }
 
+// HIP graphs: capture the work issued to `stream` between begin and end
+// (thread-local capture mode), instantiate it, and replay it with one launch.
+// Only launches belong in a capture: every entry point used inside must have
+// run once before (their grow-only buffers are then allocated) and must not
+// copy from host memory or wait on the host.
+int needle2_gpu_graph_begin(void *stream) {
+    return guarded([&] {
+        ND_CHECK(stream, "graph capture needs a stream created by needle2_gpu_stream_create");
+        ND_HIP(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal));
+    });
+}
+
+void *needle2_gpu_graph_end(void *stream) {
+    hipGraphExec_t exec = nullptr;
+    if (guarded([&] {
+            hipGraph_t graph = nullptr;
+            ND_HIP(hipStreamEndCapture(static_cast<hipStream_t>(stream), &graph));
+            const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            ND_HIP(e);
+        }))
+        return nullptr;
+    return exec;
+}
+
+int needle2_gpu_graph_launch(void *graph, void *stream) {
+    return guarded([&] {
+        ND_CHECK(graph, "graph launch: null graph");
+        ND_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), static_cast<hipStream_t>(stream)));
+    });
+}
+
+void needle2_gpu_graph_destroy(void *graph) {
+    if (graph) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
+}
+
 void *needle2_gpu_event_create(void) {
     hipEvent_t e = nullptr;
     if (guarded([&] { ND_HIP(hipEventCreate(&e)); })) return nullptr;

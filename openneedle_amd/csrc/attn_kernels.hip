@@ -37,7 +37,8 @@ __global__ __launch_bounds__(256) void kv_store_kernel(KvStoreArgs a) {
     const int kh = wave % a.kvheads;
     const int i = (wave / a.kvheads) % a.count;
     const int seq = wave / (a.kvheads * a.count);
-    const int slot = a.first_slot[seq] + i;  // validated on the host
+    const int slot = a.first_slot[seq] + i;
+    if (slot < 0 || slot >= a.capacity) return;  // wave-uniform; device-side slot tables are not host-checked
     const size_t src = static_cast<size_t>(wave) * a.head_dim;
     const size_t dst_row = (static_cast<size_t>(seq) * a.kvheads + kh) * a.capacity + slot;
     const int HD = a.head_dim;

@@ -143,6 +143,36 @@ int needle2_gpu_kv_store(void *h, int layer, const float *d_k, const float *d_v,
     });
 }
 
+// needle2_gpu_kv_store with the per-sequence first slots already in device
+// memory (d_first_slot[seqs]): no host copy and no host wait, so a decode
+// step built from it can be captured in a HIP graph and replayed while the
+// caller advances d_first_slot on the device. Rows whose slot falls outside
+// [0, capacity) are skipped.
+int needle2_gpu_kv_store_device(void *h, int layer, const float *d_k, const float *d_v, int count,
+                                const int *d_first_slot, void *stream) {
+    return guarded([&] {
+        KvHandle &kv = *kv_of(h);
+        check_layer(kv, layer);
+        ND_CHECK(count >= 0, "KV store: count must be >= 0");
+        if (count == 0) return;
+        ND_CHECK(d_k && d_v && d_first_slot, "KV store: null input");
+        KvStoreArgs a{};
+        a.k = d_k;
+        a.v = d_v;
+        a.k8 = kv.k8.p + kv.layer_codes() * layer;
+        a.v8 = kv.v8.p + kv.layer_codes() * layer;
+        a.ks = kv.ks.p + kv.layer_scales() * layer;
+        a.vs = kv.vs.p + kv.layer_scales() * layer;
+        a.first_slot = d_first_slot;
+        a.seqs = kv.seqs;
+        a.count = count;
+        a.kvheads = kv.kvheads;
+        a.head_dim = kv.head_dim;
+        a.capacity = kv.capacity;
+        launch_kv_store(a, static_cast<hipStream_t>(stream));
+    });
+}
+
 // One decode-attention step of `layer` for every sequence.
 // d_q, d_out: device fp32 [seqs][heads][head_dim]; heads is a multiple of
 // kvheads (1, 2, 4 or 8 query heads per kv head). Sequence s attends the

@@ -93,6 +93,11 @@ def _library():
     _bind(lib, "needle2_gpu_kv_destroy", [_P])
     _bind(lib, "needle2_gpu_kv_storage_bytes", [_P], ct.c_size_t)
     _bind(lib, "needle2_gpu_kv_store", [_P, _I, _P, _P, _I, _I, _P, _P], _I)
+    _bind(lib, "needle2_gpu_kv_store_device", [_P, _I, _P, _P, _I, _P, _P], _I)
+    _bind(lib, "needle2_gpu_graph_begin", [_P], _I)
+    _bind(lib, "needle2_gpu_graph_end", [_P], _P)
+    _bind(lib, "needle2_gpu_graph_launch", [_P, _P], _I)
+    _bind(lib, "needle2_gpu_graph_destroy", [_P])
     _bind(lib, "needle2_gpu_attention", [_P, _I, _P, _P, _I, _I, _P, _P, _I, _P], _I)
     _bind(lib, "needle2_gpu_kv_import", [_P, _I, _I, _P, _P, _P, _P, _I, _I], _I)
     _bind(lib, "needle2_gpu_kv_export", [_P, _I, _I, _P, _P, _P, _P, _I, _I], _I)
@@ -351,6 +356,43 @@ class Event:
             self.ptr = None
 
 
+class Graph:
+    """Work issued to ``stream`` inside ``with Graph.capture(stream) as g:`` replayed by ``g.launch(stream)``.
+
+    Everything captured must have run once eagerly before (buffers allocated)
+    and must not read host memory: plan runs, attention, ``store_device``.
+    """
+
+    def __init__(self):
+        self._lib = _library()
+        self.ptr = None
+
+    @classmethod
+    def capture(cls, stream: Stream):
+        import contextlib
+
+        g = cls()
+
+        @contextlib.contextmanager
+        def cm():
+            _check(g._lib.needle2_gpu_graph_begin(stream.ptr), "graph begin")
+            try:
+                yield g
+            finally:
+                g.ptr = g._lib.needle2_gpu_graph_end(stream.ptr)
+            if not g.ptr:
+                raise RuntimeError(f"graph capture failed: {last_error()}")
+        return cm()
+
+    def launch(self, stream: Stream) -> None:
+        _check(self._lib.needle2_gpu_graph_launch(self.ptr, stream.ptr), "graph launch")
+
+    def __del__(self):
+        if getattr(self, "ptr", None):
+            self._lib.needle2_gpu_graph_destroy(self.ptr)
+            self.ptr = None
+
+
 def copy_kernel(dst: DeviceArray, src: DeviceArray, nbytes: int, stream: "Stream | None" = None) -> None:
     assert nbytes <= dst.nbytes and nbytes <= src.nbytes
     _check(_library().needle2_gpu_copy_kernel(dst.ptr, src.ptr, int(nbytes), stream.ptr if stream else None), "copy")
@@ -431,6 +473,12 @@ class KVCache:
         _check(self._lib.needle2_gpu_kv_store(self.ptr, layer, int(d_k), int(d_v), int(count), first,
                                               per_seq.ctypes.data if per_seq is not None else None,
                                               stream.ptr if stream else None), "KV store")
+
+    def store_device(self, layer: int, d_k, d_v, count: int, d_first_slot, stream: "Stream | None" = None) -> None:
+        """:meth:`store` with the per-sequence first slots in device memory (int32 [seqs]); capturable."""
+        _check(self._lib.needle2_gpu_kv_store_device(self.ptr, layer, int(d_k), int(d_v), int(count),
+                                                     int(d_first_slot), stream.ptr if stream else None),
+               "KV store")
 
     def attention(self, layer: int, d_q, d_out, heads: int, length: int, d_slots=None, d_lengths=None,
                   splits: int = 0, stream: "Stream | None" = None) -> None:
