@@ -136,13 +136,25 @@ __global__ __launch_bounds__(256) void sdot_prepare_kernel(const float *__restri
 // GEMV
 // ---------------------------------------------------------------------------
 // 8 four-bit codes (one dword) -> int8 centroids for codes {0,2,4,6} and {1,3,5,7}.
+// (x & m) | c in one VALU op (the compiler emits a separate and + or); GFX9
+// VALU takes one scalar operand, so the mask comes in a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m_vgpr, uint32_t c_sgpr) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m_vgpr), "s"(c_sgpr));
+    return r;
+}
+
+// 13 VALU ops: 3 masks/shifts for the low-bit selectors, 4 for the high-half
+// selectors, 6 byte permutes.
 __device__ __forceinline__ void decode_nib(uint32_t w, uint32_t T0, uint32_t T1, uint32_t T2, uint32_t T3,
                                            uint32_t &ce, uint32_t &co) {
-    const uint32_t e = w & 0x07070707u, o = (w >> 4) & 0x07070707u;
+    const uint32_t m4 = 0x04040404u;
+    const uint32_t w4 = w >> 4;
+    const uint32_t e = w & 0x07070707u, o = w4 & 0x07070707u;
     const uint32_t le = __builtin_amdgcn_perm(T1, T0, e), he = __builtin_amdgcn_perm(T3, T2, e);
     const uint32_t lo = __builtin_amdgcn_perm(T1, T0, o), ho = __builtin_amdgcn_perm(T3, T2, o);
-    const uint32_t se = ((w >> 1) & 0x04040404u) | 0x03020100u;  // bit 3 of each code picks high half
-    const uint32_t so = ((w >> 5) & 0x04040404u) | 0x03020100u;
+    const uint32_t se = and_or(w >> 1, m4, 0x03020100u);  // bit 3 of each code picks the high half
+    const uint32_t so = and_or(w4 >> 1, m4, 0x03020100u);
     ce = __builtin_amdgcn_perm(he, le, se);
     co = __builtin_amdgcn_perm(ho, lo, so);
 }
@@ -599,6 +611,161 @@ void launch_sdot_mfma(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     else launch_sdot_mfma_j<KIND, 4>(g, job0, jobs, njobs, blocks, batch, s);
 }
 
+// ---------------------------------------------------------------------------
+// int8 GEMV for one batch row (decode), one thread per output row.
+//
+// The row's permuted int8 activations and group scales (a few KiB) are
+// staged in LDS once per workgroup; after that barrier the waves never
+// synchronise again. Each thread streams its row's 16-byte code chunks
+// through a register ring kRowRing chunks deep (a chunk is refilled right
+// after it is decoded, so loads run continuously ahead), decodes every code
+// dword once (v_perm_b32 centroid lookups) and accumulates v_dot4_i32_i8
+// against wave-uniform LDS reads. Groups close with the reference's epilogue
+//   value += (float(dot) * (half(norm) * cs)) * x_scale[g]
+// in group order (sdot.cpp:43-44, 142-149): bit-identical outputs.
+// ---------------------------------------------------------------------------
+constexpr int kRowRing = 8;
+constexpr int kRowMaxDev = 32768;  // staged activation bytes per workgroup
+
+template <int KIND, int GROUP>
+struct RowSlot {
+    static constexpr int kCodes = KIND == kNib ? 32 : 64;                // codes per chunk
+    static constexpr int kNorms = GROUP >= kCodes ? 1 : kCodes / GROUP;  // norms a chunk needs
+    u32x4 code;
+    uint16_t norm[kNorms];
+};
+
+template <int KIND, int GROUP>
+__device__ __forceinline__ void row_load(RowSlot<KIND, GROUP> &sl, __amdgpu_buffer_rsrc_t codes,
+                                         __amdgpu_buffer_rsrc_t norms, int c) {
+    using S = RowSlot<KIND, GROUP>;
+    sl.code = __builtin_amdgcn_raw_buffer_load_b128(codes, threadIdx.x * 16u,
+                                                   __builtin_amdgcn_readfirstlane(c * kRowsPerBlock * 16), 0);
+#pragma unroll
+    for (int k = 0; k < S::kNorms; ++k) {
+        const int g = c * S::kCodes / GROUP + k;  // the chunk's group (GROUP >= chunk) or its k-th group
+        sl.norm[k] = __builtin_amdgcn_raw_buffer_load_b16(
+            norms, threadIdx.x * 2u, __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2), 0);
+    }
+}
+
+template <int KIND, int GROUP>
+__device__ __forceinline__ void row_compute(const RowSlot<KIND, GROUP> &sl, const uint32_t *lq, const float *lxs,
+                                            const uint32_t cent[4], float cs, int c, int groups, float &value,
+                                            int &dot) {
+    using S = RowSlot<KIND, GROUP>;
+    const uint32_t words[4] = {sl.code.x, sl.code.y, sl.code.z, sl.code.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        if constexpr (KIND == kNib) {
+            uint32_t ce, co;
+            decode_nib(words[d], cent[0], cent[1], cent[2], cent[3], ce, co);
+            const uint32_t *qd = lq + c * 8 + d * 2;  // permuted: codes {0,2,4,6}, then {1,3,5,7}
+            dot = __builtin_amdgcn_sdot4(static_cast<int>(ce), static_cast<int>(qd[0]), dot, false);
+            dot = __builtin_amdgcn_sdot4(static_cast<int>(co), static_cast<int>(qd[1]), dot, false);
+        } else {
+            const uint32_t *qd = lq + c * 16 + d * 4;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+                dot = __builtin_amdgcn_sdot4(
+                    static_cast<int>(__builtin_amdgcn_perm(0u, cent[0], (words[d] >> (2 * m)) & 0x03030303u)),
+                    static_cast<int>(qd[m]), dot, false);
+        }
+        constexpr int kPer = S::kCodes / 4;  // codes per dword
+        const int pos_end = c * S::kCodes + (d + 1) * kPer;
+        const bool closes = GROUP >= S::kCodes ? (d == 3 && pos_end % GROUP == 0) : ((d + 1) * kPer) % GROUP == 0;
+        if (closes) {
+            const int k = GROUP >= S::kCodes ? 0 : (d + 1) * kPer / GROUP - 1;
+            const int g = pos_end / GROUP - 1;
+            if (g < groups) {
+                const float ns = h2f(sl.norm[k]) * cs;  // sdot.cpp:43-44
+                value = value + (static_cast<float>(dot) * ns) * lxs[g];
+            }
+            dot = 0;
+        }
+    }
+}
+
+template <int KIND, int GROUP>
+__global__ __launch_bounds__(kRowsPerBlock) void sdot_row_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+                                                                int njobs, SdotGeom geom) {
+    using S = RowSlot<KIND, GROUP>;
+    extern __shared__ __attribute__((aligned(16))) uint32_t row_lds[];
+    const int blk = blockIdx.x;
+    SdotJob J = job0;
+    if (njobs > 0) {
+        const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
+        int j = 0;
+        for (int k = 1; k < njobs; ++k)
+            if (cj[k].block_begin <= blk) j = k;
+        J.codes = cj[j].codes;
+        J.norms = cj[j].norms;
+        J.q = cj[j].q;
+        J.xs = cj[j].xs;
+        J.y = cj[j].y;
+        J.rows = cj[j].rows;
+        J.block_begin = cj[j].block_begin;
+    }
+    const int tile = blk - J.block_begin;
+    const int row = tile * kRowsPerBlock + threadIdx.x;
+    const int groups = geom.groups;
+    const int dev = geom.windows * kWindow;
+    uint32_t *lq = row_lds;
+    float *lxs = reinterpret_cast<float *>(row_lds + dev / 4);
+    const uint32_t cent[4] = {geom.cent[0], geom.cent[1], geom.cent[2], geom.cent[3]};
+    const float cs = geom.centroid_scale;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms + static_cast<size_t>(tile) * groups * kRowsPerBlock,
+                                                     static_cast<uint32_t>(groups) * kRowsPerBlock * 2u);
+    const int nch = (groups * GROUP + S::kCodes - 1) / S::kCodes;  // chunks holding real positions
+    RowSlot<KIND, GROUP> ring[kRowRing];
+#pragma unroll
+    for (int k = 0; k < kRowRing; ++k) row_load(ring[k], codes, norms, k);
+    // stage the activation row and its group scales
+    const u32x4 *q4 = reinterpret_cast<const u32x4 *>(J.q);
+    for (int i = threadIdx.x; i < dev / 16; i += kRowsPerBlock) reinterpret_cast<u32x4 *>(lq)[i] = q4[i];
+    for (int i = threadIdx.x; i < groups; i += kRowsPerBlock) lxs[i] = J.xs[i];
+    __syncthreads();
+    float value = 0.0f;
+    int dot = 0;
+    int c0 = 0;
+    for (; c0 + kRowRing <= nch; c0 += kRowRing) {
+#pragma unroll
+        for (int k = 0; k < kRowRing; ++k) {
+            row_compute(ring[k], lq, lxs, cent, cs, c0 + k, groups, value, dot);
+            row_load(ring[k], codes, norms, c0 + k + kRowRing);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kRowRing; ++k)
+        if (c0 + k < nch) row_compute(ring[k], lq, lxs, cent, cs, c0 + k, groups, value, dot);
+    if (row < J.rows) ((ND_GLOBAL float *)J.y)[row] = value;
+}
+
+template <int KIND>
+void launch_sdot_row(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
+                     hipStream_t s) {
+    const int dev = g.windows * kWindow;
+    const size_t lds = static_cast<size_t>(dev) + static_cast<size_t>(g.groups) * 4;
+    dim3 grid(blocks), block(kRowsPerBlock);
+    switch (g.group) {
+    case 8:
+        if constexpr (KIND == kNib) {
+            hipLaunchKernelGGL((sdot_row_kernel<KIND, 8>), grid, block, lds, s, job0, jobs, njobs, g);
+            break;
+        }
+        [[fallthrough]];
+    case 16: hipLaunchKernelGGL((sdot_row_kernel<KIND, 16>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    case 32: hipLaunchKernelGGL((sdot_row_kernel<KIND, 32>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((sdot_row_kernel<KIND, 64>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((sdot_row_kernel<KIND, 128>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL((sdot_row_kernel<KIND, 256>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    }
+    ND_HIP(hipGetLastError());
+}
+
 int device_cus() {
     static int cus = [] {
         int dev = 0, n = 256;
@@ -676,6 +843,15 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     if (mfma) {
         if (g.kind == kNib) launch_sdot_mfma<kNib>(g, job0, jobs, njobs, blocks, batch, s);
         else launch_sdot_mfma<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
+        return;
+    }
+    // one batch row (decode): the barrier-free row kernel when the row fits the LDS stage
+    // (NEEDLE2_GPU_INT8_ROW=never keeps the windowed kernel)
+    const char *row_mode = std::getenv("NEEDLE2_GPU_INT8_ROW");
+    if (batch == 1 && g.group <= kWindow && g.windows * kWindow <= kRowMaxDev &&
+        !(row_mode && std::strcmp(row_mode, "never") == 0)) {
+        if (g.kind == kNib) launch_sdot_row<kNib>(g, job0, jobs, njobs, blocks, s);
+        else launch_sdot_row<kCrumb>(g, job0, jobs, njobs, blocks, s);
         return;
     }
     if (g.kind == kNib) launch_sdot_kind<kNib>(g, job0, jobs, njobs, blocks, batch, s);

@@ -122,3 +122,17 @@ def test_int8_plan_decode_batch(mode, monkeypatch):
         synchronize()
         for dy, e in zip(d_y, expected):
             np.testing.assert_array_equal(dy.download(np.empty((64, 512), np.float32)), e)
+
+
+@pytest.mark.parametrize("mode", ["auto", "never"])
+@pytest.mark.parametrize("bits,group,dim", [(4, 8, 1000), (4, 32, 1000), (4, 64, 4096), (4, 256, 1300), (2, 16, 1000),
+                                            (2, 32, 777), (2, 128, 2048)])
+def test_int8_single_row_kernels_bit_exact(bits, group, dim, mode, monkeypatch):
+    """Batch 1 (decode): the barrier-free row kernel (auto) and the windowed kernel (never), ragged shapes,
+    zero and one-hot inputs, bit-exact with the oracle."""
+    monkeypatch.setenv("NEEDLE2_GPU_INT8_ROW", mode)
+    packed, norms, cb, dense = example(bits, rows=300, dim=dim, group=group, seed=dim + group)
+    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    for x in special_inputs(dim, seed=group + 1):
+        np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group,
+                                                                           cb, x[None])[0])
