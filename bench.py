@@ -274,7 +274,7 @@ def main():
         for seqs in (64, 1):
             ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs)
             log(f"decode layer ({seqs} seqs, ctx 2048): eager {ms_e * 1e3:.1f} us, graph {ms_g * 1e3:.1f} us -> "
-                f"{seqs / (ms_g * 1e-3):.0f} tokens/s per layer")
+                f"{seqs / (min(ms_e, ms_g) * 1e-3):.0f} tokens/s per layer")
         return
     if args.only == "prefill":
         ms_p, g_p = bench_prefill(args.steps, args.warmup, stream)
@@ -348,11 +348,14 @@ def main():
         for seqs in (64, 1):
             log(f"decode layer: {seqs} sequence(s), ctx 2048, int8-path CQ4 projections + int8-KV attention")
             ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs)
-            extra[f"decode_b{seqs}_layer_us"] = round(ms_g * 1e3, 2)
+            ms_b = min(ms_e, ms_g)  # the faster way to issue the step (eager stream or graph replay)
+            extra[f"decode_b{seqs}_layer_us"] = round(ms_b * 1e3, 2)
+            extra[f"decode_b{seqs}_layer_mode"] = "graph" if ms_g < ms_e else "eager"
             extra[f"decode_b{seqs}_layer_eager_us"] = round(ms_e * 1e3, 2)
-            extra[f"decode_b{seqs}_tokens_per_s_per_layer"] = round(seqs / (ms_g * 1e-3), 0)
-            extra[f"decode_b{seqs}_tokens_per_s_27_layers"] = round(seqs / (27 * ms_g * 1e-3), 0)
-            log(f"decode layer b{seqs}: graph {ms_g * 1e3:.1f} us (eager {ms_e * 1e3:.1f} us) -> "
+            extra[f"decode_b{seqs}_layer_graph_us"] = round(ms_g * 1e3, 2)
+            extra[f"decode_b{seqs}_tokens_per_s_per_layer"] = round(seqs / (ms_b * 1e-3), 0)
+            extra[f"decode_b{seqs}_tokens_per_s_27_layers"] = round(seqs / (27 * ms_b * 1e-3), 0)
+            log(f"decode layer b{seqs}: eager {ms_e * 1e3:.1f} us, graph {ms_g * 1e3:.1f} us -> "
                 f"{extra[f'decode_b{seqs}_tokens_per_s_per_layer']:.0f} tokens/s per layer")
 
     cpu = None

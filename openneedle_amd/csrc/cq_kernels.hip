@@ -171,17 +171,6 @@ __device__ __forceinline__ void load_act(__amdgpu_buffer_rsrc_t act, int w, floa
                                              act, (k * kRowsPerBlock + threadIdx.x) * 4u, w * kWindow * 4, 0));
 }
 
-template <int GROUP, int H>
-__device__ __forceinline__ void wave_butterflies(float &v, int t) {
-    if constexpr (H < GROUP && H < 64) {
-        const float o = butterfly_partner<H>(v, t);
-        // lower lane: v + o = a + b; upper lane: o + (-v) = a - b (exact negation)
-        const float sv = (t & H) ? -v : v;
-        v = o + sv;
-        wave_butterflies<GROUP, H * 2>(v, t);
-    }
-}
-
 // In-kernel FWHT of the window (GROUP <= kWindow), identical butterflies to
 // the reference (stage h ascending: (a+b, a-b)), then the multiply by the
 // host-computed 1/sqrt(group). Strides below 64 are wave shuffles; larger

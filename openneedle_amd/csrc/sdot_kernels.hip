@@ -15,6 +15,7 @@
 //   value += (float(dot) * (half(norm) * cs)) * x_scale[g]
 // sequentially over g (sdot.cpp:43-44, 142-149), so outputs are bit-exact.
 #include "common.h"
+#include "wave.h"
 
 #include <hip/hip_fp16.h>
 
@@ -766,6 +767,130 @@ void launch_sdot_row(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs
     ND_HIP(hipGetLastError());
 }
 
+// ---------------------------------------------------------------------------
+// int8 MFMA path split over K, for small matrices (decode layers, any batch)
+//
+// A workgroup of kKs waves shares one (32 weight rows, 32 batch rows) tile;
+// wave w takes groups w, w + kKs, ... Each round every wave turns its group's
+// int32 accumulator into the reference's terms (float(dot) * ns) * x_scale
+// (sdot.cpp:142-149) and parks them in LDS (double-buffered by round); after
+// one barrier, the owner of each accumulator register adds the kKs terms in
+// group order. Each output is therefore value += term_g for g = 0, 1, 2, ...
+// exactly as the reference sums, and many more waves cover a small matrix.
+// ---------------------------------------------------------------------------
+constexpr int kKs = 8;
+
+template <int KIND, int GROUP, int J>
+__device__ __forceinline__ void mfma_terms(const MfmaSlot<KIND, GROUP, J> &sl, const uint32_t cent[4], float cs,
+                                           float (&term)[4 * J]) {
+    float value[4 * J];
+#pragma unroll
+    for (int r = 0; r < 4 * J; ++r) value[r] = -0.0f;  // -0 + t == t exactly, so value ends as the term
+    mfma_group(sl, cent, cs, value);
+#pragma unroll
+    for (int r = 0; r < 4 * J; ++r) term[r] = value[r];
+}
+
+template <int KIND, int GROUP, int J>
+__global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+                                                                int njobs, SdotGeom geom) {
+    constexpr int R = 4 * J;                          // accumulator registers in use
+    constexpr int kOwn = (R + kKs - 1) / kKs;         // registers each wave sums
+    __shared__ float park[2][kKs][R][64];
+    const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int rb = blockIdx.x;                        // 32-row block across the plan
+    const int blk = rb / (kRowsPerBlock / 32);
+    SdotJob J0 = job0;
+    if (njobs > 0) {
+        const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
+        int j = 0;
+        for (int k = 1; k < njobs; ++k)
+            if (cj[k].block_begin <= blk) j = k;
+        J0.codes = cj[j].codes;
+        J0.norms = cj[j].norms;
+        J0.q = cj[j].q;
+        J0.y = cj[j].y;
+        J0.rows = cj[j].rows;
+        J0.block_begin = cj[j].block_begin;
+        J0.batch = cj[j].batch;
+        J0.xst = cj[j].xst;
+    }
+    const int rows = J0.rows, batch = J0.batch;
+    const int tile = blk - J0.block_begin;
+    const int rt = (rb % (kRowsPerBlock / 32)) * 32 + i;
+    const int row = tile * kRowsPerBlock + rt;
+    const int b0 = static_cast<int>(blockIdx.y) * 32;
+    const int groups = geom.groups;
+    const int dev = geom.windows * kWindow;
+    const uint32_t cent[4] = {geom.cent[0], geom.cent[1], geom.cent[2], geom.cent[3]};
+    const float cs = geom.centroid_scale;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J0.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J0.norms + static_cast<size_t>(tile) * groups * kRowsPerBlock,
+                                                     static_cast<uint32_t>(groups) * kRowsPerBlock * 2u);
+    const int tile_rows = min(32, batch - b0);
+    const __amdgpu_buffer_rsrc_t q =
+        buffer_rsrc(reinterpret_cast<const int8_t *>(J0.q) + static_cast<size_t>(b0) * dev,
+                    static_cast<uint32_t>(tile_rows) * dev);
+    const __amdgpu_buffer_rsrc_t xst = buffer_rsrc(J0.xst, static_cast<uint32_t>(groups) * batch * 4u);
+
+    float value[kOwn];
+#pragma unroll
+    for (int k = 0; k < kOwn; ++k) value[k] = 0.0f;
+    const int rounds = (groups + kKs - 1) / kKs;
+    MfmaSlot<KIND, GROUP, J> cur, nxt;
+    mfma_load(cur, codes, norms, q, xst, w, rt, i, h, dev, batch, b0);
+    for (int r = 0; r < rounds; ++r) {
+        // next round's group (past the last group: zeros, or data that is never used)
+        mfma_load(nxt, codes, norms, q, xst, (r + 1) * kKs + w, rt, i, h, dev, batch, b0);
+        float term[R];
+        mfma_terms(cur, cent, cs, term);
+#pragma unroll
+        for (int k = 0; k < R; ++k) park[r & 1][w][k][lane] = term[k];
+        __syncthreads();
+        const int live = min(kKs, groups - r * kKs);  // groups of this round (uniform)
+#pragma unroll
+        for (int k = 0; k < kOwn; ++k) {
+            const int reg = w + k * kKs;
+            if (reg < R)
+                for (int src = 0; src < live; ++src) value[k] = value[k] + park[r & 1][src][reg][lane];
+        }
+        cur = nxt;
+    }
+    if (row < rows) {
+#pragma unroll
+        for (int k = 0; k < kOwn; ++k) {
+            const int reg = w + k * kKs;
+            if (reg >= R) continue;
+            const int m = b0 + 8 * (reg / 4) + 4 * h + (reg % 4);
+            if (m < batch) ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * rows + row] = value[k];
+        }
+    }
+}
+
+template <int KIND, int J>
+void launch_sdot_ks_j(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                      hipStream_t s) {
+    dim3 grid(blocks * (kRowsPerBlock / 32), (batch + 31) / 32), block(kKs * 64);
+    switch (g.group) {
+    case 32: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 32, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 64, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 128, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 256, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    }
+    ND_HIP(hipGetLastError());
+}
+
+template <int KIND>
+void launch_sdot_ks(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                    hipStream_t s) {
+    if (batch <= 8) launch_sdot_ks_j<KIND, 1>(g, job0, jobs, njobs, blocks, batch, s);
+    else if (batch <= 16) launch_sdot_ks_j<KIND, 2>(g, job0, jobs, njobs, blocks, batch, s);
+    else launch_sdot_ks_j<KIND, 4>(g, job0, jobs, njobs, blocks, batch, s);
+}
+
 int device_cus() {
     static int cus = [] {
         int dev = 0, n = 256;
@@ -798,6 +923,43 @@ void launch_sdot_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     run(1, [&](int b0, int b1) { launch_sdot_bt<KIND, 1>(g, job0, jobs, njobs, blocks, b0, b1, s); });
 }
 
+// Prepare for groups of 8 .. 64 positions, one pass without LDS: lane t of
+// block (segment, vector) owns position 256 * segment + t; the group FWHT
+// runs as in-wave butterflies (the reference's stage order and operands),
+// the group absmax as an in-wave max, then the reference's quantiser
+// (sdot.cpp:56-81: scale = absmax / 127, 1 for an all-zero group, absmax if
+// the quotient underflows; q = clamp(rint(x / scale), +-127) with IEEE
+// division), stored in the permuted order the GEMV decode expects. Same
+// values as sdot_prepare_kernel, bit for bit.
+template <int GROUP>
+__global__ __launch_bounds__(256) void sdot_prepare_wave_kernel(const float *__restrict__ x0,
+                                                                const float *const *__restrict__ xptr, int batch,
+                                                                int in, int padded, int dev, float scale, int kind,
+                                                                int8_t *__restrict__ q, float *__restrict__ xs,
+                                                                float *__restrict__ xst, int groups) {
+    const int v = blockIdx.y;
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    const int t = threadIdx.x & 63;
+    const float *xv = (xptr ? xptr[v / batch] : x0) + static_cast<size_t>(v % batch) * in;
+    float r = p < in ? xv[p] : 0.0f;
+    wave_butterflies<GROUP, 1>(r, t);
+    r = r * scale;
+    const float absmax = group_max<GROUP>(fabsf(r), t);
+    int8_t out = 0;
+    if (p < padded) {
+        float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
+        if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
+        if (p % GROUP == 0) {
+            xs[static_cast<size_t>(v) * groups + p / GROUP] = sc;
+            if (xst) xst[(static_cast<size_t>(v / batch) * groups + p / GROUP) * batch + v % batch] = sc;
+        }
+        float val = rintf(r / sc);
+        val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
+        out = static_cast<int8_t>(val);
+    }
+    if (p < dev) q[static_cast<size_t>(v) * dev + permuted_index(kind, p)] = out;
+}
+
 }  // namespace
 
 bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, int nvec, int in, int padded,
@@ -805,6 +967,21 @@ bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, i
     if (group > kPrepareMaxGroup) return false;
     ND_CHECK(group >= 8 && (group & (group - 1)) == 0, "int8 prepare: group must be a power of two >= 8");
     if (nvec <= 0) return true;
+    if (group <= 64) {
+        dim3 grid(dev / 256, nvec), block(256);
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, block, 0, s, x0, xptr, batch, in, padded, dev, scale, kind,
+                               reinterpret_cast<int8_t *>(q), xs, xst, padded / group);
+        };
+        switch (group) {
+        case 8: go(sdot_prepare_wave_kernel<8>); break;
+        case 16: go(sdot_prepare_wave_kernel<16>); break;
+        case 32: go(sdot_prepare_wave_kernel<32>); break;
+        default: go(sdot_prepare_wave_kernel<64>); break;
+        }
+        ND_HIP(hipGetLastError());
+        return true;
+    }
     const int seg = group > kPrepareMinSeg ? group : kPrepareMinSeg;
     dim3 grid((dev + seg - 1) / seg, nvec), block(256);
     hipLaunchKernelGGL(sdot_prepare_kernel, grid, block, seg * sizeof(float), s, x0, xptr, batch, in, padded, dev,
@@ -836,6 +1013,20 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     // NEEDLE2_GPU_INT8_MFMA=always / never overrides the choice (auto).
     const long mfma_waves = static_cast<long>(blocks) * (kRowsPerBlock / 32) * ((batch + 31) / 32);
     const char *mode = std::getenv("NEEDLE2_GPU_INT8_MFMA");
+    // Small matrices (fewer 32 x 32 tiles than SIMDs; decode projections) of
+    // any batch split K over kKs waves per tile (NEEDLE2_GPU_INT8_KSPLIT=
+    // always / never overrides; the transposed scales must be present, as
+    // every plan and handle provides them).
+    const char *ks_mode = std::getenv("NEEDLE2_GPU_INT8_KSPLIT");
+    const bool ks_ok = g.group >= 32 && g.group <= kWindow && g.groups >= 2;
+    bool ks = ks_ok && mfma_waves < 4L * device_cus();
+    if (ks_mode && std::strcmp(ks_mode, "always") == 0) ks = ks_ok;
+    if (ks_mode && std::strcmp(ks_mode, "never") == 0) ks = false;
+    if (ks) {
+        if (g.kind == kNib) launch_sdot_ks<kNib>(g, job0, jobs, njobs, blocks, batch, s);
+        else launch_sdot_ks<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
+        return;
+    }
     const bool mfma_ok = batch >= 2 && g.group >= 32 && g.group <= kWindow;
     bool mfma = mfma_ok && batch >= 8 && mfma_waves >= 2L * 4 * device_cus();
     if (mode && std::strcmp(mode, "always") == 0) mfma = mfma_ok;

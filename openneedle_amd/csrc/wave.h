@@ -28,6 +28,31 @@ __device__ __forceinline__ float butterfly_partner(float v, int t) {
     }
 }
 
+// In-wave FWHT stages of stride H, 2H, ... < min(GROUP, 64) on lane t's
+// value: the reference's butterfly (a + b, a - b) with the same operands
+// (cq.cpp:30-46); the lower lane adds its partner, the upper lane adds the
+// exactly negated own value, so both results are bit-identical.
+template <int GROUP, int H>
+__device__ __forceinline__ void wave_butterflies(float &v, int t) {
+    if constexpr (H < GROUP && H < 64) {
+        const float o = butterfly_partner<H>(v, t);
+        const float sv = (t & H) ? -v : v;
+        v = o + sv;
+        wave_butterflies<GROUP, H * 2>(v, t);
+    }
+}
+
+// Max over aligned groups of G lanes (G <= 64), result in every lane of the group.
+template <int G, int H = 1>
+__device__ __forceinline__ float group_max(float v, int t) {
+    if constexpr (H < G) {
+        v = fmaxf(v, butterfly_partner<H>(v, t));
+        return group_max<G, H * 2>(v, t);
+    } else {
+        return v;
+    }
+}
+
 // Max / sum over the 64 lanes, result in every lane (xor butterflies).
 __device__ __forceinline__ float wave_max(float v, int t) {
     v = fmaxf(v, butterfly_partner<1>(v, t));

@@ -84,7 +84,7 @@ def test_int8_plan_many_matrices():
         np.testing.assert_array_equal(dy.download(np.empty((2, m.shape[0]), np.float32)), e)
 
 
-@pytest.mark.parametrize("mode", ["always", "never"])
+@pytest.mark.parametrize("mode", ["always", "never", "ksplit"])
 @pytest.mark.parametrize("bits,group,batch", [(4, 32, 3), (4, 32, 9), (4, 32, 17), (4, 32, 33), (4, 32, 64),
                                               (4, 64, 40), (4, 128, 12), (4, 256, 5), (2, 32, 8), (2, 32, 33),
                                               (2, 64, 20)])
@@ -92,7 +92,11 @@ def test_int8_batched_tiles_bit_exact(bits, group, batch, mode, monkeypatch):
     """Batches run on int8 MFMA (tiles of 32 batch rows: ragged last tile) or on v_dot4 batch tiles, forced
     either way here (the library picks by size otherwise); 300 ragged weight rows, zero / one-hot activation
     rows: bit-exact with the oracle."""
-    monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", mode)
+    if mode == "ksplit":  # K split over 8 waves per tile (small-matrix path)
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "always")
+    else:
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "never")
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", mode)
     packed, norms, cb, dense = example(bits, rows=300, dim=1000, group=group, seed=7 * batch + group)
     q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
     x = activations((batch, 1000), seed=batch)
@@ -124,13 +128,19 @@ def test_int8_plan_decode_batch(mode, monkeypatch):
             np.testing.assert_array_equal(dy.download(np.empty((64, 512), np.float32)), e)
 
 
-@pytest.mark.parametrize("mode", ["auto", "never"])
+@pytest.mark.parametrize("mode", ["auto", "never", "ksplit"])
 @pytest.mark.parametrize("bits,group,dim", [(4, 8, 1000), (4, 32, 1000), (4, 64, 4096), (4, 256, 1300), (2, 16, 1000),
                                             (2, 32, 777), (2, 128, 2048)])
 def test_int8_single_row_kernels_bit_exact(bits, group, dim, mode, monkeypatch):
     """Batch 1 (decode): the barrier-free row kernel (auto) and the windowed kernel (never), ragged shapes,
     zero and one-hot inputs, bit-exact with the oracle."""
-    monkeypatch.setenv("NEEDLE2_GPU_INT8_ROW", mode)
+    if mode == "ksplit":
+        if group < 32:
+            pytest.skip("the K-split path takes groups of 32 .. 256")
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "always")
+    else:
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "never")
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_ROW", mode)
     packed, norms, cb, dense = example(bits, rows=300, dim=dim, group=group, seed=dim + group)
     q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
     for x in special_inputs(dim, seed=group + 1):
