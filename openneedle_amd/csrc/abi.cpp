@@ -131,8 +131,8 @@ void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s
 void CqHandle::gemm_device(const float *d_x, float *d_y, int m_rows, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
     if (m_rows <= 0) return;
     ND_CHECK(m.kind == kNib, "prefill GEMM: 4-bit (CQ4 / CQ3) codes only");
-    ND_CHECK(size_t(m_rows) * m.dev * 2 < (size_t(1) << 31), "prefill GEMM: m * padded input must be < 2^30");
-    st.xh.reserve(size_t(m_rows) * m.dev);
+    ND_CHECK(prefill_xf_halves(m_rows, m.dev) * 2 < (size_t(1) << 31), "prefill GEMM: m * padded input must be < 2^30");
+    st.xh.reserve(prefill_xf_halves(m_rows, m.dev));
     launch_prefill_transform(d_x, m_rows, m.in, m.padded, m.dev, m.group, m.scale, st.xh.p, s);
     uint16_t cbh[16];
     for (int i = 0; i < 16; ++i) cbh[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(m.lut[i]));

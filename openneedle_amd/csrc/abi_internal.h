@@ -10,9 +10,11 @@ void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stri
 
 void launch_copy(const void *src, void *dst, size_t bytes, hipStream_t s);
 
+// fp16 activations of the prefill GEMM in MFMA fragment order: m rounded up to 32 rows
+size_t prefill_xf_halves(int m, int dev);
 void launch_prefill_transform(const float *x, int m, int in, int padded, int dev, int group, float scale,
-                              _Float16 *xh, hipStream_t s);
-void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes, const uint16_t *norms, int rows, const _Float16 *xh,
+                              _Float16 *xf, hipStream_t s);
+void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes, const uint16_t *norms, int rows, const _Float16 *xf,
                          int m, int dev, int padded, const uint16_t *cb_half, float *y, hipStream_t s);
 
 // Runs f, converting exceptions into -1 plus the thread-local message. The
