@@ -7,15 +7,20 @@
 //    each 16-byte slice is one lane's operand of one v_mfma_f32_32x32x16_f16,
 //    so the GEMM loads X fragments straight from memory (1 KiB per wave load).
 // 2. prefill_gemm_kernel: 128 x 128 output tile per workgroup, K in steps of
-//    64 positions, two kinds of waves. Waves 0-3 (one per SIMD) each own a
-//    64 x 64 sub-tile: X fragments from memory two steps ahead, weight
-//    fragments from LDS, 16 MFMAs per step. Waves 4-7 (one per SIMD) load
-//    the 4-bit codes three steps ahead and dequantize the 128 x 64 weight
-//    tile of the next step into the other LDS buffer: codes -> fp16 codebook
-//    values through v_perm byte tables, times the fp16 group norm. One
-//    barrier per step; on each SIMD the dequantization VALU work issues while
-//    the MFMA wave's matrix instructions run. Tiles are ordered so that the
-//    M-tiles of one N-tile run on the same XCD and share its L2.
+//    64 positions, two kinds of waves. Waves 0-3 (one per SIMD) each own 64
+//    rows x 128 columns over half of the 16-position slices of every step
+//    (the two K halves are summed through LDS at the end): X fragments from
+//    memory two steps ahead, each loaded once per workgroup; weight fragments
+//    from LDS, each read by two waves; 16 MFMAs per step. Waves 4-7 (one per SIMD) load
+//    the 4-bit codes five steps ahead and dequantize the 128 x 64 weight
+//    tile two steps ahead into a ring of three LDS buffers: codes -> fp16
+//    codebook values times the fp16 group norm. One barrier per step; on each
+//    SIMD the dequantization VALU work issues while the MFMA wave's matrix
+//    instructions run. Tiles are ordered so that the
+//    M-tiles of one N-tile run on the same XCD and share its L2. The
+//    codebook lookup reads a 256-entry table of code pairs (two fp16 values
+//    per byte of codes) from LDS, one private column per lane so the reads
+//    are conflict-free: 4 v_perm + 4 ds_read_b32 + 4 v_pk_mul_f16 per 8 codes.
 //
 // Rounding: X and the weights cb*norm are fp16 (two roundings for the
 // weight), products and sums are fp32 in the MFMA; the result agrees with the
@@ -28,22 +33,19 @@ namespace nd {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16x __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
 constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kGemmThreads = 512;  // waves 0-3: MFMA (2 x 2 of 64 x 64); waves 4-7: weight dequantization
+constexpr int kGemmThreads = 512;  // waves 0-3: MFMA (64 rows x 128 columns x half of K each); 4-7: dequantization
 constexpr int kLdsRow = 72;        // halves per LDS weight row: 64 + 8 padding (conflict-free 16-byte accesses)
 constexpr int kFragBytes = 1024;   // one operand fragment: 64 lanes x 8 halves
 constexpr int kStepBytes = 4 * kFragBytes;  // the four 16-position slices of one 64-position step
 
-// Half e (0..7) of a lane's 8-half slice holds position 8 d + kCidx(e) of its
-// code dword d: the order dequant8 produces (0,2,4,6,1,3,5,7).
-__host__ __device__ constexpr int cidx(int e) { return (e & 3) * 2 + (e >> 2); }
-
 // FWHT as transform_kernel, fp16 output in fragment order: for 32-row block
 // rb, step s and slice kk, lane l holds row 32 rb + l % 32 and positions
-// 64 s + 32 (l / 32) + 8 kk + cidx(e). Rows m .. m32 - 1 are written as zeros.
+// 64 s + 32 (l / 32) + 8 kk + e, e = 0..7. Rows m .. m32 - 1 are written as zeros.
 __global__ __launch_bounds__(256) void prefill_transform_kernel(const float *__restrict__ x, int m, int in, int padded,
                                                                 int dev, int group, float scale,
                                                                 _Float16 *__restrict__ xf, int seg) {
@@ -73,7 +75,7 @@ __global__ __launch_bounds__(256) void prefill_transform_kernel(const float *__r
         uint32_t w[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int c0 = cidx(2 * q), c1 = cidx(2 * q + 1);
+            const int c0 = 2 * q, c1 = 2 * q + 1;
             const _Float16 h0 = static_cast<_Float16>(p0 + c0 < padded ? buf[8 * u + c0] * scale : 0.0f);
             const _Float16 h1 = static_cast<_Float16>(p0 + c1 < padded ? buf[8 * u + c1] * scale : 0.0f);
             w[q] = uint32_t(__builtin_bit_cast(uint16_t, h0)) | (uint32_t(__builtin_bit_cast(uint16_t, h1)) << 16);
@@ -84,35 +86,11 @@ __global__ __launch_bounds__(256) void prefill_transform_kernel(const float *__r
     }
 }
 
-// Byte lookups in a 16-entry table T (4 dwords) for the 4 byte-wide indices
-// of a code vector: i7 = idx & 7 per byte, sel picks the upper 8 entries.
-struct LutIdx {
-    uint32_t i7, sel;
-};
-__device__ __forceinline__ LutIdx lut_idx(uint32_t idx) {
-    return {idx & 0x07070707u, ((idx >> 1) & 0x04040404u) | 0x03020100u};
-}
-__device__ __forceinline__ uint32_t lut16(LutIdx x, const uint32_t (&T)[4]) {
-    const uint32_t lo = __builtin_amdgcn_perm(T[1], T[0], x.i7), hi = __builtin_amdgcn_perm(T[3], T[2], x.i7);
-    return __builtin_amdgcn_perm(hi, lo, x.sel);
-}
-
-// 8 four-bit codes (LSB first) -> 8 fp16 codebook values times the fp16 norm
-// (both halves of `norm2`), in the order 0,2,4,6,1,3,5,7 (the activations are
-// stored in the same order), which saves re-interleaving.
-__device__ __forceinline__ void dequant8(uint32_t w, const uint32_t (&LO)[4], const uint32_t (&HI)[4], uint32_t norm2,
-                                         uint32_t (&out)[4]) {
-    const LutIdx e = lut_idx(w & 0x0F0F0F0Fu), o = lut_idx((w >> 4) & 0x0F0F0F0Fu);  // codes 0,2,4,6 / 1,3,5,7
-    const uint32_t le = lut16(e, LO), he = lut16(e, HI), lo = lut16(o, LO), ho = lut16(o, HI);
-    const uint32_t v[4] = {__builtin_amdgcn_perm(he, le, 0x05010400u),   // codes 0 | 2
-                           __builtin_amdgcn_perm(he, le, 0x07030602u),   // 4 | 6
-                           __builtin_amdgcn_perm(ho, lo, 0x05010400u),   // 1 | 3
-                           __builtin_amdgcn_perm(ho, lo, 0x07030602u)};  // 5 | 7
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 n = __builtin_bit_cast(h2, norm2);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) out[q] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v[q]) * n);
-}
+// Code-pair table in LDS: entry e (a byte of codes: low nibble first) holds
+// fp16 cb[e & 15] | cb[e >> 4] << 16. Each lane reads its own column (dword
+// 64 e + lane), so a wave's 64 lookups hit 64 different banks.
+constexpr int kPairEntries = 256;
+constexpr int kPairWords = kPairEntries * 64;
 
 struct GemmArgs {
     const _Float16 *xf;  // X in fragment order (prefill_transform_kernel), rb_count blocks of 32 rows
@@ -120,7 +98,7 @@ struct GemmArgs {
     const uint16_t *norms;
     float *y;  // [m][rows]
     int m, rb_count, rows, chunks, groups, group_shift, xsteps, ksteps, mtiles, tiles;
-    uint32_t lo[4], hi[4];  // fp16 codebook, low / high byte tables
+    uint16_t cb[16];  // fp16 codebook
 };
 
 // Tile of this workgroup. Workgroups go to the 8 XCDs round robin; giving
@@ -132,24 +110,29 @@ __device__ __forceinline__ int gemm_tile(const GemmArgs &g) {
 }
 
 // ---- MFMA waves ----------------------------------------------------------
+// Wave (mi, ki) = (wave / 2, wave % 2) owns rows 64 mi .. + 64 and all 128
+// columns of the tile over slices kk = 2 ki, 2 ki + 1 of every step (half of
+// K): every X fragment is loaded once per workgroup and every weight
+// fragment is read by two waves (the vector L1 delivers about a quarter of
+// the LDS bandwidth, and LDS is shared with the dequantization waves).
 
 struct AFrags {
-    u32x4 v[2][4];  // [32-row block i][slice kk]
+    u32x4 v[2][2];  // [32-row block i][slice kk - 2 ki]
 };
 
 struct APtrs {
     __amdgpu_buffer_rsrc_t x;
-    uint32_t xv[2];  // lane offsets of the wave's two row blocks
+    uint32_t xv[2];  // lane offsets of the wave's two row blocks (slice 2 ki)
 };
 
-__device__ __forceinline__ APtrs a_ptrs(const GemmArgs &g, int rb0, int lane) {
+__device__ __forceinline__ APtrs a_ptrs(const GemmArgs &g, int rb0, int ki, int lane) {
     const uint32_t block = static_cast<uint32_t>(g.xsteps) * kStepBytes;
     // blocks past the last read zero (scalar: a VALU clamp would make the descriptor divergent)
-    const int left = __builtin_amdgcn_readfirstlane(min(2, max(0, g.rb_count - rb0)));
+    const int live = __builtin_amdgcn_readfirstlane(min(2, max(0, g.rb_count - rb0)));
     APtrs p;
-    p.x = buffer_rsrc(g.xf + static_cast<size_t>(rb0) * g.xsteps * (kStepBytes / 2), left * block);
-    p.xv[0] = lane * 16u;
-    p.xv[1] = lane * 16u + block;
+    p.x = buffer_rsrc(g.xf + static_cast<size_t>(rb0) * g.xsteps * (kStepBytes / 2), live * block);
+    p.xv[0] = lane * 16u + ki * 2 * kFragBytes;
+    p.xv[1] = p.xv[0] + block;
     return p;
 }
 
@@ -158,45 +141,54 @@ __device__ __forceinline__ void a_load(AFrags &a, const APtrs &p, int s) {
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-            a.v[i][kk] = __builtin_amdgcn_raw_buffer_load_b128(p.x, p.xv[i] + kk * kFragBytes, so, 0);
+        for (int k = 0; k < 2; ++k)
+            a.v[i][k] = __builtin_amdgcn_raw_buffer_load_b128(p.x, p.xv[i] + k * kFragBytes, so, 0);
 }
 
-struct BFrags {
-    h8 v[4][2];  // [slice kk][32-column block j]
+// Weight fragments of one slice for the four 32-column blocks: lane l holds
+// weight row l % 32 of block j, slice kk of chunk l / 32.
+struct BSlice {
+    h8 v[4];
 };
 
-// Weight fragments of one step from LDS buffer `Bs`: lane l holds weight row
-// l % 32 of the block, slice kk of chunk l / 32.
-__device__ __forceinline__ void b_read(BFrags &b, const _Float16 *Bs, int wn, int lane) {
-    const _Float16 *B = Bs + (wn * 64 + (lane & 31)) * kLdsRow + (lane >> 5) * 32;
+__device__ __forceinline__ void b_slice(BSlice &b, const _Float16 *Bs, int kk, int lane) {
+    const _Float16 *B = Bs + (lane & 31) * kLdsRow + (lane >> 5) * 32 + kk * 8;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
+    for (int j = 0; j < 4; ++j) b.v[j] = *reinterpret_cast<const h8 *>(B + j * 32 * kLdsRow);
+}
+
+__device__ __forceinline__ void mma_slice(const AFrags &x, const BSlice &b, int k, f16x (&acc)[2][4]) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) b.v[kk][j] = *reinterpret_cast<const h8 *>(B + j * 32 * kLdsRow + kk * 8);
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8, x.v[i][k]), b.v[j], acc[i][j], 0,
+                                                               0, 0);
 }
 
 // One K step of an MFMA wave (J = c % 6): X fragments of step c + 2 are
-// requested (ring of three register sets), the weight fragments of step
-// c + 1 are read from LDS buffer (c + 1) % 3 (complete since the previous
-// barrier), and step c is computed from registers only.
+// requested (ring of three register sets); each slice's weight fragments are
+// read one slice ahead of its MFMAs (the first slice of step c + 1 from LDS
+// buffer (c + 1) % 3, complete since the previous barrier), so LDS latency
+// hides behind eight MFMAs. Scheduling barriers keep the reads where they are.
 template <int J>
-__device__ __forceinline__ void mma_step(AFrags (&a)[3], BFrags (&b)[2], const GemmArgs &g, const APtrs &p, int c,
-                                         const _Float16 (&Bs)[3][kBN * kLdsRow], f16x (&acc)[2][2], int wn,
+__device__ __forceinline__ void mma_step(AFrags (&a)[3], BSlice (&b)[2], const GemmArgs &g, const APtrs &p, int c,
+                                         const _Float16 (&Bs)[3][kBN * kLdsRow], f16x (&acc)[2][4], int ki,
                                          int lane) {
     a_load(a[(J + 2) % 3], p, min(c + 2, g.ksteps - 1));  // clamped: past the end it repeats the last step
-    b_read(b[(J + 1) & 1], Bs[(J + 1) % 3], wn, lane);    // past the end: never used
-    const AFrags &x = a[J % 3];
-    const BFrags &w = b[J & 1];
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h8, x.v[i][kk]), w.v[kk][j],
-                                                                   acc[i][j], 0, 0, 0);
-    __syncthreads();
+    b_slice(b[1], Bs[J % 3], 2 * ki + 1, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_slice(a[J % 3], b[0], 0, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    b_slice(b[0], Bs[(J + 1) % 3], 2 * ki, lane);  // past the end: never used
+    __builtin_amdgcn_sched_barrier(0);
+    mma_slice(a[J % 3], b[1], 1, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    // Barrier without draining the four prefetch reads: LDS reads complete in
+    // order, so lgkmcnt(4) retires every read of buffer c % 3 (rewritten in
+    // step c + 1) while the reads of buffer (c + 1) % 3 (rewritten in step
+    // c + 2) stay in flight. This wave writes no LDS.
+    asm volatile("s_waitcnt lgkmcnt(4)\n\ts_barrier" ::: "memory");
 }
 
 // ---- dequantization waves ------------------------------------------------
@@ -243,35 +235,109 @@ __device__ __forceinline__ void code_load(CodeRegs<NG> &r, const GemmArgs &g, co
     for (int k = 0; k < NG; ++k) r.norm[k] = __builtin_amdgcn_raw_buffer_load_b16(p.n, p.nv[k], so, 0);
 }
 
-// Weight row `row`, chunk `ch` of one step -> LDS slots 32 ch .. + 32 of the row.
+// Code-pair lookups of one (weight row, chunk) of a step: 32 codes -> 16
+// dwords of two fp16 codebook values, positions in order.
 template <int NG>
-__device__ __forceinline__ void dequant_store(const CodeRegs<NG> &r, const GemmArgs &g, _Float16 *Bs, int row,
-                                              int ch) {
+__device__ __forceinline__ void table_reads(uint32_t (&v)[16], const CodeRegs<NG> &r, const uint32_t *pairs,
+                                            uint32_t lane4) {
     const uint32_t c[4] = {r.code.x, r.code.y, r.code.z, r.code.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            // byte offset 256 * (byte k of code dword q) + 4 * lane: one v_perm (selector 0x0c gives zero bytes)
+            const uint32_t off = __builtin_amdgcn_perm(c[q], lane4, 0x0c0c0400u + (k << 8));
+            v[q * 4 + k] = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const char *>(pairs) + off);
+        }
+}
+
+// The looked-up values times the fp16 group norm -> LDS slots 32 ch .. + 32
+// of weight row `row`.
+template <int NG>
+__device__ __forceinline__ void scale_store(const uint32_t (&v)[16], const CodeRegs<NG> &r, _Float16 *Bs, int row,
+                                            int ch) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     u32x4 *d = reinterpret_cast<u32x4 *>(Bs + row * kLdsRow + ch * 32);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const uint32_t nm = r.norm[q * NG / 4];
+        const h2 n = __builtin_bit_cast(h2, nm | (nm << 16));
         uint32_t w[4];
-        dequant8(c[q], g.lo, g.hi, nm | (nm << 16), w);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, v[q * 4 + k]) * n);
         d[q] = u32x4{w[0], w[1], w[2], w[3]};
     }
 }
 
+// Barrier of the dequantization waves. The last 16 LDS operations of the step
+// are table reads issued after its four weight writes; LDS operations
+// complete in order, so lgkmcnt(15) retires the writes (read by the MFMA
+// waves after this barrier) and leaves the reads in flight across it.
+__device__ __forceinline__ void deq_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(15)\n\ts_barrier" ::: "memory");
+}
+
 // One K step of a dequantization wave (J = c % 6): codes of step c + 5 are
-// requested (ring of six), step c + 2 is dequantized into LDS buffer
-// (c + 2) % 3, which the MFMA waves last read during step c - 2.
+// requested (ring of six), the table values of step c + 2 (read during step
+// c - 1) are scaled into LDS buffer (c + 2) % 3, which the MFMA waves last
+// read during step c - 1, and the table reads of step c + 3 are issued, so
+// their latency hides behind a whole step.
 template <int NG, int J>
-__device__ __forceinline__ void deq_step(CodeRegs<NG> (&r)[6], const GemmArgs &g, const DPtrs &p, int c,
+__device__ __forceinline__ void deq_step(CodeRegs<NG> (&r)[6], uint32_t (&v)[16], const GemmArgs &g,
+                                         const DPtrs &p, int c, const uint32_t *pairs, uint32_t lane4,
                                          _Float16 (&Bs)[3][kBN * kLdsRow], int row, int ch) {
     code_load(r[(J + 5) % 6], g, p, min(c + 5, g.ksteps - 1));
-    if (c + 2 < g.ksteps) dequant_store(r[(J + 2) % 6], g, Bs[(J + 2) % 3], row, ch);
-    __syncthreads();
+    if (c + 2 < g.ksteps) scale_store(v, r[(J + 2) % 6], Bs[(J + 2) % 3], row, ch);
+    table_reads(v, r[(J + 3) % 6], pairs, lane4);  // past the end: clamped codes, never stored
+    deq_barrier();
+}
+
+// Row block I of an MFMA wave's accumulators -> its slots of the park area
+// (lane-interleaved 16-byte vectors, conflict-free).
+template <int I>
+__device__ __forceinline__ void park_block(const f16x (&acc)[2][4], u32x4 *park) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            park[((I * 4 + j) * 4 + q) * 64] = __builtin_bit_cast(
+                u32x4, f32x4{acc[I][j][4 * q], acc[I][j][4 * q + 1], acc[I][j][4 * q + 2], acc[I][j][4 * q + 3]});
+}
+
+// Row block I (rows m_base + 32 I ..) of the tile: own partial sums plus the
+// parked ones of the other K half, stored to Y.
+template <int I>
+__device__ __forceinline__ void store_block(const f16x (&acc)[2][4], const u32x4 *park, const GemmArgs &g,
+                                            int m_base, int n0, int lane) {
+    // C fragment: lane l holds column l % 32, rows 8 (e / 4) + 4 (l / 32) + e % 4
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + j * 32 + (lane & 31);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 o = __builtin_bit_cast(f32x4, park[((I * 4 + j) * 4 + q) * 64]);
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const int e = 4 * q + e4;
+                const int m = m_base + I * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (n < g.rows && m < g.m) g.y[static_cast<size_t>(m) * g.rows + n] = acc[I][j][e] + o[e4];
+            }
+        }
+    }
 }
 
 template <int NG>
 __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(16))) _Float16 Bs[3][kBN * kLdsRow];
+    __shared__ __attribute__((aligned(16))) uint32_t pairs[kPairWords];
+    // all 512 threads fill the code-pair table (16 x 16-byte stores each)
+    for (int i = threadIdx.x; i < kPairWords / 4; i += kGemmThreads) {
+        const int e = i >> 4;  // 16 vectors of 4 lanes per entry
+        const uint32_t v = uint32_t(g.cb[e & 15]) | (uint32_t(g.cb[e >> 4]) << 16);
+        reinterpret_cast<u32x4 *>(pairs)[i] = u32x4{v, v, v, v};
+    }
+    __syncthreads();
     const int tile = gemm_tile(g);
     const int n0 = (tile / g.mtiles) * kBN, m0 = (tile % g.mtiles) * kBM;
     const int lane = threadIdx.x & 63;
@@ -280,70 +346,74 @@ __global__ __launch_bounds__(kGemmThreads) void prefill_gemm_kernel(GemmArgs g) 
     // Every step ends in one barrier on both sides; the loops run in sixes so
     // that every ring index is a compile-time constant.
     if (wave < 4) {
-        const int wm = wave >> 1, wn = wave & 1;  // this wave: rows 64 wm.., columns 64 wn..
-        const APtrs p = a_ptrs(g, m0 / 32 + 2 * wm, lane);
-        f16x acc[2][2];
+        const int mi = wave >> 1, ki = wave & 1;
+        const APtrs p = a_ptrs(g, m0 / 32 + 2 * mi, ki, lane);
+        f16x acc[2][4];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] = f16x{};
+            for (int j = 0; j < 4; ++j) acc[i][j] = f16x{};
         AFrags a[3];
-        BFrags b[2];
+        BSlice b[2];
         a_load(a[0], p, 0);
         a_load(a[1], p, min(1, last));
         __syncthreads();  // weights of steps 0 and 1 are in LDS
-        b_read(b[0], Bs[0], wn, lane);
+        b_slice(b[0], Bs[0], 2 * ki, lane);
         int c = 0;
         for (; c + 6 <= g.ksteps; c += 6) {
-            mma_step<0>(a, b, g, p, c, Bs, acc, wn, lane);
-            mma_step<1>(a, b, g, p, c + 1, Bs, acc, wn, lane);
-            mma_step<2>(a, b, g, p, c + 2, Bs, acc, wn, lane);
-            mma_step<3>(a, b, g, p, c + 3, Bs, acc, wn, lane);
-            mma_step<4>(a, b, g, p, c + 4, Bs, acc, wn, lane);
-            mma_step<5>(a, b, g, p, c + 5, Bs, acc, wn, lane);
+            mma_step<0>(a, b, g, p, c, Bs, acc, ki, lane);
+            mma_step<1>(a, b, g, p, c + 1, Bs, acc, ki, lane);
+            mma_step<2>(a, b, g, p, c + 2, Bs, acc, ki, lane);
+            mma_step<3>(a, b, g, p, c + 3, Bs, acc, ki, lane);
+            mma_step<4>(a, b, g, p, c + 4, Bs, acc, ki, lane);
+            mma_step<5>(a, b, g, p, c + 5, Bs, acc, ki, lane);
         }
-        if (c < g.ksteps) mma_step<0>(a, b, g, p, c, Bs, acc, wn, lane);
-        if (c + 1 < g.ksteps) mma_step<1>(a, b, g, p, c + 1, Bs, acc, wn, lane);
-        if (c + 2 < g.ksteps) mma_step<2>(a, b, g, p, c + 2, Bs, acc, wn, lane);
-        if (c + 3 < g.ksteps) mma_step<3>(a, b, g, p, c + 3, Bs, acc, wn, lane);
-        if (c + 4 < g.ksteps) mma_step<4>(a, b, g, p, c + 4, Bs, acc, wn, lane);
-        // C fragment: lane l holds column l % 32, rows 8 (e / 4) + 4 (l / 32) + e % 4
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + j * 32 + (lane & 31);
-            if (n >= g.rows) continue;
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int m = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                    if (m < g.m) g.y[static_cast<size_t>(m) * g.rows + n] = acc[i][j][e];
-                }
-        }
+        if (c < g.ksteps) mma_step<0>(a, b, g, p, c, Bs, acc, ki, lane);
+        if (c + 1 < g.ksteps) mma_step<1>(a, b, g, p, c + 1, Bs, acc, ki, lane);
+        if (c + 2 < g.ksteps) mma_step<2>(a, b, g, p, c + 2, Bs, acc, ki, lane);
+        if (c + 3 < g.ksteps) mma_step<3>(a, b, g, p, c + 3, Bs, acc, ki, lane);
+        if (c + 4 < g.ksteps) mma_step<4>(a, b, g, p, c + 4, Bs, acc, ki, lane);
+        // Sum of the two K halves: each wave parks the row block that the
+        // other half stores (over the code-pair table, no longer read), then
+        // adds the parked partial sums to its own block (a two-term fp32 sum,
+        // the same whichever side adds) and stores it: all four MFMA waves
+        // store one 32-row block each.
+        u32x4 *park = reinterpret_cast<u32x4 *>(pairs) + mi * 32 * 64 + lane;
+        if (ki == 0) park_block<1>(acc, park);
+        else park_block<0>(acc, park);
+        __syncthreads();
+        if (ki == 0) store_block<0>(acc, park, g, m0 + mi * 64, n0, lane);
+        else store_block<1>(acc, park, g, m0 + mi * 64, n0, lane);
     } else {
         const int u = threadIdx.x - 256;
         const int row = u & (kBN - 1), ch = u >> 7;  // weight row of the tile, chunk of the step
         const DPtrs p = d_ptrs<NG>(g, n0, row, ch);
+        const uint32_t lane4 = lane * 4u;
         CodeRegs<NG> r[6];
+        uint32_t v[16];
 #pragma unroll
         for (int k = 0; k < 5; ++k) code_load(r[k], g, p, min(k, last));
-        dequant_store(r[0], g, Bs[0], row, ch);
-        if (1 < g.ksteps) dequant_store(r[1], g, Bs[1], row, ch);
-        __syncthreads();
+        table_reads(v, r[0], pairs, lane4);
+        scale_store(v, r[0], Bs[0], row, ch);
+        table_reads(v, r[1], pairs, lane4);
+        if (1 < g.ksteps) scale_store(v, r[1], Bs[1], row, ch);
+        table_reads(v, r[2], pairs, lane4);
+        deq_barrier();
         int c = 0;
         for (; c + 6 <= g.ksteps; c += 6) {
-            deq_step<NG, 0>(r, g, p, c, Bs, row, ch);
-            deq_step<NG, 1>(r, g, p, c + 1, Bs, row, ch);
-            deq_step<NG, 2>(r, g, p, c + 2, Bs, row, ch);
-            deq_step<NG, 3>(r, g, p, c + 3, Bs, row, ch);
-            deq_step<NG, 4>(r, g, p, c + 4, Bs, row, ch);
-            deq_step<NG, 5>(r, g, p, c + 5, Bs, row, ch);
+            deq_step<NG, 0>(r, v, g, p, c, pairs, lane4, Bs, row, ch);
+            deq_step<NG, 1>(r, v, g, p, c + 1, pairs, lane4, Bs, row, ch);
+            deq_step<NG, 2>(r, v, g, p, c + 2, pairs, lane4, Bs, row, ch);
+            deq_step<NG, 3>(r, v, g, p, c + 3, pairs, lane4, Bs, row, ch);
+            deq_step<NG, 4>(r, v, g, p, c + 4, pairs, lane4, Bs, row, ch);
+            deq_step<NG, 5>(r, v, g, p, c + 5, pairs, lane4, Bs, row, ch);
         }
-        if (c < g.ksteps) deq_step<NG, 0>(r, g, p, c, Bs, row, ch);
-        if (c + 1 < g.ksteps) deq_step<NG, 1>(r, g, p, c + 1, Bs, row, ch);
-        if (c + 2 < g.ksteps) deq_step<NG, 2>(r, g, p, c + 2, Bs, row, ch);
-        if (c + 3 < g.ksteps) deq_step<NG, 3>(r, g, p, c + 3, Bs, row, ch);
-        if (c + 4 < g.ksteps) deq_step<NG, 4>(r, g, p, c + 4, Bs, row, ch);
+        if (c < g.ksteps) deq_step<NG, 0>(r, v, g, p, c, pairs, lane4, Bs, row, ch);
+        if (c + 1 < g.ksteps) deq_step<NG, 1>(r, v, g, p, c + 1, pairs, lane4, Bs, row, ch);
+        if (c + 2 < g.ksteps) deq_step<NG, 2>(r, v, g, p, c + 2, pairs, lane4, Bs, row, ch);
+        if (c + 3 < g.ksteps) deq_step<NG, 3>(r, v, g, p, c + 3, pairs, lane4, Bs, row, ch);
+        if (c + 4 < g.ksteps) deq_step<NG, 4>(r, v, g, p, c + 4, pairs, lane4, Bs, row, ch);
+        __syncthreads();  // the MFMA waves' K-half exchange
     }
 }
 
@@ -383,13 +453,7 @@ void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes, const uint16_t 
     g.ksteps = (padded + kBK - 1) / kBK;  // dev is a multiple of 256: whole steps stay in the row
     g.mtiles = (m + kBM - 1) / kBM;
     g.tiles = (rows + kBN - 1) / kBN * g.mtiles;
-    for (int q = 0; q < 4; ++q) {
-        g.lo[q] = g.hi[q] = 0;
-        for (int b = 0; b < 4; ++b) {
-            g.lo[q] |= uint32_t(cb_half[q * 4 + b] & 0xFF) << (8 * b);
-            g.hi[q] |= uint32_t(cb_half[q * 4 + b] >> 8) << (8 * b);
-        }
-    }
+    for (int i = 0; i < 16; ++i) g.cb[i] = cb_half[i];
     dim3 grid(g.tiles), block(kGemmThreads);
     switch (g.group_shift) {
     case 3: hipLaunchKernelGGL(prefill_gemm_kernel<4>, grid, block, 0, s, g); break;
