@@ -89,11 +89,12 @@ int needle2_gpu_sdot_linear_device(void *sdot_handle, const float *d_x, float *d
  * chunks): d_y[m][out] = FWHT-domain product of d_x[m][in] (device fp32) on
  * fp16 MFMA with fp32 accumulation; activations and cb*norm weights are
  * rounded to fp16 (agreement with needle2_cq_linear about 1e-3 normwise).
- * 4-bit codes (CQ4, CQ3) only. The _timed form records two events around
- * the GEMM kernel. */
+ * 4-bit codes (CQ4, CQ3) only. The _timed form (a timing aid, no reference
+ * counterpart) records two events around `repeat` back-to-back launches of
+ * the GEMM kernel after one activation transform. */
 int needle2_gpu_cq_gemm_device(void *cq_handle, const float *d_x, float *d_y, int m, void *stream);
 int needle2_gpu_cq_gemm_timed(void *cq_handle, const float *d_x, float *d_y, int m, void *stream, void *gemm_start,
-                              void *gemm_stop);
+                              void *gemm_stop, int repeat);
 
 /* Plans: `count` handles of one geometry (in, bits, group, codebook), matrix
  * i reading d_x[i] ([batch][in]) and writing d_y[i] ([batch][out_i]); one
@@ -120,7 +121,7 @@ int needle2_gpu_synchronize(void);
 void *needle2_gpu_stream_create(void);
 void needle2_gpu_stream_destroy(void *stream);
 int needle2_gpu_stream_synchronize(void *stream);
-void *needle2_gpu_event_create(void);
+void *needle2_gpu_event_create(void); /* timing event: recorded without a system-scope fence */
 void needle2_gpu_event_destroy(void *event);
 int needle2_gpu_event_record(void *event, void *stream);
 float needle2_gpu_event_elapsed(void *start, void *stop); /* ms; waits for stop */

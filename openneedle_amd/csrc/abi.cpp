@@ -128,7 +128,8 @@ void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s
     launch_cq_gemv(m.geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, s);
 }
 
-void CqHandle::gemm_device(const float *d_x, float *d_y, int m_rows, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
+void CqHandle::gemm_device(const float *d_x, float *d_y, int m_rows, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1,
+                           int repeat) {
     if (m_rows <= 0) return;
     ND_CHECK(m.kind == kNib, "prefill GEMM: 4-bit (CQ4 / CQ3) codes only");
     ND_CHECK(prefill_xf_halves(m_rows, m.dev) * 2 < (size_t(1) << 31), "prefill GEMM: m * padded input must be < 2^30");
@@ -137,7 +138,8 @@ void CqHandle::gemm_device(const float *d_x, float *d_y, int m_rows, hipStream_t
     uint16_t cbh[16];
     for (int i = 0; i < 16; ++i) cbh[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(m.lut[i]));
     if (ev0) ND_HIP(hipEventRecord(ev0, s));
-    launch_prefill_gemm(m.geom(), m.codes.p, m.norms.p, m.out, st.xh.p, m_rows, m.dev, m.padded, cbh, d_y, s);
+    for (int r = 0; r < repeat; ++r)
+        launch_prefill_gemm(m.geom(), m.codes.p, m.norms.p, m.out, st.xh.p, m_rows, m.dev, m.padded, cbh, d_y, s);
     if (ev1) ND_HIP(hipEventRecord(ev1, s));
 }
 
@@ -443,15 +445,17 @@ int needle2_gpu_cq_gemm_device(void *handle, const float *d_x, float *d_y, int m
     });
 }
 
-// As needle2_gpu_cq_gemm_device, with two events recorded around the GEMM
-// kernel (after the activation transform).
+// As needle2_gpu_cq_gemm_device, with two events recorded around `repeat`
+// back-to-back launches of the GEMM kernel (after one activation transform):
+// the per-launch time is the elapsed time / repeat.
 int needle2_gpu_cq_gemm_timed(void *handle, const float *d_x, float *d_y, int m, void *stream, void *gemm_start,
-                              void *gemm_stop) {
+                              void *gemm_stop, int repeat) {
     return guarded([&] {
         ND_CHECK(handle, "null CQ handle");
+        ND_CHECK(repeat >= 1, "repeat must be >= 1");
         auto *h = static_cast<CqHandle *>(handle);
         h->gemm_device(d_x, d_y, m, stream ? static_cast<hipStream_t>(stream) : h->st.stream,
-                       static_cast<hipEvent_t>(gemm_start), static_cast<hipEvent_t>(gemm_stop));
+                       static_cast<hipEvent_t>(gemm_start), static_cast<hipEvent_t>(gemm_stop), repeat);
     });
 }
 
@@ -596,9 +600,12 @@ void needle2_gpu_graph_destroy(void *graph) {
     if (graph) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
 }
 
+// Timing events: no system-scope fence when recorded (no L2 write-back and
+// invalidate between the kernels being timed), so an event pair brackets the
+// kernel itself. needle2_gpu_event_elapsed still waits for the stop event.
 void *needle2_gpu_event_create(void) {
     hipEvent_t e = nullptr;
-    if (guarded([&] { ND_HIP(hipEventCreate(&e)); })) return nullptr;
+    if (guarded([&] { ND_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence)); })) return nullptr;
     return e;
 }
 

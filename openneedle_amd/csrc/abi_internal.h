@@ -70,8 +70,9 @@ struct CqHandle {
     void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
     void linear_host(const float *x, float *y, int batch);
     void rows_host(const int64_t *ids, float *y, int count);
-    // prefill GEMM on fp16 MFMA; events (nullable) bracket the GEMM kernel
-    void gemm_device(const float *d_x, float *d_y, int m, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+    // prefill GEMM on fp16 MFMA; events (nullable) bracket `repeat` launches of the GEMM kernel
+    void gemm_device(const float *d_x, float *d_y, int m, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1,
+                     int repeat = 1);
 };
 
 struct SdotHandle {

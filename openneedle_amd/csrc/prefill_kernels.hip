@@ -2,8 +2,10 @@
 // on fp16 MFMA with fp32 accumulation (the batched form of cq.cpp:157-197,
 // as Engine::linear_batch uses it for prompt chunks, engine.cpp:607-670).
 //
-// 1. prefill_transform_kernel: per-group FWHT of X (the reference's stage
-//    order, then * 1/sqrt(group)) written as fp16 in MFMA fragment order:
+// 1. prefill_transform_wave_kernel (groups <= 64: FWHT in registers and lane
+//    butterflies) / prefill_transform_kernel (larger groups: FWHT in LDS):
+//    per-group FWHT of X (the reference's stage order, then * 1/sqrt(group))
+//    written as fp16 in MFMA fragment order:
 //    each 16-byte slice is one lane's operand of one v_mfma_f32_32x32x16_f16,
 //    so the GEMM loads X fragments straight from memory (1 KiB per wave load).
 // 2. prefill_gemm_kernel: 128 x 128 output tile per workgroup, K in steps of
@@ -26,6 +28,7 @@
 // weight), products and sums are fp32 in the MFMA; the result agrees with the
 // reference FP32 path to about 1e-3 normwise (bound 2e-3).
 #include "common.h"
+#include "wave.h"
 
 #include <hip/hip_fp16.h>
 
@@ -84,6 +87,57 @@ __global__ __launch_bounds__(256) void prefill_transform_kernel(const float *__r
         const size_t idx = (((block + s) * 4 + kk) * 64 + hh * 32 + (v & 31)) * 8;
         *reinterpret_cast<u32x4 *>(xf + idx) = u32x4{w[0], w[1], w[2], w[3]};
     }
+}
+
+// Groups of 8 .. 64: one workgroup per (32-row block, 64-position step),
+// thread (row r, unit u) = lane 8 (r % 8) + u owns positions 64 s + 8 u .. + 8
+// of row r. FWHT stages 1, 2, 4 run on the thread's eight values, stages 8,
+// 16, 32 are lane butterflies at strides 1, 2, 4 (the reference's stage order
+// and operands, as transform_kernel); the thread writes its 16-byte slice of
+// the fragment layout (eight rows of a wave: 128 contiguous bytes per slice).
+template <int GROUP>
+__global__ __launch_bounds__(256) void prefill_transform_wave_kernel(const float *__restrict__ x, int m, int in,
+                                                                     int padded, int dev, float scale,
+                                                                     _Float16 *__restrict__ xf) {
+    static_assert(GROUP >= 8 && GROUP <= 64, "in-wave FWHT");
+    const int s = blockIdx.x, rb = blockIdx.y;
+    const int t = threadIdx.x, u = t & 7, r = t >> 3;  // r: row in the block (0..31)
+    const int v = rb * 32 + r, p0 = s * kBK + 8 * u;
+    float a[8];
+    if (v < m && p0 + 8 <= in) {
+        const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<size_t>(v) * in + p0);
+        if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+            const float4 lo = src[0], hi = src[1];
+            a[0] = lo.x, a[1] = lo.y, a[2] = lo.z, a[3] = lo.w, a[4] = hi.x, a[5] = hi.y, a[6] = hi.z, a[7] = hi.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) a[e] = x[static_cast<size_t>(v) * in + p0 + e];
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = v < m && p0 + e < in ? x[static_cast<size_t>(v) * in + p0 + e] : 0.0f;
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (!(e & h)) {
+                const float lo = a[e], hi = a[e + h];
+                a[e] = lo + hi;
+                a[e + h] = lo - hi;
+            }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wave_butterflies<GROUP / 8, 1>(a[e], t);
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const _Float16 h0 = static_cast<_Float16>(p0 + 2 * q < padded ? a[2 * q] * scale : 0.0f);
+        const _Float16 h1 = static_cast<_Float16>(p0 + 2 * q + 1 < padded ? a[2 * q + 1] * scale : 0.0f);
+        w[q] = uint32_t(__builtin_bit_cast(uint16_t, h0)) | (uint32_t(__builtin_bit_cast(uint16_t, h1)) << 16);
+    }
+    const int kk = u & 3, hh = u >> 2;
+    const size_t idx = (((static_cast<size_t>(rb) * (dev / kBK) + s) * 4 + kk) * 64 + hh * 32 + r) * 8;
+    *reinterpret_cast<u32x4 *>(xf + idx) = u32x4{w[0], w[1], w[2], w[3]};
 }
 
 // Code-pair table in LDS: entry e (a byte of codes: low nibble first) holds
@@ -426,6 +480,17 @@ void launch_prefill_transform(const float *x, int m, int in, int padded, int dev
     if (m <= 0) return;
     ND_CHECK(group <= 16384, "prefill GEMM: group must be <= 16384");
     ND_CHECK(dev % kBK == 0, "internal: prefill rows must be whole 64-position steps");
+    if (group <= 64) {
+        dim3 grid(dev / kBK, (m + 31) / 32), block(256);
+        switch (group) {
+        case 8: hipLaunchKernelGGL(prefill_transform_wave_kernel<8>, grid, block, 0, s, x, m, in, padded, dev, scale, xf); break;
+        case 16: hipLaunchKernelGGL(prefill_transform_wave_kernel<16>, grid, block, 0, s, x, m, in, padded, dev, scale, xf); break;
+        case 32: hipLaunchKernelGGL(prefill_transform_wave_kernel<32>, grid, block, 0, s, x, m, in, padded, dev, scale, xf); break;
+        default: hipLaunchKernelGGL(prefill_transform_wave_kernel<64>, grid, block, 0, s, x, m, in, padded, dev, scale, xf); break;
+        }
+        ND_HIP(hipGetLastError());
+        return;
+    }
     const int seg = group > 1024 ? group : 1024;
     dim3 grid((dev + seg - 1) / seg, (m + 31) / 32 * 32), block(256);
     hipLaunchKernelGGL(prefill_transform_kernel, grid, block, seg * sizeof(float), s, x, m, in, padded, dev, group,

@@ -69,7 +69,7 @@ def _library():
     _bind(lib, "needle2_gpu_cq_linear_device", [_P, _P, _P, _I, _P], _I)
     _bind(lib, "needle2_gpu_sdot_linear_device", [_P, _P, _P, _I, _P], _I)
     _bind(lib, "needle2_gpu_cq_gemm_device", [_P, _P, _P, _I, _P], _I)
-    _bind(lib, "needle2_gpu_cq_gemm_timed", [_P, _P, _P, _I, _P, _P, _P], _I)
+    _bind(lib, "needle2_gpu_cq_gemm_timed", [_P, _P, _P, _I, _P, _P, _P, _I], _I)
     _bind(lib, "needle2_gpu_cq_plan_create", [_P, _I, _P, _P, _I], _P)
     _bind(lib, "needle2_gpu_sdot_plan_create", [_P, _I, _P, _P, _I], _P)
     _bind(lib, "needle2_gpu_plan_run", [_P, _P], _I)
@@ -268,17 +268,18 @@ class NativeCQ:
     def linear_device(self, d_x, d_y, batch: int, stream=None) -> None:
         _check(self._lib.needle2_gpu_cq_linear_device(self._handle, d_x, d_y, int(batch), stream), "cq linear_device")
 
-    def gemm_device(self, d_x, d_y, m: int, stream=None, events=None) -> None:
+    def gemm_device(self, d_x, d_y, m: int, stream=None, events=None, repeat: int = 1) -> None:
         """Prefill GEMM on fp16 MFMA: device y[m][out] from device x[m][in] (4-bit codes).
 
-        ``events``: optional (start, stop) :class:`Event` pair recorded around the GEMM kernel.
+        ``events``: optional (start, stop) :class:`Event` pair recorded around ``repeat`` back-to-back launches
+        of the GEMM kernel (a timing aid: per-launch time = elapsed / repeat).
         """
         s = stream.ptr if isinstance(stream, Stream) else stream
         if events is None:
             _check(self._lib.needle2_gpu_cq_gemm_device(self._handle, d_x, d_y, int(m), s), "cq gemm_device")
         else:
             _check(self._lib.needle2_gpu_cq_gemm_timed(self._handle, d_x, d_y, int(m), s, events[0].ptr,
-                                                       events[1].ptr), "cq gemm_device")
+                                                       events[1].ptr, int(repeat)), "cq gemm_device")
 
     def int8_device(self, d_x, d_y, batch: int, stream=None, extended: bool = True) -> None:
         _check(self._lib.needle2_gpu_sdot_linear_device(self._sdot(extended), d_x, d_y, int(batch), stream),
