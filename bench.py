@@ -259,6 +259,7 @@ def main():
     ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode"], default=None,
                     help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--sweep", action="store_true", help="with --only attn: also time fixed split counts")
+    ap.add_argument("--batch", type=int, default=1, help="with --only cq4 / cq2 / int8: activation rows per step")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one 1 GiB streaming copy kernel (reference for byte counters)")
     args = ap.parse_args()
@@ -301,9 +302,9 @@ def main():
         bits, count, rows, rot = (4, 16, 8192, 3) if args.only == "cq4" else (2, 16, 8192, 3) if args.only == "cq2" \
             else (4, 64, 4096, 2)
         packed, norms, cb = random_cq(rng, count, rows, rows, bits, 32)
-        st = Stack(packed, norms, cb, bits, 32, batch=1, rot=rot, int8=args.only == "int8")
+        st = Stack(packed, norms, cb, bits, 32, batch=args.batch, rot=rot, int8=args.only == "int8")
         ms1, g1, _ = st.run(args.steps, args.warmup, stream)
-        log(f"{args.only}: step {ms1 * 1e3:.1f} us, GEMV {g1 * 1e3:.1f} us "
+        log(f"{args.only} b{args.batch}: step {ms1 * 1e3:.1f} us, GEMV {g1 * 1e3:.1f} us "
             f"({st.bytes_per_step / (g1 * 1e-3) / 1e9:.0f} GB/s)")
         return
 
