@@ -9,9 +9,13 @@ inputs, then one GEMV launch).
 are rotated so consecutive steps never re-read data that could still sit in
 the 256 MB last-level cache.
 
-Also reported (``extra``): the same for CQ2, the int8 path on stacked CQ4
-4096x4096 matrices at batch 1/4/16, and the CPU baseline (the reference's own
-C++ library built from source, on all host cores, bounded sample).
+Also reported (``extra``): the same for CQ2; the int8 path on stacked CQ4
+4096x4096 matrices at batch 1/4/16; int8-KV decode attention; the prefill
+GEMM; one decoder layer; the latency-bound CQ4 2048x512 shape; and the
+host-pointer ABI call (H2D copy, kernels, D2H copy, wait) timed on the host.
+Kernel timings carry mean, median, p10 and p90. The CPU baseline runs the
+reference's own C++ built from source (or the oracle's port where that build is
+absent) on all host cores, on bounded samples of each workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 """
@@ -47,6 +51,23 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+SETTLE_S = 0.3
+
+
+def settle(run, seconds=SETTLE_S):
+    """Run `run()` untimed, in bursts of 20 calls, for `seconds` of wall time before a workload's warmup.
+
+    Under sustained load the GPU's power management moves its clocks for the first ~150 ms (on MI355X the
+    16 x CQ4 8192x8192 GEMV runs ~110 us for a few steps, ~147 us some 10 ms in, and settles at ~111 us after
+    ~150 ms); the timed steps should see the steady state a serving loop runs in, not that ramp."""
+    from openneedle_amd.native import synchronize
+    start = time.perf_counter()
+    while time.perf_counter() - start < seconds:
+        for _ in range(20):
+            run()
+        synchronize()
+
+
 def random_cq(rng, count, rows, cols, bits, group):
     """`count` matrices of uniform codes (uniform random bytes) and fp16 norms U[0.005, 0.05]."""
     rowbytes = cols * bits // 8
@@ -75,6 +96,8 @@ class Stack:
 
     def run(self, steps, warmup, stream):
         from openneedle_amd.native import Event, synchronize
+        turn = iter(range(1 << 62))
+        settle(lambda: self.plans[next(turn) % len(self.plans)].run(stream))
         for i in range(warmup):
             self.plans[i % len(self.plans)].run(stream)
         synchronize()
@@ -85,9 +108,15 @@ class Stack:
             self.plans[i % len(self.plans)].run(stream, gemv_events=ev[i])
         t1.record(stream)
         synchronize()
-        total_ms = t0.elapsed_ms(t1)
-        gemv_ms = [a.elapsed_ms(b) for a, b in ev]
-        return total_ms / steps, statistics.mean(gemv_ms), statistics.median(gemv_ms)
+        return t0.elapsed_ms(t1) / steps, [a.elapsed_ms(b) for a, b in ev]
+
+
+def dist_us(ms):
+    """Mean, median, p10 and p90 (microseconds) of a list of millisecond timings."""
+    a = np.asarray(ms, np.float64) * 1e3
+    return {"mean": round(float(a.mean()), 2), "median": round(float(np.median(a)), 2),
+            "p10": round(float(np.percentile(a, 10)), 2), "p90": round(float(np.percentile(a, 90)), 2),
+            "n": int(a.size)}
 
 
 ATTN_BYTES = 2 * 64 * 2048 * 8 * 64 + 2 * 64 * 2048 * 8 * 4 + 2 * 64 * 8 * 64 * 4  # K, V codes + scales + q, out
@@ -110,6 +139,8 @@ def bench_attention(steps, warmup, stream, splits=0):
         caches.append(kv)
     q = DeviceArray.from_host(rng.normal(size=(seqs, heads, hd)).astype(np.float32))
     out = DeviceArray(seqs * heads * hd * 4)
+    turn = iter(range(1 << 62))
+    settle(lambda: caches[next(turn) % 2].attention(0, q.ptr, out.ptr, heads, cap, splits=splits, stream=stream))
     for i in range(warmup):
         caches[i % 2].attention(0, q.ptr, out.ptr, heads, cap, splits=splits, stream=stream)
     synchronize()
@@ -119,7 +150,13 @@ def bench_attention(steps, warmup, stream, splits=0):
         caches[i % 2].attention(0, q.ptr, out.ptr, heads, cap, splits=splits, stream=stream)
     t1.record(stream)
     synchronize()
-    return t0.elapsed_ms(t1) / steps
+    ev = [(Event(), Event()) for _ in range(steps)]
+    for i, (a, b) in enumerate(ev):  # per-launch pairs, for the spread
+        a.record(stream)
+        caches[i % 2].attention(0, q.ptr, out.ptr, heads, cap, splits=splits, stream=stream)
+        b.record(stream)
+    synchronize()
+    return t0.elapsed_ms(t1) / steps, [a.elapsed_ms(b) for a, b in ev]
 
 
 PREFILL_FLOP = 2 * 512 * 8192 * 2048
@@ -130,7 +167,7 @@ PREFILL_REPEAT = 8  # GEMM launches between one event pair: issued one by one th
 
 
 def bench_prefill(steps, warmup, stream):
-    """512 tokens x K 2048 through CQ4 8192 x 2048 g32 on fp16 MFMA: (step ms, GEMM-kernel ms).
+    """512 tokens x K 2048 through CQ4 8192 x 2048 g32 on fp16 MFMA: (step ms, [GEMM-kernel ms per pair]).
 
     A step is the activation transform plus the GEMM (one-by-one calls, one
     event pair around all steps). The GEMM's own time comes from event pairs
@@ -142,6 +179,7 @@ def bench_prefill(steps, warmup, stream):
     q = NativeCQ(packed[0], norms[0], (8192, 2048), 4, 32, cb)
     x = DeviceArray.from_host(rng.normal(size=(512, 2048)).astype(np.float32))
     y = DeviceArray(512 * 8192 * 4)
+    settle(lambda: q.gemm_device(x.ptr, y.ptr, 512, stream))
     for _ in range(warmup):
         q.gemm_device(x.ptr, y.ptr, 512, stream)
     synchronize()
@@ -151,11 +189,11 @@ def bench_prefill(steps, warmup, stream):
         q.gemm_device(x.ptr, y.ptr, 512, stream)
     t1.record(stream)
     synchronize()
-    ev = [(Event(), Event()) for _ in range(max(1, steps // PREFILL_REPEAT))]
+    ev = [(Event(), Event()) for _ in range(steps)]
     for a, b in ev:
         q.gemm_device(x.ptr, y.ptr, 512, stream, events=(a, b), repeat=PREFILL_REPEAT)
     synchronize()
-    return t0.elapsed_ms(t1) / steps, statistics.mean(a.elapsed_ms(b) for a, b in ev) / PREFILL_REPEAT
+    return t0.elapsed_ms(t1) / steps, [a.elapsed_ms(b) / PREFILL_REPEAT for a, b in ev]
 
 
 def bench_decode_layer(steps, warmup, stream, seqs=64):
@@ -196,6 +234,7 @@ def bench_decode_layer(steps, warmup, stream, seqs=64):
             pl.run(stream)
 
     def timed(fn):
+        settle(fn)
         for _ in range(warmup):
             fn()
         synchronize()
@@ -214,46 +253,171 @@ def bench_decode_layer(steps, warmup, stream, seqs=64):
     return eager, graphed
 
 
-def cpu_baseline(budget_s=20.0):
-    """The reference's CQ::linear (oracle/_ref) - or the oracle port - on one CQ4 8192x8192 g32 matrix."""
-    import oracle
-    cores = len(os.sched_getaffinity(0))
-    rng = np.random.default_rng(11)
-    packed, norms, cb = random_cq(rng, 1, 8192, 8192, 4, 32)
-    x = rng.normal(size=8192).astype(np.float32)
-    nbytes = packed.nbytes + norms.nbytes
-    kind = "reference"
-    try:
-        m = oracle.RefCQ(packed[0], norms[0], (8192, 8192), 4, 32, cb)
-        run = lambda: m.linear(x, cores)  # noqa: E731
-    except RuntimeError:
-        kind = "port"
-        run = lambda: oracle.cq_linear(packed[0], norms[0], (8192, 8192), 4, 32, cb, x, cores)  # noqa: E731
-    run()
+def bench_small(steps, warmup, stream):
+    """CQ4 2048 x 512 g32, FP32 path, batch 1 (590 KB of weights: a launch-latency-bound shape).
+
+    Returns per-call millisecond lists: the device step (FWHT pre-pass + GEMV, one event pair per step), the GEMV
+    kernel alone, and the host-pointer ABI call (needle2_cq_linear: copy x in, transform + GEMV, copy y out, wait),
+    timed on the host around the ctypes call."""
+    from openneedle_amd.native import DeviceArray, Event, NativeCQ, Plan, synchronize
+    rng = np.random.default_rng(20261202)
+    packed, norms, cb = random_cq(rng, 1, 2048, 512, 4, 32)
+    q = NativeCQ(packed[0], norms[0], (2048, 512), 4, 32, cb)
+    xh = rng.normal(size=512).astype(np.float32)
+    x, y = DeviceArray.from_host(xh), DeviceArray(2048 * 4)
+    plan = Plan([q], [x.ptr], [y.ptr], batch=1)
+    settle(lambda: plan.run(stream))
+    for _ in range(warmup):
+        plan.run(stream)
+    synchronize()
+    ev = [tuple(Event() for _ in range(4)) for _ in range(steps)]
+    for s0, s1, g0, g1 in ev:
+        s0.record(stream)
+        plan.run(stream, gemv_events=(g0, g1))
+        s1.record(stream)
+    synchronize()
+    step = [a.elapsed_ms(b) for a, b, _, _ in ev]
+    gemv = [c.elapsed_ms(d) for _, _, c, d in ev]
+    return step, gemv, abi_calls([q], xh, max(steps, 50), warmup)
+
+
+def abi_calls(mats, x, runs, warmup=3):
+    """Host-side milliseconds of `runs` host-pointer needle2_cq_linear calls (batch 1), cycling over `mats`."""
+    for m in mats[:warmup] if len(mats) >= warmup else mats * warmup:
+        m.linear(x)
+    times = []
+    for i in range(runs):
+        m = mats[i % len(mats)]
+        t = time.perf_counter_ns()
+        m.linear(x)
+        times.append((time.perf_counter_ns() - t) / 1e6)
+    return times
+
+
+def _cpu_time(run, budget_s, min_runs=5, max_runs=100000, warmup=1):
+    """Median, p10, p90 (seconds) and count of `run()` wall times: perf_counter_ns, `warmup` untimed calls, then
+    at least `min_runs` calls and as many more as fit in `budget_s`."""
+    for _ in range(warmup):
+        run()
     times = []
     start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - start < budget_s and len(times) < 50):
+    while len(times) < min_runs or (time.perf_counter() - start < budget_s and len(times) < max_runs):
         t = time.perf_counter_ns()
         run()
         times.append((time.perf_counter_ns() - t) / 1e9)
-    med = statistics.median(times)
+    a = np.asarray(times)
+    return float(np.median(a)), float(np.percentile(a, 10)), float(np.percentile(a, 90)), len(times)
+
+
+def _spread(med, p10, p90, scale=1e3):
+    return {"median": round(med * scale, 3), "p10": round(p10 * scale, 3), "p90": round(p90 * scale, 3)}
+
+
+def cpu_baseline(budget_s=12.0, others=True):
+    """The reference's own C++ (oracle/_ref, built from source) - or the oracle's port where that library is
+    absent - on this host's cores, on bounded samples of each GPU workload.
+
+    Headline (``value``): one step of the 16 x CQ4 8192x8192 g32 FP32 GEMV (CQ::linear, rows across OpenMP
+    threads), the same 604 MB of distinct weights as the GPU step, repeated for about `budget_s` seconds.
+    ``workloads``: CQ4 2048x512 (CQ::linear, batch 1); SdotCQ's scalar int8 path on 8 distinct CQ4 4096x4096 g32
+    matrices at batch 1/4/16 (row4 blocks across threads - the reference itself only runs SDOT on ARM); the
+    prefill shape as CQ::linear over a 32-token chunk (token pairs, the arithmetic of Engine::linear_batch) of
+    CQ4 8192x2048 g32; Engine::compute_attention over int8 caches of 2048 slots, 8 heads = 8 kv heads, head_dim
+    64, for 8 sequences (one engine each)."""
+    import oracle
+    cores = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(11)
+    kind = "reference" if oracle.ref() is not None else "port"
+
+    def cq(packed, norms, shape, bits, group, cb):
+        if kind == "reference":
+            m = oracle.RefCQ(packed, norms, shape, bits, group, cb)
+            return lambda x: m.linear(x, cores)
+        return lambda x: oracle.cq_linear(packed, norms, shape, bits, group, cb, x, cores)
+
+    packed, norms, cb = random_cq(rng, 16, 8192, 8192, 4, 32)
+    mats = [cq(packed[i], norms[i], (8192, 8192), 4, 32, cb) for i in range(16)]
+    x = rng.normal(size=8192).astype(np.float32)
+    nbytes = packed.nbytes + norms.nbytes
+    med, p10, p90, n = _cpu_time(lambda: [m(x) for m in mats], budget_s)
+    del mats, packed, norms
     try:
         model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
     except (OSError, StopIteration):
         model = "unknown"
-    return {
+    out = {
         "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
-        "sample": f"1 x CQ4 8192x8192 g32 FP32 GEMV (1/16 of the step), batch 1, {len(times)} runs, "
-                  f"median {med * 1e3:.1f} ms, {model}",
-        "ms_per_step_equivalent": round(med * 16 * 1e3, 2),
+        "sample": f"{n} steps of 16 distinct CQ4 8192x8192 g32 FP32 GEMVs (batch 1, the GPU step's workload), "
+                  f"median {med * 1e3:.1f} ms per step, {cores} OpenMP threads, {model}",
+        "ms_per_step": _spread(med, p10, p90),
     }
+    if not others:
+        return out
+    w = {}
+
+    packed, norms, cb = random_cq(rng, 1, 2048, 512, 4, 32)
+    m = cq(packed[0], norms[0], (2048, 512), 4, 32, cb)
+    xs = rng.normal(size=512).astype(np.float32)
+    med, p10, p90, n = _cpu_time(lambda: m(xs), 2.0, warmup=5)
+    w["cq4_2048x512_b1"] = {"what": "CQ::linear, batch 1", "us_per_call": _spread(med, p10, p90, 1e6), "runs": n}
+
+    packed, norms, cb = random_cq(rng, 8, 4096, 4096, 4, 32)
+    if kind == "reference":
+        refs = [oracle.RefCQ(packed[i], norms[i], (4096, 4096), 4, 32, cb) for i in range(8)]
+        sd = [lambda x, r=r: r.sdot_linear(x, cores) for r in refs]
+    else:
+        sd = [lambda x, i=i: oracle.sdot_linear(packed[i], norms[i], (4096, 4096), 4, 32, cb, x, cores)
+              for i in range(8)]
+    for batch in (1, 4, 16):
+        xb = rng.normal(size=(batch, 4096)).astype(np.float32)
+        k = 8 // min(batch, 8)  # distinct matrices per timed call: 8, 2, 1
+        med, p10, p90, n = _cpu_time(lambda: [f(xb) for f in sd[:k]], 2.0, min_runs=3)
+        w[f"int8_cq4_4096_b{batch}"] = {
+            "what": f"SdotCQ scalar int8 path (prepare + row4 blocks), {k} distinct matrices per timed call",
+            "gbs": round(k * (packed[0].nbytes + norms[0].nbytes) / med / 1e9, 3),
+            "ms_per_matrix": _spread(med / k, p10 / k, p90 / k), "runs": n}
+    del sd, packed, norms
+
+    packed, norms, cb = random_cq(rng, 1, 8192, 2048, 4, 32)
+    m = cq(packed[0], norms[0], (8192, 2048), 4, 32, cb)
+    xc = rng.normal(size=(32, 2048)).astype(np.float32)
+    med, p10, p90, n = _cpu_time(lambda: m(xc), 3.0)
+    w["prefill_cq4_8192x2048_m32"] = {
+        "what": "CQ::linear over one 32-token chunk (token pairs, as Engine::linear_batch)",
+        "gflops": round(2 * 32 * 8192 * 2048 / med / 1e9, 2), "ms_per_chunk": _spread(med, p10, p90),
+        "ms_512_tokens": round(med * 16 * 1e3, 1), "runs": n}
+
+    seqs, cap, kvh, hd = 8, 2048, 8, 64
+    if kind == "reference":
+        engines = []
+        for _ in range(seqs):
+            e = oracle.RefAttention(8, kvh, hd, cap, cores)
+            e.load(rng.normal(size=(cap, kvh, hd)).astype(np.float32), rng.normal(size=(cap, kvh, hd)).astype(np.float32))
+            engines.append(e)
+        qs = rng.normal(size=(seqs, 8, hd)).astype(np.float32)
+        run = lambda: [e.attend(qs[i]) for i, e in enumerate(engines)]  # noqa: E731
+    else:
+        caches = []
+        for _ in range(seqs):
+            k, ks = oracle.kv_quantize(rng.normal(size=(cap, kvh, hd)).astype(np.float32))
+            v, vs = oracle.kv_quantize(rng.normal(size=(cap, kvh, hd)).astype(np.float32))
+            caches.append((k, v, ks, vs))
+        qs = rng.normal(size=(seqs, 8, hd)).astype(np.float32)
+        run = lambda: [oracle.attention_i8(qs[i], *c) for i, c in enumerate(caches)]  # noqa: E731
+    med, p10, p90, n = _cpu_time(run, 2.0)
+    w["attn_int8_2048"] = {
+        "what": "Engine::compute_attention (int8 K/V, one engine per sequence, 8 head work items per call)",
+        "us_per_sequence": _spread(med / seqs, p10 / seqs, p90 / seqs, 1e6),
+        "us_64_sequences": round(med / seqs * 64 * 1e6, 1), "runs": n}
+    out["workloads"] = w
+    return out
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode"], default=None,
@@ -289,13 +453,14 @@ def main():
                 f"{seqs / (min(ms_e, ms_g) * 1e-3):.0f} tokens/s per layer")
         return
     if args.only == "prefill":
-        ms_p, g_p = bench_prefill(args.steps, args.warmup, stream)
+        ms_p, g_list = bench_prefill(args.steps, args.warmup, stream)
+        g_p = statistics.mean(g_list)
         log(f"prefill: step {ms_p * 1e3:.1f} us, GEMM {g_p * 1e3:.1f} us "
             f"({PREFILL_FLOP / (g_p * 1e-3) / 1e12:.0f} TFLOP/s)")
         return
     if args.only == "attn":
         for splits in ((0, 1, 2, 4, 8) if args.sweep else (0,)):
-            ms_a = bench_attention(args.steps, args.warmup, stream, splits)
+            ms_a, _ = bench_attention(args.steps, args.warmup, stream, splits)
             log(f"attention splits={splits}: {ms_a * 1e3:.1f} us ({ATTN_BYTES / (ms_a * 1e-3) / 1e9:.0f} GB/s)")
         return
     if args.only:
@@ -303,7 +468,8 @@ def main():
             else (4, 64, 4096, 2)
         packed, norms, cb = random_cq(rng, count, rows, rows, bits, 32)
         st = Stack(packed, norms, cb, bits, 32, batch=args.batch, rot=rot, int8=args.only == "int8")
-        ms1, g1, _ = st.run(args.steps, args.warmup, stream)
+        ms1, g_list = st.run(args.steps, args.warmup, stream)
+        g1 = statistics.mean(g_list)
         log(f"{args.only} b{args.batch}: step {ms1 * 1e3:.1f} us, GEMV {g1 * 1e3:.1f} us "
             f"({st.bytes_per_step / (g1 * 1e-3) / 1e9:.0f} GB/s)")
         return
@@ -311,19 +477,38 @@ def main():
     log("building CQ4 stack: 16 x 8192x8192 g32 (3 rotations)")
     packed, norms, cb = random_cq(rng, 16, 8192, 8192, 4, 32)
     cq4 = Stack(packed, norms, cb, 4, 32, batch=1, rot=3)
-    ms, gemv_mean, gemv_med = cq4.run(args.steps, args.warmup, stream)
+    ms, gemv_ms = cq4.run(args.steps, args.warmup, stream)
+    gemv = dist_us(gemv_ms)
     nbytes = cq4.bytes_per_step
     value = nbytes / (ms * 1e-3) / 1e9
-    achieved = nbytes / (gemv_mean * 1e-3) / 1e9
-    log(f"CQ4 step {ms * 1e3:.1f} us ({value:.0f} GB/s); GEMV kernel mean {gemv_mean * 1e3:.1f} us ({achieved:.0f} GB/s)")
-    del cq4, packed, norms
+    achieved = nbytes / (gemv["mean"] * 1e-6) / 1e9
+    log(f"CQ4 step {ms * 1e3:.1f} us ({value:.0f} GB/s); GEMV kernel {gemv} us ({achieved:.0f} GB/s)")
 
     extra = {}
     if not args.no_extra:
+        # The reference's host-pointer call on one CQ4 8192x8192 matrix, cycling over the 48 resident copies.
+        flat = [m for rot in cq4.mats for m in rot]
+        abi = dist_us(abi_calls(flat, rng.normal(size=8192).astype(np.float32), max(args.steps, 50)))
+        extra["abi_cq4_8192_call_us"] = abi
+        extra["abi_cq4_8192_gbs"] = round(nbytes / 16 / (abi["median"] * 1e-6) / 1e9, 1)  # weights / call time
+        log(f"ABI needle2_cq_linear, CQ4 8192x8192 (host x/y): {abi} us")
+    del cq4, packed, norms
+
+    if not args.no_extra:
+        log("CQ4 2048x512 g32 batch 1 (latency-bound shape)")
+        st_ms, gv_ms, abi_ms = bench_small(max(args.steps, 50), args.warmup, stream)
+        extra["cq4_2048x512_step_us"] = dist_us(st_ms)
+        extra["cq4_2048x512_gemv_us"] = dist_us(gv_ms)
+        extra["cq4_2048x512_abi_call_us"] = dist_us(abi_ms)
+        log(f"CQ4 2048x512: step {extra['cq4_2048x512_step_us']} us, GEMV {extra['cq4_2048x512_gemv_us']} us, "
+            f"ABI {extra['cq4_2048x512_abi_call_us']} us")
+
         log("building CQ2 stack: 16 x 8192x8192 g32 (3 rotations)")
         packed, norms, cb = random_cq(rng, 16, 8192, 8192, 2, 32)
         cq2 = Stack(packed, norms, cb, 2, 32, batch=1, rot=3)
-        ms2, g2, _ = cq2.run(args.steps, args.warmup, stream)
+        ms2, g2_ms = cq2.run(args.steps, args.warmup, stream)
+        g2 = statistics.mean(g2_ms)
+        extra["cq2_fp32_gemv_dist_us"] = dist_us(g2_ms)
         extra["cq2_fp32_gbs"] = round(cq2.bytes_per_step / (ms2 * 1e-3) / 1e9, 1)
         extra["cq2_fp32_gemv_us"] = round(g2 * 1e3, 2)
         extra["cq2_fp32_gemv_frac"] = round(cq2.bytes_per_step / (g2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
@@ -334,7 +519,9 @@ def main():
         packed, norms, cb = random_cq(rng, 64, 4096, 4096, 4, 32)
         for batch in (1, 4, 16):
             st = Stack(packed, norms, cb, 4, 32, batch=batch, rot=2, int8=True)
-            msb, gb, _ = st.run(max(10, args.steps // 2), args.warmup, stream)
+            msb, gb_ms = st.run(args.steps, args.warmup, stream)
+            gb = statistics.mean(gb_ms)
+            extra[f"int8_b{batch}_gemv_dist_us"] = dist_us(gb_ms)
             extra[f"int8_b{batch}_gbs"] = round(st.bytes_per_step / (msb * 1e-3) / 1e9, 1)
             extra[f"int8_b{batch}_gemv_us"] = round(gb * 1e3, 2)
             extra[f"int8_b{batch}_gemv_frac"] = round(st.bytes_per_step / (gb * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
@@ -343,15 +530,18 @@ def main():
         del packed, norms
 
         log("attention: 64 seqs x 8 heads x hd 64, 2048 int8 slots")
-        ms_a = bench_attention(args.steps, args.warmup, stream)
+        ms_a, a_ms = bench_attention(args.steps, args.warmup, stream)
         extra["attn_decode_us"] = round(ms_a * 1e3, 2)
+        extra["attn_launch_dist_us"] = dist_us(a_ms)
         extra["attn_gbs"] = round(ATTN_BYTES / (ms_a * 1e-3) / 1e9, 1)
         extra["attn_frac"] = round(ATTN_BYTES / (ms_a * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         log(f"attention {ms_a * 1e3:.1f} us ({extra['attn_gbs']} GB/s)")
 
         log("prefill GEMM: 512 x 2048 through CQ4 8192 x 2048 g32 (fp16 MFMA)")
-        ms_p, g_p = bench_prefill(args.steps, args.warmup, stream)
+        ms_p, g_list = bench_prefill(args.steps, args.warmup, stream)
+        g_p = statistics.mean(g_list)
         extra["prefill_step_us"] = round(ms_p * 1e3, 2)
+        extra["prefill_gemm_dist_us"] = dist_us(g_list)
         extra["prefill_gemm_us"] = round(g_p * 1e3, 2)
         extra["prefill_tflops"] = round(PREFILL_FLOP / (g_p * 1e-3) / 1e12, 1)
         extra["prefill_mfma_util"] = round(extra["prefill_tflops"] / MFMA_FP16_PEAK_TFLOPS, 4)
@@ -372,8 +562,8 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log("CPU baseline (reference CQ::linear, all host cores)")
-        cpu = cpu_baseline()
+        log("CPU baseline (reference C++ built from source, all host cores)")
+        cpu = cpu_baseline(others=not args.no_extra)
         log(f"CPU {cpu}")
 
     line = {
@@ -391,11 +581,12 @@ def main():
         "data": "synthetic (uniform codes, fp16 norms U[0.005,0.05], x ~ N(0,1)); weights resident in HBM",
         "config": {"workload": "16 x CQ4 8192x8192 g32 GEMV, FP32 path, batch 1", "bits": 4, "group": 32,
                    "matrices": 16, "rows": 8192, "cols": 8192, "batch": 1, "weight_rotations": 3,
-                   "bytes_per_step": nbytes, "device": info["name"], "cus": info["cus"]},
+                   "bytes_per_step": nbytes, "device": info["name"], "cus": info["cus"],
+                   "untimed_settle_s": SETTLE_S},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(HEADLINE_KERNEL),
-                     "kernel": HEADLINE_KERNEL, "gemv_mean_us": round(gemv_mean * 1e3, 2),
-                     "gemv_median_us": round(gemv_med * 1e3, 2), "algorithmic_bytes": nbytes},
+                     "kernel": HEADLINE_KERNEL, "gemv_mean_us": gemv["mean"], "gemv_median_us": gemv["median"],
+                     "gemv_p10_us": gemv["p10"], "gemv_p90_us": gemv["p90"], "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu,
         "extra": extra,
     }
