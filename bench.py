@@ -101,12 +101,17 @@ class Stack:
         for i in range(warmup):
             self.plans[i % len(self.plans)].run(stream)
         synchronize()
-        ev = [(Event(), Event()) for _ in range(steps)]
+        # the step time: one event pair around `steps` plan runs, nothing recorded between them
         t0, t1 = Event(), Event()
         t0.record(stream)
         for i in range(steps):
-            self.plans[i % len(self.plans)].run(stream, gemv_events=ev[i])
+            self.plans[i % len(self.plans)].run(stream)
         t1.record(stream)
+        synchronize()
+        # then the GEMV kernel's own time: `steps` more runs with an event pair around each GEMV launch
+        ev = [(Event(), Event()) for _ in range(steps)]
+        for i in range(steps):
+            self.plans[i % len(self.plans)].run(stream, gemv_events=ev[i])
         synchronize()
         return t0.elapsed_ms(t1) / steps, [a.elapsed_ms(b) for a, b in ev]
 
@@ -281,6 +286,41 @@ def bench_small(steps, warmup, stream):
     return step, gemv, abi_calls([q], xh, max(steps, 50), warmup)
 
 
+def bench_candidates(steps, warmup, stream):
+    """Candidate rows of the LM-head geometry (CQ4 8192 x 512 g32, one input vector) through the device entry
+    point, FP32 and int8 paths, next to the full GEMV of the same matrix: {name: [ms per call]} from one event
+    pair around each call. 142 candidates gather rows into a compact matrix; 8192 run the whole matrix."""
+    from openneedle_amd.native import DeviceArray, Event, NativeCQ, synchronize
+    rng = np.random.default_rng(29)
+    packed, norms, cb = random_cq(rng, 1, 8192, 512, 4, 32)
+    q = NativeCQ(packed[0], norms[0], (8192, 512), 4, 32, cb)
+    x = DeviceArray.from_host(rng.normal(size=512).astype(np.float32))
+    y = DeviceArray(8192 * 4)
+    sp = stream.ptr
+
+    def calls(fn):
+        settle(fn, 0.05)
+        for _ in range(warmup):
+            fn()
+        synchronize()
+        ev = [(Event(), Event()) for _ in range(steps)]
+        for a, b in ev:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        synchronize()
+        return [a.elapsed_ms(b) for a, b in ev]
+
+    out = {"fp32_full": calls(lambda: q.linear_device(x.ptr, y.ptr, 1, sp)),
+           "int8_full": calls(lambda: q.int8_device(x.ptr, y.ptr, 1, sp))}
+    for count in (142, 8192):
+        ids = DeviceArray.from_host(rng.permutation(8192)[:count].astype(np.int32))
+        for int8 in (False, True):
+            out[f"{'int8' if int8 else 'fp32'}_{count}"] = calls(
+                lambda: q.candidates_device(x.ptr, ids.ptr, count, y.ptr, stream, int8=int8))
+    return out
+
+
 def abi_calls(mats, x, runs, warmup=3):
     """Host-side milliseconds of `runs` host-pointer needle2_cq_linear calls (batch 1), cycling over `mats`."""
     for m in mats[:warmup] if len(mats) >= warmup else mats * warmup:
@@ -420,7 +460,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode"], default=None,
+    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode", "cand"], default=None,
                     help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--sweep", action="store_true", help="with --only attn: also time fixed split counts")
     ap.add_argument("--batch", type=int, default=1, help="with --only cq4 / cq2 / int8: activation rows per step")
@@ -451,6 +491,10 @@ def main():
             ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs)
             log(f"decode layer ({seqs} seqs, ctx 2048): eager {ms_e * 1e3:.1f} us, graph {ms_g * 1e3:.1f} us -> "
                 f"{seqs / (min(ms_e, ms_g) * 1e-3):.0f} tokens/s per layer")
+        return
+    if args.only == "cand":
+        for k, v in bench_candidates(args.steps, args.warmup, stream).items():
+            log(f"candidates {k}: {dist_us(v)} us")
         return
     if args.only == "prefill":
         ms_p, g_list = bench_prefill(args.steps, args.warmup, stream)
@@ -546,6 +590,11 @@ def main():
         extra["prefill_tflops"] = round(PREFILL_FLOP / (g_p * 1e-3) / 1e12, 1)
         extra["prefill_mfma_util"] = round(extra["prefill_tflops"] / MFMA_FP16_PEAK_TFLOPS, 4)
         log(f"prefill GEMM {g_p * 1e3:.1f} us ({extra['prefill_tflops']} TFLOP/s), step {ms_p * 1e3:.1f} us")
+
+        log("candidate rows: LM head CQ4 8192 x 512 g32, 142 and 8192 candidates")
+        for k, v in bench_candidates(args.steps, args.warmup, stream).items():
+            extra[f"candidates_{k}_us"] = dist_us(v)
+        log(f"candidates: { {k: v['median'] for k, v in extra.items() if k.startswith('candidates_')} }")
 
         for seqs in (64, 1):
             log(f"decode layer: {seqs} sequence(s), ctx 2048, int8-path CQ4 projections + int8-KV attention")

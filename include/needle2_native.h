@@ -84,6 +84,22 @@ void *needle2_gpu_sdot_create(const uint8_t *packed, const uint16_t *norms, int 
 int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream);
 int needle2_gpu_sdot_linear_device(void *sdot_handle, const float *d_x, float *d_y, int batch, void *stream);
 
+/* Candidate rows (replaces the CQ and SDOT branches of
+ * Engine::project_candidates, needle2/csrc/engine.cpp:1302-1349, behind
+ * needle2_engine_project_candidates, engine.cpp:1530): y[i] = row ids[i] of
+ * the product of one input vector x[in], bit-identical to that row of
+ * needle2_cq_linear / needle2_sdot_linear; order and duplicates are kept.
+ * Host-pointer forms return -1 with "candidates must be nonempty" (count < 1)
+ * or "candidate outside vocabulary" (an id outside [0, out)), as the
+ * reference does. Device forms: d_ids int32 on the device, an id outside
+ * [0, out) yields NaN. */
+int needle2_gpu_cq_candidates(void *handle, const float *x, const int32_t *ids, int count, float *y);
+int needle2_gpu_cq_candidates_device(void *handle, const float *d_x, const int32_t *d_ids, int count, float *d_y,
+                                     void *stream);
+int needle2_gpu_sdot_candidates(void *sdot_handle, const float *x, const int32_t *ids, int count, float *y);
+int needle2_gpu_sdot_candidates_device(void *sdot_handle, const float *d_x, const int32_t *d_ids, int count,
+                                       float *d_y, void *stream);
+
 /* Prefill GEMM (replaces the per-token-pair CQ loops of Engine::linear_batch /
  * attention_projections_batch, needle2/csrc/engine.cpp:607-750, for prompt
  * chunks): d_y[m][out] = FWHT-domain product of d_x[m][in] (device fp32) on

@@ -113,8 +113,8 @@ Staging::~Staging() {
 // ---------------------------------------------------------------------------
 // FP32 handle
 // ---------------------------------------------------------------------------
-void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s) {
-    if (batch <= 0) return;
+void CqHandle::gemv(const uint4 *codes, const uint16_t *norms, int rows, int n_pad, const float *d_x, float *d_y,
+                    int batch, hipStream_t s) {
     const float *act = d_x;
     if (!gemv_fuses_fwht(m.group)) {
         st.rot.reserve(size_t(batch) * m.dev);
@@ -124,8 +124,70 @@ void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s
             m.transform(d_x, m.in, st.rot.p, batch, st.big, s);
         act = st.rot.p;
     }
-    const CqJob job{m.codes.p, m.norms.p, act, d_y, m.out, m.n_pad, 0, batch};
-    launch_cq_gemv(m.geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, s);
+    const CqJob job{codes, norms, act, d_y, rows, n_pad, 0, batch};
+    launch_cq_gemv(m.geom(), job, nullptr, 0, n_pad / kRowsPerBlock, s);
+}
+
+void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s) {
+    if (batch <= 0) return;
+    gemv(m.codes.p, m.norms.p, m.out, m.n_pad, d_x, d_y, batch, s);
+}
+
+// ---------------------------------------------------------------------------
+// Candidate rows (engine.cpp:1307-1349): the same GEMV kernels over a compact
+// matrix of the candidate rows, so every output is bit-identical to that row
+// of the full product; when at least half the rows are asked for, the full
+// GEMV runs and the outputs are picked.
+// ---------------------------------------------------------------------------
+Candidates gather_candidates(const Matrix &m, Staging &st, const int32_t *d_ids, int count, hipStream_t s) {
+    Candidates c;
+    if (2 * size_t(count) >= size_t(m.out)) {
+        c.full = true;
+        return c;
+    }
+    c.n_pad = (count + kRowsPerBlock - 1) / kRowsPerBlock * kRowsPerBlock;
+    st.gcodes.reserve(size_t(c.n_pad) * m.chunks);
+    st.gnorms.reserve(size_t(c.n_pad) * m.groups);
+    launch_gather_rows(m.codes.p, m.norms.p, m.out, m.chunks, m.groups, d_ids, count, c.n_pad, st.gcodes.p,
+                       st.gnorms.p, s);
+    c.codes = st.gcodes.p;
+    c.norms = st.gnorms.p;
+    return c;
+}
+
+void upload_candidates(Staging &st, const int32_t *ids, int count, int rows) {
+    ND_CHECK(ids && count > 0, "candidates must be nonempty");
+    for (int i = 0; i < count; ++i) ND_CHECK(ids[i] >= 0 && ids[i] < rows, "candidate outside vocabulary");
+    st.hids.reserve(count);
+    st.ids.reserve(count);
+    std::memcpy(st.hids.p, ids, size_t(count) * sizeof(int32_t));
+    ND_HIP(hipMemcpyAsync(st.ids.p, st.hids.p, size_t(count) * sizeof(int32_t), hipMemcpyHostToDevice, st.stream));
+}
+
+void CqHandle::candidates_device(const float *d_x, const int32_t *d_ids, int count, float *d_y, hipStream_t s) {
+    if (count <= 0) return;
+    const Candidates c = gather_candidates(m, st, d_ids, count, s);
+    if (c.full) {
+        st.yfull.reserve(m.out);
+        run_device(d_x, st.yfull.p, 1, s);
+        launch_gather_outputs(st.yfull.p, m.out, d_ids, count, 1, d_y, s);
+    } else {
+        gemv(c.codes, c.norms, count, c.n_pad, d_x, d_y, 1, s);
+    }
+}
+
+void CqHandle::candidates_host(const float *x, const int32_t *ids, int count, float *y) {
+    upload_candidates(st, ids, count, m.out);
+    st.hx.reserve(m.in);
+    st.x.reserve(m.in);
+    st.hy.reserve(count);
+    st.y.reserve(count);
+    std::memcpy(st.hx.p, x, size_t(m.in) * sizeof(float));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, size_t(m.in) * sizeof(float), hipMemcpyHostToDevice, st.stream));
+    candidates_device(st.x.p, st.ids.p, count, st.y.p, st.stream);
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, st.stream));
+    ND_HIP(hipStreamSynchronize(st.stream));
+    std::memcpy(y, st.hy.p, size_t(count) * sizeof(float));
 }
 
 void CqHandle::gemm_device(const float *d_x, float *d_y, int m_rows, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1,
@@ -219,6 +281,37 @@ void SdotHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t
     prepare_device(d_x, batch, st.q.p, st.xs.p, st.xst.p, s);
     const SdotJob job{m.codes.p, m.norms.p, st.q.p, st.xs.p, d_y, m.out, m.n_pad, 0, batch, st.xst.p};
     launch_sdot_gemv(geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, batch, s);
+}
+
+void SdotHandle::candidates_device(const float *d_x, const int32_t *d_ids, int count, float *d_y, hipStream_t s) {
+    if (count <= 0) return;
+    const Candidates c = gather_candidates(m, st, d_ids, count, s);
+    if (c.full) {
+        st.yfull.reserve(m.out);
+        run_device(d_x, st.yfull.p, 1, s);
+        launch_gather_outputs(st.yfull.p, m.out, d_ids, count, 1, d_y, s);
+        return;
+    }
+    st.q.reserve(m.dev / 4);
+    st.xs.reserve(m.groups);
+    st.xst.reserve(m.groups);
+    prepare_device(d_x, 1, st.q.p, st.xs.p, st.xst.p, s);
+    const SdotJob job{c.codes, c.norms, st.q.p, st.xs.p, d_y, count, c.n_pad, 0, 1, st.xst.p};
+    launch_sdot_gemv(geom(), job, nullptr, 0, c.n_pad / kRowsPerBlock, 1, s);
+}
+
+void SdotHandle::candidates_host(const float *x, const int32_t *ids, int count, float *y) {
+    upload_candidates(st, ids, count, m.out);
+    st.hx.reserve(m.in);
+    st.x.reserve(m.in);
+    st.hy.reserve(count);
+    st.y.reserve(count);
+    std::memcpy(st.hx.p, x, size_t(m.in) * sizeof(float));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, size_t(m.in) * sizeof(float), hipMemcpyHostToDevice, st.stream));
+    candidates_device(st.x.p, st.ids.p, count, st.y.p, st.stream);
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, st.stream));
+    ND_HIP(hipStreamSynchronize(st.stream));
+    std::memcpy(y, st.hy.p, size_t(count) * sizeof(float));
 }
 
 void SdotHandle::linear_host(const float *x, float *y, int batch) {
@@ -462,6 +555,43 @@ int needle2_gpu_cq_gemm_timed(void *handle, const float *d_x, float *d_y, int m,
 int needle2_gpu_sdot_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {
     auto *h = static_cast<SdotHandle *>(handle);
     return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream); });
+}
+
+// Candidate rows: y[i] = row ids[i] of the product for one input vector, as
+// Engine::project_candidates computes them (engine.cpp:1302-1349; ids must be
+// nonempty and inside [0, out): -1 with the reference's messages otherwise).
+int needle2_gpu_cq_candidates(void *handle, const float *x, const int32_t *ids, int count, float *y) {
+    return guarded([&] {
+        ND_CHECK(handle && x && y, "null argument");
+        static_cast<CqHandle *>(handle)->candidates_host(x, ids, count, y);
+    });
+}
+
+int needle2_gpu_cq_candidates_device(void *handle, const float *d_x, const int32_t *d_ids, int count, float *d_y,
+                                     void *stream) {
+    return guarded([&] {
+        ND_CHECK(handle, "null CQ handle");
+        ND_CHECK(count > 0, "candidates must be nonempty");
+        auto *h = static_cast<CqHandle *>(handle);
+        h->candidates_device(d_x, d_ids, count, d_y, stream ? static_cast<hipStream_t>(stream) : h->st.stream);
+    });
+}
+
+int needle2_gpu_sdot_candidates(void *handle, const float *x, const int32_t *ids, int count, float *y) {
+    return guarded([&] {
+        ND_CHECK(handle && x && y, "null argument");
+        static_cast<SdotHandle *>(handle)->candidates_host(x, ids, count, y);
+    });
+}
+
+int needle2_gpu_sdot_candidates_device(void *handle, const float *d_x, const int32_t *d_ids, int count, float *d_y,
+                                       void *stream) {
+    return guarded([&] {
+        ND_CHECK(handle, "null SDOT handle");
+        ND_CHECK(count > 0, "candidates must be nonempty");
+        auto *h = static_cast<SdotHandle *>(handle);
+        h->candidates_device(d_x, d_ids, count, d_y, stream ? static_cast<hipStream_t>(stream) : h->st.stream);
+    });
 }
 
 // Plans: count matrices sharing (in, bits, group, codebook); matrix i reads

@@ -57,17 +57,41 @@ struct Staging {
     DevBuf<float> x, rot, y, big, xs, xst;
     DevBuf<int32_t> q;
     DevBuf<_Float16> xh;  // fp16 transformed activations of the prefill GEMM
+    DevBuf<uint4> gcodes;   // candidate rows gathered into a compact matrix
+    DevBuf<uint16_t> gnorms;
+    DevBuf<int32_t> ids;
+    DevBuf<float> yfull;    // all outputs, when most rows are candidates
     HostBuf<float> hx, hy;
+    HostBuf<int32_t> hids;
     Staging();
     ~Staging();
     Staging(const Staging &) = delete;
     Staging &operator=(const Staging &) = delete;
 };
 
+// Rows ids[0..count) of a matrix as a compact matrix of n_pad rows (gathered
+// into st.gcodes / st.gnorms), or none when most rows are asked for.
+struct Candidates {
+    const uint4 *codes = nullptr;
+    const uint16_t *norms = nullptr;
+    int n_pad = 0;
+    bool full = false;  // run the whole matrix, then pick the outputs
+};
+Candidates gather_candidates(const Matrix &m, Staging &st, const int32_t *d_ids, int count, hipStream_t s);
+// Host side of needle2_gpu_*_candidates: checks the ids as the reference does
+// (engine.cpp:1302-1306), then copies them to st.ids.
+void upload_candidates(Staging &st, const int32_t *ids, int count, int rows);
+
 struct CqHandle {
     Matrix m;
     Staging st;
     void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
+    // the GEMV over rows [0, rows) of a device-layout matrix with m's geometry
+    void gemv(const uint4 *codes, const uint16_t *norms, int rows, int n_pad, const float *d_x, float *d_y, int batch,
+              hipStream_t s);
+    // d_y[i] = row d_ids[i] of W x for batch-1 x (engine.cpp:1307-1349, the CQ branch)
+    void candidates_device(const float *d_x, const int32_t *d_ids, int count, float *d_y, hipStream_t s);
+    void candidates_host(const float *x, const int32_t *ids, int count, float *y);
     void linear_host(const float *x, float *y, int batch);
     void rows_host(const int64_t *ids, float *y, int count);
     // prefill GEMM on fp16 MFMA; events (nullable) bracket `repeat` launches of the GEMM kernel
@@ -84,6 +108,9 @@ struct SdotHandle {
     SdotGeom geom() const;
     void prepare_device(const float *d_x, int batch, int32_t *q, float *xs, float *xst, hipStream_t s);
     void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
+    // d_y[i] = row d_ids[i] of the int8 product for batch-1 x (engine.cpp:1307-1349, the SDOT branch)
+    void candidates_device(const float *d_x, const int32_t *d_ids, int count, float *d_y, hipStream_t s);
+    void candidates_host(const float *x, const int32_t *ids, int count, float *y);
     void linear_host(const float *x, float *y, int batch);
 };
 

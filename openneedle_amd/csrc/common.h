@@ -203,6 +203,14 @@ void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs_dev, i
                     hipStream_t s);
 
 // Dequantize rows: y[i][0..in) = FWHT(cb[code]*norm) cropped; uses rot-sized scratch.
+// Candidate rows: output row i (< count) of a compact device-layout matrix of
+// n_pad rows (a multiple of kRowsPerBlock) holds row ids[i] of the source;
+// rows past count are zero, an id outside [0, rows) gets NaN norms.
+void launch_gather_rows(const uint4 *codes, const uint16_t *norms, int rows, int chunks, int groups,
+                        const int32_t *ids, int count, int n_pad, uint4 *out_codes, uint16_t *out_norms, hipStream_t s);
+// y[b][i] = full[b][ids[i]] over batch rows (NaN for an id outside [0, rows)).
+void launch_gather_outputs(const float *full, int rows, const int32_t *ids, int count, int batch, float *y,
+                           hipStream_t s);
 void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, const int64_t *ids, int count, int in, int padded, float *scratch, float *y,
                     hipStream_t s);
 

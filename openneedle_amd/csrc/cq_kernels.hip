@@ -12,6 +12,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
+
 namespace nd {
 
 namespace {
@@ -1128,6 +1130,37 @@ __global__ __launch_bounds__(256) void copy_kernel(const u32x4 *__restrict__ src
     for (; i < n; i += stride) dst[i] = src[i];
 }
 
+// Candidate rows (engine.cpp:1307-1349 projects only the candidate rows of
+// the LM head): output row i of a compact device-layout matrix of n_pad rows
+// takes the codes and norms of row ids[i]. Rows past `count` are zero; an id
+// outside [0, rows) gets zero codes and NaN norms, so its output is NaN.
+// Grid: x over output rows (one per lane), y strides over chunks and groups.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint4 *__restrict__ codes,
+                                                          const uint16_t *__restrict__ norms, int rows, int chunks,
+                                                          int groups, const int32_t *__restrict__ ids, int count,
+                                                          uint4 *__restrict__ out_codes, uint16_t *__restrict__ out_norms) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int id = i < count ? ids[i] : 0;
+    const bool real = i < count && id >= 0 && id < rows;
+    const uint16_t fill = i < count ? 0x7E00 : 0;  // fp16 NaN for an invalid id
+    for (int c = blockIdx.y; c < chunks; c += gridDim.y)
+        out_codes[code_index(i, c, chunks)] = real ? codes[code_index(id, c, chunks)] : make_uint4(0, 0, 0, 0);
+    for (int g = blockIdx.y; g < groups; g += gridDim.y)
+        out_norms[norm_index(i, g, groups)] = real ? norms[norm_index(id, g, groups)] : fill;
+}
+
+// y[b][i] = full[b][ids[i]] for b < batch (NaN for an id outside [0, rows)).
+__global__ __launch_bounds__(256) void gather_outputs_kernel(const float *__restrict__ full, int rows,
+                                                             const int32_t *__restrict__ ids, int count,
+                                                             float *__restrict__ y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int b = blockIdx.y;
+    if (i >= count) return;
+    const int id = ids[i];
+    y[static_cast<size_t>(b) * count + i] =
+        id >= 0 && id < rows ? full[static_cast<size_t>(b) * rows + id] : __builtin_nanf("");
+}
+
 }  // namespace
 
 void launch_copy(const void *src, void *dst, size_t bytes, hipStream_t s) {
@@ -1211,6 +1244,23 @@ void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int n
     if (blocks <= 0) return;
     if (g.kind == kNib) launch_gemv_kind<kNib>(g, job0, jobs, njobs, blocks, s);
     else launch_gemv_kind<kCrumb>(g, job0, jobs, njobs, blocks, s);
+}
+
+void launch_gather_rows(const uint4 *codes, const uint16_t *norms, int rows, int chunks, int groups,
+                        const int32_t *ids, int count, int n_pad, uint4 *out_codes, uint16_t *out_norms, hipStream_t s) {
+    if (count <= 0) return;
+    dim3 grid(n_pad / 256, std::min(std::max(chunks, groups), 64)), block(256);
+    hipLaunchKernelGGL(gather_rows_kernel, grid, block, 0, s, codes, norms, rows, chunks, groups, ids, count,
+                       out_codes, out_norms);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_gather_outputs(const float *full, int rows, const int32_t *ids, int count, int batch, float *y,
+                           hipStream_t s) {
+    if (count <= 0 || batch <= 0) return;
+    dim3 grid((count + 255) / 256, batch), block(256);
+    hipLaunchKernelGGL(gather_outputs_kernel, grid, block, 0, s, full, rows, ids, count, y);
+    ND_HIP(hipGetLastError());
 }
 
 void launch_cq_rows(const CqGeom &g, const uint4 *codes, const uint16_t *norms, const int64_t *ids,

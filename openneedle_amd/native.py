@@ -68,6 +68,9 @@ def _library():
     _bind(lib, "needle2_gpu_sdot_create", [_P, _P, _I, _I, _I, _I, _P], _P)
     _bind(lib, "needle2_gpu_cq_linear_device", [_P, _P, _P, _I, _P], _I)
     _bind(lib, "needle2_gpu_sdot_linear_device", [_P, _P, _P, _I, _P], _I)
+    for name in ("needle2_gpu_cq_candidates", "needle2_gpu_sdot_candidates"):
+        _bind(lib, name, [_P, _P, _P, _I, _P], _I)
+        _bind(lib, name + "_device", [_P, _P, _P, _I, _P, _P], _I)
     _bind(lib, "needle2_gpu_cq_gemm_device", [_P, _P, _P, _I, _P], _I)
     _bind(lib, "needle2_gpu_cq_gemm_timed", [_P, _P, _P, _I, _P, _P, _P, _I], _I)
     _bind(lib, "needle2_gpu_cq_plan_create", [_P, _I, _P, _P, _I], _P)
@@ -246,6 +249,37 @@ class NativeCQ:
             raise RuntimeError(f"SDOT linear failed: {err}")
         return y
 
+    def _candidate_ids(self, x, candidates):
+        """needle2/native.py:485-495 checks (same messages) for one input vector and candidate rows."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        if x.shape != (self.shape[1],):
+            raise ValueError(f"Expected one input vector of {self.shape[1]} values; got {x.shape}")
+        cands = np.asarray(candidates)
+        if cands.ndim != 1 or not cands.size or cands.dtype.kind not in "iu":
+            raise ValueError("candidates must be a nonempty 1D integer array")
+        if np.any((cands < 0) | (cands >= self.shape[0])):
+            raise ValueError("candidate outside vocabulary")
+        return x, np.ascontiguousarray(cands, dtype=np.int32)
+
+    def candidates(self, x, candidates):
+        """Rows `candidates` of the FP32 product for one input vector (Engine::project_candidates' CQ branch,
+        needle2/csrc/engine.cpp:1307-1349): bit-identical to linear(x)[candidates]."""
+        x, ids = self._candidate_ids(x, candidates)
+        y = np.empty(ids.size, dtype=np.float32)
+        _check(self._lib.needle2_gpu_cq_candidates(self._handle, x.ctypes.data, ids.ctypes.data, ids.size,
+                                                   y.ctypes.data), "CQ candidates")
+        return y
+
+    def candidates_int8(self, x, candidates):
+        """Rows `candidates` of the int8 product (the SDOT branch): bit-identical to linear_int8(x)[candidates]."""
+        x, ids = self._candidate_ids(x, candidates)
+        if not np.isfinite(x).all():
+            raise ValueError("SDOT input must have the expected last dimension and finite values")
+        y = np.empty(ids.size, dtype=np.float32)
+        _check(self._lib.needle2_gpu_sdot_candidates(self._sdot(True), x.ctypes.data, ids.ctypes.data, ids.size,
+                                                     y.ctypes.data), "SDOT candidates")
+        return y
+
     def rows(self, ids):
         ids = np.asarray(ids)
         if ids.dtype.kind not in "iu":
@@ -280,6 +314,16 @@ class NativeCQ:
         else:
             _check(self._lib.needle2_gpu_cq_gemm_timed(self._handle, d_x, d_y, int(m), s, events[0].ptr,
                                                        events[1].ptr, int(repeat)), "cq gemm_device")
+
+    def candidates_device(self, d_x, d_ids, count: int, d_y, stream=None, int8: bool = False) -> None:
+        """Device form of candidates / candidates_int8: d_ids int32 [count], d_y [count]."""
+        s = stream.ptr if isinstance(stream, Stream) else stream
+        if int8:
+            _check(self._lib.needle2_gpu_sdot_candidates_device(self._sdot(True), d_x, d_ids, int(count), d_y, s),
+                   "sdot candidates_device")
+        else:
+            _check(self._lib.needle2_gpu_cq_candidates_device(self._handle, d_x, d_ids, int(count), d_y, s),
+                   "cq candidates_device")
 
     def int8_device(self, d_x, d_y, batch: int, stream=None, extended: bool = True) -> None:
         _check(self._lib.needle2_gpu_sdot_linear_device(self._sdot(extended), d_x, d_y, int(batch), stream),
