@@ -321,6 +321,24 @@ def bench_candidates(steps, warmup, stream):
     return out
 
 
+def bench_archive_upload():
+    """The released model's geometry as a .cact file (random contents, 13.7 MB): Archive.load (memory map and
+    validation) plus DeviceModel (all 145 CQ matrices uploaded and relaid out, all 259 FP16 tensors as fp32
+    device arrays), timed on the host around the whole load after one untimed load. Returns (ms, bytes)."""
+    import tempfile
+    from openneedle_amd.archive import Archive, DeviceModel, synthetic_released
+    from openneedle_amd.native import synchronize
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "model.cact"
+        path.write_bytes(synthetic_released(seed=1))
+        DeviceModel(Archive.load(path))
+        synchronize()
+        t = time.perf_counter()
+        model = DeviceModel(Archive.load(path))
+        synchronize()
+        return (time.perf_counter() - t) * 1e3, model.uploaded_bytes
+
+
 def abi_calls(mats, x, runs, warmup=3):
     """Host-side milliseconds of `runs` host-pointer needle2_cq_linear calls (batch 1), cycling over `mats`."""
     for m in mats[:warmup] if len(mats) >= warmup else mats * warmup:
@@ -460,7 +478,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode", "cand"], default=None,
+    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode", "cand", "archive"],
+                    default=None,
                     help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--sweep", action="store_true", help="with --only attn: also time fixed split counts")
     ap.add_argument("--batch", type=int, default=1, help="with --only cq4 / cq2 / int8: activation rows per step")
@@ -491,6 +510,10 @@ def main():
             ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs)
             log(f"decode layer ({seqs} seqs, ctx 2048): eager {ms_e * 1e3:.1f} us, graph {ms_g * 1e3:.1f} us -> "
                 f"{seqs / (min(ms_e, ms_g) * 1e-3):.0f} tokens/s per layer")
+        return
+    if args.only == "archive":
+        ms_u, nb = bench_archive_upload()
+        log(f"archive upload: {ms_u:.1f} ms for {nb} B ({nb / (ms_u * 1e-3) / 1e9:.2f} GB/s)")
         return
     if args.only == "cand":
         for k, v in bench_candidates(args.steps, args.warmup, stream).items():
@@ -595,6 +618,11 @@ def main():
         for k, v in bench_candidates(args.steps, args.warmup, stream).items():
             extra[f"candidates_{k}_us"] = dist_us(v)
         log(f"candidates: { {k: v['median'] for k, v in extra.items() if k.startswith('candidates_')} }")
+
+        ms_u, nb = bench_archive_upload()
+        extra["archive_upload_ms"] = round(ms_u, 2)
+        extra["archive_upload_bytes"] = nb
+        log(f"archive upload (released geometry, 405 tensors): {ms_u:.1f} ms for {nb} B")
 
         for seqs in (64, 1):
             log(f"decode layer: {seqs} sequence(s), ctx 2048, int8-path CQ4 projections + int8-KV attention")

@@ -78,6 +78,17 @@ const char *needle2_gpu_error(void);
 void *needle2_gpu_sdot_create(const uint8_t *packed, const uint16_t *norms, int out, int in, int bits, int group,
                               const float *codebook);
 
+/* needle2_cq_create / needle2_gpu_sdot_create from device-resident packed
+ * codes and norms in the reference's layouts (needle2/native.py:189-197 passes
+ * host pointers): the relayout kernels are enqueued on `stream` and the call
+ * returns without waiting, so a model's matrices can be built from one bulk
+ * copy of its archive. The inputs must stay valid, and the handle unused on
+ * other streams, until `stream` has run them. */
+void *needle2_gpu_cq_create_device(const uint8_t *d_packed, const uint16_t *d_norms, int out, int in, int bits,
+                                   int group, const float *codebook, void *stream);
+void *needle2_gpu_sdot_create_device(const uint8_t *d_packed, const uint16_t *d_norms, int out, int in, int bits,
+                                     int group, const float *codebook, void *stream);
+
 /* Device-resident variants: d_x [batch][in] and d_y [batch][out] are device
  * pointers; work is enqueued on `stream` (hipStream_t, NULL = the handle's
  * stream) and the call returns without waiting. */

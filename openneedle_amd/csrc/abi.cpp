@@ -37,7 +37,7 @@ static bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 // Matrix upload
 // ---------------------------------------------------------------------------
 void Matrix::upload(const uint8_t *packed, const uint16_t *host_norms, int out_, int in_, int bits_, int group_,
-                    const float *cb, hipStream_t s) {
+                    const float *cb, hipStream_t s, bool device_inputs) {
     ND_CHECK(out_ > 0 && in_ > 0, "CQ matrix shape must be positive");
     ND_CHECK(bits_ == 2 || bits_ == 3 || bits_ == 4 || bits_ == 5, "CQ storage bits must be 2, 3, 4, or ternary marker 5");
     ND_CHECK(is_pow2(group_) && group_ >= 8, "CQ group size must be a power of two >= 8");
@@ -69,16 +69,21 @@ void Matrix::upload(const uint8_t *packed, const uint16_t *host_norms, int out_,
     }
     std::memcpy(cb_raw, cb, sizeof(float) * (bits == 5 ? 3 : 1u << bits));
 
+    codes.reserve(size_t(chunks) * n_pad);
+    norms.reserve(size_t(groups) * n_pad);
+    if (device_inputs) {
+        launch_relayout(packed, out, rowbytes, bits, padded, codes.p, n_pad, chunks, s);
+        launch_norms_transpose(host_norms, out, groups, norms.p, n_pad, s);
+        return;
+    }
     DevBuf<uint8_t> raw;
     const size_t raw_bytes = size_t(out) * rowbytes;
     raw.reserve(raw_bytes);
     ND_HIP(hipMemcpyAsync(raw.p, packed, raw_bytes, hipMemcpyHostToDevice, s));
-    codes.reserve(size_t(chunks) * n_pad);
     launch_relayout(raw.p, out, rowbytes, bits, padded, codes.p, n_pad, chunks, s);
     DevBuf<uint16_t> nraw;
     nraw.reserve(size_t(out) * groups);
     ND_HIP(hipMemcpyAsync(nraw.p, host_norms, size_t(out) * groups * 2, hipMemcpyHostToDevice, s));
-    norms.reserve(size_t(groups) * n_pad);
     launch_norms_transpose(nraw.p, out, groups, norms.p, n_pad, s);
     ND_HIP(hipStreamSynchronize(s));
 }
@@ -105,9 +110,12 @@ void Matrix::transform(const float *x, int x_stride, float *rot, int nvec, DevBu
     }
 }
 
-Staging::Staging() { ND_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking)); }
+hipStream_t Staging::stream() {
+    if (!stream_) ND_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    return stream_;
+}
 Staging::~Staging() {
-    if (stream) (void)hipStreamDestroy(stream);
+    if (stream_) (void)hipStreamDestroy(stream_);
 }
 
 // ---------------------------------------------------------------------------
@@ -161,7 +169,7 @@ void upload_candidates(Staging &st, const int32_t *ids, int count, int rows) {
     st.hids.reserve(count);
     st.ids.reserve(count);
     std::memcpy(st.hids.p, ids, size_t(count) * sizeof(int32_t));
-    ND_HIP(hipMemcpyAsync(st.ids.p, st.hids.p, size_t(count) * sizeof(int32_t), hipMemcpyHostToDevice, st.stream));
+    ND_HIP(hipMemcpyAsync(st.ids.p, st.hids.p, size_t(count) * sizeof(int32_t), hipMemcpyHostToDevice, st.stream()));
 }
 
 void CqHandle::candidates_device(const float *d_x, const int32_t *d_ids, int count, float *d_y, hipStream_t s) {
@@ -183,10 +191,10 @@ void CqHandle::candidates_host(const float *x, const int32_t *ids, int count, fl
     st.hy.reserve(count);
     st.y.reserve(count);
     std::memcpy(st.hx.p, x, size_t(m.in) * sizeof(float));
-    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, size_t(m.in) * sizeof(float), hipMemcpyHostToDevice, st.stream));
-    candidates_device(st.x.p, st.ids.p, count, st.y.p, st.stream);
-    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, st.stream));
-    ND_HIP(hipStreamSynchronize(st.stream));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, size_t(m.in) * sizeof(float), hipMemcpyHostToDevice, st.stream()));
+    candidates_device(st.x.p, st.ids.p, count, st.y.p, st.stream());
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, st.stream()));
+    ND_HIP(hipStreamSynchronize(st.stream()));
     std::memcpy(y, st.hy.p, size_t(count) * sizeof(float));
 }
 
@@ -213,10 +221,10 @@ void CqHandle::linear_host(const float *x, float *y, int batch) {
     st.x.reserve(nx);
     st.y.reserve(ny);
     std::memcpy(st.hx.p, x, nx * sizeof(float));
-    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, nx * sizeof(float), hipMemcpyHostToDevice, st.stream));
-    run_device(st.x.p, st.y.p, batch, st.stream);
-    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, ny * sizeof(float), hipMemcpyDeviceToHost, st.stream));
-    ND_HIP(hipStreamSynchronize(st.stream));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, nx * sizeof(float), hipMemcpyHostToDevice, st.stream()));
+    run_device(st.x.p, st.y.p, batch, st.stream());
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, ny * sizeof(float), hipMemcpyDeviceToHost, st.stream()));
+    ND_HIP(hipStreamSynchronize(st.stream()));
     std::memcpy(y, st.hy.p, ny * sizeof(float));
 }
 
@@ -227,11 +235,11 @@ void CqHandle::rows_host(const int64_t *ids, float *y, int count) {
     dids.reserve(count);
     st.rot.reserve(size_t(count) * m.padded);
     st.y.reserve(size_t(count) * m.in);
-    ND_HIP(hipMemcpyAsync(dids.p, ids, size_t(count) * sizeof(int64_t), hipMemcpyHostToDevice, st.stream));
+    ND_HIP(hipMemcpyAsync(dids.p, ids, size_t(count) * sizeof(int64_t), hipMemcpyHostToDevice, st.stream()));
     launch_cq_rows(m.geom(), m.codes.p, m.norms.p, dids.p, count, m.in, m.padded, st.rot.p, st.y.p,
-                   st.stream);
-    ND_HIP(hipMemcpyAsync(y, st.y.p, size_t(count) * m.in * sizeof(float), hipMemcpyDeviceToHost, st.stream));
-    ND_HIP(hipStreamSynchronize(st.stream));
+                   st.stream());
+    ND_HIP(hipMemcpyAsync(y, st.y.p, size_t(count) * m.in * sizeof(float), hipMemcpyDeviceToHost, st.stream()));
+    ND_HIP(hipStreamSynchronize(st.stream()));
 }
 
 // ---------------------------------------------------------------------------
@@ -307,10 +315,10 @@ void SdotHandle::candidates_host(const float *x, const int32_t *ids, int count, 
     st.hy.reserve(count);
     st.y.reserve(count);
     std::memcpy(st.hx.p, x, size_t(m.in) * sizeof(float));
-    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, size_t(m.in) * sizeof(float), hipMemcpyHostToDevice, st.stream));
-    candidates_device(st.x.p, st.ids.p, count, st.y.p, st.stream);
-    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, st.stream));
-    ND_HIP(hipStreamSynchronize(st.stream));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, size_t(m.in) * sizeof(float), hipMemcpyHostToDevice, st.stream()));
+    candidates_device(st.x.p, st.ids.p, count, st.y.p, st.stream());
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, st.stream()));
+    ND_HIP(hipStreamSynchronize(st.stream()));
     std::memcpy(y, st.hy.p, size_t(count) * sizeof(float));
 }
 
@@ -322,10 +330,10 @@ void SdotHandle::linear_host(const float *x, float *y, int batch) {
     st.x.reserve(nx);
     st.y.reserve(ny);
     std::memcpy(st.hx.p, x, nx * sizeof(float));
-    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, nx * sizeof(float), hipMemcpyHostToDevice, st.stream));
-    run_device(st.x.p, st.y.p, batch, st.stream);
-    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, ny * sizeof(float), hipMemcpyDeviceToHost, st.stream));
-    ND_HIP(hipStreamSynchronize(st.stream));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, nx * sizeof(float), hipMemcpyHostToDevice, st.stream()));
+    run_device(st.x.p, st.y.p, batch, st.stream());
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, ny * sizeof(float), hipMemcpyDeviceToHost, st.stream()));
+    ND_HIP(hipStreamSynchronize(st.stream()));
     std::memcpy(y, st.hy.p, ny * sizeof(float));
 }
 
@@ -448,7 +456,7 @@ void *needle2_cq_create(const uint8_t *p, const uint16_t *n, int out, int in, in
     CqHandle *h = nullptr;
     int rc = guarded([&] {
         auto u = std::make_unique<CqHandle>();
-        u->m.upload(p, n, out, in, bits, group, cb, u->st.stream);
+        u->m.upload(p, n, out, in, bits, group, cb, nullptr);
         h = u.release();
     });
     return rc ? nullptr : h;
@@ -485,14 +493,15 @@ void needle2_cq_rows(void *handle, const int64_t *ids, float *y, int count) {
 int needle2_sdot_supported(void) { return 1; }
 
 static void *sdot_create_impl(const uint8_t *p, const uint16_t *n, int out, int in, int bits, int group,
-                              const float *cb, int min_group) {
+                              const float *cb, int min_group, hipStream_t stream = nullptr,
+                              bool device_inputs = false) {
     SdotHandle *h = nullptr;
     int rc = guarded([&] {
         ND_CHECK(bits == 2 || bits == 4, "SDOT requires CQ2/CQ4");
         ND_CHECK(group >= min_group && group <= 131072, "SDOT group size outside the supported range");
         ND_CHECK(bits == 4 || group >= 16, "SDOT CQ2 requires group >= 16");
         auto u = std::make_unique<SdotHandle>();
-        u->m.upload(p, n, out, in, bits, group, cb, u->st.stream);
+        u->m.upload(p, n, out, in, bits, group, cb, stream, device_inputs);
         u->init_tables();
         h = u.release();
     });
@@ -522,9 +531,29 @@ void *needle2_gpu_sdot_create(const uint8_t *p, const uint16_t *n, int out, int 
     return sdot_create_impl(p, n, out, in, bits, group, cb, 8);
 }
 
+// Creation from device-resident packed codes and norms (the reference's
+// layouts): the relayout kernels are enqueued on `stream` and the call returns
+// without waiting, so a whole model's matrices can be built from one bulk copy
+// of its archive; the inputs must stay valid until the stream has run them.
+void *needle2_gpu_cq_create_device(const uint8_t *d_packed, const uint16_t *d_norms, int out, int in, int bits,
+                                   int group, const float *cb, void *stream) {
+    CqHandle *h = nullptr;
+    int rc = guarded([&] {
+        auto u = std::make_unique<CqHandle>();
+        u->m.upload(d_packed, d_norms, out, in, bits, group, cb, static_cast<hipStream_t>(stream), true);
+        h = u.release();
+    });
+    return rc ? nullptr : h;
+}
+
+void *needle2_gpu_sdot_create_device(const uint8_t *d_packed, const uint16_t *d_norms, int out, int in, int bits,
+                                     int group, const float *cb, void *stream) {
+    return sdot_create_impl(d_packed, d_norms, out, in, bits, group, cb, 8, static_cast<hipStream_t>(stream), true);
+}
+
 int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {
     auto *h = static_cast<CqHandle *>(handle);
-    return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream); });
+    return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream()); });
 }
 
 // Prefill GEMM: d_y[m][out] = d_x[m][in] through the matrix on fp16 MFMA
@@ -534,7 +563,7 @@ int needle2_gpu_cq_gemm_device(void *handle, const float *d_x, float *d_y, int m
     return guarded([&] {
         ND_CHECK(handle, "null CQ handle");
         auto *h = static_cast<CqHandle *>(handle);
-        h->gemm_device(d_x, d_y, m, stream ? static_cast<hipStream_t>(stream) : h->st.stream, nullptr, nullptr);
+        h->gemm_device(d_x, d_y, m, stream ? static_cast<hipStream_t>(stream) : h->st.stream(), nullptr, nullptr);
     });
 }
 
@@ -547,14 +576,14 @@ int needle2_gpu_cq_gemm_timed(void *handle, const float *d_x, float *d_y, int m,
         ND_CHECK(handle, "null CQ handle");
         ND_CHECK(repeat >= 1, "repeat must be >= 1");
         auto *h = static_cast<CqHandle *>(handle);
-        h->gemm_device(d_x, d_y, m, stream ? static_cast<hipStream_t>(stream) : h->st.stream,
+        h->gemm_device(d_x, d_y, m, stream ? static_cast<hipStream_t>(stream) : h->st.stream(),
                        static_cast<hipEvent_t>(gemm_start), static_cast<hipEvent_t>(gemm_stop), repeat);
     });
 }
 
 int needle2_gpu_sdot_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {
     auto *h = static_cast<SdotHandle *>(handle);
-    return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream); });
+    return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream()); });
 }
 
 // Candidate rows: y[i] = row ids[i] of the product for one input vector, as
@@ -573,7 +602,7 @@ int needle2_gpu_cq_candidates_device(void *handle, const float *d_x, const int32
         ND_CHECK(handle, "null CQ handle");
         ND_CHECK(count > 0, "candidates must be nonempty");
         auto *h = static_cast<CqHandle *>(handle);
-        h->candidates_device(d_x, d_ids, count, d_y, stream ? static_cast<hipStream_t>(stream) : h->st.stream);
+        h->candidates_device(d_x, d_ids, count, d_y, stream ? static_cast<hipStream_t>(stream) : h->st.stream());
     });
 }
 
@@ -590,7 +619,7 @@ int needle2_gpu_sdot_candidates_device(void *handle, const float *d_x, const int
         ND_CHECK(handle, "null SDOT handle");
         ND_CHECK(count > 0, "candidates must be nonempty");
         auto *h = static_cast<SdotHandle *>(handle);
-        h->candidates_device(d_x, d_ids, count, d_y, stream ? static_cast<hipStream_t>(stream) : h->st.stream);
+        h->candidates_device(d_x, d_ids, count, d_y, stream ? static_cast<hipStream_t>(stream) : h->st.stream());
     });
 }
 
@@ -633,7 +662,7 @@ void *needle2_gpu_sdot_plan_create(void *const *handles, int count, const float 
 
 int needle2_gpu_plan_run(void *plan, void *stream) {
     auto *p = static_cast<Plan *>(plan);
-    return guarded([&] { plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream); });
+    return guarded([&] { plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream()); });
 }
 
 // As needle2_gpu_plan_run, also recording two events on the stream right
@@ -641,7 +670,7 @@ int needle2_gpu_plan_run(void *plan, void *stream) {
 int needle2_gpu_plan_run_timed(void *plan, void *stream, void *gemv_start, void *gemv_stop) {
     auto *p = static_cast<Plan *>(plan);
     return guarded([&] {
-        plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream, static_cast<hipEvent_t>(gemv_start),
+        plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream(), static_cast<hipEvent_t>(gemv_start),
                  static_cast<hipEvent_t>(gemv_stop));
     });
 }

@@ -44,16 +44,19 @@ struct Matrix {
     DevBuf<uint4> codes;
     DevBuf<uint16_t> norms;
 
+    // packed [out][rowbytes] and norms [out][groups] in host memory (copied, then waited for), or with
+    // `device_inputs` in device memory (read by the relayout kernels on `s`; nothing waited for).
     void upload(const uint8_t *packed, const uint16_t *norms, int out, int in, int bits, int group, const float *cb,
-                hipStream_t s);
+                hipStream_t s, bool device_inputs = false);
     CqGeom geom() const;
     // rot[v] = FWHT(x[v]) over dev positions for nvec vectors.
     void transform(const float *x, int x_stride, float *rot, int nvec, DevBuf<float> &big, hipStream_t s) const;
 };
 
-// Per-handle stream and grow-only staging buffers.
+// Per-handle stream (created on first use: creating one costs ~150 us, and
+// device-resident callers pass their own) and grow-only staging buffers.
 struct Staging {
-    hipStream_t stream = nullptr;
+    hipStream_t stream();
     DevBuf<float> x, rot, y, big, xs, xst;
     DevBuf<int32_t> q;
     DevBuf<_Float16> xh;  // fp16 transformed activations of the prefill GEMM
@@ -63,10 +66,13 @@ struct Staging {
     DevBuf<float> yfull;    // all outputs, when most rows are candidates
     HostBuf<float> hx, hy;
     HostBuf<int32_t> hids;
-    Staging();
+    Staging() = default;
     ~Staging();
     Staging(const Staging &) = delete;
     Staging &operator=(const Staging &) = delete;
+
+  private:
+    hipStream_t stream_ = nullptr;
 };
 
 // Rows ids[0..count) of a matrix as a compact matrix of n_pad rows (gathered

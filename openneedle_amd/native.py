@@ -68,6 +68,8 @@ def _library():
     _bind(lib, "needle2_gpu_sdot_create", [_P, _P, _I, _I, _I, _I, _P], _P)
     _bind(lib, "needle2_gpu_cq_linear_device", [_P, _P, _P, _I, _P], _I)
     _bind(lib, "needle2_gpu_sdot_linear_device", [_P, _P, _P, _I, _P], _I)
+    _bind(lib, "needle2_gpu_cq_create_device", [_P, _P, _I, _I, _I, _I, _P, _P], _P)
+    _bind(lib, "needle2_gpu_sdot_create_device", [_P, _P, _I, _I, _I, _I, _P, _P], _P)
     for name in ("needle2_gpu_cq_candidates", "needle2_gpu_sdot_candidates"):
         _bind(lib, name, [_P, _P, _P, _I, _P], _I)
         _bind(lib, name + "_device", [_P, _P, _P, _I, _P, _P], _I)
@@ -139,7 +141,11 @@ class NativeCQ:
     ``bits=5`` denotes the official signed ternary crumb storage, with 3 centroids.
     """
 
-    def __init__(self, packed, norms, shape, bits, group_size, codebook):
+    def __init__(self, packed, norms, shape, bits, group_size, codebook, *, device=None, int8: bool = False):
+        """``device``: optional (d_packed, d_norms, stream) device pointers holding the same packed codes and
+        norms; the handles are then built from them on ``stream`` without copying (the caller synchronizes the
+        stream before freeing them or using the matrix elsewhere). ``int8``: also build the int8 (SDOT) handle
+        now, for groups the GPU int8 path takes."""
         self.shape = tuple(int(v) for v in shape)
         if len(self.shape) != 2 or min(self.shape) <= 0:
             raise ValueError("NativeCQ requires a positive two-dimensional matrix shape")
@@ -170,11 +176,25 @@ class NativeCQ:
                 if np.any(((self.packed >> shift) & 3) == 2):
                     raise ValueError("Invalid ternary crumb code 2")
         self._lib = _library()
-        self._handle = self._lib.needle2_cq_create(self.packed.ctypes.data, self.norms.ctypes.data,
-                                                   out, dim, self.bits, self.group_size,
-                                                   self.codebook.ctypes.data)
+        if device is None:
+            self._handle = self._lib.needle2_cq_create(self.packed.ctypes.data, self.norms.ctypes.data,
+                                                       out, dim, self.bits, self.group_size,
+                                                       self.codebook.ctypes.data)
+        else:
+            d_packed, d_norms, stream = device
+            stream = stream.ptr if isinstance(stream, Stream) else stream
+            self._handle = self._lib.needle2_gpu_cq_create_device(d_packed, d_norms, out, dim, self.bits,
+                                                                  self.group_size, self.codebook.ctypes.data, stream)
         if not self._handle:
             raise MemoryError(f"Could not construct native CQ matrix ({last_error()})")
+        if int8 and self.bits in (2, 4) and self.group_size >= (8 if self.bits == 4 else 16):
+            if device is None:
+                self._sdot(True)
+            else:
+                self._sdot_handle = self._lib.needle2_gpu_sdot_create_device(
+                    d_packed, d_norms, out, dim, self.bits, self.group_size, self.codebook.ctypes.data, stream)
+                if not self._sdot_handle:
+                    raise RuntimeError(f"could not construct SDOT matrix ({last_error()})")
 
     @classmethod
     def from_record(cls, record):
@@ -360,10 +380,28 @@ class DeviceArray:
         _check(self._lib.needle2_gpu_memcpy(out.ctypes.data, self.ptr + offset, out.nbytes, 1), "download")
         return out
 
+    def view(self, offset: int, nbytes: int) -> "DeviceView":
+        """Bytes [offset, offset + nbytes) of this allocation (which the view keeps alive)."""
+        assert 0 <= offset and offset + nbytes <= self.nbytes
+        return DeviceView(self, offset, nbytes)
+
     def __del__(self):
         if getattr(self, "ptr", None):
             self._lib.needle2_gpu_free(self.ptr)
             self.ptr = None
+
+
+class DeviceView(DeviceArray):
+    """A sub-range of a :class:`DeviceArray`; frees nothing itself."""
+
+    def __init__(self, base: DeviceArray, offset: int, nbytes: int):
+        self._lib = base._lib
+        self._base = base
+        self.nbytes = int(nbytes)
+        self.ptr = base.ptr + int(offset)
+
+    def __del__(self):
+        self.ptr = None
 
 
 class Stream:

@@ -49,3 +49,26 @@ def permute_like_reference(q, bits, group):
         dst = (i // chunk) * chunk + (i % width) * 16 + (i % chunk) // width
         out[g0 + dst] = q[g0 + i]
     return out
+
+
+# ---------------------------------------------------------------------------
+# .cact archives
+# ---------------------------------------------------------------------------
+def tiny_archive_bytes():
+    """The one-layer, one-engram archive that the reference's archive-validation tests build by hand
+    (tests/test_archive_validation.py:10-30 of the reference): CQ2 g8 embedding of 64 zero bytes, every other
+    tensor FP32 zeros, linspace(-1, 1, 28) codebook."""
+    from openneedle_amd import archive as A
+    layer = [(8,), (8, 8), (4, 8), (4, 8), (4,), (4,), (8, 8), (8, 8), (8,), (1,), (8,), (8,), (8,), (8,)]
+    mhc = [(1,), (1,), (1,), (1, 2), (1, 2), (1, 2, 2), (2, 16), (2, 16), (4, 16)]
+    shapes = [(16, 8)] + layer + mhc + [(8, 4), (8, 8), (8, 8), (4, 8), (8,)]
+    header = (A.TAG, len(shapes), 28, 5, 8, 16, 8, 2, 1, 1, 4, 64, 8, 2, 4, 4, 2, 4, 3, 2, 2, 3, 0, 0, 1, 0, 0, 0, 0,
+              100000.0)
+    records = [(A.CQ, shapes[0], bytes(64), 8, 2)]
+    records += [(A.FP32, s, np.zeros(s, "<f4").tobytes(), 0, 0) for s in shapes[1:]]
+    return A.pack_archive(header, np.linspace(-1, 1, 28, dtype="<f4"), records)
+
+
+def official_like_archive(seed=0, tokenizer_bytes=115215):
+    from openneedle_amd.archive import synthetic_released
+    return synthetic_released(seed, tokenizer_bytes)
