@@ -339,6 +339,29 @@ def bench_archive_upload():
         return (time.perf_counter() - t) * 1e3, model.uploaded_bytes
 
 
+def bench_engine(tokens=64):
+    """NativeEngine.step on the GPU for the released geometry (27 layers, d_model 512, random contents, KV window
+    256): whole-token latency as the caller sees it (host pointers: the token in, 8192 logits out, one wait per
+    token), fp32 and int8 KV, after 16 untimed tokens. Returns {kv: (tokens/s, [ms per token])}."""
+    from openneedle_amd.archive import Archive, synthetic_released
+    from openneedle_amd.engine import NativeEngine
+    archive = Archive(synthetic_released(seed=3, tokenizer_bytes=0))
+    out = {}
+    for kv in ("fp32", "int8"):
+        e = NativeEngine(archive, kv_cache=kv)
+        for i in range(16):
+            e.step((i * 131) % 8192)
+        times = []
+        t0 = time.perf_counter()
+        for i in range(tokens):
+            t = time.perf_counter_ns()
+            e.step((i * 37 + 11) % 8192)
+            times.append((time.perf_counter_ns() - t) / 1e6)
+        out[kv] = (tokens / (time.perf_counter() - t0), times)
+        del e
+    return out
+
+
 def abi_calls(mats, x, runs, warmup=3):
     """Host-side milliseconds of `runs` host-pointer needle2_cq_linear calls (batch 1), cycling over `mats`."""
     for m in mats[:warmup] if len(mats) >= warmup else mats * warmup:
@@ -467,6 +490,19 @@ def cpu_baseline(budget_s=12.0, others=True):
         "what": "Engine::compute_attention (int8 K/V, one engine per sequence, 8 head work items per call)",
         "us_per_sequence": _spread(med / seqs, p10 / seqs, p90 / seqs, 1e6),
         "us_64_sequences": round(med / seqs * 64 * 1e6, 1), "runs": n}
+    from openneedle_amd.archive import Archive, synthetic_released
+    if kind == "reference":
+        archive = Archive(synthetic_released(seed=3, tokenizer_bytes=0))
+        for kv in ("fp32", "int8"):
+            eng = oracle.RefEngine(archive, 0, kv == "int8", threads=cores)
+            for i in range(4):
+                eng.step((i * 131) % 8192)
+            tok = iter(range(1 << 30))
+            med, p10, p90, n = _cpu_time(lambda: eng.step((next(tok) * 37 + 11) % 8192), 3.0, warmup=0)
+            w[f"engine_{kv}_kv"] = {
+                "what": "the reference Engine::step (released geometry, random contents, batch 1, logits out)",
+                "tokens_per_s": round(1 / med, 1), "ms_per_token": _spread(med, p10, p90), "runs": n}
+            del eng
     out["workloads"] = w
     return out
 
@@ -478,7 +514,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode", "cand", "archive"],
+    ap.add_argument("--only", choices=["cq4", "cq2", "int8", "attn", "prefill", "decode", "cand", "archive",
+                                       "engine"],
                     default=None,
                     help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--sweep", action="store_true", help="with --only attn: also time fixed split counts")
@@ -510,6 +547,10 @@ def main():
             ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs)
             log(f"decode layer ({seqs} seqs, ctx 2048): eager {ms_e * 1e3:.1f} us, graph {ms_g * 1e3:.1f} us -> "
                 f"{seqs / (min(ms_e, ms_g) * 1e-3):.0f} tokens/s per layer")
+        return
+    if args.only == "engine":
+        for kv, (tps, ms) in bench_engine().items():
+            log(f"engine {kv} KV: {tps:.0f} tokens/s, per token {dist_us(ms)} us")
         return
     if args.only == "archive":
         ms_u, nb = bench_archive_upload()
@@ -618,6 +659,12 @@ def main():
         for k, v in bench_candidates(args.steps, args.warmup, stream).items():
             extra[f"candidates_{k}_us"] = dist_us(v)
         log(f"candidates: { {k: v['median'] for k, v in extra.items() if k.startswith('candidates_')} }")
+
+        log("engine: NativeEngine.step, released geometry (27 layers), batch 1")
+        for kv, (tps, ms) in bench_engine().items():
+            extra[f"engine_{kv}_kv_tokens_per_s"] = round(tps, 1)
+            extra[f"engine_{kv}_kv_token_us"] = dist_us(ms)
+            log(f"engine {kv} KV: {tps:.0f} tokens/s")
 
         ms_u, nb = bench_archive_upload()
         extra["archive_upload_ms"] = round(ms_u, 2)

@@ -316,19 +316,24 @@ RELEASED_GEOMETRY = dict(vocab_size=8192, d_model=512, num_heads=8, num_kv_heads
                          num_engram_tables=4, engram_conv_taps=4, engram_conv_dilation=3)
 
 
-def synthetic_released(seed: int = 0, tokenizer_bytes: int = 115215) -> bytes:
-    """An archive with the released model's geometry and precision map, random contents.
+def synthetic_model(geometry: dict, engram_layers=(), engram_orders=(), kv_window: int = 0, group: int = 128,
+                    seed: int = 0, heads: bool = False, tokenizer_bytes: int = 0, rope_theta: float = 100000.0,
+                    vector_scale: float = 0.1) -> bytes:
+    """An archive of the given geometry with the released precision map and random contents.
 
-    embedding and mhc_phi* CQ4 g128; attention and engram matrices CQ2 g128; everything else FP16; probe heads
-    (contrastive with 128 outputs, confidence) and a RAW tokenizer. Codes are uniform random bytes, norms fp16
-    U[0.005, 0.05], FP16 values N(0, 0.1); the codebook is the released header codebook."""
+    embedding and mhc_phi* CQ4, attention and engram matrices CQ2 (all at ``group``), everything else FP16;
+    optional probe heads (contrastive with 128 outputs, confidence) and RAW tokenizer. Codes are uniform random
+    bytes, norms fp16 U[0.005, 0.05], FP16 values N(0, vector_scale); the codebook is the released header
+    codebook."""
     rng = np.random.default_rng(seed)
-    g = RELEASED_GEOMETRY
+    g = dict(geometry)
     d = g["d_model"]
-    shapes = canonical_shapes(dict(g, engram_layers=[2, 15], engram_orders=[2, 3]))
-    shapes.update({"heads.manifest": (2,), "contrastive_head.probes": (4, d), "contrastive_head.proj": (128, 4 * d),
-                   "contrastive_head.bias": (128,), "confidence_head.probes": (8, d),
-                   "confidence_head.proj": (1, 8 * d), "confidence_head.bias": (1,)})
+    shapes = canonical_shapes(dict(g, engram_layers=list(engram_layers), engram_orders=list(engram_orders)))
+    if heads:
+        shapes.update({"heads.manifest": (2,), "contrastive_head.probes": (4, d),
+                       "contrastive_head.proj": (128, 4 * d), "contrastive_head.bias": (128,),
+                       "confidence_head.probes": (8, d), "confidence_head.proj": (1, 8 * d),
+                       "confidence_head.bias": (1,)})
     records = []
     for name, shape in shapes.items():
         if name == "embedding" or name.startswith("mhc_phi"):
@@ -339,18 +344,30 @@ def synthetic_released(seed: int = 0, tokenizer_bytes: int = 115215) -> bytes:
             bits = 0
         if bits:
             rows, cols = shape
-            padded = formats.padded_width(cols, 128)
+            padded = formats.padded_width(cols, group)
             packed = rng.integers(0, 256, size=(rows, padded * bits // 8), dtype=np.uint8)
-            norms = rng.uniform(0.005, 0.05, size=(rows, padded // 128)).astype("<f2")
-            records.append((CQ, shape, packed.tobytes() + norms.tobytes(), 128, bits))
+            norms = rng.uniform(0.005, 0.05, size=(rows, padded // group)).astype("<f2")
+            records.append((CQ, shape, packed.tobytes() + norms.tobytes(), group, bits))
         else:
             values = np.array([1, 2], "<f2") if name == "heads.manifest" else \
-                (rng.normal(size=shape) * 0.1).astype("<f2")
+                (rng.normal(size=shape) * vector_scale).astype("<f2")
             records.append((FP16, shape, values.tobytes(), 0, 0))
-    records.append((RAW, (), rng.integers(0, 256, tokenizer_bytes, dtype=np.uint8).tobytes(), 0, 0))
-    header = (TAG, len(records), 28, 256, 8, *[g[k] for k in GEOMETRY_FIELDS], 2, 2, 3, 0, 0, 2, 2, 15, 0, 0,
-              100000.0)
+    if tokenizer_bytes:
+        records.append((RAW, (), rng.integers(0, 256, tokenizer_bytes, dtype=np.uint8).tobytes(), 0, 0))
+    orders = (list(engram_orders) + [0, 0, 0, 0])[:4]
+    sites = (list(engram_layers) + [0, 0, 0, 0])[:4]
+    header = (TAG, len(records), 28, kv_window, 8, *[g[k] for k in GEOMETRY_FIELDS], len(engram_orders), *orders,
+              len(engram_layers), *sites, rope_theta)
     return pack_archive(header, formats._HEADER_CODEBOOK, records)
+
+
+def synthetic_released(seed: int = 0, tokenizer_bytes: int = 115215) -> bytes:
+    """An archive with the released model's geometry and precision map (embedding and mhc_phi* CQ4 g128;
+    attention and engram matrices CQ2 g128; everything else FP16; probe heads and a RAW tokenizer), random
+    contents: :func:`synthetic_model` with the released header's geometry, KV window 256, engram sites 2 and
+    15 of orders 2 and 3."""
+    return synthetic_model(RELEASED_GEOMETRY, engram_layers=(2, 15), engram_orders=(2, 3), kv_window=256,
+                           group=128, seed=seed, heads=True, tokenizer_bytes=tokenizer_bytes)
 
 
 @dataclass

@@ -123,6 +123,11 @@ Staging::~Staging() {
 // ---------------------------------------------------------------------------
 void CqHandle::gemv(const uint4 *codes, const uint16_t *norms, int rows, int n_pad, const float *d_x, float *d_y,
                     int batch, hipStream_t s) {
+    matrix_gemv(m, st, codes, norms, rows, n_pad, d_x, d_y, batch, s);
+}
+
+void matrix_gemv(const Matrix &m, Staging &st, const uint4 *codes, const uint16_t *norms, int rows, int n_pad,
+                 const float *d_x, float *d_y, int batch, hipStream_t s) {
     const float *act = d_x;
     if (!gemv_fuses_fwht(m.group)) {
         st.rot.reserve(size_t(batch) * m.dev);
@@ -797,63 +802,6 @@ int needle2_gpu_device_info(char *buf, int len) {
                         ";" + std::to_string(prop.totalGlobalMem) + ";" + std::to_string(prop.clockRate);
         std::snprintf(buf, size_t(len), "%s", s.c_str());
     });
-}
-
-// ===================== engine (not on the GPU path yet) ==================
-// NativeEngine (needle2/native.py:307-663) binds these lazily; creation fails
-// through the reference's own error channel (engine.cpp:1499-1547).
-static const char *kNoEngine =
-    "needle2_engine_*: the gfx950 library provides the CQ/SDOT kernels and batched int8-KV attention; "
-    "the whole-model engine is not part of this library";
-
-const char *needle2_engine_error(void) { return get_error(); }
-void *needle2_engine_create(const void *, const void *, int, int, int) {
-    set_error(kNoEngine);
-    return nullptr;
-}
-void needle2_engine_destroy(void *) {}
-void needle2_engine_set_lookup(void *, int) {}
-int needle2_engine_set_sdot(void *) {
-    set_error(kNoEngine);
-    return -1;
-}
-void needle2_engine_reset(void *, int) {}
-int needle2_engine_cache_prefix(void *) {
-    set_error(kNoEngine);
-    return -1;
-}
-int needle2_engine_reset_to_prefix(void *) {
-    set_error(kNoEngine);
-    return -1;
-}
-int needle2_engine_step(void *, int, float *, float *) {
-    set_error(kNoEngine);
-    return -1;
-}
-int needle2_engine_prefill(void *, const int *, int, int, float *, float *) {
-    set_error(kNoEngine);
-    return -1;
-}
-int needle2_engine_step_candidates(void *, int, const int *, int, float *, float *) {
-    set_error(kNoEngine);
-    return -1;
-}
-int needle2_engine_decode_loop(void *, int, int, const void *, int *, int *) {
-    set_error(kNoEngine);
-    return -1;
-}
-int needle2_engine_import(void *, int, int, const int *, const int *, int, const float *, const float *) {
-    set_error(kNoEngine);
-    return -1;
-}
-int needle2_engine_set_int8_kv(void *, int) {
-    set_error(kNoEngine);
-    return -1;
-}
-size_t needle2_engine_kv_storage_bytes(void *) { return 0; }
-int needle2_engine_project_candidates(void *, const float *, const int *, int, float *) {
-    set_error(kNoEngine);
-    return -1;
 }
 
 }  // extern "C"

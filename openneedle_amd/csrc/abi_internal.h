@@ -75,6 +75,11 @@ struct Staging {
     hipStream_t stream_ = nullptr;
 };
 
+// The FP32 GEMV over rows [0, rows) of a device-layout matrix with m's
+// geometry (codes / norms: m's own or a compact copy), staging in `st`.
+void matrix_gemv(const Matrix &m, Staging &st, const uint4 *codes, const uint16_t *norms, int rows, int n_pad,
+                 const float *d_x, float *d_y, int batch, hipStream_t s);
+
 // Rows ids[0..count) of a matrix as a compact matrix of n_pad rows (gathered
 // into st.gcodes / st.gnorms), or none when most rows are asked for.
 struct Candidates {

@@ -1,0 +1,737 @@
+// Single-sequence decode engine on the GPU behind the reference's
+// needle2_engine_* ABI (needle2/csrc/engine.cpp:340-1044, 1499-1548;
+// NativeEngine, needle2/native.py:307-663).
+//
+// One step (engine.cpp:968-1044) runs on the handle's stream as: embedding
+// row, engram rows / projections / conv, then per layer the mHC projections,
+// the mixing kernel, the fused Q|K|V|gate GEMV, the q/k norms + RoPE + KV
+// store kernel, attention, the gate kernel, the out-projection GEMV and the
+// post kernel (attention residual, Hadamard MLP, Sinkhorn routing, lane
+// mixing, next layer's rms); then the final norm and the LM-head GEMV. The
+// CQ matrices are the caller's handles (borrowed, as the reference borrows
+// its CQ pointers) and run through the library's bit-exact GEMV kernels with
+// the engine's own staging; dense tensors are copied to device memory at
+// creation. The host computes what depends only on the position and the
+// token history (slot lists, RoPE angles with std::cos / std::sin, engram
+// hashes) and uploads it once per step.
+#include "abi_internal.h"
+#include "attn.h"
+#include "engine.h"
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace nd {
+
+namespace {
+
+// needle2/csrc/engine.cpp:14-19 (layouts must match the reference's).
+struct TensorDescC {
+    void *cq;
+    const float *data;
+    int rows, cols;
+};
+struct EngineConfigC {
+    int vocab, dim, heads, kvheads, layers, head_dim, max_seq, hada, lanes, window;
+    int slots, subdim, tables, taps, dilation, num_orders, orders[4], num_sites, sites[4];
+    float rope_theta;
+};
+
+thread_local std::string engine_error;
+
+// One matrix tensor of the model: a CQ handle or dense fp32 rows on the device.
+struct Mat {
+    const Matrix *cq = nullptr;
+    const float *dense = nullptr;
+    int rows = 0, cols = 0;
+};
+
+// Row tiles of several CQ matrices that share one input, run as one GEMV
+// launch (matrices of one geometry) after at most one activation transform.
+struct GemvGroup {
+    struct Piece {
+        const Matrix *m;
+        int first, rows;  // rows [first, first + rows) of m
+        float *y;         // receives the piece's whole row tiles, from tile first / 256
+    };
+    const Matrix *m0 = nullptr;
+    DevBuf<uint8_t> jobs;
+    DevBuf<float> rot, big;
+    int njobs = 0, blocks = 0;
+    const float *x = nullptr;
+    CqJob job0{};
+
+    static bool compatible(const Matrix &a, const Matrix &b) {
+        return a.in == b.in && a.bits == b.bits && a.group == b.group &&
+               std::memcmp(a.lut, b.lut, sizeof a.lut) == 0;
+    }
+
+    void build(const std::vector<Piece> &pieces, const float *input) {
+        m0 = pieces[0].m;
+        x = input;
+        const bool fused = gemv_fuses_fwht(m0->group);
+        if (!fused) rot.reserve(m0->dev);
+        const float *act = fused ? input : rot.p;
+        std::vector<CqJob> host;
+        for (const Piece &p : pieces) {
+            ND_CHECK(compatible(*m0, *p.m), "internal: GEMV group of mixed geometry");
+            const int tile0 = p.first / kRowsPerBlock;
+            const int tile1 = (p.first + p.rows - 1) / kRowsPerBlock;
+            const int tiles = tile1 - tile0 + 1;
+            const int rows = std::min(tiles * kRowsPerBlock, p.m->out - tile0 * kRowsPerBlock);
+            host.push_back(CqJob{p.m->codes.p + size_t(tile0) * p.m->chunks * kRowsPerBlock,
+                                 p.m->norms.p + size_t(tile0) * p.m->groups * kRowsPerBlock, act, p.y, rows,
+                                 tiles * kRowsPerBlock, blocks, 1});
+            blocks += tiles;
+        }
+        njobs = static_cast<int>(host.size());
+        job0 = host[0];
+        if (njobs > 1) {
+            jobs.reserve(host.size() * sizeof(CqJob));
+            ND_HIP(hipMemcpy(jobs.p, host.data(), host.size() * sizeof(CqJob), hipMemcpyHostToDevice));
+        }
+    }
+
+    void run(hipStream_t s) {
+        if (!gemv_fuses_fwht(m0->group)) {
+            if (gemv_prepass(m0->group))
+                launch_rot_many(x, nullptr, 1, 1, m0->in, m0->dev, m0->group, m0->scale, rot.p, s);
+            else
+                m0->transform(x, m0->in, rot.p, 1, big, s);
+        }
+        if (njobs > 1)
+            launch_cq_gemv(m0->geom(), CqJob{}, reinterpret_cast<const CqJob *>(jobs.p), njobs, blocks, s);
+        else
+            launch_cq_gemv(m0->geom(), job0, nullptr, 0, blocks, s);
+    }
+};
+
+// GEMVs of several matrices over one input: CQ matrices in as few groups as
+// their geometries allow, dense ones through the dense kernel.
+struct Projection {
+    std::vector<std::unique_ptr<GemvGroup>> groups;
+    struct Dense {
+        const float *w;
+        int cols, first, rows;
+        float *y;
+    };
+    std::vector<Dense> dense;
+    const float *x = nullptr;
+
+    // (matrix, first row, rows, output)
+    void add(const Mat &m, int first, int rows, float *y, std::vector<std::vector<GemvGroup::Piece>> &pending) {
+        if (!m.cq) {
+            dense.push_back(Dense{m.dense, m.cols, first, rows, y});
+            return;
+        }
+        for (auto &g : pending)
+            if (GemvGroup::compatible(*g[0].m, *m.cq)) {
+                g.push_back({m.cq, first, rows, y});
+                return;
+            }
+        pending.push_back({{m.cq, first, rows, y}});
+    }
+    void finish(std::vector<std::vector<GemvGroup::Piece>> &pending, const float *input) {
+        x = input;
+        for (auto &p : pending) {
+            groups.push_back(std::make_unique<GemvGroup>());
+            groups.back()->build(p, input);
+        }
+    }
+    void run(hipStream_t s) {
+        for (auto &g : groups) g->run(s);
+        for (auto &d : dense) launch_eng_dense(d.w, d.cols, d.first, d.rows, x, d.y, s);
+    }
+};
+
+}  // namespace
+
+struct GpuEngine {
+    EngineConfigC c{};
+    int abits = 0, position = 0, prefix = 0, capacity = 0, engring = 1, history_cap = 1;
+    bool int8_kv = false;
+    std::vector<int> history;
+    std::vector<float> rope_div;
+    std::vector<Mat> mats;                 // per tensor (matrix tensors only)
+    std::vector<std::unique_ptr<DevBuf<float>>> dense;  // device copies of dense tensors
+    std::vector<const float *> dptr;       // per tensor: device fp32 data (dense) or null
+    hipStream_t stream = nullptr;
+    EngineDims dims{};
+    EngineBufs b{};
+    DevBuf<float> work;
+    DevBuf<int> slots;
+    DevBuf<int8_t> kv8;
+    DevBuf<float> kv32, kvs;
+    std::vector<KvLayer> kv;
+    std::vector<LayerDev> layer;
+    MhcDev mh{};
+    DevBuf<StepParams> params;
+    HostBuf<StepParams> hparams;
+    DevBuf<float> logits, part, embed_z, row_scratch;
+    HostBuf<float> hlogits, hhidden;
+    std::vector<Projection> mhc_proj, qkvg, oproj;
+    std::vector<std::array<int, 3>> mhc_row;
+    const float *phi[3] = {nullptr, nullptr, nullptr};  // dense mHC matrices (null: CQ)
+    std::vector<Projection> engram_kv;
+    Projection lm_head;
+    Staging st;  // the engine's own staging (candidate rows)
+
+    int ti(int l) const { return 1 + 14 * l; }
+    int mh0() const { return 1 + 14 * c.layers; }
+    int engram_base() const { return mh0() + 9; }
+    int final_norm() const { return engram_base() + 4 * c.num_sites; }
+
+    GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count, int activation_bits);
+    ~GpuEngine() {
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+    void reset(int prefix_len);
+    int cache_slot(int pos) const {
+        return !c.window ? pos : pos < prefix ? pos : prefix + (pos - prefix) % c.window;
+    }
+    void step(int token, float *logits_out, float *hidden_out);
+    void project_candidates(const int *candidates, int count, float *out);
+    size_t kv_storage_bytes() const { return kv8.n + kv32.n * sizeof(float) + kvs.n * sizeof(float); }
+};
+
+GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count, int activation_bits)
+    : c(cfg), abits(activation_bits) {
+    ND_CHECK(td && count > 0, "engine: no tensors");
+    ND_CHECK(abits == 0 || abits == 8, "engine: activation bits must be 0 or 8");
+    const int D = c.dim, N = c.lanes, HD = c.head_dim, A = c.heads * HD, K = c.kvheads * HD;
+    ND_CHECK(D > 0 && (N == 1 || N == 2 || N == 4 || N == 8) && c.layers > 0 && c.heads > 0 && c.kvheads > 0 &&
+                 c.heads % c.kvheads == 0 && c.heads / c.kvheads <= 8,
+             "engine: unsupported geometry (mHC lanes 1, 2, 4 or 8; at most 8 heads per kv head)");
+    ND_CHECK(HD % 4 == 0 && HD <= 2 * kEngMaxHalfHd && D <= 4096 && c.hada >= D && c.hada <= 4096 &&
+                 (c.hada & (c.hada - 1)) == 0,
+             "engine: unsupported head / Hadamard geometry");
+    ND_CHECK(c.num_sites >= 0 && c.num_sites <= kEngMaxSites && c.num_orders >= 0 && c.num_orders <= 4,
+             "engine: unsupported engram geometry");
+    ND_CHECK(!c.num_sites || (c.tables > 0 && c.tables <= kEngMaxTables && c.num_orders > 0 &&
+                              c.tables % c.num_orders == 0 && c.tables * c.subdim == D && c.taps > 0 &&
+                              c.taps <= kEngMaxTaps && c.dilation > 0),
+             "engine: unsupported engram geometry");
+    ND_CHECK(count >= final_norm() + 1, "engine: tensor count does not match the geometry");
+    ND_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+
+    // tensors: matrices keep the caller's CQ handle; dense data goes to the device as fp32
+    mats.resize(count);
+    dense.resize(count);
+    dptr.assign(count, nullptr);
+    for (int i = 0; i < count; ++i) {
+        mats[i].rows = td[i].rows;
+        mats[i].cols = td[i].cols;
+        if (td[i].cq) {
+            mats[i].cq = &static_cast<CqHandle *>(td[i].cq)->m;
+        } else {
+            ND_CHECK(td[i].data, "engine: tensor without data");
+            dense[i] = std::make_unique<DevBuf<float>>();
+            dense[i]->reserve(size_t(td[i].rows) * td[i].cols);
+            ND_HIP(hipMemcpy(dense[i]->p, td[i].data, size_t(td[i].rows) * td[i].cols * sizeof(float),
+                             hipMemcpyHostToDevice));
+            dptr[i] = dense[i]->p;
+            mats[i].dense = dense[i]->p;
+        }
+    }
+    auto vec = [&](int i) {
+        ND_CHECK(dptr[i], "engine: vector tensors must be dense");
+        return dptr[i];
+    };
+    auto mat = [&](int i, int rows, int cols) -> const Mat & {
+        const Mat &m = mats[i];
+        if (m.cq) {
+            ND_CHECK(m.cq->out == rows && m.cq->in == cols, "engine: CQ matrix shape does not match the geometry");
+        } else {
+            ND_CHECK(m.rows * m.cols == rows * cols, "engine: dense matrix shape does not match the geometry");
+        }
+        return m;
+    };
+
+    dims.D = D;
+    dims.N = N;
+    dims.H = c.heads;
+    dims.KV = c.kvheads;
+    dims.HD = HD;
+    dims.A = A;
+    dims.K = K;
+    dims.hada = c.hada;
+    dims.layers = c.layers;
+    dims.tables = c.tables;
+    dims.subdim = c.subdim;
+    dims.taps = c.taps;
+    dims.abits = abits;
+    dims.sqrt_d = std::sqrt(float(D));
+    dims.inv_hada = 1 / std::sqrt(float(c.hada));
+    dims.scale = 1 / std::sqrt(float(HD));
+    engring = int(int64_t(c.taps - 1) * c.dilation + 1);
+    ND_CHECK(engring >= 1, "invalid Engram ring size");
+    dims.engring = engring;
+    int max_order = 1;
+    for (int i = 0; i < c.num_orders; ++i) max_order = std::max(max_order, c.orders[i]);
+    history_cap = c.num_sites ? engring + max_order - 1 : 1;
+    history.assign(history_cap, 0);
+    rope_div.resize(HD / 2);
+    for (int j = 0; j < HD / 2; ++j) rope_div[j] = std::pow(c.rope_theta, float(2 * j) / HD);  // engine.cpp:400
+
+    // work buffers (one allocation)
+    const int mhc_tiles = 2 * kRowsPerBlock;  // a piece spans at most two row tiles
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        const size_t at = off;
+        off += (n + 63) / 64 * 64;
+        return at;
+    };
+    const size_t ox = take(N * D), onx = take(N * D), ou = take(D), obx = take(D), oz = take(D), oq = take(A),
+                 ok = take(K), ov = take(K), og = take(A), oa = take(A), op = take(D), oh = take(size_t(c.layers) * D),
+                 ohp = take(N), ohq = take(N), ohr = take(N * N), om0 = take(mhc_tiles), om1 = take(mhc_tiles),
+                 om2 = take(mhc_tiles), oe = take(D), oek = take(size_t(std::max(1, c.num_sites)) * D),
+                 oev = take(size_t(std::max(1, c.num_sites)) * D), orv = take(D),
+                 oring = take(size_t(std::max(1, c.num_sites)) * engring * D), ozf = take(D);
+    work.reserve(off);
+    ND_HIP(hipMemset(work.p, 0, off * sizeof(float)));
+    float *w = work.p;
+    b.x = w + ox;
+    b.nx = w + onx;
+    b.u = w + ou;
+    b.bx = w + obx;
+    b.z = w + oz;
+    b.q = w + oq;
+    b.k = w + ok;
+    b.v = w + ov;
+    b.gate = w + og;
+    b.att = w + oa;
+    b.proj = w + op;
+    b.hidden = w + oh;
+    b.hpre = w + ohp;
+    b.hpost = w + ohq;
+    b.hres = w + ohr;
+    b.mhc_out[0] = w + om0;
+    b.mhc_out[1] = w + om1;
+    b.mhc_out[2] = w + om2;
+    b.e = w + oe;
+    b.ek = w + oek;
+    b.ev = w + oev;
+    b.rawv = w + orv;
+    b.engring = w + oring;
+    b.zf = w + ozf;
+    params.reserve(1);
+    hparams.reserve(1);
+    std::memset(hparams.p, 0, sizeof(StepParams));
+    logits.reserve(c.vocab);
+    embed_z.reserve(D);
+
+    // layers
+    const int mhi = mh0();
+    mh.a_pre = vec(mhi);
+    mh.a_post = vec(mhi + 1);
+    mh.a_res = vec(mhi + 2);
+    mh.b_pre = vec(mhi + 3);
+    mh.b_post = vec(mhi + 4);
+    mh.b_res = vec(mhi + 5);
+    layer.resize(c.layers);
+    mhc_proj.resize(c.layers);
+    qkvg.resize(c.layers);
+    oproj.resize(c.layers);
+    mhc_row.resize(c.layers);
+    for (int l = 0; l < c.layers; ++l) {
+        const int t0 = ti(l);
+        LayerDev &L = layer[l];
+        L.norm_in = vec(t0);
+        L.q_norm = vec(t0 + 4);
+        L.k_norm = vec(t0 + 5);
+        L.post_norm = vec(t0 + 8);
+        L.attn_gate = vec(t0 + 9);
+        L.pre_hada = vec(t0 + 10);
+        L.d1 = vec(t0 + 11);
+        L.d2 = vec(t0 + 12);
+        L.d3 = vec(t0 + 13);
+        {
+            std::vector<std::vector<GemvGroup::Piece>> pend;
+            qkvg[l].add(mat(t0 + 1, A, D), 0, A, b.q, pend);
+            qkvg[l].add(mat(t0 + 2, K, D), 0, K, b.k, pend);
+            qkvg[l].add(mat(t0 + 3, K, D), 0, K, b.v, pend);
+            qkvg[l].add(mat(t0 + 6, A, D), 0, A, b.gate, pend);
+            qkvg[l].finish(pend, b.z);
+        }
+        {
+            std::vector<std::vector<GemvGroup::Piece>> pend;
+            oproj[l].add(mat(t0 + 7, D, A), 0, D, b.proj, pend);
+            oproj[l].finish(pend, b.att);
+        }
+        {
+            const int rows[3] = {N, N, N * N};
+            std::vector<std::vector<GemvGroup::Piece>> pend;
+            for (int m = 0; m < 3; ++m) {
+                const Mat &M = mat(mhi + 6 + m, c.layers * rows[m], N * D);
+                const int first = l * rows[m];
+                if (M.cq) {  // the GEMV's row tiles; dense ones run inside the mixing kernel
+                    mhc_row[l][m] = first - first / kRowsPerBlock * kRowsPerBlock;
+                    mhc_proj[l].add(M, first, rows[m], b.mhc_out[m], pend);
+                } else {
+                    mhc_row[l][m] = 0;
+                }
+                phi[m] = M.cq ? nullptr : M.dense;
+            }
+            mhc_proj[l].finish(pend, b.nx);
+        }
+    }
+    for (int s = 0; s < c.num_sites; ++s) {
+        ND_CHECK(c.sites[s] >= 0 && c.sites[s] < c.layers, "engine: engram site outside the layers");
+        const int e0 = engram_base() + 4 * s;
+        ND_CHECK(mats[e0].cq ? mats[e0].cq->in == c.subdim : mats[e0].cols == c.subdim,
+                 "engine: engram tables shape does not match the geometry");
+        (void)vec(e0 + 3);
+        engram_kv.emplace_back();
+        std::vector<std::vector<GemvGroup::Piece>> pend;
+        engram_kv.back().add(mat(e0 + 1, D, D), 0, D, b.ek + s * D, pend);
+        engram_kv.back().add(mat(e0 + 2, D, D), 0, D, b.rawv, pend);
+        engram_kv.back().finish(pend, b.e);
+        if (mats[e0].cq) row_scratch.reserve(size_t(c.tables) * mats[e0].cq->padded);
+    }
+    (void)vec(final_norm());
+    {
+        std::vector<std::vector<GemvGroup::Piece>> pend;
+        lm_head.add(mat(0, c.vocab, D), 0, c.vocab, logits.p, pend);
+        lm_head.finish(pend, b.zf);
+    }
+    if (mats[0].cq) row_scratch.reserve(std::max(row_scratch.n, size_t(mats[0].cq->padded)));
+    reset(0);
+}
+
+void GpuEngine::reset(int prefix_len) {
+    ND_CHECK(prefix_len >= 0 && prefix_len <= c.max_seq, "prefix length outside [0, max_seq]");
+    position = 0;
+    prefix = prefix_len;
+    std::fill(history.begin(), history.end(), 0);
+    capacity = c.window ? c.window + prefix : c.max_seq;  // engine.cpp:433-449
+    dims.capacity = capacity;
+    const int G = c.heads / c.kvheads;
+    if (int8_kv)
+        ND_CHECK(attn_supported(c.head_dim, G), "int8 KV attention: head_dim 32/64/128 with 1, 2, 4 or 8 heads per kv head");
+    else
+        ND_CHECK(size_t(G) * capacity * sizeof(float) <= 65536, "fp32 KV attention: heads per kv head x context too large");
+    const size_t per_layer = size_t(c.kvheads) * capacity * c.head_dim;
+    const size_t scales = size_t(c.kvheads) * capacity;
+    kv.assign(c.layers, KvLayer{});
+    if (int8_kv) {
+        kv32.release();
+        kv8.reserve(2 * per_layer * c.layers);
+        kvs.reserve(2 * scales * c.layers);
+        for (int l = 0; l < c.layers; ++l) {
+            kv[l].k8 = kv8.p + 2 * per_layer * l;
+            kv[l].v8 = kv[l].k8 + per_layer;
+            kv[l].ks = kvs.p + 2 * scales * l;
+            kv[l].vs = kv[l].ks + scales;
+        }
+    } else {
+        kv8.release();
+        kvs.release();
+        kv32.reserve(2 * per_layer * c.layers);
+        for (int l = 0; l < c.layers; ++l) {
+            kv[l].k32 = kv32.p + 2 * per_layer * l;
+            kv[l].v32 = kv[l].k32 + per_layer;
+        }
+    }
+    slots.reserve(capacity);
+    b.slots = slots.p;
+    if (c.num_sites) ND_HIP(hipMemsetAsync(b.engring, 0, size_t(c.num_sites) * engring * c.dim * sizeof(float), stream));
+    ND_HIP(hipStreamSynchronize(stream));
+}
+
+void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
+    const int D = c.dim, HD = c.head_dim;
+    if (token < 0 || token >= c.vocab) throw Error("token outside vocabulary");
+    if (!c.window && position >= capacity) throw Error("maximum context reached");
+    history[position % history_cap] = token;
+    StepParams &p = *hparams.p;
+    p.token = token;
+    p.position = position;
+    p.slot = cache_slot(position);
+    p.prefix = prefix;
+    p.window = c.window;
+    p.prefix_count = c.window ? std::min(prefix, position + 1) : 0;  // engine.cpp:900-902
+    p.start = c.window ? std::max(prefix, position - c.window + 1) : 0;
+    p.length = p.prefix_count + std::max(0, position - p.start + 1);
+    for (int j = 0; j < HD / 2; ++j) {
+        const float a = position / rope_div[j];
+        p.rope_cos[j] = std::cos(a);
+        p.rope_sin[j] = std::sin(a);
+    }
+    if (c.num_sites) {  // engine.cpp:755-781
+        const int heads = c.tables / c.num_orders;
+        auto hist = [&](int q) { return history[((q % history_cap) + history_cap) % history_cap]; };
+        for (int s = 0; s < c.num_sites; ++s) {
+            p.engram_zero[s] = 0;
+            for (int table = 0; table < c.tables; ++table) {
+                const int order = c.orders[table / heads];
+                p.engram_rows[s][table] = 0;
+                if (position + 1 < order || (c.window && order - 1 >= c.window && position - order + 1 >= prefix)) {
+                    p.engram_zero[s] |= 1 << table;
+                    continue;
+                }
+                uint32_t acc = uint32_t(0x9e3779b9) * uint32_t(table + 1);
+                for (int j = 0; j < order; ++j) acc = (acc ^ uint32_t(hist(position - j))) * uint32_t(0x01000193);
+                acc ^= acc >> 15;
+                p.engram_rows[s][table] = int64_t(table) * c.slots + acc % uint32_t(c.slots);
+            }
+        }
+        p.ring_row = position % engring;
+        for (int tap = 0; tap < c.taps; ++tap) {
+            const int past = position - tap * c.dilation;
+            const bool live = past >= 0 && (!c.window || tap * c.dilation < c.window || past < prefix);
+            p.tap_rows[tap] = live ? past % engring : -1;
+        }
+    }
+    hipStream_t s = stream;
+    ND_HIP(hipMemcpyAsync(params.p, hparams.p, sizeof(StepParams), hipMemcpyHostToDevice, s));
+    StepParams *dp = params.p;
+
+    // embedding row, lanes (engine.cpp:972-974)
+    const Mat &emb = mats[0];
+    if (emb.cq)
+        launch_cq_rows(emb.cq->geom(), emb.cq->codes.p, emb.cq->norms.p, &dp->token, 1, D, emb.cq->padded,
+                       row_scratch.p, embed_z.p, s);
+    else
+        launch_eng_dense_rows(emb.dense, D, &dp->token, 1, embed_z.p, s);
+    launch_eng_start(embed_z.p, b, dims, s);
+
+    for (int site = 0; site < c.num_sites; ++site) {
+        const int e0 = engram_base() + 4 * site;
+        const Mat &tab = mats[e0];
+        if (tab.cq)
+            launch_cq_rows(tab.cq->geom(), tab.cq->codes.p, tab.cq->norms.p, &dp->engram_rows[site][0], c.tables,
+                           c.subdim, tab.cq->padded, row_scratch.p, b.e, s);
+        else
+            launch_eng_dense_rows(tab.dense, c.subdim, &dp->engram_rows[site][0], c.tables, b.e, s);
+        launch_eng_engram_in(b, dp, site, dims, s);
+        engram_kv[site].run(s);
+        launch_eng_engram_out(b, dptr[e0 + 3], dp, site, dims, s);
+    }
+
+    const int G = c.heads / c.kvheads;
+    for (int l = 0; l < c.layers; ++l) {
+        mhc_proj[l].run(s);
+        int sites[kEngMaxSites], ns = 0;
+        for (int k = 0; k < c.num_sites; ++k)
+            if (c.sites[k] == l) sites[ns++] = k;
+        launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), phi, sites, ns, dims, s);
+        qkvg[l].run(s);
+        launch_eng_qk(b, layer[l], kv[l], dp, dims, s);
+        if (int8_kv) {
+            AttnArgs a{};
+            a.k8 = kv[l].k8;
+            a.v8 = kv[l].v8;
+            a.ks = kv[l].ks;
+            a.vs = kv[l].vs;
+            a.q = b.q;
+            a.out = b.att;
+            a.slots = b.slots;
+            a.lengths = nullptr;
+            a.seqs = 1;
+            a.kvheads = c.kvheads;
+            a.head_dim = HD;
+            a.capacity = capacity;
+            a.length = p.length;
+            const int tiles = (p.length + 255) / 256;
+            a.splits = std::max(1, std::min(tiles, 64 / c.kvheads));
+            const int per = (tiles + a.splits - 1) / a.splits * 256;
+            a.splits = std::max(1, (p.length + per - 1) / per);
+            a.slots_per_split = per;
+            if (a.splits > 1) part.reserve(size_t(c.heads) * a.splits * (HD + 2));
+            a.part = part.p;
+            a.scale = dims.scale;
+            launch_attention(a, G, s);
+        } else {
+            launch_eng_attn_f32(b, kv[l], p.length, dims, s);
+        }
+        launch_eng_gate(b, dims, s);
+        oproj[l].run(s);
+        launch_eng_post(b, layer[l], mh, l, l + 1 < c.layers, dims, s);
+    }
+    launch_eng_final(b, dptr[final_norm()], dims, s);
+    if (logits_out) {
+        launch_eng_quantize(b.zf, D, abits, s);
+        lm_head.run(s);
+        hlogits.reserve(c.vocab);
+        ND_HIP(hipMemcpyAsync(hlogits.p, logits.p, size_t(c.vocab) * sizeof(float), hipMemcpyDeviceToHost, s));
+    }
+    if (hidden_out) {
+        hhidden.reserve(size_t(c.layers) * D);
+        ND_HIP(hipMemcpyAsync(hhidden.p, b.hidden, size_t(c.layers) * D * sizeof(float), hipMemcpyDeviceToHost, s));
+    }
+    ND_HIP(hipStreamSynchronize(s));
+    if (logits_out) std::memcpy(logits_out, hlogits.p, size_t(c.vocab) * sizeof(float));
+    if (hidden_out) std::memcpy(hidden_out, hhidden.p, size_t(c.layers) * D * sizeof(float));
+    ++position;
+}
+
+// engine.cpp:1302-1349: the final hidden state of the last step, quantised,
+// through the LM head's candidate rows.
+void GpuEngine::project_candidates(const int *candidates, int count, float *out) {
+    ND_CHECK(candidates && count > 0, "candidates must be nonempty");
+    for (int i = 0; i < count; ++i)
+        ND_CHECK(candidates[i] >= 0 && candidates[i] < c.vocab, "candidate outside vocabulary");
+    if (!out) return;
+    hipStream_t s = stream;
+    launch_eng_quantize(b.zf, c.dim, abits, s);
+    st.hids.reserve(count);
+    st.ids.reserve(count);
+    st.y.reserve(count);
+    st.hy.reserve(count);
+    std::memcpy(st.hids.p, candidates, size_t(count) * sizeof(int32_t));
+    ND_HIP(hipMemcpyAsync(st.ids.p, st.hids.p, size_t(count) * sizeof(int32_t), hipMemcpyHostToDevice, s));
+    const Mat &head = mats[0];
+    if (head.cq) {
+        const Candidates cand = gather_candidates(*head.cq, st, st.ids.p, count, s);
+        if (cand.full) {
+            lm_head.run(s);
+            launch_gather_outputs(logits.p, c.vocab, st.ids.p, count, 1, st.y.p, s);
+        } else {
+            matrix_gemv(*head.cq, st, cand.codes, cand.norms, count, cand.n_pad, b.zf, st.y.p, 1, s);
+        }
+    } else {
+        lm_head.run(s);
+        launch_gather_outputs(logits.p, c.vocab, st.ids.p, count, 1, st.y.p, s);
+    }
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, s));
+    ND_HIP(hipStreamSynchronize(s));
+    std::memcpy(out, st.hy.p, size_t(count) * sizeof(float));
+}
+
+}  // namespace nd
+
+using namespace nd;
+
+extern "C" {
+
+// needle2/csrc/engine.cpp:1499-1548: the same entry points and error channel.
+const char *needle2_engine_error(void) { return engine_error.c_str(); }
+
+void *needle2_engine_create(const void *config, const void *tensors, int count, int threads, int activation_bits) {
+    (void)threads;
+    try {
+        if (!config || !tensors) throw Error("engine: null configuration or tensor table");
+        return new GpuEngine(*static_cast<const EngineConfigC *>(config), static_cast<const TensorDescC *>(tensors),
+                             count, activation_bits);
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return nullptr;
+    }
+}
+
+void needle2_engine_destroy(void *p) { delete static_cast<GpuEngine *>(p); }
+
+// The reference's projection lookup modes are CPU summation schemes; every mode runs the GPU GEMV.
+void needle2_engine_set_lookup(void *, int) {}
+
+// engine.cpp:1506-1509 on a host without DotProd: the int8 engine path is not available here.
+int needle2_engine_set_sdot(void *) {
+    engine_error = "SDOT requires an ARM64 CPU with DotProd support";
+    return -1;
+}
+
+void needle2_engine_reset(void *p, int prefix) {
+    try {
+        static_cast<GpuEngine *>(p)->reset(prefix);
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+    }
+}
+
+int needle2_engine_cache_prefix(void *) {
+    engine_error = "prefix snapshots are not implemented by the GPU engine";
+    return -1;
+}
+
+int needle2_engine_reset_to_prefix(void *) {
+    engine_error = "prefix snapshots are not implemented by the GPU engine";
+    return -1;
+}
+
+int needle2_engine_step(void *p, int token, float *logits, float *hidden) {
+    try {
+        static_cast<GpuEngine *>(p)->step(token, logits, hidden);
+        return 0;
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
+}
+
+// engine.cpp:1045-1301 computes a prompt in chunks with the same per-token
+// arithmetic; here the tokens run as consecutive steps.
+int needle2_engine_prefill(void *p, const int *tokens, int num_tokens, int last_only, float *logits, float *hidden) {
+    try {
+        auto *e = static_cast<GpuEngine *>(p);
+        if (num_tokens <= 0) return 0;
+        for (int i = 0; i < num_tokens; ++i)
+            if (tokens[i] < 0 || tokens[i] >= e->c.vocab) throw Error("token outside vocabulary");
+        if (!e->c.window && e->position + num_tokens > e->capacity) throw Error("maximum context reached");
+        for (int i = 0; i < num_tokens; ++i) {
+            float *out = nullptr;
+            if (logits) out = last_only ? (i + 1 == num_tokens ? logits : nullptr) : logits + size_t(i) * e->c.vocab;
+            e->step(tokens[i], out, i + 1 == num_tokens ? hidden : nullptr);
+        }
+        return 0;
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
+}
+
+int needle2_engine_step_candidates(void *p, int token, const int *candidates, int num_candidates,
+                                   float *candidate_logits, float *hidden) {
+    try {
+        auto *e = static_cast<GpuEngine *>(p);
+        ND_CHECK(candidates && num_candidates > 0, "candidates must be nonempty");
+        for (int i = 0; i < num_candidates; ++i)
+            ND_CHECK(candidates[i] >= 0 && candidates[i] < e->c.vocab, "candidate outside vocabulary");
+        e->step(token, nullptr, hidden);
+        e->project_candidates(candidates, num_candidates, candidate_logits);
+        return 0;
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
+}
+
+int needle2_engine_project_candidates(void *p, const int *candidates, int num_candidates, float *candidate_logits) {
+    try {
+        static_cast<GpuEngine *>(p)->project_candidates(candidates, num_candidates, candidate_logits);
+        return 0;
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
+}
+
+int needle2_engine_decode_loop(void *, int, int, const void *, int *, int *) {
+    engine_error = "the grammar-constrained decode loop is not implemented by the GPU engine";
+    return -1;
+}
+
+int needle2_engine_import(void *, int, int, const int *, const int *, int, const float *, const float *) {
+    engine_error = "state import is not implemented by the GPU engine";
+    return -1;
+}
+
+int needle2_engine_set_int8_kv(void *p, int enable) {
+    try {
+        auto *e = static_cast<GpuEngine *>(p);
+        e->int8_kv = enable != 0;
+        e->reset(e->prefix);
+        return 0;
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
+}
+
+size_t needle2_engine_kv_storage_bytes(void *p) { return static_cast<GpuEngine *>(p)->kv_storage_bytes(); }
+
+}  // extern "C"

@@ -1,0 +1,88 @@
+// Single-sequence decode engine on the GPU (needle2/csrc/engine.cpp:340-1044):
+// device argument blocks shared by engine.cpp and engine_kernels.hip.
+#pragma once
+
+#include "common.h"
+
+namespace nd {
+
+constexpr int kEngMaxHalfHd = 64;  // head_dim <= 128
+constexpr int kEngMaxTables = 16;  // engram tables per site
+constexpr int kEngMaxSites = 4;
+constexpr int kEngMaxTaps = 16;
+constexpr int kEngThreads = 1024;  // every glue kernel is one workgroup of this size
+
+// Values of one step that depend only on the position, the token history and
+// the cache geometry; the host computes them (with the reference's own
+// integer hashing and std::cos / std::sin) and uploads them once per step.
+struct StepParams {
+    int64_t token;                                     // embedding row
+    int position, slot;                                // this token's cache slot (engine.cpp:500)
+    int length, prefix_count, start, prefix, window;   // attention slot list (engine.cpp:898-911)
+    int ring_row;                                      // engram ring row of this position
+    int engram_zero[kEngMaxSites];                     // bit t: table t of site s reads zeros
+    int tap_rows[kEngMaxTaps];                         // ring row read by each conv tap, -1: skipped
+    int64_t engram_rows[kEngMaxSites][kEngMaxTables];  // table row per (site, table)
+    float rope_cos[kEngMaxHalfHd], rope_sin[kEngMaxHalfHd];
+};
+
+struct EngineDims {
+    int D, N, H, KV, HD, A, K, hada, layers, tables, subdim, taps, capacity, engring, abits;
+    float sqrt_d;    // std::sqrt(float(D)) (engine.cpp:974, 987)
+    float inv_hada;  // 1 / std::sqrt(float(hada)), the Hadamard normalisation
+    float scale;     // 1 / std::sqrt(float(head_dim)) (engine.cpp:914)
+};
+
+// Layer parameters (device pointers into the engine's fp32 copies of the
+// dense tensors; the matrices run through the GEMV kernels).
+struct LayerDev {
+    const float *norm_in, *q_norm, *k_norm, *post_norm, *attn_gate, *pre_hada, *d1, *d2, *d3;
+};
+
+// The mHC scalars and vectors of the model (engine.cpp:980-984, 1036).
+struct MhcDev {
+    const float *a_pre, *a_post, *a_res, *b_pre, *b_post, *b_res;
+};
+
+// Work buffers of one step (device).
+struct EngineBufs {
+    float *x, *nx, *u, *bx, *z, *q, *k, *v, *gate, *att, *proj, *hidden;
+    float *hpre, *hpost, *hres;     // mixed gates (N, N, N*N)
+    float *mhc_out[3];              // raw mHC projections of the layer (pre, post, res rows)
+    float *e, *ek, *ev, *rawv;      // engram rows [D], keys [sites][D], values [sites][D], raw values [D]
+    float *engring;                 // [sites][engring][D]
+    float *zf;                      // final hidden, input of the LM head
+    int *slots;                     // attention slot list
+};
+
+// KV cache of one layer: fp32 (k32 / v32) or int8 codes with fp32 scales,
+// [kvheads][capacity][head_dim] (scales [kvheads][capacity]).
+struct KvLayer {
+    float *k32, *v32;
+    int8_t *k8, *v8;
+    float *ks, *vs;
+};
+
+void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, hipStream_t s);
+void launch_eng_engram_in(const EngineBufs &b, const StepParams *p, int site, const EngineDims &d, hipStream_t s);
+void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepParams *p, int site,
+                           const EngineDims &d, hipStream_t s);
+// mixing, engram gates and the attention input of layer l; phi[m]: dense mHC
+// matrix m (computed in-kernel from b.nx) or null, then mhc_row[m] is the
+// first row of the layer inside b.mhc_out[m]; sites: engram sites at this layer
+void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
+                    const float *const *phi, const int *sites, int nsites, const EngineDims &d, hipStream_t s);
+void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
+                   const EngineDims &d, hipStream_t s);
+void launch_eng_attn_f32(const EngineBufs &b, const KvLayer &kv, int length, const EngineDims &d, hipStream_t s);
+void launch_eng_gate(const EngineBufs &b, const EngineDims &d, hipStream_t s);
+void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
+                     const EngineDims &d, hipStream_t s);
+void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, hipStream_t s);
+void launch_eng_quantize(float *x, int n, int bits, hipStream_t s);
+// y[r] = dot(W[first + r], x) over cols for r < rows (dense fp32 matrices)
+void launch_eng_dense(const float *w, int cols, int first, int rows, const float *x, float *y, hipStream_t s);
+// y[i][:] = W[ids[i]][:] (dense row copy)
+void launch_eng_dense_rows(const float *w, int cols, const int64_t *ids, int count, float *y, hipStream_t s);
+
+}  // namespace nd

@@ -1,0 +1,556 @@
+// Glue kernels of the single-sequence decode engine (needle2/csrc/engine.cpp:
+// 968-1044 and the helpers it calls). Every kernel is one workgroup of
+// kEngThreads threads working on the model's small vectors (d_model, the mHC
+// lanes, one token's heads), in the reference's formulas and operation order
+// per element; block-wide sums and maxima are tree reductions, so results
+// agree with the reference to fp32 rounding rather than bit for bit.
+//   rms(x, gain)        y = x * (1 / sqrt(sum(x^2) / n + 1e-6)) * (1 + gain)   (engine.cpp:181-184)
+//   activation_quant    x = clamp(rint(x / (a / m)), -m-1, m) * (a / m), a = max|x|, m = 2^(bits-1)-1
+//   sigmoid(x)          1 / (1 + exp(-x))
+//   hadamard(v, n)      butterflies h = 1, 2, .., n/2 of (a + b, a - b), then * 1/sqrt(n)   (cq.cpp:30-46)
+//   sinkhorn(a, n)      20 row / column normalisations after exp(a - max)     (engine.cpp:151-180)
+#include "engine.h"
+#include "wave.h"
+
+#include <cmath>
+
+namespace nd {
+
+namespace {
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Block-wide sum / max of one value per thread (every thread gets the result).
+__device__ float block_sum(float v, float *red) {
+    v = wave_sum(v, threadIdx.x & 63);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) s += red[w];
+    return s;
+}
+
+__device__ float block_max(float v, float *red) {
+    v = wave_max(v, threadIdx.x & 63);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) m = fmaxf(m, red[w]);
+    return m;
+}
+
+// y = rms(x) (* (1 + gain)); x and y may alias. Ends with a barrier.
+__device__ void rms_block(const float *x, float *y, int n, const float *gain, float *red) {
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s += x[i] * x[i];
+    s = block_sum(s, red);
+    const float r = 1.0f / sqrtf(s / static_cast<float>(n) + 1e-6f);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i] * r;
+        y[i] = gain ? v * (1.0f + gain[i]) : v;
+    }
+    __syncthreads();
+}
+
+// engine.cpp:185-190. Ends with a barrier.
+__device__ void quantize_block(float *x, int n, int bits, float *red) {
+    if (!bits) return;
+    float a = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) a = fmaxf(a, fabsf(x[i]));
+    a = block_max(a, red);
+    if (a == 0.0f) {
+        __syncthreads();
+        return;
+    }
+    const int m = (1 << (bits - 1)) - 1;
+    const float scale = a / static_cast<float>(m);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float q = rintf(x[i] / scale);
+        q = fmaxf(static_cast<float>(-m - 1), fminf(static_cast<float>(m), q));
+        x[i] = q * scale;
+    }
+    __syncthreads();
+}
+
+// In-place normalised FWHT of v[0..n) in LDS (n a power of two). Ends with a barrier.
+__device__ void hadamard_block(float *v, int n, float inv) {
+    for (int h = 1; h < n; h <<= 1) {
+        for (int p = threadIdx.x; p < n / 2; p += blockDim.x) {
+            const int j = (p / h) * 2 * h + p % h;
+            const float a = v[j], b = v[j + h];
+            v[j] = a + b;
+            v[j + h] = a - b;
+        }
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < n; i += blockDim.x) v[i] *= inv;
+    __syncthreads();
+}
+
+// engine.cpp:151-180 for an N x N matrix (N <= 8) held by one wave, lane
+// l = N i + j holding a[i][j] (lanes past N * N hold copies of lane 0's group
+// and never mix into it): row sums over lanes that differ in the low log2(N)
+// bits, column sums over the next log2(N) bits (tree sums, not the
+// reference's left-to-right ones).
+template <int N, int H0, int H1>
+__device__ __forceinline__ float lanes_sum(float v, int lane) {
+    if constexpr (H0 < H1) {
+        v += butterfly_partner<H0>(v, lane);
+        return lanes_sum<N, H0 * 2, H1>(v, lane);
+    } else {
+        return v;
+    }
+}
+template <int H0, int H1>
+__device__ __forceinline__ float lanes_max(float v, int lane) {
+    if constexpr (H0 < H1) {
+        v = fmaxf(v, butterfly_partner<H0>(v, lane));
+        return lanes_max<H0 * 2, H1>(v, lane);
+    } else {
+        return v;
+    }
+}
+template <int H0, int H1>
+__device__ __forceinline__ float lanes_min(float v, int lane) {
+    if constexpr (H0 < H1) {
+        v = fminf(v, butterfly_partner<H0>(v, lane));
+        return lanes_min<H0 * 2, H1>(v, lane);
+    } else {
+        return v;
+    }
+}
+
+template <int N>
+__device__ float sinkhorn_lanes(float a, int lane) {
+    constexpr int NN = N * N;
+    const float mx = lanes_max<1, NN>(a, lane), mn = lanes_min<1, NN>(a, lane);
+    if (!isfinite(mx) || mx - mn > 60.0f) {  // log space (wave-uniform branch)
+        for (int it = 0; it < 20; ++it) {
+            float m = lanes_max<1, N>(a, lane);
+            a -= m + logf(lanes_sum<N, 1, N>(expf(a - m), lane));
+            m = lanes_max<N, NN>(a, lane);
+            a -= m + logf(lanes_sum<N, N, NN>(expf(a - m), lane));
+        }
+        return expf(a);
+    }
+    a = expf(a - mx);
+    for (int it = 0; it < 20; ++it) {
+        a *= 1.0f / lanes_sum<N, 1, N>(a, lane);
+        a *= 1.0f / lanes_sum<N, N, NN>(a, lane);
+    }
+    return a;
+}
+
+__device__ float sinkhorn_wave(float a, int n, int lane) {
+    switch (n) {
+    case 1: return sinkhorn_lanes<1>(a, lane);
+    case 2: return sinkhorn_lanes<2>(a, lane);
+    case 4: return sinkhorn_lanes<4>(a, lane);
+    default: return sinkhorn_lanes<8>(a, lane);
+    }
+}
+
+// x[n][d] = z[d] * sqrt(D) for every lane (engine.cpp:973-974), then nx = rms(x).
+__global__ __launch_bounds__(kEngThreads) void eng_start_kernel(const float *__restrict__ z, EngineBufs b,
+                                                                EngineDims d) {
+    __shared__ float red[kEngThreads / 64];
+    for (int i = threadIdx.x; i < d.N * d.D; i += blockDim.x) b.x[i] = z[i % d.D] * d.sqrt_d;
+    __syncthreads();
+    rms_block(b.x, b.nx, d.N * d.D, nullptr, red);
+}
+
+// Tables the step does not read become zeros; then the activation quantiser (engine.cpp:760-768).
+__global__ __launch_bounds__(kEngThreads) void eng_engram_in_kernel(EngineBufs b, const StepParams *__restrict__ p,
+                                                                    int site, EngineDims d) {
+    __shared__ float red[kEngThreads / 64];
+    const int zero = p->engram_zero[site];
+    for (int i = threadIdx.x; i < d.D; i += blockDim.x)
+        if ((zero >> (i / d.subdim)) & 1) b.e[i] = 0.0f;
+    __syncthreads();
+    quantize_block(b.e, d.D, d.abits, red);
+}
+
+// Raw values into the ring, then the dilated causal conv over the taps (engine.cpp:771-780).
+__global__ __launch_bounds__(kEngThreads) void eng_engram_out_kernel(EngineBufs b, const float *__restrict__ taps,
+                                                                     const StepParams *__restrict__ p, int site,
+                                                                     EngineDims d) {
+    float *ring = b.engring + static_cast<size_t>(site) * d.engring * d.D;
+    for (int i = threadIdx.x; i < d.D; i += blockDim.x) {
+        ring[static_cast<size_t>(p->ring_row) * d.D + i] = b.rawv[i];
+        float sum = 0.0f;
+        for (int t = 0; t < d.taps; ++t) {
+            const int r = p->tap_rows[t];
+            if (r >= 0) sum += taps[t * d.D + i] * ring[static_cast<size_t>(r) * d.D + i];
+        }
+        b.ev[site * d.D + i] = sum;
+    }
+}
+
+struct MixArgs {
+    int l, nsites;
+    int sites[kEngMaxSites];
+    int mhc_row[3];
+    const float *phi[3];  // dense mHC matrices (rows of all layers, N * D columns), or null: b.mhc_out holds them
+};
+
+// engine.cpp:980-992: lane gates from the mHC projections, the pre-mixed
+// residual u = bx, engram gates, then z = quant(rms(bx) * (1 + norm_in)).
+__global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b, LayerDev ld, MhcDev mh, MixArgs m,
+                                                              EngineDims d) {
+    __shared__ float red[kEngThreads / 64];
+    __shared__ float hp[16];
+    __shared__ float zs[4096], ps[4096];
+    __shared__ float proj[2 * 8 + 64];  // this layer's mHC projections: pre [N], post [N], res [N * N]
+    const int N = d.N, D = d.D, l = m.l;
+    const int rows[3] = {N, N, N * N}, base[3] = {0, N, 2 * N};
+    {  // dense matrices: one wave per row; CQ ones: the GEMV's output
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, cols = N * D;
+        for (int task = wave; task < 2 * N + N * N; task += blockDim.x >> 6) {
+            const int mm = task < N ? 0 : task < 2 * N ? 1 : 2, r = task - base[mm];
+            if (m.phi[mm]) {
+                const float *w = m.phi[mm] + static_cast<size_t>(l * rows[mm] + r) * cols;
+                float sum = 0.0f;
+                for (int i = lane; i < cols; i += 64) sum += w[i] * b.nx[i];
+                sum = wave_sum(sum, lane);
+                if (lane == 0) proj[task] = sum;
+            } else if (lane == 0) {
+                proj[task] = b.mhc_out[mm][m.mhc_row[mm] + r];
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < static_cast<unsigned>(N)) {
+        const int n = threadIdx.x;
+        const float pre = proj[n], post = proj[N + n];
+        const float hpre = sigmoidf_(mh.a_pre[l] * pre + mh.b_pre[l * N + n] + (n == l % N ? 4.0f : -4.0f));
+        const float hpost = 2.0f * sigmoidf_(mh.a_post[l] * post + mh.b_post[l * N + n] + (n == l % N ? 0.0f : -4.0f));
+        hp[n] = hpre;
+        b.hpre[n] = hpre;
+        b.hpost[n] = hpost;
+    }
+    for (int i = threadIdx.x; i < N * N; i += blockDim.x) b.hres[i] = proj[2 * N + i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+        float sum = 0.0f;
+        for (int n = 0; n < N; ++n) sum += hp[n] * b.x[n * D + i];
+        b.u[i] = sum;
+        b.bx[i] = sum;
+    }
+    __syncthreads();
+    for (int k = 0; k < m.nsites; ++k) {
+        const int s = m.sites[k];
+        rms_block(b.u, zs, D, nullptr, red);
+        rms_block(b.ek + s * D, ps, D, nullptr, red);
+        float dot = 0.0f;
+        for (int i = threadIdx.x; i < D; i += blockDim.x) dot += zs[i] * ps[i];
+        dot = block_sum(dot, red);
+        const float alpha = sigmoidf_(dot / d.sqrt_d);
+        for (int i = threadIdx.x; i < D; i += blockDim.x) b.bx[i] += alpha * b.ev[s * D + i];
+        __syncthreads();
+    }
+    rms_block(b.bx, b.z, D, ld.norm_in, red);
+    quantize_block(b.z, D, d.abits, red);
+}
+
+// engine.cpp:994-1021: per-head rms of q and k, RoPE (first half paired with
+// second half), the new token's K/V into its cache slot (fp32, or the int8
+// quantiser of kv_store), and the attention slot list.
+__global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b, LayerDev ld, KvLayer kv,
+                                                             const StepParams *__restrict__ p, EngineDims d) {
+    const int HD = d.HD, half = HD / 2;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int heads = d.H + d.KV;
+    for (int h = wave; h < heads; h += blockDim.x >> 6) {  // one wave per head (q heads, then k heads)
+        float *src = h < d.H ? b.q + h * HD : b.k + (h - d.H) * HD;
+        const float *gain = h < d.H ? ld.q_norm : ld.k_norm;
+        float ss = 0.0f;
+        for (int i = lane; i < HD; i += 64) ss += src[i] * src[i];
+        ss = wave_sum(ss, lane);
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + 1e-6f);
+        // lane j rotates the pair (j, j + HD/2): it reads and writes both, nobody else does
+        for (int j = lane; j < half; j += 64) {
+            const float co = p->rope_cos[j], si = p->rope_sin[j];
+            const float a = src[j] * r * (1.0f + gain[j]), c = src[j + half] * r * (1.0f + gain[j + half]);
+            src[j] = a * co - c * si;
+            src[j + half] = c * co + a * si;
+        }
+    }
+    __syncthreads();
+    // the new token's K / V (one wave per kv head)
+    const int slot = p->slot;
+    for (int kh = wave; kh < d.KV; kh += blockDim.x >> 6) {
+        const float *kr = b.k + kh * HD, *vr = b.v + kh * HD;
+        const size_t row = static_cast<size_t>(kh) * d.capacity + slot;
+        if (kv.k32) {
+            for (int i = lane; i < HD; i += 64) {
+                kv.k32[row * HD + i] = kr[i];
+                kv.v32[row * HD + i] = vr[i];
+            }
+        } else {
+            float mk = 0.0f, mv = 0.0f;
+            for (int i = lane; i < HD; i += 64) {
+                mk = fmaxf(mk, fabsf(kr[i]));
+                mv = fmaxf(mv, fabsf(vr[i]));
+            }
+            mk = wave_max(mk, lane);
+            mv = wave_max(mv, lane);
+            const float sk = mk > 0 ? mk / 127.0f : 1.0f, sv = mv > 0 ? mv / 127.0f : 1.0f;
+            const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
+            if (lane == 0) {
+                kv.ks[row] = sk;
+                kv.vs[row] = sv;
+            }
+            for (int i = lane; i < HD; i += 64) {
+                const float qk = fmaxf(-127.0f, fminf(127.0f, rintf(kr[i] * ik)));
+                const float qv = fmaxf(-127.0f, fminf(127.0f, rintf(vr[i] * iv)));
+                kv.k8[row * HD + i] = static_cast<int8_t>(qk);
+                kv.v8[row * HD + i] = static_cast<int8_t>(qv);
+            }
+        }
+    }
+    // slot list of this position (engine.cpp:907-909, cache_slot engine.cpp:500)
+    for (int s = threadIdx.x; s < p->length; s += blockDim.x) {
+        const int pos = s < p->prefix_count ? s : p->start + s - p->prefix_count;
+        b.slots[s] = !p->window ? pos : pos < p->prefix ? pos : p->prefix + (pos - p->prefix) % p->window;
+    }
+}
+
+// fp32-KV attention of one token (engine.cpp:915-929 and 816-897, the fp32
+// branch): one workgroup per kv head, its G query heads together. Scores are
+// the reference's sequential dot times 1/sqrt(HD); the softmax sum is a tree
+// sum, and each output element sums its slots in order over two interleaved
+// halves of the slot list.
+__global__ __launch_bounds__(256) void eng_attn_f32_kernel(EngineBufs b, KvLayer kv, int length, EngineDims d) {
+    extern __shared__ float sc[];  // [G][length]
+    __shared__ float qs[1024];      // the G query heads, G * HD <= 1024
+    __shared__ float part[256];
+    __shared__ float red[4];
+    const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, t = threadIdx.x;
+    const float *kc = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
+    const float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
+    for (int i = t; i < G * HD; i += blockDim.x) qs[i] = b.q[kh * G * HD + i];
+    __syncthreads();
+    for (int s = t; s < length; s += blockDim.x) {
+        const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(b.slots[s]) * HD);
+        for (int g = 0; g < G; ++g) {
+            const float *q = qs + g * HD;
+            float dot = 0.0f;
+            for (int c = 0; c < HD / 4; ++c) {
+                const float4 k = k4[c];
+                dot += q[4 * c] * k.x;
+                dot += q[4 * c + 1] * k.y;
+                dot += q[4 * c + 2] * k.z;
+                dot += q[4 * c + 3] * k.w;
+            }
+            sc[g * length + s] = dot * d.scale;
+        }
+    }
+    __syncthreads();
+    for (int g = 0; g < G; ++g) {
+        float mx = -INFINITY;
+        for (int s = t; s < length; s += blockDim.x) mx = fmaxf(mx, sc[g * length + s]);
+        mx = block_max(mx, red);
+        float den = 0.0f;
+        for (int s = t; s < length; s += blockDim.x) {
+            const float e = expf(sc[g * length + s] - mx);
+            sc[g * length + s] = e;
+            den += e;
+        }
+        den = block_sum(den, red);
+        const float inv = 1.0f / den;
+        for (int s = t; s < length; s += blockDim.x) sc[g * length + s] *= inv;
+        __syncthreads();
+    }
+    const int pairs = G * HD;
+    if (pairs <= 128) {  // two threads per output element, the even and the odd slots
+        if (t < 2 * pairs) {
+            const int o = t % pairs, h = t / pairs, g = o / HD, i = o % HD;
+            const float *p = sc + g * length;
+            float a = 0.0f;
+#pragma unroll 4
+            for (int s = h; s < length; s += 2) a += p[s] * vc[static_cast<size_t>(b.slots[s]) * HD + i];
+            part[t] = a;
+        }
+        __syncthreads();
+        if (t < pairs) b.att[kh * G * HD + t] = part[t] + part[pairs + t];
+    } else {
+        for (int o = t; o < pairs; o += blockDim.x) {
+            const int g = o / HD, i = o % HD;
+            const float *p = sc + g * length;
+            float a = 0.0f;
+#pragma unroll 4
+            for (int s = 0; s < length; ++s) a += p[s] * vc[static_cast<size_t>(b.slots[s]) * HD + i];
+            b.att[kh * G * HD + o] = a;
+        }
+    }
+}
+
+// att *= sigmoid(gate); then the activation quantiser (engine.cpp:1023-1024).
+__global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b, EngineDims d) {
+    __shared__ float red[kEngThreads / 64];
+    for (int i = threadIdx.x; i < d.A; i += blockDim.x) b.att[i] *= sigmoidf_(b.gate[i]);
+    __syncthreads();
+    quantize_block(b.att, d.A, d.abits, red);
+}
+
+// engine.cpp:1025-1039: attention residual, Hadamard MLP, mHC residual
+// routing (Sinkhorn) and lane mixing, the layer's hidden state; then the next
+// layer's rms of x when `next_rms`.
+__global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b, LayerDev ld, MhcDev mh, int l,
+                                                               int next_rms, EngineDims d) {
+    __shared__ float red[kEngThreads / 64];
+    __shared__ float mlp[4096];
+    __shared__ float hr[64], hpo[8];
+    const int D = d.D, N = d.N;
+    if (threadIdx.x < 64) {  // residual routing: wave 0
+        const int lane = threadIdx.x, ij = lane % (N * N);
+        const float a = sinkhorn_wave(b.hres[ij] * mh.a_res[l] + mh.b_res[l * N * N + ij], N, lane);
+        if (lane < N * N) hr[lane] = a;
+        if (lane < N) hpo[lane] = b.hpost[lane];
+    }
+    rms_block(b.proj, b.proj, D, ld.post_norm, red);
+    const float ag = sigmoidf_(ld.attn_gate[0]);
+    for (int i = threadIdx.x; i < D; i += blockDim.x) b.bx[i] += ag * b.proj[i];
+    __syncthreads();
+    rms_block(b.bx, b.z, D, ld.pre_hada, red);
+    for (int i = threadIdx.x; i < d.hada; i += blockDim.x) mlp[i] = i < D ? b.z[i] * ld.d1[i] : 0.0f;
+    __syncthreads();
+    hadamard_block(mlp, d.hada, d.inv_hada);
+    for (int i = threadIdx.x; i < d.hada; i += blockDim.x) {
+        const float a = mlp[i] * ld.d2[i];
+        mlp[i] = a * sigmoidf_(a);
+    }
+    __syncthreads();
+    hadamard_block(mlp, d.hada, d.inv_hada);
+    for (int i = threadIdx.x; i < D; i += blockDim.x) b.bx[i] = b.bx[i] + ld.d3[i] * mlp[i] - b.u[i];
+    __syncthreads();
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {  // column i of every lane: this thread alone
+        float nx[8];
+        for (int n = 0; n < N; ++n) {
+            float val = hpo[n] * b.bx[i];
+            for (int j = 0; j < N; ++j) val += hr[n * N + j] * b.x[j * D + i];
+            nx[n] = val;
+        }
+        float sum = 0.0f;
+        for (int n = 0; n < N; ++n) {
+            b.x[n * D + i] = nx[n];
+            sum += nx[n];
+        }
+        b.hidden[l * D + i] = sum / static_cast<float>(N);
+    }
+    __syncthreads();
+    if (next_rms) rms_block(b.x, b.nx, N * D, nullptr, red);
+}
+
+// z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
+__global__ __launch_bounds__(kEngThreads) void eng_final_kernel(EngineBufs b, const float *__restrict__ final_norm,
+                                                                EngineDims d) {
+    __shared__ float red[kEngThreads / 64];
+    rms_block(b.hidden + (d.layers - 1) * d.D, b.zf, d.D, final_norm, red);
+}
+
+__global__ __launch_bounds__(kEngThreads) void eng_quantize_kernel(float *x, int n, int bits) {
+    __shared__ float red[kEngThreads / 64];
+    quantize_block(x, n, bits, red);
+}
+
+// One wave per output row of a dense fp32 matrix.
+__global__ __launch_bounds__(256) void eng_dense_kernel(const float *__restrict__ w, int cols, int first, int rows,
+                                                        const float *__restrict__ x, float *__restrict__ y) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *row = w + static_cast<size_t>(first + r) * cols;
+    float s = 0.0f;
+    for (int i = lane; i < cols; i += 64) s += row[i] * x[i];
+    s = wave_sum(s, lane);
+    if (lane == 0) y[r] = s;
+}
+
+__global__ __launch_bounds__(256) void eng_dense_rows_kernel(const float *__restrict__ w, int cols,
+                                                             const int64_t *__restrict__ ids, int count,
+                                                             float *__restrict__ y) {
+    const int i = blockIdx.y;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x)
+        y[static_cast<size_t>(i) * cols + c] = w[static_cast<size_t>(ids[i]) * cols + c];
+}
+
+}  // namespace
+
+void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, hipStream_t s) {
+    hipLaunchKernelGGL(eng_start_kernel, dim3(1), dim3(kEngThreads), 0, s, z, b, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_engram_in(const EngineBufs &b, const StepParams *p, int site, const EngineDims &d, hipStream_t s) {
+    hipLaunchKernelGGL(eng_engram_in_kernel, dim3(1), dim3(kEngThreads), 0, s, b, p, site, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepParams *p, int site,
+                           const EngineDims &d, hipStream_t s) {
+    hipLaunchKernelGGL(eng_engram_out_kernel, dim3(1), dim3(kEngThreads), 0, s, b, taps, p, site, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
+                    const float *const *phi, const int *sites, int nsites, const EngineDims &d, hipStream_t s) {
+    MixArgs m{};
+    for (int i = 0; i < 3; ++i) m.phi[i] = phi[i];
+    m.l = l;
+    m.nsites = nsites;
+    for (int i = 0; i < nsites; ++i) m.sites[i] = sites[i];
+    for (int i = 0; i < 3; ++i) m.mhc_row[i] = mhc_row[i];
+    hipLaunchKernelGGL(eng_mix_kernel, dim3(1), dim3(kEngThreads), 0, s, b, ld, mh, m, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
+                   const EngineDims &d, hipStream_t s) {
+    hipLaunchKernelGGL(eng_qk_kernel, dim3(1), dim3(kEngThreads), 0, s, b, ld, kv, p, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_attn_f32(const EngineBufs &b, const KvLayer &kv, int length, const EngineDims &d, hipStream_t s) {
+    const size_t lds = static_cast<size_t>(d.H / d.KV) * length * sizeof(float);
+    hipLaunchKernelGGL(eng_attn_f32_kernel, dim3(d.KV), dim3(256), lds, s, b, kv, length, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_gate(const EngineBufs &b, const EngineDims &d, hipStream_t s) {
+    hipLaunchKernelGGL(eng_gate_kernel, dim3(1), dim3(kEngThreads), 0, s, b, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
+                     const EngineDims &d, hipStream_t s) {
+    hipLaunchKernelGGL(eng_post_kernel, dim3(1), dim3(kEngThreads), 0, s, b, ld, mh, l, next_rms ? 1 : 0, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, hipStream_t s) {
+    hipLaunchKernelGGL(eng_final_kernel, dim3(1), dim3(kEngThreads), 0, s, b, final_norm, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_quantize(float *x, int n, int bits, hipStream_t s) {
+    if (!bits) return;
+    hipLaunchKernelGGL(eng_quantize_kernel, dim3(1), dim3(kEngThreads), 0, s, x, n, bits);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_dense(const float *w, int cols, int first, int rows, const float *x, float *y, hipStream_t s) {
+    if (rows <= 0) return;
+    hipLaunchKernelGGL(eng_dense_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, w, cols, first, rows, x, y);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_dense_rows(const float *w, int cols, const int64_t *ids, int count, float *y, hipStream_t s) {
+    if (count <= 0) return;
+    hipLaunchKernelGGL(eng_dense_rows_kernel, dim3((cols + 255) / 256, count), dim3(256), 0, s, w, cols, ids, count,
+                       y);
+    ND_HIP(hipGetLastError());
+}
+
+}  // namespace nd

@@ -323,3 +323,63 @@ class RefAttention:
         out = np.empty((self.heads, self.hd), np.float32)
         self.L.refh_attn_compute(self.h, self.count - 1, _ptr(q), _ptr(out))
         return out
+
+
+class RefEngine:
+    """The reference's own Engine (engine.cpp, built into oracle/_ref) over an archive, with the tensor
+    descriptors NativeEngine builds (needle2/native.py:382-395): CQ records through the reference's CQ handles,
+    everything else (the mHC matrices too) as dequantized fp32."""
+
+    def __init__(self, archive, activation_bits=0, int8_kv=False, threads=1):
+        from openneedle_amd.archive import CQ
+        from openneedle_amd.engine import _TensorDesc, _EngineConfig, engine_config, engine_tensors
+        L = ref()
+        if L is None:
+            raise RuntimeError("oracle/_ref was not built (reference sources absent)")
+        self.L = L
+        self.m = archive.metadata
+        self._owners, descs = [], []
+        for name in engine_tensors(archive):
+            rec = archive.tensors[name]
+            if rec.dtype == CQ and not name.startswith("mhc_"):
+                q = RefCQ(rec.packed, rec.norms, rec.shape, rec.bits, rec.group_size, rec.cq_codebook())
+                self._owners.append(q)
+                descs.append(_TensorDesc(q.h, None, *rec.shape))
+            else:
+                a = np.ascontiguousarray(rec.dequantize(), dtype=np.float32)
+                self._owners.append(a)
+                rows, cols = (a.shape[0], int(np.prod(a.shape[1:]))) if a.ndim > 1 else (1, a.size)
+                descs.append(_TensorDesc(None, a.ctypes.data, rows, cols))
+        self._cfg = engine_config(self.m)
+        self._descs = (_TensorDesc * len(descs))(*descs)
+        for name, args, res in (
+                ("needle2_engine_create", [ct.POINTER(_EngineConfig), ct.POINTER(_TensorDesc), ct.c_int, ct.c_int,
+                                           ct.c_int], ct.c_void_p),
+                ("needle2_engine_destroy", [ct.c_void_p], None),
+                ("needle2_engine_reset", [ct.c_void_p, ct.c_int], None),
+                ("needle2_engine_step", [ct.c_void_p, ct.c_int, ct.c_void_p, ct.c_void_p], ct.c_int),
+                ("needle2_engine_step_candidates", [ct.c_void_p, ct.c_int, ct.c_void_p, ct.c_int, ct.c_void_p,
+                                                    ct.c_void_p], ct.c_int),
+                ("needle2_engine_set_int8_kv", [ct.c_void_p, ct.c_int], ct.c_int),
+                ("needle2_engine_error", [], ct.c_char_p)):
+            f = getattr(L, name)
+            f.argtypes, f.restype = args, res
+        self.h = L.needle2_engine_create(ct.byref(self._cfg), self._descs, len(descs), threads, activation_bits)
+        if not self.h:
+            raise RuntimeError(L.needle2_engine_error().decode())
+        if int8_kv:
+            assert L.needle2_engine_set_int8_kv(self.h, 1) == 0
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.needle2_engine_destroy(self.h)
+
+    def reset(self, prefix=0):
+        self.L.needle2_engine_reset(self.h, prefix)
+
+    def step(self, token):
+        logits = np.empty(self.m["vocab_size"], np.float32)
+        hidden = np.empty((self.m["num_layers"], self.m["d_model"]), np.float32)
+        if self.L.needle2_engine_step(self.h, int(token), logits.ctypes.data, hidden.ctypes.data):
+            raise RuntimeError(self.L.needle2_engine_error().decode())
+        return logits, hidden

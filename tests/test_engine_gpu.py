@@ -1,0 +1,121 @@
+"""The GPU engine behind needle2_engine_* against the reference's own Engine (engine.cpp, built from source in
+oracle/_ref) on the same archive: logits and per-layer hidden states of every step.
+
+The CQ GEMVs are bit-exact; the glue (norms, gates, softmax, Hadamard MLP, Sinkhorn) uses tree reductions and
+the device exp / log, so the bar is fp32 rounding accumulated over the layers: |gpu - ref| <= ATOL + RTOL |ref|.
+With the int8 KV cache or 8-bit activations a rounding difference can move one quantised code by one step, so
+those cases are bounded by a relative L2 error instead."""
+import numpy as np
+import pytest
+
+import oracle
+from openneedle_amd.archive import Archive, synthetic_model, synthetic_released
+from openneedle_amd.engine import NativeEngine
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-5, 2e-4
+SMALL = dict(vocab_size=512, d_model=64, num_heads=2, num_kv_heads=1, num_layers=3, head_dim=32, max_seq_len=64,
+             hada_n=64, mhc_lanes=4, engram_slots=32, engram_sub_dim=16, num_engram_tables=4, engram_conv_taps=4,
+             engram_conv_dilation=3)
+TOKENS = [5, 17, 300, 2, 9, 9, 511, 0, 42, 77, 128, 3, 64, 200, 7, 8, 250, 31, 1, 99]
+
+
+def small(window=0, seed=1):
+    return Archive(synthetic_model(SMALL, engram_layers=(1,), engram_orders=(2, 3), kv_window=window, group=32,
+                                   seed=seed))
+
+
+def run_both(archive, tokens, int8_kv=False, abits=0):
+    gpu = NativeEngine(archive, activation_bits=abits, kv_cache="int8" if int8_kv else "fp32")
+    ref = oracle.RefEngine(archive, abits, int8_kv)
+    out = []
+    for t in tokens:
+        lg, hd = gpu.step(t, return_hidden=True)
+        rl, rh = ref.step(t)
+        out.append((lg, hd, rl, rh))
+    return out
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("window", [0, 8])
+def test_small_model_fp32_kv(window):
+    for i, (lg, hd, rl, rh) in enumerate(run_both(small(window), TOKENS)):
+        print(f"step {i}: logits {np.abs(lg - rl).max():.2e} hidden {np.abs(hd - rh).max():.2e}", flush=True)
+        np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL, err_msg=f"hidden, step {i}")
+        np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL, err_msg=f"logits, step {i}")
+
+
+@pytest.mark.parametrize("window", [0, 8])
+def test_small_model_int8_kv(window):
+    for i, (lg, hd, rl, rh) in enumerate(run_both(small(window, seed=2), TOKENS, int8_kv=True)):
+        print(f"step {i}: logits rel {rel_l2(lg, rl):.2e} hidden rel {rel_l2(hd, rh):.2e}", flush=True)
+        assert rel_l2(hd, rh) < 1e-3 and rel_l2(lg, rl) < 1e-3, f"step {i}"
+
+
+def test_small_model_quantized_activations():
+    for i, (lg, hd, rl, rh) in enumerate(run_both(small(0, seed=3), TOKENS[:10], abits=8)):
+        print(f"step {i}: logits rel {rel_l2(lg, rl):.2e} hidden rel {rel_l2(hd, rh):.2e}", flush=True)
+        assert rel_l2(hd, rh) < 2e-2 and rel_l2(lg, rl) < 2e-2, f"step {i}"
+
+
+def test_released_geometry():
+    """27 layers of the released geometry (random contents), fp32 and int8 KV."""
+    a = Archive(synthetic_released(seed=5, tokenizer_bytes=0))
+    for int8 in (False, True):
+        for i, (lg, hd, rl, rh) in enumerate(run_both(a, TOKENS[:6], int8_kv=int8)):
+            print(f"int8={int8} step {i}: logits {np.abs(lg - rl).max():.2e} rel {rel_l2(lg, rl):.2e}", flush=True)
+            if int8:  # 27 layers: a code moved by one step in some layer's K / V shows in every later layer
+                assert rel_l2(hd, rh) < 1e-2 and rel_l2(lg, rl) < 1e-2
+            else:
+                np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL)
+                np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL)
+
+
+def test_candidates_equal_full_logits():
+    """needle2's own contract (tests/test_candidate_projection_dense.py): candidate logits equal the full
+    projection indexed by the candidates, order and duplicates kept, and leave the state as step does."""
+    a = small(0, seed=4)
+    full, sel = NativeEngine(a), NativeEngine(a)
+    rng = np.random.default_rng(51)
+    for count in (2, 142, 300, 512):
+        ids = rng.permutation(512)[:count].astype(np.int32)
+        ids[-1] = ids[0]
+        full.reset()
+        sel.reset()
+        for t in (2, 51, 302, 17):
+            e, eh = full.step(t, return_hidden=True)
+            g, gh = sel.step_candidates(t, ids, return_hidden=True)
+            np.testing.assert_array_equal(g, e[ids])
+            np.testing.assert_array_equal(gh, eh)
+        np.testing.assert_array_equal(sel.step(33), full.step(33))
+
+
+def test_prefill_equals_steps():
+    a = small(8, seed=6)
+    e1, e2 = NativeEngine(a), NativeEngine(a)
+    stepped = np.stack([e1.step(t) for t in TOKENS[:12]])
+    np.testing.assert_array_equal(e2.prefill(TOKENS[:12]), stepped)
+    np.testing.assert_array_equal(e2.step(4), e1.step(4))
+    e3 = NativeEngine(a)
+    np.testing.assert_array_equal(e3.prefill(TOKENS[:12], last_only=True), stepped[-1])
+
+
+def test_engine_errors():
+    e = NativeEngine(small())
+    with pytest.raises(ValueError, match="within the vocabulary"):
+        e.step(512)
+    with pytest.raises(ValueError, match="candidate outside vocabulary"):
+        e.step_candidates(1, [0, 512])
+    with pytest.raises(RuntimeError, match="SDOT requires"):
+        NativeEngine(small(), matmul="sdot")
+    for _ in range(64):
+        e.step(1, compute_logits=False)
+    with pytest.raises(RuntimeError, match="maximum context reached"):
+        e.step(1)
+    assert e.kv_storage_bytes == 2 * 3 * 1 * 64 * 32 * 4
+    e.set_int8_kv(True)
+    assert e.kv_storage_bytes == 2 * 3 * 1 * 64 * 32 + 2 * 3 * 1 * 64 * 4
