@@ -177,6 +177,7 @@ struct GpuEngine {
     std::vector<Projection> mhc_proj, qkvg, oproj;
     std::vector<std::array<int, 3>> mhc_row;
     const float *phi[3] = {nullptr, nullptr, nullptr};  // dense mHC matrices (null: CQ)
+    int mhc_rows[3] = {0, 0, 0};
     std::vector<Projection> engram_kv;
     Projection lm_head;
     Staging st;  // the engine's own staging (candidate rows)
@@ -369,13 +370,14 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
             for (int m = 0; m < 3; ++m) {
                 const Mat &M = mat(mhi + 6 + m, c.layers * rows[m], N * D);
                 const int first = l * rows[m];
-                if (M.cq) {  // the GEMV's row tiles; dense ones run inside the mixing kernel
+                if (M.cq) {  // the GEMV's row tiles; dense rows go through one multi-matrix launch
                     mhc_row[l][m] = first - first / kRowsPerBlock * kRowsPerBlock;
                     mhc_proj[l].add(M, first, rows[m], b.mhc_out[m], pend);
                 } else {
                     mhc_row[l][m] = 0;
                 }
                 phi[m] = M.cq ? nullptr : M.dense;
+                mhc_rows[m] = rows[m];
             }
             mhc_proj[l].finish(pend, b.nx);
         }
@@ -516,13 +518,20 @@ void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
     const int G = c.heads / c.kvheads;
     for (int l = 0; l < c.layers; ++l) {
         mhc_proj[l].run(s);
+        {
+            const int first[3] = {l * mhc_rows[0], l * mhc_rows[1], l * mhc_rows[2]};
+            launch_eng_dense3(phi, first, mhc_rows, b.mhc_out, c.lanes * c.dim, b.nx, s);
+        }
         int sites[kEngMaxSites], ns = 0;
         for (int k = 0; k < c.num_sites; ++k)
             if (c.sites[k] == l) sites[ns++] = k;
-        launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), phi, sites, ns, dims, s);
+        launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, s);
         qkvg[l].run(s);
-        launch_eng_qk(b, layer[l], kv[l], dp, dims, s);
-        if (int8_kv) {
+        if (!int8_kv) {
+            launch_eng_attn_fused(b, layer[l], kv[l], dp, p.length, dims, s);
+            launch_eng_quantize(b.att, c.heads * HD, abits, s);
+        } else {
+            launch_eng_qk(b, layer[l], kv[l], dp, dims, s);
             AttnArgs a{};
             a.k8 = kv[l].k8;
             a.v8 = kv[l].v8;
@@ -546,10 +555,8 @@ void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
             a.part = part.p;
             a.scale = dims.scale;
             launch_attention(a, G, s);
-        } else {
-            launch_eng_attn_f32(b, kv[l], p.length, dims, s);
+            launch_eng_gate(b, dims, s);
         }
-        launch_eng_gate(b, dims, s);
         oproj[l].run(s);
         launch_eng_post(b, layer[l], mh, l, l + 1 < c.layers, dims, s);
     }

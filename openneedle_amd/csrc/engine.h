@@ -67,14 +67,15 @@ void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, 
 void launch_eng_engram_in(const EngineBufs &b, const StepParams *p, int site, const EngineDims &d, hipStream_t s);
 void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepParams *p, int site,
                            const EngineDims &d, hipStream_t s);
-// mixing, engram gates and the attention input of layer l; phi[m]: dense mHC
-// matrix m (computed in-kernel from b.nx) or null, then mhc_row[m] is the
+// mixing, engram gates and the attention input of layer l; mhc_row[m] is the
 // first row of the layer inside b.mhc_out[m]; sites: engram sites at this layer
 void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
-                    const float *const *phi, const int *sites, int nsites, const EngineDims &d, hipStream_t s);
+                    const int *sites, int nsites, const EngineDims &d, hipStream_t s);
 void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                    const EngineDims &d, hipStream_t s);
-void launch_eng_attn_f32(const EngineBufs &b, const KvLayer &kv, int length, const EngineDims &d, hipStream_t s);
+// fp32 KV: norms + RoPE + KV store + attention + output gate of every kv head, one launch
+void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
+                           int length, const EngineDims &d, hipStream_t s);
 void launch_eng_gate(const EngineBufs &b, const EngineDims &d, hipStream_t s);
 void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
                      const EngineDims &d, hipStream_t s);
@@ -82,6 +83,9 @@ void launch_eng_final(const EngineBufs &b, const float *final_norm, const Engine
 void launch_eng_quantize(float *x, int n, int bits, hipStream_t s);
 // y[r] = dot(W[first + r], x) over cols for r < rows (dense fp32 matrices)
 void launch_eng_dense(const float *w, int cols, int first, int rows, const float *x, float *y, hipStream_t s);
+// y[m][r] = dot(W_m[first[m] + r], x) for r < rows[m], m < 3 (a null W_m is skipped), one launch
+void launch_eng_dense3(const float *const *w, const int *first, const int *rows, float *const *y, int cols,
+                       const float *x, hipStream_t s);
 // y[i][:] = W[ids[i]][:] (dense row copy)
 void launch_eng_dense_rows(const float *w, int cols, const int64_t *ids, int count, float *y, hipStream_t s);
 

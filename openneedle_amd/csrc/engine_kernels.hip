@@ -74,9 +74,35 @@ __device__ void quantize_block(float *x, int n, int bits, float *red) {
     __syncthreads();
 }
 
-// In-place normalised FWHT of v[0..n) in LDS (n a power of two). Ends with a barrier.
+// One butterfly stage of stride H < 64 on a wave's 64 consecutive values:
+// the lower element becomes a + b, the upper a - b.
+template <int H>
+__device__ __forceinline__ float fwht_stage(float x, int lane) {
+    const float p = butterfly_partner<H>(x, lane);
+    return (lane & H) ? p - x : x + p;
+}
+
+// In-place normalised FWHT of v[0..n) in LDS (n a power of two): stages 1..32
+// in registers over 64-value chunks, the larger strides through LDS, in the
+// reference's stage order. Ends with a barrier.
 __device__ void hadamard_block(float *v, int n, float inv) {
-    for (int h = 1; h < n; h <<= 1) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    int h = 1;
+    if (n >= 64) {
+        for (int c = wave; c < n / 64; c += waves) {
+            float x = v[c * 64 + lane];
+            x = fwht_stage<1>(x, lane);
+            x = fwht_stage<2>(x, lane);
+            x = fwht_stage<4>(x, lane);
+            x = fwht_stage<8>(x, lane);
+            x = fwht_stage<16>(x, lane);
+            x = fwht_stage<32>(x, lane);
+            v[c * 64 + lane] = x;
+        }
+        __syncthreads();
+        h = 64;
+    }
+    for (; h < n; h <<= 1) {
         for (int p = threadIdx.x; p < n / 2; p += blockDim.x) {
             const int j = (p / h) * 2 * h + p % h;
             const float a = v[j], b = v[j + h];
@@ -192,7 +218,6 @@ struct MixArgs {
     int l, nsites;
     int sites[kEngMaxSites];
     int mhc_row[3];
-    const float *phi[3];  // dense mHC matrices (rows of all layers, N * D columns), or null: b.mhc_out holds them
 };
 
 // engine.cpp:980-992: lane gates from the mHC projections, the pre-mixed
@@ -204,21 +229,10 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b, Laye
     __shared__ float zs[4096], ps[4096];
     __shared__ float proj[2 * 8 + 64];  // this layer's mHC projections: pre [N], post [N], res [N * N]
     const int N = d.N, D = d.D, l = m.l;
-    const int rows[3] = {N, N, N * N}, base[3] = {0, N, 2 * N};
-    {  // dense matrices: one wave per row; CQ ones: the GEMV's output
-        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, cols = N * D;
-        for (int task = wave; task < 2 * N + N * N; task += blockDim.x >> 6) {
-            const int mm = task < N ? 0 : task < 2 * N ? 1 : 2, r = task - base[mm];
-            if (m.phi[mm]) {
-                const float *w = m.phi[mm] + static_cast<size_t>(l * rows[mm] + r) * cols;
-                float sum = 0.0f;
-                for (int i = lane; i < cols; i += 64) sum += w[i] * b.nx[i];
-                sum = wave_sum(sum, lane);
-                if (lane == 0) proj[task] = sum;
-            } else if (lane == 0) {
-                proj[task] = b.mhc_out[mm][m.mhc_row[mm] + r];
-            }
-        }
+    const int base[3] = {0, N, 2 * N};
+    for (int task = threadIdx.x; task < 2 * N + N * N; task += blockDim.x) {
+        const int mm = task < N ? 0 : task < 2 * N ? 1 : 2;
+        proj[task] = b.mhc_out[mm][m.mhc_row[mm] + task - base[mm]];
     }
     __syncthreads();
     if (threadIdx.x < static_cast<unsigned>(N)) {
@@ -317,23 +331,46 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b, Layer
     }
 }
 
-// fp32-KV attention of one token (engine.cpp:915-929 and 816-897, the fp32
-// branch): one workgroup per kv head, its G query heads together. Scores are
-// the reference's sequential dot times 1/sqrt(HD); the softmax sum is a tree
-// sum, and each output element sums its slots in order over two interleaved
-// halves of the slot list.
-__global__ __launch_bounds__(256) void eng_attn_f32_kernel(EngineBufs b, KvLayer kv, int length, EngineDims d) {
+// The fp32-KV attention step of one kv head in one workgroup: the norms and
+// RoPE of its G query heads and of its K head, the new K / V row into the
+// cache, attention over the slot list (computed in place from the position,
+// engine.cpp:900-909) and the output gate att *= sigmoid(gate)
+// (engine.cpp:994-1023). Nothing crosses kv heads, so one launch does it all.
+__device__ __forceinline__ int slot_at(const StepParams *p, int s) {
+    const int pos = s < p->prefix_count ? s : p->start + s - p->prefix_count;
+    return !p->window ? pos : pos < p->prefix ? pos : p->prefix + (pos - p->prefix) % p->window;
+}
+
+__global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b, LayerDev ld, KvLayer kv,
+                                                             const StepParams *__restrict__ p, EngineDims d) {
     extern __shared__ float sc[];  // [G][length]
-    __shared__ float qs[1024];      // the G query heads, G * HD <= 1024
+    __shared__ float qs[1024];
     __shared__ float part[256];
     __shared__ float red[4];
-    const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, t = threadIdx.x;
-    const float *kc = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
-    const float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
-    for (int i = t; i < G * HD; i += blockDim.x) qs[i] = b.q[kh * G * HD + i];
+    const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63, length = p->length;
+    float *kc = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
+    float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
+    // norms + RoPE: heads 0..G-1 are this block's query heads (into qs), head G its K row (into the cache)
+    for (int h = wave; h <= G; h += blockDim.x >> 6) {
+        const float *src = h < G ? b.q + (kh * G + h) * HD : b.k + kh * HD;
+        const float *gain = h < G ? ld.q_norm : ld.k_norm;
+        float *dst = h < G ? qs + h * HD : kc + static_cast<size_t>(p->slot) * HD;
+        float ss = 0.0f;
+        for (int i = lane; i < HD; i += 64) ss += src[i] * src[i];
+        ss = wave_sum(ss, lane);
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + 1e-6f);
+        for (int j = lane; j < half; j += 64) {
+            const float co = p->rope_cos[j], si = p->rope_sin[j];
+            const float a = src[j] * r * (1.0f + gain[j]), c = src[j + half] * r * (1.0f + gain[j + half]);
+            dst[j] = a * co - c * si;
+            dst[j + half] = c * co + a * si;
+        }
+    }
+    for (int i = t; i < HD; i += blockDim.x) vc[static_cast<size_t>(p->slot) * HD + i] = b.v[kh * HD + i];
     __syncthreads();
     for (int s = t; s < length; s += blockDim.x) {
-        const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(b.slots[s]) * HD);
+        const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, s)) * HD);
         for (int g = 0; g < G; ++g) {
             const float *q = qs + g * HD;
             float dot = 0.0f;
@@ -367,22 +404,25 @@ __global__ __launch_bounds__(256) void eng_attn_f32_kernel(EngineBufs b, KvLayer
     if (pairs <= 128) {  // two threads per output element, the even and the odd slots
         if (t < 2 * pairs) {
             const int o = t % pairs, h = t / pairs, g = o / HD, i = o % HD;
-            const float *p = sc + g * length;
+            const float *pr = sc + g * length;
             float a = 0.0f;
 #pragma unroll 4
-            for (int s = h; s < length; s += 2) a += p[s] * vc[static_cast<size_t>(b.slots[s]) * HD + i];
+            for (int s = h; s < length; s += 2) a += pr[s] * vc[static_cast<size_t>(slot_at(p, s)) * HD + i];
             part[t] = a;
         }
         __syncthreads();
-        if (t < pairs) b.att[kh * G * HD + t] = part[t] + part[pairs + t];
+        if (t < pairs) {
+            const int o = kh * G * HD + t;
+            b.att[o] = (part[t] + part[pairs + t]) * sigmoidf_(b.gate[o]);
+        }
     } else {
         for (int o = t; o < pairs; o += blockDim.x) {
             const int g = o / HD, i = o % HD;
-            const float *p = sc + g * length;
+            const float *pr = sc + g * length;
             float a = 0.0f;
 #pragma unroll 4
-            for (int s = 0; s < length; ++s) a += p[s] * vc[static_cast<size_t>(b.slots[s]) * HD + i];
-            b.att[kh * G * HD + o] = a;
+            for (int s = 0; s < length; ++s) a += pr[s] * vc[static_cast<size_t>(slot_at(p, s)) * HD + i];
+            b.att[kh * G * HD + o] = a * sigmoidf_(b.gate[kh * G * HD + o]);
         }
     }
 }
@@ -468,6 +508,25 @@ __global__ __launch_bounds__(256) void eng_dense_kernel(const float *__restrict_
     if (lane == 0) y[r] = s;
 }
 
+// Rows of up to three dense matrices over one input, one workgroup per row:
+// block b < rows[0] is row first[0] + b of w[0] into y[0][b], and so on.
+struct DenseRows {
+    const float *w[3];
+    float *y[3];
+    int first[3], rows[3];
+};
+
+__global__ __launch_bounds__(256) void eng_dense_multi_kernel(DenseRows a, int cols, const float *__restrict__ x) {
+    __shared__ float red[4];
+    int r = blockIdx.x, m = 0;
+    while (m < 2 && r >= a.rows[m]) r -= a.rows[m++];
+    const float *row = a.w[m] + static_cast<size_t>(a.first[m] + r) * cols;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < cols; i += blockDim.x) s += row[i] * x[i];
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) a.y[m][r] = s;
+}
+
 __global__ __launch_bounds__(256) void eng_dense_rows_kernel(const float *__restrict__ w, int cols,
                                                              const int64_t *__restrict__ ids, int count,
                                                              float *__restrict__ y) {
@@ -495,9 +554,8 @@ void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepPar
 }
 
 void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
-                    const float *const *phi, const int *sites, int nsites, const EngineDims &d, hipStream_t s) {
+                    const int *sites, int nsites, const EngineDims &d, hipStream_t s) {
     MixArgs m{};
-    for (int i = 0; i < 3; ++i) m.phi[i] = phi[i];
     m.l = l;
     m.nsites = nsites;
     for (int i = 0; i < nsites; ++i) m.sites[i] = sites[i];
@@ -512,9 +570,10 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_attn_f32(const EngineBufs &b, const KvLayer &kv, int length, const EngineDims &d, hipStream_t s) {
+void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
+                           int length, const EngineDims &d, hipStream_t s) {
     const size_t lds = static_cast<size_t>(d.H / d.KV) * length * sizeof(float);
-    hipLaunchKernelGGL(eng_attn_f32_kernel, dim3(d.KV), dim3(256), lds, s, b, kv, length, d);
+    hipLaunchKernelGGL(eng_attn_fused_kernel, dim3(d.KV), dim3(256), lds, s, b, ld, kv, p, d);
     ND_HIP(hipGetLastError());
 }
 
@@ -543,6 +602,22 @@ void launch_eng_quantize(float *x, int n, int bits, hipStream_t s) {
 void launch_eng_dense(const float *w, int cols, int first, int rows, const float *x, float *y, hipStream_t s) {
     if (rows <= 0) return;
     hipLaunchKernelGGL(eng_dense_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, w, cols, first, rows, x, y);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_dense3(const float *const *w, const int *first, const int *rows, float *const *y, int cols,
+                       const float *x, hipStream_t s) {
+    DenseRows a{};
+    int total = 0;
+    for (int m = 0; m < 3; ++m) {
+        a.w[m] = w[m];
+        a.y[m] = y[m];
+        a.first[m] = first[m];
+        a.rows[m] = w[m] ? rows[m] : 0;
+        total += a.rows[m];
+    }
+    if (!total) return;
+    hipLaunchKernelGGL(eng_dense_multi_kernel, dim3(total), dim3(256), 0, s, a, cols, x);
     ND_HIP(hipGetLastError());
 }
 
