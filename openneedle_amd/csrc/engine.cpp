@@ -208,7 +208,7 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     ND_CHECK(D > 0 && (N == 1 || N == 2 || N == 4 || N == 8) && c.layers > 0 && c.heads > 0 && c.kvheads > 0 &&
                  c.heads % c.kvheads == 0 && c.heads / c.kvheads <= 8,
              "engine: unsupported geometry (mHC lanes 1, 2, 4 or 8; at most 8 heads per kv head)");
-    ND_CHECK(HD % 4 == 0 && HD <= 2 * kEngMaxHalfHd && D <= 4096 && c.hada >= D && c.hada <= 4096 &&
+    ND_CHECK(HD % 4 == 0 && HD <= 2 * kEngMaxHalfHd && D <= kEngThreads && c.hada >= D && c.hada <= 4096 &&
                  (c.hada & (c.hada - 1)) == 0,
              "engine: unsupported head / Hadamard geometry");
     ND_CHECK(c.num_sites >= 0 && c.num_sites <= kEngMaxSites && c.num_orders >= 0 && c.num_orders <= 4,
@@ -416,7 +416,7 @@ void GpuEngine::reset(int prefix_len) {
     if (int8_kv)
         ND_CHECK(attn_supported(c.head_dim, G), "int8 KV attention: head_dim 32/64/128 with 1, 2, 4 or 8 heads per kv head");
     else
-        ND_CHECK(size_t(G) * capacity * sizeof(float) <= 65536, "fp32 KV attention: heads per kv head x context too large");
+        ND_CHECK(size_t(G) * capacity * sizeof(float) <= 49152, "fp32 KV attention: heads per kv head x context too large");
     const size_t per_layer = size_t(c.kvheads) * capacity * c.head_dim;
     const size_t scales = size_t(c.kvheads) * capacity;
     kv.assign(c.layers, KvLayer{});

@@ -344,8 +344,7 @@ __device__ __forceinline__ int slot_at(const StepParams *p, int s) {
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d) {
     extern __shared__ float sc[];  // [G][length]
-    __shared__ float qs[1024];
-    __shared__ float part[256];
+    __shared__ float qs[8 * 1024];  // query heads, then the partial outputs [R][G][HD] (1024 G floats)
     __shared__ float red[4];
     const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63, length = p->length;
@@ -400,30 +399,38 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b, Layer
         for (int s = t; s < length; s += blockDim.x) sc[g * length + s] *= inv;
         __syncthreads();
     }
-    const int pairs = G * HD;
-    if (pairs <= 128) {  // two threads per output element, the even and the odd slots
-        if (t < 2 * pairs) {
-            const int o = t % pairs, h = t / pairs, g = o / HD, i = o % HD;
-            const float *pr = sc + g * length;
-            float a = 0.0f;
-#pragma unroll 4
-            for (int s = h; s < length; s += 2) a += pr[s] * vc[static_cast<size_t>(slot_at(p, s)) * HD + i];
-            part[t] = a;
-        }
-        __syncthreads();
-        if (t < pairs) {
-            const int o = kh * G * HD + t;
-            b.att[o] = (part[t] + part[pairs + t]) * sigmoidf_(b.gate[o]);
-        }
-    } else {
-        for (int o = t; o < pairs; o += blockDim.x) {
-            const int g = o / HD, i = o % HD;
-            const float *pr = sc + g * length;
-            float a = 0.0f;
-#pragma unroll 4
-            for (int s = 0; s < length; ++s) a += pr[s] * vc[static_cast<size_t>(slot_at(p, s)) * HD + i];
-            b.att[kh * G * HD + o] = a * sigmoidf_(b.gate[kh * G * HD + o]);
-        }
+    // values: thread t takes 16-byte column c = t % (HD / 4) of the V rows of slots r, r + R, ..
+    // (r = t / (HD / 4), R = 256 / (HD / 4) subsets), so its loads are all in flight together; the R
+    // partial sums per output then add up in subset order
+    constexpr int kMaxG = 8;
+    const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
+    float4 acc[kMaxG];
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+    for (int s = r; s < length; s += R) {
+        const float4 v = reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_at(p, s)) * HD)[c4];
+#pragma unroll
+        for (int g = 0; g < kMaxG; ++g)
+            if (g < G) {
+                const float pr = sc[g * length + s];
+                acc[g].x += pr * v.x;
+                acc[g].y += pr * v.y;
+                acc[g].z += pr * v.z;
+                acc[g].w += pr * v.w;
+            }
+    }
+    float4 *wpart = reinterpret_cast<float4 *>(qs);  // [R][G][HD / 4]: R * G * HD = 1024 G floats
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g)
+        if (g < G) wpart[(r * G + g) * cols4 + c4] = acc[g];
+    __syncthreads();
+    for (int o = t; o < G * HD; o += blockDim.x) {
+        const float *wp = reinterpret_cast<const float *>(wpart);
+        float a = 0.0f;
+        for (int k = 0; k < R; ++k) a += wp[k * G * HD + o];
+        b.att[kh * G * HD + o] = a * sigmoidf_(b.gate[kh * G * HD + o]);
     }
 }
 
@@ -437,51 +444,75 @@ __global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b, Eng
 
 // engine.cpp:1025-1039: attention residual, Hadamard MLP, mHC residual
 // routing (Sinkhorn) and lane mixing, the layer's hidden state; then the next
-// layer's rms of x when `next_rms`.
+// layer's rms of x when `next_rms`. Thread i < D owns column i of every
+// vector (loaded once at the start); only the Hadamard transforms go through
+// LDS.
 __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b, LayerDev ld, MhcDev mh, int l,
                                                                int next_rms, EngineDims d) {
     __shared__ float red[kEngThreads / 64];
     __shared__ float mlp[4096];
     __shared__ float hr[64], hpo[8];
-    const int D = d.D, N = d.N;
+    const int D = d.D, N = d.N, i = threadIdx.x;
+    const bool own = i < D;
+    // every load of the kernel, issued before the first wait
+    float proj = 0.0f, gn = 0.0f, bx = 0.0f, u = 0.0f, gh = 0.0f, d1 = 0.0f, d3 = 0.0f, x[8];
+    if (own) {
+        proj = b.proj[i];
+        gn = ld.post_norm[i];
+        bx = b.bx[i];
+        u = b.u[i];
+        gh = ld.pre_hada[i];
+        d1 = ld.d1[i];
+        d3 = ld.d3[i];
+        for (int n = 0; n < N; ++n) x[n] = b.x[n * D + i];
+    }
+    const float ag = sigmoidf_(ld.attn_gate[0]);
     if (threadIdx.x < 64) {  // residual routing: wave 0
         const int lane = threadIdx.x, ij = lane % (N * N);
         const float a = sinkhorn_wave(b.hres[ij] * mh.a_res[l] + mh.b_res[l * N * N + ij], N, lane);
         if (lane < N * N) hr[lane] = a;
         if (lane < N) hpo[lane] = b.hpost[lane];
     }
-    rms_block(b.proj, b.proj, D, ld.post_norm, red);
-    const float ag = sigmoidf_(ld.attn_gate[0]);
-    for (int i = threadIdx.x; i < D; i += blockDim.x) b.bx[i] += ag * b.proj[i];
-    __syncthreads();
-    rms_block(b.bx, b.z, D, ld.pre_hada, red);
-    for (int i = threadIdx.x; i < d.hada; i += blockDim.x) mlp[i] = i < D ? b.z[i] * ld.d1[i] : 0.0f;
+    // proj = rms(proj) * (1 + post_norm); bx += sigmoid(attn_gate) * proj
+    float r = 1.0f / sqrtf(block_sum(own ? proj * proj : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+    proj = proj * r * (1.0f + gn);
+    bx += ag * proj;
+    // z = rms(bx) * (1 + pre_hada); mlp = hadamard(silu_diag(hadamard(z * d1 | 0), d2)) (engine.cpp:1029-1033)
+    r = 1.0f / sqrtf(block_sum(own ? bx * bx : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+    const float z = bx * r * (1.0f + gh);
+    if (i < d.hada) mlp[i] = own ? z * d1 : 0.0f;  // columns past D are zero padding (D <= threads)
+    for (int k = i + blockDim.x; k < d.hada; k += blockDim.x) mlp[k] = 0.0f;
     __syncthreads();
     hadamard_block(mlp, d.hada, d.inv_hada);
-    for (int i = threadIdx.x; i < d.hada; i += blockDim.x) {
-        const float a = mlp[i] * ld.d2[i];
-        mlp[i] = a * sigmoidf_(a);
+    for (int k = threadIdx.x; k < d.hada; k += blockDim.x) {
+        const float a = mlp[k] * ld.d2[k];
+        mlp[k] = a * sigmoidf_(a);
     }
     __syncthreads();
     hadamard_block(mlp, d.hada, d.inv_hada);
-    for (int i = threadIdx.x; i < D; i += blockDim.x) b.bx[i] = b.bx[i] + ld.d3[i] * mlp[i] - b.u[i];
-    __syncthreads();
-    for (int i = threadIdx.x; i < D; i += blockDim.x) {  // column i of every lane: this thread alone
-        float nx[8];
+    // bx = bx + d3 * mlp - u; x[n] = hpost[n] bx + sum_j hres[n][j] x[j]; hidden = mean over lanes
+    float ss = 0.0f;
+    if (own) {
+        bx = bx + d3 * mlp[i] - u;
+        float nx[8], sum = 0.0f;
         for (int n = 0; n < N; ++n) {
-            float val = hpo[n] * b.bx[i];
-            for (int j = 0; j < N; ++j) val += hr[n * N + j] * b.x[j * D + i];
+            float val = hpo[n] * bx;
+            for (int j = 0; j < N; ++j) val += hr[n * N + j] * x[j];
             nx[n] = val;
         }
-        float sum = 0.0f;
         for (int n = 0; n < N; ++n) {
             b.x[n * D + i] = nx[n];
             sum += nx[n];
+            ss += nx[n] * nx[n];
+            x[n] = nx[n];
         }
         b.hidden[l * D + i] = sum / static_cast<float>(N);
     }
-    __syncthreads();
-    if (next_rms) rms_block(b.x, b.nx, N * D, nullptr, red);
+    if (next_rms) {  // the next layer's nx = rms(x) over all N * D values
+        r = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(N * D) + 1e-6f);
+        if (own)
+            for (int n = 0; n < N; ++n) b.nx[n * D + i] = x[n] * r;
+    }
 }
 
 // z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
