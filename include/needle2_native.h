@@ -59,13 +59,35 @@ void needle2_sdot_destroy(void *handle);
 /* needle2/csrc/sdot.cpp:356-359. Bit-exact with the reference's int8 arithmetic. */
 void needle2_sdot_linear(void *handle, const float *x, float *y, int batch, int threads);
 
-/* needle2/csrc/engine.cpp:1500-1548. The whole-model engine is not part of
- * this library: needle2_engine_create returns NULL and needle2_engine_error()
- * explains why (NativeEngine raises RuntimeError, needle2/native.py:405-406).
- * The remaining needle2_engine_* symbols exist so that binding them succeeds. */
+/* needle2/csrc/engine.cpp:1499-1548: the single-sequence engine, on the GPU.
+ * config is the reference's EngineConfig (engine.cpp:15-19), tensors its
+ * TensorDesc table (engine.cpp:14) with CQ entries pointing at this library's
+ * CQ handles (borrowed) and dense entries at host fp32 data (copied at
+ * creation). threads is ignored. Failures return NULL / -1 with the message
+ * in needle2_engine_error(). needle2_engine_set_sdot fails as the reference
+ * does on a host without DotProd; cache_prefix, reset_to_prefix, import and
+ * decode_loop are not implemented (-1). */
 const char *needle2_engine_error(void);
 void *needle2_engine_create(const void *config, const void *tensors, int count, int threads, int activation_bits);
 void needle2_engine_destroy(void *engine);
+void needle2_engine_set_lookup(void *engine, int mode);
+int needle2_engine_set_sdot(void *engine);
+void needle2_engine_reset(void *engine, int prefix);
+int needle2_engine_cache_prefix(void *engine);
+int needle2_engine_reset_to_prefix(void *engine);
+int needle2_engine_step(void *engine, int token, float *logits, float *hidden);
+int needle2_engine_prefill(void *engine, const int *tokens, int num_tokens, int last_only, float *logits,
+                           float *hidden);
+int needle2_engine_step_candidates(void *engine, int token, const int *candidates, int num_candidates,
+                                   float *candidate_logits, float *hidden);
+int needle2_engine_project_candidates(void *engine, const int *candidates, int num_candidates,
+                                      float *candidate_logits);
+int needle2_engine_decode_loop(void *engine, int first_token, int max_new_tokens, const void *dfa,
+                               int *output_tokens, int *out_generated_count);
+int needle2_engine_import(void *engine, int pos, int prefix, const int *ids, const int *positions, int count,
+                          const float *k, const float *v);
+int needle2_engine_set_int8_kv(void *engine, int enable);
+size_t needle2_engine_kv_storage_bytes(void *engine);
 
 /* ======================= 2. Additive gfx950 exports ===================== */
 
