@@ -661,9 +661,9 @@ def main():
         log(f"candidates: { {k: v['median'] for k, v in extra.items() if k.startswith('candidates_')} }")
 
         log("engine: NativeEngine.step, released geometry (27 layers), batch 1")
-        for kv, (tps, ms) in bench_engine().items():
+        for kv, (tps, tok_ms) in bench_engine().items():
             extra[f"engine_{kv}_kv_tokens_per_s"] = round(tps, 1)
-            extra[f"engine_{kv}_kv_token_us"] = dist_us(ms)
+            extra[f"engine_{kv}_kv_token_us"] = dist_us(tok_ms)
             log(f"engine {kv} KV: {tps:.0f} tokens/s")
 
         ms_u, nb = bench_archive_upload()
