@@ -362,6 +362,36 @@ def bench_engine(tokens=64):
     return out
 
 
+PROMPT_TOKENS = 512
+
+
+def prompt_tokens():
+    return [(i * 97 + 5) % 8192 for i in range(PROMPT_TOKENS)]
+
+
+def bench_engine_prefill(runs=8):
+    """NativeEngine.prefill of a 512-token prompt (released geometry, chunks of 32, last logits only) after
+    reset(), timed on the host around the call, after one untimed prompt. Returns {kv: (tokens/s, [ms per
+    prompt])}."""
+    from openneedle_amd.archive import Archive, synthetic_released
+    from openneedle_amd.engine import NativeEngine
+    archive = Archive(synthetic_released(seed=3, tokenizer_bytes=0))
+    tokens = prompt_tokens()
+    out = {}
+    for kv in ("fp32", "int8"):
+        e = NativeEngine(archive, kv_cache=kv)
+        e.prefill(tokens, last_only=True)
+        times = []
+        for _ in range(runs):
+            e.reset()
+            t = time.perf_counter_ns()
+            e.prefill(tokens, last_only=True)
+            times.append((time.perf_counter_ns() - t) / 1e6)
+        out[kv] = (PROMPT_TOKENS / (statistics.median(times) * 1e-3), times)
+        del e
+    return out
+
+
 def abi_calls(mats, x, runs, warmup=3):
     """Host-side milliseconds of `runs` host-pointer needle2_cq_linear calls (batch 1), cycling over `mats`."""
     for m in mats[:warmup] if len(mats) >= warmup else mats * warmup:
@@ -502,6 +532,15 @@ def cpu_baseline(budget_s=12.0, others=True):
             w[f"engine_{kv}_kv"] = {
                 "what": "the reference Engine::step (released geometry, random contents, batch 1, logits out)",
                 "tokens_per_s": round(1 / med, 1), "ms_per_token": _spread(med, p10, p90), "runs": n}
+            tokens = prompt_tokens()
+
+            def prompt():
+                eng.reset(0)
+                eng.prefill(tokens, last_only=True)
+            med, p10, p90, n = _cpu_time(prompt, 4.0, min_runs=3, warmup=1)
+            w[f"engine_prefill_{kv}_kv"] = {
+                "what": f"the reference Engine::prefill, {PROMPT_TOKENS}-token prompt (chunks of 32, last logits)",
+                "tokens_per_s": round(PROMPT_TOKENS / med, 1), "ms_per_prompt": _spread(med, p10, p90), "runs": n}
             del eng
     out["workloads"] = w
     return out
@@ -551,6 +590,8 @@ def main():
     if args.only == "engine":
         for kv, (tps, ms) in bench_engine().items():
             log(f"engine {kv} KV: {tps:.0f} tokens/s, per token {dist_us(ms)} us")
+        for kv, (tps, ms) in bench_engine_prefill().items():
+            log(f"engine prefill {kv} KV: {tps:.0f} tokens/s, per prompt {dist_us(ms)} us")
         return
     if args.only == "archive":
         ms_u, nb = bench_archive_upload()
@@ -665,6 +706,11 @@ def main():
             extra[f"engine_{kv}_kv_tokens_per_s"] = round(tps, 1)
             extra[f"engine_{kv}_kv_token_us"] = dist_us(tok_ms)
             log(f"engine {kv} KV: {tps:.0f} tokens/s")
+        log(f"engine prefill: NativeEngine.prefill, released geometry, {PROMPT_TOKENS}-token prompt")
+        for kv, (tps, pr_ms) in bench_engine_prefill().items():
+            extra[f"engine_prefill_{kv}_kv_tokens_per_s"] = round(tps, 1)
+            extra[f"engine_prefill_{kv}_kv_prompt_us"] = dist_us(pr_ms)
+            log(f"engine prefill {kv} KV: {tps:.0f} tokens/s")
 
         ms_u, nb = bench_archive_upload()
         extra["archive_upload_ms"] = round(ms_u, 2)

@@ -32,6 +32,9 @@ struct AttnArgs {
     const int *lengths;    // nullable, device
     int seqs, kvheads, head_dim, capacity, length, splits, slots_per_split;
     float scale;           // 1/sqrt(head_dim), computed on the host like the reference
+    int slots_stride;      // sequence s's list starts at slots + s * slots_stride (0: one shared list)
+    int shared_cache;      // nonzero: every sequence reads the same [kvheads][capacity] cache (the
+                           // tokens of one prompt chunk, each with its own slot list)
 };
 
 bool attn_supported(int head_dim, int group);

@@ -104,12 +104,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const uint32_t cap = static_cast<uint32_t>(a.capacity);
 
     const ND_CONST float *qh = (const ND_CONST float *)(a.q + (static_cast<size_t>(seq) * H + kh * G) * HD);
-    const size_t row0 = (static_cast<size_t>(seq) * a.kvheads + kh) * cap;
+    const size_t row0 = (static_cast<size_t>(a.shared_cache ? 0 : seq) * a.kvheads + kh) * cap;
     const auto rk = buffer_rsrc(a.k8 + row0 * HD, cap * HD);
     const auto rv = buffer_rsrc(a.v8 + row0 * HD, cap * HD);
     const auto rks = buffer_rsrc(a.ks + row0, cap * 4u);
     const auto rvs = buffer_rsrc(a.vs + row0, cap * 4u);
-    const auto rsl = buffer_rsrc(a.slots, static_cast<uint32_t>(a.length) * 4u);
+    const auto rsl = buffer_rsrc(a.slots + static_cast<size_t>(seq) * a.slots_stride, static_cast<uint32_t>(a.length) * 4u);
     const int vj = lane % LPR, vr = lane / LPR;  // value phase: word group, slot lane
 
     // slot of list position s, or -1 when not attended

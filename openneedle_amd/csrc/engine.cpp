@@ -53,16 +53,20 @@ struct Mat {
 
 // Row tiles of several CQ matrices that share one input, run as one GEMV
 // launch (matrices of one geometry) after at most one activation transform.
+// The job table holds `tokens` copies of the pieces, token-major, each over
+// its token's input row and into its token's output rows, so a launch over
+// the first n tokens runs n times the workgroups of one token.
 struct GemvGroup {
     struct Piece {
         const Matrix *m;
         int first, rows;  // rows [first, first + rows) of m
         float *y;         // receives the piece's whole row tiles, from tile first / 256
+        int ystride;      // floats between consecutive tokens' outputs
     };
     const Matrix *m0 = nullptr;
     DevBuf<uint8_t> jobs;
     DevBuf<float> rot, big;
-    int njobs = 0, blocks = 0;
+    int pieces = 0, per_token = 0;  // jobs and workgroups of one token
     const float *x = nullptr;
     CqJob job0{};
 
@@ -71,43 +75,48 @@ struct GemvGroup {
                std::memcmp(a.lut, b.lut, sizeof a.lut) == 0;
     }
 
-    void build(const std::vector<Piece> &pieces, const float *input) {
-        m0 = pieces[0].m;
+    // input: [tokens][m.in] rows
+    void build(const std::vector<Piece> &ps, const float *input, int tokens) {
+        m0 = ps[0].m;
         x = input;
         const bool fused = gemv_fuses_fwht(m0->group);
-        if (!fused) rot.reserve(m0->dev);
-        const float *act = fused ? input : rot.p;
+        if (!fused) rot.reserve(size_t(m0->dev) * tokens);
         std::vector<CqJob> host;
-        for (const Piece &p : pieces) {
-            ND_CHECK(compatible(*m0, *p.m), "internal: GEMV group of mixed geometry");
-            const int tile0 = p.first / kRowsPerBlock;
-            const int tile1 = (p.first + p.rows - 1) / kRowsPerBlock;
-            const int tiles = tile1 - tile0 + 1;
-            const int rows = std::min(tiles * kRowsPerBlock, p.m->out - tile0 * kRowsPerBlock);
-            host.push_back(CqJob{p.m->codes.p + size_t(tile0) * p.m->chunks * kRowsPerBlock,
-                                 p.m->norms.p + size_t(tile0) * p.m->groups * kRowsPerBlock, act, p.y, rows,
-                                 tiles * kRowsPerBlock, blocks, 1});
-            blocks += tiles;
-        }
-        njobs = static_cast<int>(host.size());
+        int blocks = 0;
+        for (int t = 0; t < tokens; ++t)
+            for (const Piece &p : ps) {
+                ND_CHECK(compatible(*m0, *p.m), "internal: GEMV group of mixed geometry");
+                const int tile0 = p.first / kRowsPerBlock;
+                const int tile1 = (p.first + p.rows - 1) / kRowsPerBlock;
+                const int tiles = tile1 - tile0 + 1;
+                const int rows = std::min(tiles * kRowsPerBlock, p.m->out - tile0 * kRowsPerBlock);
+                const float *act = fused ? input + size_t(t) * m0->in : rot.p + size_t(t) * m0->dev;
+                host.push_back(CqJob{p.m->codes.p + size_t(tile0) * p.m->chunks * kRowsPerBlock,
+                                     p.m->norms.p + size_t(tile0) * p.m->groups * kRowsPerBlock, act,
+                                     p.y + size_t(t) * p.ystride, rows, tiles * kRowsPerBlock, blocks, 1});
+                blocks += tiles;
+            }
+        pieces = static_cast<int>(ps.size());
+        per_token = blocks / tokens;
         job0 = host[0];
-        if (njobs > 1) {
+        if (host.size() > 1) {
             jobs.reserve(host.size() * sizeof(CqJob));
             ND_HIP(hipMemcpy(jobs.p, host.data(), host.size() * sizeof(CqJob), hipMemcpyHostToDevice));
         }
     }
 
-    void run(hipStream_t s) {
+    void run(hipStream_t s, int tokens) {
         if (!gemv_fuses_fwht(m0->group)) {
             if (gemv_prepass(m0->group))
-                launch_rot_many(x, nullptr, 1, 1, m0->in, m0->dev, m0->group, m0->scale, rot.p, s);
+                launch_rot_many(x, nullptr, tokens, tokens, m0->in, m0->dev, m0->group, m0->scale, rot.p, s);
             else
-                m0->transform(x, m0->in, rot.p, 1, big, s);
+                m0->transform(x, m0->in, rot.p, tokens, big, s);
         }
+        const int njobs = pieces * tokens;
         if (njobs > 1)
-            launch_cq_gemv(m0->geom(), CqJob{}, reinterpret_cast<const CqJob *>(jobs.p), njobs, blocks, s);
+            launch_cq_gemv(m0->geom(), CqJob{}, reinterpret_cast<const CqJob *>(jobs.p), njobs, per_token * tokens, s);
         else
-            launch_cq_gemv(m0->geom(), job0, nullptr, 0, blocks, s);
+            launch_cq_gemv(m0->geom(), job0, nullptr, 0, per_token, s);
     }
 };
 
@@ -119,33 +128,35 @@ struct Projection {
         const float *w;
         int cols, first, rows;
         float *y;
+        int ystride;
     };
     std::vector<Dense> dense;
     const float *x = nullptr;
 
-    // (matrix, first row, rows, output)
-    void add(const Mat &m, int first, int rows, float *y, std::vector<std::vector<GemvGroup::Piece>> &pending) {
+    // (matrix, first row, rows, output, floats between tokens' outputs)
+    void add(const Mat &m, int first, int rows, float *y, int ystride,
+             std::vector<std::vector<GemvGroup::Piece>> &pending) {
         if (!m.cq) {
-            dense.push_back(Dense{m.dense, m.cols, first, rows, y});
+            dense.push_back(Dense{m.dense, m.cols, first, rows, y, ystride});
             return;
         }
         for (auto &g : pending)
             if (GemvGroup::compatible(*g[0].m, *m.cq)) {
-                g.push_back({m.cq, first, rows, y});
+                g.push_back({m.cq, first, rows, y, ystride});
                 return;
             }
-        pending.push_back({{m.cq, first, rows, y}});
+        pending.push_back({{m.cq, first, rows, y, ystride}});
     }
-    void finish(std::vector<std::vector<GemvGroup::Piece>> &pending, const float *input) {
+    void finish(std::vector<std::vector<GemvGroup::Piece>> &pending, const float *input, int tokens) {
         x = input;
         for (auto &p : pending) {
             groups.push_back(std::make_unique<GemvGroup>());
-            groups.back()->build(p, input);
+            groups.back()->build(p, input, tokens);
         }
     }
-    void run(hipStream_t s) {
-        for (auto &g : groups) g->run(s);
-        for (auto &d : dense) launch_eng_dense(d.w, d.cols, d.first, d.rows, x, d.y, s);
+    void run(hipStream_t s, int tokens) {
+        for (auto &g : groups) g->run(s, tokens);
+        for (auto &d : dense) launch_eng_dense(d.w, d.cols, d.first, d.rows, x, d.y, d.ystride, tokens, s);
     }
 };
 
@@ -154,6 +165,8 @@ struct Projection {
 struct GpuEngine {
     EngineConfigC c{};
     int abits = 0, position = 0, prefix = 0, capacity = 0, engring = 1, history_cap = 1;
+    int chunk = 1;  // prompt chunk (engine.cpp:1054); the work buffers hold this many tokens
+    int ring = 0;   // KV slots past the prefix of a window model: the window plus chunk - 1
     bool int8_kv = false;
     std::vector<int> history;
     std::vector<float> rope_div;
@@ -172,6 +185,10 @@ struct GpuEngine {
     MhcDev mh{};
     DevBuf<StepParams> params;
     HostBuf<StepParams> hparams;
+    DevBuf<int64_t> ids;   // per chunk: tokens [chunk], then engram rows [sites][chunk][tables]
+    HostBuf<int64_t> hids;
+    DevBuf<int> lens;      // per chunk: attention list lengths [chunk]
+    HostBuf<int> hlens;
     DevBuf<float> logits, part, embed_z, row_scratch;
     HostBuf<float> hlogits, hhidden;
     std::vector<Projection> mhc_proj, qkvg, oproj;
@@ -192,10 +209,14 @@ struct GpuEngine {
         if (stream) (void)hipStreamDestroy(stream);
     }
     void reset(int prefix_len);
-    int cache_slot(int pos) const {
-        return !c.window ? pos : pos < prefix ? pos : prefix + (pos - prefix) % c.window;
-    }
+    // engine.cpp:500 with a ring of `ring` slots: positions inside the window
+    // keep distinct slots over a whole chunk
+    int cache_slot(int pos) const { return !c.window ? pos : pos < prefix ? pos : prefix + (pos - prefix) % ring; }
+    int max_length() const { return c.window ? c.window + prefix : capacity; }
+    void set_token(int t, int token);
+    void run(int tokens);
     void step(int token, float *logits_out, float *hidden_out);
+    void prefill(const int *tokens, int num_tokens, bool last_only, float *logits_out, float *hidden_out);
     void project_candidates(const int *candidates, int count, float *out);
     size_t kv_storage_bytes() const { return kv8.n + kv32.n * sizeof(float) + kvs.n * sizeof(float); }
 };
@@ -279,20 +300,25 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     rope_div.resize(HD / 2);
     for (int j = 0; j < HD / 2; ++j) rope_div[j] = std::pow(c.rope_theta, float(2 * j) / HD);  // engine.cpp:400
 
-    // work buffers (one allocation)
+    // work buffers (one allocation), `chunk` tokens each
+    chunk = c.window ? std::min(kEngMaxChunk, c.window) : kEngMaxChunk;
     const int mhc_tiles = 2 * kRowsPerBlock;  // a piece spans at most two row tiles
+    const int sites = std::max(1, c.num_sites);
+    dims.sites = sites;
+    dims.mhc_stride = mhc_tiles;
     size_t off = 0;
     auto take = [&](size_t n) {
         const size_t at = off;
-        off += (n + 63) / 64 * 64;
+        off += (n * chunk + 63) / 64 * 64;
         return at;
     };
     const size_t ox = take(N * D), onx = take(N * D), ou = take(D), obx = take(D), oz = take(D), oq = take(A),
                  ok = take(K), ov = take(K), og = take(A), oa = take(A), op = take(D), oh = take(size_t(c.layers) * D),
                  ohp = take(N), ohq = take(N), ohr = take(N * N), om0 = take(mhc_tiles), om1 = take(mhc_tiles),
-                 om2 = take(mhc_tiles), oe = take(D), oek = take(size_t(std::max(1, c.num_sites)) * D),
-                 oev = take(size_t(std::max(1, c.num_sites)) * D), orv = take(D),
-                 oring = take(size_t(std::max(1, c.num_sites)) * engring * D), ozf = take(D);
+                 om2 = take(mhc_tiles), oe = take(D), oek = take(size_t(sites) * D), oev = take(size_t(sites) * D),
+                 orv = take(D), ozf = take(D);
+    const size_t oring = off;  // shared by the chunk
+    off += (size_t(sites) * engring * D + 63) / 64 * 64;
     work.reserve(off);
     ND_HIP(hipMemset(work.p, 0, off * sizeof(float)));
     float *w = work.p;
@@ -320,11 +346,16 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     b.rawv = w + orv;
     b.engring = w + oring;
     b.zf = w + ozf;
-    params.reserve(1);
-    hparams.reserve(1);
-    std::memset(hparams.p, 0, sizeof(StepParams));
-    logits.reserve(c.vocab);
-    embed_z.reserve(D);
+    params.reserve(chunk);
+    hparams.reserve(chunk);
+    std::memset(hparams.p, 0, chunk * sizeof(StepParams));
+    ids.reserve(size_t(chunk) * (1 + size_t(sites) * std::max(1, c.tables)));
+    hids.reserve(ids.n);
+    std::memset(hids.p, 0, ids.n * sizeof(int64_t));
+    lens.reserve(chunk);
+    hlens.reserve(chunk);
+    logits.reserve(size_t(chunk) * c.vocab);
+    embed_z.reserve(size_t(chunk) * D);
 
     // layers
     const int mhi = mh0();
@@ -353,16 +384,16 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
         L.d3 = vec(t0 + 13);
         {
             std::vector<std::vector<GemvGroup::Piece>> pend;
-            qkvg[l].add(mat(t0 + 1, A, D), 0, A, b.q, pend);
-            qkvg[l].add(mat(t0 + 2, K, D), 0, K, b.k, pend);
-            qkvg[l].add(mat(t0 + 3, K, D), 0, K, b.v, pend);
-            qkvg[l].add(mat(t0 + 6, A, D), 0, A, b.gate, pend);
-            qkvg[l].finish(pend, b.z);
+            qkvg[l].add(mat(t0 + 1, A, D), 0, A, b.q, A, pend);
+            qkvg[l].add(mat(t0 + 2, K, D), 0, K, b.k, K, pend);
+            qkvg[l].add(mat(t0 + 3, K, D), 0, K, b.v, K, pend);
+            qkvg[l].add(mat(t0 + 6, A, D), 0, A, b.gate, A, pend);
+            qkvg[l].finish(pend, b.z, chunk);
         }
         {
             std::vector<std::vector<GemvGroup::Piece>> pend;
-            oproj[l].add(mat(t0 + 7, D, A), 0, D, b.proj, pend);
-            oproj[l].finish(pend, b.att);
+            oproj[l].add(mat(t0 + 7, D, A), 0, D, b.proj, D, pend);
+            oproj[l].finish(pend, b.att, chunk);
         }
         {
             const int rows[3] = {N, N, N * N};
@@ -372,14 +403,14 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
                 const int first = l * rows[m];
                 if (M.cq) {  // the GEMV's row tiles; dense rows go through one multi-matrix launch
                     mhc_row[l][m] = first - first / kRowsPerBlock * kRowsPerBlock;
-                    mhc_proj[l].add(M, first, rows[m], b.mhc_out[m], pend);
+                    mhc_proj[l].add(M, first, rows[m], b.mhc_out[m], mhc_tiles, pend);
                 } else {
                     mhc_row[l][m] = 0;
                 }
                 phi[m] = M.cq ? nullptr : M.dense;
                 mhc_rows[m] = rows[m];
             }
-            mhc_proj[l].finish(pend, b.nx);
+            mhc_proj[l].finish(pend, b.nx, chunk);
         }
     }
     for (int s = 0; s < c.num_sites; ++s) {
@@ -390,18 +421,18 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
         (void)vec(e0 + 3);
         engram_kv.emplace_back();
         std::vector<std::vector<GemvGroup::Piece>> pend;
-        engram_kv.back().add(mat(e0 + 1, D, D), 0, D, b.ek + s * D, pend);
-        engram_kv.back().add(mat(e0 + 2, D, D), 0, D, b.rawv, pend);
-        engram_kv.back().finish(pend, b.e);
-        if (mats[e0].cq) row_scratch.reserve(size_t(c.tables) * mats[e0].cq->padded);
+        engram_kv.back().add(mat(e0 + 1, D, D), 0, D, b.ek + s * D, sites * D, pend);
+        engram_kv.back().add(mat(e0 + 2, D, D), 0, D, b.rawv, D, pend);
+        engram_kv.back().finish(pend, b.e, chunk);
+        if (mats[e0].cq) row_scratch.reserve(size_t(chunk) * c.tables * mats[e0].cq->padded);
     }
     (void)vec(final_norm());
     {
         std::vector<std::vector<GemvGroup::Piece>> pend;
-        lm_head.add(mat(0, c.vocab, D), 0, c.vocab, logits.p, pend);
-        lm_head.finish(pend, b.zf);
+        lm_head.add(mat(0, c.vocab, D), 0, c.vocab, logits.p, c.vocab, pend);
+        lm_head.finish(pend, b.zf, chunk);
     }
-    if (mats[0].cq) row_scratch.reserve(std::max(row_scratch.n, size_t(mats[0].cq->padded)));
+    if (mats[0].cq) row_scratch.reserve(std::max(row_scratch.n, size_t(chunk) * mats[0].cq->padded));
     reset(0);
 }
 
@@ -410,13 +441,16 @@ void GpuEngine::reset(int prefix_len) {
     position = 0;
     prefix = prefix_len;
     std::fill(history.begin(), history.end(), 0);
-    capacity = c.window ? c.window + prefix : c.max_seq;  // engine.cpp:433-449
+    // engine.cpp:433-449, with chunk - 1 more ring slots for a window model
+    ring = c.window ? c.window + chunk - 1 : 0;
+    capacity = c.window ? ring + prefix : c.max_seq;
     dims.capacity = capacity;
     const int G = c.heads / c.kvheads;
     if (int8_kv)
         ND_CHECK(attn_supported(c.head_dim, G), "int8 KV attention: head_dim 32/64/128 with 1, 2, 4 or 8 heads per kv head");
     else
-        ND_CHECK(size_t(G) * capacity * sizeof(float) <= 49152, "fp32 KV attention: heads per kv head x context too large");
+        ND_CHECK(size_t(G) * max_length() * sizeof(float) <= 49152,
+                 "fp32 KV attention: heads per kv head x context too large");
     const size_t per_layer = size_t(c.kvheads) * capacity * c.head_dim;
     const size_t scales = size_t(c.kvheads) * capacity;
     kv.assign(c.layers, KvLayer{});
@@ -439,28 +473,30 @@ void GpuEngine::reset(int prefix_len) {
             kv[l].v32 = kv[l].k32 + per_layer;
         }
     }
-    slots.reserve(capacity);
+    slots.reserve(size_t(chunk) * capacity);
     b.slots = slots.p;
     if (c.num_sites) ND_HIP(hipMemsetAsync(b.engring, 0, size_t(c.num_sites) * engring * c.dim * sizeof(float), stream));
     ND_HIP(hipStreamSynchronize(stream));
 }
 
-void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
-    const int D = c.dim, HD = c.head_dim;
-    if (token < 0 || token >= c.vocab) throw Error("token outside vocabulary");
-    if (!c.window && position >= capacity) throw Error("maximum context reached");
-    history[position % history_cap] = token;
-    StepParams &p = *hparams.p;
-    p.token = token;
-    p.position = position;
-    p.slot = cache_slot(position);
+// Token t of the next launch: its StepParams and row ids (engine.cpp:
+// 755-781, 898-911, 968-975; the token history advances here, in order).
+void GpuEngine::set_token(int t, int token) {
+    const int HD = c.head_dim, pos = position + t;
+    history[pos % history_cap] = token;
+    StepParams &p = hparams.p[t];
+    hids.p[t] = token;
+    p.position = pos;
+    p.slot = cache_slot(pos);
     p.prefix = prefix;
     p.window = c.window;
-    p.prefix_count = c.window ? std::min(prefix, position + 1) : 0;  // engine.cpp:900-902
-    p.start = c.window ? std::max(prefix, position - c.window + 1) : 0;
-    p.length = p.prefix_count + std::max(0, position - p.start + 1);
+    p.ring = ring;
+    p.chunk_start = position;
+    p.prefix_count = c.window ? std::min(prefix, pos + 1) : 0;  // engine.cpp:900-902
+    p.start = c.window ? std::max(prefix, pos - c.window + 1) : 0;
+    p.length = p.prefix_count + std::max(0, pos - p.start + 1);
     for (int j = 0; j < HD / 2; ++j) {
-        const float a = position / rope_div[j];
+        const float a = pos / rope_div[j];
         p.rope_cos[j] = std::cos(a);
         p.rope_sin[j] = std::sin(a);
     }
@@ -468,70 +504,89 @@ void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
         const int heads = c.tables / c.num_orders;
         auto hist = [&](int q) { return history[((q % history_cap) + history_cap) % history_cap]; };
         for (int s = 0; s < c.num_sites; ++s) {
+            int64_t *rows = hids.p + chunk + (size_t(s) * chunk + t) * c.tables;
             p.engram_zero[s] = 0;
             for (int table = 0; table < c.tables; ++table) {
                 const int order = c.orders[table / heads];
-                p.engram_rows[s][table] = 0;
-                if (position + 1 < order || (c.window && order - 1 >= c.window && position - order + 1 >= prefix)) {
+                rows[table] = 0;
+                if (pos + 1 < order || (c.window && order - 1 >= c.window && pos - order + 1 >= prefix)) {
                     p.engram_zero[s] |= 1 << table;
                     continue;
                 }
                 uint32_t acc = uint32_t(0x9e3779b9) * uint32_t(table + 1);
-                for (int j = 0; j < order; ++j) acc = (acc ^ uint32_t(hist(position - j))) * uint32_t(0x01000193);
+                for (int j = 0; j < order; ++j) acc = (acc ^ uint32_t(hist(pos - j))) * uint32_t(0x01000193);
                 acc ^= acc >> 15;
-                p.engram_rows[s][table] = int64_t(table) * c.slots + acc % uint32_t(c.slots);
+                rows[table] = int64_t(table) * c.slots + acc % uint32_t(c.slots);
             }
         }
-        p.ring_row = position % engring;
         for (int tap = 0; tap < c.taps; ++tap) {
-            const int past = position - tap * c.dilation;
+            const int past = pos - tap * c.dilation;
             const bool live = past >= 0 && (!c.window || tap * c.dilation < c.window || past < prefix);
-            p.tap_rows[tap] = live ? past % engring : -1;
+            p.tap_pos[tap] = live ? past : -1;
         }
     }
-    hipStream_t s = stream;
-    ND_HIP(hipMemcpyAsync(params.p, hparams.p, sizeof(StepParams), hipMemcpyHostToDevice, s));
-    StepParams *dp = params.p;
+}
 
-    // embedding row, lanes (engine.cpp:972-974)
+// The layers for the `tokens` tokens set by set_token (engine.cpp:968-1040 for
+// one token, 1056-1258 for a chunk), leaving each token's final normed hidden
+// state in zf. Tokens share nothing but the KV cache and the engram ring, which
+// every token of the chunk writes before any reads them.
+void GpuEngine::run(int tokens) {
+    const int D = c.dim, HD = c.head_dim, T = tokens;
+    hipStream_t s = stream;
+    ND_HIP(hipMemcpyAsync(params.p, hparams.p, size_t(T) * sizeof(StepParams), hipMemcpyHostToDevice, s));
+    ND_HIP(hipMemcpyAsync(ids.p, hids.p, ids.n * sizeof(int64_t), hipMemcpyHostToDevice, s));
+    const StepParams *dp = params.p;
+
+    // embedding rows, lanes (engine.cpp:972-974)
     const Mat &emb = mats[0];
     if (emb.cq)
-        launch_cq_rows(emb.cq->geom(), emb.cq->codes.p, emb.cq->norms.p, &dp->token, 1, D, emb.cq->padded,
+        launch_cq_rows(emb.cq->geom(), emb.cq->codes.p, emb.cq->norms.p, ids.p, T, D, emb.cq->padded,
                        row_scratch.p, embed_z.p, s);
     else
-        launch_eng_dense_rows(emb.dense, D, &dp->token, 1, embed_z.p, s);
-    launch_eng_start(embed_z.p, b, dims, s);
+        launch_eng_dense_rows(emb.dense, D, ids.p, T, embed_z.p, s);
+    launch_eng_start(embed_z.p, b, dims, T, s);
 
     for (int site = 0; site < c.num_sites; ++site) {
         const int e0 = engram_base() + 4 * site;
         const Mat &tab = mats[e0];
+        const int64_t *rows = ids.p + chunk + size_t(site) * chunk * c.tables;
         if (tab.cq)
-            launch_cq_rows(tab.cq->geom(), tab.cq->codes.p, tab.cq->norms.p, &dp->engram_rows[site][0], c.tables,
-                           c.subdim, tab.cq->padded, row_scratch.p, b.e, s);
+            launch_cq_rows(tab.cq->geom(), tab.cq->codes.p, tab.cq->norms.p, rows, T * c.tables, c.subdim,
+                           tab.cq->padded, row_scratch.p, b.e, s);
         else
-            launch_eng_dense_rows(tab.dense, c.subdim, &dp->engram_rows[site][0], c.tables, b.e, s);
-        launch_eng_engram_in(b, dp, site, dims, s);
-        engram_kv[site].run(s);
-        launch_eng_engram_out(b, dptr[e0 + 3], dp, site, dims, s);
+            launch_eng_dense_rows(tab.dense, c.subdim, rows, T * c.tables, b.e, s);
+        launch_eng_engram_in(b, dp, site, dims, T, s);
+        engram_kv[site].run(s, T);
+        launch_eng_engram_out(b, dptr[e0 + 3], dp, site, dims, T, s);
     }
 
     const int G = c.heads / c.kvheads;
+    int maxlen = 0;
+    for (int t = 0; t < T; ++t) maxlen = std::max(maxlen, hparams.p[t].length);
+    if (int8_kv && T > 1) {
+        for (int t = 0; t < T; ++t) hlens.p[t] = hparams.p[t].length;
+        ND_HIP(hipMemcpyAsync(lens.p, hlens.p, size_t(T) * sizeof(int), hipMemcpyHostToDevice, s));
+    }
     for (int l = 0; l < c.layers; ++l) {
-        mhc_proj[l].run(s);
+        mhc_proj[l].run(s, T);
         {
             const int first[3] = {l * mhc_rows[0], l * mhc_rows[1], l * mhc_rows[2]};
-            launch_eng_dense3(phi, first, mhc_rows, b.mhc_out, c.lanes * c.dim, b.nx, s);
+            launch_eng_dense3(phi, first, mhc_rows, b.mhc_out, dims.mhc_stride, c.lanes * c.dim, b.nx, T, s);
         }
         int sites[kEngMaxSites], ns = 0;
         for (int k = 0; k < c.num_sites; ++k)
             if (c.sites[k] == l) sites[ns++] = k;
-        launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, s);
-        qkvg[l].run(s);
+        launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, T, s);
+        qkvg[l].run(s, T);
         if (!int8_kv) {
-            launch_eng_attn_fused(b, layer[l], kv[l], dp, p.length, dims, s);
-            launch_eng_quantize(b.att, c.heads * HD, abits, s);
+            // one token: norms, RoPE, store and attention in one kernel; a chunk
+            // stores every token's K / V before any token attends
+            if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
+            launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, s);
+            launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
         } else {
-            launch_eng_qk(b, layer[l], kv[l], dp, dims, s);
+            launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
             AttnArgs a{};
             a.k8 = kv[l].k8;
             a.v8 = kv[l].v8;
@@ -540,30 +595,46 @@ void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
             a.q = b.q;
             a.out = b.att;
             a.slots = b.slots;
-            a.lengths = nullptr;
-            a.seqs = 1;
+            a.seqs = T;
             a.kvheads = c.kvheads;
             a.head_dim = HD;
             a.capacity = capacity;
-            a.length = p.length;
-            const int tiles = (p.length + 255) / 256;
-            a.splits = std::max(1, std::min(tiles, 64 / c.kvheads));
-            const int per = (tiles + a.splits - 1) / a.splits * 256;
-            a.splits = std::max(1, (p.length + per - 1) / per);
-            a.slots_per_split = per;
-            if (a.splits > 1) part.reserve(size_t(c.heads) * a.splits * (HD + 2));
-            a.part = part.p;
+            a.length = maxlen;
             a.scale = dims.scale;
+            const int tiles = (maxlen + 255) / 256;
+            if (T == 1) {  // one token: split its slots over up to 64 blocks
+                a.splits = std::max(1, std::min(tiles, 64 / c.kvheads));
+                const int per = (tiles + a.splits - 1) / a.splits * 256;
+                a.splits = std::max(1, (maxlen + per - 1) / per);
+                a.slots_per_split = per;
+                if (a.splits > 1) part.reserve(size_t(c.heads) * a.splits * (HD + 2));
+                a.part = part.p;
+            } else {  // a chunk: one block per (token, kv head), every token's own list into the shared cache
+                a.splits = 1;
+                a.slots_per_split = tiles * 256;
+                a.lengths = lens.p;
+                a.slots_stride = capacity;
+                a.shared_cache = 1;
+            }
             launch_attention(a, G, s);
-            launch_eng_gate(b, dims, s);
+            launch_eng_gate(b, dims, T, s);
         }
-        oproj[l].run(s);
-        launch_eng_post(b, layer[l], mh, l, l + 1 < c.layers, dims, s);
+        oproj[l].run(s, T);
+        launch_eng_post(b, layer[l], mh, l, l + 1 < c.layers, dims, T, s);
     }
-    launch_eng_final(b, dptr[final_norm()], dims, s);
+    launch_eng_final(b, dptr[final_norm()], dims, T, s);
+}
+
+void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
+    const int D = c.dim;
+    if (token < 0 || token >= c.vocab) throw Error("token outside vocabulary");
+    if (!c.window && position >= capacity) throw Error("maximum context reached");
+    set_token(0, token);
+    run(1);
+    hipStream_t s = stream;
     if (logits_out) {
-        launch_eng_quantize(b.zf, D, abits, s);
-        lm_head.run(s);
+        launch_eng_quantize(b.zf, D, D, abits, 1, s);
+        lm_head.run(s, 1);
         hlogits.reserve(c.vocab);
         ND_HIP(hipMemcpyAsync(hlogits.p, logits.p, size_t(c.vocab) * sizeof(float), hipMemcpyDeviceToHost, s));
     }
@@ -577,6 +648,57 @@ void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
     ++position;
 }
 
+// engine.cpp:1045-1301: the prompt in chunks of `chunk` tokens, every token's
+// layers in the same launches; logits of every token, or of the last one only,
+// and the last token's per-layer hidden states.
+void GpuEngine::prefill(const int *tokens, int num_tokens, bool last_only, float *logits_out, float *hidden_out) {
+    if (num_tokens <= 0) return;
+    for (int i = 0; i < num_tokens; ++i)
+        if (tokens[i] < 0 || tokens[i] >= c.vocab) throw Error("token outside vocabulary");
+    if (!c.window && position + num_tokens > capacity) throw Error("maximum context reached");
+    const int D = c.dim, V = c.vocab;
+    hipStream_t s = stream;
+    for (int c0 = 0; c0 < num_tokens; c0 += chunk) {
+        const int T = std::min(chunk, num_tokens - c0);
+        const bool final_chunk = c0 + T == num_tokens;
+        for (int t = 0; t < T; ++t) set_token(t, tokens[c0 + t]);
+        run(T);
+        float *dst = nullptr;
+        int rows = 0;
+        if (logits_out && !last_only) {
+            launch_eng_quantize(b.zf, D, D, abits, T, s);
+            lm_head.run(s, T);
+            dst = logits_out + size_t(c0) * V;
+            rows = T;
+        } else if (logits_out && final_chunk) {  // the last token only, through token 0's LM-head jobs
+            if (T > 1)
+                ND_HIP(hipMemcpyAsync(b.zf, b.zf + size_t(T - 1) * D, size_t(D) * sizeof(float),
+                                      hipMemcpyDeviceToDevice, s));
+            launch_eng_quantize(b.zf, D, D, abits, 1, s);
+            lm_head.run(s, 1);
+            dst = logits_out;
+            rows = 1;
+        }
+        if (dst) {
+            hlogits.reserve(size_t(chunk) * V);
+            ND_HIP(hipMemcpyAsync(hlogits.p, logits.p, size_t(rows) * V * sizeof(float), hipMemcpyDeviceToHost, s));
+        }
+        if (final_chunk && hidden_out) {
+            hhidden.reserve(size_t(c.layers) * D);
+            ND_HIP(hipMemcpyAsync(hhidden.p, b.hidden + size_t(T - 1) * c.layers * D,
+                                  size_t(c.layers) * D * sizeof(float), hipMemcpyDeviceToHost, s));
+        }
+        // the reference leaves the last token's embedding row in z (engine.cpp:1074-1075),
+        // which project_candidates reads next
+        ND_HIP(hipMemcpyAsync(b.zf, embed_z.p + size_t(T - 1) * D, size_t(D) * sizeof(float),
+                              hipMemcpyDeviceToDevice, s));
+        ND_HIP(hipStreamSynchronize(s));
+        if (dst) std::memcpy(dst, hlogits.p, size_t(rows) * V * sizeof(float));
+        if (final_chunk && hidden_out) std::memcpy(hidden_out, hhidden.p, size_t(c.layers) * D * sizeof(float));
+        position += T;
+    }
+}
+
 // engine.cpp:1302-1349: the final hidden state of the last step, quantised,
 // through the LM head's candidate rows.
 void GpuEngine::project_candidates(const int *candidates, int count, float *out) {
@@ -585,7 +707,7 @@ void GpuEngine::project_candidates(const int *candidates, int count, float *out)
         ND_CHECK(candidates[i] >= 0 && candidates[i] < c.vocab, "candidate outside vocabulary");
     if (!out) return;
     hipStream_t s = stream;
-    launch_eng_quantize(b.zf, c.dim, abits, s);
+    launch_eng_quantize(b.zf, c.dim, c.dim, abits, 1, s);
     st.hids.reserve(count);
     st.ids.reserve(count);
     st.y.reserve(count);
@@ -596,13 +718,13 @@ void GpuEngine::project_candidates(const int *candidates, int count, float *out)
     if (head.cq) {
         const Candidates cand = gather_candidates(*head.cq, st, st.ids.p, count, s);
         if (cand.full) {
-            lm_head.run(s);
+            lm_head.run(s, 1);
             launch_gather_outputs(logits.p, c.vocab, st.ids.p, count, 1, st.y.p, s);
         } else {
             matrix_gemv(*head.cq, st, cand.codes, cand.norms, count, cand.n_pad, b.zf, st.y.p, 1, s);
         }
     } else {
-        lm_head.run(s);
+        lm_head.run(s, 1);
         launch_gather_outputs(logits.p, c.vocab, st.ids.p, count, 1, st.y.p, s);
     }
     ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, s));
@@ -670,20 +792,9 @@ int needle2_engine_step(void *p, int token, float *logits, float *hidden) {
     }
 }
 
-// engine.cpp:1045-1301 computes a prompt in chunks with the same per-token
-// arithmetic; here the tokens run as consecutive steps.
 int needle2_engine_prefill(void *p, const int *tokens, int num_tokens, int last_only, float *logits, float *hidden) {
     try {
-        auto *e = static_cast<GpuEngine *>(p);
-        if (num_tokens <= 0) return 0;
-        for (int i = 0; i < num_tokens; ++i)
-            if (tokens[i] < 0 || tokens[i] >= e->c.vocab) throw Error("token outside vocabulary");
-        if (!e->c.window && e->position + num_tokens > e->capacity) throw Error("maximum context reached");
-        for (int i = 0; i < num_tokens; ++i) {
-            float *out = nullptr;
-            if (logits) out = last_only ? (i + 1 == num_tokens ? logits : nullptr) : logits + size_t(i) * e->c.vocab;
-            e->step(tokens[i], out, i + 1 == num_tokens ? hidden : nullptr);
-        }
+        static_cast<GpuEngine *>(p)->prefill(tokens, num_tokens, last_only != 0, logits, hidden);
         return 0;
     } catch (const std::exception &e) {
         engine_error = e.what();

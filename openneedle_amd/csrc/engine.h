@@ -12,22 +12,28 @@ constexpr int kEngMaxSites = 4;
 constexpr int kEngMaxTaps = 16;
 constexpr int kEngThreads = 1024;  // every glue kernel is one workgroup of this size
 
-// Values of one step that depend only on the position, the token history and
-// the cache geometry; the host computes them (with the reference's own
-// integer hashing and std::cos / std::sin) and uploads them once per step.
+// Values of one token that depend only on its position, the token history
+// and the cache geometry; the host computes them (with the reference's own
+// integer hashing and std::cos / std::sin) and uploads them once per step or
+// prompt chunk, one record per token.
 struct StepParams {
-    int64_t token;                                     // embedding row
     int position, slot;                                // this token's cache slot (engine.cpp:500)
     int length, prefix_count, start, prefix, window;   // attention slot list (engine.cpp:898-911)
-    int ring_row;                                      // engram ring row of this position
+    int ring;                                          // KV slots past the prefix (window models)
+    int chunk_start;                                   // first position of this token's chunk
     int engram_zero[kEngMaxSites];                     // bit t: table t of site s reads zeros
-    int tap_rows[kEngMaxTaps];                         // ring row read by each conv tap, -1: skipped
-    int64_t engram_rows[kEngMaxSites][kEngMaxTables];  // table row per (site, table)
+    int tap_pos[kEngMaxTaps];                          // position read by each conv tap, -1: skipped
     float rope_cos[kEngMaxHalfHd], rope_sin[kEngMaxHalfHd];
 };
 
+// Work buffers hold kEngMaxChunk tokens: token t of a launch is blockIdx.y
+// and its vectors sit t per-token sizes past the token-0 pointers below.
+constexpr int kEngMaxChunk = 32;  // prompt chunk (engine.cpp:1054)
+
 struct EngineDims {
     int D, N, H, KV, HD, A, K, hada, layers, tables, subdim, taps, capacity, engring, abits;
+    int sites;       // engram sites (per-token stride of ek / ev: sites * D)
+    int mhc_stride;  // per-token stride of each mhc_out buffer
     float sqrt_d;    // std::sqrt(float(D)) (engine.cpp:974, 987)
     float inv_hada;  // 1 / std::sqrt(float(hada)), the Hadamard normalisation
     float scale;     // 1 / std::sqrt(float(head_dim)) (engine.cpp:914)
@@ -44,13 +50,16 @@ struct MhcDev {
     const float *a_pre, *a_post, *a_res, *b_pre, *b_post, *b_res;
 };
 
-// Work buffers of one step (device).
+// Work buffers (device), token 0's vectors; token t's are t per-token sizes
+// further (EngineDims): x, nx N*D; u, bx, z, proj, e, rawv, zf D; q, gate,
+// att A; k, v K; hidden layers*D; hpre, hpost N; hres N*N; mhc_out
+// mhc_stride; ek, ev sites*D; slots capacity. The engram ring is shared.
 struct EngineBufs {
     float *x, *nx, *u, *bx, *z, *q, *k, *v, *gate, *att, *proj, *hidden;
     float *hpre, *hpost, *hres;     // mixed gates (N, N, N*N)
     float *mhc_out[3];              // raw mHC projections of the layer (pre, post, res rows)
     float *e, *ek, *ev, *rawv;      // engram rows [D], keys [sites][D], values [sites][D], raw values [D]
-    float *engring;                 // [sites][engring][D]
+    float *engring;                 // [sites][engring][D], row = position % engring
     float *zf;                      // final hidden, input of the LM head
     int *slots;                     // attention slot list
 };
@@ -63,29 +72,39 @@ struct KvLayer {
     float *ks, *vs;
 };
 
-void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, hipStream_t s);
-void launch_eng_engram_in(const EngineBufs &b, const StepParams *p, int site, const EngineDims &d, hipStream_t s);
+// Every launcher runs `tokens` tokens (blockIdx.y), with p the device array of their StepParams.
+void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s);
+void launch_eng_engram_in(const EngineBufs &b, const StepParams *p, int site, const EngineDims &d, int tokens,
+                          hipStream_t s);
+// the dilated conv of every token (in-chunk taps read the chunk's raw values),
+// then the ring rows of the chunk's last positions
 void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepParams *p, int site,
-                           const EngineDims &d, hipStream_t s);
+                           const EngineDims &d, int tokens, hipStream_t s);
 // mixing, engram gates and the attention input of layer l; mhc_row[m] is the
 // first row of the layer inside b.mhc_out[m]; sites: engram sites at this layer
 void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
-                    const int *sites, int nsites, const EngineDims &d, hipStream_t s);
+                    const int *sites, int nsites, const EngineDims &d, int tokens, hipStream_t s);
+// q / k norms, RoPE, the K / V store and (int8 KV) the slot lists of every token
 void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
-                   const EngineDims &d, hipStream_t s);
-// fp32 KV: norms + RoPE + KV store + attention + output gate of every kv head, one launch
+                   const EngineDims &d, int tokens, hipStream_t s);
+// fp32 KV attention + output gate of every kv head; with `prepared` false (one
+// token) it also does that token's norms, RoPE and KV store, else eng_qk did
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
-                           int length, const EngineDims &d, hipStream_t s);
-void launch_eng_gate(const EngineBufs &b, const EngineDims &d, hipStream_t s);
+                           int max_length, bool prepared, const EngineDims &d, int tokens, hipStream_t s);
+void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s);
 void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
-                     const EngineDims &d, hipStream_t s);
-void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, hipStream_t s);
-void launch_eng_quantize(float *x, int n, int bits, hipStream_t s);
-// y[r] = dot(W[first + r], x) over cols for r < rows (dense fp32 matrices)
-void launch_eng_dense(const float *w, int cols, int first, int rows, const float *x, float *y, hipStream_t s);
-// y[m][r] = dot(W_m[first[m] + r], x) for r < rows[m], m < 3 (a null W_m is skipped), one launch
-void launch_eng_dense3(const float *const *w, const int *first, const int *rows, float *const *y, int cols,
-                       const float *x, hipStream_t s);
+                     const EngineDims &d, int tokens, hipStream_t s);
+void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, int tokens, hipStream_t s);
+// x[t][0..n) for t < tokens, rows `stride` apart
+void launch_eng_quantize(float *x, int n, int stride, int bits, int tokens, hipStream_t s);
+// y[t][r] = dot(W[first + r], x[t]) over cols for r < rows (dense fp32 matrices); x rows cols
+// apart, y rows ystride apart
+void launch_eng_dense(const float *w, int cols, int first, int rows, const float *x, float *y, int ystride,
+                      int tokens, hipStream_t s);
+// y[m][t][r] = dot(W_m[first[m] + r], x[t]) for r < rows[m], m < 3 (a null W_m is skipped), one
+// launch; y rows ystride apart
+void launch_eng_dense3(const float *const *w, const int *first, const int *rows, float *const *y, int ystride,
+                       int cols, const float *x, int tokens, hipStream_t s);
 // y[i][:] = W[ids[i]][:] (dense row copy)
 void launch_eng_dense_rows(const float *w, int cols, const int64_t *ids, int count, float *y, hipStream_t s);
 

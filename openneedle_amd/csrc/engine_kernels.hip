@@ -1,9 +1,11 @@
-// Glue kernels of the single-sequence decode engine (needle2/csrc/engine.cpp:
-// 968-1044 and the helpers it calls). Every kernel is one workgroup of
-// kEngThreads threads working on the model's small vectors (d_model, the mHC
-// lanes, one token's heads), in the reference's formulas and operation order
-// per element; block-wide sums and maxima are tree reductions, so results
-// agree with the reference to fp32 rounding rather than bit for bit.
+// Glue kernels of the single-sequence engine (needle2/csrc/engine.cpp:968-1044
+// for one token, 1045-1301 for a prompt chunk, and the helpers they call).
+// Every kernel runs one workgroup of kEngThreads threads per token
+// (blockIdx.y) over the model's small vectors (d_model, the mHC lanes, one
+// token's heads), in the reference's formulas and operation order per
+// element; block-wide sums and maxima are tree reductions, so results agree
+// with the reference to fp32 rounding rather than bit for bit. A token's
+// arithmetic does not depend on how many tokens share the launch.
 //   rms(x, gain)        y = x * (1 / sqrt(sum(x^2) / n + 1e-6)) * (1 + gain)   (engine.cpp:181-184)
 //   activation_quant    x = clamp(rint(x / (a / m)), -m-1, m) * (a / m), a = max|x|, m = 2^(bits-1)-1
 //   sigmoid(x)          1 / (1 + exp(-x))
@@ -12,6 +14,7 @@
 #include "engine.h"
 #include "wave.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace nd {
@@ -19,6 +22,34 @@ namespace nd {
 namespace {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Token t's vectors (EngineBufs documents the per-token sizes).
+__device__ __forceinline__ EngineBufs at_token(EngineBufs b, const EngineDims &d, int t) {
+    const size_t nd = static_cast<size_t>(d.N) * d.D;
+    b.x += t * nd;
+    b.nx += t * nd;
+    b.u += t * d.D;
+    b.bx += t * d.D;
+    b.z += t * d.D;
+    b.proj += t * d.D;
+    b.e += t * d.D;
+    b.rawv += t * d.D;
+    b.zf += t * d.D;
+    b.q += t * d.A;
+    b.gate += t * d.A;
+    b.att += t * d.A;
+    b.k += t * d.K;
+    b.v += t * d.K;
+    b.hidden += static_cast<size_t>(t) * d.layers * d.D;
+    b.hpre += t * d.N;
+    b.hpost += t * d.N;
+    b.hres += t * d.N * d.N;
+    for (int m = 0; m < 3; ++m) b.mhc_out[m] += t * d.mhc_stride;
+    b.ek += t * d.sites * d.D;
+    b.ev += t * d.sites * d.D;
+    b.slots += static_cast<size_t>(t) * d.capacity;
+    return b;
+}
 
 // Block-wide sum / max of one value per thread (every thread gets the result).
 __device__ float block_sum(float v, float *red) {
@@ -179,18 +210,22 @@ __device__ float sinkhorn_wave(float a, int n, int lane) {
 }
 
 // x[n][d] = z[d] * sqrt(D) for every lane (engine.cpp:973-974), then nx = rms(x).
-__global__ __launch_bounds__(kEngThreads) void eng_start_kernel(const float *__restrict__ z, EngineBufs b,
+__global__ __launch_bounds__(kEngThreads) void eng_start_kernel(const float *__restrict__ z, EngineBufs b0,
                                                                 EngineDims d) {
     __shared__ float red[kEngThreads / 64];
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
+    z += static_cast<size_t>(blockIdx.y) * d.D;
     for (int i = threadIdx.x; i < d.N * d.D; i += blockDim.x) b.x[i] = z[i % d.D] * d.sqrt_d;
     __syncthreads();
     rms_block(b.x, b.nx, d.N * d.D, nullptr, red);
 }
 
 // Tables the step does not read become zeros; then the activation quantiser (engine.cpp:760-768).
-__global__ __launch_bounds__(kEngThreads) void eng_engram_in_kernel(EngineBufs b, const StepParams *__restrict__ p,
+__global__ __launch_bounds__(kEngThreads) void eng_engram_in_kernel(EngineBufs b0, const StepParams *__restrict__ p,
                                                                     int site, EngineDims d) {
     __shared__ float red[kEngThreads / 64];
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
+    p += blockIdx.y;
     const int zero = p->engram_zero[site];
     for (int i = threadIdx.x; i < d.D; i += blockDim.x)
         if ((zero >> (i / d.subdim)) & 1) b.e[i] = 0.0f;
@@ -198,20 +233,47 @@ __global__ __launch_bounds__(kEngThreads) void eng_engram_in_kernel(EngineBufs b
     quantize_block(b.e, d.D, d.abits, red);
 }
 
-// Raw values into the ring, then the dilated causal conv over the taps (engine.cpp:771-780).
-__global__ __launch_bounds__(kEngThreads) void eng_engram_out_kernel(EngineBufs b, const float *__restrict__ taps,
-                                                                     const StepParams *__restrict__ p, int site,
-                                                                     EngineDims d) {
-    float *ring = b.engring + static_cast<size_t>(site) * d.engring * d.D;
+// The dilated causal conv over the taps (engine.cpp:771-780): a tap inside
+// this token's chunk reads that token's raw values, an older one the ring.
+__global__ __launch_bounds__(kEngThreads) void eng_engram_conv_kernel(EngineBufs b0, const float *__restrict__ taps,
+                                                                      const StepParams *__restrict__ p, int site,
+                                                                      EngineDims d) {
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
+    p += blockIdx.y;
+    const float *ring = b0.engring + static_cast<size_t>(site) * d.engring * d.D;
     for (int i = threadIdx.x; i < d.D; i += blockDim.x) {
-        ring[static_cast<size_t>(p->ring_row) * d.D + i] = b.rawv[i];
         float sum = 0.0f;
         for (int t = 0; t < d.taps; ++t) {
-            const int r = p->tap_rows[t];
-            if (r >= 0) sum += taps[t * d.D + i] * ring[static_cast<size_t>(r) * d.D + i];
+            const int pos = p->tap_pos[t];
+            if (pos < 0) continue;
+            const float v = pos >= p->chunk_start
+                                ? b0.rawv[static_cast<size_t>(pos - p->chunk_start) * d.D + i]
+                                : ring[static_cast<size_t>(pos % d.engring) * d.D + i];
+            sum += taps[t * d.D + i] * v;
         }
         b.ev[site * d.D + i] = sum;
     }
+}
+
+// Ring rows of the chunk's last min(tokens, engring) positions (block y: one of them).
+__global__ __launch_bounds__(kEngThreads) void eng_engram_ring_kernel(EngineBufs b0, const StepParams *__restrict__ p,
+                                                                      int site, int tokens, EngineDims d) {
+    const int keep = tokens < d.engring ? tokens : d.engring;
+    const int t = tokens - keep + static_cast<int>(blockIdx.y);
+    float *ring = b0.engring + static_cast<size_t>(site) * d.engring * d.D;
+    const int row = p[t].position % d.engring;
+    for (int i = threadIdx.x; i < d.D; i += blockDim.x)
+        ring[static_cast<size_t>(row) * d.D + i] = b0.rawv[static_cast<size_t>(t) * d.D + i];
+}
+
+// Slot of entry s of a token's attention list (engine.cpp:907-909): the
+// prefix slots, then positions start.. in the cache ring, which holds `ring`
+// positions past the prefix (cache_slot, engine.cpp:500, with a ring of the
+// window plus a prompt chunk so a chunk's stores never evict what its earlier
+// tokens read).
+__device__ __forceinline__ int slot_at(const StepParams *p, int s) {
+    const int pos = s < p->prefix_count ? s : p->start + s - p->prefix_count;
+    return !p->window ? pos : pos < p->prefix ? pos : p->prefix + (pos - p->prefix) % p->ring;
 }
 
 struct MixArgs {
@@ -222,18 +284,19 @@ struct MixArgs {
 
 // engine.cpp:980-992: lane gates from the mHC projections, the pre-mixed
 // residual u = bx, engram gates, then z = quant(rms(bx) * (1 + norm_in)).
-__global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b, LayerDev ld, MhcDev mh, MixArgs m,
+__global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, MixArgs m,
                                                               EngineDims d) {
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
     __shared__ float red[kEngThreads / 64];
     __shared__ float hp[16];
     __shared__ float zs[4096], ps[4096];
     __shared__ float proj[2 * 8 + 64];  // this layer's mHC projections: pre [N], post [N], res [N * N]
     const int N = d.N, D = d.D, l = m.l;
-    const int base[3] = {0, N, 2 * N};
-    for (int task = threadIdx.x; task < 2 * N + N * N; task += blockDim.x) {
-        const int mm = task < N ? 0 : task < 2 * N ? 1 : 2;
-        proj[task] = b.mhc_out[mm][m.mhc_row[mm] + task - base[mm]];
-    }
+    // (no indexing of b's pointer arrays by a runtime value: that would place b in private memory)
+    const float *pre_rows = b.mhc_out[0] + m.mhc_row[0], *post_rows = b.mhc_out[1] + m.mhc_row[1];
+    const float *res_rows = b.mhc_out[2] + m.mhc_row[2];
+    for (int task = threadIdx.x; task < 2 * N + N * N; task += blockDim.x)
+        proj[task] = task < N ? pre_rows[task] : task < 2 * N ? post_rows[task - N] : res_rows[task - 2 * N];
     __syncthreads();
     if (threadIdx.x < static_cast<unsigned>(N)) {
         const int n = threadIdx.x;
@@ -271,8 +334,10 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b, Laye
 // engine.cpp:994-1021: per-head rms of q and k, RoPE (first half paired with
 // second half), the new token's K/V into its cache slot (fp32, or the int8
 // quantiser of kv_store), and the attention slot list.
-__global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b, LayerDev ld, KvLayer kv,
+__global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d) {
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
+    p += blockIdx.y;
     const int HD = d.HD, half = HD / 2;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int heads = d.H + d.KV;
@@ -324,11 +389,9 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b, Layer
             }
         }
     }
-    // slot list of this position (engine.cpp:907-909, cache_slot engine.cpp:500)
-    for (int s = threadIdx.x; s < p->length; s += blockDim.x) {
-        const int pos = s < p->prefix_count ? s : p->start + s - p->prefix_count;
-        b.slots[s] = !p->window ? pos : pos < p->prefix ? pos : p->prefix + (pos - p->prefix) % p->window;
-    }
+    // slot list of this position (engine.cpp:907-909)
+    if (kv.k8)
+        for (int s = threadIdx.x; s < p->length; s += blockDim.x) b.slots[s] = slot_at(p, s);
 }
 
 // The fp32-KV attention step of one kv head in one workgroup: the norms and
@@ -336,25 +399,29 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b, Layer
 // cache, attention over the slot list (computed in place from the position,
 // engine.cpp:900-909) and the output gate att *= sigmoid(gate)
 // (engine.cpp:994-1023). Nothing crosses kv heads, so one launch does it all.
-__device__ __forceinline__ int slot_at(const StepParams *p, int s) {
-    const int pos = s < p->prefix_count ? s : p->start + s - p->prefix_count;
-    return !p->window ? pos : pos < p->prefix ? pos : p->prefix + (pos - p->prefix) % p->window;
-}
 
-__global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b, LayerDev ld, KvLayer kv,
+template <bool PREPARED>
+__global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d) {
     extern __shared__ float sc[];  // [G][length]
     __shared__ float qs[8 * 1024];  // query heads, then the partial outputs [R][G][HD] (1024 G floats)
     __shared__ float red[4];
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
+    p += blockIdx.y;
     const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63, length = p->length;
-    float *kc = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
-    float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
+    const float *kc = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
+    const float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
+    if (PREPARED) {  // eng_qk normalised and rotated q and stored K / V
+        for (int i = t; i < G * HD; i += blockDim.x) qs[i] = b.q[kh * G * HD + i];
+    } else {
     // norms + RoPE: heads 0..G-1 are this block's query heads (into qs), head G its K row (into the cache)
+    float *kw = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
+    float *vw = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
     for (int h = wave; h <= G; h += blockDim.x >> 6) {
         const float *src = h < G ? b.q + (kh * G + h) * HD : b.k + kh * HD;
         const float *gain = h < G ? ld.q_norm : ld.k_norm;
-        float *dst = h < G ? qs + h * HD : kc + static_cast<size_t>(p->slot) * HD;
+        float *dst = h < G ? qs + h * HD : kw + static_cast<size_t>(p->slot) * HD;
         float ss = 0.0f;
         for (int i = lane; i < HD; i += 64) ss += src[i] * src[i];
         ss = wave_sum(ss, lane);
@@ -366,7 +433,8 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b, Layer
             dst[j + half] = c * co + a * si;
         }
     }
-    for (int i = t; i < HD; i += blockDim.x) vc[static_cast<size_t>(p->slot) * HD + i] = b.v[kh * HD + i];
+    for (int i = t; i < HD; i += blockDim.x) vw[static_cast<size_t>(p->slot) * HD + i] = b.v[kh * HD + i];
+    }
     __syncthreads();
     for (int s = t; s < length; s += blockDim.x) {
         const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, s)) * HD);
@@ -435,8 +503,9 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b, Layer
 }
 
 // att *= sigmoid(gate); then the activation quantiser (engine.cpp:1023-1024).
-__global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b, EngineDims d) {
+__global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, EngineDims d) {
     __shared__ float red[kEngThreads / 64];
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
     for (int i = threadIdx.x; i < d.A; i += blockDim.x) b.att[i] *= sigmoidf_(b.gate[i]);
     __syncthreads();
     quantize_block(b.att, d.A, d.abits, red);
@@ -447,8 +516,9 @@ __global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b, Eng
 // layer's rms of x when `next_rms`. Thread i < D owns column i of every
 // vector (loaded once at the start); only the Hadamard transforms go through
 // LDS.
-__global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b, LayerDev ld, MhcDev mh, int l,
+__global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, int l,
                                                                int next_rms, EngineDims d) {
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
     __shared__ float red[kEngThreads / 64];
     __shared__ float mlp[4096];
     __shared__ float hr[64], hpo[8];
@@ -516,22 +586,26 @@ __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b, Lay
 }
 
 // z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
-__global__ __launch_bounds__(kEngThreads) void eng_final_kernel(EngineBufs b, const float *__restrict__ final_norm,
+__global__ __launch_bounds__(kEngThreads) void eng_final_kernel(EngineBufs b0, const float *__restrict__ final_norm,
                                                                 EngineDims d) {
     __shared__ float red[kEngThreads / 64];
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
     rms_block(b.hidden + (d.layers - 1) * d.D, b.zf, d.D, final_norm, red);
 }
 
-__global__ __launch_bounds__(kEngThreads) void eng_quantize_kernel(float *x, int n, int bits) {
+__global__ __launch_bounds__(kEngThreads) void eng_quantize_kernel(float *x, int n, int stride, int bits) {
     __shared__ float red[kEngThreads / 64];
-    quantize_block(x, n, bits, red);
+    quantize_block(x + static_cast<size_t>(blockIdx.y) * stride, n, bits, red);
 }
 
 // One wave per output row of a dense fp32 matrix.
 __global__ __launch_bounds__(256) void eng_dense_kernel(const float *__restrict__ w, int cols, int first, int rows,
-                                                        const float *__restrict__ x, float *__restrict__ y) {
+                                                        const float *__restrict__ x, float *__restrict__ y,
+                                                        int ystride) {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (r >= rows) return;
+    x += static_cast<size_t>(blockIdx.y) * cols;
+    y += static_cast<size_t>(blockIdx.y) * ystride;
     const float *row = w + static_cast<size_t>(first + r) * cols;
     float s = 0.0f;
     for (int i = lane; i < cols; i += 64) s += row[i] * x[i];
@@ -547,15 +621,17 @@ struct DenseRows {
     int first[3], rows[3];
 };
 
-__global__ __launch_bounds__(256) void eng_dense_multi_kernel(DenseRows a, int cols, const float *__restrict__ x) {
+__global__ __launch_bounds__(256) void eng_dense_multi_kernel(DenseRows a, int cols, int ystride,
+                                                              const float *__restrict__ x) {
     __shared__ float red[4];
+    x += static_cast<size_t>(blockIdx.y) * cols;
     int r = blockIdx.x, m = 0;
     while (m < 2 && r >= a.rows[m]) r -= a.rows[m++];
     const float *row = a.w[m] + static_cast<size_t>(a.first[m] + r) * cols;
     float s = 0.0f;
     for (int i = threadIdx.x; i < cols; i += blockDim.x) s += row[i] * x[i];
     s = block_sum(s, red);
-    if (threadIdx.x == 0) a.y[m][r] = s;
+    if (threadIdx.x == 0) a.y[m][static_cast<size_t>(blockIdx.y) * ystride + r] = s;
 }
 
 __global__ __launch_bounds__(256) void eng_dense_rows_kernel(const float *__restrict__ w, int cols,
@@ -568,76 +644,86 @@ __global__ __launch_bounds__(256) void eng_dense_rows_kernel(const float *__rest
 
 }  // namespace
 
-void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, hipStream_t s) {
-    hipLaunchKernelGGL(eng_start_kernel, dim3(1), dim3(kEngThreads), 0, s, z, b, d);
+void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s) {
+    hipLaunchKernelGGL(eng_start_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, z, b, d);
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_engram_in(const EngineBufs &b, const StepParams *p, int site, const EngineDims &d, hipStream_t s) {
-    hipLaunchKernelGGL(eng_engram_in_kernel, dim3(1), dim3(kEngThreads), 0, s, b, p, site, d);
+void launch_eng_engram_in(const EngineBufs &b, const StepParams *p, int site, const EngineDims &d, int tokens,
+                          hipStream_t s) {
+    hipLaunchKernelGGL(eng_engram_in_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, p, site, d);
     ND_HIP(hipGetLastError());
 }
 
 void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepParams *p, int site,
-                           const EngineDims &d, hipStream_t s) {
-    hipLaunchKernelGGL(eng_engram_out_kernel, dim3(1), dim3(kEngThreads), 0, s, b, taps, p, site, d);
+                           const EngineDims &d, int tokens, hipStream_t s) {
+    hipLaunchKernelGGL(eng_engram_conv_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, taps, p, site, d);
+    ND_HIP(hipGetLastError());
+    hipLaunchKernelGGL(eng_engram_ring_kernel, dim3(1, std::min(tokens, d.engring)), dim3(kEngThreads), 0, s, b, p,
+                       site, tokens, d);
     ND_HIP(hipGetLastError());
 }
 
 void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
-                    const int *sites, int nsites, const EngineDims &d, hipStream_t s) {
+                    const int *sites, int nsites, const EngineDims &d, int tokens, hipStream_t s) {
     MixArgs m{};
     m.l = l;
     m.nsites = nsites;
     for (int i = 0; i < nsites; ++i) m.sites[i] = sites[i];
     for (int i = 0; i < 3; ++i) m.mhc_row[i] = mhc_row[i];
-    hipLaunchKernelGGL(eng_mix_kernel, dim3(1), dim3(kEngThreads), 0, s, b, ld, mh, m, d);
+    hipLaunchKernelGGL(eng_mix_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, m, d);
     ND_HIP(hipGetLastError());
 }
 
 void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
-                   const EngineDims &d, hipStream_t s) {
-    hipLaunchKernelGGL(eng_qk_kernel, dim3(1), dim3(kEngThreads), 0, s, b, ld, kv, p, d);
+                   const EngineDims &d, int tokens, hipStream_t s) {
+    hipLaunchKernelGGL(eng_qk_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, kv, p, d);
     ND_HIP(hipGetLastError());
 }
 
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
-                           int length, const EngineDims &d, hipStream_t s) {
-    const size_t lds = static_cast<size_t>(d.H / d.KV) * length * sizeof(float);
-    hipLaunchKernelGGL(eng_attn_fused_kernel, dim3(d.KV), dim3(256), lds, s, b, ld, kv, p, d);
+                           int max_length, bool prepared, const EngineDims &d, int tokens, hipStream_t s) {
+    const size_t lds = static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);
+    if (prepared)
+        hipLaunchKernelGGL(eng_attn_fused_kernel<true>, dim3(d.KV, tokens), dim3(256), lds, s, b, ld, kv, p, d);
+    else
+        hipLaunchKernelGGL(eng_attn_fused_kernel<false>, dim3(d.KV, tokens), dim3(256), lds, s, b, ld, kv, p, d);
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_gate(const EngineBufs &b, const EngineDims &d, hipStream_t s) {
-    hipLaunchKernelGGL(eng_gate_kernel, dim3(1), dim3(kEngThreads), 0, s, b, d);
+void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s) {
+    hipLaunchKernelGGL(eng_gate_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, d);
     ND_HIP(hipGetLastError());
 }
 
 void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
-                     const EngineDims &d, hipStream_t s) {
-    hipLaunchKernelGGL(eng_post_kernel, dim3(1), dim3(kEngThreads), 0, s, b, ld, mh, l, next_rms ? 1 : 0, d);
+                     const EngineDims &d, int tokens, hipStream_t s) {
+    hipLaunchKernelGGL(eng_post_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, l, next_rms ? 1 : 0,
+                       d);
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, hipStream_t s) {
-    hipLaunchKernelGGL(eng_final_kernel, dim3(1), dim3(kEngThreads), 0, s, b, final_norm, d);
+void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, int tokens, hipStream_t s) {
+    hipLaunchKernelGGL(eng_final_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, final_norm, d);
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_quantize(float *x, int n, int bits, hipStream_t s) {
+void launch_eng_quantize(float *x, int n, int stride, int bits, int tokens, hipStream_t s) {
     if (!bits) return;
-    hipLaunchKernelGGL(eng_quantize_kernel, dim3(1), dim3(kEngThreads), 0, s, x, n, bits);
+    hipLaunchKernelGGL(eng_quantize_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, x, n, stride, bits);
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_dense(const float *w, int cols, int first, int rows, const float *x, float *y, hipStream_t s) {
+void launch_eng_dense(const float *w, int cols, int first, int rows, const float *x, float *y, int ystride,
+                      int tokens, hipStream_t s) {
     if (rows <= 0) return;
-    hipLaunchKernelGGL(eng_dense_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, w, cols, first, rows, x, y);
+    hipLaunchKernelGGL(eng_dense_kernel, dim3((rows + 3) / 4, tokens), dim3(256), 0, s, w, cols, first, rows, x, y,
+                       ystride);
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_dense3(const float *const *w, const int *first, const int *rows, float *const *y, int cols,
-                       const float *x, hipStream_t s) {
+void launch_eng_dense3(const float *const *w, const int *first, const int *rows, float *const *y, int ystride,
+                       int cols, const float *x, int tokens, hipStream_t s) {
     DenseRows a{};
     int total = 0;
     for (int m = 0; m < 3; ++m) {
@@ -648,7 +734,7 @@ void launch_eng_dense3(const float *const *w, const int *first, const int *rows,
         total += a.rows[m];
     }
     if (!total) return;
-    hipLaunchKernelGGL(eng_dense_multi_kernel, dim3(total), dim3(256), 0, s, a, cols, x);
+    hipLaunchKernelGGL(eng_dense_multi_kernel, dim3(total, tokens), dim3(256), 0, s, a, cols, ystride, x);
     ND_HIP(hipGetLastError());
 }
 

@@ -117,6 +117,7 @@ class NativeEngine:
                                                     ct.c_void_p], ct.c_int),
                 ("needle2_engine_prefill", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_void_p],
                  ct.c_int),
+                ("needle2_engine_project_candidates", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p], ct.c_int),
                 ("needle2_engine_set_int8_kv", [ct.c_void_p, ct.c_int], ct.c_int),
                 ("needle2_engine_set_sdot", [ct.c_void_p], ct.c_int),
                 ("needle2_engine_set_lookup", [ct.c_void_p, ct.c_int], None),

@@ -361,6 +361,9 @@ class RefEngine:
                 ("needle2_engine_step_candidates", [ct.c_void_p, ct.c_int, ct.c_void_p, ct.c_int, ct.c_void_p,
                                                     ct.c_void_p], ct.c_int),
                 ("needle2_engine_set_int8_kv", [ct.c_void_p, ct.c_int], ct.c_int),
+                ("needle2_engine_prefill", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p,
+                                            ct.c_void_p], ct.c_int),
+                ("needle2_engine_project_candidates", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p], ct.c_int),
                 ("needle2_engine_error", [], ct.c_char_p)):
             f = getattr(L, name)
             f.argtypes, f.restype = args, res
@@ -383,3 +386,21 @@ class RefEngine:
         if self.L.needle2_engine_step(self.h, int(token), logits.ctypes.data, hidden.ctypes.data):
             raise RuntimeError(self.L.needle2_engine_error().decode())
         return logits, hidden
+
+    def prefill(self, tokens, last_only=False):
+        """Engine::prefill (engine.cpp:1045-1301): (logits [tokens][vocab] or [vocab], last token's hidden)."""
+        ids = np.ascontiguousarray(tokens, np.int32)
+        vocab = self.m["vocab_size"]
+        logits = np.empty(vocab if last_only else (ids.size, vocab), np.float32)
+        hidden = np.empty((self.m["num_layers"], self.m["d_model"]), np.float32)
+        if self.L.needle2_engine_prefill(self.h, ids.ctypes.data, ids.size, int(last_only), logits.ctypes.data,
+                                         hidden.ctypes.data):
+            raise RuntimeError(self.L.needle2_engine_error().decode())
+        return logits, hidden
+
+    def project_candidates(self, candidates):
+        ids = np.ascontiguousarray(candidates, np.int32)
+        out = np.empty(ids.size, np.float32)
+        if self.L.needle2_engine_project_candidates(self.h, ids.ctypes.data, ids.size, out.ctypes.data):
+            raise RuntimeError(self.L.needle2_engine_error().decode())
+        return out

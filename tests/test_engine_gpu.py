@@ -94,14 +94,78 @@ def test_candidates_equal_full_logits():
         np.testing.assert_array_equal(sel.step(33), full.step(33))
 
 
-def test_prefill_equals_steps():
-    a = small(8, seed=6)
+PROMPT = [int(t) for t in np.random.default_rng(61).integers(0, 512, 45)]
+
+
+def gpu_prefill(engine, tokens, last_only=False):
+    """needle2_engine_prefill with the hidden states too (NativeEngine.prefill returns logits only)."""
+    ids = np.ascontiguousarray(tokens, np.int32)
+    vocab, layers, d = (engine.metadata[k] for k in ("vocab_size", "num_layers", "d_model"))
+    logits = np.empty(vocab if last_only else (ids.size, vocab), np.float32)
+    hidden = np.empty((layers, d), np.float32)
+    assert engine._lib.needle2_engine_prefill(engine._handle, ids.ctypes.data, ids.size, int(last_only),
+                                              logits.ctypes.data, hidden.ctypes.data) == 0
+    engine.position += ids.size
+    return logits, hidden
+
+
+def gpu_project(engine, ids):
+    ids = np.ascontiguousarray(ids, np.int32)
+    out = np.empty(ids.size, np.float32)
+    assert engine._lib.needle2_engine_project_candidates(engine._handle, ids.ctypes.data, ids.size,
+                                                         out.ctypes.data) == 0
+    return out
+
+
+@pytest.mark.parametrize("window,prefix", [(0, 0), (8, 0), (8, 3)])
+@pytest.mark.parametrize("int8", [False, True])
+def test_prefill_matches_reference(window, prefix, int8):
+    """A 45-token prompt in chunks (32 tokens, or the window: 8) against the reference's chunked prefill: every
+    token's logits, the last token's hidden states, candidates projected right after (the reference projects
+    the last token's embedding row there) and the steps that follow."""
+    a = small(window, seed=7)
+    gpu = NativeEngine(a, kv_cache="int8" if int8 else "fp32")
+    ref = oracle.RefEngine(a, 0, int8)
+    gpu.reset(prefix)
+    ref.reset(prefix)
+    lg, hd = gpu_prefill(gpu, PROMPT)
+    rl, rh = ref.prefill(PROMPT)
+    ids = np.array([3, 500, 77, 3], np.int32)
+    pairs = [("logits", lg, rl), ("hidden", hd, rh), ("candidates", gpu_project(gpu, ids), ref.project_candidates(ids))]
+    for t in (11, 400, 2):
+        g, r = gpu.step(t, return_hidden=True), ref.step(t)
+        pairs += [(f"step {t} logits", g[0], r[0]), (f"step {t} hidden", g[1], r[1])]
+    for what, g, r in pairs:
+        print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
+        if int8:
+            assert rel_l2(g, r) < 1e-3, what
+        else:
+            np.testing.assert_allclose(g, r, atol=ATOL, rtol=RTOL, err_msg=what)
+
+
+def test_prefill_released_geometry():
+    """27 layers of the released geometry (window 256, chunks of 32): a 40-token prompt, last logits only."""
+    a = Archive(synthetic_released(seed=8, tokenizer_bytes=0))
+    tokens = [int(t) for t in np.random.default_rng(62).integers(0, 8192, 40)]
+    gpu, ref = NativeEngine(a), oracle.RefEngine(a)
+    lg, hd = gpu_prefill(gpu, tokens, last_only=True)
+    rl, rh = ref.prefill(tokens, last_only=True)
+    print(f"logits max {np.abs(lg - rl).max():.2e}, hidden max {np.abs(hd - rh).max():.2e}", flush=True)
+    np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("window", [0, 8])
+def test_prefill_equals_steps(window):
+    """A token's arithmetic does not depend on the launch it shares: prefill equals stepping bit for bit."""
+    a = small(window, seed=6)
     e1, e2 = NativeEngine(a), NativeEngine(a)
-    stepped = np.stack([e1.step(t) for t in TOKENS[:12]])
-    np.testing.assert_array_equal(e2.prefill(TOKENS[:12]), stepped)
+    stepped = np.stack([e1.step(t) for t in PROMPT])
+    np.testing.assert_array_equal(e2.prefill(PROMPT), stepped)
     np.testing.assert_array_equal(e2.step(4), e1.step(4))
-    e3 = NativeEngine(a)
-    np.testing.assert_array_equal(e3.prefill(TOKENS[:12], last_only=True), stepped[-1])
+    e3 = NativeEngine(a, kv_cache="int8")
+    e4 = NativeEngine(a, kv_cache="int8")
+    np.testing.assert_array_equal(e3.prefill(PROMPT, last_only=True), np.stack([e4.step(t) for t in PROMPT])[-1])
 
 
 def test_engine_errors():
