@@ -342,13 +342,15 @@ def bench_archive_upload():
 def bench_engine(tokens=64):
     """NativeEngine.step on the GPU for the released geometry (27 layers, d_model 512, random contents, KV window
     256): whole-token latency as the caller sees it (host pointers: the token in, 8192 logits out, one wait per
-    token), fp32 and int8 KV, after 16 untimed tokens. Returns {kv: (tokens/s, [ms per token])}."""
+    token), fp32 and int8 KV, and the int8 matmul path ("sdot", fp32 KV), after 16 untimed tokens. Returns
+    {config: (tokens/s, [ms per token])}."""
     from openneedle_amd.archive import Archive, synthetic_released
     from openneedle_amd.engine import NativeEngine
     archive = Archive(synthetic_released(seed=3, tokenizer_bytes=0))
     out = {}
-    for kv in ("fp32", "int8"):
-        e = NativeEngine(archive, kv_cache=kv)
+    for kv in ("fp32", "int8", "sdot"):
+        e = NativeEngine(archive, kv_cache="int8" if kv == "int8" else "fp32",
+                         matmul="sdot" if kv == "sdot" else "fp32")
         for i in range(16):
             e.step((i * 131) % 8192)
         times = []
@@ -363,6 +365,7 @@ def bench_engine(tokens=64):
 
 
 PROMPT_TOKENS = 512
+ENGINE_LABEL = {"fp32": "fp32_kv", "int8": "int8_kv", "sdot": "sdot_matmul"}
 
 
 def prompt_tokens():
@@ -378,8 +381,9 @@ def bench_engine_prefill(runs=8):
     archive = Archive(synthetic_released(seed=3, tokenizer_bytes=0))
     tokens = prompt_tokens()
     out = {}
-    for kv in ("fp32", "int8"):
-        e = NativeEngine(archive, kv_cache=kv)
+    for kv in ("fp32", "int8", "sdot"):
+        e = NativeEngine(archive, kv_cache="int8" if kv == "int8" else "fp32",
+                         matmul="sdot" if kv == "sdot" else "fp32")
         e.prefill(tokens, last_only=True)
         times = []
         for _ in range(runs):
@@ -703,13 +707,13 @@ def main():
 
         log("engine: NativeEngine.step, released geometry (27 layers), batch 1")
         for kv, (tps, tok_ms) in bench_engine().items():
-            extra[f"engine_{kv}_kv_tokens_per_s"] = round(tps, 1)
-            extra[f"engine_{kv}_kv_token_us"] = dist_us(tok_ms)
+            extra[f"engine_{ENGINE_LABEL[kv]}_tokens_per_s"] = round(tps, 1)
+            extra[f"engine_{ENGINE_LABEL[kv]}_token_us"] = dist_us(tok_ms)
             log(f"engine {kv} KV: {tps:.0f} tokens/s")
         log(f"engine prefill: NativeEngine.prefill, released geometry, {PROMPT_TOKENS}-token prompt")
         for kv, (tps, pr_ms) in bench_engine_prefill().items():
-            extra[f"engine_prefill_{kv}_kv_tokens_per_s"] = round(tps, 1)
-            extra[f"engine_prefill_{kv}_kv_prompt_us"] = dist_us(pr_ms)
+            extra[f"engine_prefill_{ENGINE_LABEL[kv]}_tokens_per_s"] = round(tps, 1)
+            extra[f"engine_prefill_{ENGINE_LABEL[kv]}_prompt_us"] = dist_us(pr_ms)
             log(f"engine prefill {kv} KV: {tps:.0f} tokens/s")
 
         ms_u, nb = bench_archive_upload()

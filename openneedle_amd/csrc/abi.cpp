@@ -250,28 +250,36 @@ void CqHandle::rows_host(const int64_t *ids, float *y, int count) {
 // ---------------------------------------------------------------------------
 // int8 handle
 // ---------------------------------------------------------------------------
-void SdotHandle::init_tables() {
+SdotGeom sdot_geom_of(const Matrix &m) {
     // sdot.cpp:38-44: cs = max|cb|/127 (1 if zero), centroids = clamp(nearbyint(cb/cs))
     float maximum = 0;
     const int n = 1 << m.bits;
     for (int i = 0; i < n; ++i) maximum = std::max(maximum, std::abs(m.cb_raw[i]));
-    centroid_scale = maximum > 0 ? maximum / 127 : 1;
-    uint8_t cent[16] = {};
-    for (int i = 0; i < n; ++i) {
-        float v = std::nearbyint(m.cb_raw[i] / centroid_scale);
-        v = v < -127.0f ? -127.0f : (127.0f < v ? 127.0f : v);
-        cent[i] = static_cast<uint8_t>(static_cast<int8_t>(v));
-    }
-    std::memcpy(centroids, cent, sizeof centroids);
-}
-
-SdotGeom SdotHandle::geom() const {
     SdotGeom g{};
     g.kind = m.kind;
     g.group = m.group;
     g.groups = m.groups;
     g.windows = m.windows;
     g.chunks = m.chunks;
+    g.centroid_scale = maximum > 0 ? maximum / 127 : 1;
+    uint8_t cent[16] = {};
+    for (int i = 0; i < n; ++i) {
+        float v = std::nearbyint(m.cb_raw[i] / g.centroid_scale);
+        v = v < -127.0f ? -127.0f : (127.0f < v ? 127.0f : v);
+        cent[i] = static_cast<uint8_t>(static_cast<int8_t>(v));
+    }
+    std::memcpy(g.cent, cent, sizeof g.cent);
+    return g;
+}
+
+void SdotHandle::init_tables() {
+    const SdotGeom g = sdot_geom_of(m);
+    centroid_scale = g.centroid_scale;
+    std::memcpy(centroids, g.cent, sizeof centroids);
+}
+
+SdotGeom SdotHandle::geom() const {
+    SdotGeom g = sdot_geom_of(m);
     g.centroid_scale = centroid_scale;
     std::memcpy(g.cent, centroids, sizeof g.cent);
     return g;

@@ -110,6 +110,9 @@ struct CqHandle {
                      int repeat = 1);
 };
 
+// The int8 path's geometry and centroid tables of a CQ matrix (sdot.cpp:35-60).
+SdotGeom sdot_geom_of(const Matrix &m);
+
 struct SdotHandle {
     Matrix m;
     Staging st;

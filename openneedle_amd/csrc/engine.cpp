@@ -49,6 +49,7 @@ struct Mat {
     const Matrix *cq = nullptr;
     const float *dense = nullptr;
     int rows = 0, cols = 0;
+    bool int8 = false;  // the CQ matrix runs the int8 path (needle2_engine_set_sdot)
 };
 
 // Row tiles of several CQ matrices that share one input, run as one GEMV
@@ -120,10 +121,75 @@ struct GemvGroup {
     }
 };
 
+// The int8 ("SDOT") counterpart of GemvGroup (engine.cpp:502-515, 560-577
+// with the SDOT path on): each token's input transformed and quantised once
+// (one prepare launch for the chunk), then the int8 GEMV over the pieces'
+// row tiles, per token and piece one job of batch 1.
+struct SdotGroup {
+    const Matrix *m0 = nullptr;
+    SdotGeom g{};
+    DevBuf<uint8_t> jobs;
+    DevBuf<int32_t> q;
+    DevBuf<float> xs, rot, big;
+    DevBuf<const float *> xptr;
+    int pieces = 0, per_token = 0;
+    const float *x = nullptr;
+    SdotJob job0{};
+
+    void build(const std::vector<GemvGroup::Piece> &ps, const float *input, int tokens) {
+        m0 = ps[0].m;
+        x = input;
+        g = sdot_geom_of(*m0);
+        q.reserve(size_t(tokens) * m0->dev / 4);
+        xs.reserve(size_t(tokens) * m0->groups);
+        rot.reserve(size_t(tokens) * m0->dev);
+        std::vector<const float *> rows_in(tokens);
+        for (int t = 0; t < tokens; ++t) rows_in[t] = input + size_t(t) * m0->in;
+        xptr.reserve(tokens);
+        ND_HIP(hipMemcpy(xptr.p, rows_in.data(), tokens * sizeof(const float *), hipMemcpyHostToDevice));
+        std::vector<SdotJob> host;
+        int blocks = 0;
+        for (int t = 0; t < tokens; ++t)
+            for (const GemvGroup::Piece &p : ps) {
+                ND_CHECK(GemvGroup::compatible(*m0, *p.m), "internal: GEMV group of mixed geometry");
+                const int tile0 = p.first / kRowsPerBlock;
+                const int tiles = (p.first + p.rows - 1) / kRowsPerBlock - tile0 + 1;
+                const int rows = std::min(tiles * kRowsPerBlock, p.m->out - tile0 * kRowsPerBlock);
+                const int32_t *qt = q.p + size_t(t) * m0->dev / 4;
+                const float *st = xs.p + size_t(t) * m0->groups;  // batch 1: the transposed scales are the same
+                host.push_back(SdotJob{p.m->codes.p + size_t(tile0) * p.m->chunks * kRowsPerBlock,
+                                       p.m->norms.p + size_t(tile0) * p.m->groups * kRowsPerBlock, qt, st,
+                                       p.y + size_t(t) * p.ystride, rows, tiles * kRowsPerBlock, blocks, 1, st});
+                blocks += tiles;
+            }
+        pieces = static_cast<int>(ps.size());
+        per_token = blocks / tokens;
+        job0 = host[0];
+        if (host.size() > 1) {
+            jobs.reserve(host.size() * sizeof(SdotJob));
+            ND_HIP(hipMemcpy(jobs.p, host.data(), host.size() * sizeof(SdotJob), hipMemcpyHostToDevice));
+        }
+    }
+
+    void run(hipStream_t s, int tokens) {
+        if (!launch_sdot_prepare(nullptr, xptr.p, 1, tokens, m0->in, m0->padded, m0->dev, m0->group, m0->scale,
+                                 m0->kind, q.p, xs.p, nullptr, s)) {
+            m0->transform(x, m0->in, rot.p, tokens, big, s);
+            launch_sdot_quantize(rot.p, m0->dev, tokens, m0->padded, m0->dev, m0->group, m0->kind, q.p, xs.p, s);
+        }
+        const int njobs = pieces * tokens;
+        if (njobs > 1)
+            launch_sdot_gemv(g, SdotJob{}, reinterpret_cast<const SdotJob *>(jobs.p), njobs, per_token * tokens, 1, s);
+        else
+            launch_sdot_gemv(g, job0, nullptr, 0, per_token, 1, s);
+    }
+};
+
 // GEMVs of several matrices over one input: CQ matrices in as few groups as
-// their geometries allow, dense ones through the dense kernel.
+// their geometries and paths allow, dense ones through the dense kernel.
 struct Projection {
     std::vector<std::unique_ptr<GemvGroup>> groups;
+    std::vector<std::unique_ptr<SdotGroup>> groups8;
     struct Dense {
         const float *w;
         int cols, first, rows;
@@ -131,31 +197,39 @@ struct Projection {
         int ystride;
     };
     std::vector<Dense> dense;
+    std::vector<std::vector<GemvGroup::Piece>> pending, pending8;
     const float *x = nullptr;
 
     // (matrix, first row, rows, output, floats between tokens' outputs)
-    void add(const Mat &m, int first, int rows, float *y, int ystride,
-             std::vector<std::vector<GemvGroup::Piece>> &pending) {
+    void add(const Mat &m, int first, int rows, float *y, int ystride) {
         if (!m.cq) {
             dense.push_back(Dense{m.dense, m.cols, first, rows, y, ystride});
             return;
         }
-        for (auto &g : pending)
+        auto &pend = m.int8 ? pending8 : pending;
+        for (auto &g : pend)
             if (GemvGroup::compatible(*g[0].m, *m.cq)) {
                 g.push_back({m.cq, first, rows, y, ystride});
                 return;
             }
-        pending.push_back({{m.cq, first, rows, y, ystride}});
+        pend.push_back({{m.cq, first, rows, y, ystride}});
     }
-    void finish(std::vector<std::vector<GemvGroup::Piece>> &pending, const float *input, int tokens) {
+    void finish(const float *input, int tokens) {
         x = input;
         for (auto &p : pending) {
             groups.push_back(std::make_unique<GemvGroup>());
             groups.back()->build(p, input, tokens);
         }
+        for (auto &p : pending8) {
+            groups8.push_back(std::make_unique<SdotGroup>());
+            groups8.back()->build(p, input, tokens);
+        }
+        pending.clear();
+        pending8.clear();
     }
     void run(hipStream_t s, int tokens) {
         for (auto &g : groups) g->run(s, tokens);
+        for (auto &g : groups8) g->run(s, tokens);
         for (auto &d : dense) launch_eng_dense(d.w, d.cols, d.first, d.rows, x, d.y, d.ystride, tokens, s);
     }
 };
@@ -215,6 +289,8 @@ struct GpuEngine {
     int max_length() const { return c.window ? c.window + prefix : capacity; }
     void set_token(int t, int token);
     void run(int tokens);
+    void build_projections();
+    void set_sdot();
     void step(int token, float *logits_out, float *hidden_out);
     void prefill(const int *tokens, int num_tokens, bool last_only, float *logits_out, float *hidden_out);
     void project_candidates(const int *candidates, int count, float *out);
@@ -382,35 +458,16 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
         L.d1 = vec(t0 + 11);
         L.d2 = vec(t0 + 12);
         L.d3 = vec(t0 + 13);
-        {
-            std::vector<std::vector<GemvGroup::Piece>> pend;
-            qkvg[l].add(mat(t0 + 1, A, D), 0, A, b.q, A, pend);
-            qkvg[l].add(mat(t0 + 2, K, D), 0, K, b.k, K, pend);
-            qkvg[l].add(mat(t0 + 3, K, D), 0, K, b.v, K, pend);
-            qkvg[l].add(mat(t0 + 6, A, D), 0, A, b.gate, A, pend);
-            qkvg[l].finish(pend, b.z, chunk);
-        }
-        {
-            std::vector<std::vector<GemvGroup::Piece>> pend;
-            oproj[l].add(mat(t0 + 7, D, A), 0, D, b.proj, D, pend);
-            oproj[l].finish(pend, b.att, chunk);
-        }
-        {
-            const int rows[3] = {N, N, N * N};
-            std::vector<std::vector<GemvGroup::Piece>> pend;
-            for (int m = 0; m < 3; ++m) {
-                const Mat &M = mat(mhi + 6 + m, c.layers * rows[m], N * D);
-                const int first = l * rows[m];
-                if (M.cq) {  // the GEMV's row tiles; dense rows go through one multi-matrix launch
-                    mhc_row[l][m] = first - first / kRowsPerBlock * kRowsPerBlock;
-                    mhc_proj[l].add(M, first, rows[m], b.mhc_out[m], mhc_tiles, pend);
-                } else {
-                    mhc_row[l][m] = 0;
-                }
-                phi[m] = M.cq ? nullptr : M.dense;
-                mhc_rows[m] = rows[m];
-            }
-            mhc_proj[l].finish(pend, b.nx, chunk);
+        (void)mat(t0 + 1, A, D), (void)mat(t0 + 2, K, D), (void)mat(t0 + 3, K, D), (void)mat(t0 + 6, A, D);
+        (void)mat(t0 + 7, D, A);
+        const int rows[3] = {N, N, N * N};
+        for (int m = 0; m < 3; ++m) {
+            const Mat &M = mat(mhi + 6 + m, c.layers * rows[m], N * D);
+            const int first = l * rows[m];
+            // the GEMV's row tiles; dense rows go through one multi-matrix launch
+            mhc_row[l][m] = M.cq ? first - first / kRowsPerBlock * kRowsPerBlock : 0;
+            phi[m] = M.cq ? nullptr : M.dense;
+            mhc_rows[m] = rows[m];
         }
     }
     for (int s = 0; s < c.num_sites; ++s) {
@@ -419,21 +476,58 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
         ND_CHECK(mats[e0].cq ? mats[e0].cq->in == c.subdim : mats[e0].cols == c.subdim,
                  "engine: engram tables shape does not match the geometry");
         (void)vec(e0 + 3);
-        engram_kv.emplace_back();
-        std::vector<std::vector<GemvGroup::Piece>> pend;
-        engram_kv.back().add(mat(e0 + 1, D, D), 0, D, b.ek + s * D, sites * D, pend);
-        engram_kv.back().add(mat(e0 + 2, D, D), 0, D, b.rawv, D, pend);
-        engram_kv.back().finish(pend, b.e, chunk);
+        (void)mat(e0 + 1, D, D), (void)mat(e0 + 2, D, D);
         if (mats[e0].cq) row_scratch.reserve(size_t(chunk) * c.tables * mats[e0].cq->padded);
     }
     (void)vec(final_norm());
-    {
-        std::vector<std::vector<GemvGroup::Piece>> pend;
-        lm_head.add(mat(0, c.vocab, D), 0, c.vocab, logits.p, c.vocab, pend);
-        lm_head.finish(pend, b.zf, chunk);
-    }
+    (void)mat(0, c.vocab, D);
     if (mats[0].cq) row_scratch.reserve(std::max(row_scratch.n, size_t(chunk) * mats[0].cq->padded));
+    build_projections();
     reset(0);
+}
+
+// The GEMV launches of every projection over the chunk's buffers, each CQ
+// matrix on its path (FP32 or int8).
+void GpuEngine::build_projections() {
+    const int D = c.dim, N = c.lanes, A = c.heads * c.head_dim, K = c.kvheads * c.head_dim;
+    const int mhi = mh0();
+    for (auto *v : {&mhc_proj, &qkvg, &oproj, &engram_kv}) v->clear();
+    mhc_proj.resize(c.layers);
+    qkvg.resize(c.layers);
+    oproj.resize(c.layers);
+    engram_kv.resize(c.num_sites);
+    lm_head = Projection{};
+    for (int l = 0; l < c.layers; ++l) {
+        const int t0 = ti(l);
+        qkvg[l].add(mats[t0 + 1], 0, A, b.q, A);
+        qkvg[l].add(mats[t0 + 2], 0, K, b.k, K);
+        qkvg[l].add(mats[t0 + 3], 0, K, b.v, K);
+        qkvg[l].add(mats[t0 + 6], 0, A, b.gate, A);
+        qkvg[l].finish(b.z, chunk);
+        oproj[l].add(mats[t0 + 7], 0, D, b.proj, D);
+        oproj[l].finish(b.att, chunk);
+        const int rows[3] = {N, N, N * N};
+        for (int m = 0; m < 3; ++m)
+            if (mats[mhi + 6 + m].cq) mhc_proj[l].add(mats[mhi + 6 + m], l * rows[m], rows[m], b.mhc_out[m], dims.mhc_stride);
+        mhc_proj[l].finish(b.nx, chunk);
+    }
+    for (int s = 0; s < c.num_sites; ++s) {
+        const int e0 = engram_base() + 4 * s;
+        engram_kv[s].add(mats[e0 + 1], 0, D, b.ek + s * D, dims.sites * D);
+        engram_kv[s].add(mats[e0 + 2], 0, D, b.rawv, D);
+        engram_kv[s].finish(b.e, chunk);
+    }
+    lm_head.add(mats[0], 0, c.vocab, logits.p, c.vocab);
+    lm_head.finish(b.zf, chunk);
+}
+
+// engine.cpp:424-432: the int8 path for the CQ matrices of 2- or 4-bit codes
+// and groups of 64 .. 131072 (the rest stay FP32), for every later step.
+void GpuEngine::set_sdot() {
+    for (Mat &m : mats)
+        if (m.cq && (m.cq->bits == 2 || m.cq->bits == 4) && m.cq->group >= 64 && m.cq->group <= 131072) m.int8 = true;
+    ND_HIP(hipStreamSynchronize(stream));
+    build_projections();
 }
 
 void GpuEngine::reset(int prefix_len) {
@@ -720,6 +814,18 @@ void GpuEngine::project_candidates(const int *candidates, int count, float *out)
         if (cand.full) {
             lm_head.run(s, 1);
             launch_gather_outputs(logits.p, c.vocab, st.ids.p, count, 1, st.y.p, s);
+        } else if (head.int8) {  // engine.cpp:1312-1323: prepare once, then the candidate rows
+            const Matrix &m = *head.cq;
+            st.q.reserve(m.dev / 4);
+            st.xs.reserve(m.groups);
+            st.rot.reserve(m.dev);
+            if (!launch_sdot_prepare(b.zf, nullptr, 1, 1, m.in, m.padded, m.dev, m.group, m.scale, m.kind, st.q.p,
+                                     st.xs.p, nullptr, s)) {
+                m.transform(b.zf, m.in, st.rot.p, 1, st.big, s);
+                launch_sdot_quantize(st.rot.p, m.dev, 1, m.padded, m.dev, m.group, m.kind, st.q.p, st.xs.p, s);
+            }
+            const SdotJob job{cand.codes, cand.norms, st.q.p, st.xs.p, st.y.p, count, cand.n_pad, 0, 1, st.xs.p};
+            launch_sdot_gemv(sdot_geom_of(m), job, nullptr, 0, cand.n_pad / kRowsPerBlock, 1, s);
         } else {
             matrix_gemv(*head.cq, st, cand.codes, cand.norms, count, cand.n_pad, b.zf, st.y.p, 1, s);
         }
@@ -758,10 +864,15 @@ void needle2_engine_destroy(void *p) { delete static_cast<GpuEngine *>(p); }
 // The reference's projection lookup modes are CPU summation schemes; every mode runs the GPU GEMV.
 void needle2_engine_set_lookup(void *, int) {}
 
-// engine.cpp:1506-1509 on a host without DotProd: the int8 engine path is not available here.
-int needle2_engine_set_sdot(void *) {
-    engine_error = "SDOT requires an ARM64 CPU with DotProd support";
-    return -1;
+// engine.cpp:1506-1509: the int8 matmul path, which the GPU runs everywhere.
+int needle2_engine_set_sdot(void *p) {
+    try {
+        static_cast<GpuEngine *>(p)->set_sdot();
+        return 0;
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
 }
 
 void needle2_engine_reset(void *p, int prefix) {

@@ -330,7 +330,7 @@ class RefEngine:
     descriptors NativeEngine builds (needle2/native.py:382-395): CQ records through the reference's CQ handles,
     everything else (the mHC matrices too) as dequantized fp32."""
 
-    def __init__(self, archive, activation_bits=0, int8_kv=False, threads=1):
+    def __init__(self, archive, activation_bits=0, int8_kv=False, threads=1, sdot=False):
         from openneedle_amd.archive import CQ
         from openneedle_amd.engine import _TensorDesc, _EngineConfig, engine_config, engine_tensors
         L = ref()
@@ -370,6 +370,9 @@ class RefEngine:
         self.h = L.needle2_engine_create(ct.byref(self._cfg), self._descs, len(descs), threads, activation_bits)
         if not self.h:
             raise RuntimeError(L.needle2_engine_error().decode())
+        if sdot:  # the Engine's int8 matmul path (engine.cpp:424-432 without the ARM feature test)
+            L.refh_engine_sdot.argtypes, L.refh_engine_sdot.restype = [ct.c_void_p], ct.c_int
+            assert L.refh_engine_sdot(self.h) == 0
         if int8_kv:
             assert L.needle2_engine_set_int8_kv(self.h, 1) == 0
 

@@ -11,6 +11,10 @@
 //   * Engine::import_state (engine.cpp:784-815), whose int8 branch is the same
 //     KV quantizer as Engine::step (engine.cpp:1005-1021), and
 //     Engine::compute_attention (engine.cpp:898-967).
+//   * Engine's SDOT matmul path: Engine::configure_sdot (engine.cpp:424-432)
+//     returns false on x86 for the same reason, so refh_engine_sdot makes the
+//     same SdotCQ matrices (2/4-bit codes, groups 64..131072) and switches
+//     the path on, leaving every other line of the Engine as built.
 // Output goes only to oracle/_ref/. No reference source is copied.
 #include "cq.cpp"
 
@@ -86,6 +90,22 @@ void refh_attn_cache(void *h, int8_t *keys, int8_t *values, float *k_scales, flo
 // Attend query q [heads][head_dim] over positions 0..pos_cur of layer 0.
 void refh_attn_compute(void *h, int pos_cur, const float *q, float *out) {
     static_cast<Engine *>(h)->compute_attention(0, pos_cur, q, out);
+}
+
+// engine.cpp:424-432 without the CPU feature test.
+int refh_engine_sdot(void *h) {
+    auto *e = static_cast<Engine *>(h);
+    try {
+        for (size_t i = 0; i < e->t.size(); ++i)
+            if (e->t[i].cq) {
+                auto *q = static_cast<CQ *>(e->t[i].cq);
+                if ((q->bits == 2 || q->bits == 4) && q->group >= 64 && q->group <= 131072)
+                    e->sdot[i] = std::make_unique<SdotCQ>(q->packed, q->norms, q->out, q->in, q->bits, q->group,
+                                                          q->cb.data());
+            }
+        e->sdot_enabled = true;
+        return 0;
+    } catch (...) { return -1; }
 }
 
 }  // extern "C"

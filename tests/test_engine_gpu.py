@@ -168,6 +168,62 @@ def test_prefill_equals_steps(window):
     np.testing.assert_array_equal(e3.prefill(PROMPT, last_only=True), np.stack([e4.step(t) for t in PROMPT])[-1])
 
 
+def small64(window=0, seed=9):
+    """The small geometry with groups of 64: every CQ matrix qualifies for the int8 path."""
+    return Archive(synthetic_model(SMALL, engram_layers=(1,), engram_orders=(2, 3), kv_window=window, group=64,
+                                   seed=seed))
+
+
+@pytest.mark.parametrize("window", [0, 8])
+@pytest.mark.parametrize("int8_kv", [False, True])
+def test_sdot_matches_reference(window, int8_kv):
+    """matmul="sdot" (engine.cpp:424-432: int8 activations x int8 centroids for 2/4-bit CQ matrices of groups
+    >= 64) against the reference Engine with the same matrices on its SDOT path: a prompt through prefill, then
+    steps and candidate rows. The int8 GEMVs are bit-exact for equal inputs; fp32 rounding in the glue can move
+    one quantised activation code by one step, so the bar is a relative L2 error."""
+    a = small64(window)
+    gpu = NativeEngine(a, matmul="sdot", kv_cache="int8" if int8_kv else "fp32")
+    ref = oracle.RefEngine(a, 0, int8_kv, sdot=True)
+    fp32 = oracle.RefEngine(a, 0, int8_kv)
+    lg, hd = gpu_prefill(gpu, PROMPT[:20])
+    rl, rh = ref.prefill(PROMPT[:20])
+    fl, _ = fp32.prefill(PROMPT[:20])
+    print(f"prefill: rel {rel_l2(lg, rl):.2e} (fp32 path vs SDOT path in the reference: {rel_l2(fl, rl):.2e})",
+          flush=True)
+    pairs = [("prefill logits", lg, rl), ("prefill hidden", hd, rh)]
+    ids = np.array([9, 300, 511, 9, 0], np.int32)
+    for t in (7, 123, 45):
+        g, r = gpu.step(t, return_hidden=True), ref.step(t)
+        pairs += [(f"step {t} logits", g[0], r[0]), (f"step {t} hidden", g[1], r[1]),
+                  (f"step {t} candidates", gpu_project(gpu, ids), ref.project_candidates(ids))]
+    for what, g, r in pairs:
+        print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
+        assert rel_l2(g, r) < 2e-3, what  # measured <= 3e-7
+
+
+def test_sdot_candidates_equal_full_logits():
+    a = small64(0, seed=10)
+    full, sel = NativeEngine(a, matmul="sdot"), NativeEngine(a, matmul="sdot")
+    ids = np.random.default_rng(52).permutation(512)[:142].astype(np.int32)
+    for t in (2, 51, 302):
+        e = full.step(t)
+        np.testing.assert_array_equal(sel.step_candidates(t, ids), e[ids])
+
+
+def test_sdot_released_geometry():
+    """27 layers of the released geometry (CQ4 / CQ2, groups of 128) on the int8 path."""
+    a = Archive(synthetic_released(seed=11, tokenizer_bytes=0))
+    gpu, ref = NativeEngine(a, matmul="sdot"), oracle.RefEngine(a, sdot=True)
+    lg, _ = gpu_prefill(gpu, TOKENS[:8], last_only=True)
+    rl, _ = ref.prefill(TOKENS[:8], last_only=True)
+    print(f"prefill rel {rel_l2(lg, rl):.2e}", flush=True)
+    assert rel_l2(lg, rl) < 1e-2
+    for t in (5, 77):
+        g, r = gpu.step(t), ref.step(t)[0]
+        print(f"step {t}: rel {rel_l2(g, r):.2e}", flush=True)
+        assert rel_l2(g, r) < 1e-2
+
+
 def test_engine_errors():
     e = NativeEngine(small())
     with pytest.raises(ValueError, match="within the vocabulary"):
