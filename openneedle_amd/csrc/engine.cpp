@@ -36,6 +36,16 @@ struct TensorDescC {
     const float *data;
     int rows, cols;
 };
+// needle2/csrc/engine.cpp:326-338: a compiled grammar as the decode loop reads it.
+struct DfaC {
+    int num_states, initial_state, eos_id, stop_id, tool_start_id, tool_end_id;
+    const int *state_types;           // 0 open, 1 exact candidates, 4 terminal
+    const int *fallback_next_states;  // -1: stay
+    const int *candidate_offsets;     // [num_states + 1]
+    const int *candidate_tokens;
+    const int *next_states;
+};
+
 struct EngineConfigC {
     int vocab, dim, heads, kvheads, layers, head_dim, max_seq, hada, lanes, window;
     int slots, subdim, tables, taps, dilation, num_orders, orders[4], num_sites, sites[4];
@@ -294,7 +304,28 @@ struct GpuEngine {
     void step(int token, float *logits_out, float *hidden_out);
     void prefill(const int *tokens, int num_tokens, bool last_only, float *logits_out, float *hidden_out);
     void project_candidates(const int *candidates, int count, float *out);
-    size_t kv_storage_bytes() const { return kv8.n + kv32.n * sizeof(float) + kvs.n * sizeof(float); }
+    // engine.cpp:410-419: the KV cache plus a cached prefix snapshot
+    size_t kv_storage_bytes() const {
+        return kv8.n + kv32.n * sizeof(float) + kvs.n * sizeof(float) + snap.k8.n + snap.k32.n * sizeof(float) +
+               snap.ks.n * sizeof(float);
+    }
+    // engine.cpp:450-494: the prefix's KV slots, token history and engram ring
+    struct Snapshot {
+        bool valid = false, int8 = false;
+        int position = 0;
+        std::vector<int> history;
+        DevBuf<float> k32, ks, ring;  // rows (layer, K | V, kv head) of prefix slots
+        DevBuf<int8_t> k8;
+    } snap;
+    void cache_prefix();
+    int reset_to_prefix();
+    void import_state(int pos, int pinned, const int *ids, const int *positions, int count, const float *k,
+                      const float *v);
+    int decode_loop(int first_token, int max_new_tokens, const DfaC *dfa, int *out, int *generated);
+    void upload_tokens(int tokens);
+    void run_engrams(int tokens);
+    // copies `prefix` slots of every (layer, K | V, kv head) row between the cache and the snapshot
+    void copy_prefix_slots(bool to_snapshot);
 };
 
 GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count, int activation_bits)
@@ -532,6 +563,11 @@ void GpuEngine::set_sdot() {
 
 void GpuEngine::reset(int prefix_len) {
     ND_CHECK(prefix_len >= 0 && prefix_len <= c.max_seq, "prefix length outside [0, max_seq]");
+    snap.valid = false;
+    snap.k32.release();
+    snap.k8.release();
+    snap.ks.release();
+    snap.ring.release();
     position = 0;
     prefix = prefix_len;
     std::fill(history.begin(), history.end(), 0);
@@ -571,6 +607,213 @@ void GpuEngine::reset(int prefix_len) {
     b.slots = slots.p;
     if (c.num_sites) ND_HIP(hipMemsetAsync(b.engring, 0, size_t(c.num_sites) * engring * c.dim * sizeof(float), stream));
     ND_HIP(hipStreamSynchronize(stream));
+}
+
+void GpuEngine::copy_prefix_slots(bool to_snapshot) {
+    const size_t rows = size_t(c.layers) * 2 * c.kvheads, HD = c.head_dim, P = prefix;
+    auto copy = [&](void *cache, void *saved, size_t elem, size_t per_slot) {
+        const size_t cache_pitch = size_t(capacity) * per_slot * elem, saved_pitch = P * per_slot * elem;
+        if (to_snapshot)
+            ND_HIP(hipMemcpy2DAsync(saved, saved_pitch, cache, cache_pitch, saved_pitch, rows, hipMemcpyDeviceToDevice,
+                                    stream));
+        else
+            ND_HIP(hipMemcpy2DAsync(cache, cache_pitch, saved, saved_pitch, saved_pitch, rows, hipMemcpyDeviceToDevice,
+                                    stream));
+    };
+    if (int8_kv) {
+        copy(kv8.p, snap.k8.p, 1, HD);
+        copy(kvs.p, snap.ks.p, sizeof(float), 1);
+    } else {
+        copy(kv32.p, snap.k32.p, sizeof(float), HD);
+    }
+    const size_t ring_floats = size_t(c.num_sites) * engring * c.dim;
+    if (ring_floats) {
+        if (to_snapshot)
+            ND_HIP(hipMemcpyAsync(snap.ring.p, b.engring, ring_floats * sizeof(float), hipMemcpyDeviceToDevice, stream));
+        else
+            ND_HIP(hipMemcpyAsync(b.engring, snap.ring.p, ring_floats * sizeof(float), hipMemcpyDeviceToDevice, stream));
+    }
+    ND_HIP(hipStreamSynchronize(stream));
+}
+
+void GpuEngine::cache_prefix() {
+    if (position <= 0 || position != prefix) throw Error("prefix snapshot requires position == prefix_len > 0");
+    const size_t rows = size_t(c.layers) * 2 * c.kvheads;
+    snap.valid = false;
+    if (int8_kv) {
+        snap.k32.release();
+        snap.k8.reserve(rows * prefix * c.head_dim);
+        snap.ks.reserve(rows * prefix);
+    } else {
+        snap.k8.release();
+        snap.ks.release();
+        snap.k32.reserve(rows * prefix * c.head_dim);
+    }
+    snap.ring.reserve(std::max<size_t>(1, size_t(c.num_sites) * engring * c.dim));
+    copy_prefix_slots(true);
+    snap.history = history;
+    snap.position = position;
+    snap.int8 = int8_kv;
+    snap.valid = true;
+}
+
+int GpuEngine::reset_to_prefix() {
+    if (!snap.valid) throw Error("no cached prefix; call cache_prefix() after consuming the complete prefix");
+    const int cached = snap.position;
+    if (prefix != cached || snap.int8 != int8_kv || capacity != (c.window ? ring + cached : c.max_seq))
+        throw Error("cached prefix geometry no longer matches the current state");
+    copy_prefix_slots(false);
+    history = snap.history;
+    position = cached;
+    return position;
+}
+
+// engine.cpp:784-815: a state computed elsewhere (the torch prefill): position
+// `pos` after `pinned` prefix tokens, the token history from ids, fp32 K / V
+// rows [layers][count][kv heads * head_dim] for the cache slots of
+// positions[count] (stored as the step stores them, fp32 or int8), and the
+// engram ring recomputed for the last ring positions.
+void GpuEngine::import_state(int pos, int pinned, const int *ids, const int *positions, int count, const float *k,
+                             const float *v) {
+    ND_CHECK(pos >= 0 && count >= 0 && (!pos || ids) && (!count || (positions && k && v)), "import: invalid state");
+    reset(pinned);
+    for (int i = 0; i < pos; ++i) ND_CHECK(ids[i] >= 0 && ids[i] < c.vocab, "token outside vocabulary");
+    const int K = c.kvheads * c.head_dim;
+    for (int t = 0; t < count; ++t) ND_CHECK(positions[t] >= 0 && cache_slot(positions[t]) < capacity,
+                                             "import: position outside the cache");
+    for (int i = std::max(0, pos - history_cap); i < pos; ++i) history[i % history_cap] = ids[i];
+    if (count > 0) {
+        const size_t n = size_t(c.layers) * count * K;
+        DevBuf<float> dk, dv;
+        DevBuf<int> dslots;
+        dk.reserve(n);
+        dv.reserve(n);
+        dslots.reserve(count);
+        std::vector<int> hs(count);
+        for (int t = 0; t < count; ++t) hs[t] = cache_slot(positions[t]);
+        ND_HIP(hipMemcpyAsync(dk.p, k, n * sizeof(float), hipMemcpyHostToDevice, stream));
+        ND_HIP(hipMemcpyAsync(dv.p, v, n * sizeof(float), hipMemcpyHostToDevice, stream));
+        ND_HIP(hipMemcpyAsync(dslots.p, hs.data(), count * sizeof(int), hipMemcpyHostToDevice, stream));
+        for (int l = 0; l < c.layers; ++l)
+            launch_eng_kv_import(dk.p + size_t(l) * count * K, dv.p + size_t(l) * count * K, dslots.p, count, kv[l],
+                                 dims, stream);
+        ND_HIP(hipStreamSynchronize(stream));
+    }
+    // only raw engram values persist: recompute the ring rows of the last positions
+    const int first = std::max(0, pos - engring);
+    if (c.num_sites && first < pos) {
+        for (int p0 = first; p0 < pos; p0 += chunk) {
+            const int T = std::min(chunk, pos - p0);
+            position = p0;
+            for (int t = 0; t < T; ++t) set_token(t, ids[p0 + t]);
+            upload_tokens(T);
+            run_engrams(T);
+        }
+        ND_HIP(hipStreamSynchronize(stream));
+    }
+    position = pos;
+}
+
+// engine.cpp:1360-1497: greedy decoding from first_token until eos / stop,
+// max_new_tokens (the first token included) or a terminal grammar state; a
+// grammar state with exact candidates projects only those rows.
+int GpuEngine::decode_loop(int first_token, int max_new_tokens, const DfaC *dfa, int *out, int *generated) {
+    if (max_new_tokens <= 0) {
+        if (generated) *generated = 0;
+        return 0;
+    }
+    if (first_token < 0 || first_token >= c.vocab) throw Error("token outside vocabulary");
+    auto check_tokens = [&](const int *ids, int n) {
+        for (int i = 0; i < n; ++i)
+            if (ids[i] < 0 || ids[i] >= c.vocab) throw Error("candidate outside vocabulary");
+    };
+    if (dfa) {
+        if (dfa->num_states <= 0 || dfa->initial_state < 0 || dfa->initial_state >= dfa->num_states ||
+            !dfa->state_types || !dfa->fallback_next_states || !dfa->candidate_offsets)
+            throw Error("invalid DFA states");
+        for (int token : {dfa->eos_id, dfa->stop_id, dfa->tool_start_id, dfa->tool_end_id})
+            if (token < 0 || token >= c.vocab) throw Error("DFA token outside vocabulary");
+        if (dfa->candidate_offsets[0] != 0) throw Error("invalid DFA offsets");
+        for (int st8 = 0; st8 < dfa->num_states; ++st8) {
+            const int type = dfa->state_types[st8], fallback = dfa->fallback_next_states[st8];
+            const int begin = dfa->candidate_offsets[st8], end = dfa->candidate_offsets[st8 + 1];
+            if ((type != 0 && type != 1 && type != 4) || fallback < -1 || fallback >= dfa->num_states || begin < 0 ||
+                end < begin)
+                throw Error("invalid DFA state");
+            if (type == 1 && begin == end) throw Error("DFA state has no candidates");
+            if (end > begin) {
+                if (!dfa->candidate_tokens || !dfa->next_states) throw Error("missing DFA transitions");
+                check_tokens(dfa->candidate_tokens + begin, end - begin);
+            }
+            for (int i = begin; i < end; ++i)
+                if (dfa->next_states[i] < 0 || dfa->next_states[i] >= dfa->num_states)
+                    throw Error("invalid DFA transition");
+        }
+    }
+    const int eos = dfa ? dfa->eos_id : 1, stop = dfa ? dfa->stop_id : 5;
+    // the transition of `state` on `token`, or -1 when the state lists no such candidate
+    auto transition = [&](int state, int token) {
+        for (int i = dfa->candidate_offsets[state]; i < dfa->candidate_offsets[state + 1]; ++i)
+            if (dfa->candidate_tokens[i] == token) return dfa->next_states[i];
+        return -1;
+    };
+    auto argmax = [](const float *x, int n) {
+        int best = 0;
+        for (int i = 1; i < n; ++i)
+            if (x[i] > x[best]) best = i;
+        return best;
+    };
+    int count = 0;
+    out[count++] = first_token;
+    if (first_token == eos || first_token == stop) {
+        if (generated) *generated = count;
+        return 0;
+    }
+    int state = 0;
+    if (dfa) {
+        state = dfa->initial_state;
+        const int next = transition(state, first_token);
+        if (next >= 0) {
+            state = next;
+        } else {
+            if (dfa->state_types[state] != 0) throw Error("first token rejected by DFA");
+            if (dfa->fallback_next_states[state] >= 0) state = dfa->fallback_next_states[state];
+        }
+    }
+    std::vector<float> scores(c.vocab);
+    int token = first_token;
+    while (count < max_new_tokens) {
+        const int type = dfa ? dfa->state_types[state] : 0;
+        if (type == 4) break;
+        int next_token;
+        if (type == 0) {
+            step(token, scores.data(), nullptr);
+            next_token = argmax(scores.data(), c.vocab);
+            if (dfa) {
+                const int next = transition(state, next_token);
+                if (next >= 0) state = next;
+                else if (dfa->fallback_next_states[state] >= 0) state = dfa->fallback_next_states[state];
+            }
+        } else {
+            const int begin = dfa->candidate_offsets[state], n = dfa->candidate_offsets[state + 1] - begin;
+            const int *cands = dfa->candidate_tokens + begin;
+            int pick = 0;
+            if (n == 1) {
+                step(token, nullptr, nullptr);
+            } else {
+                step(token, nullptr, nullptr);
+                project_candidates(cands, n, scores.data());
+                pick = argmax(scores.data(), n);
+            }
+            next_token = cands[pick];
+            state = dfa->next_states[begin + pick];
+        }
+        out[count++] = next_token;
+        token = next_token;
+        if (next_token == eos || next_token == stop || (dfa && dfa->state_types[state] == 4)) break;
+    }
+    if (generated) *generated = count;
+    return 0;
 }
 
 // Token t of the next launch: its StepParams and row ids (engine.cpp:
@@ -621,26 +864,17 @@ void GpuEngine::set_token(int t, int token) {
     }
 }
 
-// The layers for the `tokens` tokens set by set_token (engine.cpp:968-1040 for
-// one token, 1056-1258 for a chunk), leaving each token's final normed hidden
-// state in zf. Tokens share nothing but the KV cache and the engram ring, which
-// every token of the chunk writes before any reads them.
-void GpuEngine::run(int tokens) {
-    const int D = c.dim, HD = c.head_dim, T = tokens;
+// The StepParams and row ids of the first T tokens, to the device.
+void GpuEngine::upload_tokens(int T) {
+    ND_HIP(hipMemcpyAsync(params.p, hparams.p, size_t(T) * sizeof(StepParams), hipMemcpyHostToDevice, stream));
+    ND_HIP(hipMemcpyAsync(ids.p, hids.p, ids.n * sizeof(int64_t), hipMemcpyHostToDevice, stream));
+}
+
+// Engram rows, their quantiser, key / value projections, the conv and the ring
+// for the T uploaded tokens (engine.cpp:755-781).
+void GpuEngine::run_engrams(int T) {
     hipStream_t s = stream;
-    ND_HIP(hipMemcpyAsync(params.p, hparams.p, size_t(T) * sizeof(StepParams), hipMemcpyHostToDevice, s));
-    ND_HIP(hipMemcpyAsync(ids.p, hids.p, ids.n * sizeof(int64_t), hipMemcpyHostToDevice, s));
     const StepParams *dp = params.p;
-
-    // embedding rows, lanes (engine.cpp:972-974)
-    const Mat &emb = mats[0];
-    if (emb.cq)
-        launch_cq_rows(emb.cq->geom(), emb.cq->codes.p, emb.cq->norms.p, ids.p, T, D, emb.cq->padded,
-                       row_scratch.p, embed_z.p, s);
-    else
-        launch_eng_dense_rows(emb.dense, D, ids.p, T, embed_z.p, s);
-    launch_eng_start(embed_z.p, b, dims, T, s);
-
     for (int site = 0; site < c.num_sites; ++site) {
         const int e0 = engram_base() + 4 * site;
         const Mat &tab = mats[e0];
@@ -654,6 +888,27 @@ void GpuEngine::run(int tokens) {
         engram_kv[site].run(s, T);
         launch_eng_engram_out(b, dptr[e0 + 3], dp, site, dims, T, s);
     }
+}
+
+// The layers for the `tokens` tokens set by set_token (engine.cpp:968-1040 for
+// one token, 1056-1258 for a chunk), leaving each token's final normed hidden
+// state in zf. Tokens share nothing but the KV cache and the engram ring, which
+// every token of the chunk writes before any reads them.
+void GpuEngine::run(int tokens) {
+    const int D = c.dim, HD = c.head_dim, T = tokens;
+    hipStream_t s = stream;
+    upload_tokens(T);
+    const StepParams *dp = params.p;
+
+    // embedding rows, lanes (engine.cpp:972-974)
+    const Mat &emb = mats[0];
+    if (emb.cq)
+        launch_cq_rows(emb.cq->geom(), emb.cq->codes.p, emb.cq->norms.p, ids.p, T, D, emb.cq->padded,
+                       row_scratch.p, embed_z.p, s);
+    else
+        launch_eng_dense_rows(emb.dense, D, ids.p, T, embed_z.p, s);
+    launch_eng_start(embed_z.p, b, dims, T, s);
+    run_engrams(T);
 
     const int G = c.heads / c.kvheads;
     int maxlen = 0;
@@ -883,14 +1138,23 @@ void needle2_engine_reset(void *p, int prefix) {
     }
 }
 
-int needle2_engine_cache_prefix(void *) {
-    engine_error = "prefix snapshots are not implemented by the GPU engine";
-    return -1;
+int needle2_engine_cache_prefix(void *p) {
+    try {
+        static_cast<GpuEngine *>(p)->cache_prefix();
+        return 0;
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
 }
 
-int needle2_engine_reset_to_prefix(void *) {
-    engine_error = "prefix snapshots are not implemented by the GPU engine";
-    return -1;
+int needle2_engine_reset_to_prefix(void *p) {
+    try {
+        return static_cast<GpuEngine *>(p)->reset_to_prefix();
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
 }
 
 int needle2_engine_step(void *p, int token, float *logits, float *hidden) {
@@ -939,14 +1203,26 @@ int needle2_engine_project_candidates(void *p, const int *candidates, int num_ca
     }
 }
 
-int needle2_engine_decode_loop(void *, int, int, const void *, int *, int *) {
-    engine_error = "the grammar-constrained decode loop is not implemented by the GPU engine";
-    return -1;
+int needle2_engine_decode_loop(void *p, int first_token, int max_new_tokens, const void *dfa, int *output_tokens,
+                               int *generated) {
+    try {
+        return static_cast<GpuEngine *>(p)->decode_loop(first_token, max_new_tokens, static_cast<const DfaC *>(dfa),
+                                                        output_tokens, generated);
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
 }
 
-int needle2_engine_import(void *, int, int, const int *, const int *, int, const float *, const float *) {
-    engine_error = "state import is not implemented by the GPU engine";
-    return -1;
+int needle2_engine_import(void *p, int position, int pinned, const int *ids, const int *positions, int count,
+                          const float *k, const float *v) {
+    try {
+        static_cast<GpuEngine *>(p)->import_state(position, pinned, ids, positions, count, k, v);
+        return 0;
+    } catch (const std::exception &e) {
+        engine_error = e.what();
+        return -1;
+    }
 }
 
 int needle2_engine_set_int8_kv(void *p, int enable) {

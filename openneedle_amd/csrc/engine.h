@@ -92,6 +92,9 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, hipStream_t s);
 void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s);
+// K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
+void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
+                          const EngineDims &d, hipStream_t s);
 void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
                      const EngineDims &d, int tokens, hipStream_t s);
 void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, int tokens, hipStream_t s);

@@ -502,6 +502,39 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     }
 }
 
+// Imported K / V rows [count][kvheads][head_dim] into cache slots[count] of
+// one layer, fp32 or through the step's int8 quantiser (engine.cpp:788-811):
+// one wave per (row, kv head).
+__global__ __launch_bounds__(64) void eng_kv_import_kernel(const float *__restrict__ k, const float *__restrict__ v,
+                                                           const int *__restrict__ slots, KvLayer kv, EngineDims d) {
+    const int t = blockIdx.x / d.KV, kh = blockIdx.x % d.KV, lane = threadIdx.x, HD = d.HD;
+    const float *kr = k + (static_cast<size_t>(t) * d.KV + kh) * HD, *vr = v + (static_cast<size_t>(t) * d.KV + kh) * HD;
+    const size_t row = static_cast<size_t>(kh) * d.capacity + slots[t];
+    if (kv.k32) {
+        for (int i = lane; i < HD; i += 64) {
+            kv.k32[row * HD + i] = kr[i];
+            kv.v32[row * HD + i] = vr[i];
+        }
+        return;
+    }
+    float mk = 0.0f, mv = 0.0f;
+    for (int i = lane; i < HD; i += 64) {
+        mk = fmaxf(mk, fabsf(kr[i]));
+        mv = fmaxf(mv, fabsf(vr[i]));
+    }
+    mk = wave_max(mk, lane);
+    mv = wave_max(mv, lane);
+    const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
+    if (lane == 0) {
+        kv.ks[row] = mk > 0 ? mk / 127.0f : 1.0f;
+        kv.vs[row] = mv > 0 ? mv / 127.0f : 1.0f;
+    }
+    for (int i = lane; i < HD; i += 64) {
+        kv.k8[row * HD + i] = static_cast<int8_t>(fmaxf(-127.0f, fminf(127.0f, rintf(kr[i] * ik))));
+        kv.v8[row * HD + i] = static_cast<int8_t>(fmaxf(-127.0f, fminf(127.0f, rintf(vr[i] * iv))));
+    }
+}
+
 // att *= sigmoid(gate); then the activation quantiser (engine.cpp:1023-1024).
 __global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, EngineDims d) {
     __shared__ float red[kEngThreads / 64];
@@ -688,6 +721,13 @@ void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLaye
         hipLaunchKernelGGL(eng_attn_fused_kernel<true>, dim3(d.KV, tokens), dim3(256), lds, s, b, ld, kv, p, d);
     else
         hipLaunchKernelGGL(eng_attn_fused_kernel<false>, dim3(d.KV, tokens), dim3(256), lds, s, b, ld, kv, p, d);
+    ND_HIP(hipGetLastError());
+}
+
+void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
+                          const EngineDims &d, hipStream_t s) {
+    if (count <= 0) return;
+    hipLaunchKernelGGL(eng_kv_import_kernel, dim3(count * d.KV), dim3(64), 0, s, k, v, slots, kv, d);
     ND_HIP(hipGetLastError());
 }
 

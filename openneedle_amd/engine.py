@@ -61,6 +61,14 @@ def engine_tensors(archive: Archive):
     return names
 
 
+class _DFAStateDesc(ct.Structure):
+    """needle2/native.py:291-305: a compiled grammar as needle2_engine_decode_loop reads it."""
+    _fields_ = [("num_states", ct.c_int), ("initial_state", ct.c_int), ("eos_id", ct.c_int), ("stop_id", ct.c_int),
+                ("tool_start_id", ct.c_int), ("tool_end_id", ct.c_int), ("state_types", ct.POINTER(ct.c_int)),
+                ("fallback_next_states", ct.POINTER(ct.c_int)), ("candidate_offsets", ct.POINTER(ct.c_int)),
+                ("candidate_tokens", ct.POINTER(ct.c_int)), ("next_states", ct.POINTER(ct.c_int))]
+
+
 class NativeEngine:
     """Entire token forward on the GPU; one independent unpadded sequence per instance (needle2/native.py:307)."""
 
@@ -119,6 +127,12 @@ class NativeEngine:
                  ct.c_int),
                 ("needle2_engine_project_candidates", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p], ct.c_int),
                 ("needle2_engine_set_int8_kv", [ct.c_void_p, ct.c_int], ct.c_int),
+                ("needle2_engine_cache_prefix", [ct.c_void_p], ct.c_int),
+                ("needle2_engine_decode_loop", [ct.c_void_p, ct.c_int, ct.c_int, ct.POINTER(_DFAStateDesc),
+                                                ct.POINTER(ct.c_int), ct.POINTER(ct.c_int)], ct.c_int),
+                ("needle2_engine_import", [ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_void_p, ct.c_int,
+                                           ct.c_void_p, ct.c_void_p], ct.c_int),
+                ("needle2_engine_reset_to_prefix", [ct.c_void_p], ct.c_int),
                 ("needle2_engine_set_sdot", [ct.c_void_p], ct.c_int),
                 ("needle2_engine_set_lookup", [ct.c_void_p, ct.c_int], None),
                 ("needle2_engine_kv_storage_bytes", [ct.c_void_p], ct.c_size_t),
@@ -159,6 +173,22 @@ class NativeEngine:
         self._lib.needle2_engine_reset(self._handle, int(prefix_len))
         self.position = 0
         self.prefix_len = int(prefix_len)
+
+    def cache_prefix(self):
+        """Snapshot the complete pinned prefix (needle2/native.py:447-459): its KV slots, the token history
+        and the engram ring, kept in device memory. Requires ``position == prefix_len > 0``; ``reset()``
+        discards the snapshot."""
+        if self.position <= 0 or self.position != self.prefix_len:
+            raise ValueError("prefix snapshot requires position == prefix_len > 0")
+        if self._lib.needle2_engine_cache_prefix(self._handle):
+            raise RuntimeError(self._lib.needle2_engine_error().decode())
+
+    def reset_to_prefix(self):
+        """Restore the snapshot without a forward pass (needle2/native.py:461-470)."""
+        position = self._lib.needle2_engine_reset_to_prefix(self._handle)
+        if position < 0:
+            raise RuntimeError(self._lib.needle2_engine_error().decode())
+        self.position = self.prefix_len = position
 
     def step(self, token_id: int, *, return_hidden: bool = False, compute_logits: bool = True, candidates=None):
         if candidates is not None:
@@ -219,6 +249,46 @@ class NativeEngine:
             raise RuntimeError(self._lib.needle2_engine_error().decode())
         self.position += int(ids.size)
         return logits
+
+    def decode(self, first_token: int, max_new_tokens: int = 128, grammar_dfa=None) -> list[int]:
+        """Greedy decoding in the library until eos, max_new_tokens or a terminal grammar state
+        (needle2/native.py:622-663); ``grammar_dfa`` is an object with a ``_desc`` (_DFAStateDesc) and a
+        ``validate(vocab_size)`` method, as the reference's NativeGrammarDFA."""
+        if not isinstance(max_new_tokens, (int, np.integer)) or not 0 <= max_new_tokens <= np.iinfo(np.int32).max:
+            raise ValueError("max_new_tokens must be a nonnegative int32")
+        if not isinstance(first_token, (int, np.integer)) or not 0 <= first_token < self.metadata["vocab_size"]:
+            raise ValueError("first_token outside vocabulary")
+        if grammar_dfa is not None:
+            grammar_dfa.validate(self.metadata["vocab_size"])
+        if max_new_tokens == 0:
+            return []
+        if not self.metadata["kv_window"]:
+            max_new_tokens = min(max_new_tokens, self.metadata["max_seq_len"] - self.position + 1)
+        output = (ct.c_int * (max_new_tokens + 1))()
+        count = ct.c_int(0)
+        desc = ct.byref(grammar_dfa._desc) if grammar_dfa is not None else None
+        if self._lib.needle2_engine_decode_loop(self._handle, int(first_token), int(max_new_tokens), desc, output,
+                                                ct.byref(count)):
+            raise RuntimeError(self._lib.needle2_engine_error().decode())
+        self.position += count.value - 1
+        return [output[i] for i in range(count.value)]
+
+    def import_state(self, token_ids, positions, keys, values):
+        """needle2_engine_import (engine.cpp:784-815): the state after ``token_ids`` with the KV rows of
+        ``positions`` (keys / values [layers][len(positions)][kv_heads][head_dim] fp32), as the reference's
+        torch prefill hands it over (needle2/native.py:558-590)."""
+        ids = np.ascontiguousarray(token_ids, np.int32)
+        pos = np.ascontiguousarray(positions, np.int32)
+        k = np.ascontiguousarray(keys, np.float32)
+        v = np.ascontiguousarray(values, np.float32)
+        m = self.metadata
+        shape = (m["num_layers"], pos.size, m["num_kv_heads"], m["head_dim"])
+        if k.shape != shape or v.shape != shape:
+            raise ValueError(f"keys and values must have shape {shape}")
+        if self._lib.needle2_engine_import(self._handle, ids.size, self.prefix_len, ids.ctypes.data, pos.ctypes.data,
+                                           pos.size, k.ctypes.data, v.ctypes.data):
+            raise RuntimeError(self._lib.needle2_engine_error().decode())
+        self.position = int(ids.size)
 
     def generate(self, token_ids, max_new_tokens: int = 32, eos_token_id: int | None = None, prefix_len: int = 0):
         """Greedy continuation of a prompt (needle2/native.py:596-616, native prefill)."""

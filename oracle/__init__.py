@@ -364,6 +364,12 @@ class RefEngine:
                 ("needle2_engine_prefill", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p,
                                             ct.c_void_p], ct.c_int),
                 ("needle2_engine_project_candidates", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p], ct.c_int),
+                ("needle2_engine_cache_prefix", [ct.c_void_p], ct.c_int),
+                ("needle2_engine_decode_loop", [ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_void_p,
+                                                ct.c_void_p], ct.c_int),
+                ("needle2_engine_import", [ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_void_p, ct.c_int,
+                                           ct.c_void_p, ct.c_void_p], ct.c_int),
+                ("needle2_engine_reset_to_prefix", [ct.c_void_p], ct.c_int),
                 ("needle2_engine_error", [], ct.c_char_p)):
             f = getattr(L, name)
             f.argtypes, f.restype = args, res

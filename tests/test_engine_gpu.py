@@ -224,14 +224,127 @@ def test_sdot_released_geometry():
         assert rel_l2(g, r) < 1e-2
 
 
+@pytest.mark.parametrize("kv", ["fp32", "int8"])
+def test_prefix_snapshot_restore(kv):
+    """needle2's own scenario (tests/test_runtime_regressions.py:40-56) against the reference Engine: a pinned
+    prefix of 9 tokens, snapshot, a long continuation through the window ring, restore, another continuation;
+    both engines restore the same state, and restoring twice gives the same logits bit for bit."""
+    a = small(8, seed=12)
+    int8 = kv == "int8"
+    gpu, ref = NativeEngine(a, kv_cache=kv), oracle.RefEngine(a, 0, int8)
+    ids = [int(t) for t in np.random.default_rng(23).integers(2, 500, 60)]
+    gpu.reset(9)
+    ref.reset(9)
+    gpu_prefill(gpu, ids[:9])
+    ref.prefill(ids[:9])
+    gpu.cache_prefix()
+    assert ref.L.needle2_engine_cache_prefix(ref.h) == 0
+    gpu_prefill(gpu, ids[9:])
+    ref.prefill(ids[9:])
+    firsts = []
+    for _ in range(2):
+        gpu.reset_to_prefix()
+        assert gpu.position == gpu.prefix_len == 9
+        assert ref.L.needle2_engine_reset_to_prefix(ref.h) == 9
+        lg, _ = gpu_prefill(gpu, ids[20:35])
+        rl, _ = ref.prefill(ids[20:35])
+        firsts.append(lg)
+        if int8:
+            assert rel_l2(lg, rl) < 1e-3
+        else:
+            np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL)
+    np.testing.assert_array_equal(firsts[0], firsts[1])
+    # reset() discards the snapshot (needle2/native.py:447-452)
+    gpu.reset(9)
+    with pytest.raises(RuntimeError, match="no cached prefix"):
+        gpu.reset_to_prefix()
+    with pytest.raises(ValueError, match="prefix snapshot requires"):
+        gpu.cache_prefix()
+
+
+def _dfa():
+    """Four states: open (7 -> 1), exact candidates {20, 30, 40, 50} (-> 2, 2, 0, 2), exact {60} (-> 3),
+    terminal."""
+    import ctypes as ct
+    from openneedle_amd.engine import _DFAStateDesc
+    arrays = dict(types=[0, 1, 1, 4], fallback=[-1, -1, -1, -1], offsets=[0, 1, 5, 6, 6],
+                  tokens=[7, 20, 30, 40, 50, 60], nexts=[1, 2, 2, 0, 2, 3])
+    keep = {k: (ct.c_int * len(v))(*v) for k, v in arrays.items()}
+    desc = _DFAStateDesc(4, 0, 1, 5, 10, 11, keep["types"], keep["fallback"], keep["offsets"], keep["tokens"],
+                         keep["nexts"])
+
+    class Grammar:
+        _desc = desc
+        _keep = keep
+
+        def validate(self, vocab):
+            assert vocab > 60
+    return Grammar()
+
+
+@pytest.mark.parametrize("grammar", [False, True])
+def test_decode_loop_matches_reference(grammar):
+    """needle2_engine_decode_loop against the reference's (engine.cpp:1360-1497) after the same prompt: the same
+    tokens, unconstrained or through a grammar with exact-candidate states."""
+    import ctypes as ct
+    a = small(0, seed=13)
+    gpu, ref = NativeEngine(a), oracle.RefEngine(a)
+    gpu_prefill(gpu, PROMPT[:10])
+    ref.prefill(PROMPT[:10])
+    g = _dfa() if grammar else None
+    first = 7 if grammar else 42
+    out = gpu.decode(first, 14, g)
+    buf, count = (ct.c_int * 15)(), ct.c_int(0)
+    assert ref.L.needle2_engine_decode_loop(ref.h, first, 14, ct.addressof(g._desc) if g else None,
+                                            ct.addressof(buf), ct.addressof(count)) == 0
+    print(out, flush=True)
+    assert out == list(buf[:count.value])
+    if grammar:
+        assert all(t in (7, 20, 30, 40, 50, 60) for t in out[:2])
+    # the state after decoding is the reference's too
+    np.testing.assert_allclose(gpu.step(3), ref.step(3)[0], atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("window,prefix", [(0, 0), (8, 3)])
+@pytest.mark.parametrize("kv", ["fp32", "int8"])
+def test_import_matches_reference(window, prefix, kv):
+    """needle2_engine_import (engine.cpp:784-815): token history plus K / V rows of the cached positions (the
+    pinned prefix and the window for a window model), then steps, against the reference's import."""
+    a = small(window, seed=14)
+    m = a.metadata
+    rng = np.random.default_rng(64)
+    ids = [int(t) for t in rng.integers(2, 500, 20)]
+    positions = list(range(20)) if not window else list(range(prefix)) + list(range(20 - window, 20))
+    shape = (m["num_layers"], len(positions), m["num_kv_heads"], m["head_dim"])
+    k = rng.standard_normal(shape).astype(np.float32)
+    v = rng.standard_normal(shape).astype(np.float32)
+    gpu, ref = NativeEngine(a, kv_cache=kv), oracle.RefEngine(a, 0, kv == "int8")
+    gpu.reset(prefix)
+    gpu.import_state(ids, positions, k, v)
+    idc, pc = np.asarray(ids, np.int32), np.asarray(positions, np.int32)
+    assert ref.L.needle2_engine_import(ref.h, len(ids), prefix, idc.ctypes.data, pc.ctypes.data, len(positions),
+                                       k.ctypes.data, v.ctypes.data) == 0
+    assert gpu.position == 20
+    for t in (5, 400, 33):
+        g, r = gpu.step(t, return_hidden=True), ref.step(t)
+        print(f"step {t}: rel {rel_l2(g[0], r[0]):.2e}", flush=True)
+        if kv == "int8":
+            assert rel_l2(g[0], r[0]) < 1e-3 and rel_l2(g[1], r[1]) < 1e-3
+        else:
+            np.testing.assert_allclose(g[0], r[0], atol=ATOL, rtol=RTOL)
+            np.testing.assert_allclose(g[1], r[1], atol=ATOL, rtol=RTOL)
+
+
 def test_engine_errors():
     e = NativeEngine(small())
     with pytest.raises(ValueError, match="within the vocabulary"):
         e.step(512)
     with pytest.raises(ValueError, match="candidate outside vocabulary"):
         e.step_candidates(1, [0, 512])
-    with pytest.raises(RuntimeError, match="SDOT requires"):
-        NativeEngine(small(), matmul="sdot")
+    with pytest.raises(ValueError, match="activation"):  # needle2/native.py: SDOT takes fp32 activations
+        NativeEngine(small(), matmul="sdot", activation_bits=8)
+    with pytest.raises(RuntimeError, match="no cached prefix"):
+        e.reset_to_prefix()
     for _ in range(64):
         e.step(1, compute_logits=False)
     with pytest.raises(RuntimeError, match="maximum context reached"):
