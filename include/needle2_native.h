@@ -63,10 +63,14 @@ void needle2_sdot_linear(void *handle, const float *x, float *y, int batch, int 
  * config is the reference's EngineConfig (engine.cpp:15-19), tensors its
  * TensorDesc table (engine.cpp:14) with CQ entries pointing at this library's
  * CQ handles (borrowed) and dense entries at host fp32 data (copied at
- * creation). threads is ignored. Failures return NULL / -1 with the message
- * in needle2_engine_error(). needle2_engine_set_sdot fails as the reference
- * does on a host without DotProd; cache_prefix, reset_to_prefix, import and
- * decode_loop are not implemented (-1). */
+ * creation); dfa is the reference's DFAStateDesc (engine.cpp:326-338).
+ * threads and set_lookup's mode are ignored (one GPU path per matrix).
+ * set_sdot switches the 2/4-bit CQ matrices of groups 64..131072 to the int8
+ * path on any host (the reference needs an ARM64 CPU with DotProd); prefill
+ * runs chunks of 32 tokens (or the window) through the same per-token
+ * arithmetic. For a window model the device KV ring holds chunk - 1 slots more
+ * than the reference's (window + prefix), and kv_storage_bytes counts them.
+ * Failures return NULL / -1 with the message in needle2_engine_error(). */
 const char *needle2_engine_error(void);
 void *needle2_engine_create(const void *config, const void *tensors, int count, int threads, int activation_bits);
 void needle2_engine_destroy(void *engine);
