@@ -709,12 +709,12 @@ def main():
         for kv, (tps, tok_ms) in bench_engine().items():
             extra[f"engine_{ENGINE_LABEL[kv]}_tokens_per_s"] = round(tps, 1)
             extra[f"engine_{ENGINE_LABEL[kv]}_token_us"] = dist_us(tok_ms)
-            log(f"engine {kv} KV: {tps:.0f} tokens/s")
+            log(f"engine {ENGINE_LABEL[kv]}: {tps:.0f} tokens/s")
         log(f"engine prefill: NativeEngine.prefill, released geometry, {PROMPT_TOKENS}-token prompt")
         for kv, (tps, pr_ms) in bench_engine_prefill().items():
             extra[f"engine_prefill_{ENGINE_LABEL[kv]}_tokens_per_s"] = round(tps, 1)
             extra[f"engine_prefill_{ENGINE_LABEL[kv]}_prompt_us"] = dist_us(pr_ms)
-            log(f"engine prefill {kv} KV: {tps:.0f} tokens/s")
+            log(f"engine prefill {ENGINE_LABEL[kv]}: {tps:.0f} tokens/s")
 
         ms_u, nb = bench_archive_upload()
         extra["archive_upload_ms"] = round(ms_u, 2)

@@ -408,9 +408,7 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void cq_gemv_kernel(CqJob job0, c
     CqJob J = job0;
     if (njobs > 0) {
         const ND_CONST CqJob *cj = (const ND_CONST CqJob *)(jobs);
-        int j = 0;
-        for (int k = 1; k < njobs; ++k)
-            if (cj[k].block_begin <= blk) j = k;
+        const int j = find_job(cj, njobs, blk);
         J.codes = cj[j].codes;
         J.norms = cj[j].norms;
         J.act = cj[j].act;
@@ -779,9 +777,7 @@ __global__ __launch_bounds__(kSplitThreads, 4) void cq_gemv_split_kernel(CqJob j
     CqJob J = job0;
     if (njobs > 0) {
         const ND_CONST CqJob *cj = (const ND_CONST CqJob *)(jobs);
-        int j = 0;
-        for (int k = 1; k < njobs; ++k)
-            if (cj[k].block_begin <= blk) j = k;
+        const int j = find_job(cj, njobs, blk);
         J.codes = cj[j].codes;
         J.norms = cj[j].norms;
         J.act = cj[j].act;
@@ -1047,9 +1043,7 @@ __global__ __launch_bounds__(kQuadThreads) __attribute__((amdgpu_waves_per_eu(8,
     CqJob J = job0;
     if (njobs > 0) {
         const ND_CONST CqJob *cj = (const ND_CONST CqJob *)(jobs);
-        int j = 0;
-        for (int k = 1; k < njobs; ++k)
-            if (cj[k].block_begin <= blk) j = k;
+        const int j = find_job(cj, njobs, blk);
         J.codes = cj[j].codes;
         J.norms = cj[j].norms;
         J.act = cj[j].act;

@@ -328,9 +328,7 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
     SdotJob J = job0;
     if (njobs > 0) {
         const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
-        int j = 0;
-        for (int k = 1; k < njobs; ++k)
-            if (cj[k].block_begin <= blk) j = k;
+        const int j = find_job(cj, njobs, blk);
         J.codes = cj[j].codes;
         J.norms = cj[j].norms;
         J.q = cj[j].q;
@@ -532,9 +530,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_mfma_kernel(SdotJob job0, 
     SdotJob J0 = job0;
     if (njobs > 0) {
         const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
-        int j = 0;
-        for (int k = 1; k < njobs; ++k)
-            if (cj[k].block_begin <= blk) j = k;
+        const int j = find_job(cj, njobs, blk);
         J0.codes = cj[j].codes;
         J0.norms = cj[j].norms;
         J0.q = cj[j].q;
@@ -696,9 +692,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_row_kernel(SdotJob job0, c
     SdotJob J = job0;
     if (njobs > 0) {
         const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
-        int j = 0;
-        for (int k = 1; k < njobs; ++k)
-            if (cj[k].block_begin <= blk) j = k;
+        const int j = find_job(cj, njobs, blk);
         J.codes = cj[j].codes;
         J.norms = cj[j].norms;
         J.q = cj[j].q;
@@ -804,9 +798,7 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
     SdotJob J0 = job0;
     if (njobs > 0) {
         const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
-        int j = 0;
-        for (int k = 1; k < njobs; ++k)
-            if (cj[k].block_begin <= blk) j = k;
+        const int j = find_job(cj, njobs, blk);
         J0.codes = cj[j].codes;
         J0.norms = cj[j].norms;
         J0.q = cj[j].q;

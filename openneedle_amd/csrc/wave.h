@@ -71,4 +71,19 @@ __device__ __forceinline__ float wave_sum(float v, int t) {
     return v + butterfly_partner<32>(v, t);
 }
 
+// Index of the job whose workgroup range holds `blk` in a job table sorted by
+// block_begin (jobs[0] begins at 0): the last j with jobs[j].block_begin <=
+// blk, by binary search, so a table of one job per (token, matrix piece)
+// costs a few scalar loads per workgroup rather than one per job.
+template <class P>
+__device__ __forceinline__ int find_job(P jobs, int njobs, int blk) {
+    int lo = 0, hi = njobs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (jobs[mid].block_begin <= blk) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
 }  // namespace nd
