@@ -60,7 +60,7 @@ def settle(run, seconds=SETTLE_S):
     Under sustained load the GPU's power management moves its clocks for the first ~150 ms (on MI355X the
     16 x CQ4 8192x8192 GEMV runs ~110 us for a few steps, ~147 us some 10 ms in, and settles at ~111 us after
     ~150 ms); the timed steps should see the steady state a serving loop runs in, not that ramp."""
-    from openneedle_amd.native import synchronize
+    from openneedle_amd.device import synchronize
     start = time.perf_counter()
     while time.perf_counter() - start < seconds:
         for _ in range(20):
@@ -81,7 +81,8 @@ class Stack:
     """`rot` rotations of the same `count` matrices (distinct device copies) with plans."""
 
     def __init__(self, packed, norms, cb, bits, group, batch, rot, int8=False):
-        from openneedle_amd.native import DeviceArray, NativeCQ, Plan
+        from openneedle_amd.cq import CQMatrix, Plan
+        from openneedle_amd.device import DeviceArray
         count, rows, _ = packed.shape
         cols = norms.shape[2] * group
         rng = np.random.default_rng(7)
@@ -89,13 +90,13 @@ class Stack:
         self.y = [DeviceArray(batch * rows * 4) for _ in range(count)]
         self.mats, self.plans = [], []
         for _ in range(rot):
-            mats = [NativeCQ(packed[i], norms[i], (rows, cols), bits, group, cb) for i in range(count)]
+            mats = [CQMatrix(packed[i], norms[i], (rows, cols), bits, group, cb) for i in range(count)]
             self.mats.append(mats)
             self.plans.append(Plan(mats, [d.ptr for d in self.x], [d.ptr for d in self.y], batch=batch, int8=int8))
         self.bytes_per_step = packed.nbytes + norms.nbytes
 
     def run(self, steps, warmup, stream):
-        from openneedle_amd.native import Event, synchronize
+        from openneedle_amd.device import Event, synchronize
         turn = iter(range(1 << 62))
         settle(lambda: self.plans[next(turn) % len(self.plans)].run(stream))
         for i in range(warmup):
@@ -130,7 +131,8 @@ ATTN_BYTES = 2 * 64 * 2048 * 8 * 64 + 2 * 64 * 2048 * 8 * 4 + 2 * 64 * 8 * 64 * 
 def bench_attention(steps, warmup, stream, splits=0):
     """64 sequences x 8 heads (8 kv heads) x head_dim 64, 2048 cached slots: one
     decode-attention launch per step over a cache filled through the store kernel."""
-    from openneedle_amd.native import DeviceArray, Event, KVCache, synchronize
+    from openneedle_amd.device import DeviceArray, Event, synchronize
+    from openneedle_amd.kv import KVCache
     seqs, cap, kvh, hd, heads = 64, 2048, 8, 64, 8
     rng = np.random.default_rng(5)
     caches = []
@@ -178,10 +180,11 @@ def bench_prefill(steps, warmup, stream):
     event pair around all steps). The GEMM's own time comes from event pairs
     around PREFILL_REPEAT back-to-back GEMM launches, so that the device, not
     the host's launch rate, sets the pace."""
-    from openneedle_amd.native import DeviceArray, Event, NativeCQ, synchronize
+    from openneedle_amd.cq import CQMatrix
+    from openneedle_amd.device import DeviceArray, Event, synchronize
     rng = np.random.default_rng(17)
     packed, norms, cb = random_cq(rng, 1, 8192, 2048, 4, 32)
-    q = NativeCQ(packed[0], norms[0], (8192, 2048), 4, 32, cb)
+    q = CQMatrix(packed[0], norms[0], (8192, 2048), 4, 32, cb)
     x = DeviceArray.from_host(rng.normal(size=(512, 2048)).astype(np.float32))
     y = DeviceArray(512 * 8192 * 4)
     settle(lambda: q.gemm_device(x.ptr, y.ptr, 512, stream))
@@ -201,60 +204,70 @@ def bench_prefill(steps, warmup, stream):
     return t0.elapsed_ms(t1) / steps, [a.elapsed_ms(b) / PREFILL_REPEAT for a, b in ev]
 
 
-def bench_decode_layer(steps, warmup, stream, seqs=64):
+def bench_decode_layer(steps, warmup, stream, seqs=64, graph=True):
     """One decoder layer for `seqs` sequences at context 2048 (hidden 512, 8 heads = 8 kv heads, head_dim 64,
     MLP 2048): int8-path CQ4 g32 projections Q|K|V (one plan), KV store of the new token, decode attention
     over 2048 int8 slots, O, MLP up and down. Elementwise glue (norms, RoPE, gates, activation) is omitted.
-    Returns (eager ms per step, ms per step replaying the step captured in a HIP graph)."""
-    from openneedle_amd.native import DeviceArray, Event, Graph, KVCache, NativeCQ, Plan, synchronize
+    Returns (eager ms per step, ms per step replaying the step captured in a HIP graph, or None without
+    `graph`). Everything is released in a fixed order at the end: the graph first, then the plans and the
+    cache, then the buffers and matrices they read."""
+    from openneedle_amd.cq import CQMatrix, Plan
+    from openneedle_amd.device import DeviceArray, Event, Graph, Teardown, synchronize
+    from openneedle_amd.kv import KVCache
     cap, kvh, hd, heads, hidden, mlp = 2048, 8, 64, 8, 512, 2048
     rng = np.random.default_rng(23)
+    with Teardown() as td:
+        def mat(rows, cols):
+            packed, norms, cb = random_cq(rng, 1, rows, cols, 4, 32)
+            return td.add(CQMatrix(packed[0], norms[0], (rows, cols), 4, 32, cb))
 
-    def mat(rows, cols):
-        packed, norms, cb = random_cq(rng, 1, rows, cols, 4, 32)
-        return NativeCQ(packed[0], norms[0], (rows, cols), 4, 32, cb)
+        wq, wk, wv, wo = (mat(hidden, hidden) for _ in range(4))
+        wu, wd = mat(mlp, hidden), mat(hidden, mlp)
+        buf = {n: td.add(DeviceArray(seqs * w * 4)) for n, w in
+               (("x", hidden), ("q", hidden), ("k", hidden), ("v", hidden), ("a", hidden), ("o", hidden),
+                ("u", mlp), ("d", hidden))}
+        buf["x"].upload(rng.normal(size=(seqs, hidden)).astype(np.float32))
 
-    wq, wk, wv, wo = (mat(hidden, hidden) for _ in range(4))
-    wu, wd = mat(mlp, hidden), mat(hidden, mlp)
-    buf = {n: DeviceArray(seqs * w * 4) for n, w in
-           (("x", hidden), ("q", hidden), ("k", hidden), ("v", hidden), ("a", hidden), ("o", hidden),
-            ("u", mlp), ("d", hidden))}
-    buf["x"].upload(rng.normal(size=(seqs, hidden)).astype(np.float32))
-    p = lambda ms, xs, ys: Plan(ms, [buf[n].ptr for n in xs], [buf[n].ptr for n in ys], batch=seqs, int8=True)  # noqa: E731
-    plans = [p([wq, wk, wv], "xxx", "qkv"), p([wo], "a", "o"), p([wu], "o", "u"), p([wd], "u", "d")]
-    kv = KVCache(1, cap, kvh, hd, seqs)
-    for c0 in range(0, cap - 1, 512):
-        n = min(512, cap - 1 - c0)
-        k = DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32))
-        v = DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32))
-        kv.store(0, k.ptr, v.ptr, n, first_slot=c0, stream=stream)
-        stream.synchronize()
-    first = DeviceArray.from_host(np.full(seqs, cap - 1, np.int32))  # the new token's slot, on the device
+        def plan(ms, xs, ys):
+            return td.add(Plan(ms, [buf[n] for n in xs], [buf[n] for n in ys], batch=seqs, int8=True))
 
-    def step():
-        plans[0].run(stream)
-        kv.store_device(0, buf["k"].ptr, buf["v"].ptr, 1, first.ptr, stream=stream)
-        kv.attention(0, buf["q"].ptr, buf["a"].ptr, heads, cap, stream=stream)
-        for pl in plans[1:]:
-            pl.run(stream)
+        plans = [plan([wq, wk, wv], "xxx", "qkv"), plan([wo], "a", "o"), plan([wu], "o", "u"), plan([wd], "u", "d")]
+        kv = td.add(KVCache(1, cap, kvh, hd, seqs))
+        for c0 in range(0, cap - 1, 512):
+            n = min(512, cap - 1 - c0)
+            with DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32)) as k, \
+                    DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32)) as v:
+                kv.store(0, k, v, n, first_slot=c0, stream=stream)
+                stream.synchronize()
+        first = td.add(DeviceArray.from_host(np.full(seqs, cap - 1, np.int32)))  # the new token's slot
 
-    def timed(fn):
-        settle(fn)
-        for _ in range(warmup):
-            fn()
-        synchronize()
-        t0, t1 = Event(), Event()
-        t0.record(stream)
-        for _ in range(steps):
-            fn()
-        t1.record(stream)
-        synchronize()
-        return t0.elapsed_ms(t1) / steps
+        def step():
+            plans[0].run(stream)
+            kv.store_device(0, buf["k"], buf["v"], 1, first, stream=stream)
+            kv.attention(0, buf["q"], buf["a"], heads, cap, stream=stream)
+            for pl in plans[1:]:
+                pl.run(stream)
 
-    eager = timed(step)
-    with Graph.capture(stream) as g:
-        step()
-    graphed = timed(lambda: g.launch(stream))
+        def timed(fn):
+            settle(fn)
+            for _ in range(warmup):
+                fn()
+            synchronize()
+            with Event() as t0, Event() as t1:
+                t0.record(stream)
+                for _ in range(steps):
+                    fn()
+                t1.record(stream)
+                synchronize()
+                return t0.elapsed_ms(t1) / steps
+
+        eager = timed(step)
+        graphed = None
+        if graph:
+            with Graph.capture(stream) as g:
+                step()
+            td.add(g)  # registered last: released first
+            graphed = timed(lambda: g.launch(stream))
     return eager, graphed
 
 
@@ -264,10 +277,11 @@ def bench_small(steps, warmup, stream):
     Returns per-call millisecond lists: the device step (FWHT pre-pass + GEMV, one event pair per step), the GEMV
     kernel alone, and the host-pointer ABI call (needle2_cq_linear: copy x in, transform + GEMV, copy y out, wait),
     timed on the host around the ctypes call."""
-    from openneedle_amd.native import DeviceArray, Event, NativeCQ, Plan, synchronize
+    from openneedle_amd.cq import CQMatrix, Plan
+    from openneedle_amd.device import DeviceArray, Event, synchronize
     rng = np.random.default_rng(20261202)
     packed, norms, cb = random_cq(rng, 1, 2048, 512, 4, 32)
-    q = NativeCQ(packed[0], norms[0], (2048, 512), 4, 32, cb)
+    q = CQMatrix(packed[0], norms[0], (2048, 512), 4, 32, cb)
     xh = rng.normal(size=512).astype(np.float32)
     x, y = DeviceArray.from_host(xh), DeviceArray(2048 * 4)
     plan = Plan([q], [x.ptr], [y.ptr], batch=1)
@@ -290,10 +304,11 @@ def bench_candidates(steps, warmup, stream):
     """Candidate rows of the LM-head geometry (CQ4 8192 x 512 g32, one input vector) through the device entry
     point, FP32 and int8 paths, next to the full GEMV of the same matrix: {name: [ms per call]} from one event
     pair around each call. 142 candidates gather rows into a compact matrix; 8192 run the whole matrix."""
-    from openneedle_amd.native import DeviceArray, Event, NativeCQ, synchronize
+    from openneedle_amd.cq import CQMatrix
+    from openneedle_amd.device import DeviceArray, Event, synchronize
     rng = np.random.default_rng(29)
     packed, norms, cb = random_cq(rng, 1, 8192, 512, 4, 32)
-    q = NativeCQ(packed[0], norms[0], (8192, 512), 4, 32, cb)
+    q = CQMatrix(packed[0], norms[0], (8192, 512), 4, 32, cb)
     x = DeviceArray.from_host(rng.normal(size=512).astype(np.float32))
     y = DeviceArray(8192 * 4)
     sp = stream.ptr
@@ -311,13 +326,13 @@ def bench_candidates(steps, warmup, stream):
         synchronize()
         return [a.elapsed_ms(b) for a, b in ev]
 
-    out = {"fp32_full": calls(lambda: q.linear_device(x.ptr, y.ptr, 1, sp)),
-           "int8_full": calls(lambda: q.int8_device(x.ptr, y.ptr, 1, sp))}
+    out = {"fp32_full": calls(lambda: q.matvec_device(x.ptr, y.ptr, 1, sp)),
+           "int8_full": calls(lambda: q.matvec_int8_device(x.ptr, y.ptr, 1, sp))}
     for count in (142, 8192):
         ids = DeviceArray.from_host(rng.permutation(8192)[:count].astype(np.int32))
         for int8 in (False, True):
             out[f"{'int8' if int8 else 'fp32'}_{count}"] = calls(
-                lambda: q.candidates_device(x.ptr, ids.ptr, count, y.ptr, stream, int8=int8))
+                lambda: q.select_device(x.ptr, ids.ptr, count, y.ptr, stream, int8=int8))
     return out
 
 
@@ -327,7 +342,7 @@ def bench_archive_upload():
     device arrays), timed on the host around the whole load after one untimed load. Returns (ms, bytes)."""
     import tempfile
     from openneedle_amd.archive import Archive, DeviceModel, synthetic_released
-    from openneedle_amd.native import synchronize
+    from openneedle_amd.device import synchronize
     with tempfile.TemporaryDirectory() as tmp:
         path = Path(tmp) / "model.cact"
         path.write_bytes(synthetic_released(seed=1))
@@ -340,17 +355,17 @@ def bench_archive_upload():
 
 
 def bench_engine(tokens=64):
-    """NativeEngine.step on the GPU for the released geometry (27 layers, d_model 512, random contents, KV window
+    """GpuEngine.step on the GPU for the released geometry (27 layers, d_model 512, random contents, KV window
     256): whole-token latency as the caller sees it (host pointers: the token in, 8192 logits out, one wait per
     token), fp32 and int8 KV, and the int8 matmul path ("sdot", fp32 KV), after 16 untimed tokens. Returns
     {config: (tokens/s, [ms per token])}."""
     from openneedle_amd.archive import Archive, synthetic_released
-    from openneedle_amd.engine import NativeEngine
+    from openneedle_amd.engine import GpuEngine
     archive = Archive(synthetic_released(seed=3, tokenizer_bytes=0))
     out = {}
     for kv in ("fp32", "int8", "sdot"):
-        e = NativeEngine(archive, kv_cache="int8" if kv == "int8" else "fp32",
-                         matmul="sdot" if kv == "sdot" else "fp32")
+        e = GpuEngine(archive, kv_cache="int8" if kv == "int8" else "fp32",
+                      matmul="int8" if kv == "sdot" else "fp32")
         for i in range(16):
             e.step((i * 131) % 8192)
         times = []
@@ -360,7 +375,7 @@ def bench_engine(tokens=64):
             e.step((i * 37 + 11) % 8192)
             times.append((time.perf_counter_ns() - t) / 1e6)
         out[kv] = (tokens / (time.perf_counter() - t0), times)
-        del e
+        e.close()
     return out
 
 
@@ -373,17 +388,17 @@ def prompt_tokens():
 
 
 def bench_engine_prefill(runs=8):
-    """NativeEngine.prefill of a 512-token prompt (released geometry, chunks of 32, last logits only) after
+    """GpuEngine.prefill of a 512-token prompt (released geometry, chunks of 32, last logits only) after
     reset(), timed on the host around the call, after one untimed prompt. Returns {kv: (tokens/s, [ms per
     prompt])}."""
     from openneedle_amd.archive import Archive, synthetic_released
-    from openneedle_amd.engine import NativeEngine
+    from openneedle_amd.engine import GpuEngine
     archive = Archive(synthetic_released(seed=3, tokenizer_bytes=0))
     tokens = prompt_tokens()
     out = {}
     for kv in ("fp32", "int8", "sdot"):
-        e = NativeEngine(archive, kv_cache="int8" if kv == "int8" else "fp32",
-                         matmul="sdot" if kv == "sdot" else "fp32")
+        e = GpuEngine(archive, kv_cache="int8" if kv == "int8" else "fp32",
+                      matmul="int8" if kv == "sdot" else "fp32")
         e.prefill(tokens, last_only=True)
         times = []
         for _ in range(runs):
@@ -392,19 +407,19 @@ def bench_engine_prefill(runs=8):
             e.prefill(tokens, last_only=True)
             times.append((time.perf_counter_ns() - t) / 1e6)
         out[kv] = (PROMPT_TOKENS / (statistics.median(times) * 1e-3), times)
-        del e
+        e.close()
     return out
 
 
 def abi_calls(mats, x, runs, warmup=3):
     """Host-side milliseconds of `runs` host-pointer needle2_cq_linear calls (batch 1), cycling over `mats`."""
     for m in mats[:warmup] if len(mats) >= warmup else mats * warmup:
-        m.linear(x)
+        m.matvec(x)
     times = []
     for i in range(runs):
         m = mats[i % len(mats)]
         t = time.perf_counter_ns()
-        m.linear(x)
+        m.matvec(x)
         times.append((time.perf_counter_ns() - t) / 1e6)
     return times
 
@@ -562,6 +577,7 @@ def main():
                     default=None,
                     help="run a single workload (for profiling); prints no JSON line")
     ap.add_argument("--sweep", action="store_true", help="with --only attn: also time fixed split counts")
+    ap.add_argument("--graph", action="store_true", help="with --only decode: also replay the step from a HIP graph")
     ap.add_argument("--batch", type=int, default=1, help="with --only cq4 / cq2 / int8: activation rows per step")
     ap.add_argument("--calibrate", action="store_true",
                     help="also run one 1 GiB streaming copy kernel (reference for byte counters)")
@@ -571,14 +587,14 @@ def main():
               "build runs on a single MI355X. Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    from openneedle_amd.native import Stream, device_info
+    from openneedle_amd.device import Stream, device_info
     info = device_info()
     log(f"device {info}")
     stream = Stream()
     rng = np.random.default_rng(20261201)
 
     if args.calibrate:
-        from openneedle_amd.native import DeviceArray, copy_kernel, synchronize
+        from openneedle_amd.device import DeviceArray, copy_kernel, synchronize
         a, b = DeviceArray(1 << 30), DeviceArray(1 << 30)
         copy_kernel(b, a, 1 << 30, stream)
         synchronize()
@@ -587,9 +603,10 @@ def main():
 
     if args.only == "decode":
         for seqs in (64, 1):
-            ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs)
-            log(f"decode layer ({seqs} seqs, ctx 2048): eager {ms_e * 1e3:.1f} us, graph {ms_g * 1e3:.1f} us -> "
-                f"{seqs / (min(ms_e, ms_g) * 1e-3):.0f} tokens/s per layer")
+            ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs, graph=args.graph)
+            graph = f", graph {ms_g * 1e3:.1f} us" if ms_g is not None else ""
+            log(f"decode layer ({seqs} seqs, ctx 2048): eager {ms_e * 1e3:.1f} us{graph} -> "
+                f"{seqs / (min(ms_e, ms_g or ms_e) * 1e-3):.0f} tokens/s per layer")
         return
     if args.only == "engine":
         for kv, (tps, ms) in bench_engine().items():
@@ -705,12 +722,12 @@ def main():
             extra[f"candidates_{k}_us"] = dist_us(v)
         log(f"candidates: { {k: v['median'] for k, v in extra.items() if k.startswith('candidates_')} }")
 
-        log("engine: NativeEngine.step, released geometry (27 layers), batch 1")
+        log("engine: GpuEngine.step, released geometry (27 layers), batch 1")
         for kv, (tps, tok_ms) in bench_engine().items():
             extra[f"engine_{ENGINE_LABEL[kv]}_tokens_per_s"] = round(tps, 1)
             extra[f"engine_{ENGINE_LABEL[kv]}_token_us"] = dist_us(tok_ms)
             log(f"engine {ENGINE_LABEL[kv]}: {tps:.0f} tokens/s")
-        log(f"engine prefill: NativeEngine.prefill, released geometry, {PROMPT_TOKENS}-token prompt")
+        log(f"engine prefill: GpuEngine.prefill, released geometry, {PROMPT_TOKENS}-token prompt")
         for kv, (tps, pr_ms) in bench_engine_prefill().items():
             extra[f"engine_prefill_{ENGINE_LABEL[kv]}_tokens_per_s"] = round(tps, 1)
             extra[f"engine_prefill_{ENGINE_LABEL[kv]}_prompt_us"] = dist_us(pr_ms)

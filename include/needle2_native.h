@@ -33,7 +33,10 @@ const char *needle2_native_features(void);
 /* needle2/csrc/cq.cpp:350-352. Uploads packed codes ([out][padded*bits/8],
  * LSB-first), fp16 norms ([out][padded/group]) and the codebook (16/8/4/3
  * floats) to device memory; the host buffers are not retained.
- * bits: 2, 3, 4 or 5 (ternary crumbs); group: power of two >= 8. */
+ * bits: 2, 3, 4 or 5 (ternary crumbs); group: power of two >= 8. Returns NULL
+ * (reason in needle2_gpu_error) for a codebook that is not finite and strictly
+ * increasing, a norm that is not finite or is negative, or a ternary crumb 2:
+ * the inputs the reference's loader refuses (needle2/native.py:190-202). */
 void *needle2_cq_create(const uint8_t *packed, const uint16_t *norms, int out, int in, int bits, int group,
                         const float *codebook);
 /* needle2/csrc/cq.cpp:353 */
@@ -43,7 +46,9 @@ void needle2_cq_destroy(void *handle);
 void needle2_cq_linear(void *handle, const float *x, float *y, int batch, int threads);
 /* needle2/csrc/cq.cpp:357-359. Every mode runs the GPU GEMV (same tolerance contract). */
 void needle2_cq_linear_lookup(void *handle, const float *x, float *y, int batch, int threads, int mode);
-/* needle2/csrc/cq.cpp:360-366. One x for count matrices; ys[i] receives matrix i's output. */
+/* needle2/csrc/cq.cpp:287-292, 360-366. One x for count matrices; ys[i] receives matrix i's output.
+ * Matrices of one input length and group share one copy and one transform of x (one GEMV launch per
+ * storage geometry); otherwise each runs alone. Every mode runs the GPU GEMV. */
 void needle2_cq_linear_many(void *const *handles, int count, const float *x, float *const *ys, int threads,
                             int mode);
 /* needle2/csrc/cq.cpp:367-370. y: [count][in] = FWHT(cb[code]*norm) of each row. */

@@ -1,10 +1,17 @@
 """gfx950 (MI355X) implementation of OpenNeedle's quantized-matmul hot path.
 
-``openneedle_amd.native`` mirrors the reference's ctypes loader
-(``needle2/native.py``) over ``libneedle2_native.so``: CQ2/CQ3/CQ4/ternary FP32
-GEMV, the bit-exact int8 ("SDOT") GEMV, row dequantization, plus device-resident
-entry points, int8-KV decode attention and the prefill GEMM.
-"""
-from . import formats  # noqa: F401
+The product is ``libneedle2_native.so`` (``csrc/``): the reference's C ABI
+(``needle2_cq_*``, ``needle2_sdot_*``, ``needle2_engine_*``) plus additive
+device-resident exports (``needle2_gpu_*``). The Python modules are this
+repository's own interface to it:
 
-__all__ = ["formats", "native"]
+- ``_ffi``    locating, loading and typing the library;
+- ``device``  device memory, streams, events, HIP graphs, ordered teardown;
+- ``cq``      CQ matrices (FP32 and int8 products, rows, candidates, the
+              prefill GEMM) and multi-matrix plans;
+- ``kv``      the int8 KV cache of a decode batch and its attention;
+- ``engine``  the single-sequence decode engine;
+- ``archive`` / ``formats``  the ``.cact`` file and the CQ storage format.
+"""
+
+__all__ = ["archive", "cq", "device", "engine", "formats", "kv"]

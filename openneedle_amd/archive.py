@@ -375,7 +375,7 @@ class DeviceModel:
     """Every tensor of an archive in device memory, uploaded once.
 
     The span of the file holding the CQ payloads goes to the device in one copy; each CQ record then becomes a
-    :class:`~openneedle_amd.native.NativeCQ` whose relayout kernels read its codes and norms there (plus its
+    :class:`~openneedle_amd.cq.CQMatrix` whose relayout kernels read its codes and norms there (plus its
     int8 twin for CQ2 / CQ4 when ``int8``), and the copy is freed once they have run. The FP16 / FP32 tensors
     go up as one fp32 buffer; ``dense[name]`` is a device view of it. The archive stays referenced: the
     handles keep host views of the mapped file for later lazily built int8 twins."""
@@ -386,7 +386,8 @@ class DeviceModel:
     uploaded_bytes: int = 0
 
     def __post_init__(self):
-        from .native import DeviceArray, NativeCQ, Stream
+        from .cq import CQMatrix
+        from .device import DeviceArray, Stream
         tensors = self.archive.tensors.values()
         cq = [r for r in tensors if r.dtype == CQ]
         stream = Stream()
@@ -397,11 +398,12 @@ class DeviceModel:
             span.upload(np.frombuffer(self.archive.raw[lo:hi], dtype=np.uint8))
             for r in cq:
                 at = span.ptr + r.offset - lo
-                self.matrices[r.name] = NativeCQ(r.packed, r.norms, r.shape, r.bits, r.group_size, r.cq_codebook(),
-                                                 device=(at, at + r.shape[0] * r.rowbytes, stream), int8=self.int8)
+                self.matrices[r.name] = CQMatrix.from_record(r, device=(at, at + r.shape[0] * r.rowbytes, stream),
+                                                             int8=self.int8)
             stream.synchronize()
             self.uploaded_bytes += hi - lo
-            del span
+            span.close()  # the relayouts that read it have run
+        stream.close()
         dense = [r for r in tensors if r.dtype in (FP16, FP32)]
         if dense:
             values = [r.dequantize().reshape(-1) for r in dense]

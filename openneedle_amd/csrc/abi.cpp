@@ -33,15 +33,43 @@ void hip_fail(const char *expr, hipError_t e, const char *file, int line) {
 
 static bool is_pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
+// Inputs the kernels cannot run meaningfully are refused at creation (the
+// reference's Python loader refuses the same ones before its C call,
+// needle2/native.py:190-202): a codebook that is not finite and strictly
+// increasing, a norm that is not finite or is below zero (-0 is a zero
+// norm), and the reserved ternary crumb 2, which has no centroid.
+static void check_codebook(const float *cb, int n) {
+    for (int i = 0; i < n; ++i)
+        ND_CHECK(std::isfinite(cb[i]) && (i == 0 || cb[i - 1] < cb[i]),
+                 "CQ codebook: centroids must be finite and strictly increasing");
+}
+
+static void check_norms(const uint16_t *norms, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const uint16_t h = norms[i];
+        ND_CHECK((h & 0x7C00u) != 0x7C00u && !((h & 0x8000u) && (h & 0x7FFFu)),
+                 "CQ norms: every fp16 group norm must be finite and >= 0");
+    }
+}
+
+static void check_ternary(const uint8_t *packed, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const uint8_t b = packed[i];
+        // crumb value 2 = high bit set, low bit clear
+        ND_CHECK(((b >> 1) & ~b & 0x55u) == 0, "CQ ternary codes: crumb value 2 is reserved");
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Matrix upload
 // ---------------------------------------------------------------------------
 void Matrix::upload(const uint8_t *packed, const uint16_t *host_norms, int out_, int in_, int bits_, int group_,
                     const float *cb, hipStream_t s, bool device_inputs) {
-    ND_CHECK(out_ > 0 && in_ > 0, "CQ matrix shape must be positive");
-    ND_CHECK(bits_ == 2 || bits_ == 3 || bits_ == 4 || bits_ == 5, "CQ storage bits must be 2, 3, 4, or ternary marker 5");
-    ND_CHECK(is_pow2(group_) && group_ >= 8, "CQ group size must be a power of two >= 8");
+    ND_CHECK(out_ > 0 && in_ > 0, "CQ matrix shape must be positive (rows and columns)");
+    ND_CHECK(bits_ == 2 || bits_ == 3 || bits_ == 4 || bits_ == 5, "CQ bits must be 2, 3 or 4 (5: ternary crumbs)");
+    ND_CHECK(is_pow2(group_) && group_ >= 8, "CQ group must be a power of two of at least 8");
     ND_CHECK(packed && host_norms && cb, "CQ create: null buffer");
+    check_codebook(cb, bits_ == 5 ? 3 : 1 << bits_);
     out = out_;
     in = in_;
     bits = bits_;
@@ -68,6 +96,11 @@ void Matrix::upload(const uint8_t *packed, const uint16_t *host_norms, int out_,
         std::memcpy(lut, cb, sizeof(float) * (1u << bits));
     }
     std::memcpy(cb_raw, cb, sizeof(float) * (bits == 5 ? 3 : 1u << bits));
+    // host inputs are checked before anything is allocated (device inputs are the caller's to vouch for)
+    if (!device_inputs) {
+        check_norms(host_norms, size_t(out) * groups);
+        if (bits == 5) check_ternary(packed, size_t(out) * rowbytes);
+    }
 
     codes.reserve(size_t(chunks) * n_pad);
     norms.reserve(size_t(groups) * n_pad);
@@ -338,6 +371,8 @@ void SdotHandle::candidates_host(const float *x, const int32_t *ids, int count, 
 void SdotHandle::linear_host(const float *x, float *y, int batch) {
     if (batch <= 0) return;
     const size_t nx = size_t(batch) * m.in, ny = size_t(batch) * m.out;
+    // a non-finite value has no int8 code (the reference's loader refuses it, needle2/native.py:249-250)
+    for (size_t i = 0; i < nx; ++i) ND_CHECK(std::isfinite(x[i]), "int8 input values must be finite");
     st.hx.reserve(nx);
     st.hy.reserve(ny);
     st.x.reserve(nx);
@@ -449,6 +484,60 @@ static bool same_geometry(const Matrix &a, const Matrix &b) {
     return a.in == b.in && a.bits == b.bits && a.group == b.group && std::memcmp(a.lut, b.lut, sizeof a.lut) == 0;
 }
 
+// needle2_cq_linear_many for matrices of one input length and group, staged
+// in the first handle's buffers and run on its stream.
+static void linear_many(const std::vector<CqHandle *> &hs, const float *x, float *const *ys) {
+    CqHandle &h0 = *hs[0];
+    const Matrix &m0 = h0.m;
+    Staging &st = h0.st;
+    const hipStream_t s = st.stream();
+    const int n = static_cast<int>(hs.size());
+    std::vector<size_t> at(static_cast<size_t>(n) + 1, 0);  // output offsets in the shared y buffer
+    for (int i = 0; i < n; ++i) at[i + 1] = at[i] + size_t(hs[i]->m.out);
+    st.hx.reserve(m0.in);
+    st.x.reserve(m0.in);
+    st.y.reserve(at[n]);
+    st.hy.reserve(at[n]);
+    std::memcpy(st.hx.p, x, size_t(m0.in) * sizeof(float));
+    ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, size_t(m0.in) * sizeof(float), hipMemcpyHostToDevice, s));
+    // the one transform: the shared rotated x, unless the GEMV fuses the FWHT into its table build
+    const float *act = st.x.p;
+    if (!gemv_fuses_fwht(m0.group)) {
+        st.rot.reserve(m0.dev);
+        if (gemv_prepass(m0.group)) launch_rot_many(st.x.p, nullptr, 1, 1, m0.in, m0.dev, m0.group, m0.scale, st.rot.p, s);
+        else m0.transform(st.x.p, m0.in, st.rot.p, 1, st.big, s);
+        act = st.rot.p;
+    }
+    // job tables: one per run of equal storage geometry, all in one upload
+    std::vector<CqJob> jobs(static_cast<size_t>(n));
+    std::vector<std::pair<int, int>> runs;  // (first job, blocks) per launch
+    int block = 0;
+    for (int i = 0; i < n; ++i) {
+        const Matrix &mi = hs[i]->m;
+        if (i == 0 || !same_geometry(mi, hs[runs.back().first]->m)) {
+            runs.push_back({i, 0});
+            block = 0;
+        }
+        jobs[i] = CqJob{mi.codes.p, mi.norms.p, act, st.y.p + at[i], mi.out, mi.n_pad, block, 1};
+        block += mi.n_pad / kRowsPerBlock;
+        runs.back().second = block;
+    }
+    const size_t table = jobs.size() * sizeof(CqJob);
+    st.hjobs.reserve(table);
+    st.jobs.reserve(table);
+    std::memcpy(st.hjobs.p, jobs.data(), table);
+    ND_HIP(hipMemcpyAsync(st.jobs.p, st.hjobs.p, table, hipMemcpyHostToDevice, s));
+    for (size_t r = 0; r < runs.size(); ++r) {
+        const int first = runs[r].first;
+        const int njobs = (r + 1 < runs.size() ? runs[r + 1].first : n) - first;
+        launch_cq_gemv(hs[first]->m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(st.jobs.p) + first, njobs,
+                       runs[r].second, s);
+    }
+    ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, at[n] * sizeof(float), hipMemcpyDeviceToHost, s));
+    ND_HIP(hipStreamSynchronize(s));
+    for (int i = 0; i < n; ++i) std::memcpy(ys[i], st.hy.p + at[i], size_t(hs[i]->m.out) * sizeof(float));
+}
+
 }  // namespace nd
 
 using namespace nd;
@@ -491,11 +580,31 @@ void needle2_cq_linear_lookup(void *handle, const float *x, float *y, int batch,
     needle2_cq_linear(handle, x, y, batch, threads);
 }
 
-// cq.cpp:360-366: one shared x for several matrices.
+// cq.cpp:287-292, 360-366: one x through several matrices. When every
+// matrix takes the same input length and group (the reference's
+// compatible_rotation), x is copied in once and transformed once, and each
+// run of matrices with one storage geometry (bits and codebook) is one GEMV
+// launch over a job table; all outputs come back in one copy and one wait.
+// Otherwise each matrix runs on its own, as the reference falls back. Every
+// mode runs the same GEMV (the reference's table modes are other CPU
+// summation orders under one tolerance contract).
 void needle2_cq_linear_many(void *const *handles, int count, const float *x, float *const *ys, int threads, int mode) {
     (void)threads;
     (void)mode;
-    for (int i = 0; i < count; ++i) needle2_cq_linear(handles[i], x, ys[i], 1, threads);
+    if (count <= 0) return;
+    std::vector<CqHandle *> hs(static_cast<size_t>(count));
+    for (int i = 0; i < count; ++i) hs[i] = static_cast<CqHandle *>(handles[i]);
+    bool shared = true;
+    for (int i = 1; i < count; ++i) shared = shared && hs[i]->m.in == hs[0]->m.in && hs[i]->m.group == hs[0]->m.group;
+    const int rc = guarded([&] {
+        if (!shared) {
+            for (int i = 0; i < count; ++i) hs[i]->linear_host(x, ys[i], 1);
+            return;
+        }
+        linear_many(hs, x, ys);
+    });
+    if (rc)
+        for (int i = 0; i < count; ++i) poison(ys[i], size_t(hs[i]->m.out));
 }
 
 void needle2_cq_rows(void *handle, const int64_t *ids, float *y, int count) {

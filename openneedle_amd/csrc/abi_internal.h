@@ -66,6 +66,8 @@ struct Staging {
     DevBuf<float> yfull;    // all outputs, when most rows are candidates
     HostBuf<float> hx, hy;
     HostBuf<int32_t> hids;
+    DevBuf<uint8_t> jobs;   // per-call job tables (needle2_cq_linear_many)
+    HostBuf<uint8_t> hjobs;
     Staging() = default;
     ~Staging();
     Staging(const Staging &) = delete;

@@ -780,7 +780,13 @@ int GpuEngine::decode_loop(int first_token, int max_new_tokens, const DfaC *dfa,
             if (dfa->fallback_next_states[state] >= 0) state = dfa->fallback_next_states[state];
         }
     }
-    std::vector<float> scores(c.vocab);
+    // a state may list more candidates than the vocabulary (duplicates are valid): the score buffer
+    // holds the full logits or the largest candidate list, whichever is longer
+    size_t score_len = size_t(c.vocab);
+    if (dfa)
+        for (int st8 = 0; st8 < dfa->num_states; ++st8)
+            score_len = std::max(score_len, size_t(dfa->candidate_offsets[st8 + 1] - dfa->candidate_offsets[st8]));
+    std::vector<float> scores(score_len);
     int token = first_token;
     while (count < max_new_tokens) {
         const int type = dfa ? dfa->state_types[state] : 0;

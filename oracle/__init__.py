@@ -236,6 +236,14 @@ class RefCQ:
                                      bits, group, _ptr(self.cb))
         self.s = None
 
+    @property
+    def handle(self):
+        return self.h
+
+    @classmethod
+    def from_record(cls, rec):
+        return cls(rec.packed, rec.norms, rec.shape, rec.bits, rec.group_size, rec.cq_codebook())
+
     def __del__(self):
         if getattr(self, "h", None):
             self.L.needle2_cq_destroy(self.h)
@@ -325,91 +333,18 @@ class RefAttention:
         return out
 
 
-class RefEngine:
-    """The reference's own Engine (engine.cpp, built into oracle/_ref) over an archive, with the tensor
-    descriptors NativeEngine builds (needle2/native.py:382-395): CQ records through the reference's CQ handles,
-    everything else (the mHC matrices too) as dequantized fp32."""
-
-    def __init__(self, archive, activation_bits=0, int8_kv=False, threads=1, sdot=False):
-        from openneedle_amd.archive import CQ
-        from openneedle_amd.engine import _TensorDesc, _EngineConfig, engine_config, engine_tensors
-        L = ref()
-        if L is None:
-            raise RuntimeError("oracle/_ref was not built (reference sources absent)")
-        self.L = L
-        self.m = archive.metadata
-        self._owners, descs = [], []
-        for name in engine_tensors(archive):
-            rec = archive.tensors[name]
-            if rec.dtype == CQ and not name.startswith("mhc_"):
-                q = RefCQ(rec.packed, rec.norms, rec.shape, rec.bits, rec.group_size, rec.cq_codebook())
-                self._owners.append(q)
-                descs.append(_TensorDesc(q.h, None, *rec.shape))
-            else:
-                a = np.ascontiguousarray(rec.dequantize(), dtype=np.float32)
-                self._owners.append(a)
-                rows, cols = (a.shape[0], int(np.prod(a.shape[1:]))) if a.ndim > 1 else (1, a.size)
-                descs.append(_TensorDesc(None, a.ctypes.data, rows, cols))
-        self._cfg = engine_config(self.m)
-        self._descs = (_TensorDesc * len(descs))(*descs)
-        for name, args, res in (
-                ("needle2_engine_create", [ct.POINTER(_EngineConfig), ct.POINTER(_TensorDesc), ct.c_int, ct.c_int,
-                                           ct.c_int], ct.c_void_p),
-                ("needle2_engine_destroy", [ct.c_void_p], None),
-                ("needle2_engine_reset", [ct.c_void_p, ct.c_int], None),
-                ("needle2_engine_step", [ct.c_void_p, ct.c_int, ct.c_void_p, ct.c_void_p], ct.c_int),
-                ("needle2_engine_step_candidates", [ct.c_void_p, ct.c_int, ct.c_void_p, ct.c_int, ct.c_void_p,
-                                                    ct.c_void_p], ct.c_int),
-                ("needle2_engine_set_int8_kv", [ct.c_void_p, ct.c_int], ct.c_int),
-                ("needle2_engine_prefill", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p,
-                                            ct.c_void_p], ct.c_int),
-                ("needle2_engine_project_candidates", [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p], ct.c_int),
-                ("needle2_engine_cache_prefix", [ct.c_void_p], ct.c_int),
-                ("needle2_engine_decode_loop", [ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_void_p,
-                                                ct.c_void_p], ct.c_int),
-                ("needle2_engine_import", [ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p, ct.c_void_p, ct.c_int,
-                                           ct.c_void_p, ct.c_void_p], ct.c_int),
-                ("needle2_engine_reset_to_prefix", [ct.c_void_p], ct.c_int),
-                ("needle2_engine_error", [], ct.c_char_p)):
-            f = getattr(L, name)
-            f.argtypes, f.restype = args, res
-        self.h = L.needle2_engine_create(ct.byref(self._cfg), self._descs, len(descs), threads, activation_bits)
-        if not self.h:
-            raise RuntimeError(L.needle2_engine_error().decode())
-        if sdot:  # the Engine's int8 matmul path (engine.cpp:424-432 without the ARM feature test)
-            L.refh_engine_sdot.argtypes, L.refh_engine_sdot.restype = [ct.c_void_p], ct.c_int
-            assert L.refh_engine_sdot(self.h) == 0
-        if int8_kv:
-            assert L.needle2_engine_set_int8_kv(self.h, 1) == 0
-
-    def __del__(self):
-        if getattr(self, "h", None):
-            self.L.needle2_engine_destroy(self.h)
-
-    def reset(self, prefix=0):
-        self.L.needle2_engine_reset(self.h, prefix)
-
-    def step(self, token):
-        logits = np.empty(self.m["vocab_size"], np.float32)
-        hidden = np.empty((self.m["num_layers"], self.m["d_model"]), np.float32)
-        if self.L.needle2_engine_step(self.h, int(token), logits.ctypes.data, hidden.ctypes.data):
-            raise RuntimeError(self.L.needle2_engine_error().decode())
-        return logits, hidden
-
-    def prefill(self, tokens, last_only=False):
-        """Engine::prefill (engine.cpp:1045-1301): (logits [tokens][vocab] or [vocab], last token's hidden)."""
-        ids = np.ascontiguousarray(tokens, np.int32)
-        vocab = self.m["vocab_size"]
-        logits = np.empty(vocab if last_only else (ids.size, vocab), np.float32)
-        hidden = np.empty((self.m["num_layers"], self.m["d_model"]), np.float32)
-        if self.L.needle2_engine_prefill(self.h, ids.ctypes.data, ids.size, int(last_only), logits.ctypes.data,
-                                         hidden.ctypes.data):
-            raise RuntimeError(self.L.needle2_engine_error().decode())
-        return logits, hidden
-
-    def project_candidates(self, candidates):
-        ids = np.ascontiguousarray(candidates, np.int32)
-        out = np.empty(ids.size, np.float32)
-        if self.L.needle2_engine_project_candidates(self.h, ids.ctypes.data, ids.size, out.ctypes.data):
-            raise RuntimeError(self.L.needle2_engine_error().decode())
-        return out
+def RefEngine(archive, activation_bits=0, int8_kv=False, threads=1, sdot=False):
+    """The reference's own Engine (engine.cpp, built into oracle/_ref) over an archive, driven through the
+    same binding as the GPU engine (``openneedle_amd.engine.EngineBinding``): CQ records through the
+    reference's CQ handles, everything else (the mHC matrices too) as dequantized fp32."""
+    from openneedle_amd.engine import EngineBinding
+    L = ref()
+    if L is None:
+        raise RuntimeError("oracle/_ref was not built (reference sources absent)")
+    eng = EngineBinding(L, archive, RefCQ.from_record, activation_bits, threads)
+    if sdot:  # the Engine's int8 matmul path (engine.cpp:424-432 without the ARM feature test)
+        L.refh_engine_sdot.argtypes, L.refh_engine_sdot.restype = [ct.c_void_p], ct.c_int
+        assert L.refh_engine_sdot(eng.h) == 0
+    if int8_kv:
+        eng.set_int8_kv(True)
+    return eng

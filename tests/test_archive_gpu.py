@@ -26,7 +26,7 @@ def test_everything_uploaded(model):
     assert model.uploaded_bytes == span + 364279 * 4
     for name, t in a.tensors.items():
         if t.dtype == A.CQ:
-            assert model.matrices[name]._sdot_handle  # int8 twins built from the same device copy
+            assert model.matrices[name]._int8  # int8 twins built from the same device copy
     assert set(model.matrices) == {n for n, t in a.tensors.items() if t.dtype == A.CQ}
 
 
@@ -37,8 +37,8 @@ def test_matrices_bit_exact(model, name):
     q = model.matrices[name]
     x = activations((2, t.shape[1]), seed=len(name))
     expected = oracle.cq_linear(t.packed, t.norms, t.shape, t.bits, t.group_size, t.codebook, x, 8)
-    np.testing.assert_array_equal(q.linear(x), expected)
-    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(t.packed, t.norms, t.shape, t.bits,
+    np.testing.assert_array_equal(q.matvec(x), expected)
+    np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(t.packed, t.norms, t.shape, t.bits,
                                                                        t.group_size, t.codebook, x, 8))
 
 
@@ -47,7 +47,7 @@ def test_lm_head_candidates_from_archive(model):
     q = model.matrices["embedding"]
     x = activations(512, seed=8)
     ids = np.random.default_rng(2).permutation(8192)[:142].astype(np.int32)
-    np.testing.assert_array_equal(q.candidates(x, ids), q.linear(x)[ids])
+    np.testing.assert_array_equal(q.select(x, ids), q.matvec(x)[ids])
 
 
 def test_dense_tensors_uploaded(model):

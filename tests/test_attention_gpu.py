@@ -11,7 +11,8 @@ import numpy as np
 import pytest
 
 import oracle
-from openneedle_amd.native import DeviceArray, KVCache, synchronize
+from openneedle_amd.device import DeviceArray, synchronize
+from openneedle_amd.kv import KVCache
 
 pytestmark = pytest.mark.gpu
 

@@ -11,7 +11,8 @@ import pytest
 
 import oracle
 from openneedle_amd import formats
-from openneedle_amd.native import DeviceArray, NativeCQ, Plan, synchronize
+from openneedle_amd.cq import CQMatrix, Plan
+from openneedle_amd.device import DeviceArray, synchronize
 from tests.cases import activations, baseline, example
 
 pytestmark = pytest.mark.gpu
@@ -23,34 +24,34 @@ def check(got, expected, bits):
 @pytest.mark.parametrize("bits", [2, 3, 4, 5])
 def test_reference_example_all_modes(bits):
     packed, norms, cb, dense = example(bits)
-    q = NativeCQ(packed, norms, dense.shape, bits, 128, cb)
+    q = CQMatrix(packed, norms, dense.shape, bits, 128, cb)
     x = activations((2, 3, 257))
     expected = oracle.cq_linear(packed, norms, dense.shape, bits, 128, cb, x)
-    for threads in (1, 2):
-        for lookup in (0, 1, 2, 3):
-            got = q.linear(x, threads, lookup=lookup)
-            assert got.shape == (2, 3, 9)
-            check(got, expected, bits)
-            np.testing.assert_allclose(got, x.astype(np.float64) @ dense.T, atol=3e-6, rtol=2e-5)
+    for lookup in (0, 1, 2, 3):
+        got = q.matvec(x, mode=lookup)
+        assert got.shape == (2, 3, 9)
+        check(got, expected, bits)
+        np.testing.assert_allclose(got, x.astype(np.float64) @ dense.T, atol=3e-6, rtol=2e-5)
     assert np.all(got[..., 0] == 0)
     ids = np.array([[8, 2], [0, 2]])
     np.testing.assert_array_equal(q.rows(ids), oracle.cq_rows(packed, norms, dense.shape, bits, 128, cb, ids))
-    np.testing.assert_allclose(q.dequantize(), dense, atol=2e-7, rtol=3e-5)
+    np.testing.assert_allclose(q.dense(), dense, atol=2e-7, rtol=3e-5)
     np.testing.assert_allclose(q.rows(2), dense[2], atol=2e-7, rtol=3e-5)
 
 
 def test_bounds_and_empty_batch():
     packed, norms, cb, dense = example(2)
-    q = NativeCQ(packed, norms, dense.shape, 2, 128, cb)
-    with pytest.raises(IndexError):
+    q = CQMatrix(packed, norms, dense.shape, 2, 128, cb)
+    from openneedle_amd._ffi import GpuError
+    with pytest.raises(GpuError, match="outside"):
         q.rows([-1])
-    with pytest.raises(IndexError):
+    with pytest.raises(GpuError, match="outside"):
         q.rows([q.shape[0]])
     with pytest.raises(TypeError):
         q.rows([1.5])
     with pytest.raises(ValueError):
-        q.linear(np.ones(256))
-    assert q.linear(np.empty((0, 257))).shape == (0, 9)
+        q.matvec(np.ones(256))
+    assert q.matvec(np.empty((0, 257))).shape == (0, 9)
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 5])
@@ -58,19 +59,19 @@ def test_bounds_and_empty_batch():
 @pytest.mark.parametrize("rows,dim", [(33, 200), (300, 1000)])
 def test_groups_and_ragged_shapes(bits, group, rows, dim):
     packed, norms, cb, dense = example(bits, rows=rows, dim=dim, group=group, seed=bits * 1000 + group)
-    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
     x = activations((3, dim), seed=group)
     expected = oracle.cq_linear(packed, norms, dense.shape, bits, group, cb, x, 4)
-    check(q.linear(x), expected, bits)
+    check(q.matvec(x), expected, bits)
 
 
 def test_huge_group_global_fwht():
     """group > 16384 runs the FWHT as global-memory butterfly stages."""
     bits, group, dim = 4, 32768, 40000
     packed, norms, cb, dense = example(bits, rows=7, dim=dim, group=group, seed=5)
-    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
     x = activations((2, dim), seed=6)
-    np.testing.assert_array_equal(q.linear(x), oracle.cq_linear(packed, norms, dense.shape, bits, group, cb, x, 4))
+    np.testing.assert_array_equal(q.matvec(x), oracle.cq_linear(packed, norms, dense.shape, bits, group, cb, x, 4))
     np.testing.assert_array_equal(q.rows([3, 0]), oracle.cq_rows(packed, norms, dense.shape, bits, group, cb, [3, 0]))
 
 
@@ -78,42 +79,42 @@ def test_lloyd_max_codebook():
     for bits in (2, 3, 4):
         packed, norms, _, _ = baseline(bits, 512, 1024, group=128, seed=bits)
         cb = formats.codebook(bits, 128)
-        q = NativeCQ(packed, norms, (512, 1024), bits, 128, cb)
+        q = CQMatrix(packed, norms, (512, 1024), bits, 128, cb)
         x = activations((2, 1024), seed=bits)
-        check(q.linear(x), oracle.cq_linear(packed, norms, (512, 1024), bits, 128, cb, x, 4), bits)
+        check(q.matvec(x), oracle.cq_linear(packed, norms, (512, 1024), bits, 128, cb, x, 4), bits)
 
 
 def test_single_token_decode_shape_bit_exact():
     """2048 x 512 CQ4 g32, batch 1 (the CPU-runnable decode GEMV)."""
     packed, norms, cb, _ = baseline(4, 2048, 512)
-    q = NativeCQ(packed, norms, (2048, 512), 4, 32, cb)
+    q = CQMatrix(packed, norms, (2048, 512), 4, 32, cb)
     x = activations(512, seed=11)
-    np.testing.assert_array_equal(q.linear(x), oracle.cq_linear(packed, norms, (2048, 512), 4, 32, cb, x, 8))
+    np.testing.assert_array_equal(q.matvec(x), oracle.cq_linear(packed, norms, (2048, 512), 4, 32, cb, x, 8))
 
 
 @pytest.mark.parametrize("bits", [2, 4])
 def test_full_size_8192_matrix(bits):
     """One 8192 x 8192 g32 matrix of the HBM-bound stack, batch 1 and 2."""
     packed, norms, cb, _ = baseline(bits, 8192, 8192, seed=77 + bits)
-    q = NativeCQ(packed, norms, (8192, 8192), bits, 32, cb)
+    q = CQMatrix(packed, norms, (8192, 8192), bits, 32, cb)
     x = activations((2, 8192), seed=12)
     expected = oracle.cq_linear(packed, norms, (8192, 8192), bits, 32, cb, x, 8)
-    check(q.linear(x), expected, bits)
-    check(q.linear(x[1]), expected[1], bits)
+    check(q.matvec(x), expected, bits)
+    check(q.matvec(x[1]), expected[1], bits)
 
 
 def test_device_entry_and_plan():
     mats, xs, expected = [], [], []
     for i in range(3):
         packed, norms, cb, _ = baseline(4, 1000 + 256 * i, 768, seed=300 + i)
-        mats.append(NativeCQ(packed, norms, (1000 + 256 * i, 768), 4, 32, cb))
+        mats.append(CQMatrix(packed, norms, (1000 + 256 * i, 768), 4, 32, cb))
         x = activations(768, seed=400 + i)
         xs.append(x)
         expected.append(oracle.cq_linear(packed, norms, mats[-1].shape, 4, 32, cb, x))
     d_x = [DeviceArray.from_host(x) for x in xs]
     d_y = [DeviceArray(4 * m.shape[0]) for m in mats]
     for m, dx, dy, e in zip(mats, d_x, d_y, expected):
-        m.linear_device(dx.ptr, dy.ptr, 1)
+        m.matvec_device(dx.ptr, dy.ptr, 1)
         synchronize()
         np.testing.assert_array_equal(dy.download(np.empty(m.shape[0], np.float32)), e)
     for dy in d_y:
@@ -124,3 +125,37 @@ def test_device_entry_and_plan():
         synchronize()
         for m, dy, e in zip(mats, d_y, expected):
             np.testing.assert_array_equal(dy.download(np.empty(m.shape[0], np.float32)), e)
+
+
+def _many_case(specs, seed):
+    """Matrices of the given (rows, bits, group, dim) with their oracle inputs."""
+    mats, refs = [], []
+    for i, (rows, bits, group, dim) in enumerate(specs):
+        packed, norms, cb, dense = example(bits, rows=rows, dim=dim, group=group, seed=seed + i)
+        mats.append(CQMatrix(packed, norms, dense.shape, bits, group, cb))
+        refs.append((packed, norms, dense.shape, bits, group, cb))
+    return mats, refs
+
+
+@pytest.mark.parametrize("mode", [0, 1, 4])
+def test_linear_many_shared_transform(mode):
+    """needle2_cq_linear_many (cq.cpp:287-292, 360-366): matrices of one input length and group share one
+    transform; runs of one storage geometry share a GEMV launch. Mixed widths, codebooks and row counts
+    (group 32: pre-pass FWHT; group 128: FWHT fused in the GEMV)."""
+    from openneedle_amd.cq import matvec_many
+    for group in (32, 128):
+        specs = [(300, 4, group, 700), (257, 4, group, 700), (1000, 2, group, 700), (9, 5, group, 700),
+                 (64, 3, group, 700), (513, 4, group, 700)]
+        mats, refs = _many_case(specs, seed=900 + group)
+        x = activations(700, seed=group)
+        for out, ref in zip(matvec_many(mats, x, mode=mode), refs):
+            np.testing.assert_array_equal(out, oracle.cq_linear(*ref, x))
+
+
+def test_linear_many_falls_back_per_matrix():
+    """Different groups (or input lengths) cannot share a transform: each matrix runs alone, same outputs."""
+    from openneedle_amd.cq import matvec_many
+    mats, refs = _many_case([(100, 4, 32, 512), (200, 2, 64, 512), (50, 4, 128, 512)], seed=950)
+    x = activations(512, seed=951)
+    for out, ref in zip(matvec_many(mats, x), refs):
+        np.testing.assert_array_equal(out, oracle.cq_linear(*ref, x))

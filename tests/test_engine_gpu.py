@@ -10,7 +10,7 @@ import pytest
 
 import oracle
 from openneedle_amd.archive import Archive, synthetic_model, synthetic_released
-from openneedle_amd.engine import NativeEngine
+from openneedle_amd.engine import EngineError, GpuEngine
 
 pytestmark = pytest.mark.gpu
 
@@ -27,12 +27,12 @@ def small(window=0, seed=1):
 
 
 def run_both(archive, tokens, int8_kv=False, abits=0):
-    gpu = NativeEngine(archive, activation_bits=abits, kv_cache="int8" if int8_kv else "fp32")
+    gpu = GpuEngine(archive, activation_bits=abits, kv_cache="int8" if int8_kv else "fp32")
     ref = oracle.RefEngine(archive, abits, int8_kv)
     out = []
     for t in tokens:
-        lg, hd = gpu.step(t, return_hidden=True)
-        rl, rh = ref.step(t)
+        lg, hd = gpu.step(t, hidden=True)
+        rl, rh = ref.step(t, hidden=True)
         out.append((lg, hd, rl, rh))
     return out
 
@@ -79,7 +79,7 @@ def test_candidates_equal_full_logits():
     """needle2's own contract (tests/test_candidate_projection_dense.py): candidate logits equal the full
     projection indexed by the candidates, order and duplicates kept, and leave the state as step does."""
     a = small(0, seed=4)
-    full, sel = NativeEngine(a), NativeEngine(a)
+    full, sel = GpuEngine(a), GpuEngine(a)
     rng = np.random.default_rng(51)
     for count in (2, 142, 300, 512):
         ids = rng.permutation(512)[:count].astype(np.int32)
@@ -87,34 +87,22 @@ def test_candidates_equal_full_logits():
         full.reset()
         sel.reset()
         for t in (2, 51, 302, 17):
-            e, eh = full.step(t, return_hidden=True)
-            g, gh = sel.step_candidates(t, ids, return_hidden=True)
+            e, eh = full.step(t, hidden=True)
+            g, gh = sel.step_candidates(t, ids, hidden=True)
             np.testing.assert_array_equal(g, e[ids])
             np.testing.assert_array_equal(gh, eh)
-        np.testing.assert_array_equal(sel.step(33), full.step(33))
+        np.testing.assert_array_equal(sel.step(33)[0], full.step(33)[0])
 
 
 PROMPT = [int(t) for t in np.random.default_rng(61).integers(0, 512, 45)]
 
 
 def gpu_prefill(engine, tokens, last_only=False):
-    """needle2_engine_prefill with the hidden states too (NativeEngine.prefill returns logits only)."""
-    ids = np.ascontiguousarray(tokens, np.int32)
-    vocab, layers, d = (engine.metadata[k] for k in ("vocab_size", "num_layers", "d_model"))
-    logits = np.empty(vocab if last_only else (ids.size, vocab), np.float32)
-    hidden = np.empty((layers, d), np.float32)
-    assert engine._lib.needle2_engine_prefill(engine._handle, ids.ctypes.data, ids.size, int(last_only),
-                                              logits.ctypes.data, hidden.ctypes.data) == 0
-    engine.position += ids.size
-    return logits, hidden
+    return engine.prefill(tokens, last_only=last_only, hidden=True)
 
 
 def gpu_project(engine, ids):
-    ids = np.ascontiguousarray(ids, np.int32)
-    out = np.empty(ids.size, np.float32)
-    assert engine._lib.needle2_engine_project_candidates(engine._handle, ids.ctypes.data, ids.size,
-                                                         out.ctypes.data) == 0
-    return out
+    return engine.project_candidates(ids)
 
 
 @pytest.mark.parametrize("window,prefix", [(0, 0), (8, 0), (8, 3)])
@@ -124,16 +112,16 @@ def test_prefill_matches_reference(window, prefix, int8):
     token's logits, the last token's hidden states, candidates projected right after (the reference projects
     the last token's embedding row there) and the steps that follow."""
     a = small(window, seed=7)
-    gpu = NativeEngine(a, kv_cache="int8" if int8 else "fp32")
+    gpu = GpuEngine(a, kv_cache="int8" if int8 else "fp32")
     ref = oracle.RefEngine(a, 0, int8)
     gpu.reset(prefix)
     ref.reset(prefix)
     lg, hd = gpu_prefill(gpu, PROMPT)
-    rl, rh = ref.prefill(PROMPT)
+    rl, rh = ref.prefill(PROMPT, hidden=True)
     ids = np.array([3, 500, 77, 3], np.int32)
     pairs = [("logits", lg, rl), ("hidden", hd, rh), ("candidates", gpu_project(gpu, ids), ref.project_candidates(ids))]
     for t in (11, 400, 2):
-        g, r = gpu.step(t, return_hidden=True), ref.step(t)
+        g, r = gpu.step(t, hidden=True), ref.step(t, hidden=True)
         pairs += [(f"step {t} logits", g[0], r[0]), (f"step {t} hidden", g[1], r[1])]
     for what, g, r in pairs:
         print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
@@ -147,9 +135,9 @@ def test_prefill_released_geometry():
     """27 layers of the released geometry (window 256, chunks of 32): a 40-token prompt, last logits only."""
     a = Archive(synthetic_released(seed=8, tokenizer_bytes=0))
     tokens = [int(t) for t in np.random.default_rng(62).integers(0, 8192, 40)]
-    gpu, ref = NativeEngine(a), oracle.RefEngine(a)
+    gpu, ref = GpuEngine(a), oracle.RefEngine(a)
     lg, hd = gpu_prefill(gpu, tokens, last_only=True)
-    rl, rh = ref.prefill(tokens, last_only=True)
+    rl, rh = ref.prefill(tokens, last_only=True, hidden=True)
     print(f"logits max {np.abs(lg - rl).max():.2e}, hidden max {np.abs(hd - rh).max():.2e}", flush=True)
     np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL)
     np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL)
@@ -159,13 +147,13 @@ def test_prefill_released_geometry():
 def test_prefill_equals_steps(window):
     """A token's arithmetic does not depend on the launch it shares: prefill equals stepping bit for bit."""
     a = small(window, seed=6)
-    e1, e2 = NativeEngine(a), NativeEngine(a)
-    stepped = np.stack([e1.step(t) for t in PROMPT])
-    np.testing.assert_array_equal(e2.prefill(PROMPT), stepped)
-    np.testing.assert_array_equal(e2.step(4), e1.step(4))
-    e3 = NativeEngine(a, kv_cache="int8")
-    e4 = NativeEngine(a, kv_cache="int8")
-    np.testing.assert_array_equal(e3.prefill(PROMPT, last_only=True), np.stack([e4.step(t) for t in PROMPT])[-1])
+    e1, e2 = GpuEngine(a), GpuEngine(a)
+    stepped = np.stack([e1.step(t)[0] for t in PROMPT])
+    np.testing.assert_array_equal(e2.prefill(PROMPT)[0], stepped)
+    np.testing.assert_array_equal(e2.step(4)[0], e1.step(4)[0])
+    e3 = GpuEngine(a, kv_cache="int8")
+    e4 = GpuEngine(a, kv_cache="int8")
+    np.testing.assert_array_equal(e3.prefill(PROMPT, last_only=True)[0], np.stack([e4.step(t)[0] for t in PROMPT])[-1])
 
 
 def small64(window=0, seed=9):
@@ -177,23 +165,23 @@ def small64(window=0, seed=9):
 @pytest.mark.parametrize("window", [0, 8])
 @pytest.mark.parametrize("int8_kv", [False, True])
 def test_sdot_matches_reference(window, int8_kv):
-    """matmul="sdot" (engine.cpp:424-432: int8 activations x int8 centroids for 2/4-bit CQ matrices of groups
+    """matmul="int8" (engine.cpp:424-432: int8 activations x int8 centroids for 2/4-bit CQ matrices of groups
     >= 64) against the reference Engine with the same matrices on its SDOT path: a prompt through prefill, then
     steps and candidate rows. The int8 GEMVs are bit-exact for equal inputs; fp32 rounding in the glue can move
     one quantised activation code by one step, so the bar is a relative L2 error."""
     a = small64(window)
-    gpu = NativeEngine(a, matmul="sdot", kv_cache="int8" if int8_kv else "fp32")
+    gpu = GpuEngine(a, matmul="int8", kv_cache="int8" if int8_kv else "fp32")
     ref = oracle.RefEngine(a, 0, int8_kv, sdot=True)
     fp32 = oracle.RefEngine(a, 0, int8_kv)
     lg, hd = gpu_prefill(gpu, PROMPT[:20])
-    rl, rh = ref.prefill(PROMPT[:20])
+    rl, rh = ref.prefill(PROMPT[:20], hidden=True)
     fl, _ = fp32.prefill(PROMPT[:20])
     print(f"prefill: rel {rel_l2(lg, rl):.2e} (fp32 path vs SDOT path in the reference: {rel_l2(fl, rl):.2e})",
           flush=True)
     pairs = [("prefill logits", lg, rl), ("prefill hidden", hd, rh)]
     ids = np.array([9, 300, 511, 9, 0], np.int32)
     for t in (7, 123, 45):
-        g, r = gpu.step(t, return_hidden=True), ref.step(t)
+        g, r = gpu.step(t, hidden=True), ref.step(t, hidden=True)
         pairs += [(f"step {t} logits", g[0], r[0]), (f"step {t} hidden", g[1], r[1]),
                   (f"step {t} candidates", gpu_project(gpu, ids), ref.project_candidates(ids))]
     for what, g, r in pairs:
@@ -203,23 +191,23 @@ def test_sdot_matches_reference(window, int8_kv):
 
 def test_sdot_candidates_equal_full_logits():
     a = small64(0, seed=10)
-    full, sel = NativeEngine(a, matmul="sdot"), NativeEngine(a, matmul="sdot")
+    full, sel = GpuEngine(a, matmul="int8"), GpuEngine(a, matmul="int8")
     ids = np.random.default_rng(52).permutation(512)[:142].astype(np.int32)
     for t in (2, 51, 302):
-        e = full.step(t)
-        np.testing.assert_array_equal(sel.step_candidates(t, ids), e[ids])
+        e = full.step(t)[0]
+        np.testing.assert_array_equal(sel.step_candidates(t, ids)[0], e[ids])
 
 
 def test_sdot_released_geometry():
     """27 layers of the released geometry (CQ4 / CQ2, groups of 128) on the int8 path."""
     a = Archive(synthetic_released(seed=11, tokenizer_bytes=0))
-    gpu, ref = NativeEngine(a, matmul="sdot"), oracle.RefEngine(a, sdot=True)
+    gpu, ref = GpuEngine(a, matmul="int8"), oracle.RefEngine(a, sdot=True)
     lg, _ = gpu_prefill(gpu, TOKENS[:8], last_only=True)
     rl, _ = ref.prefill(TOKENS[:8], last_only=True)
     print(f"prefill rel {rel_l2(lg, rl):.2e}", flush=True)
     assert rel_l2(lg, rl) < 1e-2
     for t in (5, 77):
-        g, r = gpu.step(t), ref.step(t)[0]
+        g, r = gpu.step(t)[0], ref.step(t)[0]
         print(f"step {t}: rel {rel_l2(g, r):.2e}", flush=True)
         assert rel_l2(g, r) < 1e-2
 
@@ -231,21 +219,21 @@ def test_prefix_snapshot_restore(kv):
     both engines restore the same state, and restoring twice gives the same logits bit for bit."""
     a = small(8, seed=12)
     int8 = kv == "int8"
-    gpu, ref = NativeEngine(a, kv_cache=kv), oracle.RefEngine(a, 0, int8)
+    gpu, ref = GpuEngine(a, kv_cache=kv), oracle.RefEngine(a, 0, int8)
     ids = [int(t) for t in np.random.default_rng(23).integers(2, 500, 60)]
     gpu.reset(9)
     ref.reset(9)
     gpu_prefill(gpu, ids[:9])
     ref.prefill(ids[:9])
     gpu.cache_prefix()
-    assert ref.L.needle2_engine_cache_prefix(ref.h) == 0
+    ref.cache_prefix()
     gpu_prefill(gpu, ids[9:])
     ref.prefill(ids[9:])
     firsts = []
     for _ in range(2):
         gpu.reset_to_prefix()
-        assert gpu.position == gpu.prefix_len == 9
-        assert ref.L.needle2_engine_reset_to_prefix(ref.h) == 9
+        assert gpu.position == gpu.prefix == 9
+        assert ref.reset_to_prefix() == 9
         lg, _ = gpu_prefill(gpu, ids[20:35])
         rl, _ = ref.prefill(ids[20:35])
         firsts.append(lg)
@@ -256,53 +244,60 @@ def test_prefix_snapshot_restore(kv):
     np.testing.assert_array_equal(firsts[0], firsts[1])
     # reset() discards the snapshot (needle2/native.py:447-452)
     gpu.reset(9)
-    with pytest.raises(RuntimeError, match="no cached prefix"):
+    with pytest.raises(EngineError, match="no cached prefix"):
         gpu.reset_to_prefix()
-    with pytest.raises(ValueError, match="prefix snapshot requires"):
+    with pytest.raises(EngineError, match="prefix snapshot requires"):
         gpu.cache_prefix()
 
 
 def _dfa():
     """Four states: open (7 -> 1), exact candidates {20, 30, 40, 50} (-> 2, 2, 0, 2), exact {60} (-> 3),
-    terminal."""
+    terminal. Returns the descriptor and the arrays it points into (kept alive by the caller)."""
     import ctypes as ct
-    from openneedle_amd.engine import _DFAStateDesc
+    from openneedle_amd.engine import DFAStateDesc
     arrays = dict(types=[0, 1, 1, 4], fallback=[-1, -1, -1, -1], offsets=[0, 1, 5, 6, 6],
                   tokens=[7, 20, 30, 40, 50, 60], nexts=[1, 2, 2, 0, 2, 3])
     keep = {k: (ct.c_int * len(v))(*v) for k, v in arrays.items()}
-    desc = _DFAStateDesc(4, 0, 1, 5, 10, 11, keep["types"], keep["fallback"], keep["offsets"], keep["tokens"],
-                         keep["nexts"])
-
-    class Grammar:
-        _desc = desc
-        _keep = keep
-
-        def validate(self, vocab):
-            assert vocab > 60
-    return Grammar()
+    desc = DFAStateDesc(4, 0, 1, 5, 10, 11, keep["types"], keep["fallback"], keep["offsets"], keep["tokens"],
+                        keep["nexts"])
+    return desc, keep
 
 
 @pytest.mark.parametrize("grammar", [False, True])
 def test_decode_loop_matches_reference(grammar):
     """needle2_engine_decode_loop against the reference's (engine.cpp:1360-1497) after the same prompt: the same
     tokens, unconstrained or through a grammar with exact-candidate states."""
-    import ctypes as ct
     a = small(0, seed=13)
-    gpu, ref = NativeEngine(a), oracle.RefEngine(a)
+    gpu, ref = GpuEngine(a), oracle.RefEngine(a)
     gpu_prefill(gpu, PROMPT[:10])
     ref.prefill(PROMPT[:10])
-    g = _dfa() if grammar else None
+    desc, keep = _dfa() if grammar else (None, None)
     first = 7 if grammar else 42
-    out = gpu.decode(first, 14, g)
-    buf, count = (ct.c_int * 15)(), ct.c_int(0)
-    assert ref.L.needle2_engine_decode_loop(ref.h, first, 14, ct.addressof(g._desc) if g else None,
-                                            ct.addressof(buf), ct.addressof(count)) == 0
+    out = gpu.decode(first, 14, desc)
+    expected = ref.decode(first, 14, desc)
     print(out, flush=True)
-    assert out == list(buf[:count.value])
+    assert out == expected
     if grammar:
         assert all(t in (7, 20, 30, 40, 50, 60) for t in out[:2])
     # the state after decoding is the reference's too
-    np.testing.assert_allclose(gpu.step(3), ref.step(3)[0], atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(gpu.step(3)[0], ref.step(3)[0], atol=ATOL, rtol=RTOL)
+
+
+def test_decode_loop_with_duplicate_candidates():
+    """A grammar state may list more candidates than the vocabulary holds (duplicates are valid): the loop's
+    score buffer must hold them all. Checked against the reference's loop."""
+    import ctypes as ct
+    from openneedle_amd.engine import DFAStateDesc
+    a = small(0, seed=15)
+    n = 700  # > vocab 512
+    cands = [int(t) for t in np.random.default_rng(65).integers(0, 512, n)]
+    arrays = dict(types=[0, 1, 4], fallback=[-1, -1, -1], offsets=[0, 1, 1 + n, 1 + n],
+                  tokens=[7] + cands, nexts=[1] + [2] * n)
+    keep = {k: (ct.c_int * len(v))(*v) for k, v in arrays.items()}
+    desc = DFAStateDesc(3, 0, 1, 5, 10, 11, keep["types"], keep["fallback"], keep["offsets"], keep["tokens"],
+                        keep["nexts"])
+    gpu, ref = GpuEngine(a), oracle.RefEngine(a)
+    assert gpu.decode(7, 4, desc) == ref.decode(7, 4, desc)
 
 
 @pytest.mark.parametrize("window,prefix", [(0, 0), (8, 3)])
@@ -318,15 +313,13 @@ def test_import_matches_reference(window, prefix, kv):
     shape = (m["num_layers"], len(positions), m["num_kv_heads"], m["head_dim"])
     k = rng.standard_normal(shape).astype(np.float32)
     v = rng.standard_normal(shape).astype(np.float32)
-    gpu, ref = NativeEngine(a, kv_cache=kv), oracle.RefEngine(a, 0, kv == "int8")
-    gpu.reset(prefix)
-    gpu.import_state(ids, positions, k, v)
-    idc, pc = np.asarray(ids, np.int32), np.asarray(positions, np.int32)
-    assert ref.L.needle2_engine_import(ref.h, len(ids), prefix, idc.ctypes.data, pc.ctypes.data, len(positions),
-                                       k.ctypes.data, v.ctypes.data) == 0
+    gpu, ref = GpuEngine(a, kv_cache=kv), oracle.RefEngine(a, 0, kv == "int8")
+    for e in (gpu, ref):
+        e.reset(prefix)
+        e.import_state(ids, positions, k, v)
     assert gpu.position == 20
     for t in (5, 400, 33):
-        g, r = gpu.step(t, return_hidden=True), ref.step(t)
+        g, r = gpu.step(t, hidden=True), ref.step(t, hidden=True)
         print(f"step {t}: rel {rel_l2(g[0], r[0]):.2e}", flush=True)
         if kv == "int8":
             assert rel_l2(g[0], r[0]) < 1e-3 and rel_l2(g[1], r[1]) < 1e-3
@@ -336,18 +329,19 @@ def test_import_matches_reference(window, prefix, kv):
 
 
 def test_engine_errors():
-    e = NativeEngine(small())
-    with pytest.raises(ValueError, match="within the vocabulary"):
+    """The engine checks its own arguments (the C ABI's error channel, needle2_engine_error)."""
+    e = GpuEngine(small())
+    with pytest.raises(EngineError, match="token outside vocabulary"):
         e.step(512)
-    with pytest.raises(ValueError, match="candidate outside vocabulary"):
+    with pytest.raises(EngineError, match="candidate outside vocabulary"):
         e.step_candidates(1, [0, 512])
-    with pytest.raises(ValueError, match="activation"):  # needle2/native.py: SDOT takes fp32 activations
-        NativeEngine(small(), matmul="sdot", activation_bits=8)
-    with pytest.raises(RuntimeError, match="no cached prefix"):
+    with pytest.raises(EngineError, match="candidates must be nonempty"):
+        e.project_candidates([])
+    with pytest.raises(EngineError, match="no cached prefix"):
         e.reset_to_prefix()
     for _ in range(64):
-        e.step(1, compute_logits=False)
-    with pytest.raises(RuntimeError, match="maximum context reached"):
+        e.step(1, logits=False)
+    with pytest.raises(EngineError, match="maximum context reached"):
         e.step(1)
     assert e.kv_storage_bytes == 2 * 3 * 1 * 64 * 32 * 4
     e.set_int8_kv(True)

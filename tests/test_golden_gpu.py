@@ -9,7 +9,9 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from openneedle_amd.native import DeviceArray, KVCache, NativeCQ, synchronize
+from openneedle_amd.cq import CQMatrix
+from openneedle_amd.device import DeviceArray, synchronize
+from openneedle_amd.kv import KVCache
 
 pytestmark = pytest.mark.gpu
 
@@ -28,8 +30,8 @@ def names(prefix):
 def test_cq(name):
     f = load(name)
     rows, dim, bits, group = (int(v) for v in f["shape"])
-    q = NativeCQ(f["packed"], f["norms"].view(np.float16), (rows, dim), bits, group, f["cb"])
-    np.testing.assert_array_equal(q.linear(f["x"]), f["y"])
+    q = CQMatrix(f["packed"], f["norms"].view(np.float16), (rows, dim), bits, group, f["cb"])
+    np.testing.assert_array_equal(q.matvec(f["x"]), f["y"])
     if "ids" in f:
         np.testing.assert_array_equal(q.rows(f["ids"]), f["rows"])
 
@@ -38,8 +40,8 @@ def test_cq(name):
 def test_sdot(name):
     f = load(name)
     rows, dim, bits, group = (int(v) for v in f["shape"])
-    q = NativeCQ(f["packed"], f["norms"].view(np.float16), (rows, dim), bits, group, f["cb"])
-    np.testing.assert_array_equal(q.linear_sdot(f["x"]), f["y"])
+    q = CQMatrix(f["packed"], f["norms"].view(np.float16), (rows, dim), bits, group, f["cb"])
+    np.testing.assert_array_equal(q.matvec_int8(f["x"], reference_bound=True), f["y"])
 
 
 @pytest.mark.parametrize("name", names("attn_"))

@@ -5,7 +5,9 @@ synchronizations between the replays."""
 import numpy as np
 import pytest
 
-from openneedle_amd.native import DeviceArray, Graph, KVCache, NativeCQ, Plan, Stream, synchronize
+from openneedle_amd.cq import CQMatrix, Plan
+from openneedle_amd.device import DeviceArray, Graph, Stream, synchronize
+from openneedle_amd.kv import KVCache
 from tests.cases import activations, baseline
 
 pytestmark = pytest.mark.gpu
@@ -17,7 +19,7 @@ def layer(seed):
     mats = []
     for i in range(4):
         packed, norms, cb, _ = baseline(4, HIDDEN, HIDDEN, seed=seed + i)
-        mats.append(NativeCQ(packed, norms, (HIDDEN, HIDDEN), 4, 32, cb))
+        mats.append(CQMatrix(packed, norms, (HIDDEN, HIDDEN), 4, 32, cb))
     return mats
 
 

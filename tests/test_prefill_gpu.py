@@ -12,7 +12,8 @@ import pytest
 
 import oracle
 from openneedle_amd import formats
-from openneedle_amd.native import DeviceArray, NativeCQ, synchronize
+from openneedle_amd.cq import CQMatrix
+from openneedle_amd.device import DeviceArray, synchronize
 from tests.cases import activations, baseline, example
 
 pytestmark = pytest.mark.gpu
@@ -37,7 +38,7 @@ def normwise(got, ref):
 def test_prefill_chunk_full_size():
     """512 tokens x K 2048 through a CQ4 8192 x 2048 g32 matrix."""
     packed, norms, cb, _ = baseline(4, 8192, 2048, seed=41)
-    q = NativeCQ(packed, norms, (8192, 2048), 4, 32, cb)
+    q = CQMatrix(packed, norms, (8192, 2048), 4, 32, cb)
     x = activations((512, 2048), seed=42)
     got = gemm(q, x)
     ref = oracle.cq_linear(packed, norms, (8192, 2048), 4, 32, cb, x, 16)
@@ -55,7 +56,7 @@ def test_ragged_shapes_and_groups(bits, group, m, rows, dim):
     packed, norms, cb, dense = example(bits, rows=rows, dim=dim, group=group, seed=bits * 100 + group + m)
     norms[0] = 1  # no all-zero row: normwise checks per row
     dense = formats.dequantize_dense(packed, norms, (rows, dim), bits, group, cb)
-    q = NativeCQ(packed, norms, (rows, dim), bits, group, cb)
+    q = CQMatrix(packed, norms, (rows, dim), bits, group, cb)
     x = activations((m, dim), seed=group + m)
     got = gemm(q, x)
     ref = oracle.cq_linear(packed, norms, (rows, dim), bits, group, cb, x, 4)
@@ -68,7 +69,7 @@ def test_ragged_shapes_and_groups(bits, group, m, rows, dim):
 def test_lloyd_max_codebook():
     packed, norms, _, _ = baseline(4, 1024, 1024, group=128, seed=9)
     cb = formats.codebook(4, 128)
-    q = NativeCQ(packed, norms, (1024, 1024), 4, 128, cb)
+    q = CQMatrix(packed, norms, (1024, 1024), 4, 128, cb)
     x = activations((96, 1024), seed=10)
     ref = oracle.cq_linear(packed, norms, (1024, 1024), 4, 128, cb, x, 8)
     assert normwise(gemm(q, x), ref) <= NORMWISE
@@ -76,7 +77,7 @@ def test_lloyd_max_codebook():
 
 def test_two_bit_codes_refused():
     packed, norms, cb, _ = example(2)
-    q = NativeCQ(packed, norms, (9, 257), 2, 128, cb)
+    q = CQMatrix(packed, norms, (9, 257), 2, 128, cb)
     d = DeviceArray(4 * 257 * 2)
     with pytest.raises(RuntimeError, match="4-bit"):
         q.gemm_device(d.ptr, d.ptr, 1)

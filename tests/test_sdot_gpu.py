@@ -5,7 +5,8 @@ import numpy as np
 import pytest
 
 import oracle
-from openneedle_amd.native import DeviceArray, NativeCQ, Plan, synchronize
+from openneedle_amd.cq import CQMatrix, Plan
+from openneedle_amd.device import DeviceArray, synchronize
 from tests.cases import activations, baseline, example
 
 pytestmark = pytest.mark.gpu
@@ -24,54 +25,57 @@ def special_inputs(dim, seed):
 @pytest.mark.parametrize("rows", [9, 129])
 def test_reference_domain_bit_exact(bits, group, rows):
     packed, norms, cb, dense = example(bits, rows=rows, dim=257, group=group)
-    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
     x = special_inputs(257, seed=315)
     expected = oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x)
-    for threads in (1, 4):
-        np.testing.assert_array_equal(q.linear_sdot(x, threads), expected)
-    np.testing.assert_array_equal(q.linear_sdot(x[2]), expected[2])
+    np.testing.assert_array_equal(q.matvec_int8(x, reference_bound=True), expected)
+    np.testing.assert_array_equal(q.matvec_int8(x[2], reference_bound=True), expected[2])
 
 
 def test_reference_group_bounds():
+    """needle2_sdot_create keeps the reference's groups (sdot.cpp:351-354); needle2_sdot_linear refuses
+    non-finite inputs (the reference's loader does, needle2/native.py:249-250) and poisons y with NaN."""
+    from openneedle_amd._ffi import GpuError
     packed, norms, cb, dense = example(4, group=32)
-    q = NativeCQ(packed, norms, dense.shape, 4, 32, cb)
-    with pytest.raises(ValueError, match="between 64 and 131072"):
-        q.linear_sdot(np.ones(257, np.float32))
-    with pytest.raises(ValueError, match="finite"):
-        NativeCQ(*example(4)[:2], (9, 257), 4, 128, example(4)[2]).linear_sdot(np.full(257, np.nan, np.float32))
+    q = CQMatrix(packed, norms, dense.shape, 4, 32, cb)
+    with pytest.raises(GpuError, match="group"):
+        q.matvec_int8(np.ones(257, np.float32), reference_bound=True)
+    q128 = CQMatrix(*example(4)[:2], (9, 257), 4, 128, example(4)[2])
+    with pytest.raises(GpuError, match="finite"):
+        q128.matvec_int8(np.full(257, np.nan, np.float32), reference_bound=True)
 
 
 @pytest.mark.parametrize("bits,group", [(4, 8), (4, 16), (4, 32), (2, 16), (2, 32), (4, 256), (2, 512), (4, 1024)])
 def test_extended_groups_bit_exact(bits, group):
     packed, norms, cb, dense = example(bits, rows=300, dim=1000, group=group, seed=group + bits)
-    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
     x = special_inputs(1000, seed=group)
-    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
+    np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
 
 
 def test_subnormal_scale_guard():
     packed, norms, cb, dense = example(4, rows=4, dim=64, group=32)
-    q = NativeCQ(packed, norms, dense.shape, 4, 32, cb)
+    q = CQMatrix(packed, norms, dense.shape, 4, 32, cb)
     x = np.zeros(64, np.float32)
     x[:32] = np.float32(4e-45)
     x[40] = np.float32(1e-39)
-    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, dense.shape, 4, 32, cb, x))
+    np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, 4, 32, cb, x))
 
 
 @pytest.mark.parametrize("batch", [1, 4, 16])
 def test_int8_4096_square_batches(batch):
     """CQ4 4096 x 4096 g32, activations quantized per group after the FWHT."""
     packed, norms, cb, _ = baseline(4, 4096, 4096, seed=33)
-    q = NativeCQ(packed, norms, (4096, 4096), 4, 32, cb)
+    q = CQMatrix(packed, norms, (4096, 4096), 4, 32, cb)
     x = activations((batch, 4096), seed=batch)
-    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, (4096, 4096), 4, 32, cb, x, 8))
+    np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, (4096, 4096), 4, 32, cb, x, 8))
 
 
 def test_int8_plan_many_matrices():
     mats, d_x, d_y, expected = [], [], [], []
     for i in range(3):
         packed, norms, cb, _ = baseline(4, 512 + 64 * i, 1024, seed=500 + i)
-        m = NativeCQ(packed, norms, (512 + 64 * i, 1024), 4, 32, cb)
+        m = CQMatrix(packed, norms, (512 + 64 * i, 1024), 4, 32, cb)
         x = activations((2, 1024), seed=600 + i)
         mats.append(m)
         expected.append(oracle.sdot_linear(packed, norms, m.shape, 4, 32, cb, x))
@@ -98,13 +102,13 @@ def test_int8_batched_tiles_bit_exact(bits, group, batch, mode, monkeypatch):
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "never")
         monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", mode)
     packed, norms, cb, dense = example(bits, rows=300, dim=1000, group=group, seed=7 * batch + group)
-    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
     x = activations((batch, 1000), seed=batch)
     x[0] = 0
     if batch > 2:
         x[2] = 0
         x[2, 5] = 1
-    np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
+    np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
 
 
 @pytest.mark.parametrize("mode", ["always", "auto"])
@@ -116,7 +120,7 @@ def test_int8_plan_decode_batch(mode, monkeypatch):
     d_in = DeviceArray.from_host(x)
     for i in range(3):
         packed, norms, cb, _ = baseline(4, 512, 512, seed=700 + i)
-        m = NativeCQ(packed, norms, (512, 512), 4, 32, cb)
+        m = CQMatrix(packed, norms, (512, 512), 4, 32, cb)
         mats.append(m)
         expected.append(oracle.sdot_linear(packed, norms, m.shape, 4, 32, cb, x))
         d_y.append(DeviceArray(64 * 4 * 512))
@@ -142,7 +146,7 @@ def test_int8_single_row_kernels_bit_exact(bits, group, dim, mode, monkeypatch):
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "never")
         monkeypatch.setenv("NEEDLE2_GPU_INT8_ROW", mode)
     packed, norms, cb, dense = example(bits, rows=300, dim=dim, group=group, seed=dim + group)
-    q = NativeCQ(packed, norms, dense.shape, bits, group, cb)
+    q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
     for x in special_inputs(dim, seed=group + 1):
-        np.testing.assert_array_equal(q.linear_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group,
+        np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group,
                                                                            cb, x[None])[0])
