@@ -126,6 +126,16 @@ void *needle2_gpu_sdot_create_device(const uint8_t *d_packed, const uint16_t *d_
 int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream);
 int needle2_gpu_sdot_linear_device(void *sdot_handle, const float *d_x, float *d_y, int batch, void *stream);
 
+/* No counterpart in the reference: needle2_gpu_sdot_linear_device for callers
+ * that cannot allocate (work captured into a HIP graph, serving loops that
+ * forbid allocation). The same kernels, with the quantized activations and
+ * scales in a static 4 MiB device array the library holds per GPU until the
+ * process ends; nothing is allocated. stream NULL: the null stream. Returns -1
+ * when batch * (padded input + 8 * groups) bytes (each part rounded up to 256)
+ * exceed 4 MiB, or for groups above 16384. All calls on one GPU share the
+ * array: calls that overlap in time on one GPU race. */
+int needle2_gpu_sdot_linear_device_noalloc(void *sdot_handle, const float *d_x, float *d_y, int batch, void *stream);
+
 /* Candidate rows (replaces the CQ and SDOT branches of
  * Engine::project_candidates, needle2/csrc/engine.cpp:1302-1349, behind
  * needle2_engine_project_candidates, engine.cpp:1530): y[i] = row ids[i] of

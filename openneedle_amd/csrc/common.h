@@ -149,6 +149,9 @@ __host__ __device__ inline size_t norm_index(int r, int g, int groups) {
 // Groups up to 64 take a batched pre-pass (launch_rot_many) ahead of the
 // quarter-split GEMV; groups above one window use the generic transform pass.
 inline bool gemv_fuses_fwht(int group) { return group > 64 && group <= kWindow; }
+
+// Largest group the int8 path's one-launch prepare (FWHT + quantize in LDS) takes.
+constexpr int kSdotFusedPrepareMaxGroup = 16384;
 inline bool gemv_prepass(int group) { return group <= 64; }
 
 struct CqJob {

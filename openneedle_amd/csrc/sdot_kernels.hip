@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void sdot_quantize_kernel(const float *__restr
 // (a + b, a - b), then one multiply by 1/sqrt(group)), so the rotated values,
 // and from them the int8 codes and scales, are bit-identical to a separate
 // transform followed by sdot_quantize_kernel. seg = max(group, 1024).
-constexpr int kPrepareMaxGroup = 16384;
+constexpr int kPrepareMaxGroup = kSdotFusedPrepareMaxGroup;
 constexpr int kPrepareMinSeg = 1024;
 
 __global__ __launch_bounds__(256) void sdot_prepare_kernel(const float *__restrict__ x0,
