@@ -157,7 +157,8 @@ int needle2_gpu_sdot_candidates_device(void *sdot_handle, const float *d_x, cons
  * chunks): d_y[m][out] = FWHT-domain product of d_x[m][in] (device fp32) on
  * fp16 MFMA with fp32 accumulation; activations and cb*norm weights are
  * rounded to fp16 (agreement with needle2_cq_linear about 1e-3 normwise).
- * 4-bit codes (CQ4, CQ3) only. The _timed form (a timing aid, no reference
+ * Every storage width: 2-bit and ternary codes are widened to 4-bit codes in
+ * device memory on the first call (kept with the handle). The _timed form (a timing aid, no reference
  * counterpart) records two events around `repeat` back-to-back launches of
  * the GEMM kernel after one activation transform. */
 int needle2_gpu_cq_gemm_device(void *cq_handle, const float *d_x, float *d_y, int m, void *stream);

@@ -15,6 +15,7 @@
 #include <limits>
 #include <memory>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 namespace nd {
@@ -239,15 +240,25 @@ void CqHandle::candidates_host(const float *x, const int32_t *ids, int count, fl
 void CqHandle::gemm_device(const float *d_x, float *d_y, int m_rows, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1,
                            int repeat) {
     if (m_rows <= 0) return;
-    ND_CHECK(m.kind == kNib, "prefill GEMM: 4-bit (CQ4 / CQ3) codes only");
     ND_CHECK(prefill_xf_halves(m_rows, m.dev) * 2 < (size_t(1) << 31), "prefill GEMM: m * padded input must be < 2^30");
+    const uint4 *c4 = m.codes.p;
+    if (m.kind == kCrumb) {  // CQ2 / ternary: the GEMM reads 4-bit codes, widened once
+        if (!codes4.p) {
+            DevBuf<uint4> wide;
+            wide.reserve(size_t(m.n_pad) * m.chunks * 2);
+            launch_widen_crumbs(m.codes.p, m.chunks, m.n_pad, wide.p, s);
+            std::swap(codes4.p, wide.p);
+            std::swap(codes4.n, wide.n);
+        }
+        c4 = codes4.p;
+    }
     st.xh.reserve(prefill_xf_halves(m_rows, m.dev));
     launch_prefill_transform(d_x, m_rows, m.in, m.padded, m.dev, m.group, m.scale, st.xh.p, s);
     uint16_t cbh[16];
     for (int i = 0; i < 16; ++i) cbh[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(m.lut[i]));
     if (ev0) ND_HIP(hipEventRecord(ev0, s));
     for (int r = 0; r < repeat; ++r)
-        launch_prefill_gemm(m.geom(), m.codes.p, m.norms.p, m.out, st.xh.p, m_rows, m.dev, m.padded, cbh, d_y, s);
+        launch_prefill_gemm(m.geom(), c4, m.dev / 32, m.norms.p, m.out, st.xh.p, m_rows, m.dev, m.padded, cbh, d_y, s);
     if (ev1) ND_HIP(hipEventRecord(ev1, s));
 }
 

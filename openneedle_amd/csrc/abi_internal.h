@@ -14,8 +14,12 @@ void launch_copy(const void *src, void *dst, size_t bytes, hipStream_t s);
 size_t prefill_xf_halves(int m, int dev);
 void launch_prefill_transform(const float *x, int m, int in, int padded, int dev, int group, float scale,
                               _Float16 *xf, hipStream_t s);
-void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes, const uint16_t *norms, int rows, const _Float16 *xf,
-                         int m, int dev, int padded, const uint16_t *cb_half, float *y, hipStream_t s);
+// codes4: the matrix's codes as 4-bit device codes (chunks4 = dev / 32 chunks per row tile row)
+void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes4, int chunks4, const uint16_t *norms, int rows,
+                         const _Float16 *xf, int m, int dev, int padded, const uint16_t *cb_half, float *y,
+                         hipStream_t s);
+// 2-bit device codes of n_pad rows -> the same positions as 4-bit device codes (for the prefill GEMM)
+void launch_widen_crumbs(const uint4 *codes2, int chunks2, int n_pad, uint4 *codes4, hipStream_t s);
 
 // Runs f, converting exceptions into -1 plus the thread-local message. The
 // message is cleared first so a non-empty needle2_gpu_error() after a call
@@ -98,6 +102,7 @@ void upload_candidates(Staging &st, const int32_t *ids, int count, int rows);
 struct CqHandle {
     Matrix m;
     Staging st;
+    DevBuf<uint4> codes4;  // 2-bit matrices: the codes widened to 4 bits for the prefill GEMM (built on first use)
     void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
     // the GEMV over rows [0, rows) of a device-layout matrix with m's geometry
     void gemv(const uint4 *codes, const uint16_t *norms, int rows, int n_pad, const float *d_x, float *d_y, int batch,

@@ -24,6 +24,9 @@
 //    per byte of codes) from LDS, one private column per lane so the reads
 //    are conflict-free: 4 v_perm + 4 ds_read_b32 + 4 v_pk_mul_f16 per 8 codes.
 //
+// 2-bit (CQ2, ternary) matrices are widened once to 4-bit device codes of the
+// same positions (widen_crumbs_kernel), so one kernel serves every width.
+//
 // Rounding: X and the weights cb*norm are fp16 (two roundings for the
 // weight), products and sums are fp32 in the MFMA; the result agrees with the
 // reference FP32 path to about 1e-3 normwise (bound 2e-3).
@@ -498,20 +501,21 @@ void launch_prefill_transform(const float *x, int m, int in, int padded, int dev
     ND_HIP(hipGetLastError());
 }
 
-void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes, const uint16_t *norms, int rows, const _Float16 *xf,
-                         int m, int dev, int padded, const uint16_t *cb_half, float *y, hipStream_t s) {
+void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes4, int chunks4, const uint16_t *norms, int rows,
+                         const _Float16 *xf, int m, int dev, int padded, const uint16_t *cb_half, float *y,
+                         hipStream_t s) {
     if (m <= 0) return;
-    ND_CHECK(geom.kind == kNib, "prefill GEMM: 4-bit (CQ4 / CQ3) codes only");
     ND_CHECK(geom.group >= 8, "prefill GEMM: groups of 8 or more");
+    ND_CHECK(chunks4 * 32 == dev, "internal: prefill GEMM takes 4-bit codes (32 per chunk)");
     GemmArgs g{};
     g.xf = xf;
-    g.codes = codes;
+    g.codes = codes4;
     g.norms = norms;
     g.y = y;
     g.m = m;
     g.rb_count = (m + 31) / 32;
     g.rows = rows;
-    g.chunks = geom.chunks;
+    g.chunks = chunks4;
     g.groups = geom.groups;
     g.group_shift = __builtin_ctz(static_cast<unsigned>(geom.group));
     g.xsteps = dev / kBK;
@@ -525,6 +529,48 @@ void launch_prefill_gemm(const CqGeom &geom, const uint4 *codes, const uint16_t 
     case 4: hipLaunchKernelGGL(prefill_gemm_kernel<2>, grid, block, 0, s, g); break;
     default: hipLaunchKernelGGL(prefill_gemm_kernel<1>, grid, block, 0, s, g); break;
     }
+    ND_HIP(hipGetLastError());
+}
+
+namespace {
+
+// 2-bit device codes -> 4-bit device codes of the same positions (crumb i of
+// a byte becomes nibble i): the prefill GEMM's input for CQ2 and ternary
+// matrices. One thread per (row tile, 32-position chunk, row).
+__global__ __launch_bounds__(256) void widen_crumbs_kernel(const uint4 *__restrict__ src, int chunks2,
+                                                           uint4 *__restrict__ dst, int chunks4) {
+    const size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int row = static_cast<int>(idx % kRowsPerBlock);
+    const size_t tc = idx / kRowsPerBlock;
+    const int c4 = static_cast<int>(tc % chunks4);
+    const size_t tile = tc / chunks4;
+    const uint4 in = src[(tile * chunks2 + c4 / 2) * kRowsPerBlock + row];
+    const uint32_t half[2] = {(c4 & 1) ? in.z : in.x, (c4 & 1) ? in.w : in.y};  // bytes 8 (c4 % 2) .. + 8
+    uint32_t out[4];
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            uint32_t r = 0;
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const uint32_t byte = (half[d] >> (8 * (2 * k + b))) & 0xFFu;
+                const uint32_t nib = (byte & 3u) | ((byte >> 2) & 3u) << 4 | ((byte >> 4) & 3u) << 8 |
+                                     ((byte >> 6) & 3u) << 12;
+                r |= nib << (16 * b);
+            }
+            out[2 * d + k] = r;
+        }
+    dst[idx] = uint4{out[0], out[1], out[2], out[3]};
+}
+
+}  // namespace
+
+void launch_widen_crumbs(const uint4 *codes2, int chunks2, int n_pad, uint4 *codes4, hipStream_t s) {
+    const int chunks4 = 2 * chunks2;
+    const size_t total = static_cast<size_t>(n_pad) * chunks4;  // n_pad is a multiple of 256
+    hipLaunchKernelGGL(widen_crumbs_kernel, dim3(static_cast<unsigned>(total / 256)), dim3(256), 0, s, codes2, chunks2,
+                       codes4, chunks4);
     ND_HIP(hipGetLastError());
 }
 

@@ -49,7 +49,7 @@ def test_prefill_chunk_full_size():
     assert rows.max() <= NORMWISE, rows.max()
 
 
-@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("bits", [2, 3, 4, 5])
 @pytest.mark.parametrize("group", [8, 16, 32, 64, 128, 256, 1024])
 @pytest.mark.parametrize("m,rows,dim", [(1, 33, 200), (37, 300, 1000), (130, 129, 512)])
 def test_ragged_shapes_and_groups(bits, group, m, rows, dim):
@@ -75,9 +75,13 @@ def test_lloyd_max_codebook():
     assert normwise(gemm(q, x), ref) <= NORMWISE
 
 
-def test_two_bit_codes_refused():
-    packed, norms, cb, _ = example(2)
-    q = CQMatrix(packed, norms, (9, 257), 2, 128, cb)
-    d = DeviceArray(4 * 257 * 2)
-    with pytest.raises(RuntimeError, match="4-bit"):
-        q.gemm_device(d.ptr, d.ptr, 1)
+def test_released_layer_shapes_cq2():
+    """The released model's layer projections are CQ2 g128 (q 512 x 512, k / v 256 x 512): a 32-token chunk."""
+    for rows in (512, 256):
+        packed, norms, _, _ = baseline(2, rows, 512, group=128, seed=rows)
+        cb = formats.codebook(2, 128)
+        q = CQMatrix(packed, norms, (rows, 512), 2, 128, cb)
+        x = activations((32, 512), seed=rows + 1)
+        ref = oracle.cq_linear(packed, norms, (rows, 512), 2, 128, cb, x, 8)
+        assert normwise(gemm(q, x), ref) <= NORMWISE
+        assert normwise(gemm(q, x), ref) <= NORMWISE  # the widened codes are reused
