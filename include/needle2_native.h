@@ -126,6 +126,13 @@ void *needle2_gpu_sdot_create_device(const uint8_t *d_packed, const uint16_t *d_
 int needle2_gpu_cq_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream);
 int needle2_gpu_sdot_linear_device(void *sdot_handle, const float *d_x, float *d_y, int batch, void *stream);
 
+/* The int32 group dots of the int8 product (the accumulators of SdotCQ::dot_group,
+ * needle2/csrc/sdot.cpp:108-137): d_dots[b][row][g] = sum over group g of
+ * centroid(code) * q(x_b), from the kernels needle2_gpu_sdot_linear_device runs
+ * for this batch on a large matrix (batch 1: the row kernel; 2 or more: the
+ * 4x4x4 batch-tile MFMA kernel). Groups of 8 .. 256. */
+int needle2_gpu_sdot_dots_device(void *sdot_handle, const float *d_x, int32_t *d_dots, int batch, void *stream);
+
 /* No counterpart in the reference: needle2_gpu_sdot_linear_device for callers
  * that cannot allocate (work captured into a HIP graph, serving loops that
  * forbid allocation). The same kernels, with the quantized activations and

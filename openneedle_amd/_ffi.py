@@ -63,6 +63,7 @@ SIGNATURES: dict[str, tuple] = {
     "needle2_gpu_cq_linear_device": (i32, [vp, vp, vp, i32, vp]),
     "needle2_gpu_sdot_linear_device": (i32, [vp, vp, vp, i32, vp]),
     "needle2_gpu_sdot_linear_device_noalloc": (i32, [vp, vp, vp, i32, vp]),
+    "needle2_gpu_sdot_dots_device": (i32, [vp, vp, vp, i32, vp]),
     "needle2_gpu_cq_candidates": (i32, [vp, vp, vp, i32, vp]),
     "needle2_gpu_cq_candidates_device": (i32, [vp, vp, vp, i32, vp, vp]),
     "needle2_gpu_sdot_candidates": (i32, [vp, vp, vp, i32, vp]),

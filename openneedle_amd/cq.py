@@ -242,6 +242,11 @@ class CQMatrix:
         check(self._lib.needle2_gpu_sdot_linear_device(self.int8_handle(), addr(d_x), addr(d_y), int(batch),
                                                        stream_ptr(stream)), "int8 matvec (device)")
 
+    def int8_dots_device(self, d_x, d_dots, batch: int, stream=None) -> None:
+        """The int32 group dots of the int8 product, ``d_dots[b][row][group]`` (device int32)."""
+        check(self._lib.needle2_gpu_sdot_dots_device(self.int8_handle(), addr(d_x), addr(d_dots), int(batch),
+                                                     stream_ptr(stream)), "int8 dots (device)")
+
     def select_device(self, d_x, d_ids, count: int, d_y, stream=None, *, int8: bool = False) -> None:
         if int8:
             check(self._lib.needle2_gpu_sdot_candidates_device(self.int8_handle(), addr(d_x), addr(d_ids),

@@ -348,6 +348,16 @@ void SdotHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t
     launch_sdot_gemv(geom(), job, nullptr, 0, m.n_pad / kRowsPerBlock, batch, s);
 }
 
+void SdotHandle::dots_device(const float *d_x, int32_t *d_dots, int batch, hipStream_t s) {
+    if (batch <= 0) return;
+    st.q.reserve(size_t(batch) * m.dev / 4);
+    st.xs.reserve(size_t(batch) * m.groups);
+    st.xst.reserve(size_t(batch) * m.groups);
+    prepare_device(d_x, batch, st.q.p, st.xs.p, st.xst.p, s);
+    const SdotJob job{m.codes.p, m.norms.p, st.q.p, st.xs.p, nullptr, m.out, m.n_pad, 0, batch, st.xst.p};
+    launch_sdot_dots(geom(), job, m.n_pad / kRowsPerBlock, batch, d_dots, s);
+}
+
 void SdotHandle::candidates_device(const float *d_x, const int32_t *d_ids, int count, float *d_y, hipStream_t s) {
     if (count <= 0) return;
     const Candidates c = gather_candidates(m, st, d_ids, count, s);
@@ -717,6 +727,16 @@ int needle2_gpu_cq_gemm_timed(void *handle, const float *d_x, float *d_y, int m,
 int needle2_gpu_sdot_linear_device(void *handle, const float *d_x, float *d_y, int batch, void *stream) {
     auto *h = static_cast<SdotHandle *>(handle);
     return guarded([&] { h->run_device(d_x, d_y, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream()); });
+}
+
+// The int32 group dots of the int8 product (sdot.cpp:108-137): d_dots[b][row][g],
+// from the kernels the GEMV runs for this batch on a large matrix.
+int needle2_gpu_sdot_dots_device(void *handle, const float *d_x, int32_t *d_dots, int batch, void *stream) {
+    return guarded([&] {
+        ND_CHECK(handle && d_x && d_dots, "int8 dots: null argument");
+        auto *h = static_cast<SdotHandle *>(handle);
+        h->dots_device(d_x, d_dots, batch, stream ? static_cast<hipStream_t>(stream) : h->st.stream());
+    });
 }
 
 // Candidate rows: y[i] = row ids[i] of the product for one input vector, as

@@ -129,6 +129,8 @@ struct SdotHandle {
     SdotGeom geom() const;
     void prepare_device(const float *d_x, int batch, int32_t *q, float *xs, float *xst, hipStream_t s);
     void run_device(const float *d_x, float *d_y, int batch, hipStream_t s);
+    // d_dots[b][row][g] = the int32 group dots of the int8 product (sdot.cpp:108-137)
+    void dots_device(const float *d_x, int32_t *d_dots, int batch, hipStream_t s);
     // d_y[i] = row d_ids[i] of the int8 product for batch-1 x (engine.cpp:1307-1349, the SDOT branch)
     void candidates_device(const float *d_x, const int32_t *d_ids, int count, float *d_y, hipStream_t s);
     void candidates_host(const float *x, const int32_t *ids, int count, float *y);

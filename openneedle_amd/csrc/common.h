@@ -232,5 +232,9 @@ void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded
 // The batch (uniform across jobs) is processed in tiles that decode each code once.
 void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs_dev, int njobs, int total_blocks,
                       int batch, hipStream_t s);
+// The same products' int32 group dots, dots[b][row][g], from the kernels the GEMV runs for this batch on a
+// large matrix (batch 1: the row kernel; 2 or more: the 4 x 4 x 4 batch-tile kernel); one job only.
+void launch_sdot_dots(const SdotGeom &g, const SdotJob &job0, int total_blocks, int batch, int32_t *dots,
+                      hipStream_t s);
 
 }  // namespace nd

@@ -21,6 +21,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 namespace nd {
 
@@ -634,22 +635,23 @@ struct RowSlot {
 
 template <int KIND, int GROUP>
 __device__ __forceinline__ void row_load(RowSlot<KIND, GROUP> &sl, __amdgpu_buffer_rsrc_t codes,
-                                         __amdgpu_buffer_rsrc_t norms, int c) {
+                                         __amdgpu_buffer_rsrc_t norms, int c, int groups) {
     using S = RowSlot<KIND, GROUP>;
     sl.code = __builtin_amdgcn_raw_buffer_load_b128(codes, threadIdx.x * 16u,
                                                    __builtin_amdgcn_readfirstlane(c * kRowsPerBlock * 16), 0);
 #pragma unroll
     for (int k = 0; k < S::kNorms; ++k) {
-        const int g = c * S::kCodes / GROUP + k;  // the chunk's group (GROUP >= chunk) or its k-th group
+        // the chunk's group (GROUP >= chunk) or its k-th group; phantom groups past the last read the last
+        const int g = min(c * S::kCodes / GROUP + k, groups - 1);
         sl.norm[k] = __builtin_amdgcn_raw_buffer_load_b16(
             norms, threadIdx.x * 2u, __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2), 0);
     }
 }
 
-template <int KIND, int GROUP>
+template <int KIND, int GROUP, bool DOTS>
 __device__ __forceinline__ void row_compute(const RowSlot<KIND, GROUP> &sl, const uint32_t *lq, const float *lxs,
                                             const uint32_t cent[4], float cs, int c, int groups, float &value,
-                                            int &dot) {
+                                            int &dot, int32_t *dots_row) {
     using S = RowSlot<KIND, GROUP>;
     const uint32_t words[4] = {sl.code.x, sl.code.y, sl.code.z, sl.code.w};
 #pragma unroll
@@ -675,17 +677,21 @@ __device__ __forceinline__ void row_compute(const RowSlot<KIND, GROUP> &sl, cons
             const int k = GROUP >= S::kCodes ? 0 : (d + 1) * kPer / GROUP - 1;
             const int g = pos_end / GROUP - 1;
             if (g < groups) {
-                const float ns = h2f(sl.norm[k]) * cs;  // sdot.cpp:43-44
-                value = value + (static_cast<float>(dot) * ns) * lxs[g];
+                if constexpr (DOTS) {
+                    if (dots_row) dots_row[g] = dot;
+                } else {
+                    const float ns = h2f(sl.norm[k]) * cs;  // sdot.cpp:43-44
+                    value = value + (static_cast<float>(dot) * ns) * lxs[g];
+                }
             }
             dot = 0;
         }
     }
 }
 
-template <int KIND, int GROUP>
+template <int KIND, int GROUP, bool DOTS>
 __global__ __launch_bounds__(kRowsPerBlock) void sdot_row_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
-                                                                int njobs, SdotGeom geom) {
+                                                                int njobs, SdotGeom geom, int32_t *__restrict__ dots) {
     using S = RowSlot<KIND, GROUP>;
     extern __shared__ __attribute__((aligned(16))) uint32_t row_lds[];
     const int blk = blockIdx.x;
@@ -717,7 +723,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_row_kernel(SdotJob job0, c
     const int nch = (groups * GROUP + S::kCodes - 1) / S::kCodes;  // chunks holding real positions
     RowSlot<KIND, GROUP> ring[kRowRing];
 #pragma unroll
-    for (int k = 0; k < kRowRing; ++k) row_load(ring[k], codes, norms, k);
+    for (int k = 0; k < kRowRing; ++k) row_load(ring[k], codes, norms, min(k, nch - 1), groups);
     // stage the activation row and its group scales
     const u32x4 *q4 = reinterpret_cast<const u32x4 *>(J.q);
     for (int i = threadIdx.x; i < dev / 16; i += kRowsPerBlock) reinterpret_cast<u32x4 *>(lq)[i] = q4[i];
@@ -725,40 +731,424 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_row_kernel(SdotJob job0, c
     __syncthreads();
     float value = 0.0f;
     int dot = 0;
+    int32_t *dots_row = DOTS && row < J.rows ? dots + static_cast<size_t>(row) * groups : nullptr;
     int c0 = 0;
     for (; c0 + kRowRing <= nch; c0 += kRowRing) {
 #pragma unroll
         for (int k = 0; k < kRowRing; ++k) {
-            row_compute(ring[k], lq, lxs, cent, cs, c0 + k, groups, value, dot);
-            row_load(ring[k], codes, norms, c0 + k + kRowRing);
+            row_compute<KIND, GROUP, DOTS>(ring[k], lq, lxs, cent, cs, c0 + k, groups, value, dot, dots_row);
+            row_load(ring[k], codes, norms, min(c0 + k + kRowRing, nch - 1), groups);
         }
     }
 #pragma unroll
     for (int k = 0; k < kRowRing; ++k)
-        if (c0 + k < nch) row_compute(ring[k], lq, lxs, cent, cs, c0 + k, groups, value, dot);
-    if (row < J.rows) ((ND_GLOBAL float *)J.y)[row] = value;
+        if (c0 + k < nch) row_compute<KIND, GROUP, DOTS>(ring[k], lq, lxs, cent, cs, c0 + k, groups, value, dot, dots_row);
+    if (!DOTS && row < J.rows) ((ND_GLOBAL float *)J.y)[row] = value;
 }
 
-template <int KIND>
+template <int KIND, bool DOTS>
 void launch_sdot_row(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
-                     hipStream_t s) {
+                     int32_t *dots, hipStream_t s) {
     const int dev = g.windows * kWindow;
     const size_t lds = static_cast<size_t>(dev) + static_cast<size_t>(g.groups) * 4;
     dim3 grid(blocks), block(kRowsPerBlock);
     switch (g.group) {
     case 8:
         if constexpr (KIND == kNib) {
-            hipLaunchKernelGGL((sdot_row_kernel<KIND, 8>), grid, block, lds, s, job0, jobs, njobs, g);
+            hipLaunchKernelGGL((sdot_row_kernel<KIND, 8, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots);
             break;
         }
         [[fallthrough]];
-    case 16: hipLaunchKernelGGL((sdot_row_kernel<KIND, 16>), grid, block, lds, s, job0, jobs, njobs, g); break;
-    case 32: hipLaunchKernelGGL((sdot_row_kernel<KIND, 32>), grid, block, lds, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL((sdot_row_kernel<KIND, 64>), grid, block, lds, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL((sdot_row_kernel<KIND, 128>), grid, block, lds, s, job0, jobs, njobs, g); break;
-    default: hipLaunchKernelGGL((sdot_row_kernel<KIND, 256>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    case 16: hipLaunchKernelGGL((sdot_row_kernel<KIND, 16, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+    case 32: hipLaunchKernelGGL((sdot_row_kernel<KIND, 32, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+    case 64: hipLaunchKernelGGL((sdot_row_kernel<KIND, 64, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+    case 128: hipLaunchKernelGGL((sdot_row_kernel<KIND, 128, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+    default: hipLaunchKernelGGL((sdot_row_kernel<KIND, 256, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
     }
     ND_HIP(hipGetLastError());
+}
+
+// ---------------------------------------------------------------------------
+// int8 GEMV for batch tiles of 2 .. 16 rows, one thread per output row.
+//
+// As the row kernel (codes streamed through a register ring, decoded once
+// per code dword with v_perm_b32), but the products of a decoded code dword
+// with the tile's batch rows run on v_mfma_i32_4x4x4_16b_i8 instead of one
+// v_dot4_i32_i8 per batch row: in each of its 16 blocks, block l / 4 of lane
+// l, the matrix instruction takes 4 activations of batch row l % 4 (A) and
+// the 4 centroids lane l decoded for its own weight row (B), so accumulator
+// register r of lane l is the dot of weight row l with batch row r of the
+// quad. One quad of batch rows per 4 x 4 x 4 product; NQ quads per tile. The
+// tile's permuted int8 activations and group scales are staged in LDS once
+// per workgroup; after that barrier the waves never synchronise again. Each
+// group closes with the reference's epilogue for every batch row of the tile
+//   value += (float(dot) * (half(norm) * cs)) * x_scale[g]
+// in group order (sdot.cpp:43-44, 142-149): bit-identical outputs. With
+// DOTS the int32 group dots themselves are stored (dots[b][row][g]).
+// ---------------------------------------------------------------------------
+constexpr int kQuadMaxLds = 160 * 1024;
+
+template <int KIND, int GROUP, int NQ, bool DOTS>
+__global__ __launch_bounds__(kRowsPerBlock) void sdot_quad_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+                                                                 int njobs, SdotGeom geom, int32_t *__restrict__ dots) {
+    using S = RowSlot<KIND, GROUP>;
+    constexpr int TB = 4 * NQ;  // batch rows of the tile
+    extern __shared__ __attribute__((aligned(16))) uint32_t quad_lds[];
+    const int blk = blockIdx.x;
+    SdotJob J = job0;
+    if (njobs > 0) {
+        const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
+        const int j = find_job(cj, njobs, blk);
+        J.codes = cj[j].codes;
+        J.norms = cj[j].norms;
+        J.q = cj[j].q;
+        J.xs = cj[j].xs;
+        J.y = cj[j].y;
+        J.rows = cj[j].rows;
+        J.block_begin = cj[j].block_begin;
+        J.batch = cj[j].batch;
+    }
+    const int tile = blk - J.block_begin;
+    const int row = tile * kRowsPerBlock + threadIdx.x;
+    const int groups = geom.groups;
+    const int dev = geom.windows * kWindow;
+    const int qdw = dev / 4;  // activation dwords per batch row
+    const int b0 = static_cast<int>(blockIdx.y) * TB;
+    const int nb = min(TB, J.batch - b0);  // valid batch rows of the tile (uniform)
+    uint32_t *lq = quad_lds;
+    float *lxs = reinterpret_cast<float *>(quad_lds + TB * qdw);
+    const uint32_t cent[4] = {geom.cent[0], geom.cent[1], geom.cent[2], geom.cent[3]};
+    const float cs = geom.centroid_scale;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms + static_cast<size_t>(tile) * groups * kRowsPerBlock,
+                                                     static_cast<uint32_t>(groups) * kRowsPerBlock * 2u);
+    const int nch = (groups * GROUP + S::kCodes - 1) / S::kCodes;  // chunks holding real positions
+    RowSlot<KIND, GROUP> ring[kRowRing];
+#pragma unroll
+    for (int k = 0; k < kRowRing; ++k) row_load(ring[k], codes, norms, min(k, nch - 1), groups);
+    // stage the tile's activation rows and group scales (rows past the batch as zeros)
+    const u32x4 *q4 = reinterpret_cast<const u32x4 *>(J.q) + static_cast<size_t>(b0) * (qdw / 4);
+    for (int i = threadIdx.x; i < TB * qdw / 4; i += kRowsPerBlock)
+        reinterpret_cast<u32x4 *>(lq)[i] = i / (qdw / 4) < nb ? q4[i] : u32x4{0, 0, 0, 0};
+    for (int i = threadIdx.x; i < TB * groups; i += kRowsPerBlock)
+        lxs[i] = i / groups < nb ? J.xs[static_cast<size_t>(b0) * groups + i] : 0.0f;
+    __syncthreads();
+    const int lb = threadIdx.x & 3;  // the batch row of each quad this lane feeds to the matrix instruction
+    float value[TB];
+#pragma unroll
+    for (int b = 0; b < TB; ++b) value[b] = 0.0f;
+    v4i acc[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) acc[q] = v4i{0, 0, 0, 0};
+    auto chunk = [&](const RowSlot<KIND, GROUP> &sl, int c) {
+        constexpr int QPC = KIND == kNib ? 8 : 16;  // activation dwords per chunk
+        const uint32_t words[4] = {sl.code.x, sl.code.y, sl.code.z, sl.code.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            uint32_t wq[4];  // the centroid dwords of this code dword, in activation-dword order
+            constexpr int W = KIND == kNib ? 2 : 4;
+            if constexpr (KIND == kNib) {
+                decode_nib(words[d], cent[0], cent[1], cent[2], cent[3], wq[0], wq[1]);
+            } else {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) wq[m] = __builtin_amdgcn_perm(0u, cent[0], (words[d] >> (2 * m)) & 0x03030303u);
+            }
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const uint32_t *qa = lq + (4 * q + lb) * qdw + c * QPC + d * W;
+#pragma unroll
+                for (int m = 0; m < W; ++m)
+                    acc[q] = __builtin_amdgcn_mfma_i32_4x4x4i8(static_cast<int>(qa[m]), static_cast<int>(wq[m]), acc[q],
+                                                              0, 0, 0);
+            }
+            constexpr int kPer = S::kCodes / 4;  // codes per dword
+            const int pos_end = c * S::kCodes + (d + 1) * kPer;
+            const bool closes =
+                GROUP >= S::kCodes ? (d == 3 && pos_end % GROUP == 0) : ((d + 1) * kPer) % GROUP == 0;
+            if (closes) {
+                const int k = GROUP >= S::kCodes ? 0 : (d + 1) * kPer / GROUP - 1;
+                const int g = pos_end / GROUP - 1;
+                if (g < groups) {
+                    if constexpr (DOTS) {
+                        if (row < J.rows)
+#pragma unroll
+                            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                                for (int r = 0; r < 4; ++r)
+                                    if (4 * q + r < nb)
+                                        dots[(static_cast<size_t>(b0 + 4 * q + r) * J.rows + row) * groups + g] =
+                                            acc[q][r];
+                    } else {
+                        const float ns = h2f(sl.norm[k]) * cs;  // sdot.cpp:43-44
+#pragma unroll
+                        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                value[4 * q + r] =
+                                    value[4 * q + r] + (static_cast<float>(acc[q][r]) * ns) * lxs[(4 * q + r) * groups + g];
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) acc[q] = v4i{0, 0, 0, 0};
+            }
+        }
+    };
+    int c0 = 0;
+    for (; c0 + kRowRing <= nch; c0 += kRowRing) {
+#pragma unroll
+        for (int k = 0; k < kRowRing; ++k) {
+            chunk(ring[k], c0 + k);
+            row_load(ring[k], codes, norms, min(c0 + k + kRowRing, nch - 1), groups);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kRowRing; ++k)
+        if (c0 + k < nch) chunk(ring[k], c0 + k);
+    if constexpr (!DOTS) {
+        if (row < J.rows) {
+#pragma unroll
+            for (int b = 0; b < TB; ++b)
+                if (b < nb) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + b) * J.rows + row] = value[b];
+        }
+    }
+}
+
+template <int KIND, bool DOTS>
+bool launch_sdot_quad(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                      int32_t *dots, hipStream_t s) {
+    const int dev = g.windows * kWindow;
+    const int tb = batch >= 16 ? 16 : (batch + 3) / 4 * 4;  // rows per tile
+    const size_t lds = static_cast<size_t>(tb) * dev + static_cast<size_t>(tb) * g.groups * 4;
+    if (lds > kQuadMaxLds || g.group > kWindow) return false;
+    dim3 grid(blocks, (batch + tb - 1) / tb), block(kRowsPerBlock);
+    auto go = [&](auto nq) {
+        constexpr int NQ = decltype(nq)::value;
+        switch (g.group) {
+        case 8:
+            if constexpr (KIND == kNib) {
+                hipLaunchKernelGGL((sdot_quad_kernel<KIND, 8, NQ, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots);
+                break;
+            }
+            [[fallthrough]];
+        case 16: hipLaunchKernelGGL((sdot_quad_kernel<KIND, 16, NQ, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+        case 32: hipLaunchKernelGGL((sdot_quad_kernel<KIND, 32, NQ, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+        case 64: hipLaunchKernelGGL((sdot_quad_kernel<KIND, 64, NQ, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+        case 128: hipLaunchKernelGGL((sdot_quad_kernel<KIND, 128, NQ, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+        default: hipLaunchKernelGGL((sdot_quad_kernel<KIND, 256, NQ, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+        }
+    };
+    switch (tb / 4) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    default: go(std::integral_constant<int, 4>{}); break;
+    }
+    ND_HIP(hipGetLastError());
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// int8 GEMV for batch tiles of 16 rows, groups of one or more whole code
+// chunks (4-bit: 32 .. 256, 2-bit: 64 .. 256), one wave per 64 weight rows.
+//
+// Each code chunk (16 bytes per weight row: 32 four-bit or 64 two-bit codes)
+// is 4 (4-bit) or 8 (2-bit) v_mfma_i32_16x16x32_i8, 1 or 2 per 16 of the
+// wave's weight rows: lane (j, t) = (l % 16, l / 16) decodes code dword t of
+// weight row 16 m + j for each m (every code decoded once) as the B operand,
+// and feeds the permuted activations of batch row j that pair with that dword
+// (A, one LDS read per chunk for all its products); accumulator register r of
+// lane (j, t) is then the dot of weight row 16 m + j with batch row 4 t + r. The
+// tile's activations and group scales are staged in LDS once per workgroup.
+// Each group closes with the reference's epilogue for every batch row
+//   value += (float(dot) * (half(norm) * cs)) * x_scale[g]
+// in group order (sdot.cpp:43-44, 142-149): bit-identical outputs. With DOTS
+// the int32 group dots are stored (dots[b][row][g]).
+// ---------------------------------------------------------------------------
+struct Tile16Slot {
+    uint32_t code[4];  // dword t of the chunk, weight rows 16 m + j
+    uint16_t norm[4];  // their group norms, loaded with the chunk that closes a group
+};
+
+template <int KIND, int GROUP, bool DOTS>
+__global__ __launch_bounds__(kRowsPerBlock) void sdot_tile16_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+                                                                   int njobs, SdotGeom geom, int32_t *__restrict__ dots) {
+    constexpr int CODES = KIND == kNib ? 32 : 64;  // codes per chunk
+    constexpr int H = CODES / 32;                  // products per chunk and 16 weight rows
+    static_assert(GROUP >= CODES && GROUP <= kWindow, "one or more whole chunks per group");
+    constexpr int TB = 16;
+    constexpr int CPG = GROUP / CODES;  // chunks per group (divides kRowRing)
+    static_assert(kRowRing % CPG == 0, "group closes at fixed ring slots");
+    extern __shared__ __attribute__((aligned(16))) uint32_t t16_lds[];
+    const int blk = blockIdx.x;
+    SdotJob J = job0;
+    if (njobs > 0) {
+        const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
+        const int j = find_job(cj, njobs, blk);
+        J.codes = cj[j].codes;
+        J.norms = cj[j].norms;
+        J.q = cj[j].q;
+        J.xs = cj[j].xs;
+        J.y = cj[j].y;
+        J.rows = cj[j].rows;
+        J.block_begin = cj[j].block_begin;
+        J.batch = cj[j].batch;
+    }
+    const int tile = blk - J.block_begin;
+    const int lane = threadIdx.x & 63;
+    const int jr = lane & 15, t = lane >> 4;
+    const int wrow = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 64;  // the wave's first row in the tile
+    const int groups = geom.groups;
+    const int dev = geom.windows * kWindow;
+    const int qdw = dev / 4;
+    const int b0 = static_cast<int>(blockIdx.y) * TB;
+    const int nb = min(TB, J.batch - b0);
+    uint32_t *lq = t16_lds;
+    float *lxs = reinterpret_cast<float *>(t16_lds + TB * qdw);
+    const uint32_t cent[4] = {geom.cent[0], geom.cent[1], geom.cent[2], geom.cent[3]};
+    const float cs = geom.centroid_scale;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J.norms + static_cast<size_t>(tile) * groups * kRowsPerBlock,
+                                                     static_cast<uint32_t>(groups) * kRowsPerBlock * 2u);
+    const int nch = groups * CPG;  // chunks holding real positions
+    // per-lane offsets: code dword t of weight row wrow + 16 m + jr, and its fp16 norm
+    uint32_t cv[4], nv[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        cv[m] = (wrow + 16 * m + jr) * 16u + 4u * t;
+        nv[m] = (wrow + 16 * m + jr) * 2u;
+    }
+    // The ring prefetch past the last chunk re-reads the last chunk (never used).
+    auto load = [&](Tile16Slot &sl, int c, bool closes) {
+        const int so = __builtin_amdgcn_readfirstlane(c * kRowsPerBlock * 16);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) sl.code[m] = __builtin_amdgcn_raw_buffer_load_b32(codes, cv[m], so, 0);
+        if (closes) {
+            const int no = __builtin_amdgcn_readfirstlane(c / CPG * kRowsPerBlock * 2);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) sl.norm[m] = __builtin_amdgcn_raw_buffer_load_b16(norms, nv[m], no, 0);
+        }
+    };
+    Tile16Slot ring[kRowRing];
+#pragma unroll
+    for (int k = 0; k < kRowRing; ++k) load(ring[k], min(k, nch - 1), (k + 1) % CPG == 0);
+    // stage the tile's activation rows and group scales (rows past the batch as zeros)
+    const u32x4 *q4 = reinterpret_cast<const u32x4 *>(J.q) + static_cast<size_t>(b0) * (qdw / 4);
+    for (int i = threadIdx.x; i < TB * qdw / 4; i += kRowsPerBlock)
+        reinterpret_cast<u32x4 *>(lq)[i] = i / (qdw / 4) < nb ? q4[i] : u32x4{0, 0, 0, 0};
+    for (int i = threadIdx.x; i < TB * groups; i += kRowsPerBlock)
+        lxs[i] = i / groups < nb ? J.xs[static_cast<size_t>(b0) * groups + i] : 0.0f;
+    __syncthreads();
+    float value[4][4];  // [m][r]: weight row wrow + 16 m + jr, batch row 4 t + r
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) value[m][r] = 0.0f;
+    v4i acc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = v4i{0, 0, 0, 0};
+    const uint32_t *qrow = lq + jr * qdw + 2 * H * t;  // batch row jr: the activation dwords of code dword t
+    const float *xrow = lxs + 4 * t * groups;      // scales of batch rows 4t .. 4t + 3
+    auto chunk = [&](const Tile16Slot &sl, int c, bool closes) {
+        long a[H];
+        if constexpr (KIND == kNib) {
+            const auto q2 = *reinterpret_cast<const uint32_t __attribute__((ext_vector_type(2))) *>(qrow + c * 8);
+            a[0] = static_cast<long>(q2[0]) | (static_cast<long>(q2[1]) << 32);
+        } else {
+            const u32x4 q4v = *reinterpret_cast<const u32x4 *>(qrow + c * 16);
+            a[0] = static_cast<long>(q4v.x) | (static_cast<long>(q4v.y) << 32);
+            a[1] = static_cast<long>(q4v.z) | (static_cast<long>(q4v.w) << 32);
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            uint32_t wq[2 * H];  // the centroid dwords of code dword t, in activation-dword order
+            if constexpr (KIND == kNib) {
+                decode_nib(sl.code[m], cent[0], cent[1], cent[2], cent[3], wq[0], wq[1]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    wq[k] = __builtin_amdgcn_perm(0u, cent[0], (sl.code[m] >> (2 * k)) & 0x03030303u);
+            }
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                const long b = static_cast<long>(wq[2 * h]) | (static_cast<long>(wq[2 * h + 1]) << 32);
+                acc[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[h], b, acc[m], 0, 0, 0);
+            }
+        }
+        if (closes) {
+            const int g = c / CPG;
+            if constexpr (DOTS) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int row = tile * kRowsPerBlock + wrow + 16 * m + jr;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (4 * t + r < nb && row < J.rows)
+                            dots[(static_cast<size_t>(b0 + 4 * t + r) * J.rows + row) * groups + g] = acc[m][r];
+                }
+            } else {
+                float xsb[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) xsb[r] = xrow[r * groups + g];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const float ns = h2f(sl.norm[m]) * cs;  // sdot.cpp:43-44
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        value[m][r] = value[m][r] + (static_cast<float>(acc[m][r]) * ns) * xsb[r];
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m) acc[m] = v4i{0, 0, 0, 0};
+        }
+    };
+    int c0 = 0;
+    for (; c0 + kRowRing <= nch; c0 += kRowRing) {
+#pragma unroll
+        for (int k = 0; k < kRowRing; ++k) {
+            chunk(ring[k], c0 + k, (k + 1) % CPG == 0);
+            load(ring[k], min(c0 + k + kRowRing, nch - 1), (k + 1) % CPG == 0);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kRowRing; ++k)
+        if (c0 + k < nch) chunk(ring[k], c0 + k, (k + 1) % CPG == 0);
+    if constexpr (!DOTS) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int row = tile * kRowsPerBlock + wrow + 16 * m + jr;
+            if (row < J.rows)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (4 * t + r < nb)
+                        ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + 4 * t + r) * J.rows + row] = value[m][r];
+        }
+    }
+}
+
+template <int KIND, bool DOTS>
+bool launch_sdot_tile16(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                        int32_t *dots, hipStream_t s) {
+    const int dev = g.windows * kWindow;
+    const size_t lds = static_cast<size_t>(16) * dev + static_cast<size_t>(16) * g.groups * 4;
+    if (g.group < (KIND == kNib ? 32 : 64) || g.group > kWindow || lds > kQuadMaxLds) return false;
+    dim3 grid(blocks, (batch + 15) / 16), block(kRowsPerBlock);
+    switch (g.group) {
+    case 32:
+        if constexpr (KIND == kNib) {
+            hipLaunchKernelGGL((sdot_tile16_kernel<KIND, 32, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots);
+            break;
+        }
+        [[fallthrough]];
+    case 64: hipLaunchKernelGGL((sdot_tile16_kernel<KIND, 64, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+    case 128: hipLaunchKernelGGL((sdot_tile16_kernel<KIND, 128, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+    default: hipLaunchKernelGGL((sdot_tile16_kernel<KIND, 256, DOTS>), grid, block, lds, s, job0, jobs, njobs, g, dots); break;
+    }
+    ND_HIP(hipGetLastError());
+    return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -993,23 +1383,36 @@ void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded
     ND_HIP(hipGetLastError());
 }
 
+// 16-row batch tiles from 8 rows up (NEEDLE2_GPU_INT8_TILE16: "always" from
+// 2 rows, "never").
+static bool tile16_wanted(int batch) {
+    const char *mode = std::getenv("NEEDLE2_GPU_INT8_TILE16");
+    if (mode && std::strcmp(mode, "never") == 0) return false;
+    if (mode && std::strcmp(mode, "always") == 0) return batch >= 2;
+    return batch >= 8;
+}
+
 void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
                       hipStream_t s) {
     if (blocks <= 0 || batch <= 0) return;
     ND_CHECK(g.group >= 8, "int8 path: group must be >= 8");
     ND_CHECK(g.kind == kNib || g.group >= 16, "int8 path: 2-bit codes need group >= 16");
-    // Batches of 8 or more rows go to MFMA (groups of 32 .. 256; its jobs carry
-    // the transposed scales) when the 32-row x 32-batch-row wave tiles give
-    // at least two waves per SIMD; smaller batches decode once per row and
-    // run v_dot4, which does no work for padding batch rows.
-    // NEEDLE2_GPU_INT8_MFMA=always / never overrides the choice (auto).
+    // Kernel by size (environment overrides, "always" / "never", let the
+    // tests run every kernel on every shape):
+    //  - small matrices (fewer 32 x 32 tiles than SIMDs: decode projections)
+    //    of any batch split K over kKs waves per tile (NEEDLE2_GPU_INT8_KSPLIT);
+    //  - one batch row: the barrier-free row kernel (NEEDLE2_GPU_INT8_ROW);
+    //  - 8 or more: batch tiles of 16 rows on v_mfma_i32_16x16x32_i8, every
+    //    code decoded once per tile (NEEDLE2_GPU_INT8_TILE16);
+    //  - 2 or more: batch tiles of up to 16 rows on v_mfma_i32_4x4x4_16b_i8,
+    //    one lane per weight row, every code decoded once per tile
+    //    (NEEDLE2_GPU_INT8_QUAD);
+    //  - otherwise 32 x 32 batch tiles on v_mfma_i32_32x32x32_i8 for 8 or
+    //    more rows (NEEDLE2_GPU_INT8_MFMA) and v_dot4 batch tiles below.
     const long mfma_waves = static_cast<long>(blocks) * (kRowsPerBlock / 32) * ((batch + 31) / 32);
     const char *mode = std::getenv("NEEDLE2_GPU_INT8_MFMA");
-    // Small matrices (fewer 32 x 32 tiles than SIMDs; decode projections) of
-    // any batch split K over kKs waves per tile (NEEDLE2_GPU_INT8_KSPLIT=
-    // always / never overrides; the transposed scales must be present, as
-    // every plan and handle provides them).
     const char *ks_mode = std::getenv("NEEDLE2_GPU_INT8_KSPLIT");
+    const char *quad_mode = std::getenv("NEEDLE2_GPU_INT8_QUAD");
     const bool ks_ok = g.group >= 32 && g.group <= kWindow && g.groups >= 2;
     bool ks = ks_ok && mfma_waves < 4L * device_cus();
     if (ks_mode && std::strcmp(ks_mode, "always") == 0) ks = ks_ok;
@@ -1020,25 +1423,54 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
         return;
     }
     const bool mfma_ok = batch >= 2 && g.group >= 32 && g.group <= kWindow;
+    const bool mfma_forced = mode && std::strcmp(mode, "always") == 0;
+    const char *row_mode = std::getenv("NEEDLE2_GPU_INT8_ROW");
+    if (!mfma_forced && batch == 1 && g.group <= kWindow && g.windows * kWindow <= kRowMaxDev &&
+        !(row_mode && std::strcmp(row_mode, "never") == 0)) {
+        if (g.kind == kNib) launch_sdot_row<kNib, false>(g, job0, jobs, njobs, blocks, nullptr, s);
+        else launch_sdot_row<kCrumb, false>(g, job0, jobs, njobs, blocks, nullptr, s);
+        return;
+    }
+    if (!mfma_forced && tile16_wanted(batch)) {
+        const bool done = g.kind == kNib ? launch_sdot_tile16<kNib, false>(g, job0, jobs, njobs, blocks, batch, nullptr, s)
+                                         : launch_sdot_tile16<kCrumb, false>(g, job0, jobs, njobs, blocks, batch, nullptr, s);
+        if (done) return;
+    }
+    if (!mfma_forced && batch >= 2 && !(quad_mode && std::strcmp(quad_mode, "never") == 0)) {
+        const bool done = g.kind == kNib ? launch_sdot_quad<kNib, false>(g, job0, jobs, njobs, blocks, batch, nullptr, s)
+                                         : launch_sdot_quad<kCrumb, false>(g, job0, jobs, njobs, blocks, batch, nullptr, s);
+        if (done) return;
+    }
     bool mfma = mfma_ok && batch >= 8 && mfma_waves >= 2L * 4 * device_cus();
-    if (mode && std::strcmp(mode, "always") == 0) mfma = mfma_ok;
+    if (mfma_forced) mfma = mfma_ok;
     if (mode && std::strcmp(mode, "never") == 0) mfma = false;
     if (mfma) {
         if (g.kind == kNib) launch_sdot_mfma<kNib>(g, job0, jobs, njobs, blocks, batch, s);
         else launch_sdot_mfma<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
         return;
     }
-    // one batch row (decode): the barrier-free row kernel when the row fits the LDS stage
-    // (NEEDLE2_GPU_INT8_ROW=never keeps the windowed kernel)
-    const char *row_mode = std::getenv("NEEDLE2_GPU_INT8_ROW");
-    if (batch == 1 && g.group <= kWindow && g.windows * kWindow <= kRowMaxDev &&
-        !(row_mode && std::strcmp(row_mode, "never") == 0)) {
-        if (g.kind == kNib) launch_sdot_row<kNib>(g, job0, jobs, njobs, blocks, s);
-        else launch_sdot_row<kCrumb>(g, job0, jobs, njobs, blocks, s);
-        return;
-    }
     if (g.kind == kNib) launch_sdot_kind<kNib>(g, job0, jobs, njobs, blocks, batch, s);
     else launch_sdot_kind<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
+}
+
+void launch_sdot_dots(const SdotGeom &g, const SdotJob &job0, int blocks, int batch, int32_t *dots, hipStream_t s) {
+    if (blocks <= 0 || batch <= 0) return;
+    ND_CHECK(g.group >= 8 && g.group <= kWindow, "int8 dots: groups of 8 .. 256");
+    ND_CHECK(g.kind == kNib || g.group >= 16, "int8 path: 2-bit codes need group >= 16");
+    if (batch == 1) {
+        ND_CHECK(g.windows * kWindow <= kRowMaxDev, "int8 dots: the row exceeds the batch-1 kernel's stage");
+        if (g.kind == kNib) launch_sdot_row<kNib, true>(g, job0, nullptr, 0, blocks, dots, s);
+        else launch_sdot_row<kCrumb, true>(g, job0, nullptr, 0, blocks, dots, s);
+        return;
+    }
+    bool done = false;
+    if (tile16_wanted(batch))
+        done = g.kind == kNib ? launch_sdot_tile16<kNib, true>(g, job0, nullptr, 0, blocks, batch, dots, s)
+                              : launch_sdot_tile16<kCrumb, true>(g, job0, nullptr, 0, blocks, batch, dots, s);
+    if (!done)
+        done = g.kind == kNib ? launch_sdot_quad<kNib, true>(g, job0, nullptr, 0, blocks, batch, dots, s)
+                              : launch_sdot_quad<kCrumb, true>(g, job0, nullptr, 0, blocks, batch, dots, s);
+    ND_CHECK(done, "int8 dots: the batch tile exceeds the kernel's LDS stage");
 }
 
 }  // namespace nd

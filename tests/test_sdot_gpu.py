@@ -88,19 +88,24 @@ def test_int8_plan_many_matrices():
         np.testing.assert_array_equal(dy.download(np.empty((2, m.shape[0]), np.float32)), e)
 
 
-@pytest.mark.parametrize("mode", ["always", "never", "ksplit"])
+@pytest.mark.parametrize("mode", ["tile16", "quad", "always", "never", "ksplit"])
 @pytest.mark.parametrize("bits,group,batch", [(4, 32, 3), (4, 32, 9), (4, 32, 17), (4, 32, 33), (4, 32, 64),
                                               (4, 64, 40), (4, 128, 12), (4, 256, 5), (2, 32, 8), (2, 32, 33),
-                                              (2, 64, 20)])
+                                              (2, 64, 20), (4, 8, 6), (4, 16, 16), (2, 16, 2), (4, 32, 2)])
 def test_int8_batched_tiles_bit_exact(bits, group, batch, mode, monkeypatch):
-    """Batches run on int8 MFMA (tiles of 32 batch rows: ragged last tile) or on v_dot4 batch tiles, forced
-    either way here (the library picks by size otherwise); 300 ragged weight rows, zero / one-hot activation
-    rows: bit-exact with the oracle."""
+    """Batches of 2 or more on each kernel, forced here (the library picks by size otherwise): 16 x 16 x 32
+    int8 MFMA batch tiles of 16 rows (tile16: ragged last tile; groups below one code chunk fall back to the
+    quad kernel), 4 x 4 x 4 int8 MFMA batch tiles of up to 16 rows, one lane per weight row (quad: ragged last
+    quad and tile), 32 x 32 x 32 int8 MFMA tiles of 32 batch rows (always), v_dot4 batch tiles (never) and the
+    K split (ksplit); 300 ragged weight rows, zero / one-hot activation rows: bit-exact with the oracle."""
     if mode == "ksplit":  # K split over 8 waves per tile (small-matrix path)
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "always")
     else:
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "never")
-        monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", mode)
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_TILE16", "always" if mode == "tile16" else "never")
+        if mode == "never":
+            monkeypatch.setenv("NEEDLE2_GPU_INT8_QUAD", "never")
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", "auto" if mode in ("quad", "tile16") else mode)
     packed, norms, cb, dense = example(bits, rows=300, dim=1000, group=group, seed=7 * batch + group)
     q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
     x = activations((batch, 1000), seed=batch)
