@@ -204,12 +204,14 @@ def bench_prefill(steps, warmup, stream):
     return t0.elapsed_ms(t1) / steps, [a.elapsed_ms(b) / PREFILL_REPEAT for a, b in ev]
 
 
-def bench_decode_layer(steps, warmup, stream, seqs=64, graph=True):
+def bench_decode_layer(steps, warmup, stream, seqs=64, graph=True, parts=None):
     """One decoder layer for `seqs` sequences at context 2048 (hidden 512, 8 heads = 8 kv heads, head_dim 64,
     MLP 2048): int8-path CQ4 g32 projections Q|K|V (one plan), KV store of the new token, decode attention
     over 2048 int8 slots, O, MLP up and down. Elementwise glue (norms, RoPE, gates, activation) is omitted.
     Returns (eager ms per step, ms per step replaying the step captured in a HIP graph, or None without
-    `graph`). Everything is released in a fixed order at the end: the graph first, then the plans and the
+    `graph`). With a dict `parts`, also fills it with ms per call of each launch group run alone back to back
+    (`<plan>_plan`: prepare + GEMV; `<plan>_gemv`: the GEMV launch alone, from events around it; `kv_store`,
+    `attention`). Everything is released in a fixed order at the end: the graph first, then the plans and the
     cache, then the buffers and matrices they read."""
     from openneedle_amd.cq import CQMatrix, Plan
     from openneedle_amd.device import DeviceArray, Event, Graph, Teardown, synchronize
@@ -262,6 +264,21 @@ def bench_decode_layer(steps, warmup, stream, seqs=64, graph=True):
                 return t0.elapsed_ms(t1) / steps
 
         eager = timed(step)
+        if parts is not None:  # each launch group alone (back to back), and the GEMV part of each plan
+            def gemv_only(pl):
+                with Event() as e0, Event() as e1:
+                    total = 0.0
+                    for _ in range(steps):
+                        pl.run(stream, gemv_events=(e0, e1))
+                        synchronize()
+                        total += e0.elapsed_ms(e1)
+                    return total / steps
+
+            for name, pl in zip(("qkv", "o", "up", "down"), plans):
+                parts[f"{name}_plan"] = timed(lambda: pl.run(stream))
+                parts[f"{name}_gemv"] = gemv_only(pl)
+            parts["kv_store"] = timed(lambda: kv.store_device(0, buf["k"], buf["v"], 1, first, stream=stream))
+            parts["attention"] = timed(lambda: kv.attention(0, buf["q"], buf["a"], heads, cap, stream=stream))
         graphed = None
         if graph:
             with Graph.capture(stream) as g:
@@ -603,10 +620,12 @@ def main():
 
     if args.only == "decode":
         for seqs in (64, 1):
-            ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs, graph=args.graph)
+            parts = {}
+            ms_e, ms_g = bench_decode_layer(args.steps, args.warmup, stream, seqs, graph=args.graph, parts=parts)
             graph = f", graph {ms_g * 1e3:.1f} us" if ms_g is not None else ""
             log(f"decode layer ({seqs} seqs, ctx 2048): eager {ms_e * 1e3:.1f} us{graph} -> "
                 f"{seqs / (min(ms_e, ms_g or ms_e) * 1e-3):.0f} tokens/s per layer")
+            log("  alone: " + ", ".join(f"{k} {v * 1e3:.1f} us" for k, v in parts.items()))
         return
     if args.only == "engine":
         for kv, (tps, ms) in bench_engine().items():

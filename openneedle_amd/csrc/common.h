@@ -180,6 +180,7 @@ struct SdotJob {
     float *y;
     int rows, n_pad, block_begin, batch;
     const float *xst;         // the same scales transposed, [groups][batch] (MFMA path; null: dot4 path only)
+    int ystride;              // floats between batch rows of y (0: rows)
 };
 
 // ---------------------------------------------------------------------------

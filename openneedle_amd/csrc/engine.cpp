@@ -132,17 +132,21 @@ struct GemvGroup {
 };
 
 // The int8 ("SDOT") counterpart of GemvGroup (engine.cpp:502-515, 560-577
-// with the SDOT path on): each token's input transformed and quantised once
-// (one prepare launch for the chunk), then the int8 GEMV over the pieces'
-// row tiles, per token and piece one job of batch 1.
+// with the SDOT path on): the inputs of a launch's tokens transformed and
+// quantised by one prepare launch, then the int8 GEMV over the pieces' row
+// tiles: one job of batch 1 per piece for a single token (decode step), and
+// for a prompt chunk of T tokens one job of batch T per piece
+// (engine.cpp:607-640, linear_batch on the SDOT path), so the batch kernels
+// decode each code once per batch tile. Both are bit-identical per token.
 struct SdotGroup {
     const Matrix *m0 = nullptr;
     SdotGeom g{};
     DevBuf<uint8_t> jobs;
+    DevBuf<uint8_t> batched;  // for T = 2 .. tokens: `pieces` jobs of batch T at offset (T - 2) * pieces
     DevBuf<int32_t> q;
-    DevBuf<float> xs, rot, big;
+    DevBuf<float> xs, xst, rot, big;
     DevBuf<const float *> xptr;
-    int pieces = 0, per_token = 0;
+    int pieces = 0, per_token = 0, max_tokens = 0;
     const float *x = nullptr;
     SdotJob job0{};
 
@@ -174,18 +178,42 @@ struct SdotGroup {
             }
         pieces = static_cast<int>(ps.size());
         per_token = blocks / tokens;
+        max_tokens = tokens;
         job0 = host[0];
         if (host.size() > 1) {
             jobs.reserve(host.size() * sizeof(SdotJob));
             ND_HIP(hipMemcpy(jobs.p, host.data(), host.size() * sizeof(SdotJob), hipMemcpyHostToDevice));
         }
+        // batch jobs: token 0's pieces over all rows of the chunk (q, scales and
+        // outputs of consecutive tokens are consecutive rows)
+        if (tokens >= 2 && m0->group <= kWindow) {
+            xst.reserve(size_t(tokens) * m0->groups);
+            std::vector<SdotJob> bt;
+            for (int t = 2; t <= tokens; ++t)
+                for (int k = 0; k < pieces; ++k) {
+                    SdotJob j = host[k];
+                    j.batch = t;
+                    j.xst = xst.p;
+                    j.ystride = ps[k].ystride;
+                    bt.push_back(j);
+                }
+            batched.reserve(bt.size() * sizeof(SdotJob));
+            ND_HIP(hipMemcpy(batched.p, bt.data(), bt.size() * sizeof(SdotJob), hipMemcpyHostToDevice));
+        }
     }
 
     void run(hipStream_t s, int tokens) {
-        if (!launch_sdot_prepare(nullptr, xptr.p, 1, tokens, m0->in, m0->padded, m0->dev, m0->group, m0->scale,
-                                 m0->kind, q.p, xs.p, nullptr, s)) {
+        const bool batch = tokens >= 2 && batched.p;
+        if (!launch_sdot_prepare(nullptr, xptr.p, batch ? tokens : 1, tokens, m0->in, m0->padded, m0->dev, m0->group,
+                                 m0->scale, m0->kind, q.p, xs.p, batch ? xst.p : nullptr, s)) {
+            ND_CHECK(!batch, "internal: batched int8 prepare refused the group");
             m0->transform(x, m0->in, rot.p, tokens, big, s);
             launch_sdot_quantize(rot.p, m0->dev, tokens, m0->padded, m0->dev, m0->group, m0->kind, q.p, xs.p, s);
+        }
+        if (batch) {
+            const auto *table = reinterpret_cast<const SdotJob *>(batched.p) + size_t(tokens - 2) * pieces;
+            launch_sdot_gemv(g, SdotJob{}, table, pieces, per_token, tokens, s);
+            return;
         }
         const int njobs = pieces * tokens;
         if (njobs > 1)
@@ -274,6 +302,7 @@ struct GpuEngine {
     DevBuf<int> lens;      // per chunk: attention list lengths [chunk]
     HostBuf<int> hlens;
     DevBuf<float> logits, part, embed_z, row_scratch;
+    DevBuf<float> attn_scores;  // fp32-KV attention scores past the LDS budget
     HostBuf<float> hlogits, hhidden;
     std::vector<Projection> mhc_proj, qkvg, oproj;
     std::vector<std::array<int, 3>> mhc_row;
@@ -345,6 +374,11 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
                               c.tables % c.num_orders == 0 && c.tables * c.subdim == D && c.taps > 0 &&
                               c.taps <= kEngMaxTaps && c.dilation > 0),
              "engine: unsupported engram geometry");
+    for (int k = 0; k < c.num_sites; ++k) {
+        ND_CHECK(c.sites[k] >= 0 && c.sites[k] < c.layers, "engine: engram site outside the layers");
+        for (int j = 0; j < k; ++j)
+            ND_CHECK(c.sites[j] != c.sites[k], "engine: two engram sites on one layer (the archive format forbids it)");
+    }
     ND_CHECK(count >= final_norm() + 1, "engine: tensor count does not match the geometry");
     ND_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
 
@@ -578,9 +612,11 @@ void GpuEngine::reset(int prefix_len) {
     const int G = c.heads / c.kvheads;
     if (int8_kv)
         ND_CHECK(attn_supported(c.head_dim, G), "int8 KV attention: head_dim 32/64/128 with 1, 2, 4 or 8 heads per kv head");
+    // fp32 KV: scores past the LDS budget go to a device buffer (any context)
+    if (!int8_kv && size_t(G) * max_length() * sizeof(float) > kEngScoreLds)
+        attn_scores.reserve(size_t(chunk) * c.kvheads * G * max_length());
     else
-        ND_CHECK(size_t(G) * max_length() * sizeof(float) <= 49152,
-                 "fp32 KV attention: heads per kv head x context too large");
+        attn_scores.release();
     const size_t per_layer = size_t(c.kvheads) * capacity * c.head_dim;
     const size_t scales = size_t(c.kvheads) * capacity;
     kv.assign(c.layers, KvLayer{});
@@ -938,7 +974,7 @@ void GpuEngine::run(int tokens) {
             // one token: norms, RoPE, store and attention in one kernel; a chunk
             // stores every token's K / V before any token attends
             if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
-            launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, s);
+            launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, s);
             launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
         } else {
             launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);

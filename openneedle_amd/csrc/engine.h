@@ -10,6 +10,7 @@ constexpr int kEngMaxHalfHd = 64;  // head_dim <= 128
 constexpr int kEngMaxTables = 16;  // engram tables per site
 constexpr int kEngMaxSites = 4;
 constexpr int kEngMaxTaps = 16;
+constexpr size_t kEngScoreLds = 49152;  // bytes of fp32 attention scores kept in LDS
 constexpr int kEngThreads = 1024;  // every glue kernel is one workgroup of this size
 
 // Values of one token that depend only on its position, the token history
@@ -89,8 +90,11 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
                    const EngineDims &d, int tokens, hipStream_t s);
 // fp32 KV attention + output gate of every kv head; with `prepared` false (one
 // token) it also does that token's norms, RoPE and KV store, else eng_qk did
+// scores: null when G * max_length floats fit kEngScoreLds, else a device
+// buffer of tokens * kvheads * G * max_length floats
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
-                           int max_length, bool prepared, const EngineDims &d, int tokens, hipStream_t s);
+                           int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
+                           hipStream_t s);
 void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s);
 // K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
 void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,

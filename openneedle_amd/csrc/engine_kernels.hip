@@ -400,15 +400,22 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b0, Laye
 // engine.cpp:900-909) and the output gate att *= sigmoid(gate)
 // (engine.cpp:994-1023). Nothing crosses kv heads, so one launch does it all.
 
-template <bool PREPARED>
+// The scores [G][length] live in LDS, or, past the LDS budget (long
+// contexts), in `scores` ([tokens][kv heads][G][max_length] in device memory):
+// the same block writes, reduces and reads them, ordered by its barriers.
+template <bool PREPARED, bool GLOBAL_SCORES>
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
-                                                             const StepParams *__restrict__ p, EngineDims d) {
-    extern __shared__ float sc[];  // [G][length]
+                                                             const StepParams *__restrict__ p, EngineDims d,
+                                                             float *__restrict__ scores, int max_length) {
+    extern __shared__ float sc_lds[];  // [G][length] when the scores fit
     __shared__ float qs[8 * 1024];  // query heads, then the partial outputs [R][G][HD] (1024 G floats)
     __shared__ float red[4];
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     p += blockIdx.y;
     const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
+    float *sc = GLOBAL_SCORES
+                    ? scores + (static_cast<size_t>(blockIdx.y) * gridDim.x + kh) * G * static_cast<size_t>(max_length)
+                    : sc_lds;
     const int wave = t >> 6, lane = t & 63, length = p->length;
     const float *kc = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
     const float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
@@ -469,14 +476,16 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     }
     // values: thread t takes 16-byte column c = t % (HD / 4) of the V rows of slots r, r + R, ..
     // (r = t / (HD / 4), R = 256 / (HD / 4) subsets), so its loads are all in flight together; the R
-    // partial sums per output then add up in subset order
+    // partial sums per output then add up in subset order. When HD / 4 does not divide 256 the last
+    // threads (r == R) take no slots and write no partials: R * G * HD <= 1024 G floats fit in qs.
     constexpr int kMaxG = 8;
     const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
+    const bool sub = r < R;
     float4 acc[kMaxG];
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 8
-    for (int s = r; s < length; s += R) {
+    for (int s = sub ? r : length; s < length; s += R) {
         const float4 v = reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_at(p, s)) * HD)[c4];
 #pragma unroll
         for (int g = 0; g < kMaxG; ++g)
@@ -492,7 +501,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g)
-        if (g < G) wpart[(r * G + g) * cols4 + c4] = acc[g];
+        if (sub && g < G) wpart[(r * G + g) * cols4 + c4] = acc[g];
     __syncthreads();
     for (int o = t; o < G * HD; o += blockDim.x) {
         const float *wp = reinterpret_cast<const float *>(wpart);
@@ -715,12 +724,19 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 }
 
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
-                           int max_length, bool prepared, const EngineDims &d, int tokens, hipStream_t s) {
-    const size_t lds = static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);
-    if (prepared)
-        hipLaunchKernelGGL(eng_attn_fused_kernel<true>, dim3(d.KV, tokens), dim3(256), lds, s, b, ld, kv, p, d);
+                           int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
+                           hipStream_t s) {
+    const size_t lds = scores ? 0 : static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);
+    ND_CHECK(lds <= kEngScoreLds, "internal: fp32 attention scores exceed the LDS budget without a score buffer");
+    const dim3 grid(d.KV, tokens), block(256);
+    if (prepared && scores)
+        hipLaunchKernelGGL((eng_attn_fused_kernel<true, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length);
+    else if (prepared)
+        hipLaunchKernelGGL((eng_attn_fused_kernel<true, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0);
+    else if (scores)
+        hipLaunchKernelGGL((eng_attn_fused_kernel<false, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length);
     else
-        hipLaunchKernelGGL(eng_attn_fused_kernel<false>, dim3(d.KV, tokens), dim3(256), lds, s, b, ld, kv, p, d);
+        hipLaunchKernelGGL((eng_attn_fused_kernel<false, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0);
     ND_HIP(hipGetLastError());
 }
 

@@ -339,8 +339,10 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
         J.n_pad = cj[j].n_pad;
         J.block_begin = cj[j].block_begin;
         J.batch = cj[j].batch;
+        J.ystride = cj[j].ystride;
     }
     const int rows = J.rows;
+    const size_t ystride = J.ystride ? J.ystride : rows;
     const int tile = blk - J.block_begin;
     const int row = tile * kRowsPerBlock + threadIdx.x;
     const int windows = geom.windows, groups = geom.groups;
@@ -397,7 +399,7 @@ __global__ __launch_bounds__(kRowsPerBlock, 2) void sdot_gemv_kernel(SdotJob job
         if (w < windows) sdot_compute<KIND, GROUP, BT>(cur, lq[0], lxs[0], cent, cs, value, dot, w, groups, wpg);
         if (row < rows) {
 #pragma unroll
-            for (int b = 0; b < BT; ++b) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + b) * rows + row] = value[b];
+            for (int b = 0; b < BT; ++b) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + b) * ystride + row] = value[b];
         }
     }
 }
@@ -539,6 +541,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_mfma_kernel(SdotJob job0, 
         J0.rows = cj[j].rows;
         J0.block_begin = cj[j].block_begin;
         J0.batch = cj[j].batch;
+        J0.ystride = cj[j].ystride;
         J0.xst = cj[j].xst;
     }
     const int rows = J0.rows, batch = J0.batch;
@@ -583,7 +586,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_mfma_kernel(SdotJob job0, 
 #pragma unroll
         for (int r = 0; r < 4 * J; ++r) {
             const int m = b0 + 8 * (r / 4) + 4 * h + (r % 4);
-            if (m < batch) ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * rows + row] = value[r];
+            if (m < batch) ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * (J0.ystride ? J0.ystride : rows) + row] = value[r];
         }
     }
 }
@@ -807,6 +810,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_quad_kernel(SdotJob job0, 
         J.rows = cj[j].rows;
         J.block_begin = cj[j].block_begin;
         J.batch = cj[j].batch;
+        J.ystride = cj[j].ystride;
     }
     const int tile = blk - J.block_begin;
     const int row = tile * kRowsPerBlock + threadIdx.x;
@@ -910,7 +914,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_quad_kernel(SdotJob job0, 
         if (row < J.rows) {
 #pragma unroll
             for (int b = 0; b < TB; ++b)
-                if (b < nb) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + b) * J.rows + row] = value[b];
+                if (b < nb) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + b) * (J.ystride ? J.ystride : J.rows) + row] = value[b];
         }
     }
 }
@@ -994,6 +998,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_tile16_kernel(SdotJob job0
         J.rows = cj[j].rows;
         J.block_begin = cj[j].block_begin;
         J.batch = cj[j].batch;
+        J.ystride = cj[j].ystride;
     }
     const int tile = blk - J.block_begin;
     const int lane = threadIdx.x & 63;
@@ -1124,7 +1129,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_tile16_kernel(SdotJob job0
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     if (4 * t + r < nb)
-                        ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + 4 * t + r) * J.rows + row] = value[m][r];
+                        ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + 4 * t + r) * (J.ystride ? J.ystride : J.rows) + row] = value[m][r];
         }
     }
 }
@@ -1196,6 +1201,7 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
         J0.rows = cj[j].rows;
         J0.block_begin = cj[j].block_begin;
         J0.batch = cj[j].batch;
+        J0.ystride = cj[j].ystride;
         J0.xst = cj[j].xst;
     }
     const int rows = J0.rows, batch = J0.batch;
@@ -1247,7 +1253,7 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
             const int reg = w + k * kKs;
             if (reg >= R) continue;
             const int m = b0 + 8 * (reg / 4) + 4 * h + (reg % 4);
-            if (m < batch) ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * rows + row] = value[k];
+            if (m < batch) ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * (J0.ystride ? J0.ystride : rows) + row] = value[k];
         }
     }
 }

@@ -75,6 +75,64 @@ def test_released_geometry():
                 np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL)
 
 
+# Geometries the constructor accepts beyond the small model's 4 lanes, 2 query heads per kv head of 32 and one
+# engram site: every lane count (Sinkhorn and mixing loops of 1, 2, 8 lanes), 1 / 4 / 8 query heads per kv head,
+# head_dim 128 at 8 heads per kv head (the fused attention's partial sums fill its LDS exactly), head_dim 48
+# (HD / 4 does not divide the 256 threads of the value pass) and two engram sites (the archive format keeps
+# sites on distinct layers, needle2/archive.py:34-35, and so does the engine's constructor).
+VARIANTS = {
+    "lanes1": (dict(mhc_lanes=1), (1,)),
+    "lanes2": (dict(mhc_lanes=2), (1,)),
+    "lanes8": (dict(mhc_lanes=8), (1,)),
+    "heads_per_kv1": (dict(num_heads=2, num_kv_heads=2), (1,)),
+    "heads_per_kv4": (dict(num_heads=4, num_kv_heads=1), (1,)),
+    "heads_per_kv8_hd128": (dict(num_heads=8, num_kv_heads=1, head_dim=128), (1,)),
+    "hd48": (dict(head_dim=48), (1,)),
+    "two_sites": (dict(), (0, 2)),
+}
+
+
+@pytest.mark.parametrize("name", list(VARIANTS))
+def test_geometry_variants(name):
+    geo, sites = VARIANTS[name]
+    a = Archive(synthetic_model(dict(SMALL, **geo), engram_layers=sites, engram_orders=(2, 3), group=32, seed=31))
+    for i, (lg, hd, rl, rh) in enumerate(run_both(a, TOKENS[:8])):
+        print(f"{name} fp32 KV step {i}: logits {np.abs(lg - rl).max():.2e} hidden {np.abs(hd - rh).max():.2e}",
+              flush=True)
+        np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL, err_msg=f"hidden, step {i}")
+        np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL, err_msg=f"logits, step {i}")
+    if dict(SMALL, **geo)["head_dim"] in (32, 64, 128):
+        for i, (lg, hd, rl, rh) in enumerate(run_both(a, TOKENS[:8], int8_kv=True)):
+            print(f"{name} int8 KV step {i}: logits rel {rel_l2(lg, rl):.2e}", flush=True)
+            assert rel_l2(hd, rh) < 1e-3 and rel_l2(lg, rl) < 1e-3, f"step {i}"
+
+
+def test_long_context_fp32_kv():
+    """fp32 KV past the LDS budget of the fused attention (2 heads per kv head x 8192 positions of scores):
+    7000 imported positions, then steps and a prompt chunk, against the reference."""
+    a = Archive(synthetic_model(dict(SMALL, max_seq_len=8192), engram_layers=(1,), engram_orders=(2, 3), group=32,
+                                seed=33))
+    n = 7000
+    rng = np.random.default_rng(70)
+    ids = [int(t) for t in rng.integers(2, 500, n)]
+    shape = (SMALL["num_layers"], n, SMALL["num_kv_heads"], SMALL["head_dim"])
+    k = rng.standard_normal(shape).astype(np.float32)
+    v = rng.standard_normal(shape).astype(np.float32)
+    gpu, ref = GpuEngine(a), oracle.RefEngine(a)
+    for e in (gpu, ref):
+        e.import_state(ids, list(range(n)), k, v)
+    pairs = []
+    for t in (5, 400, 33):
+        g, r = gpu.step(t, hidden=True), ref.step(t, hidden=True)
+        pairs += [(f"step {t} logits", g[0], r[0]), (f"step {t} hidden", g[1], r[1])]
+    lg, hd = gpu_prefill(gpu, PROMPT[:9])
+    rl, rh = ref.prefill(PROMPT[:9], hidden=True)
+    pairs += [("prefill logits", lg, rl), ("prefill hidden", hd, rh)]
+    for what, g, r in pairs:
+        print(f"{what}: max {np.abs(g - r).max():.2e}", flush=True)
+        np.testing.assert_allclose(g, r, atol=ATOL, rtol=RTOL, err_msg=what)
+
+
 def test_candidates_equal_full_logits():
     """needle2's own contract (tests/test_candidate_projection_dense.py): candidate logits equal the full
     projection indexed by the candidates, order and duplicates kept, and leave the state as step does."""
@@ -187,6 +245,18 @@ def test_sdot_matches_reference(window, int8_kv):
     for what, g, r in pairs:
         print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
         assert rel_l2(g, r) < 2e-3, what  # measured <= 3e-7
+
+
+@pytest.mark.parametrize("window", [0, 8])
+def test_sdot_prefill_equals_steps(window):
+    """matmul="int8": a prompt chunk runs each projection as one int8 GEMV of batch T (the batch-tile kernels,
+    every code decoded once per tile) instead of T single-token jobs; every token's logits equal stepping bit for
+    bit."""
+    a = small64(window, seed=12)
+    e1, e2 = GpuEngine(a, matmul="int8"), GpuEngine(a, matmul="int8")
+    stepped = np.stack([e1.step(t)[0] for t in PROMPT])
+    np.testing.assert_array_equal(e2.prefill(PROMPT)[0], stepped)
+    np.testing.assert_array_equal(e2.step(4)[0], e1.step(4)[0])
 
 
 def test_sdot_candidates_equal_full_logits():
