@@ -204,51 +204,75 @@ def bench_prefill(steps, warmup, stream):
     return t0.elapsed_ms(t1) / steps, [a.elapsed_ms(b) / PREFILL_REPEAT for a, b in ev]
 
 
-def bench_decode_layer(steps, warmup, stream, seqs=64, graph=True, parts=None):
+class DecodeLayer:
     """One decoder layer for `seqs` sequences at context 2048 (hidden 512, 8 heads = 8 kv heads, head_dim 64,
     MLP 2048): int8-path CQ4 g32 projections Q|K|V (one plan), KV store of the new token, decode attention
     over 2048 int8 slots, O, MLP up and down. Elementwise glue (norms, RoPE, gates, activation) is omitted.
-    Returns (eager ms per step, ms per step replaying the step captured in a HIP graph, or None without
-    `graph`). With a dict `parts`, also fills it with ms per call of each launch group run alone back to back
-    (`<plan>_plan`: prepare + GEMV; `<plan>_gemv`: the GEMV launch alone, from events around it; `kv_store`,
-    `attention`). Everything is released in a fixed order at the end: the graph first, then the plans and the
-    cache, then the buffers and matrices they read."""
-    from openneedle_amd.cq import CQMatrix, Plan
-    from openneedle_amd.device import DeviceArray, Event, Graph, Teardown, synchronize
-    from openneedle_amd.kv import KVCache
-    cap, kvh, hd, heads, hidden, mlp = 2048, 8, 64, 8, 512, 2048
-    rng = np.random.default_rng(23)
-    with Teardown() as td:
-        def mat(rows, cols):
-            packed, norms, cb = random_cq(rng, 1, rows, cols, 4, 32)
-            return td.add(CQMatrix(packed[0], norms[0], (rows, cols), 4, 32, cb))
+    Every object goes into `td` (a Teardown), which releases them in reverse order; the host codes, norms and
+    codebook of each matrix stay in `host` (name -> (packed, norms, cb))."""
 
-        wq, wk, wv, wo = (mat(hidden, hidden) for _ in range(4))
-        wu, wd = mat(mlp, hidden), mat(hidden, mlp)
-        buf = {n: td.add(DeviceArray(seqs * w * 4)) for n, w in
-               (("x", hidden), ("q", hidden), ("k", hidden), ("v", hidden), ("a", hidden), ("o", hidden),
-                ("u", mlp), ("d", hidden))}
-        buf["x"].upload(rng.normal(size=(seqs, hidden)).astype(np.float32))
+    CAP, KVH, HD, HEADS, HIDDEN, MLP = 2048, 8, 64, 8, 512, 2048
+
+    def __init__(self, seqs, td, stream, seed=23):
+        from openneedle_amd.cq import CQMatrix, Plan
+        from openneedle_amd.device import DeviceArray
+        from openneedle_amd.kv import KVCache
+        self.seqs, self.stream = seqs, stream
+        cap, kvh, hd, hidden, mlp = self.CAP, self.KVH, self.HD, self.HIDDEN, self.MLP
+        rng = np.random.default_rng(seed)
+        self.host, self.mats = {}, {}
+        for name, rows, cols in (("wq", hidden, hidden), ("wk", hidden, hidden), ("wv", hidden, hidden),
+                                 ("wo", hidden, hidden), ("wu", mlp, hidden), ("wd", hidden, mlp)):
+            packed, norms, cb = random_cq(rng, 1, rows, cols, 4, 32)
+            self.host[name] = (packed[0], norms[0], cb)
+            self.mats[name] = td.add(CQMatrix(packed[0], norms[0], (rows, cols), 4, 32, cb))
+        self.widths = {"x": hidden, "q": hidden, "k": hidden, "v": hidden, "a": hidden, "o": hidden, "u": mlp,
+                       "d": hidden}
+        self.buf = {n: td.add(DeviceArray(seqs * w * 4)) for n, w in self.widths.items()}
+        self.buf["x"].upload(rng.normal(size=(seqs, hidden)).astype(np.float32))
+        m, buf = self.mats, self.buf
 
         def plan(ms, xs, ys):
-            return td.add(Plan(ms, [buf[n] for n in xs], [buf[n] for n in ys], batch=seqs, int8=True))
+            return td.add(Plan([m[n] for n in ms], [buf[n] for n in xs], [buf[n] for n in ys], batch=seqs,
+                               int8=True))
 
-        plans = [plan([wq, wk, wv], "xxx", "qkv"), plan([wo], "a", "o"), plan([wu], "o", "u"), plan([wd], "u", "d")]
-        kv = td.add(KVCache(1, cap, kvh, hd, seqs))
+        self.plans = {"qkv": plan(["wq", "wk", "wv"], "xxx", "qkv"), "o": plan(["wo"], "a", "o"),
+                      "up": plan(["wu"], "o", "u"), "down": plan(["wd"], "u", "d")}
+        self.kv = td.add(KVCache(1, cap, kvh, hd, seqs))
         for c0 in range(0, cap - 1, 512):
             n = min(512, cap - 1 - c0)
             with DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32)) as k, \
                     DeviceArray.from_host(rng.normal(size=(seqs, n, kvh, hd)).astype(np.float32)) as v:
-                kv.store(0, k, v, n, first_slot=c0, stream=stream)
+                self.kv.store(0, k, v, n, first_slot=c0, stream=stream)
                 stream.synchronize()
-        first = td.add(DeviceArray.from_host(np.full(seqs, cap - 1, np.int32)))  # the new token's slot
+        self.first = td.add(DeviceArray.from_host(np.full(seqs, cap - 1, np.int32)))  # the new token's slot
 
-        def step():
-            plans[0].run(stream)
-            kv.store_device(0, buf["k"], buf["v"], 1, first, stream=stream)
-            kv.attention(0, buf["q"], buf["a"], heads, cap, stream=stream)
-            for pl in plans[1:]:
-                pl.run(stream)
+    def store(self):
+        self.kv.store_device(0, self.buf["k"], self.buf["v"], 1, self.first, stream=self.stream)
+
+    def attention(self):
+        self.kv.attention(0, self.buf["q"], self.buf["a"], self.HEADS, self.CAP, stream=self.stream)
+
+    def step(self):
+        self.plans["qkv"].run(self.stream)
+        self.store()
+        self.attention()
+        for name in ("o", "up", "down"):
+            self.plans[name].run(self.stream)
+
+    def download(self, name):
+        return self.buf[name].download(np.empty((self.seqs, self.widths[name]), np.float32))
+
+
+def bench_decode_layer(steps, warmup, stream, seqs=64, graph=True, parts=None):
+    """The :class:`DecodeLayer` step for `seqs` sequences. Returns (eager ms per step, ms per step replaying
+    the step captured in a HIP graph, or None without `graph`). With a dict `parts`, also fills it with ms per
+    call of each launch group run alone back to back (`<plan>_plan`: prepare + GEMV; `<plan>_gemv`: the GEMV
+    launch alone, from events around it; `kv_store`, `attention`). Everything is released in a fixed order at
+    the end: the graph first, then the plans and the cache, then the buffers and matrices they read."""
+    from openneedle_amd.device import Event, Graph, Teardown, synchronize
+    with Teardown() as td:
+        layer = DecodeLayer(seqs, td, stream)
 
         def timed(fn):
             settle(fn)
@@ -263,7 +287,7 @@ def bench_decode_layer(steps, warmup, stream, seqs=64, graph=True, parts=None):
                 synchronize()
                 return t0.elapsed_ms(t1) / steps
 
-        eager = timed(step)
+        eager = timed(layer.step)
         if parts is not None:  # each launch group alone (back to back), and the GEMV part of each plan
             def gemv_only(pl):
                 with Event() as e0, Event() as e1:
@@ -274,15 +298,15 @@ def bench_decode_layer(steps, warmup, stream, seqs=64, graph=True, parts=None):
                         total += e0.elapsed_ms(e1)
                     return total / steps
 
-            for name, pl in zip(("qkv", "o", "up", "down"), plans):
+            for name, pl in layer.plans.items():
                 parts[f"{name}_plan"] = timed(lambda: pl.run(stream))
                 parts[f"{name}_gemv"] = gemv_only(pl)
-            parts["kv_store"] = timed(lambda: kv.store_device(0, buf["k"], buf["v"], 1, first, stream=stream))
-            parts["attention"] = timed(lambda: kv.attention(0, buf["q"], buf["a"], heads, cap, stream=stream))
+            parts["kv_store"] = timed(layer.store)
+            parts["attention"] = timed(layer.attention)
         graphed = None
         if graph:
             with Graph.capture(stream) as g:
-                step()
+                layer.step()
             td.add(g)  # registered last: released first
             graphed = timed(lambda: g.launch(stream))
     return eager, graphed

@@ -1,0 +1,81 @@
+"""The composed decode layer the bench times (bench.DecodeLayer: 64 sequences, hidden 512, 8 heads = 8 kv heads
+of 64, MLP 2048, int8-path CQ4 g32 projections, int8 KV cache of 2048 slots), one step, every stage against the
+oracle on the stage's own GPU input:
+
+- Q | K | V, O, MLP up and down: bit-exact with oracle.sdot_linear (the reference's SdotCQ arithmetic);
+- the new token's K / V rows in the cache: bit-exact with oracle.kv_quantize;
+- attention over the whole cache as the GPU holds it, per (sequence, head): normwise relative error at most
+  1e-5 against both oracle.attention_i8 and the fp64 closed form, and every output within 4e-6 * max|v| of
+  fp64 (v: the head's dequantized values). The queries come out of the Q projection with a standard deviation
+  of about 3.2 (scores about 3x those of tests/test_attention_gpu.py, where the per-output 1e-6 + 1e-5 bar
+  holds); on such inputs the oracle's own sequential fp32 arithmetic reaches 4.8e-6 normwise and
+  1.7e-6 * max|v| per output against fp64, so the bars are about twice the reference's own error;
+- the slots before the new token are untouched by the step."""
+import numpy as np
+import pytest
+
+import bench
+import oracle
+from openneedle_amd.device import Stream, Teardown, synchronize
+
+pytestmark = pytest.mark.gpu
+
+NORMWISE, PER_VALUE = 1e-5, 4e-6
+
+
+def fp64_attention(q, k8, v8, ks, vs):
+    heads, hd = q.shape
+    group = heads // k8.shape[1]
+    out, vmax = np.empty((heads, hd)), np.empty(heads)
+    for h in range(heads):
+        kh = h // group
+        k = k8[:, kh].astype(np.float64) * ks[:, kh, None]
+        v = v8[:, kh].astype(np.float64) * vs[:, kh, None]
+        s = k @ q[h].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ v
+        vmax[h] = np.abs(v).max()
+    return out, vmax
+
+
+def normwise(a, b):
+    return np.linalg.norm(a - b, axis=-1) / np.linalg.norm(b, axis=-1)
+
+
+def linear(layer, name, x):
+    packed, norms, cb = layer.host[name]
+    rows = packed.shape[0]
+    return oracle.sdot_linear(packed, norms, (rows, x.shape[1]), 4, 32, cb, x, 8)
+
+
+def test_decode_layer_b64_against_oracle():
+    seqs, L = 64, bench.DecodeLayer
+    with Teardown() as td:
+        stream = td.add(Stream())
+        layer = L(seqs, td, stream)
+        before = [layer.kv.read(0, s, L.CAP - 1) for s in (0, 37, 63)]
+        layer.step()
+        synchronize()
+        got = {n: layer.download(n) for n in layer.widths}
+        for w, xin, out in (("wq", "x", "q"), ("wk", "x", "k"), ("wv", "x", "v"), ("wo", "a", "o"),
+                            ("wu", "o", "u"), ("wd", "u", "d")):
+            np.testing.assert_array_equal(got[out], linear(layer, w, got[xin]), err_msg=f"{w}: {xin} -> {out}")
+        shape = (seqs, L.KVH, L.HD)
+        k8, ks = oracle.kv_quantize(got["k"].reshape(shape))
+        v8, vs = oracle.kv_quantize(got["v"].reshape(shape))
+        for s in range(seqs):
+            keys, values, kscale, vscale = layer.kv.read(0, s, L.CAP)
+            np.testing.assert_array_equal(keys[-1], k8[s], err_msg=f"seq {s}: new K row")
+            np.testing.assert_array_equal(values[-1], v8[s], err_msg=f"seq {s}: new V row")
+            np.testing.assert_array_equal(kscale[-1], ks[s])
+            np.testing.assert_array_equal(vscale[-1], vs[s])
+            qs, att = got["q"][s].reshape(L.HEADS, L.HD), got["a"][s].reshape(L.HEADS, L.HD)
+            want = oracle.attention_i8(qs, keys, values, kscale, vscale)
+            exact, vmax = fp64_attention(qs, keys, values, kscale, vscale)
+            assert normwise(att, want).max() <= NORMWISE, f"seq {s}: attention vs oracle {normwise(att, want)}"
+            assert normwise(att, exact).max() <= NORMWISE, f"seq {s}: attention vs fp64 {normwise(att, exact)}"
+            per_value = (np.abs(att - exact) / vmax[:, None]).max()
+            assert per_value <= PER_VALUE, f"seq {s}: attention vs fp64, {per_value:.2e} of max|v|"
+        for s, old in zip((0, 37, 63), before):
+            for a, b in zip(layer.kv.read(0, s, L.CAP - 1), old):
+                np.testing.assert_array_equal(a, b, err_msg=f"seq {s}: older slots changed")
