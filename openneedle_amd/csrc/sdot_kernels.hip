@@ -1279,6 +1279,134 @@ void launch_sdot_ks(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs,
     else launch_sdot_ks_j<KIND, 4>(g, job0, jobs, njobs, blocks, batch, s);
 }
 
+// ---------------------------------------------------------------------------
+// int8 path split over K on 16 x 16 tiles, for small matrices of 4-bit codes
+// (decode-layer projections at batch 2 and more)
+//
+// As sdot_mfma_ks_kernel, with a workgroup of kKs waves sharing one tile of
+// 16 weight rows x 16 batch rows, so a small matrix spreads over four times
+// the workgroups. Wave w takes groups w, w + kKs, ...; each 32-position step
+// of a group is one v_mfma_i32_16x16x32_i8: lane (j, t) = (l % 16, l / 16)
+// feeds batch row j's activations paired with code dword t of the chunk (A)
+// and the decoded centroids of that dword for weight row j (B); accumulator
+// register r of lane (j, t) is then the dot of weight row j with batch row
+// 4 t + r. Each round every wave turns its group's four dots into the
+// reference's terms (float(dot) * ns) * x_scale (sdot.cpp:142-149) and parks
+// them in LDS; after one barrier wave r (< 4) adds register r's kKs terms in
+// group order, so every output is value += term_g for g = 0, 1, 2, ... as
+// the reference sums: bit-identical outputs.
+// ---------------------------------------------------------------------------
+template <int GROUP>
+struct Ks16Slot {
+    static constexpr int kSteps = GROUP / 32;
+    uint32_t code[kSteps];  // code dword t of each step's chunk, weight row j
+    uint32_t q[2 * kSteps];  // batch row j's activation dwords 2t, 2t + 1 of each step
+    float xs[4];             // scales of batch rows 4t .. 4t + 3
+    uint16_t norm;           // weight row j's group norm
+};
+
+template <int GROUP>
+__global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+                                                             int njobs, SdotGeom geom) {
+    using S = Ks16Slot<GROUP>;
+    __shared__ float park[2][kKs][4][64];
+    const int lane = threadIdx.x & 63, jr = lane & 15, t = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int rb = blockIdx.x;  // 16-row block across the plan
+    const int blk = rb / (kRowsPerBlock / 16);
+    SdotJob J0 = job0;
+    if (njobs > 0) {
+        const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
+        const int j = find_job(cj, njobs, blk);
+        J0.codes = cj[j].codes;
+        J0.norms = cj[j].norms;
+        J0.q = cj[j].q;
+        J0.y = cj[j].y;
+        J0.rows = cj[j].rows;
+        J0.block_begin = cj[j].block_begin;
+        J0.batch = cj[j].batch;
+        J0.ystride = cj[j].ystride;
+        J0.xst = cj[j].xst;
+    }
+    const int rows = J0.rows, batch = J0.batch;
+    const int tile = blk - J0.block_begin;
+    const int rt = (rb % (kRowsPerBlock / 16)) * 16 + jr;  // this lane's weight row within the tile
+    const int row = tile * kRowsPerBlock + rt;
+    const int b0 = static_cast<int>(blockIdx.y) * 16;
+    const int nb = min(16, batch - b0);
+    const int groups = geom.groups;
+    const int dev = geom.windows * kWindow;
+    const uint32_t cent[4] = {geom.cent[0], geom.cent[1], geom.cent[2], geom.cent[3]};
+    const float cs = geom.centroid_scale;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J0.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms = buffer_rsrc(J0.norms + static_cast<size_t>(tile) * groups * kRowsPerBlock,
+                                                     static_cast<uint32_t>(groups) * kRowsPerBlock * 2u);
+    // batch rows past the tile's last read zeros (their offsets lie past the resource's end)
+    const __amdgpu_buffer_rsrc_t q = buffer_rsrc(reinterpret_cast<const int8_t *>(J0.q) + static_cast<size_t>(b0) * dev,
+                                                 static_cast<uint32_t>(nb) * dev);
+    const __amdgpu_buffer_rsrc_t xst = buffer_rsrc(J0.xst, static_cast<uint32_t>(groups) * batch * 4u);
+    const uint32_t qv = static_cast<uint32_t>(jr) * dev + 8u * t, cv = rt * 16u + 4u * t, nv = rt * 2u;
+    auto load = [&](S &sl, int g) {  // g < groups
+#pragma unroll
+        for (int st = 0; st < S::kSteps; ++st) {
+            const int c = g * S::kSteps + st;  // chunk of 32 positions
+            sl.code[st] = __builtin_amdgcn_raw_buffer_load_b32(codes, cv, __builtin_amdgcn_readfirstlane(c * kRowsPerBlock * 16), 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(q, qv + c * 32u, 0, 0);
+            sl.q[2 * st] = v[0];
+            sl.q[2 * st + 1] = v[1];
+        }
+        // scales of batch rows b0 + 4t .. + 3 (rows past the batch read the last row's, never stored)
+        const int so = __builtin_amdgcn_readfirstlane(g * batch * 4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            sl.xs[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xst, min(b0 + 4 * t + k, batch - 1) * 4u, so, 0));
+        sl.norm = __builtin_amdgcn_raw_buffer_load_b16(norms, nv, __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2), 0);
+    };
+    float value = 0.0f;  // wave w < 4: batch row 4t + w, weight row rt
+    const int rounds = (groups + kKs - 1) / kKs;
+    S cur, nxt;
+    load(cur, min(w, groups - 1));
+    for (int r = 0; r < rounds; ++r) {
+        load(nxt, min((r + 1) * kKs + w, groups - 1));  // past the last group: re-read, never used
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int st = 0; st < S::kSteps; ++st) {
+            uint32_t ce, co;
+            decode_nib(cur.code[st], cent[0], cent[1], cent[2], cent[3], ce, co);
+            const long a = static_cast<long>(cur.q[2 * st]) | (static_cast<long>(cur.q[2 * st + 1]) << 32);
+            const long b = static_cast<long>(ce) | (static_cast<long>(co) << 32);
+            acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, acc, 0, 0, 0);
+        }
+        const float ns = h2f(cur.norm) * cs;  // sdot.cpp:43-44
+#pragma unroll
+        for (int k = 0; k < 4; ++k) park[r & 1][w][k][lane] = (static_cast<float>(acc[k]) * ns) * cur.xs[k];
+        __syncthreads();
+        const int live = min(kKs, groups - r * kKs);  // groups of this round (uniform)
+        if (w < 4)
+            for (int src = 0; src < live; ++src) value = value + park[r & 1][src][w][lane];
+        cur = nxt;
+    }
+    const int m = b0 + 4 * t + w;
+    if (w < 4 && row < rows && m < batch)
+        ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * (J0.ystride ? J0.ystride : rows) + row] = value;
+}
+
+bool launch_sdot_ks16(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                      hipStream_t s) {
+    if (g.kind != kNib || g.group < 32 || g.group > kWindow) return false;
+    dim3 grid(blocks * (kRowsPerBlock / 16), (batch + 15) / 16), block(kKs * 64);
+    switch (g.group) {
+    case 32: hipLaunchKernelGGL(sdot_ks16_kernel<32>, grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL(sdot_ks16_kernel<64>, grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL(sdot_ks16_kernel<128>, grid, block, 0, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL(sdot_ks16_kernel<256>, grid, block, 0, s, job0, jobs, njobs, g); break;
+    }
+    ND_HIP(hipGetLastError());
+    return true;
+}
+
 int device_cus() {
     static int cus = [] {
         int dev = 0, n = 256;
@@ -1398,6 +1526,24 @@ static bool tile16_wanted(int batch) {
     return batch >= 8;
 }
 
+// The K split for small matrices (NEEDLE2_GPU_INT8_KSPLIT "always" / "never") and, within it, the 16 x 16
+// tiles (4-bit codes, batch 2 and more; NEEDLE2_GPU_INT8_KS16 "never", or "always" from batch 1).
+static bool ks_chosen(const SdotGeom &g, int blocks, int batch) {
+    const long mfma_waves = static_cast<long>(blocks) * (kRowsPerBlock / 32) * ((batch + 31) / 32);
+    const char *ks_mode = std::getenv("NEEDLE2_GPU_INT8_KSPLIT");
+    const bool ks_ok = g.group >= 32 && g.group <= kWindow && g.groups >= 2;
+    bool ks = ks_ok && mfma_waves < 4L * device_cus();
+    if (ks_mode && std::strcmp(ks_mode, "always") == 0) ks = ks_ok;
+    if (ks_mode && std::strcmp(ks_mode, "never") == 0) ks = false;
+    return ks;
+}
+
+static bool ks16_chosen(const SdotGeom &g, int batch) {
+    const char *ks16_mode = std::getenv("NEEDLE2_GPU_INT8_KS16");
+    return g.kind == kNib && !(ks16_mode && std::strcmp(ks16_mode, "never") == 0) &&
+           (batch >= 2 || (ks16_mode && std::strcmp(ks16_mode, "always") == 0));
+}
+
 void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
                       hipStream_t s) {
     if (blocks <= 0 || batch <= 0) return;
@@ -1406,7 +1552,9 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     // Kernel by size (environment overrides, "always" / "never", let the
     // tests run every kernel on every shape):
     //  - small matrices (fewer 32 x 32 tiles than SIMDs: decode projections)
-    //    of any batch split K over kKs waves per tile (NEEDLE2_GPU_INT8_KSPLIT);
+    //    of any batch split K over kKs waves per tile (NEEDLE2_GPU_INT8_KSPLIT),
+    //    on 16 x 16 tiles for 4-bit codes at batch 2 and more
+    //    (NEEDLE2_GPU_INT8_KS16: "never", or "always" from batch 1);
     //  - one batch row: the barrier-free row kernel (NEEDLE2_GPU_INT8_ROW);
     //  - 8 or more: batch tiles of 16 rows on v_mfma_i32_16x16x32_i8, every
     //    code decoded once per tile (NEEDLE2_GPU_INT8_TILE16);
@@ -1417,13 +1565,9 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     //    more rows (NEEDLE2_GPU_INT8_MFMA) and v_dot4 batch tiles below.
     const long mfma_waves = static_cast<long>(blocks) * (kRowsPerBlock / 32) * ((batch + 31) / 32);
     const char *mode = std::getenv("NEEDLE2_GPU_INT8_MFMA");
-    const char *ks_mode = std::getenv("NEEDLE2_GPU_INT8_KSPLIT");
     const char *quad_mode = std::getenv("NEEDLE2_GPU_INT8_QUAD");
-    const bool ks_ok = g.group >= 32 && g.group <= kWindow && g.groups >= 2;
-    bool ks = ks_ok && mfma_waves < 4L * device_cus();
-    if (ks_mode && std::strcmp(ks_mode, "always") == 0) ks = ks_ok;
-    if (ks_mode && std::strcmp(ks_mode, "never") == 0) ks = false;
-    if (ks) {
+    if (ks_chosen(g, blocks, batch)) {
+        if (ks16_chosen(g, batch) && launch_sdot_ks16(g, job0, jobs, njobs, blocks, batch, s)) return;
         if (g.kind == kNib) launch_sdot_ks<kNib>(g, job0, jobs, njobs, blocks, batch, s);
         else launch_sdot_ks<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
         return;

@@ -88,7 +88,7 @@ def test_int8_plan_many_matrices():
         np.testing.assert_array_equal(dy.download(np.empty((2, m.shape[0]), np.float32)), e)
 
 
-@pytest.mark.parametrize("mode", ["tile16", "quad", "always", "never", "ksplit"])
+@pytest.mark.parametrize("mode", ["tile16", "quad", "always", "never", "ksplit", "ksplit32"])
 @pytest.mark.parametrize("bits,group,batch", [(4, 32, 3), (4, 32, 9), (4, 32, 17), (4, 32, 33), (4, 32, 64),
                                               (4, 64, 40), (4, 128, 12), (4, 256, 5), (2, 32, 8), (2, 32, 33),
                                               (2, 64, 20), (4, 8, 6), (4, 16, 16), (2, 16, 2), (4, 32, 2)])
@@ -97,9 +97,11 @@ def test_int8_batched_tiles_bit_exact(bits, group, batch, mode, monkeypatch):
     int8 MFMA batch tiles of 16 rows (tile16: ragged last tile; groups below one code chunk fall back to the
     quad kernel), 4 x 4 x 4 int8 MFMA batch tiles of up to 16 rows, one lane per weight row (quad: ragged last
     quad and tile), 32 x 32 x 32 int8 MFMA tiles of 32 batch rows (always), v_dot4 batch tiles (never) and the
-    K split (ksplit); 300 ragged weight rows, zero / one-hot activation rows: bit-exact with the oracle."""
-    if mode == "ksplit":  # K split over 8 waves per tile (small-matrix path)
+    K split on 16 x 16 tiles (ksplit; 4-bit codes, else 32 x 32) and on 32 x 32 tiles (ksplit32); 300 ragged
+    weight rows, zero / one-hot activation rows: bit-exact with the oracle."""
+    if mode.startswith("ksplit"):  # K split over 8 waves per tile (small-matrix path)
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "always")
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_KS16", "never" if mode == "ksplit32" else "auto")
     else:
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "never")
         monkeypatch.setenv("NEEDLE2_GPU_INT8_TILE16", "always" if mode == "tile16" else "never")
@@ -116,10 +118,14 @@ def test_int8_batched_tiles_bit_exact(bits, group, batch, mode, monkeypatch):
     np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
 
 
-@pytest.mark.parametrize("mode", ["always", "auto"])
+@pytest.mark.parametrize("mode", ["always", "auto", "ksplit32"])
 def test_int8_plan_decode_batch(mode, monkeypatch):
-    """A layer's Q | K | V projections for 64 sequences in one plan (one prepare and one GEMV launch)."""
-    monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", mode)
+    """A layer's Q | K | V projections for 64 sequences in one plan (one prepare and one GEMV launch): the
+    16 x 16 K-split kernel (auto), the 32 x 32 K-split kernel (ksplit32), the 32 x 32 x 32 MFMA kernel
+    (always)."""
+    monkeypatch.setenv("NEEDLE2_GPU_INT8_MFMA", "always" if mode == "always" else "auto")
+    if mode == "ksplit32":
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_KS16", "never")
     mats, d_x, d_y, expected = [], [], [], []
     x = activations((64, 512), seed=640)
     d_in = DeviceArray.from_host(x)
@@ -137,16 +143,18 @@ def test_int8_plan_decode_batch(mode, monkeypatch):
             np.testing.assert_array_equal(dy.download(np.empty((64, 512), np.float32)), e)
 
 
-@pytest.mark.parametrize("mode", ["auto", "never", "ksplit"])
+@pytest.mark.parametrize("mode", ["auto", "never", "ksplit", "ksplit16"])
 @pytest.mark.parametrize("bits,group,dim", [(4, 8, 1000), (4, 32, 1000), (4, 64, 4096), (4, 256, 1300), (2, 16, 1000),
                                             (2, 32, 777), (2, 128, 2048)])
 def test_int8_single_row_kernels_bit_exact(bits, group, dim, mode, monkeypatch):
-    """Batch 1 (decode): the barrier-free row kernel (auto) and the windowed kernel (never), ragged shapes,
-    zero and one-hot inputs, bit-exact with the oracle."""
-    if mode == "ksplit":
+    """Batch 1 (decode): the barrier-free row kernel (auto), the windowed kernel (never) and the K split on
+    32 x 32 (ksplit) and 16 x 16 tiles (ksplit16, 4-bit codes), ragged shapes, zero and one-hot inputs,
+    bit-exact with the oracle."""
+    if mode.startswith("ksplit"):
         if group < 32:
             pytest.skip("the K-split path takes groups of 32 .. 256")
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "always")
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_KS16", "always" if mode == "ksplit16" else "never")
     else:
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "never")
         monkeypatch.setenv("NEEDLE2_GPU_INT8_ROW", mode)
@@ -155,3 +163,4 @@ def test_int8_single_row_kernels_bit_exact(bits, group, dim, mode, monkeypatch):
     for x in special_inputs(dim, seed=group + 1):
         np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group,
                                                                            cb, x[None])[0])
+
