@@ -443,6 +443,21 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     for (int i = t; i < HD; i += blockDim.x) vw[static_cast<size_t>(p->slot) * HD + i] = b.v[kh * HD + i];
     }
     __syncthreads();
+    // values: thread t takes 16-byte column c = t % (HD / 4) of the V rows of slots r, r + R, ..
+    // (r = t / (HD / 4), R = 256 / (HD / 4) subsets), so its loads are all in flight together; the R
+    // partial sums per output then add up in subset order. When HD / 4 does not divide 256 the last
+    // threads (r == R) take no slots and write no partials: R * G * HD <= 1024 G floats fit in qs.
+    // The first kPre rows of each thread are loaded here, before the scores and the softmax.
+    constexpr int kMaxG = 8, kPre = 8;
+    const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
+    const bool sub = r < R;
+    float4 vpre[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+        const int s = r + k * R;
+        vpre[k] = sub && s < length ? reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_at(p, s)) * HD)[c4]
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
     for (int s = t; s < length; s += blockDim.x) {
         const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, s)) * HD);
         for (int g = 0; g < G; ++g) {
@@ -474,19 +489,10 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         for (int s = t; s < length; s += blockDim.x) sc[g * length + s] *= inv;
         __syncthreads();
     }
-    // values: thread t takes 16-byte column c = t % (HD / 4) of the V rows of slots r, r + R, ..
-    // (r = t / (HD / 4), R = 256 / (HD / 4) subsets), so its loads are all in flight together; the R
-    // partial sums per output then add up in subset order. When HD / 4 does not divide 256 the last
-    // threads (r == R) take no slots and write no partials: R * G * HD <= 1024 G floats fit in qs.
-    constexpr int kMaxG = 8;
-    const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
-    const bool sub = r < R;
     float4 acc[kMaxG];
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 8
-    for (int s = sub ? r : length; s < length; s += R) {
-        const float4 v = reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_at(p, s)) * HD)[c4];
+    auto accumulate = [&](int s, const float4 &v) {
 #pragma unroll
         for (int g = 0; g < kMaxG; ++g)
             if (g < G) {
@@ -496,7 +502,13 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
                 acc[g].z += pr * v.z;
                 acc[g].w += pr * v.w;
             }
-    }
+    };
+#pragma unroll
+    for (int k = 0; k < kPre; ++k)
+        if (sub && r + k * R < length) accumulate(r + k * R, vpre[k]);
+#pragma unroll 8
+    for (int s = sub ? r + kPre * R : length; s < length; s += R)
+        accumulate(s, reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_at(p, s)) * HD)[c4]);
     float4 *wpart = reinterpret_cast<float4 *>(qs);  // [R][G][HD / 4]: R * G * HD = 1024 G floats
     __syncthreads();
 #pragma unroll
