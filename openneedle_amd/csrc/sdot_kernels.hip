@@ -1476,6 +1476,69 @@ __global__ __launch_bounds__(256) void sdot_prepare_wave_kernel(const float *__r
     if (p < dev) q[static_cast<size_t>(v) * dev + permuted_index(kind, p)] = out;
 }
 
+// Prepare for groups of 128 and 256 positions, one wave per group without
+// LDS: lane t holds positions t + 64 k (k < GROUP / 64) of its wave's group;
+// the FWHT stages 1 .. 32 run as in-wave butterflies on every k, then the
+// stages 64 and 128 between a lane's own values, in the reference's stage
+// order and with its operands (x + y, x - y); then the absmax over the wave
+// and the reference's quantiser as in sdot_prepare_wave_kernel. Same values
+// as sdot_prepare_kernel, bit for bit.
+template <int GROUP>
+__global__ __launch_bounds__(256) void sdot_prepare_wave_group_kernel(const float *__restrict__ x0,
+                                                                      const float *const *__restrict__ xptr, int batch,
+                                                                      int in, int padded, int dev, float scale,
+                                                                      int kind, int8_t *__restrict__ q,
+                                                                      float *__restrict__ xs, float *__restrict__ xst,
+                                                                      int groups) {
+    constexpr int VPL = GROUP / 64;  // values per lane
+    const int v = blockIdx.y;
+    const int t = threadIdx.x & 63;
+    const int base = (blockIdx.x * 4 + static_cast<int>(threadIdx.x >> 6)) * GROUP;  // wave-uniform
+    if (base >= dev) return;
+    const float *xv = (xptr ? xptr[v / batch] : x0) + static_cast<size_t>(v % batch) * in;
+    float r[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int p = base + t + 64 * k;
+        r[k] = p < in ? xv[p] : 0.0f;
+        wave_butterflies<64, 1>(r[k], t);
+    }
+#pragma unroll
+    for (int h = 1; h < VPL; h *= 2)  // stages 64 h
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+            if (!(k & h)) {
+                const float a = r[k], b = r[k + h];
+                r[k] = a + b;
+                r[k + h] = a - b;
+            }
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        r[k] = r[k] * scale;
+        m = fmaxf(m, fabsf(r[k]));
+    }
+    const float absmax = wave_max(m, t);
+    const bool live = base < padded;  // a whole group of the padded length
+    float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
+    if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
+    if (live && t == 0) {
+        xs[static_cast<size_t>(v) * groups + base / GROUP] = sc;
+        if (xst) xst[(static_cast<size_t>(v / batch) * groups + base / GROUP) * batch + v % batch] = sc;
+    }
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int p = base + t + 64 * k;
+        int8_t out = 0;
+        if (live) {
+            float val = rintf(r[k] / sc);
+            val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
+            out = static_cast<int8_t>(val);
+        }
+        if (p < dev) q[static_cast<size_t>(v) * dev + permuted_index(kind, p)] = out;
+    }
+}
+
 }  // namespace
 
 bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, int nvec, int in, int padded,
@@ -1495,6 +1558,17 @@ bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, i
         case 32: go(sdot_prepare_wave_kernel<32>); break;
         default: go(sdot_prepare_wave_kernel<64>); break;
         }
+        ND_HIP(hipGetLastError());
+        return true;
+    }
+    if (group <= 256) {
+        dim3 grid((dev + 4 * group - 1) / (4 * group), nvec), block(256);
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, block, 0, s, x0, xptr, batch, in, padded, dev, scale, kind,
+                               reinterpret_cast<int8_t *>(q), xs, xst, padded / group);
+        };
+        if (group == 128) go(sdot_prepare_wave_group_kernel<128>);
+        else go(sdot_prepare_wave_group_kernel<256>);
         ND_HIP(hipGetLastError());
         return true;
     }

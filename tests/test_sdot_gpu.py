@@ -53,13 +53,23 @@ def test_extended_groups_bit_exact(bits, group):
     np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
 
 
-def test_subnormal_scale_guard():
-    packed, norms, cb, dense = example(4, rows=4, dim=64, group=32)
-    q = CQMatrix(packed, norms, dense.shape, 4, 32, cb)
-    x = np.zeros(64, np.float32)
-    x[:32] = np.float32(4e-45)
-    x[40] = np.float32(1e-39)
-    np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, 4, 32, cb, x))
+@pytest.mark.parametrize("group", [32, 128, 256])
+def test_subnormal_scale_guard(group):
+    """Subnormal inputs (absmax / 127 underflows to zero: the scale is absmax itself), a zero group and a
+    one-hot group, through the one-wave-per-group prepare kernels (groups of up to 64 positions per wave, or
+    GROUP / 64 positions per lane for 128 and 256)."""
+    dim = 4 * group + 7
+    packed, norms, cb, dense = example(4, rows=40, dim=dim, group=group, seed=group)
+    q = CQMatrix(packed, norms, dense.shape, 4, group, cb)
+    x = np.zeros((2, dim), np.float32)
+    x[0, :group] = np.float32(4e-45)
+    x[0, group + 8] = np.float32(1e-39)
+    x[0, 3 * group + 1] = 1
+    x[1] = activations((1, dim), seed=group)[0]
+    x[1, group:2 * group] = 0
+    np.testing.assert_array_equal(q.matvec_int8(x), oracle.sdot_linear(packed, norms, dense.shape, 4, group, cb, x))
+    np.testing.assert_array_equal(q.matvec_int8(x[1]), oracle.sdot_linear(packed, norms, dense.shape, 4, group, cb,
+                                                                          x[1:])[0])
 
 
 @pytest.mark.parametrize("batch", [1, 4, 16])
