@@ -25,6 +25,7 @@ import argparse
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -45,6 +46,35 @@ def measured_traffic(kernel):
         return json.load(open(ROOT / "profiles" / "traffic.json"))["kernels"][kernel]["hbm_bytes"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def gpu_name(reported: str) -> str:
+    """The runtime's device name, or (when the runtime reports none) the GPU agent's marketing name from
+    rocminfo, run as a child process."""
+    if reported:
+        return reported
+    try:
+        out = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=30).stdout
+        names = [l.split(":", 1)[1].strip() for l in out.splitlines() if l.strip().startswith("Marketing Name:")]
+        gpus = [n for n in names if "Instinct" in n or "MI" in n]
+        return (gpus or names or [""])[-1]
+    except (OSError, ValueError, subprocess.SubprocessError):
+        return ""
+
+
+def cpu_model() -> str:
+    """lscpu's model name (the host CPU the baseline ran on), else /proc/cpuinfo's."""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=30).stdout
+        for l in out.splitlines():
+            if l.strip().startswith("Model name:"):
+                return l.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        return next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        return "unknown"
 
 
 def log(msg):
@@ -512,12 +542,9 @@ def cpu_baseline(budget_s=12.0, others=True):
     nbytes = packed.nbytes + norms.nbytes
     med, p10, p90, n = _cpu_time(lambda: [m(x) for m in mats], budget_s)
     del mats, packed, norms
-    try:
-        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
-    except (OSError, StopIteration):
-        model = "unknown"
+    model = cpu_model()
     out = {
-        "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+        "value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind, "cpu_model": model,
         "sample": f"{n} steps of 16 distinct CQ4 8192x8192 g32 FP32 GEMVs (batch 1, the GPU step's workload), "
                   f"median {med * 1e3:.1f} ms per step, {cores} OpenMP threads, {model}",
         "ms_per_step": _spread(med, p10, p90),
@@ -630,6 +657,7 @@ def main():
 
     from openneedle_amd.device import Stream, device_info
     info = device_info()
+    info["name"] = gpu_name(info["name"])
     log(f"device {info}")
     stream = Stream()
     rng = np.random.default_rng(20261201)

@@ -9,7 +9,8 @@
 // head h of kv head kh = h / G,
 //   s = dot(q_h, float(k_i8)) * k_scale * (1/sqrt(HD))   (sequential over d)
 //   p = softmax(s);  out[d] = sum_s (p_s * v_scale_s) * float(v_i8[s][d]).
-// The dot is the reference's sequential fp32 sum (no contraction). The
+// The dot runs over d in the reference's order but with fused multiply-adds
+// (one rounding per term instead of two), and the value sums likewise. The
 // softmax and the value sum are computed split-context (flash decoding):
 // each block owns a range of cache slots for one (sequence, kv head) and
 // keeps a running max m, a running sum l and unnormalized outputs o; a merge
