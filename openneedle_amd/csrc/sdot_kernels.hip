@@ -1280,15 +1280,17 @@ void launch_sdot_ks(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs,
 }
 
 // ---------------------------------------------------------------------------
-// int8 path split over K on 16 x 16 tiles, for small matrices of 4-bit codes
-// (decode-layer projections at batch 2 and more)
+// int8 path split over K on 16 x 16 tiles, for small matrices (decode-layer
+// projections and prompt chunks at batch 2 and more)
 //
 // As sdot_mfma_ks_kernel, with a workgroup of kKs waves sharing one tile of
 // 16 weight rows x 16 batch rows, so a small matrix spreads over four times
 // the workgroups. Wave w takes groups w, w + kKs, ...; each 32-position step
 // of a group is one v_mfma_i32_16x16x32_i8: lane (j, t) = (l % 16, l / 16)
-// feeds batch row j's activations paired with code dword t of the chunk (A)
-// and the decoded centroids of that dword for weight row j (B); accumulator
+// feeds batch row j's activations of positions 8t .. 8t + 7 of the step (A)
+// and weight row j's decoded centroids of the same positions (B): code
+// dword t of the step's 32 four-bit codes, or crumb selectors 2(t % 2) and
+// 2(t % 2) + 1 of code dword t / 2 of its 32 two-bit codes; accumulator
 // register r of lane (j, t) is then the dot of weight row j with batch row
 // 4 t + r. Each round every wave turns its group's four dots into the
 // reference's terms (float(dot) * ns) * x_scale (sdot.cpp:142-149) and parks
@@ -1299,13 +1301,13 @@ void launch_sdot_ks(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs,
 template <int GROUP>
 struct Ks16Slot {
     static constexpr int kSteps = GROUP / 32;
-    uint32_t code[kSteps];  // code dword t of each step's chunk, weight row j
+    uint32_t code[kSteps];  // the code dword of each step holding positions 8t .. 8t + 7, weight row j
     uint32_t q[2 * kSteps];  // batch row j's activation dwords 2t, 2t + 1 of each step
     float xs[4];             // scales of batch rows 4t .. 4t + 3
     uint16_t norm;           // weight row j's group norm
 };
 
-template <int GROUP>
+template <int KIND, int GROUP>
 __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
                                                              int njobs, SdotGeom geom) {
     using S = Ks16Slot<GROUP>;
@@ -1347,12 +1349,16 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
     const __amdgpu_buffer_rsrc_t q = buffer_rsrc(reinterpret_cast<const int8_t *>(J0.q) + static_cast<size_t>(b0) * dev,
                                                  static_cast<uint32_t>(nb) * dev);
     const __amdgpu_buffer_rsrc_t xst = buffer_rsrc(J0.xst, static_cast<uint32_t>(groups) * batch * 4u);
-    const uint32_t qv = static_cast<uint32_t>(jr) * dev + 8u * t, cv = rt * 16u + 4u * t, nv = rt * 2u;
+    // code byte offset of this lane's dword within a 16-byte chunk (4-bit: one step per chunk; 2-bit: the
+    // step's half of a 64-position chunk is added per step)
+    const uint32_t qv = static_cast<uint32_t>(jr) * dev + 8u * t, nv = rt * 2u;
+    const uint32_t cv = rt * 16u + (KIND == kNib ? 4u * t : 4u * (t >> 1));
     auto load = [&](S &sl, int g) {  // g < groups
 #pragma unroll
         for (int st = 0; st < S::kSteps; ++st) {
-            const int c = g * S::kSteps + st;  // chunk of 32 positions
-            sl.code[st] = __builtin_amdgcn_raw_buffer_load_b32(codes, cv, __builtin_amdgcn_readfirstlane(c * kRowsPerBlock * 16), 0);
+            const int c = g * S::kSteps + st;  // step of 32 positions
+            const int so = KIND == kNib ? c * kRowsPerBlock * 16 : (c >> 1) * kRowsPerBlock * 16 + (c & 1) * 8;
+            sl.code[st] = __builtin_amdgcn_raw_buffer_load_b32(codes, cv, __builtin_amdgcn_readfirstlane(so), 0);
             const auto v = __builtin_amdgcn_raw_buffer_load_b64(q, qv + c * 32u, 0, 0);
             sl.q[2 * st] = v[0];
             sl.q[2 * st + 1] = v[1];
@@ -1374,7 +1380,13 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
 #pragma unroll
         for (int st = 0; st < S::kSteps; ++st) {
             uint32_t ce, co;
-            decode_nib(cur.code[st], cent[0], cent[1], cent[2], cent[3], ce, co);
+            if constexpr (KIND == kNib) {
+                decode_nib(cur.code[st], cent[0], cent[1], cent[2], cent[3], ce, co);
+            } else {  // crumb selectors 2 (t % 2) and 2 (t % 2) + 1 of the dword
+                const uint32_t wd = cur.code[st] >> (4 * (t & 1));
+                ce = __builtin_amdgcn_perm(0u, cent[0], wd & 0x03030303u);
+                co = __builtin_amdgcn_perm(0u, cent[0], (wd >> 2) & 0x03030303u);
+            }
             const long a = static_cast<long>(cur.q[2 * st]) | (static_cast<long>(cur.q[2 * st + 1]) << 32);
             const long b = static_cast<long>(ce) | (static_cast<long>(co) << 32);
             acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, acc, 0, 0, 0);
@@ -1393,17 +1405,24 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
         ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * (J0.ystride ? J0.ystride : rows) + row] = value;
 }
 
-bool launch_sdot_ks16(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
-                      hipStream_t s) {
-    if (g.kind != kNib || g.group < 32 || g.group > kWindow) return false;
+template <int KIND>
+void launch_sdot_ks16_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
+                           int batch, hipStream_t s) {
     dim3 grid(blocks * (kRowsPerBlock / 16), (batch + 15) / 16), block(kKs * 64);
     switch (g.group) {
-    case 32: hipLaunchKernelGGL(sdot_ks16_kernel<32>, grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL(sdot_ks16_kernel<64>, grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL(sdot_ks16_kernel<128>, grid, block, 0, s, job0, jobs, njobs, g); break;
-    default: hipLaunchKernelGGL(sdot_ks16_kernel<256>, grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 32: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 64>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 128>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
     }
     ND_HIP(hipGetLastError());
+}
+
+bool launch_sdot_ks16(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                      hipStream_t s) {
+    if (g.group < 32 || g.group > kWindow) return false;
+    if (g.kind == kNib) launch_sdot_ks16_kind<kNib>(g, job0, jobs, njobs, blocks, batch, s);
+    else launch_sdot_ks16_kind<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
     return true;
 }
 
@@ -1601,7 +1620,7 @@ static bool tile16_wanted(int batch) {
 }
 
 // The K split for small matrices (NEEDLE2_GPU_INT8_KSPLIT "always" / "never") and, within it, the 16 x 16
-// tiles (4-bit codes, batch 2 and more; NEEDLE2_GPU_INT8_KS16 "never", or "always" from batch 1).
+// tiles (batch 2 and more; NEEDLE2_GPU_INT8_KS16 "never", or "always" from batch 1).
 static bool ks_chosen(const SdotGeom &g, int blocks, int batch) {
     const long mfma_waves = static_cast<long>(blocks) * (kRowsPerBlock / 32) * ((batch + 31) / 32);
     const char *ks_mode = std::getenv("NEEDLE2_GPU_INT8_KSPLIT");
@@ -1614,7 +1633,7 @@ static bool ks_chosen(const SdotGeom &g, int blocks, int batch) {
 
 static bool ks16_chosen(const SdotGeom &g, int batch) {
     const char *ks16_mode = std::getenv("NEEDLE2_GPU_INT8_KS16");
-    return g.kind == kNib && !(ks16_mode && std::strcmp(ks16_mode, "never") == 0) &&
+    return !(ks16_mode && std::strcmp(ks16_mode, "never") == 0) &&
            (batch >= 2 || (ks16_mode && std::strcmp(ks16_mode, "always") == 0));
 }
 
@@ -1627,8 +1646,8 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     // tests run every kernel on every shape):
     //  - small matrices (fewer 32 x 32 tiles than SIMDs: decode projections)
     //    of any batch split K over kKs waves per tile (NEEDLE2_GPU_INT8_KSPLIT),
-    //    on 16 x 16 tiles for 4-bit codes at batch 2 and more
-    //    (NEEDLE2_GPU_INT8_KS16: "never", or "always" from batch 1);
+    //    on 16 x 16 tiles at batch 2 and more (NEEDLE2_GPU_INT8_KS16:
+    //    "never", or "always" from batch 1);
     //  - one batch row: the barrier-free row kernel (NEEDLE2_GPU_INT8_ROW);
     //  - 8 or more: batch tiles of 16 rows on v_mfma_i32_16x16x32_i8, every
     //    code decoded once per tile (NEEDLE2_GPU_INT8_TILE16);
