@@ -3,11 +3,13 @@
 // NativeEngine, needle2/native.py:307-663).
 //
 // One step (engine.cpp:968-1044) runs on the handle's stream as: embedding
-// row, engram rows / projections / conv, then per layer the mHC projections,
-// the mixing kernel, the fused Q|K|V|gate GEMV, the q/k norms + RoPE + KV
-// store kernel, attention, the gate kernel, the out-projection GEMV and the
-// post kernel (attention residual, Hadamard MLP, Sinkhorn routing, lane
-// mixing, next layer's rms); then the final norm and the LM-head GEMV. The
+// row, then per layer the mHC projections, the mixing kernel, the fused
+// Q|K|V|gate GEMV, the q/k norms + RoPE + KV store kernel, attention, the
+// gate kernel, the out-projection GEMV and the post kernel (attention
+// residual, Hadamard MLP, Sinkhorn routing, lane mixing, next layer's rms);
+// then the final norm and the LM-head GEMV. The engram rows / projections /
+// conv of each site depend on the token history only: they run on a second
+// stream, which the step joins just before that site's mixing kernel. The
 // CQ matrices are the caller's handles (borrowed, as the reference borrows
 // its CQ pointers) and run through the library's bit-exact GEMV kernels with
 // the engine's own staging; dense tensors are copied to device memory at
@@ -286,6 +288,11 @@ struct GpuEngine {
     std::vector<std::unique_ptr<DevBuf<float>>> dense;  // device copies of dense tensors
     std::vector<const float *> dptr;       // per tensor: device fp32 data (dense) or null
     hipStream_t stream = nullptr;
+    // The engram work of a launch depends only on the token history: it runs on
+    // `side` from the uploaded tokens on, and the main stream waits for site k
+    // (ev_site[k]) just before the mixing kernel of layer sites[k].
+    hipStream_t side = nullptr;
+    hipEvent_t ev_upload = nullptr, ev_site[kEngMaxSites] = {};
     EngineDims dims{};
     EngineBufs b{};
     DevBuf<float> work;
@@ -301,7 +308,7 @@ struct GpuEngine {
     HostBuf<int64_t> hids;
     DevBuf<int> lens;      // per chunk: attention list lengths [chunk]
     HostBuf<int> hlens;
-    DevBuf<float> logits, part, embed_z, row_scratch;
+    DevBuf<float> logits, part, embed_z, row_scratch, engram_scratch;
     DevBuf<float> attn_scores;  // fp32-KV attention scores past the LDS budget
     HostBuf<float> hlogits, hhidden;
     std::vector<Projection> mhc_proj, qkvg, oproj;
@@ -319,6 +326,11 @@ struct GpuEngine {
 
     GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count, int activation_bits);
     ~GpuEngine() {
+        if (side) (void)hipStreamSynchronize(side);
+        for (hipEvent_t e : ev_site)
+            if (e) (void)hipEventDestroy(e);
+        if (ev_upload) (void)hipEventDestroy(ev_upload);
+        if (side) (void)hipStreamDestroy(side);
         if (stream) (void)hipStreamDestroy(stream);
     }
     void reset(int prefix_len);
@@ -352,7 +364,7 @@ struct GpuEngine {
                       const float *v);
     int decode_loop(int first_token, int max_new_tokens, const DfaC *dfa, int *out, int *generated);
     void upload_tokens(int tokens);
-    void run_engrams(int tokens);
+    void run_engram_site(int site, int tokens, hipStream_t s);
     // copies `prefix` slots of every (layer, K | V, kv head) row between the cache and the snapshot
     void copy_prefix_slots(bool to_snapshot);
 };
@@ -381,6 +393,11 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     }
     ND_CHECK(count >= final_norm() + 1, "engine: tensor count does not match the geometry");
     ND_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+    if (c.num_sites) {
+        ND_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+        ND_HIP(hipEventCreateWithFlags(&ev_upload, hipEventDisableTiming));
+        for (int k = 0; k < c.num_sites; ++k) ND_HIP(hipEventCreateWithFlags(&ev_site[k], hipEventDisableTiming));
+    }
 
     // tensors: matrices keep the caller's CQ handle; dense data goes to the device as fp32
     mats.resize(count);
@@ -542,7 +559,7 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
                  "engine: engram tables shape does not match the geometry");
         (void)vec(e0 + 3);
         (void)mat(e0 + 1, D, D), (void)mat(e0 + 2, D, D);
-        if (mats[e0].cq) row_scratch.reserve(size_t(chunk) * c.tables * mats[e0].cq->padded);
+        if (mats[e0].cq) engram_scratch.reserve(size_t(chunk) * c.tables * mats[e0].cq->padded);
     }
     (void)vec(final_norm());
     (void)mat(0, c.vocab, D);
@@ -743,9 +760,9 @@ void GpuEngine::import_state(int pos, int pinned, const int *ids, const int *pos
             position = p0;
             for (int t = 0; t < T; ++t) set_token(t, ids[p0 + t]);
             upload_tokens(T);
-            run_engrams(T);
+            for (int site = 0; site < c.num_sites; ++site) run_engram_site(site, T, stream);
+            ND_HIP(hipStreamSynchronize(stream));  // the host rewrites the token buffers next chunk
         }
-        ND_HIP(hipStreamSynchronize(stream));
     }
     position = pos;
 }
@@ -913,17 +930,16 @@ void GpuEngine::upload_tokens(int T) {
 }
 
 // Engram rows, their quantiser, key / value projections, the conv and the ring
-// for the T uploaded tokens (engine.cpp:755-781).
-void GpuEngine::run_engrams(int T) {
-    hipStream_t s = stream;
+// of one site for the T uploaded tokens (engine.cpp:755-781).
+void GpuEngine::run_engram_site(int site, int T, hipStream_t s) {
     const StepParams *dp = params.p;
-    for (int site = 0; site < c.num_sites; ++site) {
+    {
         const int e0 = engram_base() + 4 * site;
         const Mat &tab = mats[e0];
         const int64_t *rows = ids.p + chunk + size_t(site) * chunk * c.tables;
         if (tab.cq)
             launch_cq_rows(tab.cq->geom(), tab.cq->codes.p, tab.cq->norms.p, rows, T * c.tables, c.subdim,
-                           tab.cq->padded, row_scratch.p, b.e, s);
+                           tab.cq->padded, engram_scratch.p, b.e, s);
         else
             launch_eng_dense_rows(tab.dense, c.subdim, rows, T * c.tables, b.e, s);
         launch_eng_engram_in(b, dp, site, dims, T, s);
@@ -940,6 +956,7 @@ void GpuEngine::run(int tokens) {
     const int D = c.dim, HD = c.head_dim, T = tokens;
     hipStream_t s = stream;
     upload_tokens(T);
+    if (c.num_sites) ND_HIP(hipEventRecord(ev_upload, s));
     const StepParams *dp = params.p;
 
     // embedding rows, lanes (engine.cpp:972-974)
@@ -950,7 +967,20 @@ void GpuEngine::run(int tokens) {
     else
         launch_eng_dense_rows(emb.dense, D, ids.p, T, embed_z.p, s);
     launch_eng_start(embed_z.p, b, dims, T, s);
-    run_engrams(T);
+    // engram sites up to layer `upto` onto the side stream, behind the upload
+    bool sent[kEngMaxSites] = {};
+    auto send_sites = [&](int upto) {
+        for (int k = 0; k < c.num_sites; ++k)
+            if (!sent[k] && c.sites[k] <= upto) {
+                run_engram_site(k, T, side);
+                ND_HIP(hipEventRecord(ev_site[k], side));
+                sent[k] = true;
+            }
+    };
+    if (c.num_sites) {
+        ND_HIP(hipStreamWaitEvent(side, ev_upload, 0));
+        send_sites(1);
+    }
 
     const int G = c.heads / c.kvheads;
     int maxlen = 0;
@@ -959,16 +989,30 @@ void GpuEngine::run(int tokens) {
         for (int t = 0; t < T; ++t) hlens.p[t] = hparams.p[t].length;
         ND_HIP(hipMemcpyAsync(lens.p, hlens.p, size_t(T) * sizeof(int), hipMemcpyHostToDevice, s));
     }
-    for (int l = 0; l < c.layers; ++l) {
-        mhc_proj[l].run(s, T);
-        {
-            const int first[3] = {l * mhc_rows[0], l * mhc_rows[1], l * mhc_rows[2]};
-            launch_eng_dense3(phi, first, mhc_rows, b.mhc_out, dims.mhc_stride, c.lanes * c.dim, b.nx, T, s);
-        }
-        int sites[kEngMaxSites], ns = 0;
+    // a layer's post runs with the next layer's mHC projections and mixing
+    // when those are dense and the geometry fits the fused kernel
+    const bool fuse = phi[0] && phi[1] && phi[2] && eng_post_mix_fits(dims);
+    auto layer_sites = [&](int l, int *sites) {  // waits for their engram work
+        int ns = 0;
         for (int k = 0; k < c.num_sites; ++k)
-            if (c.sites[k] == l) sites[ns++] = k;
-        launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, T, s);
+            if (c.sites[k] == l) {
+                ND_CHECK(sent[k], "internal: engram site joined before it was sent");
+                sites[ns++] = k;
+                ND_HIP(hipStreamWaitEvent(s, ev_site[k], 0));
+            }
+        return ns;
+    };
+    for (int l = 0; l < c.layers; ++l) {
+        if (l == 0 || !fuse) {
+            mhc_proj[l].run(s, T);
+            {
+                const int first[3] = {l * mhc_rows[0], l * mhc_rows[1], l * mhc_rows[2]};
+                launch_eng_dense3(phi, first, mhc_rows, b.mhc_out, dims.mhc_stride, c.lanes * c.dim, b.nx, T, s);
+            }
+            int sites[kEngMaxSites];
+            const int ns = layer_sites(l, sites);
+            launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, T, s);
+        }
         qkvg[l].run(s, T);
         if (!int8_kv) {
             // one token: norms, RoPE, store and attention in one kernel; a chunk
@@ -1011,7 +1055,15 @@ void GpuEngine::run(int tokens) {
             launch_eng_gate(b, dims, T, s);
         }
         oproj[l].run(s, T);
-        launch_eng_post(b, layer[l], mh, l, l + 1 < c.layers, dims, T, s);
+        if (fuse && l + 1 < c.layers) {
+            int sites[kEngMaxSites];
+            const int ns = layer_sites(l + 1, sites);
+            const int first[3] = {(l + 1) * mhc_rows[0], (l + 1) * mhc_rows[1], (l + 1) * mhc_rows[2]};
+            launch_eng_post_mix(b, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, dims, T, s);
+        } else {
+            launch_eng_post(b, layer[l], mh, l, l + 1 < c.layers, dims, T, s);
+        }
+        send_sites(l + 3);  // two layers ahead of their use
     }
     launch_eng_final(b, dptr[final_norm()], dims, T, s);
 }

@@ -282,22 +282,11 @@ struct MixArgs {
     int mhc_row[3];
 };
 
-// engine.cpp:980-992: lane gates from the mHC projections, the pre-mixed
-// residual u = bx, engram gates, then z = quant(rms(bx) * (1 + norm_in)).
-__global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, MixArgs m,
-                                                              EngineDims d) {
-    const EngineBufs b = at_token(b0, d, blockIdx.y);
-    __shared__ float red[kEngThreads / 64];
-    __shared__ float hp[16];
-    __shared__ float zs[4096], ps[4096];
-    __shared__ float proj[2 * 8 + 64];  // this layer's mHC projections: pre [N], post [N], res [N * N]
-    const int N = d.N, D = d.D, l = m.l;
-    // (no indexing of b's pointer arrays by a runtime value: that would place b in private memory)
-    const float *pre_rows = b.mhc_out[0] + m.mhc_row[0], *post_rows = b.mhc_out[1] + m.mhc_row[1];
-    const float *res_rows = b.mhc_out[2] + m.mhc_row[2];
-    for (int task = threadIdx.x; task < 2 * N + N * N; task += blockDim.x)
-        proj[task] = task < N ? pre_rows[task] : task < 2 * N ? post_rows[task - N] : res_rows[task - 2 * N];
-    __syncthreads();
+// Lane gates of layer l from its mHC projections proj (LDS: pre [N], post
+// [N], res [N * N]) into hp (LDS) and b (engine.cpp:980-986).
+__device__ __forceinline__ void mix_gates(const EngineBufs &b, const MhcDev &mh, int l, const float *proj, float *hp,
+                                          const EngineDims &d) {
+    const int N = d.N;
     if (threadIdx.x < static_cast<unsigned>(N)) {
         const int n = threadIdx.x;
         const float pre = proj[n], post = proj[N + n];
@@ -308,14 +297,13 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, Lay
         b.hpost[n] = hpost;
     }
     for (int i = threadIdx.x; i < N * N; i += blockDim.x) b.hres[i] = proj[2 * N + i];
-    __syncthreads();
-    for (int i = threadIdx.x; i < D; i += blockDim.x) {
-        float sum = 0.0f;
-        for (int n = 0; n < N; ++n) sum += hp[n] * b.x[n * D + i];
-        b.u[i] = sum;
-        b.bx[i] = sum;
-    }
-    __syncthreads();
+}
+
+// The engram gates of the layer's sites on bx (engine.cpp:987-991), after a barrier that
+// follows the stores of b.u and b.bx. Ends with a barrier.
+__device__ void mix_sites(const EngineBufs &b, const MixArgs &m, const EngineDims &d, float *red, float *zs,
+                          float *ps) {
+    const int D = d.D;
     for (int k = 0; k < m.nsites; ++k) {
         const int s = m.sites[k];
         rms_block(b.u, zs, D, nullptr, red);
@@ -327,6 +315,34 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, Lay
         for (int i = threadIdx.x; i < D; i += blockDim.x) b.bx[i] += alpha * b.ev[s * D + i];
         __syncthreads();
     }
+}
+
+// engine.cpp:980-992: lane gates from the mHC projections, the pre-mixed
+// residual u = bx, engram gates, then z = quant(rms(bx) * (1 + norm_in)).
+__global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, MixArgs m,
+                                                              EngineDims d) {
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
+    __shared__ float red[kEngThreads / 64];
+    __shared__ float hp[16];
+    __shared__ float zs[4096], ps[4096];
+    __shared__ float proj[2 * 8 + 64];  // this layer's mHC projections: pre [N], post [N], res [N * N]
+    const int N = d.N, D = d.D;
+    // (no indexing of b's pointer arrays by a runtime value: that would place b in private memory)
+    const float *pre_rows = b.mhc_out[0] + m.mhc_row[0], *post_rows = b.mhc_out[1] + m.mhc_row[1];
+    const float *res_rows = b.mhc_out[2] + m.mhc_row[2];
+    for (int task = threadIdx.x; task < 2 * N + N * N; task += blockDim.x)
+        proj[task] = task < N ? pre_rows[task] : task < 2 * N ? post_rows[task - N] : res_rows[task - 2 * N];
+    __syncthreads();
+    mix_gates(b, mh, m.l, proj, hp, d);
+    __syncthreads();
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+        float sum = 0.0f;
+        for (int n = 0; n < N; ++n) sum += hp[n] * b.x[n * D + i];
+        b.u[i] = sum;
+        b.bx[i] = sum;
+    }
+    __syncthreads();
+    mix_sites(b, m, d, red, zs, ps);
     rms_block(b.bx, b.z, D, ld.norm_in, red);
     quantize_block(b.z, D, d.abits, red);
 }
@@ -570,16 +586,15 @@ __global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, En
 // layer's rms of x when `next_rms`. Thread i < D owns column i of every
 // vector (loaded once at the start); only the Hadamard transforms go through
 // LDS.
-__global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, int l,
-                                                               int next_rms, EngineDims d) {
-    const EngineBufs b = at_token(b0, d, blockIdx.y);
-    __shared__ float red[kEngThreads / 64];
-    __shared__ float mlp[4096];
-    __shared__ float hr[64], hpo[8];
+// With nxs (LDS, N * D floats, may alias mlp) the next layer's rms goes there
+// instead of to b.nx; x[0..N) ends as thread i's column of the new lanes.
+__device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l,
+                                           int next_rms, const EngineDims &d, float *red, float *mlp, float *hr,
+                                           float *hpo, float *nxs, float (&x)[8]) {
     const int D = d.D, N = d.N, i = threadIdx.x;
     const bool own = i < D;
     // every load of the kernel, issued before the first wait
-    float proj = 0.0f, gn = 0.0f, bx = 0.0f, u = 0.0f, gh = 0.0f, d1 = 0.0f, d3 = 0.0f, x[8];
+    float proj = 0.0f, gn = 0.0f, bx = 0.0f, u = 0.0f, gh = 0.0f, d1 = 0.0f, d3 = 0.0f;
     if (own) {
         proj = b.proj[i];
         gn = ld.post_norm[i];
@@ -634,9 +649,20 @@ __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, La
     }
     if (next_rms) {  // the next layer's nx = rms(x) over all N * D values
         r = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(N * D) + 1e-6f);
+        float *nx = nxs ? nxs : b.nx;
         if (own)
-            for (int n = 0; n < N; ++n) b.nx[n * D + i] = x[n] * r;
+            for (int n = 0; n < N; ++n) nx[n * D + i] = x[n] * r;
     }
+}
+
+__global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, int l,
+                                                               int next_rms, EngineDims d) {
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
+    __shared__ float red[kEngThreads / 64];
+    __shared__ float mlp[4096];
+    __shared__ float hr[64], hpo[8];
+    float x[8];
+    post_layer(b, ld, mh, l, next_rms, d, red, mlp, hr, hpo, nullptr, x);
 }
 
 // z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
@@ -686,6 +712,116 @@ __global__ __launch_bounds__(256) void eng_dense_multi_kernel(DenseRows a, int c
     for (int i = threadIdx.x; i < cols; i += blockDim.x) s += row[i] * x[i];
     s = block_sum(s, red);
     if (threadIdx.x == 0) a.y[m][static_cast<size_t>(blockIdx.y) * ystride + r] = s;
+}
+
+// Row r of the dense mHC projections: pre rows, then post rows, then res rows.
+__device__ __forceinline__ const float4 *mhc_row_ptr(const DenseRows &w, int r, int N, int cols) {
+    const int m = r < N ? 0 : r < 2 * N ? 1 : 2;
+    const int local = r - (m == 0 ? 0 : m == 1 ? N : 2 * N);
+    const float *base = m == 0 ? w.w[0] : m == 1 ? w.w[1] : w.w[2];
+    const int first = m == 0 ? w.first[0] : m == 1 ? w.first[1] : w.first[2];
+    return reinterpret_cast<const float4 *>(base + static_cast<size_t>(first + local) * cols);
+}
+
+// One workgroup per token does eng_post_kernel's work for layer l, then the
+// next layer's dense mHC projections (eng_dense_multi_kernel's rows) and
+// eng_mix_kernel's work (engine.cpp:1024-1040, then 968-992 of layer l + 1),
+// which saves two launches per layer. The projection weights (rows of N * D
+// floats, N * D a multiple of 256) are loaded at the start, into registers,
+// while the post waits on its own loads; the rms'd lanes stay in LDS and each
+// thread's column of the new lanes in registers. One wave sums a projection
+// row in eng_dense_multi_kernel's order: lane l's float4 column l + 64 k holds
+// element k of that kernel's threads 4 l .. 4 l + 3, whose partial sums the
+// lane keeps apart, and block_sum's tree over 64 threads and the sequential
+// sum of its four waves follow, so the outputs are the same bits as the
+// separate launches'. Needs D <= THREADS, N * D <= 4096.
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, LayerDev ld, LayerDev ldn, MhcDev mh,
+                                                               int l, DenseRows w, MixArgs m, EngineDims d) {
+    constexpr int kWaves = THREADS / 64, kPF = 8;  // float4 columns per lane held for each prefetched row
+    constexpr int kRowsPF = (24 + kWaves - 1) / kWaves;  // rows per wave held (24: the mHC rows at N = 4)
+    const EngineBufs b = at_token(b0, d, blockIdx.y);
+    __shared__ float red[kWaves];
+    __shared__ float mlp[4096];  // the MLP vector, then the rms'd lanes
+    __shared__ float hr[64], hpo[8], hp[16];
+    __shared__ float zs[4096], ps[4096];
+    __shared__ float proj[2 * 8 + 64];
+    const int N = d.N, D = d.D, R = 2 * N + N * N, cols = N * D, c4n = cols / 4;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = threadIdx.x;
+    float4 pf[kRowsPF][kPF];
+#pragma unroll
+    for (int j = 0; j < kRowsPF; ++j) {
+        const int r = wave + j * kWaves;
+        const float4 *row = r < R ? mhc_row_ptr(w, r, N, cols) : nullptr;
+#pragma unroll
+        for (int k = 0; k < kPF; ++k)
+            pf[j][k] = row && lane + 64 * k < c4n ? row[lane + 64 * k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    float x[8];
+    post_layer(b, ld, mh, l, 1, d, red, mlp, hr, hpo, mlp, x);
+    __syncthreads();
+    const float4 *nx4 = reinterpret_cast<const float4 *>(mlp);
+    auto fma4 = [](float4 &acc, const float4 &a, const float4 &c) {
+        acc.x += a.x * c.x;
+        acc.y += a.y * c.y;
+        acc.z += a.z * c.z;
+        acc.w += a.w * c.w;
+    };
+    auto row_sum = [&](float4 acc) {  // threads 4 lane .. 4 lane + 3 -> block_sum over 256 threads
+        float v = (acc.x + acc.y) + (acc.z + acc.w);
+        v += butterfly_partner<1>(v, lane);
+        v += butterfly_partner<2>(v, lane);
+        v += butterfly_partner<4>(v, lane);
+        v += butterfly_partner<8>(v, lane);
+        const int iv = __builtin_bit_cast(int, v);
+        float total = 0.0f;
+        total += __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+        total += __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+        total += __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+        total += __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+        return total;
+    };
+#pragma unroll
+    for (int j = 0; j < kRowsPF; ++j) {
+        const int r = wave + j * kWaves;  // uniform over the wave
+        if (r < R) {
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int k = 0; k < kPF; ++k)
+                if (lane + 64 * k < c4n) fma4(acc, pf[j][k], nx4[lane + 64 * k]);
+            const float4 *row = mhc_row_ptr(w, r, N, cols);
+            for (int c = lane + 64 * kPF; c < c4n; c += 64) fma4(acc, row[c], nx4[c]);
+            const float sum = row_sum(acc);
+            if (lane == 0) proj[r] = sum;
+        }
+    }
+    for (int r = wave + kRowsPF * kWaves; r < R; r += kWaves) {
+        const float4 *row = mhc_row_ptr(w, r, N, cols);
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int c = lane; c < c4n; c += 64) fma4(acc, row[c], nx4[c]);
+        const float sum = row_sum(acc);
+        if (lane == 0) proj[r] = sum;
+    }
+    __syncthreads();
+    mix_gates(b, mh, l + 1, proj, hp, d);
+    __syncthreads();
+    const bool own = i < D;
+    float u = 0.0f;
+    if (own) {
+        for (int n = 0; n < N; ++n) u += hp[n] * x[n];
+        b.u[i] = u;
+        b.bx[i] = u;
+    }
+    if (m.nsites) {
+        __syncthreads();
+        mix_sites(b, m, d, red, zs, ps);
+        rms_block(b.bx, b.z, D, ldn.norm_in, red);
+    } else {  // rms_block's arithmetic on the registers
+        const float r = 1.0f / sqrtf(block_sum(own ? u * u : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+        if (own) b.z[i] = u * r * (1.0f + ldn.norm_in[i]);
+        __syncthreads();
+    }
+    quantize_block(b.z, D, d.abits, red);
 }
 
 __global__ __launch_bounds__(256) void eng_dense_rows_kernel(const float *__restrict__ w, int cols,
@@ -768,6 +904,31 @@ void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, 
                      const EngineDims &d, int tokens, hipStream_t s) {
     hipLaunchKernelGGL(eng_post_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, l, next_rms ? 1 : 0,
                        d);
+    ND_HIP(hipGetLastError());
+}
+
+bool eng_post_mix_fits(const EngineDims &d) {
+    return d.D <= kEngThreads && d.N * d.D <= 4096 && (d.N * d.D) % 256 == 0 && d.hada <= 4096;
+}
+
+void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
+                         const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
+                         int tokens, hipStream_t s) {
+    ND_CHECK(eng_post_mix_fits(d), "internal: fused post / mixing launch outside its geometry");
+    DenseRows a{};
+    for (int k = 0; k < 3; ++k) {
+        a.w[k] = w[k];
+        a.first[k] = first[k];
+    }
+    MixArgs m{};
+    m.l = l + 1;
+    m.nsites = nsites;
+    for (int k = 0; k < nsites; ++k) m.sites[k] = sites[k];
+    if (d.D <= 512)
+        hipLaunchKernelGGL(eng_post_mix_kernel<512>, dim3(1, tokens), dim3(512), 0, s, b, ld, ldn, mh, l, a, m, d);
+    else
+        hipLaunchKernelGGL(eng_post_mix_kernel<kEngThreads>, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, ldn, mh,
+                           l, a, m, d);
     ND_HIP(hipGetLastError());
 }
 
