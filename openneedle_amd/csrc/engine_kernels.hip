@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace nd {
 
@@ -200,15 +201,6 @@ __device__ float sinkhorn_lanes(float a, int lane) {
     return a;
 }
 
-__device__ float sinkhorn_wave(float a, int n, int lane) {
-    switch (n) {
-    case 1: return sinkhorn_lanes<1>(a, lane);
-    case 2: return sinkhorn_lanes<2>(a, lane);
-    case 4: return sinkhorn_lanes<4>(a, lane);
-    default: return sinkhorn_lanes<8>(a, lane);
-    }
-}
-
 // x[n][d] = z[d] * sqrt(D) for every lane (engine.cpp:973-974), then nx = rms(x).
 __global__ __launch_bounds__(kEngThreads) void eng_start_kernel(const float *__restrict__ z, EngineBufs b0,
                                                                 EngineDims d) {
@@ -284,9 +276,8 @@ struct MixArgs {
 
 // Lane gates of layer l from its mHC projections proj (LDS: pre [N], post
 // [N], res [N * N]) into hp (LDS) and b (engine.cpp:980-986).
-__device__ __forceinline__ void mix_gates(const EngineBufs &b, const MhcDev &mh, int l, const float *proj, float *hp,
-                                          const EngineDims &d) {
-    const int N = d.N;
+template <int N>
+__device__ __forceinline__ void mix_gates(const EngineBufs &b, const MhcDev &mh, int l, const float *proj, float *hp) {
     if (threadIdx.x < static_cast<unsigned>(N)) {
         const int n = threadIdx.x;
         const float pre = proj[n], post = proj[N + n];
@@ -319,6 +310,7 @@ __device__ void mix_sites(const EngineBufs &b, const MixArgs &m, const EngineDim
 
 // engine.cpp:980-992: lane gates from the mHC projections, the pre-mixed
 // residual u = bx, engram gates, then z = quant(rms(bx) * (1 + norm_in)).
+template <int N>
 __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, MixArgs m,
                                                               EngineDims d) {
     const EngineBufs b = at_token(b0, d, blockIdx.y);
@@ -326,17 +318,18 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, Lay
     __shared__ float hp[16];
     __shared__ float zs[4096], ps[4096];
     __shared__ float proj[2 * 8 + 64];  // this layer's mHC projections: pre [N], post [N], res [N * N]
-    const int N = d.N, D = d.D;
+    const int D = d.D;
     // (no indexing of b's pointer arrays by a runtime value: that would place b in private memory)
     const float *pre_rows = b.mhc_out[0] + m.mhc_row[0], *post_rows = b.mhc_out[1] + m.mhc_row[1];
     const float *res_rows = b.mhc_out[2] + m.mhc_row[2];
     for (int task = threadIdx.x; task < 2 * N + N * N; task += blockDim.x)
         proj[task] = task < N ? pre_rows[task] : task < 2 * N ? post_rows[task - N] : res_rows[task - 2 * N];
     __syncthreads();
-    mix_gates(b, mh, m.l, proj, hp, d);
+    mix_gates<N>(b, mh, m.l, proj, hp);
     __syncthreads();
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
         float sum = 0.0f;
+#pragma unroll
         for (int n = 0; n < N; ++n) sum += hp[n] * b.x[n * D + i];
         b.u[i] = sum;
         b.bx[i] = sum;
@@ -423,9 +416,10 @@ template <bool PREPARED, bool GLOBAL_SCORES>
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d,
                                                              float *__restrict__ scores, int max_length) {
+    constexpr int kMaxG = 8, kPre = 8, kWaves = 4;
     extern __shared__ float sc_lds[];  // [G][length] when the scores fit
     __shared__ float qs[8 * 1024];  // query heads, then the partial outputs [R][G][HD] (1024 G floats)
-    __shared__ float red[4];
+    __shared__ float red[kMaxG * kWaves];
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     p += blockIdx.y;
     const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
@@ -435,6 +429,16 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     const int wave = t >> 6, lane = t & 63, length = p->length;
     const float *kc = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
     const float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
+    // loaded before the norms: the output gate of output t, and at head_dim 64 the K row of this thread's
+    // first slot unless this kernel stores that row below (the new token's)
+    const float gate_t = t < G * HD ? b.gate[kh * G * HD + t] : 0.0f;
+    const bool k_early = HD == 64 && t < length && (PREPARED || slot_at(p, t) != p->slot);
+    float4 kpre[16];
+    if (k_early) {
+        const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, t)) * HD);
+#pragma unroll
+        for (int c = 0; c < 16; ++c) kpre[c] = k4[c];
+    }
     if (PREPARED) {  // eng_qk normalised and rotated q and stored K / V
         for (int i = t; i < G * HD; i += blockDim.x) qs[i] = b.q[kh * G * HD + i];
     } else {
@@ -464,7 +468,6 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     // partial sums per output then add up in subset order. When HD / 4 does not divide 256 the last
     // threads (r == R) take no slots and write no partials: R * G * HD <= 1024 G floats fit in qs.
     // The first kPre rows of each thread are loaded here, before the scores and the softmax.
-    constexpr int kMaxG = 8, kPre = 8;
     const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
     const bool sub = r < R;
     float4 vpre[kPre];
@@ -474,37 +477,88 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         vpre[k] = sub && s < length ? reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_at(p, s)) * HD)[c4]
                                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    for (int s = t; s < length; s += blockDim.x) {
-        const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, s)) * HD);
-        for (int g = 0; g < G; ++g) {
-            const float *q = qs + g * HD;
-            float dot = 0.0f;
-            for (int c = 0; c < HD / 4; ++c) {
-                const float4 k = k4[c];
-                dot += q[4 * c] * k.x;
-                dot += q[4 * c + 1] * k.y;
-                dot += q[4 * c + 2] * k.z;
-                dot += q[4 * c + 3] * k.w;
+    if (HD == 64) {
+        for (int s = t; s < length; s += blockDim.x) {
+            float4 k[16];
+            const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, s)) * HD);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) k[c] = s == t && k_early ? kpre[c] : k4[c];
+            for (int g = 0; g < G; ++g) {
+                const float *q = qs + g * HD;
+                float dot = 0.0f;
+#pragma unroll
+                for (int c = 0; c < 16; ++c) {
+                    dot += q[4 * c] * k[c].x;
+                    dot += q[4 * c + 1] * k[c].y;
+                    dot += q[4 * c + 2] * k[c].z;
+                    dot += q[4 * c + 3] * k[c].w;
+                }
+                sc[g * length + s] = dot * d.scale;
             }
-            sc[g * length + s] = dot * d.scale;
+        }
+    } else {
+        for (int s = t; s < length; s += blockDim.x) {
+            const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, s)) * HD);
+            for (int g = 0; g < G; ++g) {
+                const float *q = qs + g * HD;
+                float dot = 0.0f;
+                for (int c = 0; c < HD / 4; ++c) {
+                    const float4 k = k4[c];
+                    dot += q[4 * c] * k.x;
+                    dot += q[4 * c + 1] * k.y;
+                    dot += q[4 * c + 2] * k.z;
+                    dot += q[4 * c + 3] * k.w;
+                }
+                sc[g * length + s] = dot * d.scale;
+            }
         }
     }
     __syncthreads();
-    for (int g = 0; g < G; ++g) {
-        float mx = -INFINITY;
-        for (int s = t; s < length; s += blockDim.x) mx = fmaxf(mx, sc[g * length + s]);
-        mx = block_max(mx, red);
-        float den = 0.0f;
-        for (int s = t; s < length; s += blockDim.x) {
-            const float e = expf(sc[g * length + s] - mx);
-            sc[g * length + s] = e;
-            den += e;
+    // softmax of the G heads' rows together: block_max, then block_sum, in their
+    // orders (per thread over its slots, the wave's butterfly, the waves in order)
+    float mx[kMaxG], den[kMaxG];
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) {
+        mx[g] = -INFINITY;
+        if (g < G) {
+            for (int s = t; s < length; s += blockDim.x) mx[g] = fmaxf(mx[g], sc[g * length + s]);
+            mx[g] = wave_max(mx[g], lane);
         }
-        den = block_sum(den, red);
-        const float inv = 1.0f / den;
-        for (int s = t; s < length; s += blockDim.x) sc[g * length + s] *= inv;
-        __syncthreads();
     }
+    if (lane == 0)
+#pragma unroll
+        for (int g = 0; g < kMaxG; ++g)
+            if (g < G) red[g * kWaves + wave] = mx[g];
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) {
+        den[g] = 0.0f;
+        if (g < G) {
+            float m = red[g * kWaves];
+            for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[g * kWaves + w]);
+            for (int s = t; s < length; s += blockDim.x) {
+                const float e = expf(sc[g * length + s] - m);
+                sc[g * length + s] = e;
+                den[g] += e;
+            }
+            den[g] = wave_sum(den[g], lane);
+        }
+    }
+    __syncthreads();
+    if (lane == 0)
+#pragma unroll
+        for (int g = 0; g < kMaxG; ++g)
+            if (g < G) red[g * kWaves + wave] = den[g];
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g)
+        if (g < G) {
+            float sum = 0.0f;
+            for (int w = 0; w < kWaves; ++w) sum += red[g * kWaves + w];
+            const float inv = 1.0f / sum;
+            for (int s = t; s < length; s += blockDim.x) sc[g * length + s] *= inv;
+        }
+    __syncthreads();
     float4 acc[kMaxG];
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -535,7 +589,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         const float *wp = reinterpret_cast<const float *>(wpart);
         float a = 0.0f;
         for (int k = 0; k < R; ++k) a += wp[k * G * HD + o];
-        b.att[kh * G * HD + o] = a * sigmoidf_(b.gate[kh * G * HD + o]);
+        b.att[kh * G * HD + o] = a * sigmoidf_(o == t ? gate_t : b.gate[kh * G * HD + o]);
     }
 }
 
@@ -588,10 +642,13 @@ __global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, En
 // LDS.
 // With nxs (LDS, N * D floats, may alias mlp) the next layer's rms goes there
 // instead of to b.nx; x[0..N) ends as thread i's column of the new lanes.
+// after_loads() runs once the kernel's own loads are issued, before their
+// first use (loads it issues are waited for after them).
+template <int N, class F>
 __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l,
                                            int next_rms, const EngineDims &d, float *red, float *mlp, float *hr,
-                                           float *hpo, float *nxs, float (&x)[8]) {
-    const int D = d.D, N = d.N, i = threadIdx.x;
+                                           float *hpo, float *nxs, float (&x)[8], F &&after_loads) {
+    const int D = d.D, i = threadIdx.x;
     const bool own = i < D;
     // every load of the kernel, issued before the first wait
     float proj = 0.0f, gn = 0.0f, bx = 0.0f, u = 0.0f, gh = 0.0f, d1 = 0.0f, d3 = 0.0f;
@@ -603,14 +660,22 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
         gh = ld.pre_hada[i];
         d1 = ld.d1[i];
         d3 = ld.d3[i];
+#pragma unroll
         for (int n = 0; n < N; ++n) x[n] = b.x[n * D + i];
     }
-    const float ag = sigmoidf_(ld.attn_gate[0]);
+    const float d2 = i < d.hada ? ld.d2[i] : 0.0f;
+    float hraw = 0.0f, hpost = 0.0f;
+    const int lane = threadIdx.x & 63, ij = lane % (N * N);
     if (threadIdx.x < 64) {  // residual routing: wave 0
-        const int lane = threadIdx.x, ij = lane % (N * N);
-        const float a = sinkhorn_wave(b.hres[ij] * mh.a_res[l] + mh.b_res[l * N * N + ij], N, lane);
+        hraw = b.hres[ij];
+        if (lane < N) hpost = b.hpost[lane];
+    }
+    after_loads();
+    const float ag = sigmoidf_(ld.attn_gate[0]);
+    if (threadIdx.x < 64) {
+        const float a = sinkhorn_lanes<N>(hraw * mh.a_res[l] + mh.b_res[l * N * N + ij], lane);
         if (lane < N * N) hr[lane] = a;
-        if (lane < N) hpo[lane] = b.hpost[lane];
+        if (lane < N) hpo[lane] = hpost;
     }
     // proj = rms(proj) * (1 + post_norm); bx += sigmoid(attn_gate) * proj
     float r = 1.0f / sqrtf(block_sum(own ? proj * proj : 0.0f, red) / static_cast<float>(D) + 1e-6f);
@@ -624,7 +689,7 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
     __syncthreads();
     hadamard_block(mlp, d.hada, d.inv_hada);
     for (int k = threadIdx.x; k < d.hada; k += blockDim.x) {
-        const float a = mlp[k] * ld.d2[k];
+        const float a = mlp[k] * (k == i ? d2 : ld.d2[k]);
         mlp[k] = a * sigmoidf_(a);
     }
     __syncthreads();
@@ -634,11 +699,14 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
     if (own) {
         bx = bx + d3 * mlp[i] - u;
         float nx[8], sum = 0.0f;
+#pragma unroll
         for (int n = 0; n < N; ++n) {
             float val = hpo[n] * bx;
+#pragma unroll
             for (int j = 0; j < N; ++j) val += hr[n * N + j] * x[j];
             nx[n] = val;
         }
+#pragma unroll
         for (int n = 0; n < N; ++n) {
             b.x[n * D + i] = nx[n];
             sum += nx[n];
@@ -651,10 +719,12 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
         r = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(N * D) + 1e-6f);
         float *nx = nxs ? nxs : b.nx;
         if (own)
+#pragma unroll
             for (int n = 0; n < N; ++n) nx[n * D + i] = x[n] * r;
     }
 }
 
+template <int N>
 __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, int l,
                                                                int next_rms, EngineDims d) {
     const EngineBufs b = at_token(b0, d, blockIdx.y);
@@ -662,7 +732,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, La
     __shared__ float mlp[4096];
     __shared__ float hr[64], hpo[8];
     float x[8];
-    post_layer(b, ld, mh, l, next_rms, d, red, mlp, hr, hpo, nullptr, x);
+    post_layer<N>(b, ld, mh, l, next_rms, d, red, mlp, hr, hpo, nullptr, x, [] {});
 }
 
 // z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
@@ -735,30 +805,32 @@ __device__ __forceinline__ const float4 *mhc_row_ptr(const DenseRows &w, int r, 
 // lane keeps apart, and block_sum's tree over 64 threads and the sequential
 // sum of its four waves follow, so the outputs are the same bits as the
 // separate launches'. Needs D <= THREADS, N * D <= 4096.
-template <int THREADS>
+template <int THREADS, int N>
 __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, LayerDev ld, LayerDev ldn, MhcDev mh,
                                                                int l, DenseRows w, MixArgs m, EngineDims d) {
     constexpr int kWaves = THREADS / 64, kPF = 8;  // float4 columns per lane held for each prefetched row
-    constexpr int kRowsPF = (24 + kWaves - 1) / kWaves;  // rows per wave held (24: the mHC rows at N = 4)
+    constexpr int R = 2 * N + N * N;              // mHC projection rows
+    constexpr int kRowsPF = std::min((R + kWaves - 1) / kWaves, 3);  // rows per wave held in registers
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     __shared__ float red[kWaves];
     __shared__ float mlp[4096];  // the MLP vector, then the rms'd lanes
     __shared__ float hr[64], hpo[8], hp[16];
     __shared__ float zs[4096], ps[4096];
     __shared__ float proj[2 * 8 + 64];
-    const int N = d.N, D = d.D, R = 2 * N + N * N, cols = N * D, c4n = cols / 4;
+    const int D = d.D, cols = N * D, c4n = cols / 4;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = threadIdx.x;
     float4 pf[kRowsPF][kPF];
-#pragma unroll
-    for (int j = 0; j < kRowsPF; ++j) {
-        const int r = wave + j * kWaves;
-        const float4 *row = r < R ? mhc_row_ptr(w, r, N, cols) : nullptr;
-#pragma unroll
-        for (int k = 0; k < kPF; ++k)
-            pf[j][k] = row && lane + 64 * k < c4n ? row[lane + 64 * k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
     float x[8];
-    post_layer(b, ld, mh, l, 1, d, red, mlp, hr, hpo, mlp, x);
+    post_layer<N>(b, ld, mh, l, 1, d, red, mlp, hr, hpo, mlp, x, [&] {
+#pragma unroll
+        for (int j = 0; j < kRowsPF; ++j) {
+            const int r = wave + j * kWaves;
+            const float4 *row = r < R ? mhc_row_ptr(w, r, N, cols) : nullptr;
+#pragma unroll
+            for (int k = 0; k < kPF; ++k)
+                pf[j][k] = row && lane + 64 * k < c4n ? row[lane + 64 * k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    });
     __syncthreads();
     const float4 *nx4 = reinterpret_cast<const float4 *>(mlp);
     auto fma4 = [](float4 &acc, const float4 &a, const float4 &c) {
@@ -803,11 +875,12 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         if (lane == 0) proj[r] = sum;
     }
     __syncthreads();
-    mix_gates(b, mh, l + 1, proj, hp, d);
+    mix_gates<N>(b, mh, l + 1, proj, hp);
     __syncthreads();
     const bool own = i < D;
     float u = 0.0f;
     if (own) {
+#pragma unroll
         for (int n = 0; n < N; ++n) u += hp[n] * x[n];
         b.u[i] = u;
         b.bx[i] = u;
@@ -833,6 +906,17 @@ __global__ __launch_bounds__(256) void eng_dense_rows_kernel(const float *__rest
 }
 
 }  // namespace
+
+// f(std::integral_constant<int, N>) for the engine's lane count N (1, 2, 4 or 8).
+template <class F>
+void with_lanes(int n, F &&f) {
+    switch (n) {
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    default: f(std::integral_constant<int, 8>{}); break;
+    }
+}
 
 void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s) {
     hipLaunchKernelGGL(eng_start_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, z, b, d);
@@ -861,7 +945,10 @@ void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, i
     m.nsites = nsites;
     for (int i = 0; i < nsites; ++i) m.sites[i] = sites[i];
     for (int i = 0; i < 3; ++i) m.mhc_row[i] = mhc_row[i];
-    hipLaunchKernelGGL(eng_mix_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, m, d);
+    with_lanes(d.N, [&](auto n) {
+        hipLaunchKernelGGL(eng_mix_kernel<decltype(n)::value>, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, m,
+                           d);
+    });
     ND_HIP(hipGetLastError());
 }
 
@@ -902,8 +989,10 @@ void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, hipSt
 
 void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
                      const EngineDims &d, int tokens, hipStream_t s) {
-    hipLaunchKernelGGL(eng_post_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, l, next_rms ? 1 : 0,
-                       d);
+    with_lanes(d.N, [&](auto n) {
+        hipLaunchKernelGGL(eng_post_kernel<decltype(n)::value>, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, l,
+                           next_rms ? 1 : 0, d);
+    });
     ND_HIP(hipGetLastError());
 }
 
@@ -924,11 +1013,15 @@ void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev
     m.l = l + 1;
     m.nsites = nsites;
     for (int k = 0; k < nsites; ++k) m.sites[k] = sites[k];
-    if (d.D <= 512)
-        hipLaunchKernelGGL(eng_post_mix_kernel<512>, dim3(1, tokens), dim3(512), 0, s, b, ld, ldn, mh, l, a, m, d);
-    else
-        hipLaunchKernelGGL(eng_post_mix_kernel<kEngThreads>, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, ldn, mh,
-                           l, a, m, d);
+    with_lanes(d.N, [&](auto n) {
+        constexpr int N = decltype(n)::value;
+        if (d.D <= 512)
+            hipLaunchKernelGGL((eng_post_mix_kernel<512, N>), dim3(1, tokens), dim3(512), 0, s, b, ld, ldn, mh, l, a,
+                               m, d);
+        else
+            hipLaunchKernelGGL((eng_post_mix_kernel<kEngThreads, N>), dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld,
+                               ldn, mh, l, a, m, d);
+    });
     ND_HIP(hipGetLastError());
 }
 
