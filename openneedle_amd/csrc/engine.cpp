@@ -3,13 +3,16 @@
 // NativeEngine, needle2/native.py:307-663).
 //
 // One step (engine.cpp:968-1044) runs on the handle's stream as: embedding
-// row, then per layer the mHC projections, the mixing kernel, the fused
-// Q|K|V|gate GEMV, the q/k norms + RoPE + KV store kernel, attention, the
-// gate kernel, the out-projection GEMV and the post kernel (attention
-// residual, Hadamard MLP, Sinkhorn routing, lane mixing, next layer's rms);
-// then the final norm and the LM-head GEMV. The engram rows / projections /
-// conv of each site depend on the token history only: they run on a second
-// stream, which the step joins just before that site's mixing kernel. The
+// row, then per layer the mHC projections and the mixing kernel, the fused
+// Q|K|V|gate GEMV, attention (fp32 KV: norms, RoPE, K / V store, attention
+// and output gate in one launch; int8 KV: the norms + RoPE + store kernel,
+// attention and the gate kernel; either launch also runs the layer's
+// Sinkhorn routing in one more workgroup), the out-projection GEMV and the
+// post kernel (attention residual, Hadamard MLP, lane mixing, next layer's
+// rms), which for dense mHC matrices also runs the next layer's projections
+// and mixing; then the final norm and the LM-head GEMV. The engram rows /
+// projections / conv of each site depend on the token history only: they run
+// on a second stream, which the step joins just before that site's mixing. The
 // CQ matrices are the caller's handles (borrowed, as the reference borrows
 // its CQ pointers) and run through the library's bit-exact GEMV kernels with
 // the engine's own staging; dense tensors are copied to device memory at
@@ -472,7 +475,8 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     };
     const size_t ox = take(N * D), onx = take(N * D), ou = take(D), obx = take(D), oz = take(D), oq = take(A),
                  ok = take(K), ov = take(K), og = take(A), oa = take(A), op = take(D), oh = take(size_t(c.layers) * D),
-                 ohp = take(N), ohq = take(N), ohr = take(N * N), om0 = take(mhc_tiles), om1 = take(mhc_tiles),
+                 ohp = take(N), ohq = take(N), ohr = take(N * N), oht = take(N * N), om0 = take(mhc_tiles),
+                 om1 = take(mhc_tiles),
                  om2 = take(mhc_tiles), oe = take(D), oek = take(size_t(sites) * D), oev = take(size_t(sites) * D),
                  orv = take(D), ozf = take(D);
     const size_t oring = off;  // shared by the chunk
@@ -495,6 +499,7 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     b.hpre = w + ohp;
     b.hpost = w + ohq;
     b.hres = w + ohr;
+    b.hroute = w + oht;
     b.mhc_out[0] = w + om0;
     b.mhc_out[1] = w + om1;
     b.mhc_out[2] = w + om2;
@@ -1018,7 +1023,7 @@ void GpuEngine::run(int tokens) {
             // one token: norms, RoPE, store and attention in one kernel; a chunk
             // stores every token's K / V before any token attends
             if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
-            launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, s);
+            launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, mh, l, s);
             launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
         } else {
             launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
@@ -1052,7 +1057,7 @@ void GpuEngine::run(int tokens) {
                 a.shared_cache = 1;
             }
             launch_attention(a, G, s);
-            launch_eng_gate(b, dims, T, s);
+            launch_eng_gate(b, dims, T, mh, l, s);
         }
         oproj[l].run(s, T);
         if (fuse && l + 1 < c.layers) {
@@ -1061,7 +1066,7 @@ void GpuEngine::run(int tokens) {
             const int first[3] = {(l + 1) * mhc_rows[0], (l + 1) * mhc_rows[1], (l + 1) * mhc_rows[2]};
             launch_eng_post_mix(b, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, dims, T, s);
         } else {
-            launch_eng_post(b, layer[l], mh, l, l + 1 < c.layers, dims, T, s);
+            launch_eng_post(b, layer[l], l, l + 1 < c.layers, dims, T, s);
         }
         send_sites(l + 3);  // two layers ahead of their use
     }

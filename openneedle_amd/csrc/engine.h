@@ -53,11 +53,12 @@ struct MhcDev {
 
 // Work buffers (device), token 0's vectors; token t's are t per-token sizes
 // further (EngineDims): x, nx N*D; u, bx, z, proj, e, rawv, zf D; q, gate,
-// att A; k, v K; hidden layers*D; hpre, hpost N; hres N*N; mhc_out
+// att A; k, v K; hidden layers*D; hpre, hpost N; hres, hroute N*N; mhc_out
 // mhc_stride; ek, ev sites*D; slots capacity. The engram ring is shared.
 struct EngineBufs {
     float *x, *nx, *u, *bx, *z, *q, *k, *v, *gate, *att, *proj, *hidden;
     float *hpre, *hpost, *hres;     // mixed gates (N, N, N*N)
+    float *hroute;                  // Sinkhorn of the layer's residual routing logits (N*N)
     float *mhc_out[3];              // raw mHC projections of the layer (pre, post, res rows)
     float *e, *ek, *ev, *rawv;      // engram rows [D], keys [sites][D], values [sites][D], raw values [D]
     float *engring;                 // [sites][engring][D], row = position % engring
@@ -92,14 +93,15 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 // token) it also does that token's norms, RoPE and KV store, else eng_qk did
 // scores: null when G * max_length floats fit kEngScoreLds, else a device
 // buffer of tokens * kvheads * G * max_length floats
+// Both also run layer l's residual routing (Sinkhorn of hres into hroute) in one more workgroup per token.
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           hipStream_t s);
-void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s);
+                           const MhcDev &mh, int l, hipStream_t s);
+void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, const MhcDev &mh, int l, hipStream_t s);
 // K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
 void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
                           const EngineDims &d, hipStream_t s);
-void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
+void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_rms,
                      const EngineDims &d, int tokens, hipStream_t s);
 // The post of layer l, then layer l + 1's dense mHC projections (rows first[m] .. of the three
 // matrices w[m]) and mixing with the engram sites[0..nsites), in one launch; only where

@@ -1,9 +1,10 @@
 // Glue kernels of the single-sequence engine (needle2/csrc/engine.cpp:968-1044
 // for one token, 1045-1301 for a prompt chunk, and the helpers they call).
-// Every kernel runs one workgroup of kEngThreads threads per token
-// (blockIdx.y) over the model's small vectors (d_model, the mHC lanes, one
-// token's heads), in the reference's formulas and operation order per
-// element; block-wide sums and maxima are tree reductions, so results agree
+// The glue kernels run one workgroup per token (blockIdx.y; the attention
+// one per kv head, plus the routing workgroup) over the model's small
+// vectors (d_model, the mHC lanes, one token's heads), in the reference's
+// formulas and operation order per element; block-wide sums and maxima are
+// tree reductions, so results agree
 // with the reference to fp32 rounding rather than bit for bit. A token's
 // arithmetic does not depend on how many tokens share the launch.
 //   rms(x, gain)        y = x * (1 / sqrt(sum(x^2) / n + 1e-6)) * (1 + gain)   (engine.cpp:181-184)
@@ -45,6 +46,7 @@ __device__ __forceinline__ EngineBufs at_token(EngineBufs b, const EngineDims &d
     b.hpre += t * d.N;
     b.hpost += t * d.N;
     b.hres += t * d.N * d.N;
+    b.hroute += t * d.N * d.N;
     for (int m = 0; m < 3; ++m) b.mhc_out[m] += t * d.mhc_stride;
     b.ek += t * d.sites * d.D;
     b.ev += t * d.sites * d.D;
@@ -199,6 +201,24 @@ __device__ float sinkhorn_lanes(float a, int lane) {
         a *= 1.0f / lanes_sum<N, N, NN>(a, lane);
     }
     return a;
+}
+
+// Layer l's residual routing hroute = sinkhorn(hres * a_res[l] + b_res[l])
+// (engine.cpp:1034) by wave 0 of a workgroup of its own, which runs beside
+// the attention (or gate) workgroups of the launch and takes no part in their
+// barriers; the post kernel reads the result.
+__device__ void route_wave(const EngineBufs &b, const MhcDev &mh, int l, const EngineDims &d) {
+    if (threadIdx.x >= 64) return;
+    const int lane = threadIdx.x, N = d.N, ij = lane % (N * N);
+    const float a = b.hres[ij] * mh.a_res[l] + mh.b_res[l * N * N + ij];
+    float r;
+    switch (N) {
+    case 1: r = sinkhorn_lanes<1>(a, lane); break;
+    case 2: r = sinkhorn_lanes<2>(a, lane); break;
+    case 4: r = sinkhorn_lanes<4>(a, lane); break;
+    default: r = sinkhorn_lanes<8>(a, lane); break;
+    }
+    if (lane < N * N) b.hroute[lane] = r;
 }
 
 // x[n][d] = z[d] * sqrt(D) for every lane (engine.cpp:973-974), then nx = rms(x).
@@ -415,7 +435,12 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b0, Laye
 template <bool PREPARED, bool GLOBAL_SCORES>
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d,
-                                                             float *__restrict__ scores, int max_length) {
+                                                             float *__restrict__ scores, int max_length, MhcDev mh,
+                                                             int layer) {
+    if (blockIdx.x == d.KV) {  // the routing workgroup
+        route_wave(at_token(b0, d, blockIdx.y), mh, layer, d);
+        return;
+    }
     constexpr int kMaxG = 8, kPre = 8, kWaves = 4;
     extern __shared__ float sc_lds[];  // [G][length] when the scores fit
     __shared__ float qs[8 * 1024];  // query heads, then the partial outputs [R][G][HD] (1024 G floats)
@@ -627,16 +652,21 @@ __global__ __launch_bounds__(64) void eng_kv_import_kernel(const float *__restri
 }
 
 // att *= sigmoid(gate); then the activation quantiser (engine.cpp:1023-1024).
-__global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, EngineDims d) {
+__global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, EngineDims d, MhcDev mh, int l) {
     __shared__ float red[kEngThreads / 64];
     const EngineBufs b = at_token(b0, d, blockIdx.y);
+    if (blockIdx.x == 1) {  // the routing workgroup
+        route_wave(b, mh, l, d);
+        return;
+    }
     for (int i = threadIdx.x; i < d.A; i += blockDim.x) b.att[i] *= sigmoidf_(b.gate[i]);
     __syncthreads();
     quantize_block(b.att, d.A, d.abits, red);
 }
 
 // engine.cpp:1025-1039: attention residual, Hadamard MLP, mHC residual
-// routing (Sinkhorn) and lane mixing, the layer's hidden state; then the next
+// routing (hroute, whose Sinkhorn ran beside the attention) and lane mixing,
+// the layer's hidden state; then the next
 // layer's rms of x when `next_rms`. Thread i < D owns column i of every
 // vector (loaded once at the start); only the Hadamard transforms go through
 // LDS.
@@ -645,7 +675,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, En
 // after_loads() runs once the kernel's own loads are issued, before their
 // first use (loads it issues are waited for after them).
 template <int N, class F>
-__device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l,
+__device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &ld, int l,
                                            int next_rms, const EngineDims &d, float *red, float *mlp, float *hr,
                                            float *hpo, float *nxs, float (&x)[8], F &&after_loads) {
     const int D = d.D, i = threadIdx.x;
@@ -664,17 +694,16 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
         for (int n = 0; n < N; ++n) x[n] = b.x[n * D + i];
     }
     const float d2 = i < d.hada ? ld.d2[i] : 0.0f;
-    float hraw = 0.0f, hpost = 0.0f;
-    const int lane = threadIdx.x & 63, ij = lane % (N * N);
-    if (threadIdx.x < 64) {  // residual routing: wave 0
-        hraw = b.hres[ij];
+    float route = 0.0f, hpost = 0.0f;
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x < 64) {  // residual routing (computed beside the attention): wave 0
+        if (lane < N * N) route = b.hroute[lane];
         if (lane < N) hpost = b.hpost[lane];
     }
     after_loads();
     const float ag = sigmoidf_(ld.attn_gate[0]);
     if (threadIdx.x < 64) {
-        const float a = sinkhorn_lanes<N>(hraw * mh.a_res[l] + mh.b_res[l * N * N + ij], lane);
-        if (lane < N * N) hr[lane] = a;
+        if (lane < N * N) hr[lane] = route;
         if (lane < N) hpo[lane] = hpost;
     }
     // proj = rms(proj) * (1 + post_norm); bx += sigmoid(attn_gate) * proj
@@ -725,14 +754,14 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
 }
 
 template <int N>
-__global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, int l,
-                                                               int next_rms, EngineDims d) {
+__global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, LayerDev ld, int l, int next_rms,
+                                                               EngineDims d) {
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     __shared__ float red[kEngThreads / 64];
     __shared__ float mlp[4096];
     __shared__ float hr[64], hpo[8];
     float x[8];
-    post_layer<N>(b, ld, mh, l, next_rms, d, red, mlp, hr, hpo, nullptr, x, [] {});
+    post_layer<N>(b, ld, l, next_rms, d, red, mlp, hr, hpo, nullptr, x, [] {});
 }
 
 // z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
@@ -821,7 +850,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = threadIdx.x;
     float4 pf[kRowsPF][kPF];
     float x[8];
-    post_layer<N>(b, ld, mh, l, 1, d, red, mlp, hr, hpo, mlp, x, [&] {
+    post_layer<N>(b, ld, l, 1, d, red, mlp, hr, hpo, mlp, x, [&] {
 #pragma unroll
         for (int j = 0; j < kRowsPF; ++j) {
             const int r = wave + j * kWaves;
@@ -960,18 +989,22 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           hipStream_t s) {
+                           const MhcDev &mh, int l, hipStream_t s) {
     const size_t lds = scores ? 0 : static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);
     ND_CHECK(lds <= kEngScoreLds, "internal: fp32 attention scores exceed the LDS budget without a score buffer");
-    const dim3 grid(d.KV, tokens), block(256);
+    const dim3 grid(d.KV + 1, tokens), block(256);  // workgroup KV: the routing
     if (prepared && scores)
-        hipLaunchKernelGGL((eng_attn_fused_kernel<true, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length);
+        hipLaunchKernelGGL((eng_attn_fused_kernel<true, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length,
+                           mh, l);
     else if (prepared)
-        hipLaunchKernelGGL((eng_attn_fused_kernel<true, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0);
+        hipLaunchKernelGGL((eng_attn_fused_kernel<true, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0, mh,
+                           l);
     else if (scores)
-        hipLaunchKernelGGL((eng_attn_fused_kernel<false, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length);
+        hipLaunchKernelGGL((eng_attn_fused_kernel<false, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length,
+                           mh, l);
     else
-        hipLaunchKernelGGL((eng_attn_fused_kernel<false, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0);
+        hipLaunchKernelGGL((eng_attn_fused_kernel<false, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0, mh,
+                           l);
     ND_HIP(hipGetLastError());
 }
 
@@ -982,15 +1015,15 @@ void launch_eng_kv_import(const float *k, const float *v, const int *slots, int 
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s) {
-    hipLaunchKernelGGL(eng_gate_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, d);
+void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, const MhcDev &mh, int l, hipStream_t s) {
+    hipLaunchKernelGGL(eng_gate_kernel, dim3(2, tokens), dim3(kEngThreads), 0, s, b, d, mh, l);  // x = 1: the routing
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_post(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, bool next_rms,
+void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_rms,
                      const EngineDims &d, int tokens, hipStream_t s) {
     with_lanes(d.N, [&](auto n) {
-        hipLaunchKernelGGL(eng_post_kernel<decltype(n)::value>, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, l,
+        hipLaunchKernelGGL(eng_post_kernel<decltype(n)::value>, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, l,
                            next_rms ? 1 : 0, d);
     });
     ND_HIP(hipGetLastError());
