@@ -283,10 +283,20 @@ __global__ __launch_bounds__(kEngThreads) void eng_engram_ring_kernel(EngineBufs
 // positions past the prefix (cache_slot, engine.cpp:500, with a ring of the
 // window plus a prompt chunk so a chunk's stores never evict what its earlier
 // tokens read).
-__device__ __forceinline__ int slot_at(const StepParams *p, int s) {
-    const int pos = s < p->prefix_count ? s : p->start + s - p->prefix_count;
-    return !p->window ? pos : pos < p->prefix ? pos : p->prefix + (pos - p->prefix) % p->ring;
-}
+// SlotMap holds the token's list parameters in registers and computes a slot
+// without branches (the ring offset is computed and discarded where unused).
+struct SlotMap {
+    int prefix_count, start, window, prefix, ring;
+    __device__ explicit SlotMap(const StepParams *p)
+        : prefix_count(p->prefix_count), start(p->start), window(p->window), prefix(p->prefix),
+          ring(p->ring > 0 ? p->ring : 1) {}
+    __device__ int operator()(int s) const {
+        const int pos = s < prefix_count ? s : start + s - prefix_count;
+        const int wrapped = prefix + (pos - prefix) % ring;
+        return !window || pos < prefix ? pos : wrapped;
+    }
+};
+__device__ __forceinline__ int slot_at(const StepParams *p, int s) { return SlotMap(p)(s); }
 
 struct MixArgs {
     int l, nsites;
@@ -456,11 +466,14 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     const float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
     // loaded before the norms: the output gate of output t, and at head_dim 64 the K row of this thread's
     // first slot unless this kernel stores that row below (the new token's)
+    // (loads without branches: an entry past the list reads slot 0 and is not used)
+    const SlotMap slot_of(p);
     const float gate_t = t < G * HD ? b.gate[kh * G * HD + t] : 0.0f;
-    const bool k_early = HD == 64 && t < length && (PREPARED || slot_at(p, t) != p->slot);
+    const int slot_t = t < length ? slot_of(t) : 0;
+    const bool k_early = HD == 64 && t < length && (PREPARED || slot_t != p->slot);
     float4 kpre[16];
-    if (k_early) {
-        const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, t)) * HD);
+    if (HD == 64) {
+        const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_t) * HD);
 #pragma unroll
         for (int c = 0; c < 16; ++c) kpre[c] = k4[c];
     }
@@ -496,18 +509,27 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
     const bool sub = r < R;
     float4 vpre[kPre];
+    {  // buffer loads: an entry past the list reads zeros (offset past the resource)
+        const __amdgpu_buffer_rsrc_t vres = buffer_rsrc(vc, static_cast<uint32_t>(d.capacity) * HD * 4u);
 #pragma unroll
-    for (int k = 0; k < kPre; ++k) {
-        const int s = r + k * R;
-        vpre[k] = sub && s < length ? reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_at(p, s)) * HD)[c4]
-                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int k = 0; k < kPre; ++k) {
+            const int s = r + k * R;
+            const uint32_t off = sub && s < length ? (static_cast<uint32_t>(slot_of(s)) * HD + 4u * c4) * 4u
+                                                   : 0xFFFFFFF0u;
+            vpre[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0));
+        }
     }
     if (HD == 64) {
         for (int s = t; s < length; s += blockDim.x) {
             float4 k[16];
-            const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, s)) * HD);
+            if (s == t && k_early) {
 #pragma unroll
-            for (int c = 0; c < 16; ++c) k[c] = s == t && k_early ? kpre[c] : k4[c];
+                for (int c = 0; c < 16; ++c) k[c] = kpre[c];
+            } else {
+                const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_of(s)) * HD);
+#pragma unroll
+                for (int c = 0; c < 16; ++c) k[c] = k4[c];
+            }
             for (int g = 0; g < G; ++g) {
                 const float *q = qs + g * HD;
                 float dot = 0.0f;
@@ -523,7 +545,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         }
     } else {
         for (int s = t; s < length; s += blockDim.x) {
-            const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_at(p, s)) * HD);
+            const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_of(s)) * HD);
             for (int g = 0; g < G; ++g) {
                 const float *q = qs + g * HD;
                 float dot = 0.0f;
@@ -598,12 +620,24 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
                 acc[g].w += pr * v.w;
             }
     };
+    // the preloaded rows: an entry past the list adds 0 * 0 (its probability and its zero row)
 #pragma unroll
-    for (int k = 0; k < kPre; ++k)
-        if (sub && r + k * R < length) accumulate(r + k * R, vpre[k]);
+    for (int k = 0; k < kPre; ++k) {
+        const int s = r + k * R;
+        const bool use = sub && s < length;
+#pragma unroll
+        for (int g = 0; g < kMaxG; ++g)
+            if (g < G) {
+                const float pr = use ? sc[g * length + s] : 0.0f;
+                acc[g].x += pr * vpre[k].x;
+                acc[g].y += pr * vpre[k].y;
+                acc[g].z += pr * vpre[k].z;
+                acc[g].w += pr * vpre[k].w;
+            }
+    }
 #pragma unroll 8
     for (int s = sub ? r + kPre * R : length; s < length; s += R)
-        accumulate(s, reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_at(p, s)) * HD)[c4]);
+        accumulate(s, reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_of(s)) * HD)[c4]);
     float4 *wpart = reinterpret_cast<float4 *>(qs);  // [R][G][HD / 4]: R * G * HD = 1024 G floats
     __syncthreads();
 #pragma unroll
