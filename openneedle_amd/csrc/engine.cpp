@@ -207,9 +207,20 @@ struct SdotGroup {
         }
     }
 
-    void run(hipStream_t s, int tokens) {
+    // The buffers run() prepares for `tokens` tokens, for a kernel that prepares
+    // them itself (groups of 128 or 256 positions).
+    bool target(PrepTarget &pt, int tokens) const {
+        if ((m0->group != 128 && m0->group != 256) || (tokens >= 2 && !batched.p)) return false;
+        pt = PrepTarget{reinterpret_cast<int8_t *>(q.p), xs.p, tokens >= 2 ? xst.p : nullptr, m0->dev, m0->padded,
+                        m0->groups, m0->kind, m0->group, m0->scale};
+        return true;
+    }
+
+    // prepared: the input was prepared into target()'s buffers already
+    void run(hipStream_t s, int tokens, bool prepared = false) {
         const bool batch = tokens >= 2 && batched.p;
-        if (!launch_sdot_prepare(nullptr, xptr.p, batch ? tokens : 1, tokens, m0->in, m0->padded, m0->dev, m0->group,
+        if (!prepared &&
+            !launch_sdot_prepare(nullptr, xptr.p, batch ? tokens : 1, tokens, m0->in, m0->padded, m0->dev, m0->group,
                                  m0->scale, m0->kind, q.p, xs.p, batch ? xst.p : nullptr, s)) {
             ND_CHECK(!batch, "internal: batched int8 prepare refused the group");
             m0->transform(x, m0->in, rot.p, tokens, big, s);
@@ -270,9 +281,13 @@ struct Projection {
         pending.clear();
         pending8.clear();
     }
-    void run(hipStream_t s, int tokens) {
+    // A projection of one int8 group only: the target of the kernel that writes its input.
+    bool prep_target(PrepTarget &pt, int tokens) const {
+        return groups.empty() && dense.empty() && groups8.size() == 1 && groups8[0]->target(pt, tokens);
+    }
+    void run(hipStream_t s, int tokens, bool prepared = false) {
         for (auto &g : groups) g->run(s, tokens);
-        for (auto &g : groups8) g->run(s, tokens);
+        for (auto &g : groups8) g->run(s, tokens, prepared);
         for (auto &d : dense) launch_eng_dense(d.w, d.cols, d.first, d.rows, x, d.y, d.ystride, tokens, s);
     }
 };
@@ -1007,6 +1022,14 @@ void GpuEngine::run(int tokens) {
             }
         return ns;
     };
+    // int8 projections of one group of 128 or 256 positions take their input
+    // prepared by the kernel that writes it (the mixing / post kernel for
+    // Q|K|V|gate, the attention or gate kernel for the out-projection)
+    auto target = [&](const Projection &p, PrepTarget &pt) {
+        pt = PrepTarget{};
+        return p.prep_target(pt, T);
+    };
+    bool qkvg_prepared = false;  // layer l's Q|K|V|gate input was prepared by the kernel that wrote z
     for (int l = 0; l < c.layers; ++l) {
         if (l == 0 || !fuse) {
             mhc_proj[l].run(s, T);
@@ -1016,14 +1039,24 @@ void GpuEngine::run(int tokens) {
             }
             int sites[kEngMaxSites];
             const int ns = layer_sites(l, sites);
-            launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, T, s);
+            PrepTarget pt;
+            qkvg_prepared = target(qkvg[l], pt);
+            launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, T, pt, s);
         }
-        qkvg[l].run(s, T);
+        qkvg[l].run(s, T, qkvg_prepared);
+        PrepTarget ot;
+        bool o_prepared = target(oproj[l], ot);
         if (!int8_kv) {
             // one token: norms, RoPE, store and attention in one kernel; a chunk
-            // stores every token's K / V before any token attends
+            // stores every token's K / V before any token attends; the attention
+            // prepares the out-projection's input when a kv head's outputs are
+            // one group and no activation quantiser runs between
+            if (o_prepared && (abits || ot.group != G * HD || ot.dev != c.heads * HD)) {
+                o_prepared = false;
+                ot = PrepTarget{};
+            }
             if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
-            launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, mh, l, s);
+            launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, mh, l, ot, s);
             launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
         } else {
             launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
@@ -1057,14 +1090,16 @@ void GpuEngine::run(int tokens) {
                 a.shared_cache = 1;
             }
             launch_attention(a, G, s);
-            launch_eng_gate(b, dims, T, mh, l, s);
+            launch_eng_gate(b, dims, T, mh, l, ot, s);
         }
-        oproj[l].run(s, T);
+        oproj[l].run(s, T, o_prepared);
         if (fuse && l + 1 < c.layers) {
             int sites[kEngMaxSites];
             const int ns = layer_sites(l + 1, sites);
             const int first[3] = {(l + 1) * mhc_rows[0], (l + 1) * mhc_rows[1], (l + 1) * mhc_rows[2]};
-            launch_eng_post_mix(b, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, dims, T, s);
+            PrepTarget pt;
+            qkvg_prepared = target(qkvg[l + 1], pt);
+            launch_eng_post_mix(b, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, dims, T, pt, s);
         } else {
             launch_eng_post(b, layer[l], l, l + 1 < c.layers, dims, T, s);
         }

@@ -74,6 +74,19 @@ struct KvLayer {
     float *ks, *vs;
 };
 
+// The int8 path's prepared input of the projection that reads a kernel's
+// output (the q / xs / xst buffers its prepare launch would fill, see
+// launch_sdot_prepare): a kernel given a target with q set prepares token t's
+// row itself, one wave per group of 128 or 256 positions, in the same
+// arithmetic. xst is null for one token, else [groups][tokens].
+struct PrepTarget {
+    int8_t *q;   // [tokens][dev] permuted codes (null: nothing to prepare)
+    float *xs;   // [tokens][groups]
+    float *xst;
+    int dev, padded, groups, kind, group;
+    float scale;
+};
+
 // Every launcher runs `tokens` tokens (blockIdx.y), with p the device array of their StepParams.
 void launch_eng_start(const float *z, const EngineBufs &b, const EngineDims &d, int tokens, hipStream_t s);
 void launch_eng_engram_in(const EngineBufs &b, const StepParams *p, int site, const EngineDims &d, int tokens,
@@ -84,8 +97,10 @@ void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepPar
                            const EngineDims &d, int tokens, hipStream_t s);
 // mixing, engram gates and the attention input of layer l; mhc_row[m] is the
 // first row of the layer inside b.mhc_out[m]; sites: engram sites at this layer
+// (pt: the Q|K|V|gate projection's int8 input, prepared from z)
 void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
-                    const int *sites, int nsites, const EngineDims &d, int tokens, hipStream_t s);
+                    const int *sites, int nsites, const EngineDims &d, int tokens, const PrepTarget &pt,
+                    hipStream_t s);
 // q / k norms, RoPE, the K / V store and (int8 KV) the slot lists of every token
 void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                    const EngineDims &d, int tokens, hipStream_t s);
@@ -93,11 +108,14 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 // token) it also does that token's norms, RoPE and KV store, else eng_qk did
 // scores: null when G * max_length floats fit kEngScoreLds, else a device
 // buffer of tokens * kvheads * G * max_length floats
-// Both also run layer l's residual routing (Sinkhorn of hres into hroute) in one more workgroup per token.
+// Both also run layer l's residual routing (Sinkhorn of hres into hroute) in one more workgroup per token,
+// and prepare the out-projection's int8 input from att when pt.q is set (the attention only for a group of
+// one kv head's outputs, heads / kvheads * head_dim positions).
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           const MhcDev &mh, int l, hipStream_t s);
-void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, const MhcDev &mh, int l, hipStream_t s);
+                           const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s);
+void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, const MhcDev &mh, int l,
+                     const PrepTarget &pt, hipStream_t s);
 // K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
 void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
                           const EngineDims &d, hipStream_t s);
@@ -109,7 +127,7 @@ void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_r
 bool eng_post_mix_fits(const EngineDims &d);
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
-                         int tokens, hipStream_t s);
+                         int tokens, const PrepTarget &pt, hipStream_t s);
 void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, int tokens, hipStream_t s);
 // x[t][0..n) for t < tokens, rows `stride` apart
 void launch_eng_quantize(float *x, int n, int stride, int bits, int tokens, hipStream_t s);

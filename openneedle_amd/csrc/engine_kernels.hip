@@ -13,6 +13,7 @@
 //   hadamard(v, n)      butterflies h = 1, 2, .., n/2 of (a + b, a - b), then * 1/sqrt(n)   (cq.cpp:30-46)
 //   sinkhorn(a, n)      20 row / column normalisations after exp(a - max)     (engine.cpp:151-180)
 #include "engine.h"
+#include "sdot_prepare.h"
 #include "wave.h"
 
 #include <algorithm>
@@ -221,6 +222,39 @@ __device__ void route_wave(const EngineBufs &b, const MhcDev &mh, int l, const E
     if (lane < N * N) b.hroute[lane] = r;
 }
 
+// Token tok's int8 input of the target's projection from the vector in v
+// (position p at v[p - v0]; positions at or past n read as zero): groups
+// [g0, g1), one wave per group (prepare_group_wave), waves from w0 on.
+__device__ void prepare_groups(const PrepTarget &pt, const float *v, int v0, int n, int g0, int g1, int w0, int tok,
+                               int tokens) {
+    const int lane = threadIdx.x & 63, wave = static_cast<int>(threadIdx.x >> 6) - w0;
+    const int waves = static_cast<int>(blockDim.x >> 6) - w0;
+    if (wave < 0) return;
+    int8_t *qv = pt.q + static_cast<size_t>(tok) * pt.dev;
+    for (int g = g0 + wave; g < g1; g += waves) {
+        const int base = g * pt.group;
+        float *xs = pt.xs + static_cast<size_t>(tok) * pt.groups + g;  // stored only for a group before padded
+        float *xst = pt.xst ? pt.xst + static_cast<size_t>(g) * tokens + tok : nullptr;
+        if (pt.group == 128) {
+            float r[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int pos = base + lane + 64 * k;
+                r[k] = pos < n ? v[pos - v0] : 0.0f;
+            }
+            prepare_group_wave<128>(r, lane, base, pt.padded, pt.dev, pt.scale, pt.kind, qv, xs, xst);
+        } else {
+            float r[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int pos = base + lane + 64 * k;
+                r[k] = pos < n ? v[pos - v0] : 0.0f;
+            }
+            prepare_group_wave<256>(r, lane, base, pt.padded, pt.dev, pt.scale, pt.kind, qv, xs, xst);
+        }
+    }
+}
+
 // x[n][d] = z[d] * sqrt(D) for every lane (engine.cpp:973-974), then nx = rms(x).
 __global__ __launch_bounds__(kEngThreads) void eng_start_kernel(const float *__restrict__ z, EngineBufs b0,
                                                                 EngineDims d) {
@@ -342,7 +376,7 @@ __device__ void mix_sites(const EngineBufs &b, const MixArgs &m, const EngineDim
 // residual u = bx, engram gates, then z = quant(rms(bx) * (1 + norm_in)).
 template <int N>
 __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, LayerDev ld, MhcDev mh, MixArgs m,
-                                                              EngineDims d) {
+                                                              EngineDims d, PrepTarget pt) {
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     __shared__ float red[kEngThreads / 64];
     __shared__ float hp[16];
@@ -368,6 +402,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, Lay
     mix_sites(b, m, d, red, zs, ps);
     rms_block(b.bx, b.z, D, ld.norm_in, red);
     quantize_block(b.z, D, d.abits, red);
+    if (pt.q) prepare_groups(pt, b.z, 0, D, 0, pt.dev / pt.group, 0, blockIdx.y, gridDim.y);
 }
 
 // engine.cpp:994-1021: per-head rms of q and k, RoPE (first half paired with
@@ -446,7 +481,7 @@ template <bool PREPARED, bool GLOBAL_SCORES>
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d,
                                                              float *__restrict__ scores, int max_length, MhcDev mh,
-                                                             int layer) {
+                                                             int layer, PrepTarget pt) {
     if (blockIdx.x == d.KV) {  // the routing workgroup
         route_wave(at_token(b0, d, blockIdx.y), mh, layer, d);
         return;
@@ -644,11 +679,21 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     for (int g = 0; g < kMaxG; ++g)
         if (sub && g < G) wpart[(r * G + g) * cols4 + c4] = acc[g];
     __syncthreads();
+    float out_t = 0.0f;  // output t (with a target, G * HD <= 256: one output per thread)
     for (int o = t; o < G * HD; o += blockDim.x) {
         const float *wp = reinterpret_cast<const float *>(wpart);
         float a = 0.0f;
         for (int k = 0; k < R; ++k) a += wp[k * G * HD + o];
-        b.att[kh * G * HD + o] = a * sigmoidf_(o == t ? gate_t : b.gate[kh * G * HD + o]);
+        const float val = a * sigmoidf_(o == t ? gate_t : b.gate[kh * G * HD + o]);
+        b.att[kh * G * HD + o] = val;
+        if (o == t) out_t = val;
+    }
+    if (pt.q) {  // this kv head's outputs are one group of the out-projection's int8 input
+        float *stage = qs;
+        __syncthreads();  // every partial read
+        if (t < G * HD) stage[t] = out_t;
+        __syncthreads();
+        prepare_groups(pt, stage, kh * G * HD, d.H * HD, kh, kh + 1, 0, blockIdx.y, gridDim.y);
     }
 }
 
@@ -686,7 +731,8 @@ __global__ __launch_bounds__(64) void eng_kv_import_kernel(const float *__restri
 }
 
 // att *= sigmoid(gate); then the activation quantiser (engine.cpp:1023-1024).
-__global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, EngineDims d, MhcDev mh, int l) {
+__global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, EngineDims d, MhcDev mh, int l,
+                                                               PrepTarget pt) {
     __shared__ float red[kEngThreads / 64];
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     if (blockIdx.x == 1) {  // the routing workgroup
@@ -696,6 +742,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, En
     for (int i = threadIdx.x; i < d.A; i += blockDim.x) b.att[i] *= sigmoidf_(b.gate[i]);
     __syncthreads();
     quantize_block(b.att, d.A, d.abits, red);
+    if (pt.q) prepare_groups(pt, b.att, 0, d.A, 0, pt.dev / pt.group, 0, blockIdx.y, gridDim.y);
 }
 
 // engine.cpp:1025-1039: attention residual, Hadamard MLP, mHC residual
@@ -870,7 +917,8 @@ __device__ __forceinline__ const float4 *mhc_row_ptr(const DenseRows &w, int r, 
 // separate launches'. Needs D <= THREADS, N * D <= 4096.
 template <int THREADS, int N>
 __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, LayerDev ld, LayerDev ldn, MhcDev mh,
-                                                               int l, DenseRows w, MixArgs m, EngineDims d) {
+                                                               int l, DenseRows w, MixArgs m, EngineDims d,
+                                                               PrepTarget pt) {
     constexpr int kWaves = THREADS / 64, kPF = 8;  // float4 columns per lane held for each prefetched row
     constexpr int R = 2 * N + N * N;              // mHC projection rows
     constexpr int kRowsPF = std::min((R + kWaves - 1) / kWaves, 3);  // rows per wave held in registers
@@ -948,16 +996,22 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         b.u[i] = u;
         b.bx[i] = u;
     }
+    float z = 0.0f;  // this thread's z after the quantiser (own threads)
     if (m.nsites) {
         __syncthreads();
         mix_sites(b, m, d, red, zs, ps);
         rms_block(b.bx, b.z, D, ldn.norm_in, red);
     } else {  // rms_block's arithmetic on the registers
         const float r = 1.0f / sqrtf(block_sum(own ? u * u : 0.0f, red) / static_cast<float>(D) + 1e-6f);
-        if (own) b.z[i] = u * r * (1.0f + ldn.norm_in[i]);
+        if (own) b.z[i] = z = u * r * (1.0f + ldn.norm_in[i]);
         __syncthreads();
     }
     quantize_block(b.z, D, d.abits, red);
+    if (pt.q) {  // the next Q|K|V|gate projection's int8 input, from z staged in LDS
+        if (own) zs[i] = m.nsites || d.abits ? b.z[i] : z;
+        __syncthreads();
+        prepare_groups(pt, zs, 0, D, 0, pt.dev / pt.group, 0, blockIdx.y, gridDim.y);
+    }
 }
 
 __global__ __launch_bounds__(256) void eng_dense_rows_kernel(const float *__restrict__ w, int cols,
@@ -1002,7 +1056,8 @@ void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepPar
 }
 
 void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
-                    const int *sites, int nsites, const EngineDims &d, int tokens, hipStream_t s) {
+                    const int *sites, int nsites, const EngineDims &d, int tokens, const PrepTarget &pt,
+                    hipStream_t s) {
     MixArgs m{};
     m.l = l;
     m.nsites = nsites;
@@ -1010,7 +1065,7 @@ void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, i
     for (int i = 0; i < 3; ++i) m.mhc_row[i] = mhc_row[i];
     with_lanes(d.N, [&](auto n) {
         hipLaunchKernelGGL(eng_mix_kernel<decltype(n)::value>, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, mh, m,
-                           d);
+                           d, pt);
     });
     ND_HIP(hipGetLastError());
 }
@@ -1023,22 +1078,24 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           const MhcDev &mh, int l, hipStream_t s) {
+                           const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s) {
+    ND_CHECK(!pt.q || (pt.group == d.H / d.KV * d.HD && pt.group <= 256 && pt.dev == d.A),
+             "internal: attention prepares one kv head's outputs as one group");
     const size_t lds = scores ? 0 : static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);
     ND_CHECK(lds <= kEngScoreLds, "internal: fp32 attention scores exceed the LDS budget without a score buffer");
     const dim3 grid(d.KV + 1, tokens), block(256);  // workgroup KV: the routing
     if (prepared && scores)
         hipLaunchKernelGGL((eng_attn_fused_kernel<true, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length,
-                           mh, l);
+                           mh, l, pt);
     else if (prepared)
         hipLaunchKernelGGL((eng_attn_fused_kernel<true, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0, mh,
-                           l);
+                           l, pt);
     else if (scores)
         hipLaunchKernelGGL((eng_attn_fused_kernel<false, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length,
-                           mh, l);
+                           mh, l, pt);
     else
         hipLaunchKernelGGL((eng_attn_fused_kernel<false, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0, mh,
-                           l);
+                           l, pt);
     ND_HIP(hipGetLastError());
 }
 
@@ -1049,8 +1106,9 @@ void launch_eng_kv_import(const float *k, const float *v, const int *slots, int 
     ND_HIP(hipGetLastError());
 }
 
-void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, const MhcDev &mh, int l, hipStream_t s) {
-    hipLaunchKernelGGL(eng_gate_kernel, dim3(2, tokens), dim3(kEngThreads), 0, s, b, d, mh, l);  // x = 1: the routing
+void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, const MhcDev &mh, int l,
+                     const PrepTarget &pt, hipStream_t s) {
+    hipLaunchKernelGGL(eng_gate_kernel, dim3(2, tokens), dim3(kEngThreads), 0, s, b, d, mh, l, pt);  // x = 1: the routing
     ND_HIP(hipGetLastError());
 }
 
@@ -1069,7 +1127,7 @@ bool eng_post_mix_fits(const EngineDims &d) {
 
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
-                         int tokens, hipStream_t s) {
+                         int tokens, const PrepTarget &pt, hipStream_t s) {
     ND_CHECK(eng_post_mix_fits(d), "internal: fused post / mixing launch outside its geometry");
     DenseRows a{};
     for (int k = 0; k < 3; ++k) {
@@ -1084,10 +1142,10 @@ void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev
         constexpr int N = decltype(n)::value;
         if (d.D <= 512)
             hipLaunchKernelGGL((eng_post_mix_kernel<512, N>), dim3(1, tokens), dim3(512), 0, s, b, ld, ldn, mh, l, a,
-                               m, d);
+                               m, d, pt);
         else
             hipLaunchKernelGGL((eng_post_mix_kernel<kEngThreads, N>), dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld,
-                               ldn, mh, l, a, m, d);
+                               ldn, mh, l, a, m, d, pt);
     });
     ND_HIP(hipGetLastError());
 }

@@ -15,6 +15,7 @@
 //   value += (float(dot) * (half(norm) * cs)) * x_scale[g]
 // sequentially over g (sdot.cpp:43-44, 142-149), so outputs are bit-exact.
 #include "common.h"
+#include "sdot_prepare.h"
 #include "wave.h"
 
 #include <hip/hip_fp16.h>
@@ -28,16 +29,6 @@ namespace nd {
 namespace {
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
-
-// position p within a row -> byte index in the permuted int8 activation row
-__device__ __forceinline__ int permuted_index(int kind, int p) {
-    if (kind == kNib) {
-        int d = p >> 3, i = p & 7;  // codes 0,2,4,6 then 1,3,5,7 of each 8-code dword
-        return (d << 3) | ((i & 1) << 2) | (i >> 1);
-    }
-    int d = p >> 4, i = p & 15;  // selector m = i&3 holds crumbs m, m+4, m+8, m+12
-    return (d << 4) | ((i & 3) << 2) | (i >> 2);
-}
 
 // One block per (segment of positions, vector). seg = max(256, group).
 __global__ __launch_bounds__(256) void sdot_quantize_kernel(const float *__restrict__ rot, int rot_stride, int padded,
@@ -1496,12 +1487,7 @@ __global__ __launch_bounds__(256) void sdot_prepare_wave_kernel(const float *__r
 }
 
 // Prepare for groups of 128 and 256 positions, one wave per group without
-// LDS: lane t holds positions t + 64 k (k < GROUP / 64) of its wave's group;
-// the FWHT stages 1 .. 32 run as in-wave butterflies on every k, then the
-// stages 64 and 128 between a lane's own values, in the reference's stage
-// order and with its operands (x + y, x - y); then the absmax over the wave
-// and the reference's quantiser as in sdot_prepare_wave_kernel. Same values
-// as sdot_prepare_kernel, bit for bit.
+// LDS (prepare_group_wave). Same values as sdot_prepare_kernel, bit for bit.
 template <int GROUP>
 __global__ __launch_bounds__(256) void sdot_prepare_wave_group_kernel(const float *__restrict__ x0,
                                                                       const float *const *__restrict__ xptr, int batch,
@@ -1520,42 +1506,11 @@ __global__ __launch_bounds__(256) void sdot_prepare_wave_group_kernel(const floa
     for (int k = 0; k < VPL; ++k) {
         const int p = base + t + 64 * k;
         r[k] = p < in ? xv[p] : 0.0f;
-        wave_butterflies<64, 1>(r[k], t);
     }
-#pragma unroll
-    for (int h = 1; h < VPL; h *= 2)  // stages 64 h
-#pragma unroll
-        for (int k = 0; k < VPL; ++k)
-            if (!(k & h)) {
-                const float a = r[k], b = r[k + h];
-                r[k] = a + b;
-                r[k + h] = a - b;
-            }
-    float m = 0.0f;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-        r[k] = r[k] * scale;
-        m = fmaxf(m, fabsf(r[k]));
-    }
-    const float absmax = wave_max(m, t);
-    const bool live = base < padded;  // a whole group of the padded length
-    float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
-    if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
-    if (live && t == 0) {
-        xs[static_cast<size_t>(v) * groups + base / GROUP] = sc;
-        if (xst) xst[(static_cast<size_t>(v / batch) * groups + base / GROUP) * batch + v % batch] = sc;
-    }
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-        const int p = base + t + 64 * k;
-        int8_t out = 0;
-        if (live) {
-            float val = rintf(r[k] / sc);
-            val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
-            out = static_cast<int8_t>(val);
-        }
-        if (p < dev) q[static_cast<size_t>(v) * dev + permuted_index(kind, p)] = out;
-    }
+    prepare_group_wave<GROUP>(r, t, base, padded, dev, scale, kind, q + static_cast<size_t>(v) * dev,
+                              xs + static_cast<size_t>(v) * groups + base / GROUP,
+                              xst ? xst + (static_cast<size_t>(v / batch) * groups + base / GROUP) * batch + v % batch
+                                  : nullptr);
 }
 
 }  // namespace
