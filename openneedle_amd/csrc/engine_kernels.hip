@@ -150,6 +150,42 @@ __device__ void hadamard_block(float *v, int n, float inv) {
     __syncthreads();
 }
 
+// The same transform for n = 64 K values with thread i holding value i
+// (blockDim = 64 K): stages 1 .. 32 between the lanes of each wave, then
+// every thread gathers its column i % 64 + 64 k (k < K) from buf and runs the
+// stages 64 .. 32 K on its own copy, keeping entry i / 64: hadamard_block's
+// stage order and operands with one barrier (no earlier read of buf may be
+// pending). Returns value i.
+template <int K>
+__device__ __forceinline__ float hadamard_thread(float x, float *buf, float inv) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    x = fwht_stage<1>(x, lane);
+    x = fwht_stage<2>(x, lane);
+    x = fwht_stage<4>(x, lane);
+    x = fwht_stage<8>(x, lane);
+    x = fwht_stage<16>(x, lane);
+    x = fwht_stage<32>(x, lane);
+    buf[threadIdx.x] = x;
+    __syncthreads();
+    float c[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) c[k] = buf[lane + 64 * k];
+#pragma unroll
+    for (int h = 1; h < K; h <<= 1)
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (!(k & h)) {
+                const float a = c[k], b = c[k + h];
+                c[k] = a + b;
+                c[k + h] = a - b;
+            }
+    float out = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+        if (k == w) out = c[k];
+    return out * inv;
+}
+
 // engine.cpp:151-180 for an N x N matrix (N <= 8) held by one wave, lane
 // l = N i + j holding a[i][j] (lanes past N * N hold copies of lane 0's group
 // and never mix into it): row sums over lanes that differ in the low log2(N)
@@ -755,7 +791,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, En
 // instead of to b.nx; x[0..N) ends as thread i's column of the new lanes.
 // after_loads() runs once the kernel's own loads are issued, before their
 // first use (loads it issues are waited for after them).
-template <int N, class F>
+template <int N, int WAVES, class F>
 __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &ld, int l,
                                            int next_rms, const EngineDims &d, float *red, float *mlp, float *hr,
                                            float *hpo, float *nxs, float (&x)[8], F &&after_loads) {
@@ -794,20 +830,27 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
     // z = rms(bx) * (1 + pre_hada); mlp = hadamard(silu_diag(hadamard(z * d1 | 0), d2)) (engine.cpp:1029-1033)
     r = 1.0f / sqrtf(block_sum(own ? bx * bx : 0.0f, red) / static_cast<float>(D) + 1e-6f);
     const float z = bx * r * (1.0f + gh);
-    if (i < d.hada) mlp[i] = own ? z * d1 : 0.0f;  // columns past D are zero padding (D <= threads)
-    for (int k = i + blockDim.x; k < d.hada; k += blockDim.x) mlp[k] = 0.0f;
-    __syncthreads();
-    hadamard_block(mlp, d.hada, d.inv_hada);
-    for (int k = threadIdx.x; k < d.hada; k += blockDim.x) {
-        const float a = mlp[k] * (k == i ? d2 : ld.d2[k]);
-        mlp[k] = a * sigmoidf_(a);
+    float mv;  // value i of the MLP vector (own threads)
+    if (d.hada == 64 * WAVES) {  // one value per thread: the transforms in registers, mlp as staging
+        const float a = hadamard_thread<WAVES>(own ? z * d1 : 0.0f, mlp, d.inv_hada) * d2;
+        mv = hadamard_thread<WAVES>(a * sigmoidf_(a), mlp + d.hada, d.inv_hada);
+    } else {
+        if (i < d.hada) mlp[i] = own ? z * d1 : 0.0f;  // columns past D are zero padding (D <= threads)
+        for (int k = i + blockDim.x; k < d.hada; k += blockDim.x) mlp[k] = 0.0f;
+        __syncthreads();
+        hadamard_block(mlp, d.hada, d.inv_hada);
+        for (int k = threadIdx.x; k < d.hada; k += blockDim.x) {
+            const float a = mlp[k] * (k == i ? d2 : ld.d2[k]);
+            mlp[k] = a * sigmoidf_(a);
+        }
+        __syncthreads();
+        hadamard_block(mlp, d.hada, d.inv_hada);
+        mv = own ? mlp[i] : 0.0f;
     }
-    __syncthreads();
-    hadamard_block(mlp, d.hada, d.inv_hada);
     // bx = bx + d3 * mlp - u; x[n] = hpost[n] bx + sum_j hres[n][j] x[j]; hidden = mean over lanes
     float ss = 0.0f;
     if (own) {
-        bx = bx + d3 * mlp[i] - u;
+        bx = bx + d3 * mv - u;
         float nx[8], sum = 0.0f;
 #pragma unroll
         for (int n = 0; n < N; ++n) {
@@ -842,7 +885,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, La
     __shared__ float mlp[4096];
     __shared__ float hr[64], hpo[8];
     float x[8];
-    post_layer<N>(b, ld, l, next_rms, d, red, mlp, hr, hpo, nullptr, x, [] {});
+    post_layer<N, kEngThreads / 64>(b, ld, l, next_rms, d, red, mlp, hr, hpo, nullptr, x, [] {});
 }
 
 // z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
@@ -932,7 +975,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = threadIdx.x;
     float4 pf[kRowsPF][kPF];
     float x[8];
-    post_layer<N>(b, ld, l, 1, d, red, mlp, hr, hpo, mlp, x, [&] {
+    post_layer<N, kWaves>(b, ld, l, 1, d, red, mlp, hr, hpo, mlp, x, [&] {
 #pragma unroll
         for (int j = 0; j < kRowsPF; ++j) {
             const int r = wave + j * kWaves;
@@ -964,6 +1007,9 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         total += __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
         return total;
     };
+    float4 nxr[kPF];  // the lane's first columns of the rms'd lanes, for every row
+#pragma unroll
+    for (int k = 0; k < kPF; ++k) nxr[k] = lane + 64 * k < c4n ? nx4[lane + 64 * k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
     for (int j = 0; j < kRowsPF; ++j) {
         const int r = wave + j * kWaves;  // uniform over the wave
@@ -971,7 +1017,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
             float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
             for (int k = 0; k < kPF; ++k)
-                if (lane + 64 * k < c4n) fma4(acc, pf[j][k], nx4[lane + 64 * k]);
+                if (lane + 64 * k < c4n) fma4(acc, pf[j][k], nxr[k]);
             const float4 *row = mhc_row_ptr(w, r, N, cols);
             for (int c = lane + 64 * kPF; c < c4n; c += 64) fma4(acc, row[c], nx4[c]);
             const float sum = row_sum(acc);
