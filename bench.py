@@ -49,17 +49,38 @@ def measured_traffic(kernel):
 
 
 def gpu_name(reported: str) -> str:
-    """The runtime's device name, or (when the runtime reports none) the GPU agent's marketing name from
-    rocminfo, run as a child process."""
+    """The runtime's device name; when the runtime reports none, the GPU agent's marketing name from rocminfo;
+    when that is empty too, rocm-smi's GFX version and PCI device id ("gfx950 (PCI device 0x75a3)"). The
+    tools run as child processes."""
     if reported:
         return reported
     try:
         out = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=30).stdout
-        names = [l.split(":", 1)[1].strip() for l in out.splitlines() if l.strip().startswith("Marketing Name:")]
-        gpus = [n for n in names if "Instinct" in n or "MI" in n]
-        return (gpus or names or [""])[-1]
+        agent, names = None, []
+        for line in out.splitlines():
+            key, _, val = line.strip().partition(":")
+            if key == "Name" and agent is None:
+                agent = val.strip()
+            elif key == "Marketing Name" and agent is not None:
+                if agent.startswith("gfx") and val.strip():
+                    names.append(val.strip())
+                agent = None
+        if names:
+            return names[-1]
     except (OSError, ValueError, subprocess.SubprocessError):
-        return ""
+        pass
+    try:
+        out = subprocess.run(["rocm-smi", "--showproductname"], capture_output=True, text=True, timeout=30).stdout
+        info = {}
+        for line in out.splitlines():
+            parts = [x.strip() for x in line.split(":")]
+            if len(parts) >= 3 and parts[1] in ("Card Model", "GFX Version"):
+                info[parts[1]] = parts[2]
+        if info:
+            return f"{info.get('GFX Version', 'GPU')} (PCI device {info.get('Card Model', '?')})"
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    return ""
 
 
 def cpu_model() -> str:
