@@ -305,6 +305,9 @@ SdotGeom sdot_geom_of(const Matrix &m) {
     g.groups = m.groups;
     g.windows = m.windows;
     g.chunks = m.chunks;
+    g.in = m.in;
+    g.padded = m.padded;
+    g.scale = m.scale;
     g.centroid_scale = maximum > 0 ? maximum / 127 : 1;
     uint8_t cent[16] = {};
     for (int i = 0; i < n; ++i) {
@@ -340,6 +343,13 @@ void SdotHandle::prepare_device(const float *d_x, int batch, int32_t *q, float *
 
 void SdotHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s) {
     if (batch <= 0) return;
+    const SdotGeom g = geom();
+    if (sdot_gemv_takes_x(g, m.n_pad / kRowsPerBlock, batch)) {  // the GEMV prepares its input row itself
+        SdotJob job{m.codes.p, m.norms.p, nullptr, nullptr, d_y, m.out, m.n_pad, 0, 1, nullptr};
+        job.x = d_x;
+        launch_sdot_gemv_x(g, job, nullptr, 0, m.n_pad / kRowsPerBlock, s);
+        return;
+    }
     st.q.reserve(size_t(batch) * m.dev / 4);
     st.xs.reserve(size_t(batch) * m.groups);
     st.xst.reserve(size_t(batch) * m.groups);
@@ -460,7 +470,9 @@ static void plan_upload(Plan &p) {
                               mi.n_pad,
                               block,
                               p.batch,
-                              p.xscale_t.p + size_t(i) * p.batch * m.groups};
+                              p.xscale_t.p + size_t(i) * p.batch * m.groups,
+                              0,
+                              p.xs_in[i]};
             block += mi.n_pad / kRowsPerBlock;
         }
         host.assign(reinterpret_cast<uint8_t *>(jobs.data()), reinterpret_cast<uint8_t *>(jobs.data() + p.count));
@@ -486,6 +498,13 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
         launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s);
     } else {
         const SdotHandle &h0 = *p.sd[0];
+        const SdotGeom g0 = h0.geom();
+        if (sdot_gemv_takes_x(g0, p.blocks, p.batch)) {  // batch 1, small matrices: the GEMV prepares its input
+            if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
+            launch_sdot_gemv_x(g0, SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, s);
+            if (gemv_stop) ND_HIP(hipEventRecord(gemv_stop, s));
+            return;
+        }
         // one launch prepares every (matrix, batch row) input
         if (!launch_sdot_prepare(nullptr, p.xptr.p, p.batch, p.count * p.batch, m.in, m.padded, m.dev, m.group,
                                  m.scale, m.kind, p.q.p, p.xscale.p, p.xscale_t.p, s)) {
@@ -495,8 +514,7 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
                                  p.xscale.p, s);
         }
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
-        launch_sdot_gemv(h0.geom(), SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, p.batch,
-                         s);
+        launch_sdot_gemv(g0, SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, p.batch, s);
     }
     if (gemv_stop) ND_HIP(hipEventRecord(gemv_stop, s));
 }

@@ -170,6 +170,8 @@ struct SdotGeom {
     int kind, group, groups, windows, chunks;
     float centroid_scale;     // cs = max|cb|/127
     uint32_t cent[4];         // int8 centroids packed little-endian (16 entries)
+    int in, padded;           // input length, padded to whole groups
+    float scale;              // 1/sqrt(group), as the prepare uses it
 };
 
 struct SdotJob {
@@ -181,6 +183,7 @@ struct SdotJob {
     int rows, n_pad, block_begin, batch;
     const float *xst;         // the same scales transposed, [groups][batch] (MFMA path; null: dot4 path only)
     int ystride;              // floats between batch rows of y (0: rows)
+    const float *x;           // the fp32 input row (batch 1), for launch_sdot_gemv_x
 };
 
 // ---------------------------------------------------------------------------
@@ -233,6 +236,12 @@ void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded
 // The batch (uniform across jobs) is processed in tiles that decode each code once.
 void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs_dev, int njobs, int total_blocks,
                       int batch, hipStream_t s);
+// Batch 1 on the small-matrix K-split kernel, which then prepares each job's input row (job.x) itself
+// (the prepare kernels' arithmetic) instead of reading q / xs: true when launch_sdot_gemv would run that
+// kernel for this shape and the prepared row fits its LDS (NEEDLE2_GPU_INT8_XIN=never: always false).
+bool sdot_gemv_takes_x(const SdotGeom &g, int blocks, int batch);
+void launch_sdot_gemv_x(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs_dev, int njobs, int total_blocks,
+                        hipStream_t s);
 // The same products' int32 group dots, dots[b][row][g], from the kernels the GEMV runs for this batch on a
 // large matrix (batch 1: the row kernel; 2 or more: the 4 x 4 x 4 batch-tile kernel); one job only.
 void launch_sdot_dots(const SdotGeom &g, const SdotJob &job0, int total_blocks, int batch, int32_t *dots,

@@ -480,6 +480,35 @@ __device__ __forceinline__ void mfma_load(MfmaSlot<KIND, GROUP, J> &sl, __amdgpu
                                                    __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2), 0);
 }
 
+// mfma_load for one batch row prepared in LDS (qst: the row's permuted codes,
+// dev bytes; scst: its group scales): lane (i, h) takes what mfma_load's
+// buffer loads would return for batch row i < 1, zeros for the rows past it.
+template <int KIND, int GROUP, int J>
+__device__ __forceinline__ void mfma_load_x(MfmaSlot<KIND, GROUP, J> &sl, __amdgpu_buffer_rsrc_t codes,
+                                            __amdgpu_buffer_rsrc_t norms, const int8_t *qst, const float *scst,
+                                            int g, int rt, int i, int h, int dev, int groups) {
+    using S = MfmaSlot<KIND, GROUP, J>;
+#pragma unroll
+    for (int st = 0; st < S::kSteps; ++st) {
+        const int pos = g * GROUP + st * 32;
+        if constexpr (KIND == kNib) {
+            const int soff = __builtin_amdgcn_readfirstlane((pos / 32) * kRowsPerBlock * 16);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b64(codes, rt * 16u + h * 8u, soff, 0);
+            sl.code[2 * st] = v[0];
+            sl.code[2 * st + 1] = v[1];
+        } else {
+            const int soff = __builtin_amdgcn_readfirstlane((pos / 64) * kRowsPerBlock * 16 + ((pos / 32) % 2) * 8);
+            sl.code[st] = __builtin_amdgcn_raw_buffer_load_b32(codes, rt * 16u + h * 4u, soff, 0);
+        }
+        sl.q[st] = i == 0 && pos < dev ? *reinterpret_cast<const u32x4 *>(qst + pos + h * 16) : u32x4{0u, 0u, 0u, 0u};
+    }
+    const uint32_t sc = g < groups ? __builtin_bit_cast(uint32_t, scst[g < groups ? g : 0]) : 0u;
+#pragma unroll
+    for (int j = 0; j < J; ++j) sl.xs[j] = u32x4{j == 0 && h == 0 ? sc : 0u, 0u, 0u, 0u};
+    sl.norm = __builtin_amdgcn_raw_buffer_load_b16(norms, rt * 2u,
+                                                   __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2), 0);
+}
+
 template <int KIND, int GROUP, int J>
 __device__ __forceinline__ void mfma_group(const MfmaSlot<KIND, GROUP, J> &sl, const uint32_t cent[4], float cs,
                                            float (&value)[4 * J]) {
@@ -1171,12 +1200,17 @@ __device__ __forceinline__ void mfma_terms(const MfmaSlot<KIND, GROUP, J> &sl, c
     for (int r = 0; r < 4 * J; ++r) term[r] = value[r];
 }
 
-template <int KIND, int GROUP, int J>
+// XIN (batch 1): the workgroup prepares the job's input row J.x into LDS
+// first, each wave the groups its rounds read (prepare_lane /
+// prepare_group_wave: the prepare kernels' arithmetic), so the plan launches
+// no prepare kernel; the outputs are the same bits.
+template <int KIND, int GROUP, int J, bool XIN>
 __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
                                                                 int njobs, SdotGeom geom) {
     constexpr int R = 4 * J;                          // accumulator registers in use
     constexpr int kOwn = (R + kKs - 1) / kKs;         // registers each wave sums
     __shared__ float park[2][kKs][R][64];
+    extern __shared__ __attribute__((aligned(16))) uint8_t xin_lds[];  // XIN: q [dev], then scales [groups]
     const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int rb = blockIdx.x;                        // 32-row block across the plan
@@ -1194,6 +1228,7 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
         J0.batch = cj[j].batch;
         J0.ystride = cj[j].ystride;
         J0.xst = cj[j].xst;
+        J0.x = cj[j].x;
     }
     const int rows = J0.rows, batch = J0.batch;
     const int tile = blk - J0.block_begin;
@@ -1215,15 +1250,47 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
                     static_cast<uint32_t>(tile_rows) * dev);
     const __amdgpu_buffer_rsrc_t xst = buffer_rsrc(J0.xst, static_cast<uint32_t>(groups) * batch * 4u);
 
+    int8_t *qst = reinterpret_cast<int8_t *>(xin_lds);
+    float *scst = reinterpret_cast<float *>(xin_lds + dev);
+    if constexpr (XIN) {
+        const float *xv = J0.x;
+        const int in = geom.in, padded = geom.padded;
+        if constexpr (GROUP <= 64) {  // 64 / GROUP of the wave's groups per pass, one lane per position
+            constexpr int PER = 64 / GROUP;
+            for (int k = 0; w + kKs * PER * k < groups; ++k) {
+                const int g = w + kKs * (PER * k + lane / GROUP);
+                const int p = g * GROUP + lane % GROUP;
+                const float r = p < in ? xv[p] : 0.0f;
+                prepare_lane<GROUP>(r, lane, p, padded, dev, geom.scale, KIND, qst, scst + (g < groups ? g : 0),
+                                    nullptr);
+            }
+        } else {
+            for (int g = w; g < groups; g += kKs) {
+                float r[GROUP / 64];
+#pragma unroll
+                for (int k = 0; k < GROUP / 64; ++k) {
+                    const int p = g * GROUP + lane + 64 * k;
+                    r[k] = p < in ? xv[p] : 0.0f;
+                }
+                prepare_group_wave<GROUP>(r, lane, g * GROUP, padded, dev, geom.scale, KIND, qst, scst + g, nullptr);
+            }
+        }
+        __syncthreads();
+    }
+    auto load = [&](MfmaSlot<KIND, GROUP, J> &sl, int g) {
+        if constexpr (XIN) mfma_load_x(sl, codes, norms, qst, scst, g, rt, i, h, dev, groups);
+        else mfma_load(sl, codes, norms, q, xst, g, rt, i, h, dev, batch, b0);
+    };
+
     float value[kOwn];
 #pragma unroll
     for (int k = 0; k < kOwn; ++k) value[k] = 0.0f;
     const int rounds = (groups + kKs - 1) / kKs;
     MfmaSlot<KIND, GROUP, J> cur, nxt;
-    mfma_load(cur, codes, norms, q, xst, w, rt, i, h, dev, batch, b0);
+    load(cur, w);
     for (int r = 0; r < rounds; ++r) {
         // next round's group (past the last group: zeros, or data that is never used)
-        mfma_load(nxt, codes, norms, q, xst, (r + 1) * kKs + w, rt, i, h, dev, batch, b0);
+        load(nxt, (r + 1) * kKs + w);
         float term[R];
         mfma_terms(cur, cent, cs, term);
 #pragma unroll
@@ -1249,15 +1316,16 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
     }
 }
 
-template <int KIND, int J>
+template <int KIND, int J, bool XIN = false>
 void launch_sdot_ks_j(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
                       hipStream_t s) {
     dim3 grid(blocks * (kRowsPerBlock / 32), (batch + 31) / 32), block(kKs * 64);
+    const size_t lds = XIN ? static_cast<size_t>(g.windows) * kWindow + static_cast<size_t>(g.groups) * 4 : 0;
     switch (g.group) {
-    case 32: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 32, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 64, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 128, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    default: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 256, J>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 32: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 32, J, XIN>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 64, J, XIN>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 128, J, XIN>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 256, J, XIN>), grid, block, lds, s, job0, jobs, njobs, g); break;
     }
     ND_HIP(hipGetLastError());
 }
@@ -1467,23 +1535,10 @@ __global__ __launch_bounds__(256) void sdot_prepare_wave_kernel(const float *__r
     const int p = blockIdx.x * 256 + threadIdx.x;
     const int t = threadIdx.x & 63;
     const float *xv = (xptr ? xptr[v / batch] : x0) + static_cast<size_t>(v % batch) * in;
-    float r = p < in ? xv[p] : 0.0f;
-    wave_butterflies<GROUP, 1>(r, t);
-    r = r * scale;
-    const float absmax = group_max<GROUP>(fabsf(r), t);
-    int8_t out = 0;
-    if (p < padded) {
-        float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
-        if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
-        if (p % GROUP == 0) {
-            xs[static_cast<size_t>(v) * groups + p / GROUP] = sc;
-            if (xst) xst[(static_cast<size_t>(v / batch) * groups + p / GROUP) * batch + v % batch] = sc;
-        }
-        float val = rintf(r / sc);
-        val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
-        out = static_cast<int8_t>(val);
-    }
-    if (p < dev) q[static_cast<size_t>(v) * dev + permuted_index(kind, p)] = out;
+    const float r = p < in ? xv[p] : 0.0f;
+    prepare_lane<GROUP>(r, t, p, padded, dev, scale, kind, q + static_cast<size_t>(v) * dev,
+                        xs + static_cast<size_t>(v) * groups + p / GROUP,
+                        xst ? xst + (static_cast<size_t>(v / batch) * groups + p / GROUP) * batch + v % batch : nullptr);
 }
 
 // Prepare for groups of 128 and 256 positions, one wave per group without
@@ -1590,6 +1645,24 @@ static bool ks16_chosen(const SdotGeom &g, int batch) {
     const char *ks16_mode = std::getenv("NEEDLE2_GPU_INT8_KS16");
     return !(ks16_mode && std::strcmp(ks16_mode, "never") == 0) &&
            (batch >= 2 || (ks16_mode && std::strcmp(ks16_mode, "always") == 0));
+}
+
+// The XIN kernel's LDS: the prepared row and its scales beside the 16 KiB of parked terms.
+constexpr size_t kXinMaxLds = 32 * 1024;
+
+bool sdot_gemv_takes_x(const SdotGeom &g, int blocks, int batch) {
+    const char *mode = std::getenv("NEEDLE2_GPU_INT8_XIN");
+    if (mode && std::strcmp(mode, "never") == 0) return false;
+    const size_t lds = static_cast<size_t>(g.windows) * kWindow + static_cast<size_t>(g.groups) * 4;
+    return batch == 1 && g.group >= 32 && g.group <= kWindow && lds <= kXinMaxLds && ks_chosen(g, blocks, 1) &&
+           !ks16_chosen(g, 1);
+}
+
+void launch_sdot_gemv_x(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
+                        hipStream_t s) {
+    ND_CHECK(sdot_gemv_takes_x(g, blocks, 1), "internal: int8 GEMV with in-kernel prepare outside its shapes");
+    if (g.kind == kNib) launch_sdot_ks_j<kNib, 1, true>(g, job0, jobs, njobs, blocks, 1, s);
+    else launch_sdot_ks_j<kCrumb, 1, true>(g, job0, jobs, njobs, blocks, 1, s);
 }
 
 void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,

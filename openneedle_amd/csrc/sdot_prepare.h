@@ -18,6 +18,35 @@ __device__ __forceinline__ int permuted_index(int kind, int p) {
     return (d << 4) | ((i & 3) << 2) | (i >> 2);
 }
 
+// Groups of 8 .. 64 positions: lane t holds position p (groups are aligned
+// runs of GROUP lanes): the group FWHT as in-wave butterflies (the
+// reference's stage order and operands), the group absmax as an in-wave max,
+// then the reference's quantiser (sdot.cpp:56-81: scale = absmax / 127, 1 for
+// an all-zero group, absmax if the quotient underflows; q = clamp(rint(x /
+// scale), +-127) with IEEE division). The group's first lane stores the scale
+// at *xs (and *xst when not null); q goes to qv (the vector's row of dev
+// bytes) in the permuted order. Past `padded` a position stores zero.
+template <int GROUP>
+__device__ __forceinline__ void prepare_lane(float r, int t, int p, int padded, int dev, float scale, int kind,
+                                             int8_t *qv, float *xs, float *xst) {
+    wave_butterflies<GROUP, 1>(r, t);
+    r = r * scale;
+    const float absmax = group_max<GROUP>(fabsf(r), t);
+    int8_t out = 0;
+    if (p < padded) {
+        float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
+        if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
+        if (p % GROUP == 0) {
+            *xs = sc;
+            if (xst) *xst = sc;
+        }
+        float val = rintf(r / sc);
+        val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
+        out = static_cast<int8_t>(val);
+    }
+    if (p < dev) qv[permuted_index(kind, p)] = out;
+}
+
 // Lane t holds positions base + t + 64 k (k < GROUP / 64) of its wave's group
 // in r: the FWHT stages 1 .. 32 run as in-wave butterflies on every k, then
 // the stages 64 and 128 between a lane's own values, in the reference's

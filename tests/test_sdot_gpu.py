@@ -153,6 +153,37 @@ def test_int8_plan_decode_batch(mode, monkeypatch):
             np.testing.assert_array_equal(dy.download(np.empty((64, 512), np.float32)), e)
 
 
+@pytest.mark.parametrize("xin", ["auto", "never"])
+@pytest.mark.parametrize("bits,group,rows,dim", [(4, 32, 512, 512), (4, 32, 2048, 512), (4, 32, 512, 2048),
+                                                 (2, 128, 1536, 512), (4, 64, 300, 1000), (2, 256, 257, 1300),
+                                                 (2, 32, 640, 777)])
+def test_int8_plan_batch1_input_prepared_in_gemv(bits, group, rows, dim, xin, monkeypatch):
+    """Batch-1 plans of small matrices (decode projections) run the 32 x 32 K-split GEMV, which prepares the
+    input row itself (auto: no prepare launch) or reads the prepare kernel's output (never): three matrices
+    over one input with a zero group and a one-hot group, two runs in a row, bit-exact with the oracle."""
+    monkeypatch.setenv("NEEDLE2_GPU_INT8_XIN", xin)
+    x = activations((1, dim), seed=rows + dim)
+    x[0, :group] = 0
+    if dim > 2 * group:
+        x[0, group:2 * group] = 0
+        x[0, group + 3] = -2.5
+    d_in = DeviceArray.from_host(x)
+    mats, d_y, expected = [], [], []
+    for i in range(3):
+        packed, norms, cb, dense = example(bits, rows=rows, dim=dim, group=group, seed=900 + 7 * i + group)
+        mats.append(CQMatrix(packed, norms, dense.shape, bits, group, cb))
+        expected.append(oracle.sdot_linear(packed, norms, dense.shape, bits, group, cb, x))
+        d_y.append(DeviceArray(rows * 4))
+    plan = Plan(mats, [d_in.ptr] * 3, [d.ptr for d in d_y], batch=1, int8=True)
+    for _ in range(2):
+        for d in d_y:
+            d.fill(0x7F)
+        plan.run()
+        synchronize()
+        for dy, e in zip(d_y, expected):
+            np.testing.assert_array_equal(dy.download(np.empty((1, rows), np.float32)), e)
+
+
 @pytest.mark.parametrize("mode", ["auto", "never", "ksplit", "ksplit16"])
 @pytest.mark.parametrize("bits,group,dim", [(4, 8, 1000), (4, 32, 1000), (4, 64, 4096), (4, 256, 1300), (2, 16, 1000),
                                             (2, 32, 777), (2, 128, 2048)])
