@@ -178,7 +178,8 @@ struct SdotGroup {
                 const float *st = xs.p + size_t(t) * m0->groups;  // batch 1: the transposed scales are the same
                 host.push_back(SdotJob{p.m->codes.p + size_t(tile0) * p.m->chunks * kRowsPerBlock,
                                        p.m->norms.p + size_t(tile0) * p.m->groups * kRowsPerBlock, qt, st,
-                                       p.y + size_t(t) * p.ystride, rows, tiles * kRowsPerBlock, blocks, 1, st});
+                                       p.y + size_t(t) * p.ystride, rows, tiles * kRowsPerBlock, blocks, 1, st, 0,
+                                       rows_in[t]});
                 blocks += tiles;
             }
         pieces = static_cast<int>(ps.size());
@@ -219,6 +220,11 @@ struct SdotGroup {
     // prepared: the input was prepared into target()'s buffers already
     void run(hipStream_t s, int tokens, bool prepared = false) {
         const bool batch = tokens >= 2 && batched.p;
+        if (!prepared && tokens == 1 && sdot_gemv_takes_x(g, per_token, 1)) {  // the GEMV prepares the row itself
+            launch_sdot_gemv_x(g, job0, pieces > 1 ? reinterpret_cast<const SdotJob *>(jobs.p) : nullptr,
+                               pieces > 1 ? pieces : 0, per_token, s);
+            return;
+        }
         if (!prepared &&
             !launch_sdot_prepare(nullptr, xptr.p, batch ? tokens : 1, tokens, m0->in, m0->padded, m0->dev, m0->group,
                                  m0->scale, m0->kind, q.p, xs.p, batch ? xst.p : nullptr, s)) {
