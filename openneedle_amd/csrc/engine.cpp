@@ -20,7 +20,6 @@
 // token history (slot lists, RoPE angles with std::cos / std::sin, engram
 // hashes) and uploads it once per step.
 #include "abi_internal.h"
-#include "attn.h"
 #include "engine.h"
 
 #include <algorithm>
@@ -330,9 +329,7 @@ struct GpuEngine {
     HostBuf<StepParams> hparams;
     DevBuf<int64_t> ids;   // per chunk: tokens [chunk], then engram rows [sites][chunk][tables]
     HostBuf<int64_t> hids;
-    DevBuf<int> lens;      // per chunk: attention list lengths [chunk]
-    HostBuf<int> hlens;
-    DevBuf<float> logits, part, embed_z, row_scratch, engram_scratch;
+    DevBuf<float> logits, embed_z, row_scratch, engram_scratch;
     DevBuf<float> attn_scores;  // fp32-KV attention scores past the LDS budget
     HostBuf<float> hlogits, hhidden;
     std::vector<Projection> mhc_proj, qkvg, oproj;
@@ -536,8 +533,6 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     ids.reserve(size_t(chunk) * (1 + size_t(sites) * std::max(1, c.tables)));
     hids.reserve(ids.n);
     std::memset(hids.p, 0, ids.n * sizeof(int64_t));
-    lens.reserve(chunk);
-    hlens.reserve(chunk);
     logits.reserve(size_t(chunk) * c.vocab);
     embed_z.reserve(size_t(chunk) * D);
 
@@ -653,10 +648,8 @@ void GpuEngine::reset(int prefix_len) {
     capacity = c.window ? ring + prefix : c.max_seq;
     dims.capacity = capacity;
     const int G = c.heads / c.kvheads;
-    if (int8_kv)
-        ND_CHECK(attn_supported(c.head_dim, G), "int8 KV attention: head_dim 32/64/128 with 1, 2, 4 or 8 heads per kv head");
-    // fp32 KV: scores past the LDS budget go to a device buffer (any context)
-    if (!int8_kv && size_t(G) * max_length() * sizeof(float) > kEngScoreLds)
+    // attention scores past the LDS budget go to a device buffer (any context)
+    if (size_t(G) * max_length() * sizeof(float) > kEngScoreLds)
         attn_scores.reserve(size_t(chunk) * c.kvheads * G * max_length());
     else
         attn_scores.release();
@@ -1011,10 +1004,6 @@ void GpuEngine::run(int tokens) {
     const int G = c.heads / c.kvheads;
     int maxlen = 0;
     for (int t = 0; t < T; ++t) maxlen = std::max(maxlen, hparams.p[t].length);
-    if (int8_kv && T > 1) {
-        for (int t = 0; t < T; ++t) hlens.p[t] = hparams.p[t].length;
-        ND_HIP(hipMemcpyAsync(lens.p, hlens.p, size_t(T) * sizeof(int), hipMemcpyHostToDevice, s));
-    }
     // a layer's post runs with the next layer's mHC projections and mixing
     // when those are dense and the geometry fits the fused kernel
     const bool fuse = phi[0] && phi[1] && phi[2] && eng_post_mix_fits(dims);
@@ -1052,52 +1041,17 @@ void GpuEngine::run(int tokens) {
         qkvg[l].run(s, T, qkvg_prepared);
         PrepTarget ot;
         bool o_prepared = target(oproj[l], ot);
-        if (!int8_kv) {
-            // one token: norms, RoPE, store and attention in one kernel; a chunk
-            // stores every token's K / V before any token attends; the attention
-            // prepares the out-projection's input when a kv head's outputs are
-            // one group and no activation quantiser runs between
-            if (o_prepared && (abits || ot.group != G * HD || ot.dev != c.heads * HD)) {
-                o_prepared = false;
-                ot = PrepTarget{};
-            }
-            if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
-            launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, mh, l, ot, s);
-            launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
-        } else {
-            launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
-            AttnArgs a{};
-            a.k8 = kv[l].k8;
-            a.v8 = kv[l].v8;
-            a.ks = kv[l].ks;
-            a.vs = kv[l].vs;
-            a.q = b.q;
-            a.out = b.att;
-            a.slots = b.slots;
-            a.seqs = T;
-            a.kvheads = c.kvheads;
-            a.head_dim = HD;
-            a.capacity = capacity;
-            a.length = maxlen;
-            a.scale = dims.scale;
-            const int tiles = (maxlen + 255) / 256;
-            if (T == 1) {  // one token: split its slots over up to 64 blocks
-                a.splits = std::max(1, std::min(tiles, 64 / c.kvheads));
-                const int per = (tiles + a.splits - 1) / a.splits * 256;
-                a.splits = std::max(1, (maxlen + per - 1) / per);
-                a.slots_per_split = per;
-                if (a.splits > 1) part.reserve(size_t(c.heads) * a.splits * (HD + 2));
-                a.part = part.p;
-            } else {  // a chunk: one block per (token, kv head), every token's own list into the shared cache
-                a.splits = 1;
-                a.slots_per_split = tiles * 256;
-                a.lengths = lens.p;
-                a.slots_stride = capacity;
-                a.shared_cache = 1;
-            }
-            launch_attention(a, G, s);
-            launch_eng_gate(b, dims, T, mh, l, ot, s);
+        // one token: norms, RoPE, the KV store (fp32, or the int8 quantiser) and attention in one kernel;
+        // a chunk stores every token's K / V before any token attends; the attention prepares the
+        // out-projection's input when a kv head's outputs are one group and no activation quantiser
+        // runs between
+        if (o_prepared && (abits || ot.group != G * HD || ot.dev != c.heads * HD)) {
+            o_prepared = false;
+            ot = PrepTarget{};
         }
+        if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
+        launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, mh, l, ot, s);
+        launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
         oproj[l].run(s, T, o_prepared);
         if (fuse && l + 1 < c.layers) {
             int sites[kEngMaxSites];

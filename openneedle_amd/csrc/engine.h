@@ -101,21 +101,18 @@ void launch_eng_engram_out(const EngineBufs &b, const float *taps, const StepPar
 void launch_eng_mix(const EngineBufs &b, const LayerDev &ld, const MhcDev &mh, int l, const int *mhc_row,
                     const int *sites, int nsites, const EngineDims &d, int tokens, const PrepTarget &pt,
                     hipStream_t s);
-// q / k norms, RoPE, the K / V store and (int8 KV) the slot lists of every token
+// q / k norms, RoPE and the K / V store of every token
 void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                    const EngineDims &d, int tokens, hipStream_t s);
-// fp32 KV attention + output gate of every kv head; with `prepared` false (one
-// token) it also does that token's norms, RoPE and KV store, else eng_qk did
-// scores: null when G * max_length floats fit kEngScoreLds, else a device
-// buffer of tokens * kvheads * G * max_length floats
-// Both also run layer l's residual routing (Sinkhorn of hres into hroute) in one more workgroup per token,
-// and prepare the out-projection's int8 input from att when pt.q is set (the attention only for a group of
-// one kv head's outputs, heads / kvheads * head_dim positions).
+// Attention + output gate of every kv head over an fp32 or int8 KV cache (kv.k8 set); with `prepared`
+// false (one token) it also does that token's norms, RoPE and KV store, else eng_qk did. scores: null
+// when G * max_length floats fit kEngScoreLds, else a device buffer of tokens * kvheads * G * max_length
+// floats. It also runs layer l's residual routing (Sinkhorn of hres into hroute) in one more workgroup
+// per token, and prepares the out-projection's int8 input from att when pt.q is set (a group of one kv
+// head's outputs, heads / kvheads * head_dim positions).
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
                            const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s);
-void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, const MhcDev &mh, int l,
-                     const PrepTarget &pt, hipStream_t s);
 // K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
 void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
                           const EngineDims &d, hipStream_t s);

@@ -26,6 +26,14 @@ namespace {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Four int8 codes (little-endian bytes of w) as floats.
+__device__ __forceinline__ float4 int8x4_to_float4(uint32_t w) {
+    return make_float4(static_cast<float>(static_cast<int8_t>(w & 0xFFu)),
+                       static_cast<float>(static_cast<int8_t>((w >> 8) & 0xFFu)),
+                       static_cast<float>(static_cast<int8_t>((w >> 16) & 0xFFu)),
+                       static_cast<float>(static_cast<int8_t>(w >> 24)));
+}
+
 // Token t's vectors (EngineBufs documents the per-token sizes).
 __device__ __forceinline__ EngineBufs at_token(EngineBufs b, const EngineDims &d, int t) {
     const size_t nd = static_cast<size_t>(d.N) * d.D;
@@ -499,21 +507,23 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b0, Laye
             }
         }
     }
-    // slot list of this position (engine.cpp:907-909)
-    if (kv.k8)
-        for (int s = threadIdx.x; s < p->length; s += blockDim.x) b.slots[s] = slot_at(p, s);
 }
 
-// The fp32-KV attention step of one kv head in one workgroup: the norms and
-// RoPE of its G query heads and of its K head, the new K / V row into the
-// cache, attention over the slot list (computed in place from the position,
-// engine.cpp:900-909) and the output gate att *= sigmoid(gate)
-// (engine.cpp:994-1023). Nothing crosses kv heads, so one launch does it all.
+// The attention step of one kv head in one workgroup: the norms and RoPE of
+// its G query heads and of its K head, the new K / V row into the cache (fp32,
+// or the int8 store quantiser), attention over the slot list (computed in
+// place from the position, engine.cpp:900-909) and the output gate att *=
+// sigmoid(gate) (engine.cpp:994-1023). Nothing crosses kv heads, so one
+// launch does it all.
 
 // The scores [G][length] live in LDS, or, past the LDS budget (long
 // contexts), in `scores` ([tokens][kv heads][G][max_length] in device memory):
 // the same block writes, reduces and reads them, ordered by its barriers.
-template <bool PREPARED, bool GLOBAL_SCORES>
+// I8: an int8 KV cache (codes with a scale per row, the store kernel's
+// quantiser for the new row): s = dot(q, float(k8)) * k_scale * (1 /
+// sqrt(head_dim)), p = softmax(s), out = sum_s (p_s * v_scale_s) * float(v8)
+// (engine.cpp:898-967, as the int8 attention kernel).
+template <bool PREPARED, bool GLOBAL_SCORES, bool I8>
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d,
                                                              float *__restrict__ scores, int max_length, MhcDev mh,
@@ -533,8 +543,13 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
                     ? scores + (static_cast<size_t>(blockIdx.y) * gridDim.x + kh) * G * static_cast<size_t>(max_length)
                     : sc_lds;
     const int wave = t >> 6, lane = t & 63, length = p->length;
-    const float *kc = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
-    const float *vc = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
+    const size_t row0 = static_cast<size_t>(kh) * d.capacity;  // this kv head's first cache row
+    const float *kc = I8 ? nullptr : kv.k32 + row0 * HD;
+    const float *vc = I8 ? nullptr : kv.v32 + row0 * HD;
+    const int8_t *kc8 = I8 ? kv.k8 + row0 * HD : nullptr;
+    const int8_t *vc8 = I8 ? kv.v8 + row0 * HD : nullptr;
+    const float *ksc = I8 ? kv.ks + row0 : nullptr;
+    const float *vsc = I8 ? kv.vs + row0 : nullptr;
     // loaded before the norms: the output gate of output t, and at head_dim 64 the K row of this thread's
     // first slot unless this kernel stores that row below (the new token's)
     // (loads without branches: an entry past the list reads slot 0 and is not used)
@@ -542,22 +557,30 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     const float gate_t = t < G * HD ? b.gate[kh * G * HD + t] : 0.0f;
     const int slot_t = t < length ? slot_of(t) : 0;
     const bool k_early = HD == 64 && t < length && (PREPARED || slot_t != p->slot);
-    float4 kpre[16];
+    float4 kpre[I8 ? 4 : 16];  // fp32: the row; int8: its 64 codes
+    float kpre_s = 0.0f;
     if (HD == 64) {
-        const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_t) * HD);
+        if constexpr (I8) {
+            const float4 *k4 = reinterpret_cast<const float4 *>(kc8 + static_cast<size_t>(slot_t) * HD);
 #pragma unroll
-        for (int c = 0; c < 16; ++c) kpre[c] = k4[c];
+            for (int c = 0; c < 4; ++c) kpre[c] = k4[c];
+            kpre_s = ksc[slot_t];
+        } else {
+            const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_t) * HD);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) kpre[c] = k4[c];
+        }
     }
     if (PREPARED) {  // eng_qk normalised and rotated q and stored K / V
         for (int i = t; i < G * HD; i += blockDim.x) qs[i] = b.q[kh * G * HD + i];
     } else {
-    // norms + RoPE: heads 0..G-1 are this block's query heads (into qs), head G its K row (into the cache)
-    float *kw = kv.k32 + static_cast<size_t>(kh) * d.capacity * HD;
-    float *vw = kv.v32 + static_cast<size_t>(kh) * d.capacity * HD;
+    // norms + RoPE: heads 0..G-1 are this block's query heads (into qs), head G its K row (into the cache;
+    // int8: into LDS, then through the store kernel's quantiser)
+    float *kw = I8 ? qs + kMaxG * HD : kv.k32 + row0 * HD + static_cast<size_t>(p->slot) * HD;
     for (int h = wave; h <= G; h += blockDim.x >> 6) {
         const float *src = h < G ? b.q + (kh * G + h) * HD : b.k + kh * HD;
         const float *gain = h < G ? ld.q_norm : ld.k_norm;
-        float *dst = h < G ? qs + h * HD : kw + static_cast<size_t>(p->slot) * HD;
+        float *dst = h < G ? qs + h * HD : kw;
         float ss = 0.0f;
         for (int i = lane; i < HD; i += 64) ss += src[i] * src[i];
         ss = wave_sum(ss, lane);
@@ -568,8 +591,32 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
             dst[j] = a * co - c * si;
             dst[j + half] = c * co + a * si;
         }
+        if (I8 && h == G) {  // eng_qk_kernel's quantiser for the new K / V rows (same codes and scales)
+            const float *vr = b.v + kh * HD;
+            const size_t row = row0 + p->slot;
+            float mk = 0.0f, mv = 0.0f;
+            for (int i = lane; i < HD; i += 64) {
+                mk = fmaxf(mk, fabsf(kw[i]));
+                mv = fmaxf(mv, fabsf(vr[i]));
+            }
+            mk = wave_max(mk, lane);
+            mv = wave_max(mv, lane);
+            const float sk = mk > 0 ? mk / 127.0f : 1.0f, sv = mv > 0 ? mv / 127.0f : 1.0f;
+            const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
+            if (lane == 0) {
+                kv.ks[row] = sk;
+                kv.vs[row] = sv;
+            }
+            for (int i = lane; i < HD; i += 64) {
+                const float qk = fmaxf(-127.0f, fminf(127.0f, rintf(kw[i] * ik)));
+                const float qv = fmaxf(-127.0f, fminf(127.0f, rintf(vr[i] * iv)));
+                kv.k8[row * HD + i] = static_cast<int8_t>(qk);
+                kv.v8[row * HD + i] = static_cast<int8_t>(qv);
+            }
+        }
     }
-    for (int i = t; i < HD; i += blockDim.x) vw[static_cast<size_t>(p->slot) * HD + i] = b.v[kh * HD + i];
+    if (!I8)
+        for (int i = t; i < HD; i += blockDim.x) kv.v32[(row0 + p->slot) * HD + i] = b.v[kh * HD + i];
     }
     __syncthreads();
     // values: thread t takes 16-byte column c = t % (HD / 4) of the V rows of slots r, r + R, ..
@@ -581,16 +628,68 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     const bool sub = r < R;
     float4 vpre[kPre];
     {  // buffer loads: an entry past the list reads zeros (offset past the resource)
-        const __amdgpu_buffer_rsrc_t vres = buffer_rsrc(vc, static_cast<uint32_t>(d.capacity) * HD * 4u);
+        const uint32_t esz = I8 ? 1u : 4u;
+        const __amdgpu_buffer_rsrc_t vres =
+            buffer_rsrc(I8 ? static_cast<const void *>(vc8) : static_cast<const void *>(vc),
+                        static_cast<uint32_t>(d.capacity) * HD * esz);
 #pragma unroll
         for (int k = 0; k < kPre; ++k) {
             const int s = r + k * R;
-            const uint32_t off = sub && s < length ? (static_cast<uint32_t>(slot_of(s)) * HD + 4u * c4) * 4u
+            const uint32_t off = sub && s < length ? (static_cast<uint32_t>(slot_of(s)) * HD + 4u * c4) * esz
                                                    : 0xFFFFFFF0u;
-            vpre[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0));
+            if constexpr (I8)
+                vpre[k] = int8x4_to_float4(__builtin_amdgcn_raw_buffer_load_b32(vres, off, 0, 0));
+            else
+                vpre[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0));
         }
     }
-    if (HD == 64) {
+    if constexpr (I8) {
+        for (int s = t; s < length; s += blockDim.x) {
+            const int sl = slot_of(s);
+            if (HD == 64) {
+                u32x4 k4[4];
+                float kscale;
+                if (s == t && k_early) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) k4[c] = __builtin_bit_cast(u32x4, kpre[c]);
+                    kscale = kpre_s;
+                } else {
+                    const u32x4 *src = reinterpret_cast<const u32x4 *>(kc8 + static_cast<size_t>(sl) * HD);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) k4[c] = src[c];
+                    kscale = ksc[sl];
+                }
+                for (int g = 0; g < G; ++g) {
+                    const float *q = qs + g * HD;
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) {
+                        const float4 k = int8x4_to_float4(k4[c / 4][c % 4]);
+                        dot += q[4 * c] * k.x;
+                        dot += q[4 * c + 1] * k.y;
+                        dot += q[4 * c + 2] * k.z;
+                        dot += q[4 * c + 3] * k.w;
+                    }
+                    sc[g * length + s] = dot * kscale * d.scale;
+                }
+            } else {
+                const uint32_t *k4 = reinterpret_cast<const uint32_t *>(kc8 + static_cast<size_t>(sl) * HD);
+                const float kscale = ksc[sl];
+                for (int g = 0; g < G; ++g) {
+                    const float *q = qs + g * HD;
+                    float dot = 0.0f;
+                    for (int c = 0; c < HD / 4; ++c) {
+                        const float4 k = int8x4_to_float4(k4[c]);
+                        dot += q[4 * c] * k.x;
+                        dot += q[4 * c + 1] * k.y;
+                        dot += q[4 * c + 2] * k.z;
+                        dot += q[4 * c + 3] * k.w;
+                    }
+                    sc[g * length + s] = dot * kscale * d.scale;
+                }
+            }
+        }
+    } else if (HD == 64) {
         for (int s = t; s < length; s += blockDim.x) {
             float4 k[16];
             if (s == t && k_early) {
@@ -674,7 +773,10 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
             float sum = 0.0f;
             for (int w = 0; w < kWaves; ++w) sum += red[g * kWaves + w];
             const float inv = 1.0f / sum;
-            for (int s = t; s < length; s += blockDim.x) sc[g * length + s] *= inv;
+            for (int s = t; s < length; s += blockDim.x) {
+                const float pr = sc[g * length + s] * inv;
+                sc[g * length + s] = I8 ? pr * vsc[slot_of(s)] : pr;  // int8: p_s * v_scale_s
+            }
         }
     __syncthreads();
     float4 acc[kMaxG];
@@ -707,8 +809,12 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
             }
     }
 #pragma unroll 8
-    for (int s = sub ? r + kPre * R : length; s < length; s += R)
-        accumulate(s, reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_of(s)) * HD)[c4]);
+    for (int s = sub ? r + kPre * R : length; s < length; s += R) {
+        if constexpr (I8)
+            accumulate(s, int8x4_to_float4(reinterpret_cast<const uint32_t *>(vc8 + static_cast<size_t>(slot_of(s)) * HD)[c4]));
+        else
+            accumulate(s, reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_of(s)) * HD)[c4]);
+    }
     float4 *wpart = reinterpret_cast<float4 *>(qs);  // [R][G][HD / 4]: R * G * HD = 1024 G floats
     __syncthreads();
 #pragma unroll
@@ -764,21 +870,6 @@ __global__ __launch_bounds__(64) void eng_kv_import_kernel(const float *__restri
         kv.k8[row * HD + i] = static_cast<int8_t>(fmaxf(-127.0f, fminf(127.0f, rintf(kr[i] * ik))));
         kv.v8[row * HD + i] = static_cast<int8_t>(fmaxf(-127.0f, fminf(127.0f, rintf(vr[i] * iv))));
     }
-}
-
-// att *= sigmoid(gate); then the activation quantiser (engine.cpp:1023-1024).
-__global__ __launch_bounds__(kEngThreads) void eng_gate_kernel(EngineBufs b0, EngineDims d, MhcDev mh, int l,
-                                                               PrepTarget pt) {
-    __shared__ float red[kEngThreads / 64];
-    const EngineBufs b = at_token(b0, d, blockIdx.y);
-    if (blockIdx.x == 1) {  // the routing workgroup
-        route_wave(b, mh, l, d);
-        return;
-    }
-    for (int i = threadIdx.x; i < d.A; i += blockDim.x) b.att[i] *= sigmoidf_(b.gate[i]);
-    __syncthreads();
-    quantize_block(b.att, d.A, d.abits, red);
-    if (pt.q) prepare_groups(pt, b.att, 0, d.A, 0, pt.dev / pt.group, 0, blockIdx.y, gridDim.y);
 }
 
 // engine.cpp:1025-1039: attention residual, Hadamard MLP, mHC residual
@@ -1128,20 +1219,25 @@ void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLaye
     ND_CHECK(!pt.q || (pt.group == d.H / d.KV * d.HD && pt.group <= 256 && pt.dev == d.A),
              "internal: attention prepares one kv head's outputs as one group");
     const size_t lds = scores ? 0 : static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);
-    ND_CHECK(lds <= kEngScoreLds, "internal: fp32 attention scores exceed the LDS budget without a score buffer");
+    ND_CHECK(lds <= kEngScoreLds, "internal: attention scores exceed the LDS budget without a score buffer");
     const dim3 grid(d.KV + 1, tokens), block(256);  // workgroup KV: the routing
-    if (prepared && scores)
-        hipLaunchKernelGGL((eng_attn_fused_kernel<true, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length,
-                           mh, l, pt);
-    else if (prepared)
-        hipLaunchKernelGGL((eng_attn_fused_kernel<true, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0, mh,
-                           l, pt);
-    else if (scores)
-        hipLaunchKernelGGL((eng_attn_fused_kernel<false, true>), grid, block, 0, s, b, ld, kv, p, d, scores, max_length,
-                           mh, l, pt);
-    else
-        hipLaunchKernelGGL((eng_attn_fused_kernel<false, false>), grid, block, lds, s, b, ld, kv, p, d, nullptr, 0, mh,
-                           l, pt);
+    auto go = [&](auto i8) {
+        constexpr bool I8 = decltype(i8)::value;
+        if (prepared && scores)
+            hipLaunchKernelGGL((eng_attn_fused_kernel<true, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
+                               max_length, mh, l, pt);
+        else if (prepared)
+            hipLaunchKernelGGL((eng_attn_fused_kernel<true, false, I8>), grid, block, lds, s, b, ld, kv, p, d, nullptr,
+                               0, mh, l, pt);
+        else if (scores)
+            hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
+                               max_length, mh, l, pt);
+        else
+            hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8>), grid, block, lds, s, b, ld, kv, p, d,
+                               nullptr, 0, mh, l, pt);
+    };
+    if (kv.k8) go(std::true_type{});
+    else go(std::false_type{});
     ND_HIP(hipGetLastError());
 }
 
@@ -1149,12 +1245,6 @@ void launch_eng_kv_import(const float *k, const float *v, const int *slots, int 
                           const EngineDims &d, hipStream_t s) {
     if (count <= 0) return;
     hipLaunchKernelGGL(eng_kv_import_kernel, dim3(count * d.KV), dim3(64), 0, s, k, v, slots, kv, d);
-    ND_HIP(hipGetLastError());
-}
-
-void launch_eng_gate(const EngineBufs &b, const EngineDims &d, int tokens, const MhcDev &mh, int l,
-                     const PrepTarget &pt, hipStream_t s) {
-    hipLaunchKernelGGL(eng_gate_kernel, dim3(2, tokens), dim3(kEngThreads), 0, s, b, d, mh, l, pt);  // x = 1: the routing
     ND_HIP(hipGetLastError());
 }
 
