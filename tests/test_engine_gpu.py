@@ -101,15 +101,16 @@ def test_geometry_variants(name):
               flush=True)
         np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL, err_msg=f"hidden, step {i}")
         np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL, err_msg=f"logits, step {i}")
-    if dict(SMALL, **geo)["head_dim"] in (32, 64, 128):
-        for i, (lg, hd, rl, rh) in enumerate(run_both(a, TOKENS[:8], int8_kv=True)):
-            print(f"{name} int8 KV step {i}: logits rel {rel_l2(lg, rl):.2e}", flush=True)
-            assert rel_l2(hd, rh) < 1e-3 and rel_l2(lg, rl) < 1e-3, f"step {i}"
+    for i, (lg, hd, rl, rh) in enumerate(run_both(a, TOKENS[:8], int8_kv=True)):
+        print(f"{name} int8 KV step {i}: logits rel {rel_l2(lg, rl):.2e}", flush=True)
+        assert rel_l2(hd, rh) < 1e-3 and rel_l2(lg, rl) < 1e-3, f"step {i}"
 
 
-def test_long_context_fp32_kv():
-    """fp32 KV past the LDS budget of the fused attention (2 heads per kv head x 8192 positions of scores):
-    7000 imported positions, then steps and a prompt chunk, against the reference."""
+@pytest.mark.parametrize("int8", [False, True])
+def test_long_context(int8):
+    """A context past the LDS budget of the fused attention (2 heads per kv head x 8192 positions of scores,
+    which then go to device memory), fp32 and int8 KV: 7000 imported positions (int8: through the step's
+    quantiser), then steps and a prompt chunk, against the reference."""
     a = Archive(synthetic_model(dict(SMALL, max_seq_len=8192), engram_layers=(1,), engram_orders=(2, 3), group=32,
                                 seed=33))
     n = 7000
@@ -118,7 +119,7 @@ def test_long_context_fp32_kv():
     shape = (SMALL["num_layers"], n, SMALL["num_kv_heads"], SMALL["head_dim"])
     k = rng.standard_normal(shape).astype(np.float32)
     v = rng.standard_normal(shape).astype(np.float32)
-    gpu, ref = GpuEngine(a), oracle.RefEngine(a)
+    gpu, ref = GpuEngine(a, kv_cache="int8" if int8 else "fp32"), oracle.RefEngine(a, 0, int8)
     for e in (gpu, ref):
         e.import_state(ids, list(range(n)), k, v)
     pairs = []
@@ -129,8 +130,11 @@ def test_long_context_fp32_kv():
     rl, rh = ref.prefill(PROMPT[:9], hidden=True)
     pairs += [("prefill logits", lg, rl), ("prefill hidden", hd, rh)]
     for what, g, r in pairs:
-        print(f"{what}: max {np.abs(g - r).max():.2e}", flush=True)
-        np.testing.assert_allclose(g, r, atol=ATOL, rtol=RTOL, err_msg=what)
+        print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
+        if int8:  # a rounding difference can move one K / V code by one step (as in the short-context tests)
+            assert rel_l2(g, r) < 1e-3, what
+        else:
+            np.testing.assert_allclose(g, r, atol=ATOL, rtol=RTOL, err_msg=what)
 
 
 def test_candidates_equal_full_logits():
