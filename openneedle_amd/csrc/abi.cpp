@@ -163,7 +163,8 @@ void CqHandle::gemv(const uint4 *codes, const uint16_t *norms, int rows, int n_p
 void matrix_gemv(const Matrix &m, Staging &st, const uint4 *codes, const uint16_t *norms, int rows, int n_pad,
                  const float *d_x, float *d_y, int batch, hipStream_t s) {
     const float *act = d_x;
-    if (!gemv_fuses_fwht(m.group)) {
+    const bool xraw = gemv_prepass(m.group) && gemv_quad_takes_x(m.group, m.in);  // the GEMV transforms x itself
+    if (!gemv_fuses_fwht(m.group) && !xraw) {
         st.rot.reserve(size_t(batch) * m.dev);
         if (gemv_prepass(m.group))
             launch_rot_many(d_x, nullptr, batch, batch, m.in, m.dev, m.group, m.scale, st.rot.p, s);
@@ -172,7 +173,7 @@ void matrix_gemv(const Matrix &m, Staging &st, const uint4 *codes, const uint16_
         act = st.rot.p;
     }
     const CqJob job{codes, norms, act, d_y, rows, n_pad, 0, batch};
-    launch_cq_gemv(m.geom(), job, nullptr, 0, n_pad / kRowsPerBlock, s);
+    launch_cq_gemv(m.geom(), job, nullptr, 0, n_pad / kRowsPerBlock, s, xraw);
 }
 
 void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s) {
@@ -421,6 +422,7 @@ void SdotHandle::linear_host(const float *x, float *y, int batch) {
 // ---------------------------------------------------------------------------
 struct Plan {
     bool sdot = false;
+    bool xraw = false;  // FP32, groups <= 64: the GEMV transforms the raw inputs itself
     int count = 0, batch = 1;
     std::vector<CqHandle *> cq;
     std::vector<SdotHandle *> sd;
@@ -443,7 +445,8 @@ static void plan_upload(Plan &p) {
     if (!p.sdot) {
         p.rot.reserve(size_t(p.count) * p.batch * m.dev);
         std::vector<CqJob> jobs(p.count);
-        const bool fused = gemv_fuses_fwht(m.group);
+        p.xraw = gemv_prepass(m.group) && gemv_quad_takes_x(m.group, m.in);
+        const bool fused = gemv_fuses_fwht(m.group) || p.xraw;
         for (int i = 0; i < p.count; ++i) {
             const Matrix &mi = p.cq[i]->m;
             const float *act = fused ? p.xs_in[i] : p.rot.p + size_t(i) * p.batch * m.dev;
@@ -489,13 +492,13 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
     // x_i is [batch][in] on the device; the FP32 GEMV transforms it in-kernel
     // unless the group exceeds one table window
     if (!p.sdot) {
-        if (gemv_prepass(m.group))
+        if (gemv_prepass(m.group) && !p.xraw)
             launch_rot_many(nullptr, p.xptr.p, p.batch, p.count * p.batch, m.in, m.dev, m.group, m.scale, p.rot.p, s);
-        else if (!gemv_fuses_fwht(m.group))
+        else if (!gemv_fuses_fwht(m.group) && !p.xraw)
             for (int i = 0; i < p.count; ++i)
                 m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
-        launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s);
+        launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s, p.xraw);
     } else {
         const SdotHandle &h0 = *p.sd[0];
         const SdotGeom g0 = h0.geom();
@@ -541,7 +544,8 @@ static void linear_many(const std::vector<CqHandle *> &hs, const float *x, float
     ND_HIP(hipMemcpyAsync(st.x.p, st.hx.p, size_t(m0.in) * sizeof(float), hipMemcpyHostToDevice, s));
     // the one transform: the shared rotated x, unless the GEMV fuses the FWHT into its table build
     const float *act = st.x.p;
-    if (!gemv_fuses_fwht(m0.group)) {
+    const bool xraw = gemv_prepass(m0.group) && gemv_quad_takes_x(m0.group, m0.in);  // the GEMV transforms x itself
+    if (!gemv_fuses_fwht(m0.group) && !xraw) {
         st.rot.reserve(m0.dev);
         if (gemv_prepass(m0.group)) launch_rot_many(st.x.p, nullptr, 1, 1, m0.in, m0.dev, m0.group, m0.scale, st.rot.p, s);
         else m0.transform(st.x.p, m0.in, st.rot.p, 1, st.big, s);
@@ -570,7 +574,7 @@ static void linear_many(const std::vector<CqHandle *> &hs, const float *x, float
         const int first = runs[r].first;
         const int njobs = (r + 1 < runs.size() ? runs[r + 1].first : n) - first;
         launch_cq_gemv(hs[first]->m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(st.jobs.p) + first, njobs,
-                       runs[r].second, s);
+                       runs[r].second, s, xraw);
     }
     ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, at[n] * sizeof(float), hipMemcpyDeviceToHost, s));
     ND_HIP(hipStreamSynchronize(s));

@@ -205,9 +205,12 @@ void launch_transform(const float *x, int x_stride, float *rot, int rot_stride, 
 void launch_rot_many(const float *x0, const float *const *xptr, int batch, int nvec, int in, int dev, int group,
                      float scale, float *rot, hipStream_t s);
 
-// njobs == 0: one job passed by value (job0); otherwise jobs_dev[0..njobs).
+// njobs == 0: one job passed by value (job0); otherwise jobs_dev[0..njobs). x_raw (groups <= 64): the jobs'
+// act is the raw input [batch][in], which the GEMV transforms itself (no launch_rot_many).
 void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs_dev, int njobs, int total_blocks,
-                    hipStream_t s);
+                    hipStream_t s, bool x_raw = false);
+// Whether callers give a group <= 64 GEMV of input width `in` the raw input instead of the pre-pass output.
+bool gemv_quad_takes_x(int group, int in);
 
 // Dequantize rows: y[i][0..in) = FWHT(cb[code]*norm) cropped; uses rot-sized scratch.
 // Candidate rows: output row i (< count) of a compact device-layout matrix of

@@ -13,6 +13,8 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 namespace nd {
 
@@ -878,6 +880,30 @@ __device__ __forceinline__ float2 quad_act(__amdgpu_buffer_rsrc_t rot, int w, in
     }
 }
 
+// The same values from the raw input row (XF): the thread loads its position(s)
+// of window w (zeros past the row, the reference's padding) and runs the group
+// FWHT as rot_many_kernel does: the stages in ascending order with the
+// reference's operands, each stride h < 64 between lanes (2-bit: stride 1
+// inside the lane, which holds positions 2m and 2m + 1, and stride h >= 2 with
+// lane l ^ h, since lanes 2m and 2m + 1 hold the same pair), then * scale.
+template <int KIND, int GROUP>
+__device__ __forceinline__ float2 quad_act_x(__amdgpu_buffer_rsrc_t x, int w, int r, float scale) {
+    const int lane = r & 63;
+    if constexpr (KIND == kNib) {
+        float v = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x, r * 4u, window_offset(w), 0));
+        wave_butterflies<GROUP, 1>(v, lane);
+        return make_float2(v * scale, 0.0f);
+    } else {
+        const float x0 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x, (r >> 1) * 8u, window_offset(w), 0));
+        const float x1 =
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x, (r >> 1) * 8u + 4u, window_offset(w), 0));
+        float a = x0 + x1, b = x0 - x1;
+        wave_butterflies<GROUP, 2>(a, lane);
+        wave_butterflies<GROUP, 2>(b, lane);
+        return make_float2(a * scale, b * scale);
+    }
+}
+
 // Quarter q's share of the table of one window: 4-bit slot r, codes 4q..4q+3;
 // 2-bit slot r/2, pair entries c0 | q << 2 for c0 = 2(r&1), 2(r&1)+1.
 template <int KIND, int GROUP>
@@ -965,7 +991,9 @@ __device__ __forceinline__ void quad_add_parked(const float *P, int r, float &su
         if (gbase + k < groups) sum += P[k * kRowsPerBlock + r];
 }
 
-template <int KIND, int GROUP, int QUAD>
+// XF: J.act is the raw input ([batch][in]), transformed here (quad_act_x),
+// instead of the pre-pass output ([batch][dev]).
+template <int KIND, int GROUP, int QUAD, bool XF>
 __device__ __forceinline__ void quad_rows(const CqJob &J, const CqGeom &geom, float (*T)[QuadShape<KIND, GROUP>::kFloats],
                                           float (*P)[(kQuads - 1) * QuadShape<KIND, GROUP>::kGroups * kRowsPerBlock],
                                           int blk) {
@@ -987,15 +1015,20 @@ __device__ __forceinline__ void quad_rows(const CqJob &J, const CqGeom &geom, fl
     for (int i = 0; i < 16; ++i) lut[i] = geom.lut[i];
 
     for (int b = 0; b < batch; ++b) {
+        const int stride = XF ? geom.in : dev;
         const __amdgpu_buffer_rsrc_t rot =
-            buffer_rsrc(J.act + static_cast<size_t>(b) * dev, static_cast<uint32_t>(dev) * 4u);
+            buffer_rsrc(J.act + static_cast<size_t>(b) * stride, static_cast<uint32_t>(stride) * 4u);
+        auto act = [&](int w) {
+            if constexpr (XF) return quad_act_x<KIND, GROUP>(rot, w, r, geom.scale);
+            else return quad_act<KIND>(rot, w, r);
+        };
         QuadState<KIND, GROUP> cur, nxt;
-        float2 xr = quad_act<KIND>(rot, 0, r);
+        float2 xr = act(0);
         quad_load<KIND, GROUP>(cur, codes, norms, 0, QUAD, r);
         quad_load<KIND, GROUP>(nxt, codes, norms, 1, QUAD, r);
         __syncthreads();  // the previous batch row finished with T[0] and P
         quad_build<KIND, GROUP>(T[0], lut, xr, QUAD, r);
-        xr = quad_act<KIND>(rot, 1, r);
+        xr = act(1);
         __syncthreads();
         float sum = 0.0f, gd = 0.0f;
         // Whole window pairs, then the last window if the count is odd; one
@@ -1012,12 +1045,12 @@ __device__ __forceinline__ void quad_rows(const CqJob &J, const CqGeom &geom, fl
             if (QUAD == 0 && it > 0) quad_add_parked<KIND, GROUP>(P[1], r, sum, w - 1, groups);
             quad_compute<KIND, GROUP, QUAD>(cur, T[0], P[0], r, mask, sum, gd, w, groups, codes, norms);
             quad_build<KIND, GROUP>(T[1], lut, xr, QUAD, r);
-            xr = quad_act<KIND>(rot, w + 2, r);
+            xr = act(w + 2);
             __syncthreads();
             if (QUAD == 0) quad_add_parked<KIND, GROUP>(P[0], r, sum, w, groups);
             quad_compute<KIND, GROUP, QUAD>(nxt, T[1], P[1], r, mask, sum, gd, w + 1, groups, codes, norms);
             quad_build<KIND, GROUP>(T[0], lut, xr, QUAD, r);
-            xr = quad_act<KIND>(rot, w + 3, r);
+            xr = act(w + 3);
             __syncthreads();
         }
         if (windows & 1) {
@@ -1033,7 +1066,7 @@ __device__ __forceinline__ void quad_rows(const CqJob &J, const CqGeom &geom, fl
     }
 }
 
-template <int KIND, int GROUP>
+template <int KIND, int GROUP, bool XF>
 __global__ __launch_bounds__(kQuadThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void cq_gemv_quad_kernel(
     CqJob job0, const CqJob *__restrict__ jobs, int njobs, CqGeom geom) {
     using Q = QuadShape<KIND, GROUP>;
@@ -1056,10 +1089,10 @@ __global__ __launch_bounds__(kQuadThreads) __attribute__((amdgpu_waves_per_eu(8,
     // one straight-line copy of the window loop per quarter (compile-time
     // table offsets; no mixing of the quarters' load bookkeeping)
     switch (__builtin_amdgcn_readfirstlane(threadIdx.x / kRowsPerBlock)) {
-    case 0: quad_rows<KIND, GROUP, 0>(J, geom, T, P, blk); break;
-    case 1: quad_rows<KIND, GROUP, 1>(J, geom, T, P, blk); break;
-    case 2: quad_rows<KIND, GROUP, 2>(J, geom, T, P, blk); break;
-    default: quad_rows<KIND, GROUP, 3>(J, geom, T, P, blk); break;
+    case 0: quad_rows<KIND, GROUP, 0, XF>(J, geom, T, P, blk); break;
+    case 1: quad_rows<KIND, GROUP, 1, XF>(J, geom, T, P, blk); break;
+    case 2: quad_rows<KIND, GROUP, 2, XF>(J, geom, T, P, blk); break;
+    default: quad_rows<KIND, GROUP, 3, XF>(J, geom, T, P, blk); break;
     }
 }
 
@@ -1080,14 +1113,14 @@ __global__ __launch_bounds__(kRowsPerBlock) void rot_many_kernel(const float *__
     if (p < dev) rot[static_cast<size_t>(v) * dev + p] = x[0];
 }
 
-template <int KIND>
+template <int KIND, bool XF>
 void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
     dim3 grid(blocks), block(kRowsPerBlock), split(kSplitThreads), quad(kQuadThreads);
     switch (g.group > kWindow ? 0 : g.group) {
-    case 8: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 8>), grid, quad, 0, s, job0, jobs, njobs, g); break;
-    case 16: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 16>), grid, quad, 0, s, job0, jobs, njobs, g); break;
-    case 32: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 32>), grid, quad, 0, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 64>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+    case 8: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 8, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+    case 16: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 16, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+    case 32: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 32, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 64, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
     case 128: hipLaunchKernelGGL((cq_gemv_split_kernel<KIND, 128>), grid, split, 0, s, job0, jobs, njobs, g); break;
     case 256: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
     default: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 0>), grid, block, 0, s, job0, jobs, njobs, g); break;
@@ -1234,10 +1267,30 @@ void launch_rot_many(const float *x0, const float *const *xptr, int batch, int n
     ND_HIP(hipGetLastError());
 }
 
-void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
+// The in-kernel transform repeats the group FWHT in every workgroup and quarter
+// (about +18% GEMV time on 8192-wide inputs, +7% on 512-wide ones), so it only
+// pays where saving the pre-pass launch outweighs that: inputs of at most two
+// windows (the 8192 x 512 device call: 10.2 -> 6.7 us). NEEDLE2_GPU_FP32_XF =
+// always / never overrides.
+bool gemv_quad_takes_x(int group, int in) {
+    if (group > 64) return false;
+    const char *mode = std::getenv("NEEDLE2_GPU_FP32_XF");
+    if (mode && std::strcmp(mode, "never") == 0) return false;
+    if (mode && std::strcmp(mode, "always") == 0) return true;
+    return in <= 2 * kWindow;
+}
+
+void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s,
+                    bool x_raw) {
     if (blocks <= 0) return;
-    if (g.kind == kNib) launch_gemv_kind<kNib>(g, job0, jobs, njobs, blocks, s);
-    else launch_gemv_kind<kCrumb>(g, job0, jobs, njobs, blocks, s);
+    ND_CHECK(!x_raw || g.group <= 64, "internal: raw GEMV input for a group the pre-pass does not serve");
+    if (x_raw) {
+        if (g.kind == kNib) launch_gemv_kind<kNib, true>(g, job0, jobs, njobs, blocks, s);
+        else launch_gemv_kind<kCrumb, true>(g, job0, jobs, njobs, blocks, s);
+        return;
+    }
+    if (g.kind == kNib) launch_gemv_kind<kNib, false>(g, job0, jobs, njobs, blocks, s);
+    else launch_gemv_kind<kCrumb, false>(g, job0, jobs, njobs, blocks, s);
 }
 
 void launch_gather_rows(const uint4 *codes, const uint16_t *norms, int rows, int chunks, int groups,

@@ -84,6 +84,7 @@ struct GemvGroup {
     int pieces = 0, per_token = 0;  // jobs and workgroups of one token
     const float *x = nullptr;
     CqJob job0{};
+    bool xraw = false;  // groups <= 64: the GEMV transforms the raw input itself
 
     static bool compatible(const Matrix &a, const Matrix &b) {
         return a.in == b.in && a.bits == b.bits && a.group == b.group &&
@@ -94,7 +95,8 @@ struct GemvGroup {
     void build(const std::vector<Piece> &ps, const float *input, int tokens) {
         m0 = ps[0].m;
         x = input;
-        const bool fused = gemv_fuses_fwht(m0->group);
+        xraw = gemv_prepass(m0->group) && gemv_quad_takes_x(m0->group, m0->in);
+        const bool fused = gemv_fuses_fwht(m0->group) || xraw;
         if (!fused) rot.reserve(size_t(m0->dev) * tokens);
         std::vector<CqJob> host;
         int blocks = 0;
@@ -121,7 +123,7 @@ struct GemvGroup {
     }
 
     void run(hipStream_t s, int tokens) {
-        if (!gemv_fuses_fwht(m0->group)) {
+        if (!gemv_fuses_fwht(m0->group) && !xraw) {
             if (gemv_prepass(m0->group))
                 launch_rot_many(x, nullptr, tokens, tokens, m0->in, m0->dev, m0->group, m0->scale, rot.p, s);
             else
@@ -129,9 +131,10 @@ struct GemvGroup {
         }
         const int njobs = pieces * tokens;
         if (njobs > 1)
-            launch_cq_gemv(m0->geom(), CqJob{}, reinterpret_cast<const CqJob *>(jobs.p), njobs, per_token * tokens, s);
+            launch_cq_gemv(m0->geom(), CqJob{}, reinterpret_cast<const CqJob *>(jobs.p), njobs, per_token * tokens, s,
+                           xraw);
         else
-            launch_cq_gemv(m0->geom(), job0, nullptr, 0, per_token, s);
+            launch_cq_gemv(m0->geom(), job0, nullptr, 0, per_token, s, xraw);
     }
 };
 

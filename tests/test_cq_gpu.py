@@ -56,13 +56,35 @@ def test_bounds_and_empty_batch():
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 5])
 @pytest.mark.parametrize("group", [8, 16, 32, 64, 128, 256, 512, 1024])
-@pytest.mark.parametrize("rows,dim", [(33, 200), (300, 1000)])
+@pytest.mark.parametrize("rows,dim", [(33, 200), (300, 1000), (70, 777)])
 def test_groups_and_ragged_shapes(bits, group, rows, dim):
     packed, norms, cb, dense = example(bits, rows=rows, dim=dim, group=group, seed=bits * 1000 + group)
     q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
     x = activations((3, dim), seed=group)
     expected = oracle.cq_linear(packed, norms, dense.shape, bits, group, cb, x, 4)
     check(q.matvec(x), expected, bits)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("group", [8, 16, 32, 64])
+@pytest.mark.parametrize("dim", [300, 777])
+def test_small_groups_with_and_without_prepass(bits, group, dim, monkeypatch):
+    """Groups of 8 .. 64: the quarter-split GEMV transforms the raw input itself (NEEDLE2_GPU_FP32_XF=always;
+    by default for inputs of at most 512) or reads the activation pre-pass (never; by default for wider
+    inputs); every mode bit-exact, through the host call and a plan."""
+    packed, norms, cb, dense = example(bits, rows=300, dim=dim, group=group, seed=bits * 77 + group)
+    x = activations((2, dim), seed=group + 5)
+    expected = oracle.cq_linear(packed, norms, dense.shape, bits, group, cb, x, 4)
+    for mode in ("always", "never", "auto"):
+        monkeypatch.setenv("NEEDLE2_GPU_FP32_XF", mode)
+        q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
+        check(q.matvec(x), expected, bits)
+        d_x = DeviceArray.from_host(np.ascontiguousarray(x[1]))
+        d_y = DeviceArray(4 * dense.shape[0])
+        plan = Plan([q], [d_x.ptr], [d_y.ptr])
+        plan.run()
+        synchronize()
+        check(d_y.download(np.empty(dense.shape[0], np.float32)), expected[1], bits)
 
 
 def test_huge_group_global_fwht():
