@@ -298,13 +298,28 @@ class DecodeLayer:
                 stream.synchronize()
         self.first = td.add(DeviceArray.from_host(np.full(seqs, cap - 1, np.int32)))  # the new token's slot
 
+    splits = 0  # attention slot-range pieces (0: automatic)
+
     def store(self):
         self.kv.store_device(0, self.buf["k"], self.buf["v"], 1, self.first, stream=self.stream)
 
-    def attention(self):
-        self.kv.attention(0, self.buf["q"], self.buf["a"], self.HEADS, self.CAP, stream=self.stream)
+    def attention(self, next=None):
+        self.kv.attention(0, self.buf["q"], self.buf["a"], self.HEADS, self.CAP, splits=self.splits,
+                          stream=self.stream, next=next)
 
     def step(self):
+        """Q|K|V, store, then the chain attention -> O -> up -> down: each producer leaves the next projection's
+        input prepared (in its epilogue where the shapes allow), so those plans launch no prepare kernel."""
+        p = self.plans
+        p["qkv"].run(self.stream)
+        self.store()
+        self.attention(next=p["o"])
+        p["o"].run(self.stream, prepared=True, next=p["up"])
+        p["up"].run(self.stream, prepared=True, next=p["down"])
+        p["down"].run(self.stream, prepared=True)
+
+    def unchained_step(self):
+        """The same step with every plan preparing its own input."""
         self.plans["qkv"].run(self.stream)
         self.store()
         self.attention()

@@ -183,6 +183,17 @@ int needle2_gpu_plan_run(void *plan, void *stream);
 /* needle2_gpu_plan_run, recording gemv_start/gemv_stop (hipEvent_t) on the
  * stream immediately before and after the GEMV launch. */
 int needle2_gpu_plan_run_timed(void *plan, void *stream, void *gemv_start, void *gemv_stop);
+/* Chained int8 plans (no counterpart in the reference, whose CPU layer runs
+ * each projection on its own; Engine::attention_projections_batch,
+ * needle2/csrc/engine.cpp:671-750, quantizes each input in turn): with
+ * `prepared` non-zero the run uses the prepared input a chained call of its
+ * producer left in its staging since its last run (and prepares its input
+ * itself when none did); with `next` not NULL (a one-matrix int8 plan whose
+ * input buffer is this plan's output) the run also leaves next's input
+ * prepared, in the GEMV epilogue for groups of 32 on decode-sized matrices,
+ * else by next's prepare launch, unless next's GEMV prepares its own input
+ * (batch 1). Outputs are the bits of unchained runs; one stream per chain. */
+int needle2_gpu_plan_run_chained(void *plan, void *next, int prepared, void *stream);
 void needle2_gpu_plan_destroy(void *plan);
 
 /* Device memory, streams and events (HIP runtime of this library). */
@@ -242,6 +253,13 @@ int needle2_gpu_kv_store_device(void *kv, int layer, const float *d_k, const flo
  * [0, capacity) are skipped. splits: slot-range pieces (0: automatic). */
 int needle2_gpu_attention(void *kv, int layer, const float *d_q, float *d_out, int heads, int length,
                           const int *d_slots, const int *d_lengths, int splits, void *stream);
+/* needle2_gpu_attention that also leaves d_out prepared as the input of
+ * `next` (a one-matrix int8 plan of batch seqs reading d_out, e.g. the O
+ * projection) for needle2_gpu_plan_run_chained(next, ..., prepared = 1); no
+ * counterpart in the reference (Engine::step quantizes the attention output
+ * inside the next linear, needle2/csrc/engine.cpp:968-1044). */
+int needle2_gpu_attention_chained(void *kv, int layer, const float *d_q, float *d_out, int heads, int length,
+                                  const int *d_slots, const int *d_lengths, int splits, void *next, void *stream);
 int needle2_gpu_kv_import(void *kv, int layer, int seq, const int8_t *k, const int8_t *v, const float *k_scales,
                           const float *v_scales, int first_slot, int count);
 int needle2_gpu_kv_export(void *kv, int layer, int seq, int8_t *k, int8_t *v, float *k_scales, float *v_scales,

@@ -74,6 +74,7 @@ SIGNATURES: dict[str, tuple] = {
     "needle2_gpu_sdot_plan_create": (vp, [vp, i32, vp, vp, i32]),
     "needle2_gpu_plan_run": (i32, [vp, vp]),
     "needle2_gpu_plan_run_timed": (i32, [vp, vp, vp, vp]),
+    "needle2_gpu_plan_run_chained": (i32, [vp, vp, i32, vp]),
     "needle2_gpu_plan_destroy": (None, [vp]),
     "needle2_gpu_malloc": (vp, [sz]),
     "needle2_gpu_free": (None, [vp]),
@@ -99,6 +100,7 @@ SIGNATURES: dict[str, tuple] = {
     "needle2_gpu_kv_store": (i32, [vp, i32, vp, vp, i32, i32, vp, vp]),
     "needle2_gpu_kv_store_device": (i32, [vp, i32, vp, vp, i32, vp, vp]),
     "needle2_gpu_attention": (i32, [vp, i32, vp, vp, i32, i32, vp, vp, i32, vp]),
+    "needle2_gpu_attention_chained": (i32, [vp, i32, vp, vp, i32, i32, vp, vp, i32, vp, vp]),
     "needle2_gpu_kv_import": (i32, [vp, i32, i32, vp, vp, vp, vp, i32, i32]),
     "needle2_gpu_kv_export": (i32, [vp, i32, i32, vp, vp, vp, vp, i32, i32]),
 }

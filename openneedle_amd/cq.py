@@ -298,9 +298,19 @@ class Plan:
         if not self.ptr:
             raise GpuError(f"plan: {_ffi.last_error()}")
 
-    def run(self, stream=None, gemv_events=None) -> None:
+    def run(self, stream=None, gemv_events=None, *, next=None, prepared: bool = False) -> None:
+        """One run on ``stream``. Chained int8 plans: with ``prepared`` the run uses the prepared input a chained
+        call of its producer (a run with ``next=self``, or :meth:`KVCache.attention` with ``next=self``) left
+        since this plan's last run, or prepares it itself when none did; ``next``, a one-matrix int8 plan whose
+        input is this plan's output, gets its input prepared for its own run with ``prepared=True``. Outputs
+        are those of unchained runs."""
         s = stream_ptr(stream)
-        if gemv_events is None:
+        if next is not None or prepared:
+            if gemv_events is not None:
+                raise ValueError("plan run: timing events are for unchained runs")
+            check(self._lib.needle2_gpu_plan_run_chained(self.ptr, next.ptr if next is not None else None,
+                                                         int(bool(prepared)), s), "plan run")
+        elif gemv_events is None:
             check(self._lib.needle2_gpu_plan_run(self.ptr, s), "plan run")
         else:
             check(self._lib.needle2_gpu_plan_run_timed(self.ptr, s, gemv_events[0].ptr, gemv_events[1].ptr),

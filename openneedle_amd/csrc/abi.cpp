@@ -436,6 +436,7 @@ struct Plan {
     int blocks = 0;
     const Matrix *first = nullptr;
     Staging st;
+    bool staged = false;  // a chained producer left this plan's prepared input since its last run
 };
 
 static void plan_upload(Plan &p) {
@@ -487,8 +488,68 @@ static void plan_upload(Plan &p) {
     ND_HIP(hipMemcpy(p.jobs.p, host.data(), host.size(), hipMemcpyHostToDevice));
 }
 
-static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hipEvent_t gemv_stop = nullptr) {
+// The int8 plan's input preparation: one launch prepares every (matrix,
+// batch row) input into the plan's staging (q, xscale, xscale_t).
+static void plan_prepare(Plan &p, hipStream_t s) {
     const Matrix &m = *p.first;
+    if (!launch_sdot_prepare(nullptr, p.xptr.p, p.batch, p.count * p.batch, m.in, m.padded, m.dev, m.group,
+                             m.scale, m.kind, p.q.p, p.xscale.p, p.xscale_t.p, s)) {
+        for (int i = 0; i < p.count; ++i)
+            m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
+        launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
+                             p.xscale.p, s);
+    }
+}
+
+// Where a producer of `x` (batch rows of n values) may leave `next`'s input
+// prepared: next is a one-matrix int8 plan of groups of 32 whose input is
+// exactly x. q null otherwise.
+PrepOut plan_prep_target(const void *next_plan, const float *x, int n, int batch) {
+    PrepOut po{};
+    if (!next_plan) return po;
+    const Plan &c = *static_cast<const Plan *>(next_plan);
+    const Matrix &m = *c.first;
+    ND_CHECK(c.sdot && c.count == 1, "chained run: the next plan must be a one-matrix int8 plan");
+    ND_CHECK(c.xs_in[0] == x, "chained run: the next plan's input must be this call's output");
+    ND_CHECK(m.in == n && c.batch == batch, "chained run: the next plan's input shape differs from this output");
+    if (m.group != 32) return po;
+    po.q = reinterpret_cast<int8_t *>(c.q.p);
+    po.xs = c.xscale.p;
+    po.xst = c.xscale_t.p;
+    po.dev = m.dev;
+    po.padded = m.padded;
+    po.groups = m.groups;
+    po.kind = m.kind;
+    po.batch = c.batch;
+    po.scale = m.scale;
+    return po;
+}
+
+// Whether the int8 plan's GEMV prepares its own input (batch 1, small
+// matrices), which then needs no producer to prepare it.
+static bool plan_takes_x(const Plan &p) { return p.sdot && sdot_gemv_takes_x(p.sd[0]->geom(), p.blocks, p.batch); }
+
+bool plan_wants_input(const void *next_plan) { return !plan_takes_x(*static_cast<const Plan *>(next_plan)); }
+
+void plan_prepare_input(void *next_plan, hipStream_t s) {
+    Plan &c = *static_cast<Plan *>(next_plan);
+    plan_prepare(c, s);
+    c.staged = true;
+}
+
+void plan_mark_staged(void *next_plan) { static_cast<Plan *>(next_plan)->staged = true; }
+
+// prepared: use the prepared input a chained producer call left in the
+// staging since this plan's last run (without one, the run prepares its
+// input itself). next: an int8 plan whose input is this plan's output, left
+// prepared for its run with `prepared` (in the GEMV's epilogue where the
+// shapes allow, else by its prepare launch; not at all when next's GEMV
+// prepares its own input).
+static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hipEvent_t gemv_stop = nullptr,
+                     Plan *next = nullptr, bool prepared = false) {
+    const Matrix &m = *p.first;
+    ND_CHECK(p.sdot || (!next && !prepared), "chained run: FP32 plans neither take nor leave prepared inputs");
+    ND_CHECK(!next || p.count == 1, "chained run: the producing plan must hold one matrix");
     // x_i is [batch][in] on the device; the FP32 GEMV transforms it in-kernel
     // unless the group exceeds one table window
     if (!p.sdot) {
@@ -499,25 +560,29 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
                 m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
         launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s, p.xraw);
-    } else {
-        const SdotHandle &h0 = *p.sd[0];
-        const SdotGeom g0 = h0.geom();
-        if (sdot_gemv_takes_x(g0, p.blocks, p.batch)) {  // batch 1, small matrices: the GEMV prepares its input
-            if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
-            launch_sdot_gemv_x(g0, SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, s);
-            if (gemv_stop) ND_HIP(hipEventRecord(gemv_stop, s));
-            return;
-        }
-        // one launch prepares every (matrix, batch row) input
-        if (!launch_sdot_prepare(nullptr, p.xptr.p, p.batch, p.count * p.batch, m.in, m.padded, m.dev, m.group,
-                                 m.scale, m.kind, p.q.p, p.xscale.p, p.xscale_t.p, s)) {
-            for (int i = 0; i < p.count; ++i)
-                m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
-            launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
-                                 p.xscale.p, s);
-        }
+        if (gemv_stop) ND_HIP(hipEventRecord(gemv_stop, s));
+        return;
+    }
+    const SdotGeom g0 = p.sd[0]->geom();
+    const SdotJob *jobs = reinterpret_cast<const SdotJob *>(p.jobs.p);
+    const bool staged = prepared && p.staged;
+    p.staged = false;
+    const PrepOut target = plan_prep_target(next, p.ys[0], m.out, p.batch);  // checks next
+    const bool feed = next && plan_wants_input(next);
+    const PrepOut po = feed ? target : PrepOut{};
+    if (!staged && plan_takes_x(p)) {  // batch 1, small matrices: the GEMV prepares its input
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
-        launch_sdot_gemv(g0, SdotJob{}, reinterpret_cast<const SdotJob *>(p.jobs.p), p.count, p.blocks, p.batch, s);
+        launch_sdot_gemv_x(g0, SdotJob{}, jobs, p.count, p.blocks, s);
+        if (feed) plan_prepare_input(next, s);
+    } else {
+        if (!staged) plan_prepare(p, s);
+        if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
+        if (launch_sdot_gemv_prep(g0, SdotJob{}, jobs, p.count, p.blocks, p.batch, po, s)) {
+            plan_mark_staged(next);
+        } else {
+            launch_sdot_gemv(g0, SdotJob{}, jobs, p.count, p.blocks, p.batch, s);
+            if (feed) plan_prepare_input(next, s);
+        }
     }
     if (gemv_stop) ND_HIP(hipEventRecord(gemv_stop, s));
 }
@@ -847,6 +912,22 @@ int needle2_gpu_plan_run_timed(void *plan, void *stream, void *gemv_start, void 
     return guarded([&] {
         plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream(), static_cast<hipEvent_t>(gemv_start),
                  static_cast<hipEvent_t>(gemv_stop));
+    });
+}
+
+// A run in a chain of int8 plans (a decode layer's O -> MLP up -> MLP down):
+// with `prepared` non-zero the plan uses the prepared input that a chained
+// call of its producer (this call or needle2_gpu_attention_chained with
+// `next` = this plan) left in its staging since its last run, and prepares
+// its input itself when none did; with `next` not NULL (a one-matrix int8
+// plan whose input buffer is this plan's output) the run also leaves next's
+// input prepared, for next's run with `prepared`. Outputs are the bits of
+// unchained runs. The calls of one chain go to one stream, in order.
+int needle2_gpu_plan_run_chained(void *plan, void *next, int prepared, void *stream) {
+    auto *p = static_cast<Plan *>(plan);
+    return guarded([&] {
+        plan_run(*p, stream ? static_cast<hipStream_t>(stream) : p->st.stream(), nullptr, nullptr,
+                 static_cast<Plan *>(next), prepared != 0);
     });
 }
 

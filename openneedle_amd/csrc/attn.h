@@ -35,6 +35,8 @@ struct AttnArgs {
     int slots_stride;      // sequence s's list starts at slots + s * slots_stride (0: one shared list)
     int shared_cache;      // nonzero: every sequence reads the same [kvheads][capacity] cache (the
                            // tokens of one prompt chunk, each with its own slot list)
+    PrepOut prep;          // q set (one split, heads * head_dim a multiple of 64): out is also left
+                           // prepared as the next int8 projection's input, sequence = batch row
 };
 
 bool attn_supported(int head_dim, int group);

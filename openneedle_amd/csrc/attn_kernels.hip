@@ -21,6 +21,7 @@
 // contiguous run): codes [layer][seq][kvh][capacity][HD] int8, scales
 // [layer][seq][kvh][capacity] fp32.
 #include "attn.h"
+#include "sdot_prepare.h"
 #include "wave.h"
 
 #include <cmath>
@@ -248,7 +249,17 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         }
         const size_t head = static_cast<size_t>(seq) * H + kh * G + g;
         if (a.splits == 1) {
-            a.out[head * HD + d] = lt > 0 ? o * (1.0f / lt) : 0.0f;
+            const float val = lt > 0 ? o * (1.0f / lt) : 0.0f;
+            a.out[head * HD + d] = val;
+            if (a.prep.q) {
+                // whole waves (G * HD is a multiple of 64) over consecutive positions of the sequence's
+                // output row: groups of 32 lanes are groups of the next projection's input
+                const PrepOut &po = a.prep;
+                const int p = (kh * G + g) * HD + d;
+                prepare_lane<32>(val, lane, p, po.padded, po.dev, po.scale, po.kind,
+                                 po.q + static_cast<size_t>(seq) * po.dev, po.xs + static_cast<size_t>(seq) * po.groups + p / 32,
+                                 po.xst + static_cast<size_t>(p / 32) * po.batch + seq);
+            }
         } else {
             float *rec = a.part + (head * a.splits + sp) * (HD + 2);
             rec[2 + d] = o;

@@ -186,6 +186,28 @@ struct SdotJob {
     const float *x;           // the fp32 input row (batch 1), for launch_sdot_gemv_x
 };
 
+// Where a kernel that produces the next int8 projection's input leaves it
+// prepared (the prepare kernel's outputs): q [batch][dev] permuted codes, xs
+// [batch][groups] and xst [groups][batch] scales, for groups of 32 positions.
+// q null: nothing to prepare.
+struct PrepOut {
+    int8_t *q;
+    float *xs, *xst;
+    int dev, padded, groups, kind, batch;
+    float scale;
+};
+
+// Chained int8 plans (abi.cpp): where a producer of `x` ([batch][n] on the
+// device) may leave next_plan's input prepared (q null: next_plan's group is
+// not 32; a plan that does not read exactly x is an error); whether
+// next_plan wants it prepared at all (false: its GEMV prepares its own
+// input); next_plan's own prepare launch, marking the input as left; and the
+// mark alone, after a producer kernel filled `plan_prep_target`.
+PrepOut plan_prep_target(const void *next_plan, const float *x, int n, int batch);
+bool plan_wants_input(const void *next_plan);
+void plan_prepare_input(void *next_plan, hipStream_t s);
+void plan_mark_staged(void *next_plan);
+
 // ---------------------------------------------------------------------------
 // Kernel launchers (implemented in the .hip files).
 // ---------------------------------------------------------------------------
@@ -239,6 +261,13 @@ void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded
 // The batch (uniform across jobs) is processed in tiles that decode each code once.
 void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs_dev, int njobs, int total_blocks,
                       int batch, hipStream_t s);
+// As launch_sdot_gemv for the K-split kernel's shapes (small matrices, batch
+// 2 and more, groups 32 .. 256), with 32-row workgroups whose outputs of each
+// batch row, one group of 32 positions of the next projection's input, are
+// also left prepared in `po` (a single job whose rows are that input's
+// positions). False, with nothing launched, for other shapes.
+bool launch_sdot_gemv_prep(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs_dev, int njobs,
+                           int total_blocks, int batch, const PrepOut &po, hipStream_t s);
 // Batch 1 on the small-matrix K-split kernel, which then prepares each job's input row (job.x) itself
 // (the prepare kernels' arithmetic) instead of reading q / xs: true when launch_sdot_gemv would run that
 // kernel for this shape and the prepared row fits its LDS (NEEDLE2_GPU_INT8_XIN=never: always false).

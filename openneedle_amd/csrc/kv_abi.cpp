@@ -173,15 +173,14 @@ int needle2_gpu_kv_store_device(void *h, int layer, const float *d_k, const floa
     });
 }
 
-// One decode-attention step of `layer` for every sequence.
-// d_q, d_out: device fp32 [seqs][heads][head_dim]; heads is a multiple of
-// kvheads (1, 2, 4 or 8 query heads per kv head). Sequence s attends the
-// slots d_slots[j] (device, at least `length` entries, nullable: j) for
-// j < d_lengths[s] (device, nullable: length); no sequence attends more than
-// `length` slots, and a listed slot outside [0, capacity) is skipped.
-// splits: pieces the slot range is cut into (0: chosen from the device).
-int needle2_gpu_attention(void *h, int layer, const float *d_q, float *d_out, int heads, int length,
-                          const int *d_slots, const int *d_lengths, int splits, void *stream) {
+// One decode-attention step (needle2_gpu_attention below); with `next` not NULL (a one-matrix int8 plan of
+// batch seqs whose input buffer is d_out, e.g. the O projection) d_out is
+// also left prepared as next's input, for needle2_gpu_plan_run_chained(next,
+// ..., prepared = 1): in the attention's epilogue for groups of 32 and one
+// split, else by next's prepare launch (not at all when next's GEMV prepares
+// its own input).
+int needle2_gpu_attention_chained(void *h, int layer, const float *d_q, float *d_out, int heads, int length,
+                                  const int *d_slots, const int *d_lengths, int splits, void *next, void *stream) {
     return guarded([&] {
         KvHandle &kv = *kv_of(h);
         check_layer(kv, layer);
@@ -216,8 +215,27 @@ int needle2_gpu_attention(void *h, int layer, const float *d_q, float *d_out, in
         a.splits = splits;
         a.slots_per_split = per;
         a.scale = 1 / std::sqrt(float(kv.head_dim));  // engine.cpp:914
+        const PrepOut po = plan_prep_target(next, d_out, heads * kv.head_dim, kv.seqs);
+        const bool feed = next && plan_wants_input(next);  // not when next's GEMV prepares its own input
+        const bool fused = feed && po.q && splits == 1 && group * kv.head_dim % 64 == 0;
+        if (fused) a.prep = po;
         launch_attention(a, group, s);
+        if (fused) plan_mark_staged(next);
+        else if (feed) plan_prepare_input(next, s);
     });
+}
+
+// One decode-attention step of `layer` for every sequence.
+// d_q, d_out: device fp32 [seqs][heads][head_dim]; heads is a multiple of
+// kvheads (1, 2, 4 or 8 query heads per kv head). Sequence s attends the
+// slots d_slots[j] (device, at least `length` entries, nullable: j) for
+// j < d_lengths[s] (device, nullable: length); no sequence attends more than
+// `length` slots, and a listed slot outside [0, capacity) is skipped.
+// splits: pieces the slot range is cut into (0: chosen from the device).
+int needle2_gpu_attention(void *h, int layer, const float *d_q, float *d_out, int heads, int length,
+                          const int *d_slots, const int *d_lengths, int splits, void *stream) {
+    return needle2_gpu_attention_chained(h, layer, d_q, d_out, heads, length, d_slots, d_lengths, splits, nullptr,
+                                         stream);
 }
 
 // Copy host rows in the reference's layout ([count][kvheads][head_dim] int8,

@@ -1356,25 +1356,35 @@ void launch_sdot_ks(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs,
 // them in LDS; after one barrier wave r (< 4) adds register r's kKs terms in
 // group order, so every output is value += term_g for g = 0, 1, 2, ... as
 // the reference sums: bit-identical outputs.
+//
+// MB = 2 (PREP): a workgroup takes 32 weight rows (two 16-row blocks, every
+// wave two MFMA chains sharing the activation operand) and, with PREP, turns
+// its 32 outputs of each batch row - one whole group of 32 positions of the
+// next projection's input - into that projection's prepared input as the
+// prepare kernel would from the stored outputs (prepare_lane: FWHT, absmax,
+// quantiser; same bits), so the next plan launches no prepare kernel.
 // ---------------------------------------------------------------------------
-template <int GROUP>
+template <int GROUP, int MB>
 struct Ks16Slot {
     static constexpr int kSteps = GROUP / 32;
-    uint32_t code[kSteps];  // the code dword of each step holding positions 8t .. 8t + 7, weight row j
-    uint32_t q[2 * kSteps];  // batch row j's activation dwords 2t, 2t + 1 of each step
-    float xs[4];             // scales of batch rows 4t .. 4t + 3
-    uint16_t norm;           // weight row j's group norm
+    uint32_t code[MB][kSteps];  // per row block: the code dword of each step holding positions 8t .. 8t + 7, weight row j
+    uint32_t q[2 * kSteps];     // batch row j's activation dwords 2t, 2t + 1 of each step
+    float xs[4];                // scales of batch rows 4t .. 4t + 3
+    uint16_t norm[MB];          // weight row j's group norm, per row block
 };
 
-template <int KIND, int GROUP>
+template <int KIND, int GROUP, int MB, bool PREP>
 __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
-                                                             int njobs, SdotGeom geom) {
-    using S = Ks16Slot<GROUP>;
-    __shared__ float park[2][kKs][4][64];
+                                                             int njobs, SdotGeom geom, PrepOut po) {
+    static_assert(MB == 1 || MB == 2, "one or two 16-row blocks");
+    static_assert(!PREP || MB == 2, "the prepared groups are 32 outputs");
+    using S = Ks16Slot<GROUP, MB>;
+    constexpr int RB = 16 * MB;  // weight rows per workgroup
+    __shared__ float park[2][kKs][4 * MB][64];
     const int lane = threadIdx.x & 63, jr = lane & 15, t = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    const int rb = blockIdx.x;  // 16-row block across the plan
-    const int blk = rb / (kRowsPerBlock / 16);
+    const int rb = blockIdx.x;  // RB-row block across the plan
+    const int blk = rb / (kRowsPerBlock / RB);
     SdotJob J0 = job0;
     if (njobs > 0) {
         const ND_CONST SdotJob *cj = (const ND_CONST SdotJob *)(jobs);
@@ -1391,8 +1401,7 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
     }
     const int rows = J0.rows, batch = J0.batch;
     const int tile = blk - J0.block_begin;
-    const int rt = (rb % (kRowsPerBlock / 16)) * 16 + jr;  // this lane's weight row within the tile
-    const int row = tile * kRowsPerBlock + rt;
+    const int rbase = (rb % (kRowsPerBlock / RB)) * RB;  // the workgroup's first weight row within the tile
     const int b0 = static_cast<int>(blockIdx.y) * 16;
     const int nb = min(16, batch - b0);
     const int groups = geom.groups;
@@ -1409,15 +1418,23 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
                                                  static_cast<uint32_t>(nb) * dev);
     const __amdgpu_buffer_rsrc_t xst = buffer_rsrc(J0.xst, static_cast<uint32_t>(groups) * batch * 4u);
     // code byte offset of this lane's dword within a 16-byte chunk (4-bit: one step per chunk; 2-bit: the
-    // step's half of a 64-position chunk is added per step)
-    const uint32_t qv = static_cast<uint32_t>(jr) * dev + 8u * t, nv = rt * 2u;
-    const uint32_t cv = rt * 16u + (KIND == kNib ? 4u * t : 4u * (t >> 1));
+    // step's half of a 64-position chunk is added per step), per row block
+    const uint32_t qv = static_cast<uint32_t>(jr) * dev + 8u * t;
+    uint32_t cv[MB], nv[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+        const int rt = rbase + 16 * m + jr;
+        cv[m] = rt * 16u + (KIND == kNib ? 4u * t : 4u * (t >> 1));
+        nv[m] = rt * 2u;
+    }
     auto load = [&](S &sl, int g) {  // g < groups
 #pragma unroll
         for (int st = 0; st < S::kSteps; ++st) {
             const int c = g * S::kSteps + st;  // step of 32 positions
             const int so = KIND == kNib ? c * kRowsPerBlock * 16 : (c >> 1) * kRowsPerBlock * 16 + (c & 1) * 8;
-            sl.code[st] = __builtin_amdgcn_raw_buffer_load_b32(codes, cv, __builtin_amdgcn_readfirstlane(so), 0);
+#pragma unroll
+            for (int m = 0; m < MB; ++m)
+                sl.code[m][st] = __builtin_amdgcn_raw_buffer_load_b32(codes, cv[m], __builtin_amdgcn_readfirstlane(so), 0);
             const auto v = __builtin_amdgcn_raw_buffer_load_b64(q, qv + c * 32u, 0, 0);
             sl.q[2 * st] = v[0];
             sl.q[2 * st + 1] = v[1];
@@ -1427,52 +1444,79 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             sl.xs[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xst, min(b0 + 4 * t + k, batch - 1) * 4u, so, 0));
-        sl.norm = __builtin_amdgcn_raw_buffer_load_b16(norms, nv, __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2), 0);
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+            sl.norm[m] = __builtin_amdgcn_raw_buffer_load_b16(norms, nv[m], __builtin_amdgcn_readfirstlane(g * kRowsPerBlock * 2), 0);
     };
-    float value = 0.0f;  // wave w < 4: batch row 4t + w, weight row rt
+    // wave w < 4 MB sums accumulator register w % 4 of row block w / 4: batch row 4t + w % 4, weight row
+    // rbase + 16 (w / 4) + jr
+    float value = 0.0f;
     const int rounds = (groups + kKs - 1) / kKs;
     S cur, nxt;
     load(cur, min(w, groups - 1));
     for (int r = 0; r < rounds; ++r) {
         load(nxt, min((r + 1) * kKs + w, groups - 1));  // past the last group: re-read, never used
-        v4i acc = {0, 0, 0, 0};
+        v4i acc[MB];
+#pragma unroll
+        for (int m = 0; m < MB; ++m) acc[m] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int st = 0; st < S::kSteps; ++st) {
-            uint32_t ce, co;
-            if constexpr (KIND == kNib) {
-                decode_nib(cur.code[st], cent[0], cent[1], cent[2], cent[3], ce, co);
-            } else {  // crumb selectors 2 (t % 2) and 2 (t % 2) + 1 of the dword
-                const uint32_t wd = cur.code[st] >> (4 * (t & 1));
-                ce = __builtin_amdgcn_perm(0u, cent[0], wd & 0x03030303u);
-                co = __builtin_amdgcn_perm(0u, cent[0], (wd >> 2) & 0x03030303u);
-            }
             const long a = static_cast<long>(cur.q[2 * st]) | (static_cast<long>(cur.q[2 * st + 1]) << 32);
-            const long b = static_cast<long>(ce) | (static_cast<long>(co) << 32);
-            acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, acc, 0, 0, 0);
-        }
-        const float ns = h2f(cur.norm) * cs;  // sdot.cpp:43-44
 #pragma unroll
-        for (int k = 0; k < 4; ++k) park[r & 1][w][k][lane] = (static_cast<float>(acc[k]) * ns) * cur.xs[k];
+            for (int m = 0; m < MB; ++m) {
+                uint32_t ce, co;
+                if constexpr (KIND == kNib) {
+                    decode_nib(cur.code[m][st], cent[0], cent[1], cent[2], cent[3], ce, co);
+                } else {  // crumb selectors 2 (t % 2) and 2 (t % 2) + 1 of the dword
+                    const uint32_t wd = cur.code[m][st] >> (4 * (t & 1));
+                    ce = __builtin_amdgcn_perm(0u, cent[0], wd & 0x03030303u);
+                    co = __builtin_amdgcn_perm(0u, cent[0], (wd >> 2) & 0x03030303u);
+                }
+                const long b = static_cast<long>(ce) | (static_cast<long>(co) << 32);
+                acc[m] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, acc[m], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+            const float ns = h2f(cur.norm[m]) * cs;  // sdot.cpp:43-44
+#pragma unroll
+            for (int k = 0; k < 4; ++k) park[r & 1][w][4 * m + k][lane] = (static_cast<float>(acc[m][k]) * ns) * cur.xs[k];
+        }
         __syncthreads();
         const int live = min(kKs, groups - r * kKs);  // groups of this round (uniform)
-        if (w < 4)
+        if (w < 4 * MB)
             for (int src = 0; src < live; ++src) value = value + park[r & 1][src][w][lane];
         cur = nxt;
     }
-    const int m = b0 + 4 * t + w;
-    if (w < 4 && row < rows && m < batch)
+    const int row = tile * kRowsPerBlock + rbase + 16 * (w / 4) + jr;
+    const int m = b0 + 4 * t + (w % 4);
+    if (w < 4 * MB && row < rows && m < batch)
         ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * (J0.ystride ? J0.ystride : rows) + row] = value;
+    if constexpr (PREP) {
+        // the 16 x 32 outputs through LDS (rows past the matrix as the zeros the prepare kernel pads with),
+        // then wave w prepares batch rows 2w (lanes 0-31) and 2w + 1 (lanes 32-63) of the group
+        __shared__ float yl[16][33];
+        yl[4 * t + (w % 4)][16 * (w / 4) + jr] = row < rows ? value : 0.0f;
+        __syncthreads();
+        const int bl = 2 * w + (lane >> 5), pos = lane & 31;
+        const int b = b0 + bl;
+        const int p = tile * kRowsPerBlock + rbase + pos;  // position in the next projection's input row
+        const int gi = p / 32;
+        const size_t bs = static_cast<size_t>(b < batch ? b : 0);
+        prepare_lane<32>(yl[bl][pos], lane, p, po.padded, po.dev, po.scale, po.kind, po.q + bs * po.dev,
+                         po.xs + bs * po.groups + gi, po.xst + static_cast<size_t>(gi) * po.batch + bs, b < batch);
+    }
 }
 
-template <int KIND>
+template <int KIND, int MB, bool PREP>
 void launch_sdot_ks16_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
-                           int batch, hipStream_t s) {
-    dim3 grid(blocks * (kRowsPerBlock / 16), (batch + 15) / 16), block(kKs * 64);
+                           int batch, const PrepOut &po, hipStream_t s) {
+    dim3 grid(blocks * (kRowsPerBlock / (16 * MB)), (batch + 15) / 16), block(kKs * 64);
     switch (g.group) {
-    case 32: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 32>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 64>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 128>), grid, block, 0, s, job0, jobs, njobs, g); break;
-    default: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
+    case 32: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 32, MB, PREP>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
+    case 64: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 64, MB, PREP>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
+    case 128: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 128, MB, PREP>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
+    default: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 256, MB, PREP>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
     }
     ND_HIP(hipGetLastError());
 }
@@ -1480,8 +1524,9 @@ void launch_sdot_ks16_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob
 bool launch_sdot_ks16(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
                       hipStream_t s) {
     if (g.group < 32 || g.group > kWindow) return false;
-    if (g.kind == kNib) launch_sdot_ks16_kind<kNib>(g, job0, jobs, njobs, blocks, batch, s);
-    else launch_sdot_ks16_kind<kCrumb>(g, job0, jobs, njobs, blocks, batch, s);
+    const PrepOut none{};
+    if (g.kind == kNib) launch_sdot_ks16_kind<kNib, 1, false>(g, job0, jobs, njobs, blocks, batch, none, s);
+    else launch_sdot_ks16_kind<kCrumb, 1, false>(g, job0, jobs, njobs, blocks, batch, none, s);
     return true;
 }
 
@@ -1663,6 +1708,15 @@ void launch_sdot_gemv_x(const SdotGeom &g, const SdotJob &job0, const SdotJob *j
     ND_CHECK(sdot_gemv_takes_x(g, blocks, 1), "internal: int8 GEMV with in-kernel prepare outside its shapes");
     if (g.kind == kNib) launch_sdot_ks_j<kNib, 1, true>(g, job0, jobs, njobs, blocks, 1, s);
     else launch_sdot_ks_j<kCrumb, 1, true>(g, job0, jobs, njobs, blocks, 1, s);
+}
+
+bool launch_sdot_gemv_prep(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
+                           int batch, const PrepOut &po, hipStream_t s) {
+    if (blocks <= 0 || batch <= 0 || !po.q || g.group < 32 || g.group > kWindow) return false;
+    if (!ks_chosen(g, blocks, batch) || !ks16_chosen(g, batch)) return false;
+    if (g.kind == kNib) launch_sdot_ks16_kind<kNib, 2, true>(g, job0, jobs, njobs, blocks, batch, po, s);
+    else launch_sdot_ks16_kind<kCrumb, 2, true>(g, job0, jobs, njobs, blocks, batch, po, s);
+    return true;
 }
 
 void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,

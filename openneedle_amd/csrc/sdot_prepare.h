@@ -25,10 +25,12 @@ __device__ __forceinline__ int permuted_index(int kind, int p) {
 // an all-zero group, absmax if the quotient underflows; q = clamp(rint(x /
 // scale), +-127) with IEEE division). The group's first lane stores the scale
 // at *xs (and *xst when not null); q goes to qv (the vector's row of dev
-// bytes) in the permuted order. Past `padded` a position stores zero.
+// bytes) in the permuted order. Past `padded` a position stores zero. With
+// `store` false the lane takes part in the group's arithmetic and stores
+// nothing.
 template <int GROUP>
 __device__ __forceinline__ void prepare_lane(float r, int t, int p, int padded, int dev, float scale, int kind,
-                                             int8_t *qv, float *xs, float *xst) {
+                                             int8_t *qv, float *xs, float *xst, bool store = true) {
     wave_butterflies<GROUP, 1>(r, t);
     r = r * scale;
     const float absmax = group_max<GROUP>(fabsf(r), t);
@@ -36,7 +38,7 @@ __device__ __forceinline__ void prepare_lane(float r, int t, int p, int padded, 
     if (p < padded) {
         float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
         if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
-        if (p % GROUP == 0) {
+        if (store && p % GROUP == 0) {
             *xs = sc;
             if (xst) *xst = sc;
         }
@@ -44,7 +46,7 @@ __device__ __forceinline__ void prepare_lane(float r, int t, int p, int padded, 
         val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
         out = static_cast<int8_t>(val);
     }
-    if (p < dev) qv[permuted_index(kind, p)] = out;
+    if (store && p < dev) qv[permuted_index(kind, p)] = out;
 }
 
 // Lane t holds positions base + t + 64 k (k < GROUP / 64) of its wave's group

@@ -10,13 +10,20 @@ oracle on the stage's own GPU input:
   of about 3.2 (scores about 3x those of tests/test_attention_gpu.py, where the per-output 1e-6 + 1e-5 bar
   holds); on such inputs the oracle's own sequential fp32 arithmetic reaches 4.8e-6 normwise and
   1.7e-6 * max|v| per output against fp64, so the bars are about twice the reference's own error;
-- the slots before the new token are untouched by the step."""
+- the slots before the new token are untouched by the step.
+
+The step runs the projections after the attention as a chain (each producer leaves the next plan's input
+prepared); the chained step's outputs equal the unchained step's bit for bit, with the preparation fused into
+the producers' epilogues and with the fallback prepare launches (other batch sizes, the attention split, the
+16 x 16 K split switched off)."""
 import numpy as np
 import pytest
 
 import bench
 import oracle
-from openneedle_amd.device import Stream, Teardown, synchronize
+from openneedle_amd._ffi import GpuError
+from openneedle_amd.cq import Plan
+from openneedle_amd.device import DeviceArray, Stream, Teardown, synchronize
 
 pytestmark = pytest.mark.gpu
 
@@ -79,3 +86,60 @@ def test_decode_layer_b64_against_oracle():
         for s, old in zip((0, 37, 63), before):
             for a, b in zip(layer.kv.read(0, s, L.CAP - 1), old):
                 np.testing.assert_array_equal(a, b, err_msg=f"seq {s}: older slots changed")
+
+
+@pytest.mark.parametrize("seqs,splits,ks16", [(64, 0, "auto"), (20, 0, "auto"), (64, 2, "auto"), (64, 0, "never"),
+                                              (1, 0, "auto")])
+def test_chained_step_equals_unchained(seqs, splits, ks16, monkeypatch):
+    """Chained runs (fused epilogue preparation, or the fallback prepare launches) give the unchained bits."""
+    if ks16 != "auto":
+        monkeypatch.setenv("NEEDLE2_GPU_INT8_KS16", ks16)
+    with Teardown() as td:
+        stream = td.add(Stream())
+        layer = bench.DecodeLayer(seqs, td, stream)
+        layer.splits = splits
+        outs = {}
+        for mode in ("unchained", "chained", "unchained"):
+            for n in ("a", "o", "u", "d"):  # stale outputs would hide a missing write
+                layer.buf[n].upload(np.full((seqs, layer.widths[n]), np.nan, np.float32))
+            (layer.step if mode == "chained" else layer.unchained_step)()
+            synchronize()
+            outs.setdefault(mode, []).append({n: layer.download(n) for n in ("q", "k", "v", "a", "o", "u", "d")})
+        for n in outs["chained"][0]:
+            np.testing.assert_array_equal(outs["chained"][0][n], outs["unchained"][0][n], err_msg=n)
+            np.testing.assert_array_equal(outs["unchained"][1][n], outs["unchained"][0][n], err_msg=n)
+
+
+@pytest.mark.parametrize("seqs", [1, 64])
+def test_prepared_run_without_a_producer_prepares_itself(seqs):
+    """A run with prepared=True that no chained producer call preceded (or whose producer's input was used by
+    an earlier run) prepares its own input: the unchained bits."""
+    with Teardown() as td:
+        stream = td.add(Stream())
+        layer = bench.DecodeLayer(seqs, td, stream)
+        layer.unchained_step()
+        synchronize()
+        want = layer.download("o")
+        layer.buf["o"].upload(np.full((seqs, 512), np.nan, np.float32))
+        layer.plans["o"].run(stream, prepared=True)
+        synchronize()
+        np.testing.assert_array_equal(layer.download("o"), want)
+        layer.step()  # chained: o's staged input is used by this step's o run ...
+        layer.buf["o"].upload(np.full((seqs, 512), np.nan, np.float32))
+        layer.plans["o"].run(stream, prepared=True)  # ... so this run prepares again
+        synchronize()
+        np.testing.assert_array_equal(layer.download("o"), want)
+
+
+def test_chained_run_refuses_a_plan_not_reading_the_output():
+    with Teardown() as td:
+        stream = td.add(Stream())
+        layer = bench.DecodeLayer(4, td, stream)
+        other = td.add(DeviceArray(4 * 512 * 4))
+        stray = td.add(Plan([layer.mats["wu"]], [other], [layer.buf["u"]], batch=4, int8=True))
+        with pytest.raises(GpuError, match="next plan's input"):
+            layer.plans["o"].run(stream, prepared=False, next=stray)
+        with pytest.raises(GpuError, match="next plan's input"):
+            layer.attention(next=stray)
+        with pytest.raises(GpuError, match="one-matrix"):
+            layer.plans["o"].run(stream, next=layer.plans["qkv"])
