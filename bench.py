@@ -303,17 +303,18 @@ class DecodeLayer:
     def store(self):
         self.kv.store_device(0, self.buf["k"], self.buf["v"], 1, self.first, stream=self.stream)
 
-    def attention(self, next=None):
+    def attention(self, next=None, store=False):
+        new = (self.buf["k"], self.buf["v"], self.first) if store else None
         self.kv.attention(0, self.buf["q"], self.buf["a"], self.HEADS, self.CAP, splits=self.splits,
-                          stream=self.stream, next=next)
+                          stream=self.stream, next=next, new=new)
 
     def step(self):
-        """Q|K|V, store, then the chain attention -> O -> up -> down: each producer leaves the next projection's
-        input prepared (in its epilogue where the shapes allow), so those plans launch no prepare kernel."""
+        """Q|K|V, then the attention storing the new token first, then the chain O -> up -> down: each producer
+        leaves the next projection's input prepared (in its epilogue where the shapes allow), so those plans
+        launch no prepare kernel, and the store runs inside the attention launch."""
         p = self.plans
         p["qkv"].run(self.stream)
-        self.store()
-        self.attention(next=p["o"])
+        self.attention(next=p["o"], store=True)
         p["o"].run(self.stream, prepared=True, next=p["up"])
         p["up"].run(self.stream, prepared=True, next=p["down"])
         p["down"].run(self.stream, prepared=True)

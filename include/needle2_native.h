@@ -253,13 +253,18 @@ int needle2_gpu_kv_store_device(void *kv, int layer, const float *d_k, const flo
  * [0, capacity) are skipped. splits: slot-range pieces (0: automatic). */
 int needle2_gpu_attention(void *kv, int layer, const float *d_q, float *d_out, int heads, int length,
                           const int *d_slots, const int *d_lengths, int splits, void *stream);
-/* needle2_gpu_attention that also leaves d_out prepared as the input of
- * `next` (a one-matrix int8 plan of batch seqs reading d_out, e.g. the O
- * projection) for needle2_gpu_plan_run_chained(next, ..., prepared = 1); no
- * counterpart in the reference (Engine::step quantizes the attention output
- * inside the next linear, needle2/csrc/engine.cpp:968-1044). */
+/* needle2_gpu_attention that first stores the step's new token of every
+ * sequence (d_new_k / d_new_v [seqs][kvheads][head_dim] fp32 at slot
+ * d_new_slot[s]: needle2_gpu_kv_store_device with count 1; all three NULL:
+ * no store) and also leaves d_out prepared as the input of `next` (NULL, or
+ * a one-matrix int8 plan of batch seqs reading d_out, e.g. the O projection)
+ * for needle2_gpu_plan_run_chained(next, ..., prepared = 1). Both in the
+ * attention launch where its shapes allow. Counterpart of the store-then-
+ * attend order of Engine::step (needle2/csrc/engine.cpp:1005-1021, 898-967),
+ * whose next linear quantizes the attention output itself. */
 int needle2_gpu_attention_chained(void *kv, int layer, const float *d_q, float *d_out, int heads, int length,
-                                  const int *d_slots, const int *d_lengths, int splits, void *next, void *stream);
+                                  const int *d_slots, const int *d_lengths, int splits, const float *d_new_k,
+                                  const float *d_new_v, const int *d_new_slot, void *next, void *stream);
 int needle2_gpu_kv_import(void *kv, int layer, int seq, const int8_t *k, const int8_t *v, const float *k_scales,
                           const float *v_scales, int first_slot, int count);
 int needle2_gpu_kv_export(void *kv, int layer, int seq, int8_t *k, int8_t *v, float *k_scales, float *v_scales,

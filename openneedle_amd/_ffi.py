@@ -100,7 +100,7 @@ SIGNATURES: dict[str, tuple] = {
     "needle2_gpu_kv_store": (i32, [vp, i32, vp, vp, i32, i32, vp, vp]),
     "needle2_gpu_kv_store_device": (i32, [vp, i32, vp, vp, i32, vp, vp]),
     "needle2_gpu_attention": (i32, [vp, i32, vp, vp, i32, i32, vp, vp, i32, vp]),
-    "needle2_gpu_attention_chained": (i32, [vp, i32, vp, vp, i32, i32, vp, vp, i32, vp, vp]),
+    "needle2_gpu_attention_chained": (i32, [vp, i32, vp, vp, i32, i32, vp, vp, i32, vp, vp, vp, vp, vp]),
     "needle2_gpu_kv_import": (i32, [vp, i32, i32, vp, vp, vp, vp, i32, i32]),
     "needle2_gpu_kv_export": (i32, [vp, i32, i32, vp, vp, vp, vp, i32, i32]),
 }

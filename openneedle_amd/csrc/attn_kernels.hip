@@ -30,6 +30,31 @@ namespace nd {
 
 namespace {
 
+// One K row and one V row of HD values into the cache, by one wave.
+__device__ __forceinline__ void store_kv_row(const float *k, const float *v, int HD, int lane, int8_t *k8, int8_t *v8,
+                                             float *ks, float *vs) {
+    float mk = 0.0f, mv = 0.0f;
+    for (int d = lane; d < HD; d += 64) {
+        mk = fmaxf(mk, fabsf(k[d]));
+        mv = fmaxf(mv, fabsf(v[d]));
+    }
+    mk = wave_max(mk, lane);
+    mv = wave_max(mv, lane);
+    const float sk = mk > 0 ? mk / 127.0f : 1.0f, sv = mv > 0 ? mv / 127.0f : 1.0f;
+    const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
+    if (lane == 0) {
+        *ks = sk;
+        *vs = sv;
+    }
+    for (int d = lane; d < HD; d += 64) {
+        float qk = rintf(k[d] * ik), qv = rintf(v[d] * iv);
+        qk = fmaxf(-127.0f, fminf(127.0f, qk));
+        qv = fmaxf(-127.0f, fminf(127.0f, qv));
+        k8[d] = static_cast<int8_t>(qk);
+        v8[d] = static_cast<int8_t>(qv);
+    }
+}
+
 // One wave per (sequence, token, kv head) row; K and V rows together.
 __global__ __launch_bounds__(256) void kv_store_kernel(KvStoreArgs a) {
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
@@ -44,26 +69,8 @@ __global__ __launch_bounds__(256) void kv_store_kernel(KvStoreArgs a) {
     const size_t src = static_cast<size_t>(wave) * a.head_dim;
     const size_t dst_row = (static_cast<size_t>(seq) * a.kvheads + kh) * a.capacity + slot;
     const int HD = a.head_dim;
-    float mk = 0.0f, mv = 0.0f;
-    for (int d = lane; d < HD; d += 64) {
-        mk = fmaxf(mk, fabsf(a.k[src + d]));
-        mv = fmaxf(mv, fabsf(a.v[src + d]));
-    }
-    mk = wave_max(mk, lane);
-    mv = wave_max(mv, lane);
-    const float sk = mk > 0 ? mk / 127.0f : 1.0f, sv = mv > 0 ? mv / 127.0f : 1.0f;
-    const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
-    if (lane == 0) {
-        a.ks[dst_row] = sk;
-        a.vs[dst_row] = sv;
-    }
-    for (int d = lane; d < HD; d += 64) {
-        float qk = rintf(a.k[src + d] * ik), qv = rintf(a.v[src + d] * iv);
-        qk = fmaxf(-127.0f, fminf(127.0f, qk));
-        qv = fmaxf(-127.0f, fminf(127.0f, qv));
-        a.k8[dst_row * HD + d] = static_cast<int8_t>(qk);
-        a.v8[dst_row * HD + d] = static_cast<int8_t>(qv);
-    }
+    store_kv_row(a.k + src, a.v + src, HD, lane, a.k8 + dst_row * HD, a.v8 + dst_row * HD, a.ks + dst_row,
+                 a.vs + dst_row);
 }
 
 __device__ __forceinline__ float i8f(uint32_t w, int c) {
@@ -209,11 +216,33 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         asm volatile("" ::: "memory");
     };
 
+    // With a new token (one block per (sequence, kv head): one split, no slot
+    // list), wave 0 first stores its K and V rows at slot new_slot[seq] as
+    // kv_store_kernel does; the block barrier (a workgroup-scope release and
+    // acquire) orders those stores before the block's loads of that slot.
+    // When the slot lies past the waves' first sub-tiles, those loads are
+    // issued before the store.
+    auto store_new = [&](int ns) {
+        if (wave == 0 && ns >= 0 && static_cast<uint32_t>(ns) < cap) {
+            const size_t src = (static_cast<size_t>(seq) * a.kvheads + kh) * HD;
+            const size_t dst = row0 + ns;
+            // the cache rows this call writes (the block's own context)
+            store_kv_row(a.new_k + src, a.new_v + src, HD, lane, const_cast<int8_t *>(a.k8) + dst * HD,
+                         const_cast<int8_t *>(a.v8) + dst * HD, const_cast<float *>(a.ks) + dst,
+                         const_cast<float *>(a.vs) + dst);
+        }
+        __syncthreads();
+    };
+    const int ns = a.new_k ? a.new_slot[seq] : -1;
+    const bool store_early = a.new_k && ns < begin + 256;  // the slot may be in a first sub-tile
+
     // The next sub-tile is loaded before this one is computed; loads past the
     // end read zero.
     Tile cur, nxt;
     int st = begin + wave * 64;
+    if (store_early) store_new(ns);
     load(cur, st);
+    if (a.new_k && !store_early) store_new(ns);
     for (; st < end; st += 256) {
         load(nxt, st + 256);
         asm volatile("" ::: "memory");  // keep the prefetch ahead of the compute

@@ -173,14 +173,21 @@ int needle2_gpu_kv_store_device(void *h, int layer, const float *d_k, const floa
     });
 }
 
-// One decode-attention step (needle2_gpu_attention below); with `next` not NULL (a one-matrix int8 plan of
-// batch seqs whose input buffer is d_out, e.g. the O projection) d_out is
-// also left prepared as next's input, for needle2_gpu_plan_run_chained(next,
-// ..., prepared = 1): in the attention's epilogue for groups of 32 and one
-// split, else by next's prepare launch (not at all when next's GEMV prepares
-// its own input).
+// One decode-attention step (needle2_gpu_attention below), optionally with
+// the step's new token and the next projection:
+// - d_new_k, d_new_v, d_new_slot (all or none; device [seqs][kvheads]
+//   [head_dim] fp32 and [seqs] slots): first stores that token of every
+//   sequence at its slot, as needle2_gpu_kv_store_device with count 1 - in
+//   the attention launch with one split and no slot list, else by the store
+//   launch before it;
+// - next (a one-matrix int8 plan of batch seqs whose input buffer is d_out,
+//   e.g. the O projection): d_out is also left prepared as next's input, for
+//   needle2_gpu_plan_run_chained(next, ..., prepared = 1) - in the
+//   attention's epilogue for groups of 32 and one split, else by next's
+//   prepare launch (not at all when next's GEMV prepares its own input).
 int needle2_gpu_attention_chained(void *h, int layer, const float *d_q, float *d_out, int heads, int length,
-                                  const int *d_slots, const int *d_lengths, int splits, void *next, void *stream) {
+                                  const int *d_slots, const int *d_lengths, int splits, const float *d_new_k,
+                                  const float *d_new_v, const int *d_new_slot, void *next, void *stream) {
     return guarded([&] {
         KvHandle &kv = *kv_of(h);
         check_layer(kv, layer);
@@ -215,6 +222,29 @@ int needle2_gpu_attention_chained(void *h, int layer, const float *d_q, float *d
         a.splits = splits;
         a.slots_per_split = per;
         a.scale = 1 / std::sqrt(float(kv.head_dim));  // engine.cpp:914
+        ND_CHECK(!d_new_k == !d_new_v && !d_new_k == !d_new_slot, "attention: new K, V and slots come together");
+        if (d_new_k) {
+            if (splits == 1 && !d_slots) {
+                a.new_k = d_new_k;
+                a.new_v = d_new_v;
+                a.new_slot = d_new_slot;
+            } else {
+                KvStoreArgs st{};
+                st.k = d_new_k;
+                st.v = d_new_v;
+                st.k8 = kv.k8.p + kv.layer_codes() * layer;
+                st.v8 = kv.v8.p + kv.layer_codes() * layer;
+                st.ks = kv.ks.p + kv.layer_scales() * layer;
+                st.vs = kv.vs.p + kv.layer_scales() * layer;
+                st.first_slot = d_new_slot;
+                st.seqs = kv.seqs;
+                st.count = 1;
+                st.kvheads = kv.kvheads;
+                st.head_dim = kv.head_dim;
+                st.capacity = kv.capacity;
+                launch_kv_store(st, s);
+            }
+        }
         const PrepOut po = plan_prep_target(next, d_out, heads * kv.head_dim, kv.seqs);
         const bool feed = next && plan_wants_input(next);  // not when next's GEMV prepares its own input
         const bool fused = feed && po.q && splits == 1 && group * kv.head_dim % 64 == 0;
@@ -235,7 +265,7 @@ int needle2_gpu_attention_chained(void *h, int layer, const float *d_q, float *d
 int needle2_gpu_attention(void *h, int layer, const float *d_q, float *d_out, int heads, int length,
                           const int *d_slots, const int *d_lengths, int splits, void *stream) {
     return needle2_gpu_attention_chained(h, layer, d_q, d_out, heads, length, d_slots, d_lengths, splits, nullptr,
-                                         stream);
+                                         nullptr, nullptr, nullptr, stream);
 }
 
 // Copy host rows in the reference's layout ([count][kvheads][head_dim] int8,

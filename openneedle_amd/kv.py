@@ -48,18 +48,22 @@ class KVCache:
                                                     addr(d_first_slot), stream_ptr(stream)), "KV store")
 
     def attention(self, layer: int, d_q, d_out, heads: int, length: int, d_slots=None, d_lengths=None,
-                  splits: int = 0, stream=None, next=None) -> None:
-        """One decode step for every sequence: device q / out fp32 ``[seqs][heads][head_dim]``. ``next``: a
-        one-matrix int8 :class:`~openneedle_amd.cq.Plan` reading ``d_out`` whose input is left prepared for its
-        run with ``prepared=True``."""
-        if next is None:
+                  splits: int = 0, stream=None, next=None, new=None) -> None:
+        """One decode step for every sequence: device q / out fp32 ``[seqs][heads][head_dim]``. ``new``: (device
+        k, device v, device slots) of one new token per sequence, stored first (as :meth:`store_device` with
+        count 1). ``next``: a one-matrix int8 :class:`~openneedle_amd.cq.Plan` reading ``d_out`` whose input is
+        left prepared for its run with ``prepared=True``."""
+        if next is None and new is None:
             check(self._lib.needle2_gpu_attention(self.ptr, layer, addr(d_q), addr(d_out), int(heads), int(length),
                                                   addr(d_slots), addr(d_lengths), int(splits), stream_ptr(stream)),
                   "attention")
         else:
+            nk, nv, ns = new if new is not None else (None, None, None)
             check(self._lib.needle2_gpu_attention_chained(self.ptr, layer, addr(d_q), addr(d_out), int(heads),
                                                           int(length), addr(d_slots), addr(d_lengths), int(splits),
-                                                          next.ptr, stream_ptr(stream)), "attention")
+                                                          addr(nk), addr(nv), addr(ns),
+                                                          next.ptr if next is not None else None,
+                                                          stream_ptr(stream)), "attention")
 
     def load(self, layer: int, seq: int, k, v, ks, vs, first_slot: int = 0) -> None:
         """Copy host int8 rows and fp32 scales (reference layout) into one sequence of the cache."""

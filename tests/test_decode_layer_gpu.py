@@ -12,10 +12,11 @@ oracle on the stage's own GPU input:
   1.7e-6 * max|v| per output against fp64, so the bars are about twice the reference's own error;
 - the slots before the new token are untouched by the step.
 
-The step runs the projections after the attention as a chain (each producer leaves the next plan's input
-prepared); the chained step's outputs equal the unchained step's bit for bit, with the preparation fused into
-the producers' epilogues and with the fallback prepare launches (other batch sizes, the attention split, the
-16 x 16 K split switched off)."""
+The step stores the new token inside the attention launch and runs the projections after the attention as a
+chain (each producer leaves the next plan's input prepared); the chained step's outputs and cache rows equal
+the unchained step's (separate store launch, every plan preparing its own input) bit for bit, with the store
+and preparation fused into the attention and GEMV epilogues and with the fallback launches (other batch sizes,
+the attention split, the 16 x 16 K split switched off)."""
 import numpy as np
 import pytest
 
@@ -98,13 +99,21 @@ def test_chained_step_equals_unchained(seqs, splits, ks16, monkeypatch):
         stream = td.add(Stream())
         layer = bench.DecodeLayer(seqs, td, stream)
         layer.splits = splits
-        outs = {}
+        L, outs = bench.DecodeLayer, {}
+        zk = np.zeros((1, L.KVH, L.HD), np.int8)
+        zs = np.zeros((1, L.KVH), np.float32)
         for mode in ("unchained", "chained", "unchained"):
             for n in ("a", "o", "u", "d"):  # stale outputs would hide a missing write
                 layer.buf[n].upload(np.full((seqs, layer.widths[n]), np.nan, np.float32))
+            for s in range(seqs):  # and a stale new-token slot a missing store
+                layer.kv.load(0, s, zk, zk, zs, zs, first_slot=L.CAP - 1)
             (layer.step if mode == "chained" else layer.unchained_step)()
             synchronize()
-            outs.setdefault(mode, []).append({n: layer.download(n) for n in ("q", "k", "v", "a", "o", "u", "d")})
+            got = {n: layer.download(n) for n in ("q", "k", "v", "a", "o", "u", "d")}
+            for s in (0, seqs - 1):
+                for i, part in enumerate(layer.kv.read(0, s, 1, first_slot=L.CAP - 1)):
+                    got[f"cache{s}.{i}"] = part
+            outs.setdefault(mode, []).append(got)
         for n in outs["chained"][0]:
             np.testing.assert_array_equal(outs["chained"][0][n], outs["unchained"][0][n], err_msg=n)
             np.testing.assert_array_equal(outs["unchained"][1][n], outs["unchained"][0][n], err_msg=n)
