@@ -1342,10 +1342,11 @@ void launch_sdot_ks(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs,
 // int8 path split over K on 16 x 16 tiles, for small matrices (decode-layer
 // projections and prompt chunks at batch 2 and more)
 //
-// As sdot_mfma_ks_kernel, with a workgroup of kKs waves sharing one tile of
-// 16 weight rows x 16 batch rows, so a small matrix spreads over four times
-// the workgroups. Wave w takes groups w, w + kKs, ...; each 32-position step
-// of a group is one v_mfma_i32_16x16x32_i8: lane (j, t) = (l % 16, l / 16)
+// As sdot_mfma_ks_kernel, with a workgroup of KS (8, or 16 from 64 groups)
+// waves sharing one tile of 16 weight rows x 16 batch rows, so a small matrix
+// spreads over four times the workgroups. Wave w takes groups w, w + KS, ...;
+// each 32-position step of a group is one v_mfma_i32_16x16x32_i8: lane
+// (j, t) = (l % 16, l / 16)
 // feeds batch row j's activations of positions 8t .. 8t + 7 of the step (A)
 // and weight row j's decoded centroids of the same positions (B): code
 // dword t of the step's 32 four-bit codes, or crumb selectors 2(t % 2) and
@@ -1353,7 +1354,7 @@ void launch_sdot_ks(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs,
 // register r of lane (j, t) is then the dot of weight row j with batch row
 // 4 t + r. Each round every wave turns its group's four dots into the
 // reference's terms (float(dot) * ns) * x_scale (sdot.cpp:142-149) and parks
-// them in LDS; after one barrier wave r (< 4) adds register r's kKs terms in
+// them in LDS; after one barrier wave r (< 4) adds register r's KS terms in
 // group order, so every output is value += term_g for g = 0, 1, 2, ... as
 // the reference sums: bit-identical outputs.
 //
@@ -1373,14 +1374,14 @@ struct Ks16Slot {
     uint16_t norm[MB];          // weight row j's group norm, per row block
 };
 
-template <int KIND, int GROUP, int MB, bool PREP>
-__global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+template <int KIND, int GROUP, int MB, bool PREP, int KS>
+__global__ __launch_bounds__(KS * 64) void sdot_ks16_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
                                                              int njobs, SdotGeom geom, PrepOut po) {
     static_assert(MB == 1 || MB == 2, "one or two 16-row blocks");
     static_assert(!PREP || MB == 2, "the prepared groups are 32 outputs");
     using S = Ks16Slot<GROUP, MB>;
     constexpr int RB = 16 * MB;  // weight rows per workgroup
-    __shared__ float park[2][kKs][4 * MB][64];
+    __shared__ float park[2][KS][4 * MB][64];
     const int lane = threadIdx.x & 63, jr = lane & 15, t = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int rb = blockIdx.x;  // RB-row block across the plan
@@ -1451,11 +1452,11 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
     // wave w < 4 MB sums accumulator register w % 4 of row block w / 4: batch row 4t + w % 4, weight row
     // rbase + 16 (w / 4) + jr
     float value = 0.0f;
-    const int rounds = (groups + kKs - 1) / kKs;
+    const int rounds = (groups + KS - 1) / KS;
     S cur, nxt;
     load(cur, min(w, groups - 1));
     for (int r = 0; r < rounds; ++r) {
-        load(nxt, min((r + 1) * kKs + w, groups - 1));  // past the last group: re-read, never used
+        load(nxt, min((r + 1) * KS + w, groups - 1));  // past the last group: re-read, never used
         v4i acc[MB];
 #pragma unroll
         for (int m = 0; m < MB; ++m) acc[m] = v4i{0, 0, 0, 0};
@@ -1483,7 +1484,7 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
             for (int k = 0; k < 4; ++k) park[r & 1][w][4 * m + k][lane] = (static_cast<float>(acc[m][k]) * ns) * cur.xs[k];
         }
         __syncthreads();
-        const int live = min(kKs, groups - r * kKs);  // groups of this round (uniform)
+        const int live = min(KS, groups - r * KS);  // groups of this round (uniform)
         if (w < 4 * MB)
             for (int src = 0; src < live; ++src) value = value + park[r & 1][src][w][lane];
         cur = nxt;
@@ -1496,29 +1497,50 @@ __global__ __launch_bounds__(kKs * 64) void sdot_ks16_kernel(SdotJob job0, const
         // the 16 x 32 outputs through LDS (rows past the matrix as the zeros the prepare kernel pads with),
         // then wave w prepares batch rows 2w (lanes 0-31) and 2w + 1 (lanes 32-63) of the group
         __shared__ float yl[16][33];
-        yl[4 * t + (w % 4)][16 * (w / 4) + jr] = row < rows ? value : 0.0f;
+        if (w < 8) yl[4 * t + (w % 4)][16 * (w / 4) + jr] = row < rows ? value : 0.0f;
         __syncthreads();
-        const int bl = 2 * w + (lane >> 5), pos = lane & 31;
-        const int b = b0 + bl;
-        const int p = tile * kRowsPerBlock + rbase + pos;  // position in the next projection's input row
-        const int gi = p / 32;
-        const size_t bs = static_cast<size_t>(b < batch ? b : 0);
-        prepare_lane<32>(yl[bl][pos], lane, p, po.padded, po.dev, po.scale, po.kind, po.q + bs * po.dev,
-                         po.xs + bs * po.groups + gi, po.xst + static_cast<size_t>(gi) * po.batch + bs, b < batch);
+        if (w < 8) {
+            const int bl = 2 * w + (lane >> 5), pos = lane & 31;
+            const int b = b0 + bl;
+            const int p = tile * kRowsPerBlock + rbase + pos;  // position in the next projection's input row
+            const int gi = p / 32;
+            const size_t bs = static_cast<size_t>(b < batch ? b : 0);
+            prepare_lane<32>(yl[bl][pos], lane, p, po.padded, po.dev, po.scale, po.kind, po.q + bs * po.dev,
+                             po.xs + bs * po.groups + gi, po.xst + static_cast<size_t>(gi) * po.batch + bs, b < batch);
+        }
     }
+}
+
+template <int KIND, int MB, bool PREP, int KS>
+void launch_sdot_ks16_waves(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
+                            int batch, const PrepOut &po, hipStream_t s) {
+    dim3 grid(blocks * (kRowsPerBlock / (16 * MB)), (batch + 15) / 16), block(KS * 64);
+    switch (g.group) {
+    case 32: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 32, MB, PREP, KS>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
+    case 64: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 64, MB, PREP, KS>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
+    case 128: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 128, MB, PREP, KS>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
+    default: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 256, MB, PREP, KS>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
+    }
+    ND_HIP(hipGetLastError());
+}
+
+// 16 waves per workgroup (one group each per round) from 64 groups: half
+// the rounds of 8 waves, each round's terms still summed in group order
+// (decode-layer down projection, K = 2048: 7.2 -> 6.7 us; with 16 groups the
+// larger workgroups measured slower, 5.2 -> 6.0 us).
+// NEEDLE2_GPU_INT8_KS16_WAVES = 8 / 16 overrides.
+static int ks16_waves(const SdotGeom &g) {
+    const char *mode = std::getenv("NEEDLE2_GPU_INT8_KS16_WAVES");
+    if (mode && std::strcmp(mode, "8") == 0) return 8;
+    if (mode && std::strcmp(mode, "16") == 0) return 16;
+    return g.groups >= 64 ? 16 : 8;
 }
 
 template <int KIND, int MB, bool PREP>
 void launch_sdot_ks16_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
                            int batch, const PrepOut &po, hipStream_t s) {
-    dim3 grid(blocks * (kRowsPerBlock / (16 * MB)), (batch + 15) / 16), block(kKs * 64);
-    switch (g.group) {
-    case 32: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 32, MB, PREP>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
-    case 64: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 64, MB, PREP>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
-    case 128: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 128, MB, PREP>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
-    default: hipLaunchKernelGGL((sdot_ks16_kernel<KIND, 256, MB, PREP>), grid, block, 0, s, job0, jobs, njobs, g, po); break;
-    }
-    ND_HIP(hipGetLastError());
+    if (ks16_waves(g) == 16) launch_sdot_ks16_waves<KIND, MB, PREP, 16>(g, job0, jobs, njobs, blocks, batch, po, s);
+    else launch_sdot_ks16_waves<KIND, MB, PREP, 8>(g, job0, jobs, njobs, blocks, batch, po, s);
 }
 
 bool launch_sdot_ks16(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
