@@ -37,8 +37,8 @@ struct AttnArgs {
                            // tokens of one prompt chunk, each with its own slot list)
     PrepOut prep;          // q set (one split, heads * head_dim a multiple of 64): out is also left
                            // prepared as the next int8 projection's input, sequence = batch row
-    const float *new_k, *new_v;  // non-null (one split, no slot list, no shared cache): one new token per
-    const int *new_slot;         // sequence ([seqs][kvheads][head_dim]) is first stored at new_slot[seq]
+    const float *new_k, *new_v;  // non-null (no slot list, no shared cache): one new token per sequence
+    const int *new_slot;         // ([seqs][kvheads][head_dim]) is first stored at new_slot[seq]
 };
 
 bool attn_supported(int head_dim, int group);

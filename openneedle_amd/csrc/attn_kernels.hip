@@ -216,14 +216,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         asm volatile("" ::: "memory");
     };
 
-    // With a new token (one block per (sequence, kv head): one split, no slot
-    // list), wave 0 first stores its K and V rows at slot new_slot[seq] as
-    // kv_store_kernel does; the block barrier (a workgroup-scope release and
-    // acquire) orders those stores before the block's loads of that slot.
+    // With a new token (no slot list, so list position = slot), wave 0 of
+    // the block whose split holds slot new_slot[seq] (the last split for a
+    // slot past every range; no block for one outside the cache) first stores
+    // the token's K and V rows there as kv_store_kernel does; the block
+    // barrier (a workgroup-scope release and acquire) orders those stores
+    // before the block's loads of that slot, and no other block reads it.
     // When the slot lies past the waves' first sub-tiles, those loads are
     // issued before the store.
     auto store_new = [&](int ns) {
-        if (wave == 0 && ns >= 0 && static_cast<uint32_t>(ns) < cap) {
+        if (wave == 0) {
             const size_t src = (static_cast<size_t>(seq) * a.kvheads + kh) * HD;
             const size_t dst = row0 + ns;
             // the cache rows this call writes (the block's own context)
@@ -234,7 +236,9 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         __syncthreads();
     };
     const int ns = a.new_k ? a.new_slot[seq] : -1;
-    const bool store_early = a.new_k && ns < begin + 256;  // the slot may be in a first sub-tile
+    const bool store_here =
+        a.new_k && ns >= 0 && static_cast<uint32_t>(ns) < cap && sp == min(ns / a.slots_per_split, a.splits - 1);
+    const bool store_early = store_here && ns < begin + 256;  // the slot may be in a first sub-tile
 
     // The next sub-tile is loaded before this one is computed; loads past the
     // end read zero.
@@ -242,7 +246,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     int st = begin + wave * 64;
     if (store_early) store_new(ns);
     load(cur, st);
-    if (a.new_k && !store_early) store_new(ns);
+    if (store_here && !store_early) store_new(ns);
     for (; st < end; st += 256) {
         load(nxt, st + 256);
         asm volatile("" ::: "memory");  // keep the prefetch ahead of the compute

@@ -178,8 +178,8 @@ int needle2_gpu_kv_store_device(void *h, int layer, const float *d_k, const floa
 // - d_new_k, d_new_v, d_new_slot (all or none; device [seqs][kvheads]
 //   [head_dim] fp32 and [seqs] slots): first stores that token of every
 //   sequence at its slot, as needle2_gpu_kv_store_device with count 1 - in
-//   the attention launch with one split and no slot list, else by the store
-//   launch before it;
+//   the attention launch without a slot list (by the block whose split
+//   holds the slot), else by the store launch before it;
 // - next (a one-matrix int8 plan of batch seqs whose input buffer is d_out,
 //   e.g. the O projection): d_out is also left prepared as next's input, for
 //   needle2_gpu_plan_run_chained(next, ..., prepared = 1) - in the
@@ -224,7 +224,7 @@ int needle2_gpu_attention_chained(void *h, int layer, const float *d_q, float *d
         a.scale = 1 / std::sqrt(float(kv.head_dim));  // engine.cpp:914
         ND_CHECK(!d_new_k == !d_new_v && !d_new_k == !d_new_slot, "attention: new K, V and slots come together");
         if (d_new_k) {
-            if (splits == 1 && !d_slots) {
+            if (!d_slots) {
                 a.new_k = d_new_k;
                 a.new_v = d_new_v;
                 a.new_slot = d_new_slot;

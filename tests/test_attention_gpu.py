@@ -188,3 +188,37 @@ def test_validation_errors():
         kv.attention(0, d.ptr, d.ptr, 2, 17)
     with pytest.raises(RuntimeError, match="head_dim"):
         KVCache(1, 16, 2, 48, 1)
+
+
+@pytest.mark.parametrize("hd", [32, 64, 128])
+@pytest.mark.parametrize("splits", [0, 1, 3])
+def test_attention_storing_the_new_token(hd, splits):
+    """The new token of every sequence stored by the attention launch (at slots inside a first sub-tile, past
+    it, past every split's range, at the last slot and outside the cache): cache rows bit-identical to the
+    store kernel's (oracle.kv_quantize), outputs as attending the stored cache."""
+    rng = np.random.default_rng(hd * 10 + splits)
+    seqs, cap, kvh, heads, length = 5, 1024, 2, 4, 700
+    _, _, rows = make_cache(rng, seqs, cap, kvh, hd)
+    kv = KVCache(1, cap, kvh, hd, seqs)
+    for s, ((k8, ks), (v8, vs)) in enumerate(rows):
+        kv.load(0, s, k8, v8, ks, vs)
+    new_slot = np.array([3, 500, 900, cap - 1, cap + 7], np.int32)
+    nk = rng.normal(size=(seqs, kvh, hd)).astype(np.float32)
+    nv = rng.normal(size=(seqs, kvh, hd)).astype(np.float32)
+    q = rng.normal(size=(seqs, heads, hd)).astype(np.float32)
+    d_q, d_o = DeviceArray.from_host(q), DeviceArray(q.nbytes)
+    d_o.upload(np.full(q.shape, np.nan, np.float32))
+    d_k, d_v, d_s = DeviceArray.from_host(nk), DeviceArray.from_host(nv), DeviceArray.from_host(new_slot)
+    kv.attention(0, d_q, d_o, heads, length, splits=splits, new=(d_k, d_v, d_s))
+    synchronize()
+    got = d_o.download(np.empty(q.shape, np.float32))
+    k8n, ksn = oracle.kv_quantize(nk)
+    v8n, vsn = oracle.kv_quantize(nv)
+    for s, ((k8, ks), (v8, vs)) in enumerate(rows):
+        k8, v8, ks, vs = k8.copy(), v8.copy(), ks.copy(), vs.copy()
+        if new_slot[s] < cap:
+            k8[new_slot[s]], v8[new_slot[s]], ks[new_slot[s]], vs[new_slot[s]] = k8n[s], v8n[s], ksn[s], vsn[s]
+        for a, b in zip(kv.read(0, s, cap), (k8, v8, ks, vs)):
+            np.testing.assert_array_equal(a, b, err_msg=f"seq {s}: cache after the step")
+        ref = oracle.attention_i8(q[s], k8, v8, ks, vs, np.arange(length))
+        np.testing.assert_allclose(got[s], ref, atol=ATOL, rtol=RTOL)
