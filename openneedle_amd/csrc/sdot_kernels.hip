@@ -1608,6 +1608,76 @@ __global__ __launch_bounds__(256) void sdot_prepare_wave_kernel(const float *__r
                         xst ? xst + (static_cast<size_t>(v / batch) * groups + p / GROUP) * batch + v % batch : nullptr);
 }
 
+// Prepare for groups of 8 .. 64 positions with eight consecutive positions
+// per thread (8 times fewer workgroups than sdot_prepare_wave_kernel, and
+// 4-bit codes stored as one 8-byte word per thread): FWHT stages 1, 2, 4
+// between the thread's own values, then stages 8 .. GROUP / 2 as in-wave
+// butterflies on each value (the reference's stage order and operands), the
+// group absmax over the thread's values and GROUP / 8 lanes, then the
+// reference's quantiser as prepare_lane does it. Same values as
+// sdot_prepare_kernel, bit for bit.
+template <int GROUP>
+__global__ __launch_bounds__(256) void sdot_prepare_oct_kernel(const float *__restrict__ x0,
+                                                               const float *const *__restrict__ xptr, int batch,
+                                                               int in, int padded, int dev, float scale, int kind,
+                                                               int8_t *__restrict__ q, float *__restrict__ xs,
+                                                               float *__restrict__ xst, int groups) {
+    constexpr int L = GROUP / 8;  // lanes per group
+    const int v = blockIdx.y;
+    const int p0 = (blockIdx.x * 256 + static_cast<int>(threadIdx.x)) * 8;
+    const int t = threadIdx.x & 63;
+    const float *xv = (xptr ? xptr[v / batch] : x0) + static_cast<size_t>(v % batch) * in;
+    const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(xv, static_cast<uint32_t>(in) * 4u);  // past `in`: zeros
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        r[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, static_cast<uint32_t>(p0 + i) * 4u, 0, 0));
+#pragma unroll
+    for (int h = 1; h < 8 && h < GROUP; h *= 2)  // stages 1, 2, 4 within the thread
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & h)) {
+                const float a = r[i], b = r[i + h];
+                r[i] = a + b;
+                r[i + h] = a - b;
+            }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        wave_butterflies<L, 1>(r[i], t);  // stages 8 .. GROUP / 2 (lane strides 1 .. L / 2)
+        r[i] = r[i] * scale;
+        m = fmaxf(m, fabsf(r[i]));
+    }
+    const float absmax = group_max<L>(m, t);
+    float sc = absmax > 0 ? absmax / 127 : 1;  // sdot.cpp:77-81
+    if (sc == 0.0f) sc = absmax;                // subnormal absmax/127 underflows
+    uint32_t out[2] = {0u, 0u};                 // the 8 codes in the 4-bit permuted order
+    int8_t qb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        int8_t c = 0;
+        if (p0 + i < padded) {
+            float val = rintf(r[i] / sc);
+            val = val < -127.0f ? -127.0f : (127.0f < val ? 127.0f : val);
+            c = static_cast<int8_t>(val);
+        }
+        qb[i] = c;
+        out[i & 1] |= static_cast<uint32_t>(static_cast<uint8_t>(c)) << (8 * (i >> 1));
+    }
+    if (p0 >= dev) return;  // whole groups past the row (dev is a multiple of 256); no lane exchange follows
+    int8_t *qv = q + static_cast<size_t>(v) * dev;
+    if (kind == kNib) {
+        *reinterpret_cast<uint2 *>(qv + p0) = make_uint2(out[0], out[1]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qv[permuted_index(kind, p0 + i)] = qb[i];
+    }
+    if (p0 % GROUP == 0 && p0 < padded) {
+        xs[static_cast<size_t>(v) * groups + p0 / GROUP] = sc;
+        if (xst) xst[(static_cast<size_t>(v / batch) * groups + p0 / GROUP) * batch + v % batch] = sc;
+    }
+}
+
 // Prepare for groups of 128 and 256 positions, one wave per group without
 // LDS (prepare_group_wave). Same values as sdot_prepare_kernel, bit for bit.
 template <int GROUP>
@@ -1637,11 +1707,33 @@ __global__ __launch_bounds__(256) void sdot_prepare_wave_group_kernel(const floa
 
 }  // namespace
 
+// Groups of 8 .. 64 take the eight-positions-per-thread kernel
+// (NEEDLE2_GPU_INT8_PREPARE=lane: one position per thread).
+static bool prepare_oct_wanted() {
+    const char *mode = std::getenv("NEEDLE2_GPU_INT8_PREPARE");
+    return !(mode && std::strcmp(mode, "lane") == 0);
+}
+
 bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, int nvec, int in, int padded,
                          int dev, int group, float scale, int kind, int32_t *q, float *xs, float *xst, hipStream_t s) {
     if (group > kPrepareMaxGroup) return false;
     ND_CHECK(group >= 8 && (group & (group - 1)) == 0, "int8 prepare: group must be a power of two >= 8");
     if (nvec <= 0) return true;
+    if (group <= 64 && prepare_oct_wanted()) {
+        dim3 grid((dev + 2047) / 2048, nvec), block(256);
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, block, 0, s, x0, xptr, batch, in, padded, dev, scale, kind,
+                               reinterpret_cast<int8_t *>(q), xs, xst, padded / group);
+        };
+        switch (group) {
+        case 8: go(sdot_prepare_oct_kernel<8>); break;
+        case 16: go(sdot_prepare_oct_kernel<16>); break;
+        case 32: go(sdot_prepare_oct_kernel<32>); break;
+        default: go(sdot_prepare_oct_kernel<64>); break;
+        }
+        ND_HIP(hipGetLastError());
+        return true;
+    }
     if (group <= 64) {
         dim3 grid(dev / 256, nvec), block(256);
         auto go = [&](auto kern) {
