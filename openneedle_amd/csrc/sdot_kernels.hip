@@ -1179,15 +1179,15 @@ bool launch_sdot_tile16(const SdotGeom &g, const SdotJob &job0, const SdotJob *j
 // ---------------------------------------------------------------------------
 // int8 MFMA path split over K, for small matrices (decode layers, any batch)
 //
-// A workgroup of kKs waves shares one (32 weight rows, 32 batch rows) tile;
-// wave w takes groups w, w + kKs, ... Each round every wave turns its group's
-// int32 accumulator into the reference's terms (float(dot) * ns) * x_scale
-// (sdot.cpp:142-149) and parks them in LDS (double-buffered by round); after
-// one barrier, the owner of each accumulator register adds the kKs terms in
-// group order. Each output is therefore value += term_g for g = 0, 1, 2, ...
-// exactly as the reference sums, and many more waves cover a small matrix.
+// A workgroup of KS waves (8, or 16 from 64 groups: ks_waves) shares one
+// (32 weight rows, 32 batch rows) tile; wave w takes groups w, w + KS, ...
+// Each round every wave turns its group's int32 accumulator into the
+// reference's terms (float(dot) * ns) * x_scale (sdot.cpp:142-149) and parks
+// them in LDS (double-buffered by round); after one barrier, the owner of
+// each accumulator register adds the KS terms in group order. Each output is
+// therefore value += term_g for g = 0, 1, 2, ... exactly as the reference
+// sums, and many more waves cover a small matrix.
 // ---------------------------------------------------------------------------
-constexpr int kKs = 8;
 
 template <int KIND, int GROUP, int J>
 __device__ __forceinline__ void mfma_terms(const MfmaSlot<KIND, GROUP, J> &sl, const uint32_t cent[4], float cs,
@@ -1204,12 +1204,12 @@ __device__ __forceinline__ void mfma_terms(const MfmaSlot<KIND, GROUP, J> &sl, c
 // first, each wave the groups its rounds read (prepare_lane /
 // prepare_group_wave: the prepare kernels' arithmetic), so the plan launches
 // no prepare kernel; the outputs are the same bits.
-template <int KIND, int GROUP, int J, bool XIN>
-__global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
+template <int KIND, int GROUP, int J, bool XIN, int KS>
+__global__ __launch_bounds__(KS * 64) void sdot_mfma_ks_kernel(SdotJob job0, const SdotJob *__restrict__ jobs,
                                                                 int njobs, SdotGeom geom) {
     constexpr int R = 4 * J;                          // accumulator registers in use
-    constexpr int kOwn = (R + kKs - 1) / kKs;         // registers each wave sums
-    __shared__ float park[2][kKs][R][64];
+    constexpr int kOwn = (R + KS - 1) / KS;         // registers each wave sums
+    __shared__ float park[2][KS][R][64];
     extern __shared__ __attribute__((aligned(16))) uint8_t xin_lds[];  // XIN: q [dev], then scales [groups]
     const int lane = threadIdx.x & 63, i = lane & 31, h = lane >> 5;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
@@ -1257,15 +1257,15 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
         const int in = geom.in, padded = geom.padded;
         if constexpr (GROUP <= 64) {  // 64 / GROUP of the wave's groups per pass, one lane per position
             constexpr int PER = 64 / GROUP;
-            for (int k = 0; w + kKs * PER * k < groups; ++k) {
-                const int g = w + kKs * (PER * k + lane / GROUP);
+            for (int k = 0; w + KS * PER * k < groups; ++k) {
+                const int g = w + KS * (PER * k + lane / GROUP);
                 const int p = g * GROUP + lane % GROUP;
                 const float r = p < in ? xv[p] : 0.0f;
                 prepare_lane<GROUP>(r, lane, p, padded, dev, geom.scale, KIND, qst, scst + (g < groups ? g : 0),
                                     nullptr);
             }
         } else {
-            for (int g = w; g < groups; g += kKs) {
+            for (int g = w; g < groups; g += KS) {
                 float r[GROUP / 64];
 #pragma unroll
                 for (int k = 0; k < GROUP / 64; ++k) {
@@ -1285,21 +1285,21 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
     float value[kOwn];
 #pragma unroll
     for (int k = 0; k < kOwn; ++k) value[k] = 0.0f;
-    const int rounds = (groups + kKs - 1) / kKs;
+    const int rounds = (groups + KS - 1) / KS;
     MfmaSlot<KIND, GROUP, J> cur, nxt;
     load(cur, w);
     for (int r = 0; r < rounds; ++r) {
         // next round's group (past the last group: zeros, or data that is never used)
-        load(nxt, (r + 1) * kKs + w);
+        load(nxt, (r + 1) * KS + w);
         float term[R];
         mfma_terms(cur, cent, cs, term);
 #pragma unroll
         for (int k = 0; k < R; ++k) park[r & 1][w][k][lane] = term[k];
         __syncthreads();
-        const int live = min(kKs, groups - r * kKs);  // groups of this round (uniform)
+        const int live = min(KS, groups - r * KS);  // groups of this round (uniform)
 #pragma unroll
         for (int k = 0; k < kOwn; ++k) {
-            const int reg = w + k * kKs;
+            const int reg = w + k * KS;
             if (reg < R)
                 for (int src = 0; src < live; ++src) value[k] = value[k] + park[r & 1][src][reg][lane];
         }
@@ -1308,7 +1308,7 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
     if (row < rows) {
 #pragma unroll
         for (int k = 0; k < kOwn; ++k) {
-            const int reg = w + k * kKs;
+            const int reg = w + k * KS;
             if (reg >= R) continue;
             const int m = b0 + 8 * (reg / 4) + 4 * h + (reg % 4);
             if (m < batch) ((ND_GLOBAL float *)J0.y)[static_cast<size_t>(m) * (J0.ystride ? J0.ystride : rows) + row] = value[k];
@@ -1316,18 +1316,34 @@ __global__ __launch_bounds__(kKs * 64) void sdot_mfma_ks_kernel(SdotJob job0, co
     }
 }
 
+template <int KIND, int J, bool XIN, int KS>
+void launch_sdot_ks_waves(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
+                          hipStream_t s) {
+    dim3 grid(blocks * (kRowsPerBlock / 32), (batch + 31) / 32), block(KS * 64);
+    const size_t lds = XIN ? static_cast<size_t>(g.windows) * kWindow + static_cast<size_t>(g.groups) * 4 : 0;
+    switch (g.group) {
+    case 32: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 32, J, XIN, KS>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    case 64: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 64, J, XIN, KS>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    case 128: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 128, J, XIN, KS>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    default: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 256, J, XIN, KS>), grid, block, lds, s, job0, jobs, njobs, g); break;
+    }
+    ND_HIP(hipGetLastError());
+}
+
+// 16 waves per workgroup from 64 groups (half the rounds), as the 16 x 16 K
+// split does; NEEDLE2_GPU_INT8_KS16_WAVES = 8 / 16 overrides both.
+static int ks_waves(const SdotGeom &g) {
+    const char *mode = std::getenv("NEEDLE2_GPU_INT8_KS16_WAVES");
+    if (mode && std::strcmp(mode, "8") == 0) return 8;
+    if (mode && std::strcmp(mode, "16") == 0) return 16;
+    return g.groups >= 64 ? 16 : 8;
+}
+
 template <int KIND, int J, bool XIN = false>
 void launch_sdot_ks_j(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
                       hipStream_t s) {
-    dim3 grid(blocks * (kRowsPerBlock / 32), (batch + 31) / 32), block(kKs * 64);
-    const size_t lds = XIN ? static_cast<size_t>(g.windows) * kWindow + static_cast<size_t>(g.groups) * 4 : 0;
-    switch (g.group) {
-    case 32: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 32, J, XIN>), grid, block, lds, s, job0, jobs, njobs, g); break;
-    case 64: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 64, J, XIN>), grid, block, lds, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 128, J, XIN>), grid, block, lds, s, job0, jobs, njobs, g); break;
-    default: hipLaunchKernelGGL((sdot_mfma_ks_kernel<KIND, 256, J, XIN>), grid, block, lds, s, job0, jobs, njobs, g); break;
-    }
-    ND_HIP(hipGetLastError());
+    if (ks_waves(g) == 16) launch_sdot_ks_waves<KIND, J, XIN, 16>(g, job0, jobs, njobs, blocks, batch, s);
+    else launch_sdot_ks_waves<KIND, J, XIN, 8>(g, job0, jobs, njobs, blocks, batch, s);
 }
 
 template <int KIND>
@@ -1527,14 +1543,8 @@ void launch_sdot_ks16_waves(const SdotGeom &g, const SdotJob &job0, const SdotJo
 // 16 waves per workgroup (one group each per round) from 64 groups: half
 // the rounds of 8 waves, each round's terms still summed in group order
 // (decode-layer down projection, K = 2048: 7.2 -> 6.7 us; with 16 groups the
-// larger workgroups measured slower, 5.2 -> 6.0 us).
-// NEEDLE2_GPU_INT8_KS16_WAVES = 8 / 16 overrides.
-static int ks16_waves(const SdotGeom &g) {
-    const char *mode = std::getenv("NEEDLE2_GPU_INT8_KS16_WAVES");
-    if (mode && std::strcmp(mode, "8") == 0) return 8;
-    if (mode && std::strcmp(mode, "16") == 0) return 16;
-    return g.groups >= 64 ? 16 : 8;
-}
+// larger workgroups measured slower, 5.2 -> 6.0 us); ks_waves.
+static int ks16_waves(const SdotGeom &g) { return ks_waves(g); }
 
 template <int KIND, int MB, bool PREP>
 void launch_sdot_ks16_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks,
@@ -1841,7 +1851,7 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     // Kernel by size (environment overrides, "always" / "never", let the
     // tests run every kernel on every shape):
     //  - small matrices (fewer 32 x 32 tiles than SIMDs: decode projections)
-    //    of any batch split K over kKs waves per tile (NEEDLE2_GPU_INT8_KSPLIT),
+    //    of any batch split K over 8 or 16 waves per tile (NEEDLE2_GPU_INT8_KSPLIT),
     //    on 16 x 16 tiles at batch 2 and more (NEEDLE2_GPU_INT8_KS16:
     //    "never", or "always" from batch 1);
     //  - one batch row: the barrier-free row kernel (NEEDLE2_GPU_INT8_ROW);
