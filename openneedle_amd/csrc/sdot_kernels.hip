@@ -1717,11 +1717,16 @@ __global__ __launch_bounds__(256) void sdot_prepare_wave_group_kernel(const floa
 
 }  // namespace
 
-// Groups of 8 .. 64 take the eight-positions-per-thread kernel
-// (NEEDLE2_GPU_INT8_PREPARE=lane: one position per thread).
-static bool prepare_oct_wanted() {
+// Groups of 8 .. 64 of at least 2^20 positions in all take the
+// eight-positions-per-thread kernel (batch 16 of the 64 x 4096 stack:
+// 17.8 -> ~12 us); a decode layer's 64 x 512 inputs keep one position per
+// thread, whose latency is shorter (Q|K|V plan 7.6 -> 7.1 us).
+// NEEDLE2_GPU_INT8_PREPARE = oct / lane overrides.
+static bool prepare_oct_wanted(long values) {
     const char *mode = std::getenv("NEEDLE2_GPU_INT8_PREPARE");
-    return !(mode && std::strcmp(mode, "lane") == 0);
+    if (mode && std::strcmp(mode, "lane") == 0) return false;
+    if (mode && std::strcmp(mode, "oct") == 0) return true;
+    return values >= (1L << 20);
 }
 
 bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, int nvec, int in, int padded,
@@ -1729,7 +1734,7 @@ bool launch_sdot_prepare(const float *x0, const float *const *xptr, int batch, i
     if (group > kPrepareMaxGroup) return false;
     ND_CHECK(group >= 8 && (group & (group - 1)) == 0, "int8 prepare: group must be a power of two >= 8");
     if (nvec <= 0) return true;
-    if (group <= 64 && prepare_oct_wanted()) {
+    if (group <= 64 && prepare_oct_wanted(static_cast<long>(nvec) * dev)) {
         dim3 grid((dev + 2047) / 2048, nvec), block(256);
         auto go = [&](auto kern) {
             hipLaunchKernelGGL(kern, grid, block, 0, s, x0, xptr, batch, in, padded, dev, scale, kind,

@@ -192,11 +192,10 @@ def test_int8_plan_batch1_input_prepared_in_gemv(bits, group, rows, dim, xin, mo
 @pytest.mark.parametrize("bits,group,dim", [(4, 8, 1000), (4, 16, 777), (4, 32, 4100), (4, 64, 1300), (2, 16, 1000),
                                             (2, 32, 777), (2, 64, 2100)])
 def test_int8_prepare_kernels_bit_exact(bits, group, dim, prepare, monkeypatch):
-    """Groups of 8 .. 64: the prepare kernel with eight positions per thread (oct, the default) and with one
-    (lane, NEEDLE2_GPU_INT8_PREPARE=lane), batches 1 and 5 with zero, one-hot and ragged rows, through the
-    GEMV: bit-exact with the oracle."""
-    if prepare == "lane":
-        monkeypatch.setenv("NEEDLE2_GPU_INT8_PREPARE", "lane")
+    """Groups of 8 .. 64: the prepare kernel with eight positions per thread (oct, the default for large
+    inputs) and with one (lane), forced by NEEDLE2_GPU_INT8_PREPARE, batches 1 and 5 with zero, one-hot and
+    ragged rows, through the GEMV: bit-exact with the oracle."""
+    monkeypatch.setenv("NEEDLE2_GPU_INT8_PREPARE", prepare)
     monkeypatch.setenv("NEEDLE2_GPU_INT8_XIN", "never")  # batch 1 through the prepare kernel too
     packed, norms, cb, dense = example(bits, rows=200, dim=dim, group=group, seed=dim * 3 + group)
     q = CQMatrix(packed, norms, dense.shape, bits, group, cb)
