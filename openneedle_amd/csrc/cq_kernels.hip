@@ -589,9 +589,10 @@ __device__ __forceinline__ void load_half(HalfState<KIND, GROUP> &st, __amdgpu_b
     for (int k = 0; k < H::kGroupsPerHalf; ++k) st.norms[k] = load_norm<KIND, GROUP>(norms, w, half, r, k);
 }
 
-// One half window in the reference's order. HALF 0 adds each closed group
-// into the row sum; HALF 1 parks p_g in P[k][r] for the lower half.
-template <int KIND, int GROUP, int HALF>
+// One half window in the reference's order. Without PARK (the lower half)
+// each closed group is added into the row sum; with PARK (by default the
+// upper half) p_g goes to P[k][r] for the row sum's owner.
+template <int KIND, int GROUP, int HALF, bool PARK = HALF == 1>
 __device__ __forceinline__ void compute_half(HalfState<KIND, GROUP> &st, const float *T, float *P, int r,
                                              uint32_t mask, float &sum, float &gd, int w, int groups,
                                              __amdgpu_buffer_rsrc_t codes, __amdgpu_buffer_rsrc_t norms) {
@@ -633,7 +634,7 @@ __device__ __forceinline__ void compute_half(HalfState<KIND, GROUP> &st, const f
             if (pos_end % GROUP == 0) {
                 const int k = pos_end / GROUP - 1;
                 const float p = gd * h2f(st.norms[k]);
-                if constexpr (HALF == 0) {
+                if constexpr (!PARK) {
                     if (gbase + k < groups) sum += p;
                 } else {
                     P[k * kRowsPerBlock + r] = p;
@@ -796,6 +797,111 @@ __global__ __launch_bounds__(kSplitThreads, 4) void cq_gemv_split_kernel(CqJob j
         split_rows<KIND, GROUP, 0>(J, geom, T, P, stage, blk);
     else
         split_rows<KIND, GROUP, 1>(J, geom, T, P, stage, blk);
+}
+
+// ---------------------------------------------------------------------------
+// Window-parallel split GEMV for inputs of two windows (257 .. 512 positions,
+// groups of 128: a decode step's attention projections)
+//
+// Four threads per output row: part q = (window q / 2, half q % 2) builds its
+// half of window q / 2's table (each window has its own) and runs that half
+// with the split kernel's code, so the two windows are computed at once
+// instead of in turn. Window 0's lower half owns the row sum: after its own
+// groups it adds the parked p_g of window 0's upper half, then of window 1's
+// lower and upper halves, i.e. g = 0, 1, 2, ... as cq.cpp:157-164 sums:
+// bit-identical with the split kernel.
+// ---------------------------------------------------------------------------
+constexpr int kWsplitThreads = 4 * kRowsPerBlock;
+
+template <int KIND, int GROUP, int PART>
+__device__ __forceinline__ void wsplit_rows(const CqJob &J, const CqGeom &geom,
+                                            float (*T)[TableShape<KIND>::kFloats],
+                                            float (*P)[SplitShape<KIND, GROUP>::kGroupsPerHalf * kRowsPerBlock],
+                                            float *stage, int blk) {
+    using H = SplitShape<KIND, GROUP>;
+    constexpr int WW = PART / 2, HALF = PART % 2;
+    const int r = threadIdx.x % kRowsPerBlock;
+    const int rows = J.rows, batch = J.batch;
+    const int tile = blk - J.block_begin;
+    const int row = tile * kRowsPerBlock + r;
+    const __amdgpu_buffer_rsrc_t codes =
+        buffer_rsrc(J.codes + static_cast<size_t>(tile) * geom.chunks * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.chunks) * kRowsPerBlock * 16u);
+    const __amdgpu_buffer_rsrc_t norms =
+        buffer_rsrc(J.norms + static_cast<size_t>(tile) * geom.groups * kRowsPerBlock,
+                    static_cast<uint32_t>(geom.groups) * kRowsPerBlock * 2u);
+    const int groups = geom.groups, in = geom.in;
+    const float scale = geom.scale;
+    const uint32_t mask = KIND == kNib ? 0x3Cu : 0x78u;
+    float lut[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lut[i] = geom.lut[i];
+
+    for (int b = 0; b < batch; ++b) {
+        const __amdgpu_buffer_rsrc_t act =
+            buffer_rsrc(J.act + static_cast<size_t>(b) * in, static_cast<uint32_t>(in) * 4u);
+        HalfState<KIND, GROUP> cur;
+        float xa[1];
+        xa[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(act, r * 4u, window_offset(WW), 0));
+        load_half<KIND, GROUP>(cur, codes, norms, WW, HALF, r);
+        __syncthreads();  // the previous batch row finished with T and P
+        window_fwht<GROUP>(xa, scale, stage);
+        build_table_half<KIND>(T[WW], lut, xa[0], HALF, r);
+        __syncthreads();
+        float sum = 0.0f, gd = 0.0f;
+        compute_half<KIND, GROUP, HALF, PART != 0>(cur, T[WW], P[PART == 0 ? 0 : PART - 1], r, mask, sum, gd, WW,
+                                                   groups, codes, norms);
+        __syncthreads();
+        if constexpr (PART == 0) {
+#pragma unroll
+            for (int q = 0; q < 3; ++q) {  // parts 1, 2, 3: groups after window 0's lower half, in order
+                const int gbase = (q + 1) * H::kGroupsPerHalf;
+#pragma unroll
+                for (int k = 0; k < H::kGroupsPerHalf; ++k)
+                    if (gbase + k < groups) sum += P[q][k * kRowsPerBlock + r];
+            }
+            if (row < rows) ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b) * rows + row] = sum;
+        }
+    }
+}
+
+template <int KIND, int GROUP>
+__global__ __launch_bounds__(kWsplitThreads) void cq_gemv_wsplit_kernel(CqJob job0, const CqJob *__restrict__ jobs,
+                                                                       int njobs, CqGeom geom) {
+    using S = TableShape<KIND>;
+    using H = SplitShape<KIND, GROUP>;
+    __shared__ __attribute__((aligned(16))) float T[2][S::kFloats];
+    __shared__ float P[3][H::kGroupsPerHalf * kRowsPerBlock];
+    __shared__ float stage[GROUP > 64 ? 4 * kWindow : 1];
+    static_assert(kPositionsPerThread == 1, "window-parallel GEMV assumes one window position per row thread");
+
+    const int blk = blockIdx.x;
+    CqJob J = job0;
+    if (njobs > 0) {
+        const ND_CONST CqJob *cj = (const ND_CONST CqJob *)(jobs);
+        const int j = find_job(cj, njobs, blk);
+        J.codes = cj[j].codes;
+        J.norms = cj[j].norms;
+        J.act = cj[j].act;
+        J.y = cj[j].y;
+        J.rows = cj[j].rows;
+        J.n_pad = cj[j].n_pad;
+        J.block_begin = cj[j].block_begin;
+        J.batch = cj[j].batch;
+    }
+    switch (__builtin_amdgcn_readfirstlane(threadIdx.x / kRowsPerBlock)) {
+    case 0: wsplit_rows<KIND, GROUP, 0>(J, geom, T, P, stage, blk); break;
+    case 1: wsplit_rows<KIND, GROUP, 1>(J, geom, T, P, stage, blk); break;
+    case 2: wsplit_rows<KIND, GROUP, 2>(J, geom, T, P, stage, blk); break;
+    default: wsplit_rows<KIND, GROUP, 3>(J, geom, T, P, stage, blk); break;
+    }
+}
+
+// Inputs of two windows with groups of 128 take the window-parallel kernel
+// (NEEDLE2_GPU_FP32_WSPLIT=never: the split kernel).
+static bool wsplit_wanted(const CqGeom &g) {
+    const char *mode = std::getenv("NEEDLE2_GPU_FP32_WSPLIT");
+    return g.windows == 2 && g.group == 128 && !(mode && std::strcmp(mode, "never") == 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1121,7 +1227,12 @@ void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int
     case 16: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 16, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
     case 32: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 32, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
     case 64: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 64, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
-    case 128: hipLaunchKernelGGL((cq_gemv_split_kernel<KIND, 128>), grid, split, 0, s, job0, jobs, njobs, g); break;
+    case 128:
+        if (wsplit_wanted(g))
+            hipLaunchKernelGGL((cq_gemv_wsplit_kernel<KIND, 128>), grid, dim3(kWsplitThreads), 0, s, job0, jobs, njobs, g);
+        else
+            hipLaunchKernelGGL((cq_gemv_split_kernel<KIND, 128>), grid, split, 0, s, job0, jobs, njobs, g);
+        break;
     case 256: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 256>), grid, block, 0, s, job0, jobs, njobs, g); break;
     default: hipLaunchKernelGGL((cq_gemv_kernel<KIND, 0>), grid, block, 0, s, job0, jobs, njobs, g); break;
     }

@@ -87,6 +87,28 @@ def test_small_groups_with_and_without_prepass(bits, group, dim, monkeypatch):
         check(d_y.download(np.empty(dense.shape[0], np.float32)), expected[1], bits)
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("dim", [257, 400, 512])
+def test_two_window_inputs_window_parallel(bits, dim, monkeypatch):
+    """Groups of 128 over inputs of two windows (257 .. 512 positions: a decode step's attention projections):
+    the window-parallel kernel (default) and the split kernel (NEEDLE2_GPU_FP32_WSPLIT=never), batch 1 and 3,
+    ragged rows, through the host call and a plan: bit-exact with the oracle."""
+    packed, norms, cb, dense = example(bits, rows=300, dim=dim, group=128, seed=bits * 10 + dim)
+    x = activations((3, dim), seed=dim)
+    expected = oracle.cq_linear(packed, norms, dense.shape, bits, 128, cb, x, 4)
+    for mode in ("auto", "never"):
+        monkeypatch.setenv("NEEDLE2_GPU_FP32_WSPLIT", mode)
+        q = CQMatrix(packed, norms, dense.shape, bits, 128, cb)
+        check(q.matvec(x), expected, bits)
+        check(q.matvec(x[1:2]), expected[1:2], bits)
+        d_x = DeviceArray.from_host(np.ascontiguousarray(x))
+        d_y = DeviceArray(4 * 3 * dense.shape[0])
+        plan = Plan([q], [d_x.ptr], [d_y.ptr], batch=3)
+        plan.run()
+        synchronize()
+        check(d_y.download(np.empty((3, dense.shape[0]), np.float32)), expected, bits)
+
+
 def test_huge_group_global_fwht():
     """group > 16384 runs the FWHT as global-memory butterfly stages."""
     bits, group, dim = 4, 32768, 40000
