@@ -10,6 +10,7 @@
 // multi-matrix plans, memory/stream/event helpers and a thread-local error.
 #include "abi_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -437,6 +438,7 @@ struct Plan {
     const Matrix *first = nullptr;
     Staging st;
     bool staged = false;  // a chained producer left this plan's prepared input since its last run
+    int inputs = 0;       // distinct int8 inputs prepared per run: 1 when every matrix reads the same x
 };
 
 static void plan_upload(Plan &p) {
@@ -463,18 +465,22 @@ static void plan_upload(Plan &p) {
         p.xscale.reserve(size_t(p.count) * p.batch * m.groups);
         p.xscale_t.reserve(size_t(p.count) * p.batch * m.groups);
         std::vector<SdotJob> jobs(p.count);
+        // matrices reading one input (a Q|K|V plan) share one prepared copy of it
+        const bool shared = std::all_of(p.xs_in.begin(), p.xs_in.end(), [&](const float *x) { return x == p.xs_in[0]; });
+        p.inputs = shared ? 1 : p.count;
         for (int i = 0; i < p.count; ++i) {
             const Matrix &mi = p.sd[i]->m;
+            const size_t k = shared ? 0 : size_t(i);  // staging slot of matrix i's input
             jobs[i] = SdotJob{mi.codes.p,
                               mi.norms.p,
-                              p.q.p + size_t(i) * p.batch * m.dev / 4,
-                              p.xscale.p + size_t(i) * p.batch * m.groups,
+                              p.q.p + k * p.batch * m.dev / 4,
+                              p.xscale.p + k * p.batch * m.groups,
                               p.ys[i],
                               mi.out,
                               mi.n_pad,
                               block,
                               p.batch,
-                              p.xscale_t.p + size_t(i) * p.batch * m.groups,
+                              p.xscale_t.p + k * p.batch * m.groups,
                               0,
                               p.xs_in[i]};
             block += mi.n_pad / kRowsPerBlock;
@@ -492,11 +498,11 @@ static void plan_upload(Plan &p) {
 // batch row) input into the plan's staging (q, xscale, xscale_t).
 static void plan_prepare(Plan &p, hipStream_t s) {
     const Matrix &m = *p.first;
-    if (!launch_sdot_prepare(nullptr, p.xptr.p, p.batch, p.count * p.batch, m.in, m.padded, m.dev, m.group,
+    if (!launch_sdot_prepare(nullptr, p.xptr.p, p.batch, p.inputs * p.batch, m.in, m.padded, m.dev, m.group,
                              m.scale, m.kind, p.q.p, p.xscale.p, p.xscale_t.p, s)) {
-        for (int i = 0; i < p.count; ++i)
+        for (int i = 0; i < p.inputs; ++i)
             m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
-        launch_sdot_quantize(p.rot.p, m.dev, p.count * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
+        launch_sdot_quantize(p.rot.p, m.dev, p.inputs * p.batch, m.padded, m.dev, m.group, m.kind, p.q.p,
                              p.xscale.p, s);
     }
 }
