@@ -23,8 +23,8 @@ struct KvStoreArgs {
 // The slot range is cut into `splits` pieces of slots_per_split; with more
 // than one split, per-split records go to part and a merge pass writes out.
 struct AttnArgs {
-    const int8_t *k8, *v8;
-    const float *ks, *vs;
+    int8_t *k8, *v8;       // the layer's cache (read; written only for new_k / new_v)
+    float *ks, *vs;
     const float *q;
     float *out;
     float *part;           // [seqs * heads][splits][head_dim + 2]

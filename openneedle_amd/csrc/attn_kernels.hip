@@ -228,10 +228,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         if (wave == 0) {
             const size_t src = (static_cast<size_t>(seq) * a.kvheads + kh) * HD;
             const size_t dst = row0 + ns;
-            // the cache rows this call writes (the block's own context)
-            store_kv_row(a.new_k + src, a.new_v + src, HD, lane, const_cast<int8_t *>(a.k8) + dst * HD,
-                         const_cast<int8_t *>(a.v8) + dst * HD, const_cast<float *>(a.ks) + dst,
-                         const_cast<float *>(a.vs) + dst);
+            store_kv_row(a.new_k + src, a.new_v + src, HD, lane, a.k8 + dst * HD, a.v8 + dst * HD, a.ks + dst,
+                         a.vs + dst);
         }
         __syncthreads();
     };
