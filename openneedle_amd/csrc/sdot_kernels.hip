@@ -1553,12 +1553,31 @@ void launch_sdot_ks16_kind(const SdotGeom &g, const SdotJob &job0, const SdotJob
     else launch_sdot_ks16_waves<KIND, MB, PREP, 8>(g, job0, jobs, njobs, blocks, batch, po, s);
 }
 
+// 32-row workgroups (two MFMA chains per wave) from 4 row tiles and 16
+// groups: fewer, fuller workgroups for the larger decode projections (Q|K|V
+// 1536 x 512 g32 at 64 sequences: 5.2 -> 4.8 us); otherwise the 16-row form
+// keeps more workgroups (a 512 x 2048 down projection: 6.7 vs 7.8 us; a
+// 32-token chunk's 1536 x 512 g128 projection, 4 groups: engine prefill
+// 27.3-27.8 K vs 26.9-27.0 K tokens/s). NEEDLE2_GPU_INT8_KS16_ROWS = 16 / 32
+// overrides.
+static int ks16_rows(const SdotGeom &g, int blocks) {
+    const char *mode = std::getenv("NEEDLE2_GPU_INT8_KS16_ROWS");
+    if (mode && std::strcmp(mode, "16") == 0) return 16;
+    if (mode && std::strcmp(mode, "32") == 0) return 32;
+    return blocks >= 4 && g.groups >= 16 ? 32 : 16;
+}
+
 bool launch_sdot_ks16(const SdotGeom &g, const SdotJob &job0, const SdotJob *jobs, int njobs, int blocks, int batch,
                       hipStream_t s) {
     if (g.group < 32 || g.group > kWindow) return false;
     const PrepOut none{};
-    if (g.kind == kNib) launch_sdot_ks16_kind<kNib, 1, false>(g, job0, jobs, njobs, blocks, batch, none, s);
-    else launch_sdot_ks16_kind<kCrumb, 1, false>(g, job0, jobs, njobs, blocks, batch, none, s);
+    if (ks16_rows(g, blocks) == 32) {
+        if (g.kind == kNib) launch_sdot_ks16_kind<kNib, 2, false>(g, job0, jobs, njobs, blocks, batch, none, s);
+        else launch_sdot_ks16_kind<kCrumb, 2, false>(g, job0, jobs, njobs, blocks, batch, none, s);
+    } else {
+        if (g.kind == kNib) launch_sdot_ks16_kind<kNib, 1, false>(g, job0, jobs, njobs, blocks, batch, none, s);
+        else launch_sdot_ks16_kind<kCrumb, 1, false>(g, job0, jobs, njobs, blocks, batch, none, s);
+    }
     return true;
 }
 

@@ -99,7 +99,7 @@ def test_int8_plan_many_matrices():
 
 
 @pytest.mark.parametrize("mode", ["tile16", "quad", "always", "never", "ksplit", "ksplit_w8", "ksplit_w16",
-                                  "ksplit32", "ksplit32_w16"])
+                                  "ksplit_r16", "ksplit_r32", "ksplit32", "ksplit32_w16"])
 @pytest.mark.parametrize("bits,group,batch", [(4, 32, 3), (4, 32, 9), (4, 32, 17), (4, 32, 33), (4, 32, 64),
                                               (4, 64, 40), (4, 128, 12), (4, 256, 5), (2, 32, 8), (2, 32, 33),
                                               (2, 64, 20), (4, 8, 6), (4, 16, 16), (2, 16, 2), (4, 32, 2)])
@@ -109,13 +109,16 @@ def test_int8_batched_tiles_bit_exact(bits, group, batch, mode, monkeypatch):
     quad kernel), 4 x 4 x 4 int8 MFMA batch tiles of up to 16 rows, one lane per weight row (quad: ragged last
     quad and tile), 32 x 32 x 32 int8 MFMA tiles of 32 batch rows (always), v_dot4 batch tiles (never) and the
     K split on 16 x 16 tiles (ksplit; 4-bit codes, else 32 x 32; over 8 or 16 waves per tile by the group
-    count, or forced: ksplit_w8 / ksplit_w16) and on 32 x 32 tiles (ksplit32, ksplit32_w16); 300 ragged
-    weight rows, zero / one-hot activation rows: bit-exact with the oracle."""
+    count, or forced: ksplit_w8 / ksplit_w16; 16- or 32-row workgroups: ksplit_r16 / ksplit_r32) and on
+    32 x 32 tiles (ksplit32, ksplit32_w16); 300 ragged weight rows, zero / one-hot activation rows: bit-exact
+    with the oracle."""
     if mode.startswith("ksplit"):  # K split over the waves of a tile (small-matrix path)
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "always")
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KS16", "never" if mode.startswith("ksplit32") else "auto")
         if "_w" in mode:
             monkeypatch.setenv("NEEDLE2_GPU_INT8_KS16_WAVES", mode.split("_w")[1])
+        if "_r" in mode:  # 16- or 32-row workgroups of the 16 x 16 K split
+            monkeypatch.setenv("NEEDLE2_GPU_INT8_KS16_ROWS", mode.split("_r")[1])
     else:
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KSPLIT", "never")
         monkeypatch.setenv("NEEDLE2_GPU_INT8_TILE16", "always" if mode == "tile16" else "never")
