@@ -109,6 +109,21 @@ def test_two_window_inputs_window_parallel(bits, dim, monkeypatch):
         check(d_y.download(np.empty((3, dense.shape[0]), np.float32)), expected, bits)
 
 
+@pytest.mark.parametrize("group,dim", [(32, 1000), (128, 1000), (128, 300), (1024, 1500)])
+def test_host_calls_in_a_row(group, dim):
+    """The host-pointer call reads x from its pinned staging buffer in place (or a device copy of it where a
+    GEMV would re-read a wide row) and writes y straight back: successive calls on one handle with new inputs
+    and growing batches (the staging reallocated) each match the oracle."""
+    packed, norms, cb, dense = example(4, rows=300, dim=dim, group=group, seed=group + dim)
+    q = CQMatrix(packed, norms, dense.shape, 4, group, cb)
+    for k, batch in enumerate((1, 1, 3, 2, 7, 1)):
+        x = activations((batch, dim), seed=100 + k)
+        check(q.matvec(x), oracle.cq_linear(packed, norms, dense.shape, 4, group, cb, x, 4), 4)
+        if group <= 256 and group >= 16:
+            want = oracle.sdot_linear(packed, norms, dense.shape, 4, group, cb, x)
+            np.testing.assert_array_equal(q.matvec_int8(x), want)
+
+
 def test_huge_group_global_fwht():
     """group > 16384 runs the FWHT as global-memory butterfly stages."""
     bits, group, dim = 4, 32768, 40000
