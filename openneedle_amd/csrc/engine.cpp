@@ -335,12 +335,14 @@ struct GpuEngine {
     DevBuf<float> logits, embed_z, row_scratch, engram_scratch;
     DevBuf<float> attn_scores;  // fp32-KV attention scores past the LDS budget
     HostBuf<float> hlogits, hhidden;
+    HostBuf<float> hstep;  // a decode step's logits, written by the LM head kernel itself (pinned)
     std::vector<Projection> mhc_proj, qkvg, oproj;
     std::vector<std::array<int, 3>> mhc_row;
     const float *phi[3] = {nullptr, nullptr, nullptr};  // dense mHC matrices (null: CQ)
     int mhc_rows[3] = {0, 0, 0};
     std::vector<Projection> engram_kv;
     Projection lm_head;
+    Projection lm_head_host;  // the LM head of one token into hstep: no device-to-host copy in a step
     Staging st;  // the engine's own staging (candidate rows)
 
     int ti(int l) const { return 1 + 14 * l; }
@@ -625,6 +627,10 @@ void GpuEngine::build_projections() {
     }
     lm_head.add(mats[0], 0, c.vocab, logits.p, c.vocab);
     lm_head.finish(b.zf, chunk);
+    hstep.reserve(c.vocab);  // allocated once: the job tables below hold its address
+    lm_head_host = Projection{};
+    lm_head_host.add(mats[0], 0, c.vocab, hstep.p, c.vocab);
+    lm_head_host.finish(b.zf, 1);
 }
 
 // engine.cpp:424-432: the int8 path for the CQ matrices of 2- or 4-bit codes
@@ -1080,16 +1086,14 @@ void GpuEngine::step(int token, float *logits_out, float *hidden_out) {
     hipStream_t s = stream;
     if (logits_out) {
         launch_eng_quantize(b.zf, D, D, abits, 1, s);
-        lm_head.run(s, 1);
-        hlogits.reserve(c.vocab);
-        ND_HIP(hipMemcpyAsync(hlogits.p, logits.p, size_t(c.vocab) * sizeof(float), hipMemcpyDeviceToHost, s));
+        lm_head_host.run(s, 1);  // the GEMV stores the logits in pinned host memory
     }
     if (hidden_out) {
         hhidden.reserve(size_t(c.layers) * D);
         ND_HIP(hipMemcpyAsync(hhidden.p, b.hidden, size_t(c.layers) * D * sizeof(float), hipMemcpyDeviceToHost, s));
     }
     ND_HIP(hipStreamSynchronize(s));
-    if (logits_out) std::memcpy(logits_out, hlogits.p, size_t(c.vocab) * sizeof(float));
+    if (logits_out) std::memcpy(logits_out, hstep.p, size_t(c.vocab) * sizeof(float));
     if (hidden_out) std::memcpy(hidden_out, hhidden.p, size_t(c.layers) * D * sizeof(float));
     ++position;
 }
