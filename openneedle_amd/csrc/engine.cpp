@@ -302,6 +302,12 @@ struct Projection {
 
 }  // namespace
 
+template <class T>
+struct BufView {  // a typed range of a buffer owned elsewhere
+    T *p = nullptr;
+    size_t n = 0;
+};
+
 struct GpuEngine {
     EngineConfigC c{};
     int abits = 0, position = 0, prefix = 0, capacity = 0, engring = 1, history_cap = 1;
@@ -328,10 +334,14 @@ struct GpuEngine {
     std::vector<KvLayer> kv;
     std::vector<LayerDev> layer;
     MhcDev mh{};
-    DevBuf<StepParams> params;
-    HostBuf<StepParams> hparams;
-    DevBuf<int64_t> ids;   // per chunk: tokens [chunk], then engram rows [sites][chunk][tables]
-    HostBuf<int64_t> hids;
+    // What a launch reads from the host goes up in one copy: the row ids, then
+    // the StepParams, in one pinned buffer and its device twin; the views
+    // below point into the two.
+    DevBuf<uint8_t> upload;
+    HostBuf<uint8_t> hupload;
+    size_t params_offset = 0;  // bytes of upload before the StepParams
+    BufView<StepParams> params, hparams;
+    BufView<int64_t> ids, hids;  // per chunk: tokens [chunk], then engram rows [sites][chunk][tables]
     DevBuf<float> logits, embed_z, row_scratch, engram_scratch;
     DevBuf<float> attn_scores;  // fp32-KV attention scores past the LDS budget
     HostBuf<float> hlogits, hhidden;
@@ -532,12 +542,18 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     b.rawv = w + orv;
     b.engring = w + oring;
     b.zf = w + ozf;
-    params.reserve(chunk);
-    hparams.reserve(chunk);
-    std::memset(hparams.p, 0, chunk * sizeof(StepParams));
-    ids.reserve(size_t(chunk) * (1 + size_t(sites) * std::max(1, c.tables)));
-    hids.reserve(ids.n);
-    std::memset(hids.p, 0, ids.n * sizeof(int64_t));
+    {
+        const size_t nids = size_t(chunk) * (1 + size_t(sites) * std::max(1, c.tables));
+        params_offset = (nids * sizeof(int64_t) + 255) & ~size_t(255);
+        const size_t bytes = params_offset + size_t(chunk) * sizeof(StepParams);
+        upload.reserve(bytes);
+        hupload.reserve(bytes);
+        std::memset(hupload.p, 0, bytes);
+        ids = {reinterpret_cast<int64_t *>(upload.p), nids};
+        hids = {reinterpret_cast<int64_t *>(hupload.p), nids};
+        params = {reinterpret_cast<StepParams *>(upload.p + params_offset), size_t(chunk)};
+        hparams = {reinterpret_cast<StepParams *>(hupload.p + params_offset), size_t(chunk)};
+    }
     logits.reserve(size_t(chunk) * c.vocab);
     embed_z.reserve(size_t(chunk) * D);
 
@@ -953,8 +969,8 @@ void GpuEngine::set_token(int t, int token) {
 
 // The StepParams and row ids of the first T tokens, to the device.
 void GpuEngine::upload_tokens(int T) {
-    ND_HIP(hipMemcpyAsync(params.p, hparams.p, size_t(T) * sizeof(StepParams), hipMemcpyHostToDevice, stream));
-    ND_HIP(hipMemcpyAsync(ids.p, hids.p, ids.n * sizeof(int64_t), hipMemcpyHostToDevice, stream));
+    ND_HIP(hipMemcpyAsync(upload.p, hupload.p, params_offset + size_t(T) * sizeof(StepParams), hipMemcpyHostToDevice,
+                          stream));
 }
 
 // Engram rows, their quantiser, key / value projections, the conv and the ring
