@@ -1813,13 +1813,15 @@ void launch_sdot_quantize(const float *rot, int rot_stride, int nvec, int padded
     ND_HIP(hipGetLastError());
 }
 
-// 16-row batch tiles from 8 rows up (NEEDLE2_GPU_INT8_TILE16: "always" from
-// 2 rows, "never").
+// 16-row batch tiles from 9 rows up (NEEDLE2_GPU_INT8_TILE16: "always" from
+// 2 rows, "never"). At 8 rows the 4-row quads (two per weight row) measured
+// 162-167 us per 64 x 4096^2 g32 stack against 172-173 us for half-filled
+// 16-row tiles; at 12 rows three quads take 251 us, the tiles 178 us.
 static bool tile16_wanted(int batch) {
     const char *mode = std::getenv("NEEDLE2_GPU_INT8_TILE16");
     if (mode && std::strcmp(mode, "never") == 0) return false;
     if (mode && std::strcmp(mode, "always") == 0) return batch >= 2;
-    return batch >= 8;
+    return batch > 8;
 }
 
 // The K split for small matrices (NEEDLE2_GPU_INT8_KSPLIT "always" / "never") and, within it, the 16 x 16
@@ -1879,7 +1881,7 @@ void launch_sdot_gemv(const SdotGeom &g, const SdotJob &job0, const SdotJob *job
     //    on 16 x 16 tiles at batch 2 and more (NEEDLE2_GPU_INT8_KS16:
     //    "never", or "always" from batch 1);
     //  - one batch row: the barrier-free row kernel (NEEDLE2_GPU_INT8_ROW);
-    //  - 8 or more: batch tiles of 16 rows on v_mfma_i32_16x16x32_i8, every
+    //  - 9 or more: batch tiles of 16 rows on v_mfma_i32_16x16x32_i8, every
     //    code decoded once per tile (NEEDLE2_GPU_INT8_TILE16);
     //  - 2 or more: batch tiles of up to 16 rows on v_mfma_i32_4x4x4_16b_i8,
     //    one lane per weight row, every code decoded once per tile
