@@ -129,8 +129,10 @@ int needle2_gpu_sdot_linear_device(void *sdot_handle, const float *d_x, float *d
 /* The int32 group dots of the int8 product (the accumulators of SdotCQ::dot_group,
  * needle2/csrc/sdot.cpp:108-137): d_dots[b][row][g] = sum over group g of
  * centroid(code) * q(x_b), from the kernels needle2_gpu_sdot_linear_device runs
- * for this batch on a large matrix (batch 1: the row kernel; 2 or more: the
- * 4x4x4 batch-tile MFMA kernel). Groups of 8 .. 256. */
+ * for this batch on a large matrix (batch 1: the row kernel; 2 .. 8: the
+ * 4x4x4 batch-tile MFMA kernel; 9 or more: the 16x16x32 batch-tile MFMA
+ * kernel where a group holds whole code chunks, else the 4x4x4 one). Groups
+ * of 8 .. 256. */
 int needle2_gpu_sdot_dots_device(void *sdot_handle, const float *d_x, int32_t *d_dots, int batch, void *stream);
 
 /* No counterpart in the reference: needle2_gpu_sdot_linear_device for callers
@@ -138,8 +140,9 @@ int needle2_gpu_sdot_dots_device(void *sdot_handle, const float *d_x, int32_t *d
  * forbid allocation). The same kernels, with the quantized activations and
  * scales in a static 4 MiB device array the library holds per GPU until the
  * process ends; nothing is allocated. stream NULL: the null stream. Returns -1
- * when batch * (padded input + 8 * groups) bytes (each part rounded up to 256)
- * exceed 4 MiB, or for groups above 16384. All calls on one GPU share the
+ * when batch * (P + 8 * groups) bytes exceed 4 MiB, where P is the input
+ * padded to whole groups and then rounded up to a multiple of 256 (each of the
+ * two parts rounded up to 256 bytes), or for groups above 16384. All calls on one GPU share the
  * array: calls that overlap in time on one GPU race. */
 int needle2_gpu_sdot_linear_device_noalloc(void *sdot_handle, const float *d_x, float *d_y, int batch, void *stream);
 

@@ -249,6 +249,8 @@ void CqHandle::gemm_device(const float *d_x, float *d_y, int m_rows, hipStream_t
             DevBuf<uint4> wide;
             wide.reserve(size_t(m.n_pad) * m.chunks * 2);
             launch_widen_crumbs(m.codes.p, m.chunks, m.n_pad, wide.p, s);
+            // a later call may run on another stream: the copy is published only once it is complete
+            ND_HIP(hipStreamSynchronize(s));
             std::swap(codes4.p, wide.p);
             std::swap(codes4.n, wide.n);
         }

@@ -1075,7 +1075,8 @@ void GpuEngine::run(int tokens) {
             ot = PrepTarget{};
         }
         if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
-        launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, mh, l, ot, s);
+        launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, attn_scores.n, mh, l,
+                              ot, s);
         launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
         oproj[l].run(s, T, o_prepared);
         if (fuse && l + 1 < c.layers) {

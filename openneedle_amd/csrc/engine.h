@@ -107,12 +107,12 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 // Attention + output gate of every kv head over an fp32 or int8 KV cache (kv.k8 set); with `prepared`
 // false (one token) it also does that token's norms, RoPE and KV store, else eng_qk did. scores: null
 // when G * max_length floats fit kEngScoreLds, else a device buffer of tokens * kvheads * G * max_length
-// floats. It also runs layer l's residual routing (Sinkhorn of hres into hroute) in one more workgroup
+// floats (scores_n, checked). It also runs layer l's residual routing (Sinkhorn of hres into hroute) in one more workgroup
 // per token, and prepares the out-projection's int8 input from att when pt.q is set (a group of one kv
 // head's outputs, heads / kvheads * head_dim positions).
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s);
+                           size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s);
 // K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
 void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
                           const EngineDims &d, hipStream_t s);

@@ -540,7 +540,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     p += blockIdx.y;
     const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
     float *sc = GLOBAL_SCORES
-                    ? scores + (static_cast<size_t>(blockIdx.y) * gridDim.x + kh) * G * static_cast<size_t>(max_length)
+                    ? scores + (static_cast<size_t>(blockIdx.y) * d.KV + kh) * G * static_cast<size_t>(max_length)
                     : sc_lds;
     const int wave = t >> 6, lane = t & 63, length = p->length;
     const size_t row0 = static_cast<size_t>(kh) * d.capacity;  // this kv head's first cache row
@@ -1215,7 +1215,10 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s) {
+                           size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s) {
+    // the score slices are [tokens][kv heads][G][max_length] (the routing workgroup touches none)
+    ND_CHECK(!scores || static_cast<size_t>(tokens) * d.KV * (d.H / d.KV) * static_cast<size_t>(max_length) <= scores_n,
+             "internal: attention score buffer smaller than tokens * kv heads * G * max_length");
     ND_CHECK(!pt.q || (pt.group == d.H / d.KV * d.HD && pt.group <= 256 && pt.dev == d.A),
              "internal: attention prepares one kv head's outputs as one group");
     const size_t lds = scores ? 0 : static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);

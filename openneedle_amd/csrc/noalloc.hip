@@ -63,8 +63,10 @@ extern "C" {
 // needle2_gpu_sdot_linear_device with its staging in the library's static
 // scratch: d_x [batch][in] and d_y [batch][out] on the device, enqueued on
 // `stream` (NULL: the null stream). Refused (-1) when
-// batch * (padded input + 8 * groups) bytes, each part rounded up to 256,
-// exceed 4 MiB, or when the group is above the fused prepare's limit.
+// batch * (P + 8 * groups) bytes exceed 4 MiB, P being the input padded to
+// whole groups and then to a multiple of 256 (the device row, m.dev), each
+// of the two parts rounded up to 256 bytes, or when the group is above the
+// fused prepare's limit.
 int needle2_gpu_sdot_linear_device_noalloc(void *sdot_handle, const float *d_x, float *d_y, int batch,
                                            void *stream) {
     return guarded([&] {
@@ -78,7 +80,8 @@ int needle2_gpu_sdot_linear_device_noalloc(void *sdot_handle, const float *d_x, 
         const size_t q_bytes = aligned(size_t(batch) * m.dev);
         const size_t s_bytes = aligned(size_t(batch) * m.groups * sizeof(float));
         ND_CHECK(q_bytes + 2 * s_bytes <= kScratchBytes,
-                 "no-alloc int8 GEMV: batch * (padded input + 8 * groups) bytes exceed the 4 MiB scratch");
+                 "no-alloc int8 GEMV: batch * (input padded to whole groups, then to a multiple of 256, + 8 * groups) "
+                 "bytes exceed the 4 MiB scratch");
         uint8_t *base = scratch_address();
         auto *q = reinterpret_cast<int32_t *>(base);
         auto *xs = reinterpret_cast<float *>(base + q_bytes);

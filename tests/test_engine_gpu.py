@@ -15,6 +15,13 @@ from openneedle_amd.engine import EngineError, GpuEngine
 pytestmark = pytest.mark.gpu
 
 ATOL, RTOL = 2e-5, 2e-4
+# Relative L2 bars of the cases where a quantiser runs on glue output (about ten times the measured error):
+# int8 KV on the small models (measured <= 7e-7), 8-bit activations (3.3e-7), the int8 matmul path against
+# the reference's SDOT path (1.9e-7; released geometry 3.2e-7), a 7000-position int8 context (2.1e-6), and
+# the released geometry's 27 layers with int8 KV, where one K / V code moved by one step in an early layer
+# shows in every later one (2.3e-3).
+INT8_KV_REL, ABITS_REL, SDOT_REL, SDOT_RELEASED_REL, LONG_INT8_REL, RELEASED_INT8_KV_REL = (
+    5e-6, 5e-6, 2e-6, 5e-6, 2e-5, 5e-3)
 SMALL = dict(vocab_size=512, d_model=64, num_heads=2, num_kv_heads=1, num_layers=3, head_dim=32, max_seq_len=64,
              hada_n=64, mhc_lanes=4, engram_slots=32, engram_sub_dim=16, num_engram_tables=4, engram_conv_taps=4,
              engram_conv_dilation=3)
@@ -53,13 +60,13 @@ def test_small_model_fp32_kv(window):
 def test_small_model_int8_kv(window):
     for i, (lg, hd, rl, rh) in enumerate(run_both(small(window, seed=2), TOKENS, int8_kv=True)):
         print(f"step {i}: logits rel {rel_l2(lg, rl):.2e} hidden rel {rel_l2(hd, rh):.2e}", flush=True)
-        assert rel_l2(hd, rh) < 1e-3 and rel_l2(lg, rl) < 1e-3, f"step {i}"
+        assert rel_l2(hd, rh) < INT8_KV_REL and rel_l2(lg, rl) < INT8_KV_REL, f"step {i}"
 
 
 def test_small_model_quantized_activations():
     for i, (lg, hd, rl, rh) in enumerate(run_both(small(0, seed=3), TOKENS[:10], abits=8)):
         print(f"step {i}: logits rel {rel_l2(lg, rl):.2e} hidden rel {rel_l2(hd, rh):.2e}", flush=True)
-        assert rel_l2(hd, rh) < 2e-2 and rel_l2(lg, rl) < 2e-2, f"step {i}"
+        assert rel_l2(hd, rh) < ABITS_REL and rel_l2(lg, rl) < ABITS_REL, f"step {i}"
 
 
 def test_released_geometry():
@@ -69,7 +76,7 @@ def test_released_geometry():
         for i, (lg, hd, rl, rh) in enumerate(run_both(a, TOKENS[:6], int8_kv=int8)):
             print(f"int8={int8} step {i}: logits {np.abs(lg - rl).max():.2e} rel {rel_l2(lg, rl):.2e}", flush=True)
             if int8:  # 27 layers: a code moved by one step in some layer's K / V shows in every later layer
-                assert rel_l2(hd, rh) < 1e-2 and rel_l2(lg, rl) < 1e-2
+                assert rel_l2(hd, rh) < RELEASED_INT8_KV_REL and rel_l2(lg, rl) < RELEASED_INT8_KV_REL
             else:
                 np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL)
                 np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL)
@@ -103,7 +110,7 @@ def test_geometry_variants(name):
         np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL, err_msg=f"logits, step {i}")
     for i, (lg, hd, rl, rh) in enumerate(run_both(a, TOKENS[:8], int8_kv=True)):
         print(f"{name} int8 KV step {i}: logits rel {rel_l2(lg, rl):.2e}", flush=True)
-        assert rel_l2(hd, rh) < 1e-3 and rel_l2(lg, rl) < 1e-3, f"step {i}"
+        assert rel_l2(hd, rh) < INT8_KV_REL and rel_l2(lg, rl) < INT8_KV_REL, f"step {i}"
 
 
 @pytest.mark.parametrize("int8", [False, True])
@@ -132,9 +139,44 @@ def test_long_context(int8):
     for what, g, r in pairs:
         print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
         if int8:  # a rounding difference can move one K / V code by one step (as in the short-context tests)
-            assert rel_l2(g, r) < 1e-3, what
+            assert rel_l2(g, r) < LONG_INT8_REL, what
         else:
             np.testing.assert_allclose(g, r, atol=ATOL, rtol=RTOL, err_msg=what)
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_long_context_full_chunk(int8):
+    """A full 32-token prompt chunk at the end of a 7000-position context (scores in device memory): every token
+    of the chunk has its own score slices ([token][kv head][G][max length]), and the last token's slice ends at
+    the end of the buffer reserved for the chunk. Every token's logits against the reference."""
+    a = Archive(synthetic_model(dict(SMALL, max_seq_len=8192), engram_layers=(1,), engram_orders=(2, 3), group=32,
+                                seed=34))
+    n = 7000
+    rng = np.random.default_rng(71)
+    ids = [int(t) for t in rng.integers(2, 500, n)]
+    shape = (SMALL["num_layers"], n, SMALL["num_kv_heads"], SMALL["head_dim"])
+    k = rng.standard_normal(shape).astype(np.float32)
+    v = rng.standard_normal(shape).astype(np.float32)
+    gpu, ref = GpuEngine(a, kv_cache="int8" if int8 else "fp32"), oracle.RefEngine(a, 0, int8)
+    for e in (gpu, ref):
+        e.import_state(ids, list(range(n)), k, v)
+    chunk = PROMPT[:32]
+    lg, hd = gpu_prefill(gpu, chunk)
+    rl, rh = ref.prefill(chunk, hidden=True)
+    assert lg.shape == rl.shape and lg.shape[0] == 32
+    for what, g, r in [("logits", lg, rl), ("hidden", hd, rh)]:
+        print(f"full chunk {what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
+        if int8:
+            assert rel_l2(g, r) < LONG_INT8_REL, what
+        else:
+            np.testing.assert_allclose(g, r, atol=ATOL, rtol=RTOL, err_msg=what)
+    # the steps after the chunk read the cache rows the chunk stored
+    for t in (5, 400):
+        g, r = gpu.step(t, hidden=True), ref.step(t, hidden=True)
+        if int8:
+            assert rel_l2(g[0], r[0]) < LONG_INT8_REL
+        else:
+            np.testing.assert_allclose(g[0], r[0], atol=ATOL, rtol=RTOL, err_msg=f"step {t}")
 
 
 def test_candidates_equal_full_logits():
@@ -188,7 +230,7 @@ def test_prefill_matches_reference(window, prefix, int8):
     for what, g, r in pairs:
         print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
         if int8:
-            assert rel_l2(g, r) < 1e-3, what
+            assert rel_l2(g, r) < INT8_KV_REL, what
         else:
             np.testing.assert_allclose(g, r, atol=ATOL, rtol=RTOL, err_msg=what)
 
@@ -248,7 +290,7 @@ def test_sdot_matches_reference(window, int8_kv):
                   (f"step {t} candidates", gpu_project(gpu, ids), ref.project_candidates(ids))]
     for what, g, r in pairs:
         print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
-        assert rel_l2(g, r) < 2e-3, what  # measured <= 3e-7
+        assert rel_l2(g, r) < SDOT_REL, what
 
 
 @pytest.mark.parametrize("window", [0, 8])
@@ -279,11 +321,11 @@ def test_sdot_released_geometry():
     lg, _ = gpu_prefill(gpu, TOKENS[:8], last_only=True)
     rl, _ = ref.prefill(TOKENS[:8], last_only=True)
     print(f"prefill rel {rel_l2(lg, rl):.2e}", flush=True)
-    assert rel_l2(lg, rl) < 1e-2
+    assert rel_l2(lg, rl) < SDOT_RELEASED_REL
     for t in (5, 77):
         g, r = gpu.step(t)[0], ref.step(t)[0]
         print(f"step {t}: rel {rel_l2(g, r):.2e}", flush=True)
-        assert rel_l2(g, r) < 1e-2
+        assert rel_l2(g, r) < SDOT_RELEASED_REL
 
 
 @pytest.mark.parametrize("kv", ["fp32", "int8"])
@@ -311,8 +353,9 @@ def test_prefix_snapshot_restore(kv):
         lg, _ = gpu_prefill(gpu, ids[20:35])
         rl, _ = ref.prefill(ids[20:35])
         firsts.append(lg)
+        print(f"restored prefix, continuation: rel {rel_l2(lg, rl):.2e}", flush=True)
         if int8:
-            assert rel_l2(lg, rl) < 1e-3
+            assert rel_l2(lg, rl) < INT8_KV_REL
         else:
             np.testing.assert_allclose(lg, rl, atol=ATOL, rtol=RTOL)
     np.testing.assert_array_equal(firsts[0], firsts[1])
@@ -396,7 +439,7 @@ def test_import_matches_reference(window, prefix, kv):
         g, r = gpu.step(t, hidden=True), ref.step(t, hidden=True)
         print(f"step {t}: rel {rel_l2(g[0], r[0]):.2e}", flush=True)
         if kv == "int8":
-            assert rel_l2(g[0], r[0]) < 1e-3 and rel_l2(g[1], r[1]) < 1e-3
+            assert rel_l2(g[0], r[0]) < INT8_KV_REL and rel_l2(g[1], r[1]) < INT8_KV_REL
         else:
             np.testing.assert_allclose(g[0], r[0], atol=ATOL, rtol=RTOL)
             np.testing.assert_allclose(g[1], r[1], atol=ATOL, rtol=RTOL)

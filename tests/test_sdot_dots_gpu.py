@@ -2,8 +2,8 @@
 reference's dot_group arithmetic (sdot.cpp:108-137) as the oracle restates it (nd_sdot_dots, itself pinned
 against the integer closed form sum(clip(rint(cb / cs)) * clip(rint(rot / scale))) in tests/test_oracle.py):
 bit-exact on every (batch row, weight row, group), on the kernels the GEMV runs for the batch (batch 1: the
-row kernel; 2 .. 7: the 4 x 4 x 4 batch-tile MFMA kernel; 8 or more: the 16 x 16 x 32 batch-tile MFMA kernel
-where the group holds whole code chunks)."""
+row kernel; 2 .. 8: the 4 x 4 x 4 batch-tile MFMA kernel; 9 or more: the 16 x 16 x 32 batch-tile MFMA kernel
+where the group holds whole code chunks, else the 4 x 4 x 4 one)."""
 import numpy as np
 import pytest
 
