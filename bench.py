@@ -37,7 +37,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "CQ4/CQ2 GEMV effective HBM GB/s (% of peak); decode tokens/s at batch 1/64"
 HBM_PEAK_GBS = 8000.0
-HEADLINE_KERNEL = "cq_gemv_quad_kernel<0, 32>"
+HEADLINE_KERNEL = "cq_gemv_quad_kernel<0, 32, false>"
 
 
 def measured_traffic(kernel):
