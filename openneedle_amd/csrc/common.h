@@ -109,6 +109,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
+// Cache policy of the GEMV kernels' weight-code loads: non-temporal ("nt",
+// the buffer load's cache-policy bit 1). Each code chunk is read once per
+// call, and every load instruction reads whole lines (a wave's lanes cover
+// contiguous 16-byte pieces). On MI355X a streaming probe of the GEMVs'
+// pattern (512 workgroups, each walking its own 1.18 MB row tile) read
+// 604 MB in 101 us with plain loads and in 88.6 us with nt ones (plain
+// grid-stride streaming: 86 us); the 16 x CQ4 8192 x 8192 GEMV went from
+// 111-112 to 104-106 us, the int8 batch-1 stack from 108 to 95 us. Norm
+// loads (2 bytes per lane) keep the default policy (measured slightly
+// slower with nt), and so do the attention's K / V rows, whose lanes read
+// each 64-byte row in four 16-byte pieces (24.7 -> 30.4 us with nt).
+constexpr int kStreamLoad = 2;
+
 #ifndef ND_ROWS
 #define ND_ROWS 256
 #endif

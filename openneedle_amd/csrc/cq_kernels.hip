@@ -273,7 +273,8 @@ __device__ __forceinline__ void load_window(WindowState<KIND, GROUP> &st, __amdg
     const uint32_t norm_lane = threadIdx.x * 2u;
 #pragma unroll
     for (int c = 0; c < C; ++c)
-        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * kRowsPerBlock * 16, 0);
+        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * kRowsPerBlock * 16,
+                                                             kStreamLoad);
     // group indices are clamped (phantom groups past the last are never closed)
     if constexpr (GROUP > 0) {
 #pragma unroll
@@ -952,7 +953,7 @@ __device__ __forceinline__ u32x4 quad_chunk(__amdgpu_buffer_rsrc_t codes, int w,
     constexpr int C = TableShape<KIND>::kChunksPerWindow;
     const int soff =
         __builtin_amdgcn_readfirstlane((w * C + q * QuadShape<KIND, GROUP>::kChunks + c) * kRowsPerBlock * 16);
-    return __builtin_amdgcn_raw_buffer_load_b128(codes, r * 16u, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(codes, r * 16u, soff, kStreamLoad);
 }
 
 template <int KIND, int GROUP>

@@ -171,7 +171,7 @@ __device__ __forceinline__ void sdot_load(SdotWindow<KIND, GROUP> &st, __amdgpu_
     const uint32_t code_lane = threadIdx.x * 16u, norm_lane = threadIdx.x * 2u;
 #pragma unroll
     for (int c = 0; c < C; ++c)
-        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * CS, 0);
+        st.codes[c] = __builtin_amdgcn_raw_buffer_load_b128(codes, code_lane, (w * C + c) * CS, kStreamLoad);
     if constexpr (GROUP > 0) {
 #pragma unroll
         for (int k = 0; k < NN; ++k)
@@ -661,7 +661,7 @@ __device__ __forceinline__ void row_load(RowSlot<KIND, GROUP> &sl, __amdgpu_buff
                                          __amdgpu_buffer_rsrc_t norms, int c, int groups) {
     using S = RowSlot<KIND, GROUP>;
     sl.code = __builtin_amdgcn_raw_buffer_load_b128(codes, threadIdx.x * 16u,
-                                                   __builtin_amdgcn_readfirstlane(c * kRowsPerBlock * 16), 0);
+                                                   __builtin_amdgcn_readfirstlane(c * kRowsPerBlock * 16), kStreamLoad);
 #pragma unroll
     for (int k = 0; k < S::kNorms; ++k) {
         // the chunk's group (GROUP >= chunk) or its k-th group; phantom groups past the last read the last
@@ -1050,7 +1050,7 @@ __global__ __launch_bounds__(kRowsPerBlock) void sdot_tile16_kernel(SdotJob job0
     auto load = [&](Tile16Slot &sl, int c, bool closes) {
         const int so = __builtin_amdgcn_readfirstlane(c * kRowsPerBlock * 16);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) sl.code[m] = __builtin_amdgcn_raw_buffer_load_b32(codes, cv[m], so, 0);
+        for (int m = 0; m < 4; ++m) sl.code[m] = __builtin_amdgcn_raw_buffer_load_b32(codes, cv[m], so, kStreamLoad);
         if (closes) {
             const int no = __builtin_amdgcn_readfirstlane(c / CPG * kRowsPerBlock * 2);
 #pragma unroll
