@@ -176,6 +176,7 @@ def dist_us(ms):
             "n": int(a.size)}
 
 
+CQ4_STACK_BYTES = 16 * (8192 * 8192 // 2 + 8192 * (8192 // 32) * 2)  # 16 x CQ4 8192^2 g32: codes + fp16 norms
 ATTN_BYTES = 2 * 64 * 2048 * 8 * 64 + 2 * 64 * 2048 * 8 * 4 + 2 * 64 * 8 * 64 * 4  # K, V codes + scales + q, out
 
 
@@ -222,6 +223,44 @@ MFMA_FP16_PEAK_TFLOPS = 2500.0
 
 
 PREFILL_REPEAT = 8  # GEMM launches between one event pair: issued one by one the host is slower than the GEMM
+
+
+def calibration(stream):
+    """The limits the kernels are compared against, measured on this GPU (the library's calibration kernels):
+    the dependent-launch floor, LDS read bytes per clock per CU by lane access width, and the HBM read rate
+    of the GEMVs' per-tile walk (512 workgroups, each reading its own contiguous 1.18 MB tile, as the 16 x
+    8192^2 CQ4 stack) with plain and non-temporal loads, next to grid-stride streaming, over 604 MB passes
+    (three regions read in turn, so no pass finds the previous one in the last-level cache)."""
+    from openneedle_amd.device import DeviceArray, calibrate_launch, calibrate_lds, calibrate_stream
+    out = {"launch_floor_us": round(calibrate_launch(2000, stream), 3)}
+    for w in (4, 8, 16):
+        rate, ghz = calibrate_lds(w, stream)
+        out[f"lds_read_b{8 * w}_bytes_per_clk_per_cu"] = round(rate, 1)
+        out[f"lds_read_b{8 * w}_shader_ghz"] = round(ghz, 3)
+    nbytes = CQ4_STACK_BYTES
+    with DeviceArray(3 * nbytes) as buf:
+        for pattern, name in enumerate(("tile_walk_plain", "tile_walk_nt", "grid_stride_plain", "grid_stride_nt")):
+            us = calibrate_stream(buf, 3 * nbytes, pattern, stream)
+            out[f"{name}_tbs"] = round(nbytes / (us * 1e-6) / 1e12, 3)
+    return out
+
+
+def hipblaslt_prefill_shape(steps=200):
+    """torch.matmul (hipBLASLt) of a plain fp16 GEMM at the prefill GEMM's shape, 512 x 2048 times 2048 x
+    8192 (no dequantisation, fp16 out): mean us per GEMM over `steps` back-to-back calls (torch events)."""
+    import torch
+    a = torch.randn(512, 2048, device="cuda", dtype=torch.float16)
+    b = torch.randn(2048, 8192, device="cuda", dtype=torch.float16)
+    for _ in range(50):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        torch.matmul(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps * 1e3
 
 
 def bench_prefill(steps, warmup, stream):
@@ -712,6 +751,7 @@ def main():
         synchronize()
         log("calibration copy: 1 GiB read + 1 GiB written by copy_kernel")
         del a, b
+        log(f"calibration: {calibration(stream)}")
 
     if args.only == "decode":
         for seqs in (64, 1):
@@ -741,6 +781,14 @@ def main():
         g_p = statistics.mean(g_list)
         log(f"prefill: step {ms_p * 1e3:.1f} us, GEMM {g_p * 1e3:.1f} us "
             f"({PREFILL_FLOP / (g_p * 1e-3) / 1e12:.0f} TFLOP/s)")
+        if args.calibrate:  # torch in a child process (it does not share this process's HIP runtime)
+            res = subprocess.run([sys.executable, "-c", "import bench; print(bench.hipblaslt_prefill_shape())"],
+                                 cwd=ROOT, capture_output=True, text=True, timeout=600)
+            if res.returncode:
+                raise RuntimeError(f"hipBLASLt calibration failed: {res.stderr[-2000:]}")
+            us = float(res.stdout.strip().splitlines()[-1])
+            log(f"hipBLASLt fp16 GEMM at the same shape (torch.matmul, no dequantisation): {us:.1f} us "
+                f"({PREFILL_FLOP / (us * 1e-6) / 1e12:.0f} TFLOP/s)")
         return
     if args.only == "attn":
         for splits in ((0, 1, 2, 4, 8) if args.sweep else (0,)):
@@ -769,6 +817,9 @@ def main():
     log(f"CQ4 step {ms * 1e3:.1f} us ({value:.0f} GB/s); GEMV kernel {gemv} us ({achieved:.0f} GB/s)")
 
     extra = {}
+    # the measured limits beside the nominal peaks: launch floor, LDS rates, HBM streaming ceilings
+    extra["calibration"] = calibration(stream)
+    log(f"calibration: {extra['calibration']}")
     if not args.no_extra:
         # The reference's host-pointer call on one CQ4 8192x8192 matrix, cycling over the 48 resident copies.
         flat = [m for rot in cq4.mats for m in rot]

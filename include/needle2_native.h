@@ -207,6 +207,20 @@ int needle2_gpu_memset(void *dst, int value, size_t bytes);
 /* Streaming copy kernel (16 B per lane per step; bytes rounded down to 16), the
  * reference point for scaling hardware byte counters to HBM bytes. */
 int needle2_gpu_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
+/* Hardware calibration (no counterpart in the reference: the measured limits
+ * the kernels are compared against). calib_launch: microseconds per launch of
+ * an empty kernel issued `launches` times back to back on `stream` (the
+ * dependent-launch floor). calib_lds: LDS read bytes per shader clock per CU
+ * for `width`-byte reads (4, 8, 16; every lane its own column) and the shader
+ * clock of the run. calib_stream: microseconds per pass reading one third of
+ * the `bytes` of d_src (the thirds in turn, so no pass finds the previous one
+ * in the last-level cache; at least 3 * 512 * 48 KiB): pattern 0 / 1 the
+ * GEMVs' walk (512 workgroups, each reading its own contiguous tile front to
+ * back, tiles of whole 48 KiB multiples) with plain / non-temporal loads, 2 /
+ * 3 grid-stride streaming with plain / non-temporal loads. */
+int needle2_gpu_calib_launch(int launches, float *us_per_launch, void *stream);
+int needle2_gpu_calib_lds(int width, float *bytes_per_clk_per_cu, float *shader_ghz, void *stream);
+int needle2_gpu_calib_stream(const void *d_src, size_t bytes, int pattern, float *us, void *stream);
 int needle2_gpu_synchronize(void);
 void *needle2_gpu_stream_create(void);
 void needle2_gpu_stream_destroy(void *stream);

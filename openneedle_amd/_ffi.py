@@ -81,6 +81,9 @@ SIGNATURES: dict[str, tuple] = {
     "needle2_gpu_memcpy": (i32, [vp, vp, sz, i32]),
     "needle2_gpu_memset": (i32, [vp, i32, sz]),
     "needle2_gpu_copy_kernel": (i32, [vp, vp, sz, vp]),
+    "needle2_gpu_calib_launch": (i32, [i32, vp, vp]),
+    "needle2_gpu_calib_lds": (i32, [i32, vp, vp, vp]),
+    "needle2_gpu_calib_stream": (i32, [vp, sz, i32, vp, vp]),
     "needle2_gpu_synchronize": (i32, []),
     "needle2_gpu_stream_create": (vp, []),
     "needle2_gpu_stream_destroy": (None, [vp]),

@@ -979,6 +979,30 @@ int needle2_gpu_copy_kernel(void *dst, const void *src, size_t bytes, void *stre
     return guarded([&] { launch_copy(src, dst, bytes, static_cast<hipStream_t>(stream)); });
 }
 
+// Calibration of the limits the kernels are measured against (no
+// counterpart in the reference).
+int needle2_gpu_calib_launch(int launches, float *us_per_launch, void *stream) {
+    return guarded([&] {
+        ND_CHECK(launches > 0 && us_per_launch, "launch calibration: launches > 0 and an output");
+        *us_per_launch = calib_launch_us(launches, static_cast<hipStream_t>(stream));
+    });
+}
+
+int needle2_gpu_calib_lds(int width, float *bytes_per_clk_per_cu, float *shader_ghz, void *stream) {
+    return guarded([&] {
+        ND_CHECK(width == 4 || width == 8 || width == 16, "LDS calibration: width 4, 8 or 16 bytes");
+        ND_CHECK(bytes_per_clk_per_cu && shader_ghz, "LDS calibration: null output");
+        calib_lds(width, bytes_per_clk_per_cu, shader_ghz, static_cast<hipStream_t>(stream));
+    });
+}
+
+int needle2_gpu_calib_stream(const void *d_src, size_t bytes, int pattern, float *us, void *stream) {
+    return guarded([&] {
+        ND_CHECK(d_src && us && pattern >= 0 && pattern <= 3, "stream calibration: buffer, output, pattern 0-3");
+        *us = calib_stream_us(d_src, bytes, pattern, static_cast<hipStream_t>(stream));
+    });
+}
+
 int needle2_gpu_memset(void *dst, int value, size_t bytes) {
     return guarded([&] { ND_HIP(hipMemset(dst, value, bytes)); });
 }

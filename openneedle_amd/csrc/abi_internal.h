@@ -9,6 +9,10 @@ void launch_transform_big(const float *x, int x_stride, float *rot, int rot_stri
                           int out_limit, int group, float scale, float *scratch, hipStream_t s);
 
 void launch_copy(const void *src, void *dst, size_t bytes, hipStream_t s);
+// calibration (calib_kernels.hip)
+float calib_launch_us(int launches, hipStream_t s);
+void calib_lds(int width, float *bytes_per_clk_per_cu, float *ghz, hipStream_t s);
+float calib_stream_us(const void *src, size_t bytes, int pattern, hipStream_t s);
 
 // fp16 activations of the prefill GEMM in MFMA fragment order: m rounded up to 32 rows
 size_t prefill_xf_halves(int m, int dev);

@@ -200,6 +200,34 @@ def copy_kernel(dst: DeviceArray, src: DeviceArray, nbytes: int, stream: Stream 
     check(_ffi.lib().needle2_gpu_copy_kernel(dst.ptr, src.ptr, int(nbytes), stream_ptr(stream)), "copy kernel")
 
 
+def calibrate_launch(launches: int = 2000, stream: Stream | None = None) -> float:
+    """Microseconds per launch of an empty kernel issued back to back (the dependent-launch floor)."""
+    us = ctypes.c_float()
+    check(_ffi.lib().needle2_gpu_calib_launch(int(launches), ctypes.byref(us), stream_ptr(stream)),
+          "launch calibration")
+    return us.value
+
+
+def calibrate_lds(width: int, stream: Stream | None = None) -> tuple[float, float]:
+    """(LDS read bytes per shader clock per CU for `width`-byte lane reads, shader GHz of the run)."""
+    rate, ghz = ctypes.c_float(), ctypes.c_float()
+    check(_ffi.lib().needle2_gpu_calib_lds(int(width), ctypes.byref(rate), ctypes.byref(ghz), stream_ptr(stream)),
+          "LDS calibration")
+    return rate.value, ghz.value
+
+
+def calibrate_stream(buf: DeviceArray, nbytes: int, pattern: int, stream: Stream | None = None) -> float:
+    """Microseconds per pass reading one third of `nbytes` of `buf` (the thirds in turn): pattern 0 / 1 the
+    GEMVs' per-tile walk with plain / non-temporal loads, 2 / 3 grid-stride streaming with plain /
+    non-temporal loads."""
+    if nbytes > buf.nbytes:
+        raise ValueError("calibration read larger than its buffer")
+    us = ctypes.c_float()
+    check(_ffi.lib().needle2_gpu_calib_stream(buf.ptr, int(nbytes), int(pattern), ctypes.byref(us),
+                                              stream_ptr(stream)), "stream calibration")
+    return us.value
+
+
 def synchronize() -> None:
     check(_ffi.lib().needle2_gpu_synchronize(), "device synchronize")
 
