@@ -63,6 +63,14 @@ __device__ __forceinline__ EngineBufs at_token(EngineBufs b, const EngineDims &d
     return b;
 }
 
+// p[i] for 0 <= i < n, else 0: a buffer load, so a thread past the end takes
+// no branch (a conditional load whose result merges with a default can make
+// the compiler wait for the load right away).
+__device__ __forceinline__ float load_or_zero(const float *p, int n, int i) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(p, static_cast<uint32_t>(n) * 4u),
+                                                                          static_cast<uint32_t>(i) * 4u, 0, 0));
+}
+
 // Block-wide sum / max of one value per thread (every thread gets the result).
 __device__ float block_sum(float v, float *red) {
     v = wave_sum(v, threadIdx.x & 63);
@@ -384,13 +392,28 @@ struct MixArgs {
 
 // Lane gates of layer l from its mHC projections proj (LDS: pre [N], post
 // [N], res [N * N]) into hp (LDS) and b (engine.cpp:980-986).
+// The gate parameters of layer l for lane threadIdx.x < N, loaded ahead of
+// mix_gates.
+struct GateParams {
+    float a_pre, b_pre, a_post, b_post;
+};
 template <int N>
-__device__ __forceinline__ void mix_gates(const EngineBufs &b, const MhcDev &mh, int l, const float *proj, float *hp) {
+__device__ __forceinline__ GateParams gate_params(const MhcDev &mh, int l) {
+    GateParams g{0.0f, 0.0f, 0.0f, 0.0f};
+    if (threadIdx.x < static_cast<unsigned>(N)) {
+        const int n = threadIdx.x;
+        g = GateParams{mh.a_pre[l], mh.b_pre[l * N + n], mh.a_post[l], mh.b_post[l * N + n]};
+    }
+    return g;
+}
+template <int N>
+__device__ __forceinline__ void mix_gates(const EngineBufs &b, const GateParams &gp, int l, const float *proj,
+                                          float *hp) {
     if (threadIdx.x < static_cast<unsigned>(N)) {
         const int n = threadIdx.x;
         const float pre = proj[n], post = proj[N + n];
-        const float hpre = sigmoidf_(mh.a_pre[l] * pre + mh.b_pre[l * N + n] + (n == l % N ? 4.0f : -4.0f));
-        const float hpost = 2.0f * sigmoidf_(mh.a_post[l] * post + mh.b_post[l * N + n] + (n == l % N ? 0.0f : -4.0f));
+        const float hpre = sigmoidf_(gp.a_pre * pre + gp.b_pre + (n == l % N ? 4.0f : -4.0f));
+        const float hpost = 2.0f * sigmoidf_(gp.a_post * post + gp.b_post + (n == l % N ? 0.0f : -4.0f));
         hp[n] = hpre;
         b.hpre[n] = hpre;
         b.hpost[n] = hpost;
@@ -433,7 +456,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, Lay
     for (int task = threadIdx.x; task < 2 * N + N * N; task += blockDim.x)
         proj[task] = task < N ? pre_rows[task] : task < 2 * N ? post_rows[task - N] : res_rows[task - 2 * N];
     __syncthreads();
-    mix_gates<N>(b, mh, m.l, proj, hp);
+    mix_gates<N>(b, gate_params<N>(mh, m.l), m.l, proj, hp);
     __syncthreads();
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
         float sum = 0.0f;
@@ -523,7 +546,10 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b0, Laye
 // quantiser for the new row): s = dot(q, float(k8)) * k_scale * (1 /
 // sqrt(head_dim)), p = softmax(s), out = sum_s (p_s * v_scale_s) * float(v8)
 // (engine.cpp:898-967, as the int8 attention kernel).
-template <bool PREPARED, bool GLOBAL_SCORES, bool I8>
+// WIDE (without PREPARED): head_dim above 128 or more heads than waves (G + 1
+// > 4); otherwise each wave normalises one head from registers loaded ahead
+// of the K prefetch.
+template <bool PREPARED, bool GLOBAL_SCORES, bool I8, bool WIDE = false>
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d,
                                                              float *__restrict__ scores, int max_length, MhcDev mh,
@@ -542,7 +568,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     float *sc = GLOBAL_SCORES
                     ? scores + (static_cast<size_t>(blockIdx.y) * d.KV + kh) * G * static_cast<size_t>(max_length)
                     : sc_lds;
-    const int wave = t >> 6, lane = t & 63, length = p->length;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63, length = p->length;
     const size_t row0 = static_cast<size_t>(kh) * d.capacity;  // this kv head's first cache row
     const float *kc = I8 ? nullptr : kv.k32 + row0 * HD;
     const float *vc = I8 ? nullptr : kv.v32 + row0 * HD;
@@ -554,28 +580,112 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     // first slot unless this kernel stores that row below (the new token's)
     // (loads without branches: an entry past the list reads slot 0 and is not used)
     const SlotMap slot_of(p);
-    const float gate_t = t < G * HD ? b.gate[kh * G * HD + t] : 0.0f;
+    const float gate_t = load_or_zero(b.gate + kh * G * HD, G * HD, t);
+    // The inputs of this wave's first norm / RoPE head (h = wave <= G, head_dim
+    // <= 128: one RoPE pair per lane) and the new V row, loaded before the K
+    // prefetch below so that waiting for them does not wait for it.
+    float nv0 = 0.0f, nv1 = 0.0f, na = 0.0f, nc = 0.0f, nga = 0.0f, ngc = 0.0f, nco = 0.0f, nsi = 0.0f;
+    float vnew = 0.0f;
+    if constexpr (!PREPARED && !WIDE) {  // (every wave loads, without a branch, so the waits below stay exact)
+        const int h = wave <= G ? wave : G;
+        const float *src = h < G ? b.q + (kh * G + h) * HD : b.k + kh * HD;
+        const float *gain = h < G ? ld.q_norm : ld.k_norm;
+        nv0 = load_or_zero(src, HD, lane);
+        nv1 = load_or_zero(src, HD, lane + 64);
+        na = load_or_zero(src, half, lane);
+        nc = load_or_zero(src + half, half, lane);
+        nga = load_or_zero(gain, half, lane);
+        ngc = load_or_zero(gain + half, half, lane);
+        nco = load_or_zero(p->rope_cos, half, lane);
+        nsi = load_or_zero(p->rope_sin, half, lane);
+        if (!I8) vnew = load_or_zero(b.v + kh * HD, HD, t);
+    }
     const int slot_t = t < length ? slot_of(t) : 0;
     const bool k_early = HD == 64 && t < length && (PREPARED || slot_t != p->slot);
     float4 kpre[I8 ? 4 : 16];  // fp32: the row; int8: its 64 codes
     float kpre_s = 0.0f;
-    if (HD == 64) {
+    {  // buffer loads over this kv head's rows (nothing unless head_dim is 64; a thread past the list
+       // reads zeros without a memory request), without a branch
+        const uint32_t rows = HD == 64 ? static_cast<uint32_t>(d.capacity) : 0u;
+        const uint32_t row = t < length ? static_cast<uint32_t>(slot_t) : 0x00800000u;  // past any cache
         if constexpr (I8) {
-            const float4 *k4 = reinterpret_cast<const float4 *>(kc8 + static_cast<size_t>(slot_t) * HD);
+            const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kc8, rows * 64u);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) kpre[c] = k4[c];
-            kpre_s = ksc[slot_t];
+            for (int c = 0; c < 4; ++c)
+                kpre[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, row * 64u, c * 16, 0));
+            kpre_s = load_or_zero(ksc, static_cast<int>(rows), static_cast<int>(row));
         } else {
-            const float4 *k4 = reinterpret_cast<const float4 *>(kc + static_cast<size_t>(slot_t) * HD);
+            const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kc, rows * 256u);
 #pragma unroll
-            for (int c = 0; c < 16; ++c) kpre[c] = k4[c];
+            for (int c = 0; c < 16; ++c)
+                kpre[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, row * 256u, c * 16, 0));
         }
     }
+    // eng_qk_kernel's quantiser for the new K / V rows (same codes and scales), by
+    // the wave that wrote the rotated K row to kw (LDS)
+    auto quantize_new_kv = [&](const float *kw) {
+        const float *vr = b.v + kh * HD;
+        const size_t row = row0 + p->slot;
+        float mk = 0.0f, mv = 0.0f;
+        for (int i = lane; i < HD; i += 64) {
+            mk = fmaxf(mk, fabsf(kw[i]));
+            mv = fmaxf(mv, fabsf(vr[i]));
+        }
+        mk = wave_max(mk, lane);
+        mv = wave_max(mv, lane);
+        const float sk = mk > 0 ? mk / 127.0f : 1.0f, sv = mv > 0 ? mv / 127.0f : 1.0f;
+        const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
+        if (lane == 0) {
+            kv.ks[row] = sk;
+            kv.vs[row] = sv;
+        }
+        for (int i = lane; i < HD; i += 64) {
+            const float qk = fmaxf(-127.0f, fminf(127.0f, rintf(kw[i] * ik)));
+            const float qv = fmaxf(-127.0f, fminf(127.0f, rintf(vr[i] * iv)));
+            kv.k8[row * HD + i] = static_cast<int8_t>(qk);
+            kv.v8[row * HD + i] = static_cast<int8_t>(qv);
+        }
+    };
     if (PREPARED) {  // eng_qk normalised and rotated q and stored K / V
         for (int i = t; i < G * HD; i += blockDim.x) qs[i] = b.q[kh * G * HD + i];
+    } else if constexpr (!WIDE) {
+        // norms + RoPE, one head per wave on the preloaded values (straight-line
+        // code, LDS and global stores apart, so nothing here waits for the
+        // prefetch above): heads 0..G-1 are this block's query heads (into qs),
+        // head G its K row (into the cache; int8: into LDS, then through the
+        // store kernel's quantiser)
+        if (wave <= G) {
+            float ss = 0.0f;
+            ss += nv0 * nv0;
+            if (HD > 64) ss += nv1 * nv1;
+            ss = wave_sum(ss, lane);
+            const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + 1e-6f);
+            const float a = na * r * (1.0f + nga), c = nc * r * (1.0f + ngc);
+            const float lo = a * nco - c * nsi, hi = c * nco + a * nsi;
+            if (wave < G) {
+                if (lane < half) {
+                    qs[wave * HD + lane] = lo;
+                    qs[wave * HD + lane + half] = hi;
+                }
+            } else if constexpr (I8) {
+                float *kw = qs + kMaxG * HD;
+                if (lane < half) {
+                    kw[lane] = lo;
+                    kw[lane + half] = hi;
+                }
+                __builtin_amdgcn_wave_barrier();
+                quantize_new_kv(kw);
+            } else {
+                ND_GLOBAL float *kw = (ND_GLOBAL float *)(kv.k32 + (row0 + p->slot) * HD);
+                if (lane < half) {
+                    kw[lane] = lo;
+                    kw[lane + half] = hi;
+                }
+            }
+        }
+        if (!I8 && t < HD) ((ND_GLOBAL float *)kv.v32)[(row0 + p->slot) * HD + t] = vnew;
     } else {
-    // norms + RoPE: heads 0..G-1 are this block's query heads (into qs), head G its K row (into the cache;
-    // int8: into LDS, then through the store kernel's quantiser)
+    // the general form: any head_dim, several heads per wave
     float *kw = I8 ? qs + kMaxG * HD : kv.k32 + row0 * HD + static_cast<size_t>(p->slot) * HD;
     for (int h = wave; h <= G; h += blockDim.x >> 6) {
         const float *src = h < G ? b.q + (kh * G + h) * HD : b.k + kh * HD;
@@ -591,29 +701,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
             dst[j] = a * co - c * si;
             dst[j + half] = c * co + a * si;
         }
-        if (I8 && h == G) {  // eng_qk_kernel's quantiser for the new K / V rows (same codes and scales)
-            const float *vr = b.v + kh * HD;
-            const size_t row = row0 + p->slot;
-            float mk = 0.0f, mv = 0.0f;
-            for (int i = lane; i < HD; i += 64) {
-                mk = fmaxf(mk, fabsf(kw[i]));
-                mv = fmaxf(mv, fabsf(vr[i]));
-            }
-            mk = wave_max(mk, lane);
-            mv = wave_max(mv, lane);
-            const float sk = mk > 0 ? mk / 127.0f : 1.0f, sv = mv > 0 ? mv / 127.0f : 1.0f;
-            const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
-            if (lane == 0) {
-                kv.ks[row] = sk;
-                kv.vs[row] = sv;
-            }
-            for (int i = lane; i < HD; i += 64) {
-                const float qk = fmaxf(-127.0f, fminf(127.0f, rintf(kw[i] * ik)));
-                const float qv = fmaxf(-127.0f, fminf(127.0f, rintf(vr[i] * iv)));
-                kv.k8[row * HD + i] = static_cast<int8_t>(qk);
-                kv.v8[row * HD + i] = static_cast<int8_t>(qv);
-            }
-        }
+        if (I8 && h == G) quantize_new_kv(kw);
     }
     if (!I8)
         for (int i = t; i < HD; i += blockDim.x) kv.v32[(row0 + p->slot) * HD + i] = b.v[kh * HD + i];
@@ -888,26 +976,17 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
                                            float *hpo, float *nxs, float (&x)[8], F &&after_loads) {
     const int D = d.D, i = threadIdx.x;
     const bool own = i < D;
-    // every load of the kernel, issued before the first wait
-    float proj = 0.0f, gn = 0.0f, bx = 0.0f, u = 0.0f, gh = 0.0f, d1 = 0.0f, d3 = 0.0f;
-    if (own) {
-        proj = b.proj[i];
-        gn = ld.post_norm[i];
-        bx = b.bx[i];
-        u = b.u[i];
-        gh = ld.pre_hada[i];
-        d1 = ld.d1[i];
-        d3 = ld.d3[i];
+    // every load of the kernel, issued before the first wait (threads past D read zeros)
+    float proj = load_or_zero(b.proj, D, i), gn = load_or_zero(ld.post_norm, D, i);
+    float bx = load_or_zero(b.bx, D, i), u = load_or_zero(b.u, D, i);
+    const float gh = load_or_zero(ld.pre_hada, D, i), d1 = load_or_zero(ld.d1, D, i);
+    const float d3 = load_or_zero(ld.d3, D, i);
 #pragma unroll
-        for (int n = 0; n < N; ++n) x[n] = b.x[n * D + i];
-    }
-    const float d2 = i < d.hada ? ld.d2[i] : 0.0f;
-    float route = 0.0f, hpost = 0.0f;
+    for (int n = 0; n < N; ++n) x[n] = load_or_zero(b.x + n * D, D, i);
+    const float d2 = load_or_zero(ld.d2, d.hada, i);
+    // residual routing (computed beside the attention), used by wave 0
     const int lane = threadIdx.x & 63;
-    if (threadIdx.x < 64) {  // residual routing (computed beside the attention): wave 0
-        if (lane < N * N) route = b.hroute[lane];
-        if (lane < N) hpost = b.hpost[lane];
-    }
+    const float route = load_or_zero(b.hroute, N * N, lane), hpost = load_or_zero(b.hpost, N, lane);
     after_loads();
     const float ag = sigmoidf_(ld.attn_gate[0]);
     if (threadIdx.x < 64) {
@@ -1063,18 +1142,27 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     __shared__ float zs[4096], ps[4096];
     __shared__ float proj[2 * 8 + 64];
     const int D = d.D, cols = N * D, c4n = cols / 4;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63, i = threadIdx.x;
     float4 pf[kRowsPF][kPF];
     float x[8];
+    GateParams gp;
+    float nin;
     post_layer<N, kWaves>(b, ld, l, 1, d, red, mlp, hr, hpo, mlp, x, [&] {
+        // buffer loads over each row (wave-uniform): a row past R and columns
+        // past the row read zero, so no load waits behind a branch
 #pragma unroll
         for (int j = 0; j < kRowsPF; ++j) {
             const int r = wave + j * kWaves;
-            const float4 *row = r < R ? mhc_row_ptr(w, r, N, cols) : nullptr;
+            const __amdgpu_buffer_rsrc_t rs =
+                buffer_rsrc(mhc_row_ptr(w, r < R ? r : 0, N, cols), r < R ? static_cast<uint32_t>(c4n) * 16u : 0u);
 #pragma unroll
             for (int k = 0; k < kPF; ++k)
-                pf[j][k] = row && lane + 64 * k < c4n ? row[lane + 64 * k] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                pf[j][k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          rs, static_cast<uint32_t>(lane + 64 * k) * 16u, 0, 0));
         }
+        gp = gate_params<N>(mh, l + 1);
+        nin = load_or_zero(ldn.norm_in, D, i);
     });
     __syncthreads();
     const float4 *nx4 = reinterpret_cast<const float4 *>(mlp);
@@ -1123,7 +1211,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         if (lane == 0) proj[r] = sum;
     }
     __syncthreads();
-    mix_gates<N>(b, mh, l + 1, proj, hp);
+    mix_gates<N>(b, gp, l + 1, proj, hp);
     __syncthreads();
     const bool own = i < D;
     float u = 0.0f;
@@ -1140,7 +1228,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         rms_block(b.bx, b.z, D, ldn.norm_in, red);
     } else {  // rms_block's arithmetic on the registers
         const float r = 1.0f / sqrtf(block_sum(own ? u * u : 0.0f, red) / static_cast<float>(D) + 1e-6f);
-        if (own) b.z[i] = z = u * r * (1.0f + ldn.norm_in[i]);
+        if (own) b.z[i] = z = u * r * (1.0f + nin);
         __syncthreads();
     }
     quantize_block(b.z, D, d.abits, red);
@@ -1224,6 +1312,7 @@ void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLaye
     const size_t lds = scores ? 0 : static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);
     ND_CHECK(lds <= kEngScoreLds, "internal: attention scores exceed the LDS budget without a score buffer");
     const dim3 grid(d.KV + 1, tokens), block(256);  // workgroup KV: the routing
+    const bool wide = d.HD > 128 || d.H / d.KV + 1 > 4;  // the norms' one-head-per-wave form needs neither
     auto go = [&](auto i8) {
         constexpr bool I8 = decltype(i8)::value;
         if (prepared && scores)
@@ -1232,6 +1321,12 @@ void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLaye
         else if (prepared)
             hipLaunchKernelGGL((eng_attn_fused_kernel<true, false, I8>), grid, block, lds, s, b, ld, kv, p, d, nullptr,
                                0, mh, l, pt);
+        else if (wide && scores)
+            hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8, true>), grid, block, 0, s, b, ld, kv, p, d,
+                               scores, max_length, mh, l, pt);
+        else if (wide)
+            hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8, true>), grid, block, lds, s, b, ld, kv, p, d,
+                               nullptr, 0, mh, l, pt);
         else if (scores)
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
                                max_length, mh, l, pt);
