@@ -480,8 +480,65 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b0, Laye
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     p += blockIdx.y;
     const int HD = d.HD, half = HD / 2;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int heads = d.H + d.KV;
+    if (HD <= 128 && heads <= static_cast<int>(blockDim.x >> 6)) {
+        // one head per wave, every input loaded up front (one pair per lane), and the
+        // k-head waves store their rotated K row and the V row into the cache from
+        // registers: the same arithmetic as the general form below
+        if (wave >= heads) return;
+        const int h = wave, kh = h - d.H;
+        float *src = h < d.H ? b.q + h * HD : b.k + kh * HD;
+        const float *gain = h < d.H ? ld.q_norm : ld.k_norm;
+        const float *vr = b.v + (h < d.H ? 0 : kh) * HD;
+        const float v0 = load_or_zero(src, HD, lane), v1 = load_or_zero(src, HD, lane + 64);
+        const float a0 = load_or_zero(src, half, lane), c0 = load_or_zero(src + half, half, lane);
+        const float ga = load_or_zero(gain, half, lane), gc = load_or_zero(gain + half, half, lane);
+        const float co = load_or_zero(p->rope_cos, half, lane), si = load_or_zero(p->rope_sin, half, lane);
+        const float w0 = load_or_zero(vr, HD, lane), w1 = load_or_zero(vr, HD, lane + 64);
+        float ss = 0.0f;
+        ss += v0 * v0;
+        if (HD > 64) ss += v1 * v1;
+        ss = wave_sum(ss, lane);
+        const float r = 1.0f / sqrtf(ss / static_cast<float>(HD) + 1e-6f);
+        const float a = a0 * r * (1.0f + ga), c = c0 * r * (1.0f + gc);
+        const float lo = a * co - c * si, hi = c * co + a * si;  // elements lane and lane + half
+        if (lane < half) {
+            src[lane] = lo;
+            src[lane + half] = hi;
+        }
+        if (h < d.H) return;
+        const size_t row = static_cast<size_t>(kh) * d.capacity + p->slot;
+        if (kv.k32) {
+            ND_GLOBAL float *kc = (ND_GLOBAL float *)(kv.k32 + row * HD);
+            ND_GLOBAL float *vc = (ND_GLOBAL float *)(kv.v32 + row * HD);
+            if (lane < half) {
+                kc[lane] = lo;
+                kc[lane + half] = hi;
+            }
+            if (lane < HD) vc[lane] = w0;
+            if (lane + 64 < HD) vc[lane + 64] = w1;
+        } else {
+            const float mk = wave_max(lane < half ? fmaxf(fabsf(lo), fabsf(hi)) : 0.0f, lane);
+            const float mv = wave_max(fmaxf(fabsf(w0), fabsf(w1)), lane);
+            const float sk = mk > 0 ? mk / 127.0f : 1.0f, sv = mv > 0 ? mv / 127.0f : 1.0f;
+            const float ik = mk > 0 ? 127.0f / mk : 0.0f, iv = mv > 0 ? 127.0f / mv : 0.0f;
+            if (lane == 0) {
+                kv.ks[row] = sk;
+                kv.vs[row] = sv;
+            }
+            auto q8 = [](float x, float inv) {
+                return static_cast<int8_t>(fmaxf(-127.0f, fminf(127.0f, rintf(x * inv))));
+            };
+            if (lane < half) {
+                kv.k8[row * HD + lane] = q8(lo, ik);
+                kv.k8[row * HD + lane + half] = q8(hi, ik);
+            }
+            if (lane < HD) kv.v8[row * HD + lane] = q8(w0, iv);
+            if (lane + 64 < HD) kv.v8[row * HD + lane + 64] = q8(w1, iv);
+        }
+        return;
+    }
     for (int h = wave; h < heads; h += blockDim.x >> 6) {  // one wave per head (q heads, then k heads)
         float *src = h < d.H ? b.q + h * HD : b.k + (h - d.H) * HD;
         const float *gain = h < d.H ? ld.q_norm : ld.k_norm;
