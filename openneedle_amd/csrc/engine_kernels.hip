@@ -643,6 +643,8 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     // prefetch below so that waiting for them does not wait for it.
     float nv0 = 0.0f, nv1 = 0.0f, na = 0.0f, nc = 0.0f, nga = 0.0f, ngc = 0.0f, nco = 0.0f, nsi = 0.0f;
     float vnew = 0.0f;
+    // PREPARED: this thread's query value (G * HD <= 256: one per thread), loaded ahead of the prefetch too
+    const float qpre = PREPARED ? load_or_zero(b.q + kh * G * HD, G * HD, t) : 0.0f;
     if constexpr (!PREPARED && !WIDE) {  // (every wave loads, without a branch, so the waits below stay exact)
         const int h = wave <= G ? wave : G;
         const float *src = h < G ? b.q + (kh * G + h) * HD : b.k + kh * HD;
@@ -704,7 +706,11 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         }
     };
     if (PREPARED) {  // eng_qk normalised and rotated q and stored K / V
-        for (int i = t; i < G * HD; i += blockDim.x) qs[i] = b.q[kh * G * HD + i];
+        if (G * HD <= static_cast<int>(blockDim.x)) {
+            if (t < G * HD) qs[t] = qpre;
+        } else {
+            for (int i = t; i < G * HD; i += blockDim.x) qs[i] = b.q[kh * G * HD + i];
+        }
     } else if constexpr (!WIDE) {
         // norms + RoPE, one head per wave on the preloaded values (straight-line
         // code, LDS and global stores apart, so nothing here waits for the
@@ -771,23 +777,19 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     // The first kPre rows of each thread are loaded here, before the scores and the softmax.
     const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
     const bool sub = r < R;
+    // V loads are buffer loads: an entry past the list reads zeros (offset past the resource)
+    const uint32_t esz = I8 ? 1u : 4u;
+    const __amdgpu_buffer_rsrc_t vres = buffer_rsrc(I8 ? static_cast<const void *>(vc8) : static_cast<const void *>(vc),
+                                                    static_cast<uint32_t>(d.capacity) * HD * esz);
+    auto load_v = [&](int s) -> float4 {
+        const uint32_t off =
+            sub && s < length ? (static_cast<uint32_t>(slot_of(s)) * HD + 4u * c4) * esz : 0xFFFFFFF0u;
+        if constexpr (I8) return int8x4_to_float4(__builtin_amdgcn_raw_buffer_load_b32(vres, off, 0, 0));
+        else return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0));
+    };
     float4 vpre[kPre];
-    {  // buffer loads: an entry past the list reads zeros (offset past the resource)
-        const uint32_t esz = I8 ? 1u : 4u;
-        const __amdgpu_buffer_rsrc_t vres =
-            buffer_rsrc(I8 ? static_cast<const void *>(vc8) : static_cast<const void *>(vc),
-                        static_cast<uint32_t>(d.capacity) * HD * esz);
 #pragma unroll
-        for (int k = 0; k < kPre; ++k) {
-            const int s = r + k * R;
-            const uint32_t off = sub && s < length ? (static_cast<uint32_t>(slot_of(s)) * HD + 4u * c4) * esz
-                                                   : 0xFFFFFFF0u;
-            if constexpr (I8)
-                vpre[k] = int8x4_to_float4(__builtin_amdgcn_raw_buffer_load_b32(vres, off, 0, 0));
-            else
-                vpre[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0));
-        }
-    }
+    for (int k = 0; k < kPre; ++k) vpre[k] = load_v(r + k * R);
     if constexpr (I8) {
         for (int s = t; s < length; s += blockDim.x) {
             const int sl = slot_of(s);
@@ -927,38 +929,30 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     float4 acc[kMaxG];
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    auto accumulate = [&](int s, const float4 &v) {
+    // rows s0, s0 + R, .. in slot order from registers: an entry past the list adds 0 * 0 (its
+    // probability and its zero row)
+    auto accumulate_rows = [&](int s0, const float4 (&v)[kPre]) {
 #pragma unroll
-        for (int g = 0; g < kMaxG; ++g)
-            if (g < G) {
-                const float pr = sc[g * length + s];
-                acc[g].x += pr * v.x;
-                acc[g].y += pr * v.y;
-                acc[g].z += pr * v.z;
-                acc[g].w += pr * v.w;
-            }
+        for (int k = 0; k < kPre; ++k) {
+            const int s = s0 + k * R;
+            const bool use = sub && s < length;
+#pragma unroll
+            for (int g = 0; g < kMaxG; ++g)
+                if (g < G) {
+                    const float pr = use ? sc[g * length + s] : 0.0f;
+                    acc[g].x += pr * v[k].x;
+                    acc[g].y += pr * v[k].y;
+                    acc[g].z += pr * v[k].z;
+                    acc[g].w += pr * v[k].w;
+                }
+        }
     };
-    // the preloaded rows: an entry past the list adds 0 * 0 (its probability and its zero row)
+    accumulate_rows(r, vpre);
+    // the rest kPre rows at a time, every load of a batch in flight together
+    for (int s0 = r + kPre * R; sub && s0 < length; s0 += kPre * R) {
 #pragma unroll
-    for (int k = 0; k < kPre; ++k) {
-        const int s = r + k * R;
-        const bool use = sub && s < length;
-#pragma unroll
-        for (int g = 0; g < kMaxG; ++g)
-            if (g < G) {
-                const float pr = use ? sc[g * length + s] : 0.0f;
-                acc[g].x += pr * vpre[k].x;
-                acc[g].y += pr * vpre[k].y;
-                acc[g].z += pr * vpre[k].z;
-                acc[g].w += pr * vpre[k].w;
-            }
-    }
-#pragma unroll 8
-    for (int s = sub ? r + kPre * R : length; s < length; s += R) {
-        if constexpr (I8)
-            accumulate(s, int8x4_to_float4(reinterpret_cast<const uint32_t *>(vc8 + static_cast<size_t>(slot_of(s)) * HD)[c4]));
-        else
-            accumulate(s, reinterpret_cast<const float4 *>(vc + static_cast<size_t>(slot_of(s)) * HD)[c4]);
+        for (int k = 0; k < kPre; ++k) vpre[k] = load_v(s0 + k * R);
+        accumulate_rows(s0, vpre);
     }
     float4 *wpart = reinterpret_cast<float4 *>(qs);  // [R][G][HD / 4]: R * G * HD = 1024 G floats
     __syncthreads();
