@@ -302,21 +302,47 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     }
 }
 
-// One block per query head: out = sum_i exp(m_i - M) o_i / sum_i exp(m_i - M) l_i.
+// One block per query head: out = sum_i exp(m_i - M) o_i / sum_i exp(m_i - M) l_i, in split order.
+// The records are read kMergeBatch splits at a time, every load of a batch in
+// flight together (buffer loads with the whole offset in the range-checked
+// lane offset: splits past the count read zero and are skipped), so a merge
+// costs one memory round trip per batch, not per split.
+constexpr int kMergeBatch = 16;
 __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ part, float *__restrict__ out,
                                                          int heads_total, int splits, int hd) {
     const int head = blockIdx.x;
-    const float *rec = part + static_cast<size_t>(head) * splits * (hd + 2);
+    const uint32_t stride = static_cast<uint32_t>(hd + 2) * 4u;  // bytes per split record
+    const auto rr = buffer_rsrc(part + static_cast<size_t>(head) * splits * (hd + 2), static_cast<uint32_t>(splits) * stride);
+    auto load = [&](int i, int field) {  // field 0: m, 1: l, 2 + d: o[d]
+        return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             rr, static_cast<uint32_t>(i) * stride + static_cast<uint32_t>(field) * 4u, 0, 0));
+    };
     float M = -INFINITY;
-    for (int i = 0; i < splits; ++i) M = fmaxf(M, rec[i * (hd + 2)]);
+    for (int i0 = 0; i0 < splits; i0 += kMergeBatch) {
+        float m[kMergeBatch];
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k) m[k] = load(i0 + k, 0);
+#pragma unroll
+        for (int k = 0; k < kMergeBatch; ++k)
+            if (i0 + k < splits) M = fmaxf(M, m[k]);
+    }
     for (int d = threadIdx.x; d < hd; d += blockDim.x) {
         float L = 0.0f, O = 0.0f;
-        for (int i = 0; i < splits; ++i) {
-            const float mi = rec[i * (hd + 2)];
-            if (mi == -INFINITY) continue;  // empty split
-            const float f = expf(mi - M);
-            L += f * rec[i * (hd + 2) + 1];
-            O += f * rec[i * (hd + 2) + 2 + d];
+        for (int i0 = 0; i0 < splits; i0 += kMergeBatch) {
+            float m[kMergeBatch], l[kMergeBatch], o[kMergeBatch];
+#pragma unroll
+            for (int k = 0; k < kMergeBatch; ++k) {
+                m[k] = load(i0 + k, 0);
+                l[k] = load(i0 + k, 1);
+                o[k] = load(i0 + k, 2 + d);
+            }
+#pragma unroll
+            for (int k = 0; k < kMergeBatch; ++k) {
+                if (i0 + k >= splits || m[k] == -INFINITY) continue;  // past the count, or an empty split
+                const float f = expf(m[k] - M);
+                L += f * l[k];
+                O += f * o[k];
+            }
         }
         out[static_cast<size_t>(head) * hd + d] = L > 0 ? O * (1.0f / L) : 0.0f;
     }
