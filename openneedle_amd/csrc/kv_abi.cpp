@@ -46,8 +46,11 @@ static void check_layer(const KvHandle &kv, int layer) {
 // (sequence, kv head) pairs already (a large decode batch) there is one split
 // and no merge pass.
 static int auto_splits(int pairs, int length) {
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    static const int cus = [] {  // queried once
+        int dev = 0, n = 256;
+        if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        return n;
+    }();
     const int tiles = (length + 255) / 256;
     const int want = (2 * cus + pairs - 1) / pairs;
     return std::max(1, std::min(want, tiles));
