@@ -90,10 +90,10 @@ def test_decode_layer_b64_against_oracle():
 
 
 @pytest.mark.parametrize("seqs,splits,ks16", [(64, 0, "auto"), (20, 0, "auto"), (64, 2, "auto"), (64, 0, "never"),
-                                              (64, 0, "w8"), (1, 0, "auto")])
+                                              (64, 0, "w8"), (1, 0, "auto"), (1, 3, "auto"), (1, 1, "auto")])
 def test_chained_step_equals_unchained(seqs, splits, ks16, monkeypatch):
-    """Chained runs (fused epilogue preparation on 16- or 8-wave K splits, or the fallback prepare launches)
-    give the unchained bits."""
+    """Chained runs (fused epilogue preparation on 16- or 8-wave K splits, or the fallback prepare launches;
+    at one sequence, with the attention's slot range split or not) give the unchained bits."""
     if ks16 == "w8":
         monkeypatch.setenv("NEEDLE2_GPU_INT8_KS16_WAVES", "8")
     elif ks16 != "auto":
