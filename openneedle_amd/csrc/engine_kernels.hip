@@ -71,6 +71,25 @@ __device__ __forceinline__ float load_or_zero(const float *p, int n, int i) {
                                                                           static_cast<uint32_t>(i) * 4u, 0, 0));
 }
 
+// Reads one dword of every 64-byte line of the first BYTES bytes of the
+// kernel's arguments, all in one round of scalar loads. The compiler otherwise
+// loads argument fields where they are used, and a field indexed at run time
+// (or used late) costs a dependent round trip to memory at the kernel's start
+// for each line not yet in the scalar cache; after this they hit it.
+template <size_t BYTES>
+__device__ __forceinline__ void touch_kernargs() {
+    typedef const __attribute__((address_space(4))) uint32_t karg_t;
+    karg_t *k = (karg_t *)__builtin_amdgcn_kernarg_segment_ptr();
+    constexpr int kLines = (BYTES + 63) / 64;
+    static_assert(kLines <= 12, "arguments of at most 12 lines");
+    uint32_t v[12];
+#pragma unroll
+    for (int i = 0; i < 12; ++i) v[i] = i < kLines ? k[16 * i] : 0u;
+    // one statement uses every value, so every load is in flight before the first wait
+    asm volatile("" ::"s"(v[0]), "s"(v[1]), "s"(v[2]), "s"(v[3]), "s"(v[4]), "s"(v[5]), "s"(v[6]), "s"(v[7]),
+                 "s"(v[8]), "s"(v[9]), "s"(v[10]), "s"(v[11]));
+}
+
 // Block-wide sum / max of one value per thread (every thread gets the result).
 __device__ float block_sum(float v, float *red) {
     v = wave_sum(v, threadIdx.x & 63);
@@ -277,7 +296,7 @@ __device__ void route_wave(const EngineBufs &b, const MhcDev &mh, int l, const E
 // Token tok's int8 input of the target's projection from the vector in v
 // (position p at v[p - v0]; positions at or past n read as zero): groups
 // [g0, g1), one wave per group (prepare_group_wave), waves from w0 on.
-__device__ void prepare_groups(const PrepTarget &pt, const float *v, int v0, int n, int g0, int g1, int w0, int tok,
+__device__ void prepare_groups(PrepTarget pt, const float *v, int v0, int n, int g0, int g1, int w0, int tok,
                                int tokens) {
     const int lane = threadIdx.x & 63, wave = static_cast<int>(threadIdx.x >> 6) - w0;
     const int waves = static_cast<int>(blockDim.x >> 6) - w0;
@@ -384,6 +403,30 @@ struct SlotMap {
 };
 __device__ __forceinline__ int slot_at(const StepParams *p, int s) { return SlotMap(p)(s); }
 
+// SlotMap's slots of s0, s0 + step, .. (step > 0) without a division per entry:
+// past the prefix entries (pos - prefix) mod ring advances by step mod ring,
+// so one remainder is kept and stepped, in straight-line code. Exact for the lists
+// GpuEngine::set_token builds, whose prefix entries lie inside the prefix
+// (prefix_count <= prefix, so entry s < prefix_count is slot s).
+struct SlotWalk {
+    SlotMap m;  // a copy (in registers)
+    int s, step, rem;  // rem = (start + s - prefix_count - prefix) mod ring, in [0, ring)
+    int dstep;         // step mod ring
+    __device__ SlotWalk(const SlotMap &map, int s0, int st) : m(map), s(s0), step(st), dstep(st % map.ring) {
+        const int u = (m.start + s0 - m.prefix_count - m.prefix) % m.ring;
+        rem = u < 0 ? u + m.ring : u;
+    }
+    __device__ int slot() const {
+        const int pos = s < m.prefix_count ? s : m.start + s - m.prefix_count;
+        return s < m.prefix_count || !m.window || pos < m.prefix ? pos : m.prefix + rem;
+    }
+    __device__ void next() {
+        s += step;
+        rem += dstep;
+        rem = rem >= m.ring ? rem - m.ring : rem;
+    }
+};
+
 struct MixArgs {
     int l, nsites;
     int sites[kEngMaxSites];
@@ -477,6 +520,14 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, Lay
 // quantiser of kv_store), and the attention slot list.
 __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d) {
+    struct Args {
+        EngineBufs b0;
+        LayerDev ld;
+        KvLayer kv;
+        const StepParams *p;
+        EngineDims d;
+    };
+    touch_kernargs<sizeof(Args)>();
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     p += blockIdx.y;
     const int HD = d.HD, half = HD / 2;
@@ -611,6 +662,19 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
                                                              const StepParams *__restrict__ p, EngineDims d,
                                                              float *__restrict__ scores, int max_length, MhcDev mh,
                                                              int layer, PrepTarget pt) {
+    struct Args {
+        EngineBufs b0;
+        LayerDev ld;
+        KvLayer kv;
+        const StepParams *p;
+        EngineDims d;
+        float *scores;
+        int max_length;
+        MhcDev mh;
+        int layer;
+        PrepTarget pt;
+    };
+    touch_kernargs<offsetof(Args, pt)>();
     if (blockIdx.x == d.KV) {  // the routing workgroup
         route_wave(at_token(b0, d, blockIdx.y), mh, layer, d);
         return;
@@ -618,7 +682,8 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     constexpr int kMaxG = 8, kPre = 8, kWaves = 4;
     extern __shared__ float sc_lds[];  // [G][length] when the scores fit
     __shared__ float qs[8 * 1024];  // query heads, then the partial outputs [R][G][HD] (1024 G floats)
-    __shared__ float red[kMaxG * kWaves];
+    __shared__ float red[kMaxG * kWaves], red2[kMaxG * kWaves];
+    __shared__ float knew_scale, vnew_scale;  // int8: the new K / V rows' scales
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     p += blockIdx.y;
     const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
@@ -665,7 +730,8 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     float kpre_s = 0.0f;
     {  // buffer loads over this kv head's rows (nothing unless head_dim is 64; a thread past the list
        // reads zeros without a memory request), without a branch
-        const uint32_t rows = HD == 64 ? static_cast<uint32_t>(d.capacity) : 0u;
+        // (uniform: readfirstlane keeps the buffer descriptor in scalar registers)
+        const uint32_t rows = __builtin_amdgcn_readfirstlane(HD == 64 ? static_cast<uint32_t>(d.capacity) : 0u);
         const uint32_t row = t < length ? static_cast<uint32_t>(slot_t) : 0x00800000u;  // past any cache
         if constexpr (I8) {
             const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kc8, rows * 64u);
@@ -680,9 +746,47 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
                 kpre[c] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, row * 256u, c * 16, 0));
         }
     }
+    // values: thread t takes 16-byte column c = t % (HD / 4) of the V rows of slots r, r + R, ..
+    // (r = t / (HD / 4), R = 256 / (HD / 4) subsets), so its loads are all in flight together; the R
+    // partial sums per output then add up in subset order. When HD / 4 does not divide 256 the last
+    // threads (r == R) take no slots and write no partials: R * G * HD <= 1024 G floats fit in qs.
+    const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
+    const bool sub = r < R;
+    const uint32_t esz = I8 ? 1u : 4u;
+    // The one-slot form below (head_dim 64) takes every V row of the thread (2 kPre) and its int8
+    // scale here, ahead of the norms: the new token's row (not stored yet) is marked in vnew_rows and
+    // read from LDS instead. Other head sizes read nothing (an empty resource).
+    constexpr bool kOneSlotForm = !GLOBAL_SCORES && (PREPARED || !WIDE);
+    float4 vall[kOneSlotForm && !I8 ? 2 * kPre : 1];
+    uint32_t vall8[kOneSlotForm && I8 ? 2 * kPre : 1];  // int8: the four codes (converted where used)
+    float vsr[kOneSlotForm && I8 ? 2 * kPre : 1];
+    uint32_t vnew_rows = 0;
+    if constexpr (kOneSlotForm) {
+        // (uniform: readfirstlane keeps the buffer descriptor in scalar registers)
+        const uint32_t rows = __builtin_amdgcn_readfirstlane(HD == 64 ? static_cast<uint32_t>(d.capacity) : 0u);
+        const __amdgpu_buffer_rsrc_t ve =
+            buffer_rsrc(I8 ? static_cast<const void *>(vc8) : static_cast<const void *>(vc), rows * 64u * esz);
+        const int new_slot = PREPARED ? -1 : p->slot;  // (read once: not a scalar load per row)
+        SlotWalk wk(slot_of, r, R);
+#pragma unroll
+        for (int k = 0; k < 2 * kPre; ++k, wk.next()) {
+            const int s = r + k * R;
+            const int sl = wk.slot();
+            const bool live = sub && s < length;
+            vnew_rows |= live && sl == new_slot ? 1u << k : 0u;
+            const uint32_t off = live ? (static_cast<uint32_t>(sl) * 64u + 4u * c4) * esz : 0xFFFFFFF0u;
+            if constexpr (I8) {
+                vall8[k] = __builtin_amdgcn_raw_buffer_load_b32(ve, off, 0, 0);
+                vsr[k] = load_or_zero(vsc, static_cast<int>(rows), live ? sl : static_cast<int>(rows));
+            } else {
+                vall[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ve, off, 0, 0));
+            }
+        }
+    }
     // eng_qk_kernel's quantiser for the new K / V rows (same codes and scales), by
-    // the wave that wrote the rotated K row to kw (LDS)
-    auto quantize_new_kv = [&](const float *kw) {
+    // the wave that wrote the rotated K row to kw (LDS); with kq, the K codes (as
+    // floats) and their scale also go to LDS (kq, knew_scale) for the scores
+    auto quantize_new_kv = [&](const float *kw, float *kq) {
         const float *vr = b.v + kh * HD;
         const size_t row = row0 + p->slot;
         float mk = 0.0f, mv = 0.0f;
@@ -697,12 +801,20 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         if (lane == 0) {
             kv.ks[row] = sk;
             kv.vs[row] = sv;
+            if (kq) {
+                knew_scale = sk;
+                vnew_scale = sv;
+            }
         }
         for (int i = lane; i < HD; i += 64) {
             const float qk = fmaxf(-127.0f, fminf(127.0f, rintf(kw[i] * ik)));
             const float qv = fmaxf(-127.0f, fminf(127.0f, rintf(vr[i] * iv)));
             kv.k8[row * HD + i] = static_cast<int8_t>(qk);
             kv.v8[row * HD + i] = static_cast<int8_t>(qv);
+            if (kq) {
+                kq[i] = qk;
+                kq[HD + i] = qv;  // the V codes, after the K codes
+            }
         }
     };
     if (PREPARED) {  // eng_qk normalised and rotated q and stored K / V
@@ -737,16 +849,22 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
                     kw[lane + half] = hi;
                 }
                 __builtin_amdgcn_wave_barrier();
-                quantize_new_kv(kw);
+                quantize_new_kv(kw, qs + (kMaxG + 1) * HD);
             } else {
                 ND_GLOBAL float *kw = (ND_GLOBAL float *)(kv.k32 + (row0 + p->slot) * HD);
+                float *knew = qs + kMaxG * HD;  // the new row for the scores, from LDS
                 if (lane < half) {
                     kw[lane] = lo;
                     kw[lane + half] = hi;
+                    knew[lane] = lo;
+                    knew[lane + half] = hi;
                 }
             }
         }
-        if (!I8 && t < HD) ((ND_GLOBAL float *)kv.v32)[(row0 + p->slot) * HD + t] = vnew;
+        if (!I8 && t < HD) {
+            ((ND_GLOBAL float *)kv.v32)[(row0 + p->slot) * HD + t] = vnew;
+            qs[(kMaxG + 2) * HD + t] = vnew;  // the new V row for the values, from LDS
+        }
     } else {
     // the general form: any head_dim, several heads per wave
     float *kw = I8 ? qs + kMaxG * HD : kv.k32 + row0 * HD + static_cast<size_t>(p->slot) * HD;
@@ -764,21 +882,13 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
             dst[j] = a * co - c * si;
             dst[j + half] = c * co + a * si;
         }
-        if (I8 && h == G) quantize_new_kv(kw);
+        if (I8 && h == G) quantize_new_kv(kw, nullptr);
     }
     if (!I8)
         for (int i = t; i < HD; i += blockDim.x) kv.v32[(row0 + p->slot) * HD + i] = b.v[kh * HD + i];
     }
     __syncthreads();
-    // values: thread t takes 16-byte column c = t % (HD / 4) of the V rows of slots r, r + R, ..
-    // (r = t / (HD / 4), R = 256 / (HD / 4) subsets), so its loads are all in flight together; the R
-    // partial sums per output then add up in subset order. When HD / 4 does not divide 256 the last
-    // threads (r == R) take no slots and write no partials: R * G * HD <= 1024 G floats fit in qs.
-    // The first kPre rows of each thread are loaded here, before the scores and the softmax.
-    const int cols4 = HD / 4, R = blockDim.x / cols4, c4 = t % cols4, r = t / cols4;
-    const bool sub = r < R;
     // V loads are buffer loads: an entry past the list reads zeros (offset past the resource)
-    const uint32_t esz = I8 ? 1u : 4u;
     const __amdgpu_buffer_rsrc_t vres = buffer_rsrc(I8 ? static_cast<const void *>(vc8) : static_cast<const void *>(vc),
                                                     static_cast<uint32_t>(d.capacity) * HD * esz);
     auto load_v = [&](int s) -> float4 {
@@ -787,6 +897,121 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         if constexpr (I8) return int8x4_to_float4(__builtin_amdgcn_raw_buffer_load_b32(vres, off, 0, 0));
         else return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0));
     };
+    float4 acc[kMaxG];
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // One slot per thread (head_dim 64, scores in LDS, the new K row in LDS or
+    // none): the scores stay in registers through the block max and sum (two
+    // barriers), the probabilities p = e * (1 / sum) are formed where the values
+    // use them, and every V row of the thread (2 kPre for head_dim 64) is loaded
+    // before the softmax. Same arithmetic and order as the general form below.
+    const bool one_slot = kOneSlotForm && HD == 64 && length <= static_cast<int>(blockDim.x);
+    // GG: heads per kv head when it is 1, 2 or 4 (straight-line code over the
+    // heads); kMaxG: G at run time (heads past G skipped)
+    auto one_slot_form = [&](auto gc) {
+        constexpr int GG = decltype(gc)::value;
+        auto head = [&](int g) { return GG < kMaxG || g < G; };
+        float sv[GG];  // scores of slot t (-inf past the list, as the max's start value)
+#pragma unroll
+        for (int g = 0; g < GG; ++g) sv[g] = -INFINITY;
+        if (t < length) {
+            // the prefetched row, or for the new token's slot (not prefetched) the row written to LDS above
+            float4 kf[16];
+            float kscale = 1.0f;
+            if (k_early) {
+                if constexpr (I8) {
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) kf[c] = int8x4_to_float4(__builtin_bit_cast(u32x4, kpre[c / 4])[c % 4]);
+                    kscale = kpre_s;
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) kf[c] = kpre[c];
+                }
+            } else {
+                const float4 *kn = reinterpret_cast<const float4 *>(qs + (I8 ? kMaxG + 1 : kMaxG) * HD);
+#pragma unroll
+                for (int c = 0; c < 16; ++c) kf[c] = kn[c];
+                if constexpr (I8) kscale = knew_scale;
+            }
+#pragma unroll
+            for (int g = 0; g < GG; ++g)
+                if (head(g)) {
+                    const float *q = qs + g * HD;
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) {
+                        dot += q[4 * c] * kf[c].x;
+                        dot += q[4 * c + 1] * kf[c].y;
+                        dot += q[4 * c + 2] * kf[c].z;
+                        dot += q[4 * c + 3] * kf[c].w;
+                    }
+                    sv[g] = fmaxf(-INFINITY, I8 ? dot * kscale * d.scale : dot * d.scale);
+                }
+        }
+#pragma unroll
+        for (int g = 0; g < GG; ++g)
+            if (head(g)) {
+                const float mx = wave_max(sv[g], lane);
+                if (lane == 0) red[g * kWaves + wave] = mx;
+            }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < GG; ++g)
+            if (head(g)) {
+                float m = red[g * kWaves];
+                for (int w = 1; w < kWaves; ++w) m = fmaxf(m, red[g * kWaves + w]);
+                const float e = t < length ? expf(sv[g] - m) : 0.0f;
+                if (t < length) sc[g * length + t] = e;
+                const float den = wave_sum(e, lane);
+                if (lane == 0) red2[g * kWaves + wave] = den;
+            }
+        __syncthreads();
+        float inv[GG];
+#pragma unroll
+        for (int g = 0; g < GG; ++g) {
+            inv[g] = 0.0f;
+            if (head(g)) {
+                float sum = 0.0f;
+                for (int w = 0; w < kWaves; ++w) sum += red2[g * kWaves + w];
+                inv[g] = 1.0f / sum;
+            }
+        }
+        // the new token's V row (and int8 scale) as this block wrote it, from LDS
+        const float4 vnew4 = reinterpret_cast<const float4 *>(qs + (kMaxG + 2) * HD)[c4];
+        const float vnew_s = I8 ? vnew_scale : 0.0f;
+        auto row = [&](int k) {  // k: a compile-time row index after unrolling
+            const int s = r + k * R;
+            const bool use = sub && s < length;
+            const bool nw = (vnew_rows >> k) & 1u;
+            float4 v;
+            if constexpr (I8) v = nw ? vnew4 : int8x4_to_float4(vall8[k]);
+            else v = nw ? vnew4 : vall[k];
+#pragma unroll
+            for (int g = 0; g < GG; ++g)
+                if (head(g)) {
+                    // (read without a branch, so the reads of all rows are in flight together)
+                    float pr = sc[g * length + (use ? s : 0)] * inv[g];
+                    if constexpr (I8) pr = pr * (nw ? vnew_s : vsr[k]);  // p_s * v_scale_s
+                    pr = use ? pr : 0.0f;
+                    acc[g].x += pr * v.x;
+                    acc[g].y += pr * v.y;
+                    acc[g].z += pr * v.z;
+                    acc[g].w += pr * v.w;
+                }
+        };
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) row(k);
+        if (sub && r + kPre * R < length) {
+#pragma unroll
+            for (int k = kPre; k < 2 * kPre; ++k) row(k);
+        }
+    };
+    if (one_slot) {
+        if (G == 1) one_slot_form(std::integral_constant<int, 1>{});
+        else if (G == 2) one_slot_form(std::integral_constant<int, 2>{});
+        else if (G == 4) one_slot_form(std::integral_constant<int, 4>{});
+        else one_slot_form(std::integral_constant<int, kMaxG>{});
+    } else {
     float4 vpre[kPre];
 #pragma unroll
     for (int k = 0; k < kPre; ++k) vpre[k] = load_v(r + k * R);
@@ -926,9 +1151,6 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
             }
         }
     __syncthreads();
-    float4 acc[kMaxG];
-#pragma unroll
-    for (int g = 0; g < kMaxG; ++g) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     // rows s0, s0 + R, .. in slot order from registers: an entry past the list adds 0 * 0 (its
     // probability and its zero row)
     auto accumulate_rows = [&](int s0, const float4 (&v)[kPre]) {
@@ -953,6 +1175,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
 #pragma unroll
         for (int k = 0; k < kPre; ++k) vpre[k] = load_v(s0 + k * R);
         accumulate_rows(s0, vpre);
+    }
     }
     float4 *wpart = reinterpret_cast<float4 *>(qs);  // [R][G][HD / 4]: R * G * HD = 1024 G floats
     __syncthreads();
@@ -1183,6 +1406,17 @@ template <int THREADS, int N>
 __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, LayerDev ld, LayerDev ldn, MhcDev mh,
                                                                int l, DenseRows w, MixArgs m, EngineDims d,
                                                                PrepTarget pt) {
+    struct Args {
+        EngineBufs b0;
+        LayerDev ld, ldn;
+        MhcDev mh;
+        int l;
+        DenseRows w;
+        MixArgs m;
+        EngineDims d;
+        PrepTarget pt;
+    };
+    touch_kernargs<offsetof(Args, pt)>();
     constexpr int kWaves = THREADS / 64, kPF = 8;  // float4 columns per lane held for each prefetched row
     constexpr int R = 2 * N + N * N;              // mHC projection rows
     constexpr int kRowsPF = std::min((R + kWaves - 1) / kWaves, 3);  // rows per wave held in registers
