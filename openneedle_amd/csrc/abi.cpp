@@ -174,7 +174,7 @@ void matrix_gemv(const Matrix &m, Staging &st, const uint4 *codes, const uint16_
         act = st.rot.p;
     }
     const CqJob job{codes, norms, act, d_y, rows, n_pad, 0, batch};
-    launch_cq_gemv(m.geom(), job, nullptr, 0, n_pad / kRowsPerBlock, s, xraw);
+    launch_cq_gemv(m.geom(), job, nullptr, 0, n_pad / kRowsPerBlock, s, xraw, batch);
 }
 
 void CqHandle::run_device(const float *d_x, float *d_y, int batch, hipStream_t s) {
@@ -581,7 +581,8 @@ static void plan_run(Plan &p, hipStream_t s, hipEvent_t gemv_start = nullptr, hi
             for (int i = 0; i < p.count; ++i)
                 m.transform(p.xs_in[i], m.in, p.rot.p + size_t(i) * p.batch * m.dev, p.batch, p.st.big, s);
         if (gemv_start) ND_HIP(hipEventRecord(gemv_start, s));
-        launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s, p.xraw);
+        launch_cq_gemv(m.geom(), CqJob{}, reinterpret_cast<const CqJob *>(p.jobs.p), p.count, p.blocks, s, p.xraw,
+                       p.batch);
         if (gemv_stop) ND_HIP(hipEventRecord(gemv_stop, s));
         return;
     }

@@ -241,9 +241,10 @@ void launch_rot_many(const float *x0, const float *const *xptr, int batch, int n
                      float scale, float *rot, hipStream_t s);
 
 // njobs == 0: one job passed by value (job0); otherwise jobs_dev[0..njobs). x_raw (groups <= 64): the jobs'
-// act is the raw input [batch][in], which the GEMV transforms itself (no launch_rot_many).
+// act is the raw input [batch][in], which the GEMV transforms itself (no launch_rot_many). max_batch: the
+// largest job batch (groups <= 64 take two activation rows per pass over the codes from 2 on).
 void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs_dev, int njobs, int total_blocks,
-                    hipStream_t s, bool x_raw = false);
+                    hipStream_t s, bool x_raw = false, int max_batch = 1);
 // Whether callers give a group <= 64 GEMV of input width `in` the raw input instead of the pre-pass output.
 bool gemv_quad_takes_x(int group, int in);
 

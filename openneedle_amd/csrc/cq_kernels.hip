@@ -1028,9 +1028,10 @@ __device__ __forceinline__ void quad_build(float *__restrict__ T, const float *l
 }
 
 // One quarter window in the reference's order, refilling each spent chunk /
-// norm with window w + 2. Quarter 0 adds closed groups into the row sum;
+// norm with window w + 2 (REFILL; a pass over the same codes for another
+// activation row keeps them). Quarter 0 adds closed groups into the row sum;
 // quarters 1-3 park p_g in P[q - 1][k][r].
-template <int KIND, int GROUP, int QUAD>
+template <int KIND, int GROUP, int QUAD, bool REFILL = true>
 __device__ __forceinline__ void quad_compute(QuadState<KIND, GROUP> &st, const float *T, float *P, int r,
                                              uint32_t mask, float &sum, float &gd, int w, int groups,
                                              __amdgpu_buffer_rsrc_t codes, __amdgpu_buffer_rsrc_t norms) {
@@ -1056,7 +1057,7 @@ __device__ __forceinline__ void quad_compute(QuadState<KIND, GROUP> &st, const f
                 v[dn % (PA + 1)].b[i] = pr.y;
             }
         }
-        if ((dn & 3) == 3) st.codes[dn >> 2] = quad_chunk<KIND, GROUP>(codes, w + 2, QUAD, r, dn >> 2);
+        if (REFILL && (dn & 3) == 3) st.codes[dn >> 2] = quad_chunk<KIND, GROUP>(codes, w + 2, QUAD, r, dn >> 2);
     };
 #pragma unroll
     for (int dn = 0; dn < PA && dn < D; ++dn) issue(dn);
@@ -1080,7 +1081,7 @@ __device__ __forceinline__ void quad_compute(QuadState<KIND, GROUP> &st, const f
                     P[((QUAD - 1) * Q::kGroups + k) * kRowsPerBlock + r] = p;
                 }
                 gd = 0.0f;
-                st.norms[k] = quad_norm<KIND, GROUP>(norms, w + 2, QUAD, r, k);
+                if (REFILL) st.norms[k] = quad_norm<KIND, GROUP>(norms, w + 2, QUAD, r, k);
             }
         }
         asm volatile("" : "+v"(gd), "+v"(sum));
@@ -1100,7 +1101,7 @@ __device__ __forceinline__ void quad_add_parked(const float *P, int r, float &su
 
 // XF: J.act is the raw input ([batch][in]), transformed here (quad_act_x),
 // instead of the pre-pass output ([batch][dev]).
-template <int KIND, int GROUP, int QUAD, bool XF>
+template <int KIND, int GROUP, int QUAD, bool XF, bool PAIRS = false>
 __device__ __forceinline__ void quad_rows(const CqJob &J, const CqGeom &geom, float (*T)[QuadShape<KIND, GROUP>::kFloats],
                                           float (*P)[(kQuads - 1) * QuadShape<KIND, GROUP>::kGroups * kRowsPerBlock],
                                           int blk) {
@@ -1121,8 +1122,70 @@ __device__ __forceinline__ void quad_rows(const CqJob &J, const CqGeom &geom, fl
 #pragma unroll
     for (int i = 0; i < 16; ++i) lut[i] = geom.lut[i];
 
-    for (int b = 0; b < batch; ++b) {
-        const int stride = XF ? geom.in : dev;
+    const int stride = XF ? geom.in : dev;
+    // Two activation rows per pass over the codes (the reference pairs tokens,
+    // cq.cpp:110-152): each window's chunks are loaded once and feed both rows'
+    // tables, row b0 then row b0 + 1 (passes alternate the table and park
+    // buffers; quarter 0 adds a pass's parked groups at the next pass, before
+    // that row's next window). Per row the order of every operation is that of
+    // the one-row loop below, so the outputs are the same bits.
+    int b0 = 0;
+    for (; PAIRS && b0 + 1 < batch; b0 += 2) {
+        const __amdgpu_buffer_rsrc_t rot0 =
+            buffer_rsrc(J.act + static_cast<size_t>(b0) * stride, static_cast<uint32_t>(stride) * 4u);
+        const __amdgpu_buffer_rsrc_t rot1 =
+            buffer_rsrc(J.act + static_cast<size_t>(b0 + 1) * stride, static_cast<uint32_t>(stride) * 4u);
+        // activations of pass q = 2 w + row (past the last window: zeros)
+        auto act = [&](int q) {
+            const __amdgpu_buffer_rsrc_t &rt = (q & 1) ? rot1 : rot0;
+            if constexpr (XF) return quad_act_x<KIND, GROUP>(rt, q >> 1, r, geom.scale);
+            else return quad_act<KIND>(rt, q >> 1, r);
+        };
+        QuadState<KIND, GROUP> cur, nxt;
+        float2 xr = act(0);
+        quad_load<KIND, GROUP>(cur, codes, norms, 0, QUAD, r);
+        quad_load<KIND, GROUP>(nxt, codes, norms, 1, QUAD, r);
+        __syncthreads();  // the previous rows finished with T[0] and P
+        quad_build<KIND, GROUP>(T[0], lut, xr, QUAD, r);
+        xr = act(1);
+        __syncthreads();
+        float sum[2] = {0.0f, 0.0f}, gd = 0.0f;
+        // pass (w, row): table T[row], parked P[row]; at its start quarter 0 adds
+        // the previous pass's parked groups (the other row's, same or previous
+        // window) into that row's sum
+        auto pass = [&](auto rowc, QuadState<KIND, GROUP> &st, int w) {
+            constexpr int row = decltype(rowc)::value;
+            if (QUAD == 0 && (row == 1 || w > 0))
+                quad_add_parked<KIND, GROUP>(P[row ^ 1], r, sum[row ^ 1], row == 1 ? w : w - 1, groups);
+            quad_compute<KIND, GROUP, QUAD, row == 1>(st, T[row], P[row], r, mask, sum[row], gd, w, groups, codes,
+                                                      norms);
+            const int q = 2 * w + row;
+            quad_build<KIND, GROUP>(T[row ^ 1], lut, xr, QUAD, r);
+            xr = act(q + 2);
+            __syncthreads();
+        };
+        const int pairs = windows / 2;
+        for (int it = 0; it < pairs; ++it) {
+            const int w = 2 * it;
+            pass(std::integral_constant<int, 0>{}, cur, w);
+            pass(std::integral_constant<int, 1>{}, cur, w);
+            pass(std::integral_constant<int, 0>{}, nxt, w + 1);
+            pass(std::integral_constant<int, 1>{}, nxt, w + 1);
+        }
+        if (windows & 1) {
+            const int w = windows - 1;
+            pass(std::integral_constant<int, 0>{}, cur, w);
+            pass(std::integral_constant<int, 1>{}, cur, w);
+        }
+        if (QUAD == 0) {
+            quad_add_parked<KIND, GROUP>(P[1], r, sum[1], windows - 1, groups);
+            if (row < rows) {
+                ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0) * rows + row] = sum[0];
+                ((ND_GLOBAL float *)J.y)[static_cast<size_t>(b0 + 1) * rows + row] = sum[1];
+            }
+        }
+    }
+    for (int b = b0; b < batch; ++b) {
         const __amdgpu_buffer_rsrc_t rot =
             buffer_rsrc(J.act + static_cast<size_t>(b) * stride, static_cast<uint32_t>(stride) * 4u);
         auto act = [&](int w) {
@@ -1203,6 +1266,39 @@ __global__ __launch_bounds__(kQuadThreads) __attribute__((amdgpu_waves_per_eu(8,
     }
 }
 
+// The quarter GEMV for batches of two or more rows: rows in pairs over one
+// pass of the codes (each chunk loaded once for both), an odd last row alone.
+// One workgroup per CU (128 VGPRs per lane: the pair loop holds both rows'
+// state and the two tables' pipelines). 16 x CQ4 8192^2 g32: batch 2
+// 203 -> 181 us, batch 4 403 -> 356 us against one row per pass.
+template <int KIND, int GROUP, bool XF>
+__global__ __launch_bounds__(kQuadThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void cq_gemv_quad_pair_kernel(
+    CqJob job0, const CqJob *__restrict__ jobs, int njobs, CqGeom geom) {
+    using Q = QuadShape<KIND, GROUP>;
+    __shared__ __attribute__((aligned(16))) float T[2][Q::kFloats];
+    __shared__ float P[2][(kQuads - 1) * Q::kGroups * kRowsPerBlock];
+    const int blk = blockIdx.x;
+    CqJob J = job0;
+    if (njobs > 0) {
+        const ND_CONST CqJob *cj = (const ND_CONST CqJob *)(jobs);
+        const int j = find_job(cj, njobs, blk);
+        J.codes = cj[j].codes;
+        J.norms = cj[j].norms;
+        J.act = cj[j].act;
+        J.y = cj[j].y;
+        J.rows = cj[j].rows;
+        J.n_pad = cj[j].n_pad;
+        J.block_begin = cj[j].block_begin;
+        J.batch = cj[j].batch;
+    }
+    switch (__builtin_amdgcn_readfirstlane(threadIdx.x / kRowsPerBlock)) {
+    case 0: quad_rows<KIND, GROUP, 0, XF, true>(J, geom, T, P, blk); break;
+    case 1: quad_rows<KIND, GROUP, 1, XF, true>(J, geom, T, P, blk); break;
+    case 2: quad_rows<KIND, GROUP, 2, XF, true>(J, geom, T, P, blk); break;
+    default: quad_rows<KIND, GROUP, 3, XF, true>(J, geom, T, P, blk); break;
+    }
+}
+
 // Activation pre-pass of the quarter GEMV: rot[v][0..dev) = per-group FWHT
 // of zero-padded x (the reference's transform, cq.cpp:153-156, identical
 // butterflies), for nvec = count * batch vectors at once: vector v is row
@@ -1220,9 +1316,32 @@ __global__ __launch_bounds__(kRowsPerBlock) void rot_many_kernel(const float *__
     if (p < dev) rot[static_cast<size_t>(v) * dev + p] = x[0];
 }
 
+// Batches of two or more rows on the 4-bit quarter GEMV take the pair kernel
+// (NEEDLE2_GPU_FP32_PAIRS=never: one row per pass). 2-bit matrices keep one
+// row per pass: their GEMV is bound by the table lookups, which pairs do not
+// reduce, and the pair kernel's one workgroup per CU runs them slower
+// (16 x 8192^2 at batch 2: 132 -> 183 us).
+static bool pairs_wanted(int max_batch) {
+    const char *mode = std::getenv("NEEDLE2_GPU_FP32_PAIRS");
+    return max_batch >= 2 && !(mode && std::strcmp(mode, "never") == 0);
+}
+
 template <int KIND, bool XF>
-void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s) {
+void launch_gemv_kind(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s,
+                      int max_batch) {
     dim3 grid(blocks), block(kRowsPerBlock), split(kSplitThreads), quad(kQuadThreads);
+    if constexpr (KIND == kNib) {  // (2-bit: LDS-bound, one row per pass)
+        if (g.group <= 64 && pairs_wanted(max_batch)) {
+            switch (g.group) {
+            case 8: hipLaunchKernelGGL((cq_gemv_quad_pair_kernel<KIND, 8, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+            case 16: hipLaunchKernelGGL((cq_gemv_quad_pair_kernel<KIND, 16, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+            case 32: hipLaunchKernelGGL((cq_gemv_quad_pair_kernel<KIND, 32, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+            default: hipLaunchKernelGGL((cq_gemv_quad_pair_kernel<KIND, 64, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
+            }
+            ND_HIP(hipGetLastError());
+            return;
+        }
+    }
     switch (g.group > kWindow ? 0 : g.group) {
     case 8: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 8, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
     case 16: hipLaunchKernelGGL((cq_gemv_quad_kernel<KIND, 16, XF>), grid, quad, 0, s, job0, jobs, njobs, g); break;
@@ -1393,16 +1512,16 @@ bool gemv_quad_takes_x(int group, int in) {
 }
 
 void launch_cq_gemv(const CqGeom &g, const CqJob &job0, const CqJob *jobs, int njobs, int blocks, hipStream_t s,
-                    bool x_raw) {
+                    bool x_raw, int max_batch) {
     if (blocks <= 0) return;
     ND_CHECK(!x_raw || g.group <= 64, "internal: raw GEMV input for a group the pre-pass does not serve");
     if (x_raw) {
-        if (g.kind == kNib) launch_gemv_kind<kNib, true>(g, job0, jobs, njobs, blocks, s);
-        else launch_gemv_kind<kCrumb, true>(g, job0, jobs, njobs, blocks, s);
+        if (g.kind == kNib) launch_gemv_kind<kNib, true>(g, job0, jobs, njobs, blocks, s, max_batch);
+        else launch_gemv_kind<kCrumb, true>(g, job0, jobs, njobs, blocks, s, max_batch);
         return;
     }
-    if (g.kind == kNib) launch_gemv_kind<kNib, false>(g, job0, jobs, njobs, blocks, s);
-    else launch_gemv_kind<kCrumb, false>(g, job0, jobs, njobs, blocks, s);
+    if (g.kind == kNib) launch_gemv_kind<kNib, false>(g, job0, jobs, njobs, blocks, s, max_batch);
+    else launch_gemv_kind<kCrumb, false>(g, job0, jobs, njobs, blocks, s, max_batch);
 }
 
 void launch_gather_rows(const uint4 *codes, const uint16_t *norms, int rows, int chunks, int groups,

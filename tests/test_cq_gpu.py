@@ -87,6 +87,28 @@ def test_small_groups_with_and_without_prepass(bits, group, dim, monkeypatch):
         check(d_y.download(np.empty(dense.shape[0], np.float32)), expected[1], bits)
 
 
+@pytest.mark.parametrize("group", [8, 16, 32, 64])
+@pytest.mark.parametrize("batch", [2, 3, 5])
+@pytest.mark.parametrize("dim", [300, 1000])
+def test_batched_rows_in_pairs(group, batch, dim, monkeypatch):
+    """4-bit batches of two or more rows take two rows per pass over the codes (cq_gemv_quad_pair_kernel: the
+    chunks loaded once for both rows' tables, an odd last row alone), for raw inputs (<= 512 wide) and the
+    pre-pass; bit-identical to the oracle and to one row per pass (NEEDLE2_GPU_FP32_PAIRS=never)."""
+    packed, norms, cb, dense = example(4, rows=300, dim=dim, group=group, seed=31 * group + batch)
+    x = activations((batch, dim), seed=group + batch)
+    expected = oracle.cq_linear(packed, norms, dense.shape, 4, group, cb, x, 4)
+    for mode in ("auto", "never"):
+        monkeypatch.setenv("NEEDLE2_GPU_FP32_PAIRS", mode)
+        q = CQMatrix(packed, norms, dense.shape, 4, group, cb)
+        check(q.matvec(x), expected, 4)
+        d_x = DeviceArray.from_host(np.ascontiguousarray(x))
+        d_y = DeviceArray(4 * batch * dense.shape[0])
+        plan = Plan([q], [d_x.ptr], [d_y.ptr], batch=batch)
+        plan.run()
+        synchronize()
+        check(d_y.download(np.empty((batch, dense.shape[0]), np.float32)), expected, 4)
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("dim", [257, 400, 512])
 def test_two_window_inputs_window_parallel(bits, dim, monkeypatch):
