@@ -496,6 +496,14 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
 
     // work buffers (one allocation), `chunk` tokens each
     chunk = c.window ? std::min(kEngMaxChunk, c.window) : kEngMaxChunk;
+    {  // the score buffer of the longest slot list a reset can make (a prefix of up to max_seq)
+        const size_t G = size_t(c.heads / c.kvheads);
+        const size_t longest = size_t(c.window ? c.window + c.max_seq : c.max_seq);
+        if (G * longest * sizeof(float) > kEngScoreLds) {
+            const size_t per_token = size_t(c.kvheads) * G * longest * sizeof(float);
+            chunk = int(std::min<size_t>(chunk, std::max<size_t>(kEngMinChunk, kEngScoreBudget / per_token)));
+        }
+    }
     const int mhc_tiles = 2 * kRowsPerBlock;  // a piece spans at most two row tiles
     const int sites = std::max(1, c.num_sites);
     dims.sites = sites;

@@ -27,9 +27,16 @@ struct StepParams {
     float rope_cos[kEngMaxHalfHd], rope_sin[kEngMaxHalfHd];
 };
 
-// Work buffers hold kEngMaxChunk tokens: token t of a launch is blockIdx.y
-// and its vectors sit t per-token sizes past the token-0 pointers below.
-constexpr int kEngMaxChunk = 32;  // prompt chunk (engine.cpp:1054)
+// Work buffers hold a chunk of tokens: token t of a launch is blockIdx.y and
+// its vectors sit t per-token sizes past the token-0 pointers below.
+// Prompt chunk: at most kEngMaxChunk tokens (engine.cpp:1054 takes 32), every
+// token of a chunk in the same launches; a window model's chunk is at most its
+// window, and long contexts take a shorter chunk (down to 32) that holds the
+// attention-score buffer (chunk * kv heads * G * max length floats) to
+// kEngScoreBudget bytes.
+constexpr int kEngMaxChunk = 256;
+constexpr int kEngMinChunk = 32;
+constexpr size_t kEngScoreBudget = size_t(512) << 20;
 
 struct EngineDims {
     int D, N, H, KV, HD, A, K, hada, layers, tables, subdim, taps, capacity, engring, abits;

@@ -19,17 +19,20 @@ ATOL, RTOL = 2e-5, 2e-4
 # int8 KV on the small models (measured <= 7e-7), 8-bit activations (3.3e-7), the int8 matmul path against
 # the reference's SDOT path (1.9e-7; released geometry 3.2e-7), a 7000-position int8 context (2.1e-6), and
 # the released geometry's 27 layers with int8 KV, where one K / V code moved by one step in an early layer
-# shows in every later one (2.3e-3).
+# shows in every later one (2.3e-3). A 300-token int8-KV prompt: the same code steps, more of them over the
+# longer prompt (3.5e-5, the same with prompt chunks of 32 or 256).
 INT8_KV_REL, ABITS_REL, SDOT_REL, SDOT_RELEASED_REL, LONG_INT8_REL, RELEASED_INT8_KV_REL = (
     5e-6, 5e-6, 2e-6, 5e-6, 2e-5, 5e-3)
+LONG_PROMPT_INT8_REL = 3e-4
 SMALL = dict(vocab_size=512, d_model=64, num_heads=2, num_kv_heads=1, num_layers=3, head_dim=32, max_seq_len=64,
              hada_n=64, mhc_lanes=4, engram_slots=32, engram_sub_dim=16, num_engram_tables=4, engram_conv_taps=4,
              engram_conv_dilation=3)
 TOKENS = [5, 17, 300, 2, 9, 9, 511, 0, 42, 77, 128, 3, 64, 200, 7, 8, 250, 31, 1, 99]
 
 
-def small(window=0, seed=1):
-    return Archive(synthetic_model(SMALL, engram_layers=(1,), engram_orders=(2, 3), kv_window=window, group=32,
+def small(window=0, seed=1, max_seq=None):
+    geometry = SMALL if max_seq is None else dict(SMALL, max_seq_len=max_seq)
+    return Archive(synthetic_model(geometry, engram_layers=(1,), engram_orders=(2, 3), kv_window=window, group=32,
                                    seed=seed))
 
 
@@ -146,9 +149,10 @@ def test_long_context(int8):
 
 @pytest.mark.parametrize("int8", [False, True])
 def test_long_context_full_chunk(int8):
-    """A full 32-token prompt chunk at the end of a 7000-position context (scores in device memory): every token
-    of the chunk has its own score slices ([token][kv head][G][max length]), and the last token's slice ends at
-    the end of the buffer reserved for the chunk. Every token's logits against the reference."""
+    """A full prompt chunk (256 tokens: this model's score buffer fits the budget at the longest chunk) at the end
+    of a 7000-position context (scores in device memory): every token of the chunk has its own score slices
+    ([token][kv head][G][max length]), and the last token's slice ends at the end of the buffer reserved for the
+    chunk. Every token's logits against the reference."""
     a = Archive(synthetic_model(dict(SMALL, max_seq_len=8192), engram_layers=(1,), engram_orders=(2, 3), group=32,
                                 seed=34))
     n = 7000
@@ -160,10 +164,10 @@ def test_long_context_full_chunk(int8):
     gpu, ref = GpuEngine(a, kv_cache="int8" if int8 else "fp32"), oracle.RefEngine(a, 0, int8)
     for e in (gpu, ref):
         e.import_state(ids, list(range(n)), k, v)
-    chunk = PROMPT[:32]
+    chunk = LONG_PROMPT[:256]
     lg, hd = gpu_prefill(gpu, chunk)
     rl, rh = ref.prefill(chunk, hidden=True)
-    assert lg.shape == rl.shape and lg.shape[0] == 32
+    assert lg.shape == rl.shape and lg.shape[0] == 256
     for what, g, r in [("logits", lg, rl), ("hidden", hd, rh)]:
         print(f"full chunk {what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
         if int8:
@@ -199,6 +203,8 @@ def test_candidates_equal_full_logits():
 
 
 PROMPT = [int(t) for t in np.random.default_rng(61).integers(0, 512, 45)]
+# past one prompt chunk of a window-free model (256 tokens): two chunks, the second partial
+LONG_PROMPT = [int(t) for t in np.random.default_rng(63).integers(0, 512, 300)]
 
 
 def gpu_prefill(engine, tokens, last_only=False):
@@ -209,19 +215,21 @@ def gpu_project(engine, ids):
     return engine.project_candidates(ids)
 
 
-@pytest.mark.parametrize("window,prefix", [(0, 0), (8, 0), (8, 3)])
+@pytest.mark.parametrize("window,prefix,long", [(0, 0, False), (0, 0, True), (8, 0, False), (8, 3, False)])
 @pytest.mark.parametrize("int8", [False, True])
-def test_prefill_matches_reference(window, prefix, int8):
-    """A 45-token prompt in chunks (32 tokens, or the window: 8) against the reference's chunked prefill: every
-    token's logits, the last token's hidden states, candidates projected right after (the reference projects
-    the last token's embedding row there) and the steps that follow."""
-    a = small(window, seed=7)
+def test_prefill_matches_reference(window, prefix, long, int8):
+    """A 45-token prompt (one chunk of a window-free model, six of the window: 8) and a 300-token one (chunks of
+    256 and 44) against the reference's chunked prefill (chunks of 32): every token's logits, the last token's
+    hidden states, candidates projected right after (the reference projects the last token's embedding row
+    there) and the steps that follow."""
+    a = small(window, seed=7, max_seq=512 if long else None)
     gpu = GpuEngine(a, kv_cache="int8" if int8 else "fp32")
     ref = oracle.RefEngine(a, 0, int8)
     gpu.reset(prefix)
     ref.reset(prefix)
-    lg, hd = gpu_prefill(gpu, PROMPT)
-    rl, rh = ref.prefill(PROMPT, hidden=True)
+    prompt = LONG_PROMPT if long else PROMPT
+    lg, hd = gpu_prefill(gpu, prompt)
+    rl, rh = ref.prefill(prompt, hidden=True)
     ids = np.array([3, 500, 77, 3], np.int32)
     pairs = [("logits", lg, rl), ("hidden", hd, rh), ("candidates", gpu_project(gpu, ids), ref.project_candidates(ids))]
     for t in (11, 400, 2):
@@ -230,13 +238,13 @@ def test_prefill_matches_reference(window, prefix, int8):
     for what, g, r in pairs:
         print(f"{what}: max {np.abs(g - r).max():.2e} rel {rel_l2(g, r):.2e}", flush=True)
         if int8:
-            assert rel_l2(g, r) < INT8_KV_REL, what
+            assert rel_l2(g, r) < (LONG_PROMPT_INT8_REL if long else INT8_KV_REL), what
         else:
             np.testing.assert_allclose(g, r, atol=ATOL, rtol=RTOL, err_msg=what)
 
 
 def test_prefill_released_geometry():
-    """27 layers of the released geometry (window 256, chunks of 32): a 40-token prompt, last logits only."""
+    """27 layers of the released geometry (window 256, chunks of 256): a 40-token prompt, last logits only."""
     a = Archive(synthetic_released(seed=8, tokenizer_bytes=0))
     tokens = [int(t) for t in np.random.default_rng(62).integers(0, 8192, 40)]
     gpu, ref = GpuEngine(a), oracle.RefEngine(a)
@@ -247,17 +255,19 @@ def test_prefill_released_geometry():
     np.testing.assert_allclose(hd, rh, atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("window", [0, 8])
-def test_prefill_equals_steps(window):
-    """A token's arithmetic does not depend on the launch it shares: prefill equals stepping bit for bit."""
-    a = small(window, seed=6)
+@pytest.mark.parametrize("window,long", [(0, False), (0, True), (8, False)])
+def test_prefill_equals_steps(window, long):
+    """A token's arithmetic does not depend on the launch it shares: prefill equals stepping bit for bit (one
+    chunk, chunks of 256 and 44, chunks of the window)."""
+    a = small(window, seed=6, max_seq=512 if long else None)
+    prompt = LONG_PROMPT if long else PROMPT
     e1, e2 = GpuEngine(a), GpuEngine(a)
-    stepped = np.stack([e1.step(t)[0] for t in PROMPT])
-    np.testing.assert_array_equal(e2.prefill(PROMPT)[0], stepped)
+    stepped = np.stack([e1.step(t)[0] for t in prompt])
+    np.testing.assert_array_equal(e2.prefill(prompt)[0], stepped)
     np.testing.assert_array_equal(e2.step(4)[0], e1.step(4)[0])
     e3 = GpuEngine(a, kv_cache="int8")
     e4 = GpuEngine(a, kv_cache="int8")
-    np.testing.assert_array_equal(e3.prefill(PROMPT, last_only=True)[0], np.stack([e4.step(t)[0] for t in PROMPT])[-1])
+    np.testing.assert_array_equal(e3.prefill(prompt, last_only=True)[0], np.stack([e4.step(t)[0] for t in prompt])[-1])
 
 
 def small64(window=0, seed=9):
