@@ -318,10 +318,11 @@ RELEASED_GEOMETRY = dict(vocab_size=8192, d_model=512, num_heads=8, num_kv_heads
 
 def synthetic_model(geometry: dict, engram_layers=(), engram_orders=(), kv_window: int = 0, group: int = 128,
                     seed: int = 0, heads: bool = False, tokenizer_bytes: int = 0, rope_theta: float = 100000.0,
-                    vector_scale: float = 0.1) -> bytes:
+                    vector_scale: float = 0.1, layer_bits: int = 2) -> bytes:
     """An archive of the given geometry with the released precision map and random contents.
 
-    embedding and mhc_phi* CQ4, attention and engram matrices CQ2 (all at ``group``), everything else FP16;
+    embedding and mhc_phi* CQ4, attention and engram matrices CQ2 (``layer_bits``: CQ4 for the layers'
+    projections instead; all at ``group``), everything else FP16;
     optional probe heads (contrastive with 128 outputs, confidence) and RAW tokenizer. Codes are uniform random
     bytes, norms fp16 U[0.005, 0.05], FP16 values N(0, vector_scale); the codebook is the released header
     codebook."""
@@ -339,7 +340,7 @@ def synthetic_model(geometry: dict, engram_layers=(), engram_orders=(), kv_windo
         if name == "embedding" or name.startswith("mhc_phi"):
             bits = 4
         elif name.startswith(("layer", "engram")) and name.endswith(("_proj", ".tables")):
-            bits = 2
+            bits = layer_bits if name.startswith("layer") else 2
         else:
             bits = 0
         if bits:

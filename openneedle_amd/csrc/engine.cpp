@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <array>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -347,6 +348,7 @@ struct GpuEngine {
     HostBuf<float> hlogits, hhidden;
     HostBuf<float> hstep;  // a decode step's logits, written by the LM head kernel itself (pinned)
     std::vector<Projection> mhc_proj, qkvg, oproj;
+    std::vector<OutProj> ofused;  // per layer: the out-projection inside the attention launch (codes null: not)
     std::vector<std::array<int, 3>> mhc_row;
     const float *phi[3] = {nullptr, nullptr, nullptr};  // dense mHC matrices (null: CQ)
     int mhc_rows[3] = {0, 0, 0};
@@ -377,6 +379,7 @@ struct GpuEngine {
     void set_token(int t, int token);
     void run(int tokens);
     void build_projections();
+    OutProj out_projection(const Projection &p) const;
     void set_sdot();
     void step(int token, float *logits_out, float *hidden_out);
     void prefill(const int *tokens, int num_tokens, bool last_only, float *logits_out, float *hidden_out);
@@ -484,6 +487,7 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     dims.sqrt_d = std::sqrt(float(D));
     dims.inv_hada = 1 / std::sqrt(float(c.hada));
     dims.scale = 1 / std::sqrt(float(HD));
+    dims.ogroups = 0;
     engring = int(int64_t(c.taps - 1) * c.dilation + 1);
     ND_CHECK(engring >= 1, "invalid Engram ring size");
     dims.engring = engring;
@@ -519,13 +523,14 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
                  ohp = take(N), ohq = take(N), ohr = take(N * N), oht = take(N * N), om0 = take(mhc_tiles),
                  om1 = take(mhc_tiles),
                  om2 = take(mhc_tiles), oe = take(D), oek = take(size_t(sites) * D), oev = take(size_t(sites) * D),
-                 orv = take(D), ozf = take(D);
+                 orv = take(D), ozf = take(D), oop = take(size_t(c.kvheads) * D);
     const size_t oring = off;  // shared by the chunk
     off += (size_t(sites) * engring * D + 63) / 64 * 64;
     work.reserve(off);
     ND_HIP(hipMemset(work.p, 0, off * sizeof(float)));
     float *w = work.p;
     b.x = w + ox;
+    b.oparts = w + oop;
     b.nx = w + onx;
     b.u = w + ou;
     b.bx = w + obx;
@@ -624,6 +629,7 @@ void GpuEngine::build_projections() {
     const int D = c.dim, N = c.lanes, A = c.heads * c.head_dim, K = c.kvheads * c.head_dim;
     const int mhi = mh0();
     for (auto *v : {&mhc_proj, &qkvg, &oproj, &engram_kv}) v->clear();
+    ofused.clear();
     mhc_proj.resize(c.layers);
     qkvg.resize(c.layers);
     oproj.resize(c.layers);
@@ -638,6 +644,7 @@ void GpuEngine::build_projections() {
         qkvg[l].finish(b.z, chunk);
         oproj[l].add(mats[t0 + 7], 0, D, b.proj, D);
         oproj[l].finish(b.att, chunk);
+        ofused.push_back(out_projection(oproj[l]));
         const int rows[3] = {N, N, N * N};
         for (int m = 0; m < 3; ++m)
             if (mats[mhi + 6 + m].cq) mhc_proj[l].add(mats[mhi + 6 + m], l * rows[m], rows[m], b.mhc_out[m], dims.mhc_stride);
@@ -655,6 +662,33 @@ void GpuEngine::build_projections() {
     lm_head_host = Projection{};
     lm_head_host.add(mats[0], 0, c.vocab, hstep.p, c.vocab);
     lm_head_host.finish(b.zf, 1);
+}
+
+// The out-projection runs inside the attention launch (OutProj) when it is one
+// FP32 CQ matrix of 2- or 4-bit codes whose groups of 128 positions are the
+// G query heads of one kv head, with at most 512 rows and no activation
+// quantiser before it (NEEDLE2_ENGINE_OPROJ=gemv: always the separate GEMV).
+OutProj GpuEngine::out_projection(const Projection &p) const {
+    OutProj op{};
+    const char *mode = std::getenv("NEEDLE2_ENGINE_OPROJ");
+    if (mode && std::strcmp(mode, "gemv") == 0) return op;
+    if (p.groups.size() != 1 || !p.groups8.empty() || !p.dense.empty() || p.groups[0]->pieces != 1) return op;
+    const Matrix &m = *p.groups[0]->m0;
+    const int G = c.heads / c.kvheads;
+    if (abits || G * c.head_dim != 128 || m.group != 128 || m.in != c.heads * c.head_dim || m.out != c.dim ||
+        m.out > 512 || c.kvheads > 8 || (m.kind != kNib && m.kind != kCrumb))
+        return op;
+    const CqGeom g = m.geom();
+    op.codes = m.codes.p;
+    op.norms = m.norms.p;
+    op.parts = b.oparts;
+    op.rows = m.out;
+    op.chunks = g.chunks;
+    op.groups = g.groups;
+    op.kind = g.kind;
+    op.scale = g.scale;
+    for (int i = 0; i < 16; ++i) op.lut[i] = g.lut[i];
+    return op;
 }
 
 // engine.cpp:424-432: the int8 path for the CQ matrices of 2- or 4-bit codes
@@ -1083,19 +1117,24 @@ void GpuEngine::run(int tokens) {
             ot = PrepTarget{};
         }
         if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
+        const OutProj &op = ofused[l];
+        EngineDims pd = dims;  // the post's view: the attention's out-projection terms, or proj
+        pd.ogroups = op.codes ? c.kvheads : 0;
         launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, attn_scores.n, mh, l,
-                              ot, s);
-        launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
-        oproj[l].run(s, T, o_prepared);
+                              ot, op, s);
+        if (!op.codes) {
+            launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
+            oproj[l].run(s, T, o_prepared);
+        }
         if (fuse && l + 1 < c.layers) {
             int sites[kEngMaxSites];
             const int ns = layer_sites(l + 1, sites);
             const int first[3] = {(l + 1) * mhc_rows[0], (l + 1) * mhc_rows[1], (l + 1) * mhc_rows[2]};
             PrepTarget pt;
             qkvg_prepared = target(qkvg[l + 1], pt);
-            launch_eng_post_mix(b, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, dims, T, pt, s);
+            launch_eng_post_mix(b, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, pd, T, pt, s);
         } else {
-            launch_eng_post(b, layer[l], l, l + 1 < c.layers, dims, T, s);
+            launch_eng_post(b, layer[l], l, l + 1 < c.layers, pd, T, s);
         }
         send_sites(l + 3);  // two layers ahead of their use
     }

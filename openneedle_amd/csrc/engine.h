@@ -45,6 +45,7 @@ struct EngineDims {
     float sqrt_d;    // std::sqrt(float(D)) (engine.cpp:974, 987)
     float inv_hada;  // 1 / std::sqrt(float(hada)), the Hadamard normalisation
     float scale;     // 1 / std::sqrt(float(head_dim)) (engine.cpp:914)
+    int ogroups;     // > 0: the post adds these out-projection terms per row (oparts) instead of reading proj
 };
 
 // Layer parameters (device pointers into the engine's fp32 copies of the
@@ -71,6 +72,25 @@ struct EngineBufs {
     float *engring;                 // [sites][engring][D], row = position % engring
     float *zf;                      // final hidden, input of the LM head
     int *slots;                     // attention slot list
+    float *oparts;                  // out-projection terms [KV][D] (the attention's, see OutProj)
+};
+
+// The out-projection inside the attention launch, for an FP32 CQ matrix whose
+// groups of 128 input positions are the G query heads of one kv head (the
+// released geometry's G * head_dim = 128): the input's FWHT and every row's
+// group sum split by group, so kv head h's workgroup computes, for every
+// output row, the term p_h = gd_h * half(norm_h) of its own group (the GEMV
+// kernels' arithmetic and order: gd_h sums cb * rot over the group's
+// positions in order) into parts[token][h][row], and the post kernel adds
+// the terms in group order, sum = ((0 + p_0) + p_1) + ... as the GEMV does:
+// the same bits as the separate out-projection launch.
+struct OutProj {
+    const uint4 *codes;     // the matrix's device layout (null: no fused out-projection)
+    const uint16_t *norms;
+    float *parts;           // [tokens][kv heads][rows]
+    int rows, chunks, groups, kind;
+    float scale;            // 1 / sqrt(128)
+    float lut[16];
 };
 
 // KV cache of one layer: fp32 (k32 / v32) or int8 codes with fp32 scales,
@@ -117,9 +137,12 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 // floats (scores_n, checked). It also runs layer l's residual routing (Sinkhorn of hres into hroute) in one more workgroup
 // per token, and prepares the out-projection's int8 input from att when pt.q is set (a group of one kv
 // head's outputs, heads / kvheads * head_dim positions).
+// With op.codes set (and G * head_dim == 128, no pt) each kv head's workgroup also computes its group's
+// out-projection terms (OutProj).
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s);
+                           size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt, const OutProj &op,
+                           hipStream_t s);
 // K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
 void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
                           const EngineDims &d, hipStream_t s);

@@ -16,6 +16,8 @@
 #include "sdot_prepare.h"
 #include "wave.h"
 
+#include <hip/hip_fp16.h>
+
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
@@ -43,6 +45,7 @@ __device__ __forceinline__ EngineBufs at_token(EngineBufs b, const EngineDims &d
     b.bx += t * d.D;
     b.z += t * d.D;
     b.proj += t * d.D;
+    b.oparts += static_cast<size_t>(t) * d.KV * d.D;
     b.e += t * d.D;
     b.rawv += t * d.D;
     b.zf += t * d.D;
@@ -62,6 +65,8 @@ __device__ __forceinline__ EngineBufs at_token(EngineBufs b, const EngineDims &d
     b.slots += static_cast<size_t>(t) * d.capacity;
     return b;
 }
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
 // p[i] for 0 <= i < n, else 0: a buffer load, so a thread past the end takes
 // no branch (a conditional load whose result merges with a default can make
@@ -661,7 +666,7 @@ template <bool PREPARED, bool GLOBAL_SCORES, bool I8, bool WIDE = false>
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
                                                              const StepParams *__restrict__ p, EngineDims d,
                                                              float *__restrict__ scores, int max_length, MhcDev mh,
-                                                             int layer, PrepTarget pt) {
+                                                             int layer, PrepTarget pt, OutProj op) {
     struct Args {
         EngineBufs b0;
         LayerDev ld;
@@ -1177,6 +1182,30 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         accumulate_rows(s0, vpre);
     }
     }
+    // OutProj: this thread's rows t and t + 256 of the out-projection, the 128 positions of this kv head's
+    // group (4 code chunks of 4-bit codes, or 2 of 2-bit, plus the next group's 2 unused), and their norms,
+    // requested ahead of the output phase (rows past the matrix, or no OutProj: an empty resource, zeros)
+    constexpr int kOpRows = 2;
+    u32x4 opc[kOpRows][4];
+    uint32_t opn[kOpRows];
+    {
+        const int cpg = op.kind == 0 ? 4 : 2;  // code chunks per group of 128 positions
+        const uint32_t tiles = op.codes ? static_cast<uint32_t>((op.rows + 255) / 256) : 0u;
+        const __amdgpu_buffer_rsrc_t rc = buffer_rsrc(op.codes, __builtin_amdgcn_readfirstlane(tiles * op.chunks * 4096u));
+        const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(op.norms, __builtin_amdgcn_readfirstlane(tiles * op.groups * 512u));
+#pragma unroll
+        for (int j = 0; j < kOpRows; ++j) {
+            const int row = t + 256 * j;
+            const uint32_t tile = static_cast<uint32_t>(row >> 8), rr = static_cast<uint32_t>(row & 255);
+            const uint32_t live = row < op.rows ? 0u : 0x40000000u;  // past the matrix: past the resource
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                opc[j][c] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rc, live | (((tile * op.chunks + static_cast<uint32_t>(kh * cpg + c)) * 256u + rr) * 16u), 0, 0);
+            opn[j] = __builtin_amdgcn_raw_buffer_load_b16(
+                rn, live | (((tile * op.groups + static_cast<uint32_t>(kh)) * 256u + rr) * 2u), 0, 0);
+        }
+    }
     float4 *wpart = reinterpret_cast<float4 *>(qs);  // [R][G][HD / 4]: R * G * HD = 1024 G floats
     __syncthreads();
 #pragma unroll
@@ -1198,6 +1227,72 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         if (t < G * HD) stage[t] = out_t;
         __syncthreads();
         prepare_groups(pt, stage, kh * G * HD, d.H * HD, kh, kh + 1, 0, blockIdx.y, gridDim.y);
+    }
+    if (op.codes) {  // OutProj (G * HD == 128): this kv head's group terms of every out-projection row
+        float *stage = qs, *T = qs + 256;
+        __syncthreads();  // every partial read
+        // the GEMV's in-kernel FWHT of the group (thread t: position t; stages 1 .. 32 in the wave, 64
+        // through LDS; the same butterflies and operands), then * 1 / sqrt(128)
+        float x = t < 128 ? out_t : 0.0f;
+        wave_butterflies<128, 1>(x, lane);
+        stage[t] = x;
+        __syncthreads();
+        const float o = stage[t ^ 64];
+        x = o + ((t & 64) ? -x : x);
+        x = x * op.scale;
+        // the product table (the GEMV kernels' layout): 4-bit, slot p = position p, entry c = cb[c] * rot_p at
+        // a 17-float stride; 2-bit, slot s = positions 2s, 2s + 1, entry c0 | c1 << 2 = (cb[c0] * rot_2s,
+        // cb[c1] * rot_2s+1) at a 36-float stride
+        if (op.kind == 0) {
+            if (t < 128)
+#pragma unroll
+                for (int c = 0; c < 16; ++c) T[t * 17 + c] = op.lut[c] * x;
+        } else {
+            const int l = lane & 31;
+            const float r0 = __shfl(x, 2 * l), r1 = __shfl(x, 2 * l + 1);
+            if (t < 128 && lane < 32) {
+                float p0[4], p1[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    p0[c] = op.lut[c] * r0;
+                    p1[c] = op.lut[c] * r1;
+                }
+                float4 *dst = reinterpret_cast<float4 *>(T + ((t & ~63) / 2 + l) * 36);
+#pragma unroll
+                for (int hi = 0; hi < 4; ++hi) {
+                    dst[2 * hi] = make_float4(p0[0], p1[hi], p0[1], p1[hi]);
+                    dst[2 * hi + 1] = make_float4(p0[2], p1[hi], p0[3], p1[hi]);
+                }
+            }
+        }
+        __syncthreads();
+        // each row's group sum over the 128 positions in order, times its half norm
+        float *parts = op.parts + (static_cast<size_t>(blockIdx.y) * d.KV + kh) * op.rows;
+#pragma unroll
+        for (int j = 0; j < kOpRows; ++j) {
+            const int row = t + 256 * j;
+            float gd = 0.0f;
+            if (op.kind == 0) {
+#pragma unroll
+                for (int dw = 0; dw < 16; ++dw) {
+                    const uint32_t w = opc[j][dw >> 2][dw & 3];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) gd += T[(8 * dw + i) * 17 + ((w >> (4 * i)) & 15u)];
+                }
+            } else {
+#pragma unroll
+                for (int dw = 0; dw < 8; ++dw) {
+                    const uint32_t w = opc[j][dw >> 2][dw & 3];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float2 e = *reinterpret_cast<const float2 *>(T + (8 * dw + i) * 36 + 2 * ((w >> (4 * i)) & 15u));
+                        gd += e.x;
+                        gd += e.y;
+                    }
+                }
+            }
+            if (row < op.rows) parts[row] = gd * h2f(static_cast<uint16_t>(opn[j]));
+        }
     }
 }
 
@@ -1251,7 +1346,19 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
     const int D = d.D, i = threadIdx.x;
     const bool own = i < D;
     // every load of the kernel, issued before the first wait (threads past D read zeros)
-    float proj = load_or_zero(b.proj, D, i), gn = load_or_zero(ld.post_norm, D, i);
+    float proj, gn = load_or_zero(ld.post_norm, D, i);
+    if (d.ogroups > 0) {  // the out-projection's group terms (OutProj), added in group order as the GEMV does
+        constexpr int kMaxParts = 8;
+        float part[kMaxParts];
+#pragma unroll
+        for (int g = 0; g < kMaxParts; ++g) part[g] = load_or_zero(b.oparts + g * D, g < d.ogroups ? D : 0, i);
+        proj = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kMaxParts; ++g)
+            if (g < d.ogroups) proj += part[g];
+    } else {
+        proj = load_or_zero(b.proj, D, i);
+    }
     float bx = load_or_zero(b.bx, D, i), u = load_or_zero(b.u, D, i);
     const float gh = load_or_zero(ld.pre_hada, D, i), d1 = load_or_zero(ld.d1, D, i);
     const float d3 = load_or_zero(ld.d3, D, i);
@@ -1588,7 +1695,10 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
                            int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt, hipStream_t s) {
+                           size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt, const OutProj &op,
+                           hipStream_t s) {
+    ND_CHECK(!op.codes || (d.H / d.KV * d.HD == 128 && !pt.q && op.rows <= 512 && d.KV <= 8),
+             "internal: fused out-projection outside its geometry");
     // the score slices are [tokens][kv heads][G][max_length] (the routing workgroup touches none)
     ND_CHECK(!scores || static_cast<size_t>(tokens) * d.KV * (d.H / d.KV) * static_cast<size_t>(max_length) <= scores_n,
              "internal: attention score buffer smaller than tokens * kv heads * G * max_length");
@@ -1602,22 +1712,22 @@ void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLaye
         constexpr bool I8 = decltype(i8)::value;
         if (prepared && scores)
             hipLaunchKernelGGL((eng_attn_fused_kernel<true, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
-                               max_length, mh, l, pt);
+                               max_length, mh, l, pt, op);
         else if (prepared)
             hipLaunchKernelGGL((eng_attn_fused_kernel<true, false, I8>), grid, block, lds, s, b, ld, kv, p, d, nullptr,
-                               0, mh, l, pt);
+                               0, mh, l, pt, op);
         else if (wide && scores)
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8, true>), grid, block, 0, s, b, ld, kv, p, d,
-                               scores, max_length, mh, l, pt);
+                               scores, max_length, mh, l, pt, op);
         else if (wide)
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8, true>), grid, block, lds, s, b, ld, kv, p, d,
-                               nullptr, 0, mh, l, pt);
+                               nullptr, 0, mh, l, pt, op);
         else if (scores)
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
-                               max_length, mh, l, pt);
+                               max_length, mh, l, pt, op);
         else
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8>), grid, block, lds, s, b, ld, kv, p, d,
-                               nullptr, 0, mh, l, pt);
+                               nullptr, 0, mh, l, pt, op);
     };
     if (kv.k8) go(std::true_type{});
     else go(std::false_type{});

@@ -270,6 +270,42 @@ def test_prefill_equals_steps(window, long):
     np.testing.assert_array_equal(e3.prefill(prompt, last_only=True)[0], np.stack([e4.step(t)[0] for t in prompt])[-1])
 
 
+# G * head_dim = 128: the out-projection's groups of 128 positions are one kv head's query heads
+HEADS128 = dict(SMALL, num_heads=4, num_kv_heads=2, head_dim=64)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("int8_kv", [False, True])
+def test_out_projection_in_attention(bits, int8_kv, monkeypatch):
+    """The out-projection inside the attention launch (kv head h's workgroup computes its group's term of every
+    output row, the post adds the terms in group order) gives the separate GEMV's bits
+    (NEEDLE2_ENGINE_OPROJ=gemv): steps and a prompt, every logit and hidden state; and, with the fp32 cache,
+    matches the reference (with the int8 cache both launch forms sit 9e-4 from the reference on this model: one
+    K / V code a step apart in the glue's rounding, as in the released geometry's int8 test)."""
+    a = Archive(synthetic_model(dict(HEADS128, max_seq_len=128), engram_layers=(1,), engram_orders=(2, 3),
+                                group=128, seed=13, layer_bits=bits))
+    kv = "int8" if int8_kv else "fp32"
+    fused = GpuEngine(a, kv_cache=kv)
+    monkeypatch.setenv("NEEDLE2_ENGINE_OPROJ", "gemv")
+    gemv = GpuEngine(a, kv_cache=kv)
+    ref = oracle.RefEngine(a, 0, int8_kv)
+    lf, hf = gpu_prefill(fused, PROMPT)
+    lg, hg = gpu_prefill(gemv, PROMPT)
+    np.testing.assert_array_equal(lf, lg)
+    np.testing.assert_array_equal(hf, hg)
+    rl, rh = ref.prefill(PROMPT, hidden=True)
+    for t in TOKENS[:6]:
+        f, g, r = fused.step(t, hidden=True), gemv.step(t, hidden=True), ref.step(t, hidden=True)
+        np.testing.assert_array_equal(f[0], g[0])
+        np.testing.assert_array_equal(f[1], g[1])
+        if not int8_kv:
+            np.testing.assert_allclose(f[0], r[0], atol=ATOL, rtol=RTOL)
+            np.testing.assert_allclose(f[1], r[1], atol=ATOL, rtol=RTOL)
+    if not int8_kv:
+        np.testing.assert_allclose(lf, rl, atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(hf, rh, atol=ATOL, rtol=RTOL)
+
+
 def small64(window=0, seed=9):
     """The small geometry with groups of 64: every CQ matrix qualifies for the int8 path."""
     return Archive(synthetic_model(SMALL, engram_layers=(1,), engram_orders=(2, 3), kv_window=window, group=64,
