@@ -349,6 +349,9 @@ struct GpuEngine {
     HostBuf<float> hstep;  // a decode step's logits, written by the LM head kernel itself (pinned)
     std::vector<Projection> mhc_proj, qkvg, oproj;
     std::vector<OutProj> ofused;  // per layer: the out-projection inside the attention launch (codes null: not)
+    std::vector<QkvgFused> qfused;  // per layer: its Q|K|V|gate inside the previous post launch (wgs 0: not)
+    // the second copy of the state that a fused Q|K|V|gate post writes while its other workgroups read the first
+    float *alt_x = nullptr, *alt_u = nullptr, *alt_bx = nullptr, *alt_hpost = nullptr;
     std::vector<std::array<int, 3>> mhc_row;
     const float *phi[3] = {nullptr, nullptr, nullptr};  // dense mHC matrices (null: CQ)
     int mhc_rows[3] = {0, 0, 0};
@@ -380,6 +383,7 @@ struct GpuEngine {
     void run(int tokens);
     void build_projections();
     OutProj out_projection(const Projection &p) const;
+    QkvgFused qkvg_fusion(int l) const;
     void set_sdot();
     void step(int token, float *logits_out, float *hidden_out);
     void prefill(const int *tokens, int num_tokens, bool last_only, float *logits_out, float *hidden_out);
@@ -523,7 +527,8 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
                  ohp = take(N), ohq = take(N), ohr = take(N * N), oht = take(N * N), om0 = take(mhc_tiles),
                  om1 = take(mhc_tiles),
                  om2 = take(mhc_tiles), oe = take(D), oek = take(size_t(sites) * D), oev = take(size_t(sites) * D),
-                 orv = take(D), ozf = take(D), oop = take(size_t(c.kvheads) * D);
+                 orv = take(D), ozf = take(D), oop = take(size_t(c.kvheads) * D), ox2 = take(N * D), ou2 = take(D),
+                 obx2 = take(D), ohq2 = take(N);
     const size_t oring = off;  // shared by the chunk
     off += (size_t(sites) * engring * D + 63) / 64 * 64;
     work.reserve(off);
@@ -531,6 +536,10 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     float *w = work.p;
     b.x = w + ox;
     b.oparts = w + oop;
+    alt_x = w + ox2;
+    alt_u = w + ou2;
+    alt_bx = w + obx2;
+    alt_hpost = w + ohq2;
     b.nx = w + onx;
     b.u = w + ou;
     b.bx = w + obx;
@@ -630,6 +639,7 @@ void GpuEngine::build_projections() {
     const int mhi = mh0();
     for (auto *v : {&mhc_proj, &qkvg, &oproj, &engram_kv}) v->clear();
     ofused.clear();
+    qfused.clear();
     mhc_proj.resize(c.layers);
     qkvg.resize(c.layers);
     oproj.resize(c.layers);
@@ -645,6 +655,7 @@ void GpuEngine::build_projections() {
         oproj[l].add(mats[t0 + 7], 0, D, b.proj, D);
         oproj[l].finish(b.att, chunk);
         ofused.push_back(out_projection(oproj[l]));
+        qfused.push_back(qkvg_fusion(l));
         const int rows[3] = {N, N, N * N};
         for (int m = 0; m < 3; ++m)
             if (mats[mhi + 6 + m].cq) mhc_proj[l].add(mats[mhi + 6 + m], l * rows[m], rows[m], b.mhc_out[m], dims.mhc_stride);
@@ -689,6 +700,42 @@ OutProj GpuEngine::out_projection(const Projection &p) const {
     op.scale = g.scale;
     for (int i = 0; i < 16; ++i) op.lut[i] = g.lut[i];
     return op;
+}
+
+// Layer l's Q|K|V|gate runs inside the previous layer's post launch
+// (QkvgFused) when its four matrices are one FP32 GEMV group of 2- or 4-bit
+// codes in groups of 128 over d_model <= 512 (a multiple of 128) inputs, with
+// no activation quantiser (NEEDLE2_ENGINE_QKVG=gemv: always the separate
+// GEMV); the step takes it where the post / mixing launch is fused and layer
+// l has no engram site.
+QkvgFused GpuEngine::qkvg_fusion(int l) const {
+    QkvgFused q{};
+    const char *mode = std::getenv("NEEDLE2_ENGINE_QKVG");
+    if (mode && std::strcmp(mode, "gemv") == 0) return q;
+    const Projection &p = qkvg[l];
+    if (l == 0 || abits || p.groups.size() != 1 || !p.groups8.empty() || !p.dense.empty() ||
+        p.groups[0]->pieces != 4 || c.dim > 512 || c.dim % 128)
+        return q;
+    const int t0 = ti(l), idx[4] = {t0 + 1, t0 + 2, t0 + 3, t0 + 6};
+    float *ys[4] = {b.q, b.k, b.v, b.gate};
+    const Matrix &m0 = *mats[idx[0]].cq;
+    if (m0.group != 128 || m0.in != c.dim || (m0.kind != kNib && m0.kind != kCrumb)) return q;
+    const CqGeom g = m0.geom();
+    int wgs = 0;
+    for (int k = 0; k < 4; ++k) {
+        const Matrix *m = mats[idx[k]].cq;
+        if (!m || !GemvGroup::compatible(m0, *m)) return QkvgFused{};
+        q.piece[k] = QkvgPiece{reinterpret_cast<const uint4 *>(m->codes.p), m->norms.p, ys[k], m->out, wgs};
+        wgs += (m->out + 127) / 128;
+    }
+    q.pieces = 4;
+    q.wgs = wgs;
+    q.chunks = g.chunks;
+    q.groups = g.groups;
+    q.kind = g.kind;
+    q.scale = g.scale;
+    for (int i = 0; i < 16; ++i) q.lut[i] = g.lut[i];
+    return q;
 }
 
 // engine.cpp:424-432: the int8 path for the CQ matrices of 2- or 4-bit codes
@@ -1092,6 +1139,10 @@ void GpuEngine::run(int tokens) {
         return p.prep_target(pt, T);
     };
     bool qkvg_prepared = false;  // layer l's Q|K|V|gate input was prepared by the kernel that wrote z
+    bool qkvg_done = false;      // layer l's Q|K|V|gate ran inside the previous post launch
+    // the state buffers the kernels read (x, u, bx, hpost): a fused Q|K|V|gate post writes the other copy
+    EngineBufs cur = b;
+    float *other[4] = {alt_x, alt_u, alt_bx, alt_hpost};
     for (int l = 0; l < c.layers; ++l) {
         if (l == 0 || !fuse) {
             mhc_proj[l].run(s, T);
@@ -1103,9 +1154,10 @@ void GpuEngine::run(int tokens) {
             const int ns = layer_sites(l, sites);
             PrepTarget pt;
             qkvg_prepared = target(qkvg[l], pt);
-            launch_eng_mix(b, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, T, pt, s);
+            launch_eng_mix(cur, layer[l], mh, l, mhc_row[l].data(), sites, ns, dims, T, pt, s);
         }
-        qkvg[l].run(s, T, qkvg_prepared);
+        if (!qkvg_done) qkvg[l].run(s, T, qkvg_prepared);
+        qkvg_done = false;
         PrepTarget ot;
         bool o_prepared = target(oproj[l], ot);
         // one token: norms, RoPE, the KV store (fp32, or the int8 quantiser) and attention in one kernel;
@@ -1116,11 +1168,11 @@ void GpuEngine::run(int tokens) {
             o_prepared = false;
             ot = PrepTarget{};
         }
-        if (T > 1) launch_eng_qk(b, layer[l], kv[l], dp, dims, T, s);
+        if (T > 1) launch_eng_qk(cur, layer[l], kv[l], dp, dims, T, s);
         const OutProj &op = ofused[l];
         EngineDims pd = dims;  // the post's view: the attention's out-projection terms, or proj
         pd.ogroups = op.codes ? c.kvheads : 0;
-        launch_eng_attn_fused(b, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, attn_scores.n, mh, l,
+        launch_eng_attn_fused(cur, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, attn_scores.n, mh, l,
                               ot, op, s);
         if (!op.codes) {
             launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
@@ -1132,13 +1184,27 @@ void GpuEngine::run(int tokens) {
             const int first[3] = {(l + 1) * mhc_rows[0], (l + 1) * mhc_rows[1], (l + 1) * mhc_rows[2]};
             PrepTarget pt;
             qkvg_prepared = target(qkvg[l + 1], pt);
-            launch_eng_post_mix(b, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, pd, T, pt, s);
+            QkvgFused qf = qfused[l + 1];
+            if (T == 1 && ns == 0 && !qkvg_prepared && qf.wgs > 0) {
+                qf.x_out = other[0];
+                qf.u_out = other[1];
+                qf.bx_out = other[2];
+                qf.hpost_out = other[3];
+                launch_eng_post_mix(cur, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, pd, T, pt, &qf, s);
+                std::swap(cur.x, other[0]);
+                std::swap(cur.u, other[1]);
+                std::swap(cur.bx, other[2]);
+                std::swap(cur.hpost, other[3]);
+                qkvg_done = true;
+            } else {
+                launch_eng_post_mix(cur, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, pd, T, pt, nullptr, s);
+            }
         } else {
-            launch_eng_post(b, layer[l], l, l + 1 < c.layers, pd, T, s);
+            launch_eng_post(cur, layer[l], l, l + 1 < c.layers, pd, T, s);
         }
         send_sites(l + 3);  // two layers ahead of their use
     }
-    launch_eng_final(b, dptr[final_norm()], dims, T, s);
+    launch_eng_final(cur, dptr[final_norm()], dims, T, s);
 }
 
 void GpuEngine::step(int token, float *logits_out, float *hidden_out) {

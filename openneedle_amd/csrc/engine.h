@@ -93,6 +93,31 @@ struct OutProj {
     float lut[16];
 };
 
+// The next layer's Q|K|V|gate projection inside the fused post / mixing
+// launch of one token, for FP32 CQ matrices of 2- or 4-bit codes in groups of
+// 128 over d_model <= 512 inputs: every workgroup runs the post and mixing
+// (the same arithmetic, so every workgroup holds the same z), then one
+// 128-row slice of one piece's rows with the GEMV kernels' arithmetic and
+// order (the input's FWHT per group, the product table, gd_g summed over the
+// group's codes in order, sum = ((0 + p_0) + p_1) + ... with p_g = gd_g *
+// half(norm_g)): the separate launch's bits. Workgroup 0 alone stores the
+// layer state, into the *_out buffers (the other workgroups may still be
+// reading the inputs), which the host then takes as the current ones.
+struct QkvgPiece {
+    const uint4 *codes;
+    const uint16_t *norms;
+    float *y;            // the piece's outputs (token 0)
+    int rows, sub_begin;  // rows; first workgroup of the piece (one per 128 rows)
+};
+struct QkvgFused {
+    QkvgPiece piece[4];
+    int pieces, wgs;  // wgs: workgroups of all pieces (0: not fused)
+    int chunks, groups, kind;
+    float scale;      // 1 / sqrt(128)
+    float lut[16];
+    float *x_out, *u_out, *bx_out, *hpost_out;  // the new lanes, u, bx and lane post gates
+};
+
 // KV cache of one layer: fp32 (k32 / v32) or int8 codes with fp32 scales,
 // [kvheads][capacity][head_dim] (scales [kvheads][capacity]).
 struct KvLayer {
@@ -150,11 +175,12 @@ void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_r
                      const EngineDims &d, int tokens, hipStream_t s);
 // The post of layer l, then layer l + 1's dense mHC projections (rows first[m] .. of the three
 // matrices w[m]) and mixing with the engram sites[0..nsites), in one launch; only where
-// eng_post_mix_fits(d).
+// eng_post_mix_fits(d). qf (null: none): layer l + 1's Q|K|V|gate projection in the same launch
+// (QkvgFused; one token, no engram site, no activation quantiser, no int8 target).
 bool eng_post_mix_fits(const EngineDims &d);
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
-                         int tokens, const PrepTarget &pt, hipStream_t s);
+                         int tokens, const PrepTarget &pt, const QkvgFused *qf, hipStream_t s);
 void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, int tokens, hipStream_t s);
 // x[t][0..n) for t < tokens, rows `stride` apart
 void launch_eng_quantize(float *x, int n, int stride, int bits, int tokens, hipStream_t s);

@@ -86,13 +86,13 @@ __device__ __forceinline__ void touch_kernargs() {
     typedef const __attribute__((address_space(4))) uint32_t karg_t;
     karg_t *k = (karg_t *)__builtin_amdgcn_kernarg_segment_ptr();
     constexpr int kLines = (BYTES + 63) / 64;
-    static_assert(kLines <= 12, "arguments of at most 12 lines");
-    uint32_t v[12];
+    static_assert(kLines <= 16, "arguments of at most 16 lines");
+    uint32_t v[16];
 #pragma unroll
-    for (int i = 0; i < 12; ++i) v[i] = i < kLines ? k[16 * i] : 0u;
+    for (int i = 0; i < 16; ++i) v[i] = i < kLines ? k[16 * i] : 0u;
     // one statement uses every value, so every load is in flight before the first wait
     asm volatile("" ::"s"(v[0]), "s"(v[1]), "s"(v[2]), "s"(v[3]), "s"(v[4]), "s"(v[5]), "s"(v[6]), "s"(v[7]),
-                 "s"(v[8]), "s"(v[9]), "s"(v[10]), "s"(v[11]));
+                 "s"(v[8]), "s"(v[9]), "s"(v[10]), "s"(v[11]), "s"(v[12]), "s"(v[13]), "s"(v[14]), "s"(v[15]));
 }
 
 // Block-wide sum / max of one value per thread (every thread gets the result).
@@ -454,19 +454,23 @@ __device__ __forceinline__ GateParams gate_params(const MhcDev &mh, int l) {
     }
     return g;
 }
+// (lead false: hp only, no store to memory; hpost_out receives the post gates)
 template <int N>
 __device__ __forceinline__ void mix_gates(const EngineBufs &b, const GateParams &gp, int l, const float *proj,
-                                          float *hp) {
+                                          float *hp, float *hpost_out, bool lead) {
     if (threadIdx.x < static_cast<unsigned>(N)) {
         const int n = threadIdx.x;
         const float pre = proj[n], post = proj[N + n];
         const float hpre = sigmoidf_(gp.a_pre * pre + gp.b_pre + (n == l % N ? 4.0f : -4.0f));
         const float hpost = 2.0f * sigmoidf_(gp.a_post * post + gp.b_post + (n == l % N ? 0.0f : -4.0f));
         hp[n] = hpre;
-        b.hpre[n] = hpre;
-        b.hpost[n] = hpost;
+        if (lead) {
+            b.hpre[n] = hpre;
+            hpost_out[n] = hpost;
+        }
     }
-    for (int i = threadIdx.x; i < N * N; i += blockDim.x) b.hres[i] = proj[2 * N + i];
+    if (lead)
+        for (int i = threadIdx.x; i < N * N; i += blockDim.x) b.hres[i] = proj[2 * N + i];
 }
 
 // The engram gates of the layer's sites on bx (engine.cpp:987-991), after a barrier that
@@ -504,7 +508,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_mix_kernel(EngineBufs b0, Lay
     for (int task = threadIdx.x; task < 2 * N + N * N; task += blockDim.x)
         proj[task] = task < N ? pre_rows[task] : task < 2 * N ? post_rows[task - N] : res_rows[task - 2 * N];
     __syncthreads();
-    mix_gates<N>(b, gate_params<N>(mh, m.l), m.l, proj, hp);
+    mix_gates<N>(b, gate_params<N>(mh, m.l), m.l, proj, hp, b.hpost, true);
     __syncthreads();
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
         float sum = 0.0f;
@@ -1342,7 +1346,8 @@ __global__ __launch_bounds__(64) void eng_kv_import_kernel(const float *__restri
 template <int N, int WAVES, class F>
 __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &ld, int l,
                                            int next_rms, const EngineDims &d, float *red, float *mlp, float *hr,
-                                           float *hpo, float *nxs, float (&x)[8], F &&after_loads) {
+                                           float *hpo, float *nxs, float (&x)[8], F &&after_loads, float *xo,
+                                           bool lead) {
     const int D = d.D, i = threadIdx.x;
     const bool own = i < D;
     // every load of the kernel, issued before the first wait (threads past D read zeros)
@@ -1412,12 +1417,12 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
         }
 #pragma unroll
         for (int n = 0; n < N; ++n) {
-            b.x[n * D + i] = nx[n];
+            if (lead) xo[n * D + i] = nx[n];
             sum += nx[n];
             ss += nx[n] * nx[n];
             x[n] = nx[n];
         }
-        b.hidden[l * D + i] = sum / static_cast<float>(N);
+        if (lead) b.hidden[l * D + i] = sum / static_cast<float>(N);
     }
     if (next_rms) {  // the next layer's nx = rms(x) over all N * D values
         r = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(N * D) + 1e-6f);
@@ -1436,7 +1441,7 @@ __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, La
     __shared__ float mlp[4096];
     __shared__ float hr[64], hpo[8];
     float x[8];
-    post_layer<N, kEngThreads / 64>(b, ld, l, next_rms, d, red, mlp, hr, hpo, nullptr, x, [] {});
+    post_layer<N, kEngThreads / 64>(b, ld, l, next_rms, d, red, mlp, hr, hpo, nullptr, x, [] {}, b.x, true);
 }
 
 // z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
@@ -1509,10 +1514,14 @@ __device__ __forceinline__ const float4 *mhc_row_ptr(const DenseRows &w, int r, 
 // lane keeps apart, and block_sum's tree over 64 threads and the sequential
 // sum of its four waves follow, so the outputs are the same bits as the
 // separate launches'. Needs D <= THREADS, N * D <= 4096.
-template <int THREADS, int N>
+// QKVG (one token, THREADS 512, no engram site, no activation quantiser, no
+// int8 target): workgroup blockIdx.x also computes one 128-row slice of the
+// next layer's Q|K|V|gate projection (QkvgFused); workgroup 0 alone stores
+// the layer state, the lanes, u, bx and hpost into qf's *_out buffers.
+template <int THREADS, int N, bool QKVG>
 __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, LayerDev ld, LayerDev ldn, MhcDev mh,
                                                                int l, DenseRows w, MixArgs m, EngineDims d,
-                                                               PrepTarget pt) {
+                                                               PrepTarget pt, QkvgFused qf) {
     struct Args {
         EngineBufs b0;
         LayerDev ld, ldn;
@@ -1522,8 +1531,10 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         MixArgs m;
         EngineDims d;
         PrepTarget pt;
+        QkvgFused qf;
     };
-    touch_kernargs<offsetof(Args, pt)>();
+    static_assert(!QKVG || THREADS == 512, "the fused projection takes 4 threads per row of 128-row slices");
+    touch_kernargs<QKVG ? sizeof(Args) : offsetof(Args, pt)>();
     constexpr int kWaves = THREADS / 64, kPF = 8;  // float4 columns per lane held for each prefetched row
     constexpr int R = 2 * N + N * N;              // mHC projection rows
     constexpr int kRowsPF = std::min((R + kWaves - 1) / kWaves, 3);  // rows per wave held in registers
@@ -1531,11 +1542,58 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     __shared__ float red[kWaves];
     __shared__ float mlp[4096];  // the MLP vector, then the rms'd lanes
     __shared__ float hr[64], hpo[8], hp[16];
-    __shared__ float zs[4096], ps[4096];
+    __shared__ float zs[QKVG ? 1 : 4096], ps[QKVG ? 1 : 4096];
     __shared__ float proj[2 * 8 + 64];
+    // the projection's product table (4-bit: 17-float slot per position; 2-bit: 36-float slot per pair of
+    // positions) and the parked group terms of groups 1 .. 3
+    __shared__ __attribute__((aligned(16))) float tab[QKVG ? 256 * 36 : 1];
+    __shared__ float park[QKVG ? 3 * 128 : 1];
     const int D = d.D, cols = N * D, c4n = cols / 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63, i = threadIdx.x;
+    const bool lead = !QKVG || blockIdx.x == 0;
+    // QKVG: this thread's row r of the workgroup's slice and group g, its codes (4 chunks of 4-bit codes or
+    // 2 of 2-bit) and half norm, requested first (rows past the piece and groups past the input: zeros)
+    const int qr = i & 127, qg = i >> 7;
+    u32x4 qc[4];
+    uint32_t qn = 0;
+    float *qy = nullptr;
+    int qrow = 0, qrows = 0;
+    if constexpr (QKVG) {
+        const int wg = blockIdx.x;
+        int pi = 0;
+#pragma unroll
+        for (int k = 1; k < 4; ++k)
+            if (k < qf.pieces && wg >= qf.piece[k].sub_begin) pi = k;
+        auto pick = [&](auto get) {  // piece pi's field without indexing the argument block at run time
+            auto v = get(qf.piece[0]);
+#pragma unroll
+            for (int k = 1; k < 4; ++k)
+                if (pi == k) v = get(qf.piece[k]);
+            return v;
+        };
+        const uint4 *codes = pick([](const QkvgPiece &p) { return p.codes; });
+        const uint16_t *norms = pick([](const QkvgPiece &p) { return p.norms; });
+        qy = pick([](const QkvgPiece &p) { return p.y; });
+        qrows = pick([](const QkvgPiece &p) { return p.rows; });
+        const int sub = wg - pick([](const QkvgPiece &p) { return p.sub_begin; });
+        qrow = sub * 128 + qr;
+        const uint32_t tiles = static_cast<uint32_t>((qrows + 255) / 256);
+        const __amdgpu_buffer_rsrc_t rc =
+            buffer_rsrc(codes, __builtin_amdgcn_readfirstlane(tiles * static_cast<uint32_t>(qf.chunks) * 4096u));
+        const __amdgpu_buffer_rsrc_t rn =
+            buffer_rsrc(norms, __builtin_amdgcn_readfirstlane(tiles * static_cast<uint32_t>(qf.groups) * 512u));
+        const uint32_t tile = static_cast<uint32_t>(sub >> 1), rr = static_cast<uint32_t>((sub & 1) * 128 + qr);
+        const uint32_t live = qrow < qrows && qg < qf.groups ? 0u : 0x40000000u;  // else past the resource
+        const int cpg = qf.kind == 0 ? 4 : 2;  // code chunks per group of 128 positions
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            qc[c] = __builtin_amdgcn_raw_buffer_load_b128(
+                rc, (c < cpg ? live : 0x40000000u) |
+                        (((tile * qf.chunks + static_cast<uint32_t>(qg * cpg + c)) * 256u + rr) * 16u), 0, 0);
+        qn = __builtin_amdgcn_raw_buffer_load_b16(
+            rn, live | (((tile * qf.groups + static_cast<uint32_t>(qg)) * 256u + rr) * 2u), 0, 0);
+    }
     float4 pf[kRowsPF][kPF];
     float x[8];
     GateParams gp;
@@ -1555,7 +1613,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         }
         gp = gate_params<N>(mh, l + 1);
         nin = load_or_zero(ldn.norm_in, D, i);
-    });
+    }, QKVG ? qf.x_out : b.x, lead);
     __syncthreads();
     const float4 *nx4 = reinterpret_cast<const float4 *>(mlp);
     auto fma4 = [](float4 &acc, const float4 &a, const float4 &c) {
@@ -1603,31 +1661,108 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         if (lane == 0) proj[r] = sum;
     }
     __syncthreads();
-    mix_gates<N>(b, gp, l + 1, proj, hp);
+    mix_gates<N>(b, gp, l + 1, proj, hp, QKVG ? qf.hpost_out : b.hpost, lead);
     __syncthreads();
     const bool own = i < D;
     float u = 0.0f;
     if (own) {
 #pragma unroll
         for (int n = 0; n < N; ++n) u += hp[n] * x[n];
-        b.u[i] = u;
-        b.bx[i] = u;
+        if (lead) {
+            (QKVG ? qf.u_out : b.u)[i] = u;
+            (QKVG ? qf.bx_out : b.bx)[i] = u;
+        }
     }
     float z = 0.0f;  // this thread's z after the quantiser (own threads)
-    if (m.nsites) {
+    if (!QKVG && m.nsites) {
         __syncthreads();
         mix_sites(b, m, d, red, zs, ps);
         rms_block(b.bx, b.z, D, ldn.norm_in, red);
     } else {  // rms_block's arithmetic on the registers
         const float r = 1.0f / sqrtf(block_sum(own ? u * u : 0.0f, red) / static_cast<float>(D) + 1e-6f);
-        if (own) b.z[i] = z = u * r * (1.0f + nin);
+        if (own) {
+            z = u * r * (1.0f + nin);
+            if (lead) b.z[i] = z;
+        }
         __syncthreads();
     }
-    quantize_block(b.z, D, d.abits, red);
-    if (pt.q) {  // the next Q|K|V|gate projection's int8 input, from z staged in LDS
-        if (own) zs[i] = m.nsites || d.abits ? b.z[i] : z;
+    if constexpr (!QKVG) {
+        quantize_block(b.z, D, d.abits, red);
+        if (pt.q) {  // the next Q|K|V|gate projection's int8 input, from z staged in LDS
+            if (own) zs[i] = m.nsites || d.abits ? b.z[i] : z;
+            __syncthreads();
+            prepare_groups(pt, zs, 0, D, 0, pt.dev / pt.group, 0, blockIdx.y, gridDim.y);
+        }
+    } else {
+        // the GEMV's in-kernel FWHT of each group of 128 positions (thread i: position i; stages 1 .. 32 in
+        // the wave, 64 through LDS; the same butterflies and operands), then * 1 / sqrt(128)
+        float xr = own ? z : 0.0f;
+        wave_butterflies<128, 1>(xr, lane);
+        mlp[i] = xr;  // free: the rms'd lanes were last read before the mixing barriers
         __syncthreads();
-        prepare_groups(pt, zs, 0, D, 0, pt.dev / pt.group, 0, blockIdx.y, gridDim.y);
+        const float o = mlp[i ^ 64];
+        xr = o + ((i & 64) ? -xr : xr);
+        xr = xr * qf.scale;
+        // the product table (the GEMV kernels' layout): 4-bit, slot p = position p, entry c = cb[c] * rot_p at a
+        // 17-float stride; 2-bit, slot s = positions 2s, 2s + 1, entry c0 | c1 << 2 = (cb[c0] * rot_2s,
+        // cb[c1] * rot_2s+1) at a 36-float stride
+        if (qf.kind == 0) {
+            if (own)
+#pragma unroll
+                for (int c = 0; c < 16; ++c) tab[i * 17 + c] = qf.lut[c] * xr;
+        } else {
+            const int pl = lane & 31;
+            const float r0 = __shfl(xr, 2 * pl), r1 = __shfl(xr, 2 * pl + 1);
+            if (own && lane < 32) {
+                float p0[4], p1[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    p0[c] = qf.lut[c] * r0;
+                    p1[c] = qf.lut[c] * r1;
+                }
+                float4 *dst = reinterpret_cast<float4 *>(tab + ((i & ~63) / 2 + pl) * 36);
+#pragma unroll
+                for (int hi = 0; hi < 4; ++hi) {
+                    dst[2 * hi] = make_float4(p0[0], p1[hi], p0[1], p1[hi]);
+                    dst[2 * hi + 1] = make_float4(p0[2], p1[hi], p0[3], p1[hi]);
+                }
+            }
+        }
+        __syncthreads();
+        // row qr's group qg: gd over the group's 128 positions in order, times the half norm
+        float gd = 0.0f;
+        if (qf.kind == 0) {
+            const float *tg = tab + qg * 128 * 17;
+#pragma unroll
+            for (int dw = 0; dw < 16; ++dw) {
+                const uint32_t cw = qc[dw >> 2][dw & 3];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) gd += tg[(8 * dw + k) * 17 + ((cw >> (4 * k)) & 15u)];
+            }
+        } else {
+            const float *tg = tab + qg * 64 * 36;
+#pragma unroll
+            for (int dw = 0; dw < 8; ++dw) {
+                const uint32_t cw = qc[dw >> 2][dw & 3];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const float2 e = *reinterpret_cast<const float2 *>(tg + (8 * dw + k) * 36 + 2 * ((cw >> (4 * k)) & 15u));
+                    gd += e.x;
+                    gd += e.y;
+                }
+            }
+        }
+        const float pg = gd * h2f(static_cast<uint16_t>(qn));
+        if (qg > 0 && qg < 4) park[(qg - 1) * 128 + qr] = pg;
+        __syncthreads();
+        if (qg == 0) {  // the row sum in group order
+            float sum = 0.0f;
+            sum += pg;
+#pragma unroll
+            for (int k = 1; k < 4; ++k)
+                if (k < qf.groups) sum += park[(k - 1) * 128 + qr];
+            if (qrow < qrows) qy[qrow] = sum;
+        }
     }
 }
 
@@ -1756,8 +1891,12 @@ bool eng_post_mix_fits(const EngineDims &d) {
 
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
-                         int tokens, const PrepTarget &pt, hipStream_t s) {
+                         int tokens, const PrepTarget &pt, const QkvgFused *qf, hipStream_t s) {
     ND_CHECK(eng_post_mix_fits(d), "internal: fused post / mixing launch outside its geometry");
+    ND_CHECK(!qf || (tokens == 1 && nsites == 0 && !pt.q && d.abits == 0 && d.D <= 512 && d.D % 128 == 0 &&
+                     qf->wgs > 0 && qf->pieces >= 1 && qf->pieces <= 4 && qf->groups == d.D / 128 &&
+                     (qf->kind == 0 || qf->kind == 1) && qf->x_out && qf->u_out && qf->bx_out && qf->hpost_out),
+             "internal: fused Q|K|V|gate projection outside its geometry");
     DenseRows a{};
     for (int k = 0; k < 3; ++k) {
         a.w[k] = w[k];
@@ -1767,14 +1906,18 @@ void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev
     m.l = l + 1;
     m.nsites = nsites;
     for (int k = 0; k < nsites; ++k) m.sites[k] = sites[k];
+    const QkvgFused none{};
     with_lanes(d.N, [&](auto n) {
         constexpr int N = decltype(n)::value;
-        if (d.D <= 512)
-            hipLaunchKernelGGL((eng_post_mix_kernel<512, N>), dim3(1, tokens), dim3(512), 0, s, b, ld, ldn, mh, l, a,
-                               m, d, pt);
+        if (qf)
+            hipLaunchKernelGGL((eng_post_mix_kernel<512, N, true>), dim3(qf->wgs, 1), dim3(512), 0, s, b, ld, ldn, mh,
+                               l, a, m, d, pt, *qf);
+        else if (d.D <= 512)
+            hipLaunchKernelGGL((eng_post_mix_kernel<512, N, false>), dim3(1, tokens), dim3(512), 0, s, b, ld, ldn, mh,
+                               l, a, m, d, pt, none);
         else
-            hipLaunchKernelGGL((eng_post_mix_kernel<kEngThreads, N>), dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld,
-                               ldn, mh, l, a, m, d, pt);
+            hipLaunchKernelGGL((eng_post_mix_kernel<kEngThreads, N, false>), dim3(1, tokens), dim3(kEngThreads), 0, s,
+                               b, ld, ldn, mh, l, a, m, d, pt, none);
     });
     ND_HIP(hipGetLastError());
 }

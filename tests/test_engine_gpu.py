@@ -306,6 +306,35 @@ def test_out_projection_in_attention(bits, int8_kv, monkeypatch):
         np.testing.assert_allclose(hf, rh, atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("d_model", [256, 512])
+def test_qkvg_in_post(bits, d_model, monkeypatch):
+    """A decode step's Q|K|V|gate projection inside the previous layer's post launch (every workgroup runs the
+    post and mixing, then one 128-row slice of the projection with the GEMV's arithmetic; workgroup 0 stores
+    the state into the second copy of the buffers) gives the separate GEMV's bits (NEEDLE2_ENGINE_QKVG=gemv):
+    every logit and hidden state over steps after a prompt, groups of 128 over 2 and 4 groups, 2- and 4-bit
+    codes, a layer with an engram site (its post stays unfused) between fused ones; and matches the
+    reference."""
+    geometry = dict(SMALL, d_model=d_model, hada_n=d_model, num_heads=4, num_kv_heads=2, head_dim=64,
+                    engram_sub_dim=d_model // 4, num_layers=4, max_seq_len=128)
+    a = Archive(synthetic_model(geometry, engram_layers=(2,), engram_orders=(2, 3), group=128, seed=17,
+                                layer_bits=bits))
+    fused = GpuEngine(a)
+    monkeypatch.setenv("NEEDLE2_ENGINE_QKVG", "gemv")
+    gemv = GpuEngine(a)
+    ref = oracle.RefEngine(a)
+    for e in (fused, gemv, ref):
+        e.prefill(PROMPT[:20])
+    for t in TOKENS[:8]:
+        f, g, r = fused.step(t, hidden=True), gemv.step(t, hidden=True), ref.step(t, hidden=True)
+        np.testing.assert_array_equal(f[0], g[0])
+        np.testing.assert_array_equal(f[1], g[1])
+        np.testing.assert_allclose(f[0], r[0], atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(f[1], r[1], atol=ATOL, rtol=RTOL)
+    ids = np.array([3, 500, 77], np.int32)
+    np.testing.assert_array_equal(gpu_project(fused, ids), gpu_project(gemv, ids))
+
+
 def small64(window=0, seed=9):
     """The small geometry with groups of 64: every CQ matrix qualifies for the int8 path."""
     return Archive(synthetic_model(SMALL, engram_layers=(1,), engram_orders=(2, 3), kv_window=window, group=64,
