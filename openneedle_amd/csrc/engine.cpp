@@ -726,7 +726,7 @@ QkvgFused GpuEngine::qkvg_fusion(int l) const {
         const Matrix *m = mats[idx[k]].cq;
         if (!m || !GemvGroup::compatible(m0, *m)) return QkvgFused{};
         q.piece[k] = QkvgPiece{reinterpret_cast<const uint4 *>(m->codes.p), m->norms.p, ys[k], m->out, wgs};
-        wgs += (m->out + 127) / 128;
+        wgs += (m->out + kQkvgRows - 1) / kQkvgRows;
     }
     q.pieces = 4;
     q.wgs = wgs;

@@ -93,12 +93,19 @@ struct OutProj {
     float lut[16];
 };
 
+// Rows of the fused Q|K|V|gate projection per workgroup (512 threads: four per row, one per group)
+#ifndef ND_QKVG_ROWS
+#define ND_QKVG_ROWS 128
+#endif
+constexpr int kQkvgRows = ND_QKVG_ROWS;
+static_assert(kQkvgRows == 64 || kQkvgRows == 128, "slices of 64 or 128 rows");
+
 // The next layer's Q|K|V|gate projection inside the fused post / mixing
 // launch of one token, for FP32 CQ matrices of 2- or 4-bit codes in groups of
 // 128 over d_model <= 512 inputs: every workgroup runs the post and mixing
-// (the same arithmetic, so every workgroup holds the same z), then one
-// 128-row slice of one piece's rows with the GEMV kernels' arithmetic and
-// order (the input's FWHT per group, the product table, gd_g summed over the
+// (the same arithmetic, so every workgroup holds the same z), then one slice
+// of kQkvgRows rows of one piece with the GEMV kernels' arithmetic and order
+// (the input's FWHT per group, the product table, gd_g summed over the
 // group's codes in order, sum = ((0 + p_0) + p_1) + ... with p_g = gd_g *
 // half(norm_g)): the separate launch's bits. Workgroup 0 alone stores the
 // layer state, into the *_out buffers (the other workgroups may still be
@@ -107,7 +114,7 @@ struct QkvgPiece {
     const uint4 *codes;
     const uint16_t *norms;
     float *y;            // the piece's outputs (token 0)
-    int rows, sub_begin;  // rows; first workgroup of the piece (one per 128 rows)
+    int rows, sub_begin;  // rows; first workgroup of the piece (one per kQkvgRows rows)
 };
 struct QkvgFused {
     QkvgPiece piece[4];

@@ -479,7 +479,11 @@ __device__ void mix_sites(const EngineBufs &b, const MixArgs &m, const EngineDim
                           float *ps) {
     const int D = d.D;
     for (int k = 0; k < m.nsites; ++k) {
-        const int s = m.sites[k];
+        // (a select over the fixed slots: indexing the argument block at run time copies it to scratch)
+        int s = m.sites[0];
+#pragma unroll
+        for (int j = 1; j < kEngMaxSites; ++j)
+            if (k == j) s = m.sites[j];
         rms_block(b.u, zs, D, nullptr, red);
         rms_block(b.ek + s * D, ps, D, nullptr, red);
         float dot = 0.0f;
@@ -1515,7 +1519,7 @@ __device__ __forceinline__ const float4 *mhc_row_ptr(const DenseRows &w, int r, 
 // sum of its four waves follow, so the outputs are the same bits as the
 // separate launches'. Needs D <= THREADS, N * D <= 4096.
 // QKVG (one token, THREADS 512, no engram site, no activation quantiser, no
-// int8 target): workgroup blockIdx.x also computes one 128-row slice of the
+// int8 target): workgroup blockIdx.x also computes one kQkvgRows-row slice of the
 // next layer's Q|K|V|gate projection (QkvgFused); workgroup 0 alone stores
 // the layer state, the lanes, u, bx and hpost into qf's *_out buffers.
 template <int THREADS, int N, bool QKVG>
@@ -1533,7 +1537,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         PrepTarget pt;
         QkvgFused qf;
     };
-    static_assert(!QKVG || THREADS == 512, "the fused projection takes 4 threads per row of 128-row slices");
+    static_assert(!QKVG || THREADS == 512, "the fused projection takes 4 threads per row of its slice");
     touch_kernargs<QKVG ? sizeof(Args) : offsetof(Args, pt)>();
     constexpr int kWaves = THREADS / 64, kPF = 8;  // float4 columns per lane held for each prefetched row
     constexpr int R = 2 * N + N * N;              // mHC projection rows
@@ -1547,14 +1551,14 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     // the projection's product table (4-bit: 17-float slot per position; 2-bit: 36-float slot per pair of
     // positions) and the parked group terms of groups 1 .. 3
     __shared__ __attribute__((aligned(16))) float tab[QKVG ? 256 * 36 : 1];
-    __shared__ float park[QKVG ? 3 * 128 : 1];
+    __shared__ float park[QKVG ? 3 * kQkvgRows : 1];
     const int D = d.D, cols = N * D, c4n = cols / 4;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63, i = threadIdx.x;
     const bool lead = !QKVG || blockIdx.x == 0;
     // QKVG: this thread's row r of the workgroup's slice and group g, its codes (4 chunks of 4-bit codes or
     // 2 of 2-bit) and half norm, requested first (rows past the piece and groups past the input: zeros)
-    const int qr = i & 127, qg = i >> 7;
+    const int qr = i % kQkvgRows, qg = i / kQkvgRows;
     u32x4 qc[4];
     uint32_t qn = 0;
     float *qy = nullptr;
@@ -1577,13 +1581,13 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         qy = pick([](const QkvgPiece &p) { return p.y; });
         qrows = pick([](const QkvgPiece &p) { return p.rows; });
         const int sub = wg - pick([](const QkvgPiece &p) { return p.sub_begin; });
-        qrow = sub * 128 + qr;
+        qrow = sub * kQkvgRows + qr;
         const uint32_t tiles = static_cast<uint32_t>((qrows + 255) / 256);
         const __amdgpu_buffer_rsrc_t rc =
             buffer_rsrc(codes, __builtin_amdgcn_readfirstlane(tiles * static_cast<uint32_t>(qf.chunks) * 4096u));
         const __amdgpu_buffer_rsrc_t rn =
             buffer_rsrc(norms, __builtin_amdgcn_readfirstlane(tiles * static_cast<uint32_t>(qf.groups) * 512u));
-        const uint32_t tile = static_cast<uint32_t>(sub >> 1), rr = static_cast<uint32_t>((sub & 1) * 128 + qr);
+        const uint32_t tile = static_cast<uint32_t>(qrow >> 8), rr = static_cast<uint32_t>(qrow & 255);
         const uint32_t live = qrow < qrows && qg < qf.groups ? 0u : 0x40000000u;  // else past the resource
         const int cpg = qf.kind == 0 ? 4 : 2;  // code chunks per group of 128 positions
 #pragma unroll
@@ -1732,7 +1736,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         // row qr's group qg: gd over the group's 128 positions in order, times the half norm
         float gd = 0.0f;
         if (qf.kind == 0) {
-            const float *tg = tab + qg * 128 * 17;
+            const float *tg = tab + (qg & 3) * 128 * 17;  // (threads past the groups read a group's slots)
 #pragma unroll
             for (int dw = 0; dw < 16; ++dw) {
                 const uint32_t cw = qc[dw >> 2][dw & 3];
@@ -1740,7 +1744,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
                 for (int k = 0; k < 8; ++k) gd += tg[(8 * dw + k) * 17 + ((cw >> (4 * k)) & 15u)];
             }
         } else {
-            const float *tg = tab + qg * 64 * 36;
+            const float *tg = tab + (qg & 3) * 64 * 36;
 #pragma unroll
             for (int dw = 0; dw < 8; ++dw) {
                 const uint32_t cw = qc[dw >> 2][dw & 3];
@@ -1753,14 +1757,14 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
             }
         }
         const float pg = gd * h2f(static_cast<uint16_t>(qn));
-        if (qg > 0 && qg < 4) park[(qg - 1) * 128 + qr] = pg;
+        if (qg > 0 && qg < 4) park[(qg - 1) * kQkvgRows + qr] = pg;
         __syncthreads();
         if (qg == 0) {  // the row sum in group order
             float sum = 0.0f;
             sum += pg;
 #pragma unroll
             for (int k = 1; k < 4; ++k)
-                if (k < qf.groups) sum += park[(k - 1) * 128 + qr];
+                if (k < qf.groups) sum += park[(k - 1) * kQkvgRows + qr];
             if (qrow < qrows) qy[qrow] = sum;
         }
     }
