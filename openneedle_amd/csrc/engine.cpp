@@ -699,6 +699,9 @@ OutProj GpuEngine::out_projection(const Projection &p) const {
     op.kind = g.kind;
     op.scale = g.scale;
     for (int i = 0; i < 16; ++i) op.lut[i] = g.lut[i];
+    // a decode step's rows over 2^split workgroups per kv head (NEEDLE2_ENGINE_OSPLIT: 0, 1 or 2)
+    const char *split = std::getenv("NEEDLE2_ENGINE_OSPLIT");
+    op.split_shift = split ? std::min(2, std::max(0, std::atoi(split))) : 1;
     return op;
 }
 

@@ -91,6 +91,9 @@ struct OutProj {
     int rows, chunks, groups, kind;
     float scale;            // 1 / sqrt(128)
     float lut[16];
+    // one token with the scores in LDS: 2^split_shift workgroups per kv head, each running the head's
+    // attention (the same arithmetic) and a contiguous share of the rows; part 0 stores the outputs
+    int split_shift;
 };
 
 // Rows of the fused Q|K|V|gate projection per workgroup (512 threads: four per row, one per group)

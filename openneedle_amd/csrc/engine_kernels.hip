@@ -688,7 +688,8 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         PrepTarget pt;
     };
     touch_kernargs<offsetof(Args, pt)>();
-    if (blockIdx.x == d.KV) {  // the routing workgroup
+    const int split = op.codes ? op.split_shift : 0;  // workgroups per kv head: 1 << split
+    if (blockIdx.x == (d.KV << split)) {  // the routing workgroup
         route_wave(at_token(b0, d, blockIdx.y), mh, layer, d);
         return;
     }
@@ -699,7 +700,8 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     __shared__ float knew_scale, vnew_scale;  // int8: the new K / V rows' scales
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     p += blockIdx.y;
-    const int kh = blockIdx.x, G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
+    const int kh = blockIdx.x >> split, part = blockIdx.x & ((1 << split) - 1);
+    const int G = d.H / d.KV, HD = d.HD, half = HD / 2, t = threadIdx.x;
     float *sc = GLOBAL_SCORES
                     ? scores + (static_cast<size_t>(blockIdx.y) * d.KV + kh) * G * static_cast<size_t>(max_length)
                     : sc_lds;
@@ -1190,12 +1192,14 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         accumulate_rows(s0, vpre);
     }
     }
-    // OutProj: this thread's rows t and t + 256 of the out-projection, the 128 positions of this kv head's
-    // group (4 code chunks of 4-bit codes, or 2 of 2-bit, plus the next group's 2 unused), and their norms,
-    // requested ahead of the output phase (rows past the matrix, or no OutProj: an empty resource, zeros)
+    // OutProj: this thread's rows part * rp + t and + 256 of the out-projection (rp rows per part), the 128
+    // positions of this kv head's group (4 code chunks of 4-bit codes, or 2 of 2-bit, plus the next group's 2
+    // unused), and their norms, requested ahead of the output phase (rows past the part or the matrix, or no
+    // OutProj: an empty resource, zeros)
     constexpr int kOpRows = 2;
     u32x4 opc[kOpRows][4];
     uint32_t opn[kOpRows];
+    const int rp = (op.rows + (1 << split) - 1) >> split;
     {
         const int cpg = op.kind == 0 ? 4 : 2;  // code chunks per group of 128 positions
         const uint32_t tiles = op.codes ? static_cast<uint32_t>((op.rows + 255) / 256) : 0u;
@@ -1203,9 +1207,9 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         const __amdgpu_buffer_rsrc_t rn = buffer_rsrc(op.norms, __builtin_amdgcn_readfirstlane(tiles * op.groups * 512u));
 #pragma unroll
         for (int j = 0; j < kOpRows; ++j) {
-            const int row = t + 256 * j;
+            const int row = part * rp + t + 256 * j;
             const uint32_t tile = static_cast<uint32_t>(row >> 8), rr = static_cast<uint32_t>(row & 255);
-            const uint32_t live = row < op.rows ? 0u : 0x40000000u;  // past the matrix: past the resource
+            const uint32_t live = t + 256 * j < rp && row < op.rows ? 0u : 0x40000000u;  // else past the resource
 #pragma unroll
             for (int c = 0; c < 4; ++c)
                 opc[j][c] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -1226,7 +1230,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         float a = 0.0f;
         for (int k = 0; k < R; ++k) a += wp[k * G * HD + o];
         const float val = a * sigmoidf_(o == t ? gate_t : b.gate[kh * G * HD + o]);
-        b.att[kh * G * HD + o] = val;
+        if (part == 0) b.att[kh * G * HD + o] = val;
         if (o == t) out_t = val;
     }
     if (pt.q) {  // this kv head's outputs are one group of the out-projection's int8 input
@@ -1278,7 +1282,8 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         float *parts = op.parts + (static_cast<size_t>(blockIdx.y) * d.KV + kh) * op.rows;
 #pragma unroll
         for (int j = 0; j < kOpRows; ++j) {
-            const int row = t + 256 * j;
+            const int row = part * rp + t + 256 * j;
+            if (256 * j + (t & ~63) >= rp) continue;  // (wave-uniform) no row of this part here
             float gd = 0.0f;
             if (op.kind == 0) {
 #pragma unroll
@@ -1299,7 +1304,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
                     }
                 }
             }
-            if (row < op.rows) parts[row] = gd * h2f(static_cast<uint16_t>(opn[j]));
+            if (t + 256 * j < rp && row < op.rows) parts[row] = gd * h2f(static_cast<uint16_t>(opn[j]));
         }
     }
 }
@@ -1845,28 +1850,31 @@ void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLaye
              "internal: attention prepares one kv head's outputs as one group");
     const size_t lds = scores ? 0 : static_cast<size_t>(d.H / d.KV) * max_length * sizeof(float);
     ND_CHECK(lds <= kEngScoreLds, "internal: attention scores exceed the LDS budget without a score buffer");
-    const dim3 grid(d.KV + 1, tokens), block(256);  // workgroup KV: the routing
+    OutProj o = op;  // several workgroups per kv head only for one token with the scores in LDS
+    if (scores || tokens != 1 || !o.codes) o.split_shift = 0;
+    ND_CHECK(o.split_shift >= 0 && o.split_shift <= 2, "internal: out-projection split outside 1, 2 or 4");
+    const dim3 grid((d.KV << o.split_shift) + 1, tokens), block(256);  // the last workgroup: the routing
     const bool wide = d.HD > 128 || d.H / d.KV + 1 > 4;  // the norms' one-head-per-wave form needs neither
     auto go = [&](auto i8) {
         constexpr bool I8 = decltype(i8)::value;
         if (prepared && scores)
             hipLaunchKernelGGL((eng_attn_fused_kernel<true, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
-                               max_length, mh, l, pt, op);
+                               max_length, mh, l, pt, o);
         else if (prepared)
             hipLaunchKernelGGL((eng_attn_fused_kernel<true, false, I8>), grid, block, lds, s, b, ld, kv, p, d, nullptr,
-                               0, mh, l, pt, op);
+                               0, mh, l, pt, o);
         else if (wide && scores)
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8, true>), grid, block, 0, s, b, ld, kv, p, d,
-                               scores, max_length, mh, l, pt, op);
+                               scores, max_length, mh, l, pt, o);
         else if (wide)
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8, true>), grid, block, lds, s, b, ld, kv, p, d,
-                               nullptr, 0, mh, l, pt, op);
+                               nullptr, 0, mh, l, pt, o);
         else if (scores)
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
-                               max_length, mh, l, pt, op);
+                               max_length, mh, l, pt, o);
         else
             hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8>), grid, block, lds, s, b, ld, kv, p, d,
-                               nullptr, 0, mh, l, pt, op);
+                               nullptr, 0, mh, l, pt, o);
     };
     if (kv.k8) go(std::true_type{});
     else go(std::false_type{});

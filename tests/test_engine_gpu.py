@@ -276,15 +276,22 @@ HEADS128 = dict(SMALL, num_heads=4, num_kv_heads=2, head_dim=64)
 
 @pytest.mark.parametrize("bits", [2, 4])
 @pytest.mark.parametrize("int8_kv", [False, True])
-def test_out_projection_in_attention(bits, int8_kv, monkeypatch):
-    """The out-projection inside the attention launch (kv head h's workgroup computes its group's term of every
+@pytest.mark.parametrize("d_model,split", [(64, 0), (64, 2), (512, 0), (512, 1), (512, 2)])
+def test_out_projection_in_attention(bits, int8_kv, d_model, split, monkeypatch):
+    """The out-projection inside the attention launch (kv head h's workgroups compute its group's term of every
     output row, the post adds the terms in group order) gives the separate GEMV's bits
-    (NEEDLE2_ENGINE_OPROJ=gemv): steps and a prompt, every logit and hidden state; and, with the fp32 cache,
-    matches the reference (with the int8 cache both launch forms sit 9e-4 from the reference on this model: one
-    K / V code a step apart in the glue's rounding, as in the released geometry's int8 test)."""
-    a = Archive(synthetic_model(dict(HEADS128, max_seq_len=128), engram_layers=(1,), engram_orders=(2, 3),
-                                group=128, seed=13, layer_bits=bits))
+    (NEEDLE2_ENGINE_OPROJ=gemv): steps and a prompt, every logit and hidden state, with the rows of a step over
+    1, 2 or 4 workgroups per kv head (NEEDLE2_ENGINE_OSPLIT; each runs the head's attention); and, with the
+    fp32 cache, matches the reference (with the int8 cache both launch forms sit 9e-4 from the reference on
+    the 64-wide model: one K / V code a step apart in the glue's rounding, as in the released geometry's int8
+    test)."""
+    geometry = dict(HEADS128, max_seq_len=128)
+    if d_model != 64:
+        geometry.update(d_model=d_model, hada_n=d_model, engram_sub_dim=d_model // 4)
+    a = Archive(synthetic_model(geometry, engram_layers=(1,), engram_orders=(2, 3), group=128, seed=13,
+                                layer_bits=bits))
     kv = "int8" if int8_kv else "fp32"
+    monkeypatch.setenv("NEEDLE2_ENGINE_OSPLIT", str(split))
     fused = GpuEngine(a, kv_cache=kv)
     monkeypatch.setenv("NEEDLE2_ENGINE_OPROJ", "gemv")
     gemv = GpuEngine(a, kv_cache=kv)
