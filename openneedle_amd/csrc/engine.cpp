@@ -1103,20 +1103,23 @@ void GpuEngine::run(int tokens) {
     else
         launch_eng_dense_rows(emb.dense, D, ids.p, T, embed_z.p, s);
     launch_eng_start(embed_z.p, b, dims, T, s);
-    // engram sites up to layer `upto` onto the side stream, behind the upload
-    bool sent[kEngMaxSites] = {};
+    // engram sites up to layer `upto` onto the side stream, behind the upload (the side stream's wait for
+    // it is issued with the first site: issuing a wait costs the host ~14 us, which at the step's start
+    // would hold back the first layer's launches while the GPU idles)
+    bool sent[kEngMaxSites] = {}, side_waits = false;
     auto send_sites = [&](int upto) {
         for (int k = 0; k < c.num_sites; ++k)
             if (!sent[k] && c.sites[k] <= upto) {
+                if (!side_waits) {
+                    ND_HIP(hipStreamWaitEvent(side, ev_upload, 0));
+                    side_waits = true;
+                }
                 run_engram_site(k, T, side);
                 ND_HIP(hipEventRecord(ev_site[k], side));
                 sent[k] = true;
             }
     };
-    if (c.num_sites) {
-        ND_HIP(hipStreamWaitEvent(side, ev_upload, 0));
-        send_sites(1);
-    }
+    send_sites(1);
 
     const int G = c.heads / c.kvheads;
     int maxlen = 0;
