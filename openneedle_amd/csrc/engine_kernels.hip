@@ -1562,12 +1562,16 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     const int lane = threadIdx.x & 63, i = threadIdx.x;
     const bool lead = !QKVG || blockIdx.x == 0;
     // QKVG: this thread's row r of the workgroup's slice and group g, its codes (4 chunks of 4-bit codes or
-    // 2 of 2-bit) and half norm, requested first (rows past the piece and groups past the input: zeros)
+    // 2 of 2-bit) and half norm, requested after the post's own loads and the projection-row prefetch (the
+    // waits for those, counted in issue order, then do not wait for these; rows past the piece and groups
+    // past the input: zeros)
     const int qr = i % kQkvgRows, qg = i / kQkvgRows;
     u32x4 qc[4];
     uint32_t qn = 0;
     float *qy = nullptr;
     int qrow = 0, qrows = 0;
+    __amdgpu_buffer_rsrc_t qrc = buffer_rsrc(qf.piece[0].codes, 0u), qrn = buffer_rsrc(qf.piece[0].norms, 0u);
+    uint32_t qtile = 0, qrr = 0, qlive = 0;
     if constexpr (QKVG) {
         const int wg = blockIdx.x;
         int pi = 0;
@@ -1588,20 +1592,11 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         const int sub = wg - pick([](const QkvgPiece &p) { return p.sub_begin; });
         qrow = sub * kQkvgRows + qr;
         const uint32_t tiles = static_cast<uint32_t>((qrows + 255) / 256);
-        const __amdgpu_buffer_rsrc_t rc =
-            buffer_rsrc(codes, __builtin_amdgcn_readfirstlane(tiles * static_cast<uint32_t>(qf.chunks) * 4096u));
-        const __amdgpu_buffer_rsrc_t rn =
-            buffer_rsrc(norms, __builtin_amdgcn_readfirstlane(tiles * static_cast<uint32_t>(qf.groups) * 512u));
-        const uint32_t tile = static_cast<uint32_t>(qrow >> 8), rr = static_cast<uint32_t>(qrow & 255);
-        const uint32_t live = qrow < qrows && qg < qf.groups ? 0u : 0x40000000u;  // else past the resource
-        const int cpg = qf.kind == 0 ? 4 : 2;  // code chunks per group of 128 positions
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            qc[c] = __builtin_amdgcn_raw_buffer_load_b128(
-                rc, (c < cpg ? live : 0x40000000u) |
-                        (((tile * qf.chunks + static_cast<uint32_t>(qg * cpg + c)) * 256u + rr) * 16u), 0, 0);
-        qn = __builtin_amdgcn_raw_buffer_load_b16(
-            rn, live | (((tile * qf.groups + static_cast<uint32_t>(qg)) * 256u + rr) * 2u), 0, 0);
+        qrc = buffer_rsrc(codes, __builtin_amdgcn_readfirstlane(tiles * static_cast<uint32_t>(qf.chunks) * 4096u));
+        qrn = buffer_rsrc(norms, __builtin_amdgcn_readfirstlane(tiles * static_cast<uint32_t>(qf.groups) * 512u));
+        qtile = static_cast<uint32_t>(qrow >> 8);
+        qrr = static_cast<uint32_t>(qrow & 255);
+        qlive = qrow < qrows && qg < qf.groups ? 0u : 0x40000000u;  // else past the resource
     }
     float4 pf[kRowsPF][kPF];
     float x[8];
@@ -1622,6 +1617,16 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         }
         gp = gate_params<N>(mh, l + 1);
         nin = load_or_zero(ldn.norm_in, D, i);
+        if constexpr (QKVG) {
+            const int cpg = qf.kind == 0 ? 4 : 2;  // code chunks per group of 128 positions
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                qc[c] = __builtin_amdgcn_raw_buffer_load_b128(
+                    qrc, (c < cpg ? qlive : 0x40000000u) |
+                             (((qtile * qf.chunks + static_cast<uint32_t>(qg * cpg + c)) * 256u + qrr) * 16u), 0, 0);
+            qn = __builtin_amdgcn_raw_buffer_load_b16(
+                qrn, qlive | (((qtile * qf.groups + static_cast<uint32_t>(qg)) * 256u + qrr) * 2u), 0, 0);
+        }
     }, QKVG ? qf.x_out : b.x, lead);
     __syncthreads();
     const float4 *nx4 = reinterpret_cast<const float4 *>(mlp);
