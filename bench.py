@@ -22,6 +22,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extr
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -887,6 +888,9 @@ def main():
             extra[f"candidates_{k}_us"] = dist_us(v)
         log(f"candidates: { {k: v['median'] for k, v in extra.items() if k.startswith('candidates_')} }")
 
+        # the earlier workloads' device buffers and handles go before the latency-bound engine runs (held
+        # in reference cycles they measured slowing its step by ~5%)
+        gc.collect()
         log("engine: GpuEngine.step, released geometry (27 layers), batch 1")
         for kv, (tps, tok_ms) in bench_engine().items():
             extra[f"engine_{ENGINE_LABEL[kv]}_tokens_per_s"] = round(tps, 1)
