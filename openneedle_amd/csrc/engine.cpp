@@ -705,8 +705,8 @@ OutProj GpuEngine::out_projection(const Projection &p) const {
     return op;
 }
 
-// Layer l's Q|K|V|gate runs inside the previous layer's post launch
-// (QkvgFused) when its four matrices are one FP32 GEMV group of 2- or 4-bit
+// Layer l's Q|K|V|gate runs inside the previous layer's post launch (layer
+// 0's: inside the launch that starts the lanes and mixes) (QkvgFused) when its four matrices are one FP32 GEMV group of 2- or 4-bit
 // codes in groups of 128 over d_model <= 512 (a multiple of 128) inputs, with
 // no activation quantiser (NEEDLE2_ENGINE_QKVG=gemv: always the separate
 // GEMV); the step takes it where the post / mixing launch is fused and layer
@@ -716,7 +716,7 @@ QkvgFused GpuEngine::qkvg_fusion(int l) const {
     const char *mode = std::getenv("NEEDLE2_ENGINE_QKVG");
     if (mode && std::strcmp(mode, "gemv") == 0) return q;
     const Projection &p = qkvg[l];
-    if (l == 0 || abits || p.groups.size() != 1 || !p.groups8.empty() || !p.dense.empty() ||
+    if (abits || p.groups.size() != 1 || !p.groups8.empty() || !p.dense.empty() ||
         p.groups[0]->pieces != 4 || c.dim > 512 || c.dim % 128)
         return q;
     const int t0 = ti(l), idx[4] = {t0 + 1, t0 + 2, t0 + 3, t0 + 6};
@@ -1102,7 +1102,10 @@ void GpuEngine::run(int tokens) {
                        row_scratch.p, embed_z.p, s);
     else
         launch_eng_dense_rows(emb.dense, D, ids.p, T, embed_z.p, s);
-    launch_eng_start(embed_z.p, b, dims, T, s);
+    // a layer's post runs with the next layer's mHC projections and mixing (and the first layer's with
+    // the lanes' start) when those are dense and the geometry fits the fused kernel
+    const bool fuse = phi[0] && phi[1] && phi[2] && eng_post_mix_fits(dims);
+    if (!fuse) launch_eng_start(embed_z.p, b, dims, T, s);
     // engram sites up to layer `upto` onto the side stream, behind the upload (the side stream's wait for
     // it is issued with the first site: issuing a wait costs the host ~14 us, which at the step's start
     // would hold back the first layer's launches while the GPU idles)
@@ -1124,9 +1127,6 @@ void GpuEngine::run(int tokens) {
     const int G = c.heads / c.kvheads;
     int maxlen = 0;
     for (int t = 0; t < T; ++t) maxlen = std::max(maxlen, hparams.p[t].length);
-    // a layer's post runs with the next layer's mHC projections and mixing
-    // when those are dense and the geometry fits the fused kernel
-    const bool fuse = phi[0] && phi[1] && phi[2] && eng_post_mix_fits(dims);
     auto layer_sites = [&](int l, int *sites) {  // waits for their engram work
         int ns = 0;
         for (int k = 0; k < c.num_sites; ++k)
@@ -1150,7 +1150,23 @@ void GpuEngine::run(int tokens) {
     EngineBufs cur = b;
     float *other[4] = {alt_x, alt_u, alt_bx, alt_hpost};
     for (int l = 0; l < c.layers; ++l) {
-        if (l == 0 || !fuse) {
+        if (l == 0 && fuse) {  // the lanes' start, layer 0's projections and mixing (and Q|K|V|gate) in one launch
+            int sites[kEngMaxSites];
+            const int ns = layer_sites(0, sites);
+            const int first[3] = {0, 0, 0};
+            PrepTarget pt;
+            qkvg_prepared = target(qkvg[0], pt);
+            QkvgFused qf = qfused[0];
+            const bool with_qkvg = T == 1 && ns == 0 && !qkvg_prepared && qf.wgs > 0;
+            qf.x_out = cur.x;  // (nothing in this launch reads the state it writes)
+            qf.u_out = cur.u;
+            qf.bx_out = cur.bx;
+            qf.hpost_out = cur.hpost;
+            launch_eng_post_mix(cur, layer[0], layer[0], mh, -1, phi, first, sites, ns, dims, T, pt,
+                                with_qkvg ? &qf : nullptr, embed_z.p, s);
+            qkvg_done = with_qkvg;
+        }
+        if (!fuse) {
             mhc_proj[l].run(s, T);
             {
                 const int first[3] = {l * mhc_rows[0], l * mhc_rows[1], l * mhc_rows[2]};
@@ -1196,14 +1212,16 @@ void GpuEngine::run(int tokens) {
                 qf.u_out = other[1];
                 qf.bx_out = other[2];
                 qf.hpost_out = other[3];
-                launch_eng_post_mix(cur, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, pd, T, pt, &qf, s);
+                launch_eng_post_mix(cur, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, pd, T, pt, &qf, nullptr,
+                                    s);
                 std::swap(cur.x, other[0]);
                 std::swap(cur.u, other[1]);
                 std::swap(cur.bx, other[2]);
                 std::swap(cur.hpost, other[3]);
                 qkvg_done = true;
             } else {
-                launch_eng_post_mix(cur, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, pd, T, pt, nullptr, s);
+                launch_eng_post_mix(cur, layer[l], layer[l + 1], mh, l, phi, first, sites, ns, pd, T, pt, nullptr,
+                                    nullptr, s);
             }
         } else {
             launch_eng_post(cur, layer[l], l, l + 1 < c.layers, pd, T, s);

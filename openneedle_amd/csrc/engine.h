@@ -186,11 +186,13 @@ void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_r
 // The post of layer l, then layer l + 1's dense mHC projections (rows first[m] .. of the three
 // matrices w[m]) and mixing with the engram sites[0..nsites), in one launch; only where
 // eng_post_mix_fits(d). qf (null: none): layer l + 1's Q|K|V|gate projection in the same launch
-// (QkvgFused; one token, no engram site, no activation quantiser, no int8 target).
+// (QkvgFused; one token, no engram site, no activation quantiser, no int8 target). start (l = -1):
+// no post; the lanes come from the tokens' embedding rows start[t][D] (launch_eng_start's work), then
+// layer 0's projections and mixing.
 bool eng_post_mix_fits(const EngineDims &d);
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
-                         int tokens, const PrepTarget &pt, const QkvgFused *qf, hipStream_t s);
+                         int tokens, const PrepTarget &pt, const QkvgFused *qf, const float *start, hipStream_t s);
 void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, int tokens, hipStream_t s);
 // x[t][0..n) for t < tokens, rows `stride` apart
 void launch_eng_quantize(float *x, int n, int stride, int bits, int tokens, hipStream_t s);

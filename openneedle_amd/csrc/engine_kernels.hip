@@ -1527,10 +1527,12 @@ __device__ __forceinline__ const float4 *mhc_row_ptr(const DenseRows &w, int r, 
 // int8 target): workgroup blockIdx.x also computes one kQkvgRows-row slice of the
 // next layer's Q|K|V|gate projection (QkvgFused); workgroup 0 alone stores
 // the layer state, the lanes, u, bx and hpost into qf's *_out buffers.
-template <int THREADS, int N, bool QKVG>
+// START: no post; the token's lanes come from its embedding row ez (eng_start_kernel's work), then layer
+// 0's projections and mixing (l is -1).
+template <int THREADS, int N, bool QKVG, bool START>
 __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, LayerDev ld, LayerDev ldn, MhcDev mh,
                                                                int l, DenseRows w, MixArgs m, EngineDims d,
-                                                               PrepTarget pt, QkvgFused qf) {
+                                                               PrepTarget pt, QkvgFused qf, const float *ez) {
     struct Args {
         EngineBufs b0;
         LayerDev ld, ldn;
@@ -1541,9 +1543,10 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         EngineDims d;
         PrepTarget pt;
         QkvgFused qf;
+        const float *ez;
     };
     static_assert(!QKVG || THREADS == 512, "the fused projection takes 4 threads per row of its slice");
-    touch_kernargs<QKVG ? sizeof(Args) : offsetof(Args, pt)>();
+    touch_kernargs<QKVG ? offsetof(Args, ez) : offsetof(Args, pt)>();
     constexpr int kWaves = THREADS / 64, kPF = 8;  // float4 columns per lane held for each prefetched row
     constexpr int R = 2 * N + N * N;              // mHC projection rows
     constexpr int kRowsPF = std::min((R + kWaves - 1) / kWaves, 3);  // rows per wave held in registers
@@ -1602,7 +1605,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     float x[8];
     GateParams gp;
     float nin;
-    post_layer<N, kWaves>(b, ld, l, 1, d, red, mlp, hr, hpo, mlp, x, [&] {
+    auto issue = [&] {
         // buffer loads over each row (wave-uniform): a row past R and columns
         // past the row read zero, so no load waits behind a branch
 #pragma unroll
@@ -1627,7 +1630,29 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
             qn = __builtin_amdgcn_raw_buffer_load_b16(
                 qrn, qlive | (((qtile * qf.groups + static_cast<uint32_t>(qg)) * 256u + qrr) * 2u), 0, 0);
         }
-    }, QKVG ? qf.x_out : b.x, lead);
+    };
+    float *const xo = QKVG ? qf.x_out : b.x;
+    if constexpr (START) {
+        // the token's lanes x[n] = embedding * sqrt(d_model) and their rms (engine.cpp:972-974), the rms'd
+        // lanes into LDS for the projections below (l is -1: layer 0's mixing follows)
+        const float ze = load_or_zero(ez + static_cast<size_t>(blockIdx.y) * D, D, i);
+        issue();
+        float ss = 0.0f;
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+            x[n] = ze * d.sqrt_d;
+            ss += x[n] * x[n];
+        }
+        const float r = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(N * D) + 1e-6f);
+        if (i < D)
+#pragma unroll
+            for (int n = 0; n < N; ++n) {
+                mlp[n * D + i] = x[n] * r;
+                if (lead) xo[n * D + i] = x[n];
+            }
+    } else {
+        post_layer<N, kWaves>(b, ld, l, 1, d, red, mlp, hr, hpo, mlp, x, issue, xo, lead);
+    }
     __syncthreads();
     const float4 *nx4 = reinterpret_cast<const float4 *>(mlp);
     auto fma4 = [](float4 &acc, const float4 &a, const float4 &c) {
@@ -1908,7 +1933,7 @@ bool eng_post_mix_fits(const EngineDims &d) {
 
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
-                         int tokens, const PrepTarget &pt, const QkvgFused *qf, hipStream_t s) {
+                         int tokens, const PrepTarget &pt, const QkvgFused *qf, const float *start, hipStream_t s) {
     ND_CHECK(eng_post_mix_fits(d), "internal: fused post / mixing launch outside its geometry");
     ND_CHECK(!qf || (tokens == 1 && nsites == 0 && !pt.q && d.abits == 0 && d.D <= 512 && d.D % 128 == 0 &&
                      qf->wgs > 0 && qf->pieces >= 1 && qf->pieces <= 4 && qf->groups == d.D / 128 &&
@@ -1923,18 +1948,24 @@ void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev
     m.l = l + 1;
     m.nsites = nsites;
     for (int k = 0; k < nsites; ++k) m.sites[k] = sites[k];
+    ND_CHECK(!start || l == -1, "internal: the first layer's mixing takes l = -1");
     const QkvgFused none{};
-    with_lanes(d.N, [&](auto n) {
+    auto go = [&](auto n, auto st) {
         constexpr int N = decltype(n)::value;
+        constexpr bool S = decltype(st)::value;
         if (qf)
-            hipLaunchKernelGGL((eng_post_mix_kernel<512, N, true>), dim3(qf->wgs, 1), dim3(512), 0, s, b, ld, ldn, mh,
-                               l, a, m, d, pt, *qf);
+            hipLaunchKernelGGL((eng_post_mix_kernel<512, N, true, S>), dim3(qf->wgs, 1), dim3(512), 0, s, b, ld, ldn,
+                               mh, l, a, m, d, pt, *qf, start);
         else if (d.D <= 512)
-            hipLaunchKernelGGL((eng_post_mix_kernel<512, N, false>), dim3(1, tokens), dim3(512), 0, s, b, ld, ldn, mh,
-                               l, a, m, d, pt, none);
+            hipLaunchKernelGGL((eng_post_mix_kernel<512, N, false, S>), dim3(1, tokens), dim3(512), 0, s, b, ld, ldn,
+                               mh, l, a, m, d, pt, none, start);
         else
-            hipLaunchKernelGGL((eng_post_mix_kernel<kEngThreads, N, false>), dim3(1, tokens), dim3(kEngThreads), 0, s,
-                               b, ld, ldn, mh, l, a, m, d, pt, none);
+            hipLaunchKernelGGL((eng_post_mix_kernel<kEngThreads, N, false, S>), dim3(1, tokens), dim3(kEngThreads), 0,
+                               s, b, ld, ldn, mh, l, a, m, d, pt, none, start);
+    };
+    with_lanes(d.N, [&](auto n) {
+        if (start) go(n, std::true_type{});
+        else go(n, std::false_type{});
     });
     ND_HIP(hipGetLastError());
 }
