@@ -1224,11 +1224,12 @@ void GpuEngine::run(int tokens) {
                                     nullptr, s);
             }
         } else {
-            launch_eng_post(cur, layer[l], l, l + 1 < c.layers, pd, T, s);
+            // (the last layer's post also computes the final norm)
+            launch_eng_post(cur, layer[l], l, l + 1 < c.layers, pd, T, l + 1 == c.layers ? dptr[final_norm()] : nullptr,
+                            s);
         }
         send_sites(l + 3);  // two layers ahead of their use
     }
-    launch_eng_final(cur, dptr[final_norm()], dims, T, s);
 }
 
 void GpuEngine::step(int token, float *logits_out, float *hidden_out) {

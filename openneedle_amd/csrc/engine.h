@@ -181,8 +181,9 @@ void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLaye
 // K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
 void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
                           const EngineDims &d, hipStream_t s);
+// final_norm (the last layer; null: none): also zf = rms(hidden) * (1 + final_norm)
 void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_rms,
-                     const EngineDims &d, int tokens, hipStream_t s);
+                     const EngineDims &d, int tokens, const float *final_norm, hipStream_t s);
 // The post of layer l, then layer l + 1's dense mHC projections (rows first[m] .. of the three
 // matrices w[m]) and mixing with the engram sites[0..nsites), in one launch; only where
 // eng_post_mix_fits(d). qf (null: none): layer l + 1's Q|K|V|gate projection in the same launch
@@ -193,7 +194,6 @@ bool eng_post_mix_fits(const EngineDims &d);
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
                          int tokens, const PrepTarget &pt, const QkvgFused *qf, const float *start, hipStream_t s);
-void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, int tokens, hipStream_t s);
 // x[t][0..n) for t < tokens, rows `stride` apart
 void launch_eng_quantize(float *x, int n, int stride, int bits, int tokens, hipStream_t s);
 // y[t][r] = dot(W[first + r], x[t]) over cols for r < rows (dense fp32 matrices); x rows cols

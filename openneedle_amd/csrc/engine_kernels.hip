@@ -1442,23 +1442,25 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
     }
 }
 
+// final_norm set (the last layer): then zf = rms(hidden) * (1 + final_norm) (engine.cpp:1041-1042), thread i
+// holding hidden value i.
 template <int N>
 __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, LayerDev ld, int l, int next_rms,
-                                                               EngineDims d) {
+                                                               EngineDims d, const float *__restrict__ final_norm) {
     const EngineBufs b = at_token(b0, d, blockIdx.y);
     __shared__ float red[kEngThreads / 64];
     __shared__ float mlp[4096];
     __shared__ float hr[64], hpo[8];
     float x[8];
     post_layer<N, kEngThreads / 64>(b, ld, l, next_rms, d, red, mlp, hr, hpo, nullptr, x, [] {}, b.x, true);
-}
-
-// z = rms(hidden of the last layer) * (1 + final_norm) (engine.cpp:1041-1042).
-__global__ __launch_bounds__(kEngThreads) void eng_final_kernel(EngineBufs b0, const float *__restrict__ final_norm,
-                                                                EngineDims d) {
-    __shared__ float red[kEngThreads / 64];
-    const EngineBufs b = at_token(b0, d, blockIdx.y);
-    rms_block(b.hidden + (d.layers - 1) * d.D, b.zf, d.D, final_norm, red);
+    if (final_norm) {
+        const int i = threadIdx.x;
+        const bool own = i < d.D;
+        const float h = own ? b.hidden[l * d.D + i] : 0.0f;  // this thread's own store above
+        const float gain = own ? final_norm[i] : 0.0f;
+        const float r = 1.0f / sqrtf(block_sum(h * h, red) / static_cast<float>(d.D) + 1e-6f);
+        if (own) b.zf[i] = h * r * (1.0f + gain);
+    }
 }
 
 __global__ __launch_bounds__(kEngThreads) void eng_quantize_kernel(float *x, int n, int stride, int bits) {
@@ -1919,10 +1921,12 @@ void launch_eng_kv_import(const float *k, const float *v, const int *slots, int 
 }
 
 void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_rms,
-                     const EngineDims &d, int tokens, hipStream_t s) {
+                     const EngineDims &d, int tokens, const float *final_norm, hipStream_t s) {
+    ND_CHECK(!final_norm || (l == d.layers - 1 && !next_rms && d.D <= kEngThreads),
+             "internal: the final norm follows the last layer's post");
     with_lanes(d.N, [&](auto n) {
         hipLaunchKernelGGL(eng_post_kernel<decltype(n)::value>, dim3(1, tokens), dim3(kEngThreads), 0, s, b, ld, l,
-                           next_rms ? 1 : 0, d);
+                           next_rms ? 1 : 0, d, final_norm);
     });
     ND_HIP(hipGetLastError());
 }
@@ -1967,11 +1971,6 @@ void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev
         if (start) go(n, std::true_type{});
         else go(n, std::false_type{});
     });
-    ND_HIP(hipGetLastError());
-}
-
-void launch_eng_final(const EngineBufs &b, const float *final_norm, const EngineDims &d, int tokens, hipStream_t s) {
-    hipLaunchKernelGGL(eng_final_kernel, dim3(1, tokens), dim3(kEngThreads), 0, s, b, final_norm, d);
     ND_HIP(hipGetLastError());
 }
 
