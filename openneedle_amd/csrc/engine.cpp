@@ -1194,8 +1194,8 @@ void GpuEngine::run(int tokens) {
         const OutProj &op = ofused[l];
         EngineDims pd = dims;  // the post's view: the attention's out-projection terms, or proj
         pd.ogroups = op.codes ? c.kvheads : 0;
-        launch_eng_attn_fused(cur, layer[l], kv[l], dp, maxlen, T > 1, dims, T, attn_scores.p, attn_scores.n, mh, l,
-                              ot, op, s);
+        launch_eng_attn_fused(cur, layer[l], kv[l], dp, hparams.p[0], maxlen, T > 1, dims, T, attn_scores.p,
+                              attn_scores.n, mh, l, ot, op, s);
         if (!op.codes) {
             launch_eng_quantize(b.att, c.heads * HD, c.heads * HD, abits, T, s);
             oproj[l].run(s, T, o_prepared);

@@ -27,6 +27,14 @@ struct StepParams {
     float rope_cos[kEngMaxHalfHd], rope_sin[kEngMaxHalfHd];
 };
 
+// A decode step's slot-list parameters (StepParams' first fields), passed by
+// value to the attention launch: in its kernel arguments they arrive with the
+// first round of argument loads, a memory round trip ahead of the uploaded
+// StepParams.
+struct StepHead {
+    int slot, length, prefix_count, start, prefix, window, ring;
+};
+
 // Work buffers hold a chunk of tokens: token t of a launch is blockIdx.y and
 // its vectors sit t per-token sizes past the token-0 pointers below.
 // Prompt chunk: at most kEngMaxChunk tokens (engine.cpp:1054 takes 32), every
@@ -174,10 +182,11 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 // head's outputs, heads / kvheads * head_dim positions).
 // With op.codes set (and G * head_dim == 128, no pt) each kv head's workgroup also computes its group's
 // out-projection terms (OutProj).
+// hp: the host copy of token 0's StepParams (a step's slot list goes in the kernel arguments).
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
-                           int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt, const OutProj &op,
-                           hipStream_t s);
+                           const StepParams &hp, int max_length, bool prepared, const EngineDims &d, int tokens,
+                           float *scores, size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt,
+                           const OutProj &op, hipStream_t s);
 // K / V rows [count][kvheads][head_dim] into cache slots[count] (device) of one layer
 void launch_eng_kv_import(const float *k, const float *v, const int *slots, int count, const KvLayer &kv,
                           const EngineDims &d, hipStream_t s);

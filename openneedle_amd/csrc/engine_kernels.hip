@@ -400,6 +400,9 @@ struct SlotMap {
     __device__ explicit SlotMap(const StepParams *p)
         : prefix_count(p->prefix_count), start(p->start), window(p->window), prefix(p->prefix),
           ring(p->ring > 0 ? p->ring : 1) {}
+    __device__ explicit SlotMap(const StepHead &h)
+        : prefix_count(h.prefix_count), start(h.start), window(h.window), prefix(h.prefix),
+          ring(h.ring > 0 ? h.ring : 1) {}
     __device__ int operator()(int s) const {
         const int pos = s < prefix_count ? s : start + s - prefix_count;
         const int wrapped = prefix + (pos - prefix) % ring;
@@ -672,14 +675,15 @@ __global__ __launch_bounds__(kEngThreads) void eng_qk_kernel(EngineBufs b0, Laye
 // of the K prefetch.
 template <bool PREPARED, bool GLOBAL_SCORES, bool I8, bool WIDE = false>
 __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, LayerDev ld, KvLayer kv,
-                                                             const StepParams *__restrict__ p, EngineDims d,
-                                                             float *__restrict__ scores, int max_length, MhcDev mh,
-                                                             int layer, PrepTarget pt, OutProj op) {
+                                                             const StepParams *__restrict__ p, StepHead sh,
+                                                             EngineDims d, float *__restrict__ scores, int max_length,
+                                                             MhcDev mh, int layer, PrepTarget pt, OutProj op) {
     struct Args {
         EngineBufs b0;
         LayerDev ld;
         KvLayer kv;
         const StepParams *p;
+        StepHead sh;
         EngineDims d;
         float *scores;
         int max_length;
@@ -705,7 +709,9 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     float *sc = GLOBAL_SCORES
                     ? scores + (static_cast<size_t>(blockIdx.y) * d.KV + kh) * G * static_cast<size_t>(max_length)
                     : sc_lds;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63, length = p->length;
+    // one token (not PREPARED): the slot list from the kernel arguments
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63, length = PREPARED ? p->length : sh.length;
+    const int my_slot = PREPARED ? p->slot : sh.slot;  // this token's cache slot
     const size_t row0 = static_cast<size_t>(kh) * d.capacity;  // this kv head's first cache row
     const float *kc = I8 ? nullptr : kv.k32 + row0 * HD;
     const float *vc = I8 ? nullptr : kv.v32 + row0 * HD;
@@ -716,7 +722,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     // loaded before the norms: the output gate of output t, and at head_dim 64 the K row of this thread's
     // first slot unless this kernel stores that row below (the new token's)
     // (loads without branches: an entry past the list reads slot 0 and is not used)
-    const SlotMap slot_of(p);
+    const SlotMap slot_of = PREPARED ? SlotMap(p) : SlotMap(sh);
     const float gate_t = load_or_zero(b.gate + kh * G * HD, G * HD, t);
     // The inputs of this wave's first norm / RoPE head (h = wave <= G, head_dim
     // <= 128: one RoPE pair per lane) and the new V row, loaded before the K
@@ -740,7 +746,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         if (!I8) vnew = load_or_zero(b.v + kh * HD, HD, t);
     }
     const int slot_t = t < length ? slot_of(t) : 0;
-    const bool k_early = HD == 64 && t < length && (PREPARED || slot_t != p->slot);
+    const bool k_early = HD == 64 && t < length && (PREPARED || slot_t != my_slot);
     float4 kpre[I8 ? 4 : 16];  // fp32: the row; int8: its 64 codes
     float kpre_s = 0.0f;
     {  // buffer loads over this kv head's rows (nothing unless head_dim is 64; a thread past the list
@@ -781,7 +787,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         const uint32_t rows = __builtin_amdgcn_readfirstlane(HD == 64 ? static_cast<uint32_t>(d.capacity) : 0u);
         const __amdgpu_buffer_rsrc_t ve =
             buffer_rsrc(I8 ? static_cast<const void *>(vc8) : static_cast<const void *>(vc), rows * 64u * esz);
-        const int new_slot = PREPARED ? -1 : p->slot;  // (read once: not a scalar load per row)
+        const int new_slot = PREPARED ? -1 : my_slot;
         SlotWalk wk(slot_of, r, R);
 #pragma unroll
         for (int k = 0; k < 2 * kPre; ++k, wk.next()) {
@@ -803,7 +809,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
     // floats) and their scale also go to LDS (kq, knew_scale) for the scores
     auto quantize_new_kv = [&](const float *kw, float *kq) {
         const float *vr = b.v + kh * HD;
-        const size_t row = row0 + p->slot;
+        const size_t row = row0 + my_slot;
         float mk = 0.0f, mv = 0.0f;
         for (int i = lane; i < HD; i += 64) {
             mk = fmaxf(mk, fabsf(kw[i]));
@@ -866,7 +872,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
                 __builtin_amdgcn_wave_barrier();
                 quantize_new_kv(kw, qs + (kMaxG + 1) * HD);
             } else {
-                ND_GLOBAL float *kw = (ND_GLOBAL float *)(kv.k32 + (row0 + p->slot) * HD);
+                ND_GLOBAL float *kw = (ND_GLOBAL float *)(kv.k32 + (row0 + my_slot) * HD);
                 float *knew = qs + kMaxG * HD;  // the new row for the scores, from LDS
                 if (lane < half) {
                     kw[lane] = lo;
@@ -877,12 +883,12 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
             }
         }
         if (!I8 && t < HD) {
-            ((ND_GLOBAL float *)kv.v32)[(row0 + p->slot) * HD + t] = vnew;
+            ((ND_GLOBAL float *)kv.v32)[(row0 + my_slot) * HD + t] = vnew;
             qs[(kMaxG + 2) * HD + t] = vnew;  // the new V row for the values, from LDS
         }
     } else {
     // the general form: any head_dim, several heads per wave
-    float *kw = I8 ? qs + kMaxG * HD : kv.k32 + row0 * HD + static_cast<size_t>(p->slot) * HD;
+    float *kw = I8 ? qs + kMaxG * HD : kv.k32 + row0 * HD + static_cast<size_t>(my_slot) * HD;
     for (int h = wave; h <= G; h += blockDim.x >> 6) {
         const float *src = h < G ? b.q + (kh * G + h) * HD : b.k + kh * HD;
         const float *gain = h < G ? ld.q_norm : ld.k_norm;
@@ -900,7 +906,7 @@ __global__ __launch_bounds__(256) void eng_attn_fused_kernel(EngineBufs b0, Laye
         if (I8 && h == G) quantize_new_kv(kw, nullptr);
     }
     if (!I8)
-        for (int i = t; i < HD; i += blockDim.x) kv.v32[(row0 + p->slot) * HD + i] = b.v[kh * HD + i];
+        for (int i = t; i < HD; i += blockDim.x) kv.v32[(row0 + my_slot) * HD + i] = b.v[kh * HD + i];
     }
     __syncthreads();
     // V loads are buffer loads: an entry past the list reads zeros (offset past the resource)
@@ -1870,9 +1876,10 @@ void launch_eng_qk(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, c
 }
 
 void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLayer &kv, const StepParams *p,
-                           int max_length, bool prepared, const EngineDims &d, int tokens, float *scores,
-                           size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt, const OutProj &op,
-                           hipStream_t s) {
+                           const StepParams &hp, int max_length, bool prepared, const EngineDims &d, int tokens,
+                           float *scores, size_t scores_n, const MhcDev &mh, int l, const PrepTarget &pt,
+                           const OutProj &op, hipStream_t s) {
+    const StepHead sh{hp.slot, hp.length, hp.prefix_count, hp.start, hp.prefix, hp.window, hp.ring};
     ND_CHECK(!op.codes || (d.H / d.KV * d.HD == 128 && !pt.q && op.rows <= 512 && d.KV <= 8),
              "internal: fused out-projection outside its geometry");
     // the score slices are [tokens][kv heads][G][max_length] (the routing workgroup touches none)
@@ -1890,22 +1897,22 @@ void launch_eng_attn_fused(const EngineBufs &b, const LayerDev &ld, const KvLaye
     auto go = [&](auto i8) {
         constexpr bool I8 = decltype(i8)::value;
         if (prepared && scores)
-            hipLaunchKernelGGL((eng_attn_fused_kernel<true, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
+            hipLaunchKernelGGL((eng_attn_fused_kernel<true, true, I8>), grid, block, 0, s, b, ld, kv, p, sh, d, scores,
                                max_length, mh, l, pt, o);
         else if (prepared)
-            hipLaunchKernelGGL((eng_attn_fused_kernel<true, false, I8>), grid, block, lds, s, b, ld, kv, p, d, nullptr,
+            hipLaunchKernelGGL((eng_attn_fused_kernel<true, false, I8>), grid, block, lds, s, b, ld, kv, p, sh, d, nullptr,
                                0, mh, l, pt, o);
         else if (wide && scores)
-            hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8, true>), grid, block, 0, s, b, ld, kv, p, d,
+            hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8, true>), grid, block, 0, s, b, ld, kv, p, sh, d,
                                scores, max_length, mh, l, pt, o);
         else if (wide)
-            hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8, true>), grid, block, lds, s, b, ld, kv, p, d,
+            hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8, true>), grid, block, lds, s, b, ld, kv, p, sh, d,
                                nullptr, 0, mh, l, pt, o);
         else if (scores)
-            hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8>), grid, block, 0, s, b, ld, kv, p, d, scores,
+            hipLaunchKernelGGL((eng_attn_fused_kernel<false, true, I8>), grid, block, 0, s, b, ld, kv, p, sh, d, scores,
                                max_length, mh, l, pt, o);
         else
-            hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8>), grid, block, lds, s, b, ld, kv, p, d,
+            hipLaunchKernelGGL((eng_attn_fused_kernel<false, false, I8>), grid, block, lds, s, b, ld, kv, p, sh, d,
                                nullptr, 0, mh, l, pt, o);
     };
     if (kv.k8) go(std::true_type{});
