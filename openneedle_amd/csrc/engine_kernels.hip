@@ -106,6 +106,18 @@ __device__ float block_sum(float v, float *red) {
     return s;
 }
 
+// block_sum without its first barrier, for calls that alternate between two
+// red buffers: the barrier inside the call between two uses of one buffer
+// orders the earlier call's reads before the later call's writes.
+__device__ float block_sum_nb(float v, float *red) {
+    v = wave_sum(v, threadIdx.x & 63);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) s += red[w];
+    return s;
+}
+
 __device__ float block_max(float v, float *red) {
     v = wave_max(v, threadIdx.x & 63);
     __syncthreads();
@@ -1395,11 +1407,12 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
         if (lane < N) hpo[lane] = hpost;
     }
     // proj = rms(proj) * (1 + post_norm); bx += sigmoid(attn_gate) * proj
-    float r = 1.0f / sqrtf(block_sum(own ? proj * proj : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+    // (red holds 2 * WAVES floats: the block sums alternate between its halves)
+    float r = 1.0f / sqrtf(block_sum_nb(own ? proj * proj : 0.0f, red) / static_cast<float>(D) + 1e-6f);
     proj = proj * r * (1.0f + gn);
     bx += ag * proj;
     // z = rms(bx) * (1 + pre_hada); mlp = hadamard(silu_diag(hadamard(z * d1 | 0), d2)) (engine.cpp:1029-1033)
-    r = 1.0f / sqrtf(block_sum(own ? bx * bx : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+    r = 1.0f / sqrtf(block_sum_nb(own ? bx * bx : 0.0f, red + WAVES) / static_cast<float>(D) + 1e-6f);
     const float z = bx * r * (1.0f + gh);
     float mv;  // value i of the MLP vector (own threads)
     if (d.hada == 64 * WAVES) {  // one value per thread: the transforms in registers, mlp as staging
@@ -1440,7 +1453,7 @@ __device__ __forceinline__ void post_layer(const EngineBufs &b, const LayerDev &
         if (lead) b.hidden[l * D + i] = sum / static_cast<float>(N);
     }
     if (next_rms) {  // the next layer's nx = rms(x) over all N * D values
-        r = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(N * D) + 1e-6f);
+        r = 1.0f / sqrtf(block_sum_nb(ss, red) / static_cast<float>(N * D) + 1e-6f);
         float *nx = nxs ? nxs : b.nx;
         if (own)
 #pragma unroll
@@ -1454,7 +1467,7 @@ template <int N>
 __global__ __launch_bounds__(kEngThreads) void eng_post_kernel(EngineBufs b0, LayerDev ld, int l, int next_rms,
                                                                EngineDims d, const float *__restrict__ final_norm) {
     const EngineBufs b = at_token(b0, d, blockIdx.y);
-    __shared__ float red[kEngThreads / 64];
+    __shared__ float red[2 * (kEngThreads / 64)];
     __shared__ float mlp[4096];
     __shared__ float hr[64], hpo[8];
     float x[8];
@@ -1559,7 +1572,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     constexpr int R = 2 * N + N * N;              // mHC projection rows
     constexpr int kRowsPF = std::min((R + kWaves - 1) / kWaves, 3);  // rows per wave held in registers
     const EngineBufs b = at_token(b0, d, blockIdx.y);
-    __shared__ float red[kWaves];
+    __shared__ float red[2 * kWaves];
     __shared__ float mlp[4096];  // the MLP vector, then the rms'd lanes
     __shared__ float hr[64], hpo[8], hp[16];
     __shared__ float zs[QKVG ? 1 : 4096], ps[QKVG ? 1 : 4096];
@@ -1651,7 +1664,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
             x[n] = ze * d.sqrt_d;
             ss += x[n] * x[n];
         }
-        const float r = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(N * D) + 1e-6f);
+        const float r = 1.0f / sqrtf(block_sum_nb(ss, red) / static_cast<float>(N * D) + 1e-6f);
         if (i < D)
 #pragma unroll
             for (int n = 0; n < N; ++n) {
@@ -1726,7 +1739,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         mix_sites(b, m, d, red, zs, ps);
         rms_block(b.bx, b.z, D, ldn.norm_in, red);
     } else {  // rms_block's arithmetic on the registers
-        const float r = 1.0f / sqrtf(block_sum(own ? u * u : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+        const float r = 1.0f / sqrtf(block_sum_nb(own ? u * u : 0.0f, red + kWaves) / static_cast<float>(D) + 1e-6f);
         if (own) {
             z = u * r * (1.0f + nin);
             if (lead) b.z[i] = z;
