@@ -35,15 +35,6 @@ namespace nd {
 
 namespace {
 
-// Waits for the stream by polling it: a decode step waits on the host for every
-// token, and hipStreamSynchronize's wake-up cost 2-10% of a step (measured: step
-// 1527-1544 -> 1551-1587 tokens/s, int8 matmul path 1258-1264 -> 1289-1393).
-// The host thread spins for the step's few hundred microseconds.
-void wait_stream(hipStream_t s) {
-    for (hipError_t q = hipStreamQuery(s); q != hipSuccess; q = hipStreamQuery(s))
-        if (q != hipErrorNotReady) ND_HIP(q);
-}
-
 // needle2/csrc/engine.cpp:14-19 (layouts must match the reference's).
 struct TensorDescC {
     void *cq;
@@ -1354,7 +1345,7 @@ void GpuEngine::project_candidates(const int *candidates, int count, float *out)
         launch_gather_outputs(logits.p, c.vocab, st.ids.p, count, 1, st.y.p, s);
     }
     ND_HIP(hipMemcpyAsync(st.hy.p, st.y.p, size_t(count) * sizeof(float), hipMemcpyDeviceToHost, s));
-    wait_stream(s);
+    ND_HIP(hipStreamSynchronize(s));
     std::memcpy(out, st.hy.p, size_t(count) * sizeof(float));
 }
 
