@@ -1095,16 +1095,20 @@ void GpuEngine::run(int tokens) {
     if (c.num_sites) ND_HIP(hipEventRecord(ev_upload, s));
     const StepParams *dp = params.p;
 
-    // embedding rows, lanes (engine.cpp:972-974)
+    // a layer's post runs with the next layer's mHC projections and mixing (and the first layer's with
+    // the lanes' start) when those are dense and the geometry fits the fused kernel
+    const bool fuse = phi[0] && phi[1] && phi[2] && eng_post_mix_fits(dims);
+    // embedding rows, lanes (engine.cpp:972-974); a CQ embedding of d_model <= 512 (no padding) is decoded
+    // inside the first layer's launch
     const Mat &emb = mats[0];
-    if (emb.cq)
+    EmbedRows er{};
+    if (fuse && emb.cq && D <= 512 && emb.cq->padded == D && emb.cq->group <= D)
+        er = EmbedRows{emb.cq->codes.p, emb.cq->norms.p, ids.p, embed_z.p, emb.cq->geom()};
+    else if (emb.cq)
         launch_cq_rows(emb.cq->geom(), emb.cq->codes.p, emb.cq->norms.p, ids.p, T, D, emb.cq->padded,
                        row_scratch.p, embed_z.p, s);
     else
         launch_eng_dense_rows(emb.dense, D, ids.p, T, embed_z.p, s);
-    // a layer's post runs with the next layer's mHC projections and mixing (and the first layer's with
-    // the lanes' start) when those are dense and the geometry fits the fused kernel
-    const bool fuse = phi[0] && phi[1] && phi[2] && eng_post_mix_fits(dims);
     if (!fuse) launch_eng_start(embed_z.p, b, dims, T, s);
     // engram sites up to layer `upto` onto the side stream, behind the upload (the side stream's wait for
     // it is issued with the first site: issuing a wait costs the host ~14 us, which at the step's start
@@ -1163,7 +1167,7 @@ void GpuEngine::run(int tokens) {
             qf.bx_out = cur.bx;
             qf.hpost_out = cur.hpost;
             launch_eng_post_mix(cur, layer[0], layer[0], mh, -1, phi, first, sites, ns, dims, T, pt,
-                                with_qkvg ? &qf : nullptr, embed_z.p, s);
+                                with_qkvg ? &qf : nullptr, embed_z.p, s, er);
             qkvg_done = with_qkvg;
         }
         if (!fuse) {

@@ -136,6 +136,18 @@ struct QkvgFused {
     float *x_out, *u_out, *bx_out, *hpost_out;  // the new lanes, u, bx and lane post gates
 };
 
+// The tokens' embedding rows decoded inside the first layer's launch (a CQ
+// embedding whose padded width is d_model): the row kernel's arithmetic
+// (cb[code] * half(norm)), then the FWHT of each group in the transform's
+// stage order and the scale, into z[t][d_model] as the row kernels leave it.
+struct EmbedRows {
+    const uint4 *codes;  // null: the rows come from z, decoded by the row kernels
+    const uint16_t *norms;
+    const int64_t *ids;  // the tokens' rows
+    float *z;
+    CqGeom g;
+};
+
 // KV cache of one layer: fp32 (k32 / v32) or int8 codes with fp32 scales,
 // [kvheads][capacity][head_dim] (scales [kvheads][capacity]).
 struct KvLayer {
@@ -197,12 +209,13 @@ void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_r
 // matrices w[m]) and mixing with the engram sites[0..nsites), in one launch; only where
 // eng_post_mix_fits(d). qf (null: none): layer l + 1's Q|K|V|gate projection in the same launch
 // (QkvgFused; one token, no engram site, no activation quantiser, no int8 target). start (l = -1):
-// no post; the lanes come from the tokens' embedding rows start[t][D] (launch_eng_start's work), then
-// layer 0's projections and mixing.
+// no post; the lanes come from the tokens' embedding rows start[t][D] (launch_eng_start's work; er.codes
+// set: decoded here into start, EmbedRows), then layer 0's projections and mixing.
 bool eng_post_mix_fits(const EngineDims &d);
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
-                         int tokens, const PrepTarget &pt, const QkvgFused *qf, const float *start, hipStream_t s);
+                         int tokens, const PrepTarget &pt, const QkvgFused *qf, const float *start, hipStream_t s,
+                         const EmbedRows &er = EmbedRows{});
 // x[t][0..n) for t < tokens, rows `stride` apart
 void launch_eng_quantize(float *x, int n, int stride, int bits, int tokens, hipStream_t s);
 // y[t][r] = dot(W[first + r], x[t]) over cols for r < rows (dense fp32 matrices); x rows cols

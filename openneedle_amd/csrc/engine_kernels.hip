@@ -1553,7 +1553,8 @@ __device__ __forceinline__ const float4 *mhc_row_ptr(const DenseRows &w, int r, 
 template <int THREADS, int N, bool QKVG, bool START>
 __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, LayerDev ld, LayerDev ldn, MhcDev mh,
                                                                int l, DenseRows w, MixArgs m, EngineDims d,
-                                                               PrepTarget pt, QkvgFused qf, const float *ez) {
+                                                               PrepTarget pt, QkvgFused qf, const float *ez,
+                                                               EmbedRows er) {
     struct Args {
         EngineBufs b0;
         LayerDev ld, ldn;
@@ -1565,6 +1566,7 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         PrepTarget pt;
         QkvgFused qf;
         const float *ez;
+        EmbedRows er;
     };
     static_assert(!QKVG || THREADS == 512, "the fused projection takes 4 threads per row of its slice");
     touch_kernargs<QKVG ? offsetof(Args, ez) : offsetof(Args, pt)>();
@@ -1656,8 +1658,39 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
     if constexpr (START) {
         // the token's lanes x[n] = embedding * sqrt(d_model) and their rms (engine.cpp:972-974), the rms'd
         // lanes into LDS for the projections below (l is -1: layer 0's mixing follows)
-        const float ze = load_or_zero(ez + static_cast<size_t>(blockIdx.y) * D, D, i);
-        issue();
+        float ze;
+        if (er.codes) {  // the token's embedding row: cb[code] * half(norm) at position i, then the FWHT
+            const CqGeom &g = er.g;
+            const int row = static_cast<int>(er.ids[blockIdx.y]);
+            const int own_i = i < D ? i : 0;
+            const int cpc = g.kind == kNib ? 32 : 64, c = own_i / cpc, within = own_i % cpc;
+            const uint4 v = er.codes[code_index(row, c, g.chunks)];
+            const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t code = g.kind == kNib ? (words[within >> 3] >> ((within & 7) * 4)) & 15u
+                                                 : (words[within >> 4] >> ((within & 15) * 2)) & 3u;
+            const float norm = h2f(er.norms[norm_index(row, own_i / g.group, g.groups)]);
+            issue();
+            ze = i < D ? g.lut[code] * norm : 0.0f;
+            // stages h = 1 .. group / 2 in order, (a + b, a - b) as the transform kernel's
+            if (g.group > 1) ze = fwht_stage<1>(ze, lane);
+            if (g.group > 2) ze = fwht_stage<2>(ze, lane);
+            if (g.group > 4) ze = fwht_stage<4>(ze, lane);
+            if (g.group > 8) ze = fwht_stage<8>(ze, lane);
+            if (g.group > 16) ze = fwht_stage<16>(ze, lane);
+            if (g.group > 32) ze = fwht_stage<32>(ze, lane);
+            for (int h = 64; h < g.group; h <<= 1) {
+                mlp[i] = ze;
+                __syncthreads();
+                const float o = mlp[i ^ h];
+                __syncthreads();
+                ze = (i & h) ? o - ze : ze + o;
+            }
+            ze = i < D ? ze * g.scale : 0.0f;
+            if (lead && i < D) er.z[static_cast<size_t>(blockIdx.y) * D + i] = ze;
+        } else {
+            ze = load_or_zero(ez + static_cast<size_t>(blockIdx.y) * D, D, i);
+            issue();
+        }
         float ss = 0.0f;
 #pragma unroll
         for (int n = 0; n < N; ++n) {
@@ -1957,7 +1990,8 @@ bool eng_post_mix_fits(const EngineDims &d) {
 
 void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev &ldn, const MhcDev &mh, int l,
                          const float *const *w, const int *first, const int *sites, int nsites, const EngineDims &d,
-                         int tokens, const PrepTarget &pt, const QkvgFused *qf, const float *start, hipStream_t s) {
+                         int tokens, const PrepTarget &pt, const QkvgFused *qf, const float *start, hipStream_t s,
+                         const EmbedRows &er) {
     ND_CHECK(eng_post_mix_fits(d), "internal: fused post / mixing launch outside its geometry");
     ND_CHECK(!qf || (tokens == 1 && nsites == 0 && !pt.q && d.abits == 0 && d.D <= 512 && d.D % 128 == 0 &&
                      qf->wgs > 0 && qf->pieces >= 1 && qf->pieces <= 4 && qf->groups == d.D / 128 &&
@@ -1973,19 +2007,22 @@ void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev
     m.nsites = nsites;
     for (int k = 0; k < nsites; ++k) m.sites[k] = sites[k];
     ND_CHECK(!start || l == -1, "internal: the first layer's mixing takes l = -1");
+    ND_CHECK(!er.codes || (start && d.D <= 512 && er.g.group <= d.D && er.g.groups * er.g.group == d.D &&
+                           (er.g.kind == kNib || er.g.kind == kCrumb)),
+             "internal: embedding rows decoded in the first launch outside its geometry");
     const QkvgFused none{};
     auto go = [&](auto n, auto st) {
         constexpr int N = decltype(n)::value;
         constexpr bool S = decltype(st)::value;
         if (qf)
             hipLaunchKernelGGL((eng_post_mix_kernel<512, N, true, S>), dim3(qf->wgs, 1), dim3(512), 0, s, b, ld, ldn,
-                               mh, l, a, m, d, pt, *qf, start);
+                               mh, l, a, m, d, pt, *qf, start, er);
         else if (d.D <= 512)
             hipLaunchKernelGGL((eng_post_mix_kernel<512, N, false, S>), dim3(1, tokens), dim3(512), 0, s, b, ld, ldn,
-                               mh, l, a, m, d, pt, none, start);
+                               mh, l, a, m, d, pt, none, start, er);
         else
             hipLaunchKernelGGL((eng_post_mix_kernel<kEngThreads, N, false, S>), dim3(1, tokens), dim3(kEngThreads), 0,
-                               s, b, ld, ldn, mh, l, a, m, d, pt, none, start);
+                               s, b, ld, ldn, mh, l, a, m, d, pt, none, start, EmbedRows{});
     };
     with_lanes(d.N, [&](auto n) {
         if (start) go(n, std::true_type{});
