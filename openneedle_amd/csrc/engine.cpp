@@ -325,7 +325,7 @@ struct GpuEngine {
     // `side` from the uploaded tokens on, and the main stream waits for site k
     // (ev_site[k]) just before the mixing kernel of layer sites[k].
     hipStream_t side = nullptr;
-    hipEvent_t ev_upload = nullptr, ev_site[kEngMaxSites] = {};
+    hipEvent_t ev_site[kEngMaxSites] = {};
     EngineDims dims{};
     EngineBufs b{};
     DevBuf<float> work;
@@ -338,7 +338,7 @@ struct GpuEngine {
     // What a launch reads from the host goes up in one copy: the row ids, then
     // the StepParams, in one pinned buffer and its device twin; the views
     // below point into the two.
-    DevBuf<uint8_t> upload;
+    DevBuf<uint8_t> upload, upload_side;  // the step's upload; the side stream's copy of it
     HostBuf<uint8_t> hupload;
     size_t params_offset = 0;  // bytes of upload before the StepParams
     BufView<StepParams> params, hparams;
@@ -370,7 +370,6 @@ struct GpuEngine {
         if (side) (void)hipStreamSynchronize(side);
         for (hipEvent_t e : ev_site)
             if (e) (void)hipEventDestroy(e);
-        if (ev_upload) (void)hipEventDestroy(ev_upload);
         if (side) (void)hipStreamDestroy(side);
         if (stream) (void)hipStreamDestroy(stream);
     }
@@ -407,7 +406,8 @@ struct GpuEngine {
                       const float *v);
     int decode_loop(int first_token, int max_new_tokens, const DfaC *dfa, int *out, int *generated);
     void upload_tokens(int tokens);
-    void run_engram_site(int site, int tokens, hipStream_t s);
+    // (on the side stream the kernels read the side stream's own copy of the upload)
+    void run_engram_site(int site, int tokens, hipStream_t s, bool side_copy = false);
     // copies `prefix` slots of every (layer, K | V, kv head) row between the cache and the snapshot
     void copy_prefix_slots(bool to_snapshot);
 };
@@ -438,7 +438,6 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
     ND_HIP(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
     if (c.num_sites) {
         ND_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
-        ND_HIP(hipEventCreateWithFlags(&ev_upload, hipEventDisableTiming));
         for (int k = 0; k < c.num_sites; ++k) ND_HIP(hipEventCreateWithFlags(&ev_site[k], hipEventDisableTiming));
     }
 
@@ -569,6 +568,7 @@ GpuEngine::GpuEngine(const EngineConfigC &cfg, const TensorDescC *td, int count,
         params_offset = (nids * sizeof(int64_t) + 255) & ~size_t(255);
         const size_t bytes = params_offset + size_t(chunk) * sizeof(StepParams);
         upload.reserve(bytes);
+        upload_side.reserve(bytes);
         hupload.reserve(bytes);
         std::memset(hupload.p, 0, bytes);
         ids = {reinterpret_cast<int64_t *>(upload.p), nids};
@@ -1067,12 +1067,13 @@ void GpuEngine::upload_tokens(int T) {
 
 // Engram rows, their quantiser, key / value projections, the conv and the ring
 // of one site for the T uploaded tokens (engine.cpp:755-781).
-void GpuEngine::run_engram_site(int site, int T, hipStream_t s) {
-    const StepParams *dp = params.p;
+void GpuEngine::run_engram_site(int site, int T, hipStream_t s, bool side_copy) {
+    const uint8_t *base = side_copy ? upload_side.p : upload.p;
+    const StepParams *dp = reinterpret_cast<const StepParams *>(base + params_offset);
     {
         const int e0 = engram_base() + 4 * site;
         const Mat &tab = mats[e0];
-        const int64_t *rows = ids.p + chunk + size_t(site) * chunk * c.tables;
+        const int64_t *rows = reinterpret_cast<const int64_t *>(base) + chunk + size_t(site) * chunk * c.tables;
         if (tab.cq)
             launch_cq_rows(tab.cq->geom(), tab.cq->codes.p, tab.cq->norms.p, rows, T * c.tables, c.subdim,
                            tab.cq->padded, engram_scratch.p, b.e, s);
@@ -1092,7 +1093,6 @@ void GpuEngine::run(int tokens) {
     const int D = c.dim, HD = c.head_dim, T = tokens;
     hipStream_t s = stream;
     upload_tokens(T);
-    if (c.num_sites) ND_HIP(hipEventRecord(ev_upload, s));
     const StepParams *dp = params.p;
 
     // a layer's post runs with the next layer's mHC projections and mixing (and the first layer's with
@@ -1110,18 +1110,19 @@ void GpuEngine::run(int tokens) {
     else
         launch_eng_dense_rows(emb.dense, D, ids.p, T, embed_z.p, s);
     if (!fuse) launch_eng_start(embed_z.p, b, dims, T, s);
-    // engram sites up to layer `upto` onto the side stream, behind the upload (the side stream's wait for
-    // it is issued with the first site: issuing a wait costs the host ~14 us, which at the step's start
-    // would hold back the first layer's launches while the GPU idles)
-    bool sent[kEngMaxSites] = {}, side_waits = false;
+    // engram sites up to layer `upto` onto the side stream, behind its own copy of the upload (a wait
+    // for the main stream's copy cost the host ~14 us to issue, which held back the next layer's launches
+    // while the GPU idled); the first site issues the copy
+    bool sent[kEngMaxSites] = {}, side_copied = false;
     auto send_sites = [&](int upto) {
         for (int k = 0; k < c.num_sites; ++k)
             if (!sent[k] && c.sites[k] <= upto) {
-                if (!side_waits) {
-                    ND_HIP(hipStreamWaitEvent(side, ev_upload, 0));
-                    side_waits = true;
+                if (!side_copied) {
+                    ND_HIP(hipMemcpyAsync(upload_side.p, hupload.p, params_offset + size_t(T) * sizeof(StepParams),
+                                          hipMemcpyHostToDevice, side));
+                    side_copied = true;
                 }
-                run_engram_site(k, T, side);
+                run_engram_site(k, T, side, true);
                 ND_HIP(hipEventRecord(ev_site[k], side));
                 sent[k] = true;
             }
