@@ -706,11 +706,11 @@ OutProj GpuEngine::out_projection(const Projection &p) const {
 }
 
 // Layer l's Q|K|V|gate runs inside the previous layer's post launch (layer
-// 0's: inside the launch that starts the lanes and mixes) (QkvgFused) when its four matrices are one FP32 GEMV group of 2- or 4-bit
-// codes in groups of 128 over d_model <= 512 (a multiple of 128) inputs, with
-// no activation quantiser (NEEDLE2_ENGINE_QKVG=gemv: always the separate
-// GEMV); the step takes it where the post / mixing launch is fused and layer
-// l has no engram site.
+// 0's: inside the launch that starts the lanes and mixes; QkvgFused) when its
+// four matrices are one FP32 GEMV group of 2- or 4-bit codes in groups of 128
+// over d_model <= 512 (a multiple of 128) inputs, with no activation
+// quantiser (NEEDLE2_ENGINE_QKVG=gemv: always the separate GEMV); the step
+// takes it where the post / mixing launch is fused.
 QkvgFused GpuEngine::qkvg_fusion(int l) const {
     QkvgFused q{};
     const char *mode = std::getenv("NEEDLE2_ENGINE_QKVG");
@@ -1162,7 +1162,7 @@ void GpuEngine::run(int tokens) {
             PrepTarget pt;
             qkvg_prepared = target(qkvg[0], pt);
             QkvgFused qf = qfused[0];
-            const bool with_qkvg = T == 1 && ns == 0 && !qkvg_prepared && qf.wgs > 0;
+            const bool with_qkvg = T == 1 && !qkvg_prepared && qf.wgs > 0;
             qf.x_out = cur.x;  // (nothing in this launch reads the state it writes)
             qf.u_out = cur.u;
             qf.bx_out = cur.bx;
@@ -1212,7 +1212,7 @@ void GpuEngine::run(int tokens) {
             PrepTarget pt;
             qkvg_prepared = target(qkvg[l + 1], pt);
             QkvgFused qf = qfused[l + 1];
-            if (T == 1 && ns == 0 && !qkvg_prepared && qf.wgs > 0) {
+            if (T == 1 && !qkvg_prepared && qf.wgs > 0) {
                 qf.x_out = other[0];
                 qf.u_out = other[1];
                 qf.bx_out = other[2];

@@ -208,7 +208,7 @@ void launch_eng_post(const EngineBufs &b, const LayerDev &ld, int l, bool next_r
 // The post of layer l, then layer l + 1's dense mHC projections (rows first[m] .. of the three
 // matrices w[m]) and mixing with the engram sites[0..nsites), in one launch; only where
 // eng_post_mix_fits(d). qf (null: none): layer l + 1's Q|K|V|gate projection in the same launch
-// (QkvgFused; one token, no engram site, no activation quantiser, no int8 target). start (l = -1):
+// (QkvgFused; one token, no activation quantiser, no int8 target). start (l = -1):
 // no post; the lanes come from the tokens' embedding rows start[t][D] (launch_eng_start's work; er.codes
 // set: decoded here into start, EmbedRows), then layer 0's projections and mixing.
 bool eng_post_mix_fits(const EngineDims &d);

@@ -1544,7 +1544,7 @@ __device__ __forceinline__ const float4 *mhc_row_ptr(const DenseRows &w, int r, 
 // lane keeps apart, and block_sum's tree over 64 threads and the sequential
 // sum of its four waves follow, so the outputs are the same bits as the
 // separate launches'. Needs D <= THREADS, N * D <= 4096.
-// QKVG (one token, THREADS 512, no engram site, no activation quantiser, no
+// QKVG (one token, THREADS 512, no activation quantiser, no
 // int8 target): workgroup blockIdx.x also computes one kQkvgRows-row slice of the
 // next layer's Q|K|V|gate projection (QkvgFused); workgroup 0 alone stores
 // the layer state, the lanes, u, bx and hpost into qf's *_out buffers.
@@ -1771,6 +1771,29 @@ __global__ __launch_bounds__(THREADS) void eng_post_mix_kernel(EngineBufs b0, La
         __syncthreads();
         mix_sites(b, m, d, red, zs, ps);
         rms_block(b.bx, b.z, D, ldn.norm_in, red);
+    } else if (QKVG && m.nsites) {
+        // mix_sites' and rms_block's arithmetic on the registers (thread i holds element i), so that every
+        // workgroup holds the same z; workgroup 0 stores bx
+        float bxv = u;
+        for (int k = 0; k < m.nsites; ++k) {
+            int st = m.sites[0];
+#pragma unroll
+            for (int j = 1; j < kEngMaxSites; ++j)
+                if (k == j) st = m.sites[j];
+            const float ek = own ? b.ek[st * D + i] : 0.0f, ev = own ? b.ev[st * D + i] : 0.0f;
+            const float ru = 1.0f / sqrtf(block_sum(own ? u * u : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+            const float rk = 1.0f / sqrtf(block_sum(own ? ek * ek : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+            const float zsv = u * ru, psv = ek * rk;
+            const float alpha = sigmoidf_(block_sum(own ? zsv * psv : 0.0f, red) / d.sqrt_d);
+            bxv = bxv + alpha * ev;
+        }
+        if (lead && own) qf.bx_out[i] = bxv;
+        const float r = 1.0f / sqrtf(block_sum(own ? bxv * bxv : 0.0f, red) / static_cast<float>(D) + 1e-6f);
+        if (own) {
+            z = bxv * r * (1.0f + nin);
+            if (lead) b.z[i] = z;
+        }
+        __syncthreads();
     } else {  // rms_block's arithmetic on the registers
         const float r = 1.0f / sqrtf(block_sum_nb(own ? u * u : 0.0f, red + kWaves) / static_cast<float>(D) + 1e-6f);
         if (own) {
@@ -1993,7 +2016,7 @@ void launch_eng_post_mix(const EngineBufs &b, const LayerDev &ld, const LayerDev
                          int tokens, const PrepTarget &pt, const QkvgFused *qf, const float *start, hipStream_t s,
                          const EmbedRows &er) {
     ND_CHECK(eng_post_mix_fits(d), "internal: fused post / mixing launch outside its geometry");
-    ND_CHECK(!qf || (tokens == 1 && nsites == 0 && !pt.q && d.abits == 0 && d.D <= 512 && d.D % 128 == 0 &&
+    ND_CHECK(!qf || (tokens == 1 && !pt.q && d.abits == 0 && d.D <= 512 && d.D % 128 == 0 &&
                      qf->wgs > 0 && qf->pieces >= 1 && qf->pieces <= 4 && qf->groups == d.D / 128 &&
                      (qf->kind == 0 || qf->kind == 1) && qf->x_out && qf->u_out && qf->bx_out && qf->hpost_out),
              "internal: fused Q|K|V|gate projection outside its geometry");

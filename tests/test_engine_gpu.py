@@ -320,8 +320,8 @@ def test_qkvg_in_post(bits, d_model, monkeypatch):
     post and mixing, then one 128-row slice of the projection with the GEMV's arithmetic; workgroup 0 stores
     the state into the second copy of the buffers) gives the separate GEMV's bits (NEEDLE2_ENGINE_QKVG=gemv):
     every logit and hidden state over steps after a prompt, groups of 128 over 2 and 4 groups, 2- and 4-bit
-    codes, a layer with an engram site (its post stays unfused) between fused ones; and matches the
-    reference."""
+    codes, the post before a layer with an engram site (the site's gate applied in registers in every
+    workgroup); and matches the reference."""
     geometry = dict(SMALL, d_model=d_model, hada_n=d_model, num_heads=4, num_kv_heads=2, head_dim=64,
                     engram_sub_dim=d_model // 4, num_layers=4, max_seq_len=128)
     a = Archive(synthetic_model(geometry, engram_layers=(2,), engram_orders=(2, 3), group=128, seed=17,
